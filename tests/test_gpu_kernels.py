@@ -1,0 +1,144 @@
+"""GPU parity: block decode, quantize and GEMV through the C ABI vs the oracle.
+
+Bars: bit-exact for decoded weights and quantized bytes; rel-L2 <= 1e-3 for
+GEMV outputs (fp32 accumulation).  Small shapes are compared against the
+oracle directly; the config shapes run at full size.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from vibeblade_amd import ggml
+from vibeblade_amd.tensor import QTensor, gemv
+
+pytestmark = pytest.mark.gpu
+
+GEMV_TOL = 1e-3
+QTYPES = [ggml.GGML_TYPE_Q4_K, ggml.GGML_TYPE_Q6_K, ggml.GGML_TYPE_Q8_0]
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    torch.cuda.init()
+    yield
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def rand_weights(rows, k, seed):
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal((rows, k)) * 0.02).astype(np.float32)
+
+
+def test_dequant_matches_compiled_reference_vectors():
+    g = np.load("tests/golden/ref_vectors.npz", allow_pickle=False)
+    blocks = g["q4k_blocks"]
+    qt = QTensor.from_bytes(blocks.ravel(), ggml.GGML_TYPE_Q4_K, 1, 256 * blocks.shape[0])
+    out = qt.dequantize().cpu().numpy().ravel()
+    assert np.array_equal(bits(out), bits(g["q4k_out"].ravel()))
+
+
+@pytest.mark.parametrize("qtype", QTYPES)
+@pytest.mark.parametrize("rows,k", [(1, 256), (7, 512), (33, 4096), (5, 14336)])
+def test_dequant_random_bytes_bit_exact(qtype, rows, k):
+    rng = np.random.default_rng(rows * 131 + k)
+    rb = ggml.row_bytes(qtype, k)
+    raw = rng.integers(0, 256, (rows, rb), dtype=np.uint8)
+    # keep fp16 scales finite (random bytes may form inf/nan halves)
+    be, bb = ggml.BLOCK[qtype]
+    blk = raw.reshape(-1, bb)
+    offs = {ggml.GGML_TYPE_Q4_K: [0, 2], ggml.GGML_TYPE_Q6_K: [208], ggml.GGML_TYPE_Q8_0: [0]}[qtype]
+    for o in offs:
+        blk[:, o + 1] &= 0x7B  # exponent < 31
+    want = O.dequantize(raw, k, qtype)
+    got = QTensor.from_bytes(raw, qtype, rows, k).dequantize().cpu().numpy()
+    assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("qtype", [ggml.GGML_TYPE_F32, ggml.GGML_TYPE_F16])
+def test_dequant_plain_types(qtype):
+    w = rand_weights(9, 37, 1)
+    raw = w.tobytes() if qtype == ggml.GGML_TYPE_F32 else w.astype(np.float16).tobytes()
+    got = QTensor.from_bytes(raw, qtype, 9, 37).dequantize().cpu().numpy()
+    want = w if qtype == ggml.GGML_TYPE_F32 else w.astype(np.float16).astype(np.float32)
+    assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("qtype", QTYPES)
+def test_quantize_matches_oracle_bytes(qtype):
+    w = rand_weights(24, 1024, 2)
+    w[3, :256] = 0.0            # all-zero block
+    w[4, 5] = 0.5               # outlier
+    qt = QTensor.quantize(w, qtype)
+    assert np.array_equal(qt.to_numpy_bytes(), O.quantize(w, qtype))
+
+
+@pytest.mark.parametrize("qtype", QTYPES + [ggml.GGML_TYPE_F32, ggml.GGML_TYPE_F16])
+@pytest.mark.parametrize("rows,k", [(1, 256), (13, 512), (70, 4096), (37, 14336), (9, 28672)])
+def test_gemv_small_vs_oracle(qtype, rows, k):
+    w = rand_weights(rows, k, rows + k)
+    qt = QTensor.quantize(w, qtype)
+    x = np.random.default_rng(k).standard_normal(k).astype(np.float32)
+    y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy()
+    want = O.gemv(qt.to_numpy_bytes(), x, rows, k, qtype)
+    assert O.rel_l2(y, want) <= GEMV_TOL
+    # and each output individually close (no dropped row)
+    scale = np.abs(want).max()
+    assert np.max(np.abs(y - want)) <= 1e-3 * scale + 1e-6
+
+
+def test_gemv_zero_rows_and_errors():
+    qt = QTensor.quantize(rand_weights(4, 256, 3), ggml.GGML_TYPE_Q4_K)
+    x = torch.zeros(256, device="cuda")
+    with pytest.raises(ValueError):
+        gemv(qt, torch.zeros(255, device="cuda"))
+    from vibeblade_amd import _lib
+    y = torch.full((4,), 7.0, device="cuda")
+    _lib.call("vb_gemv", qt.ptr(), x.data_ptr(), y.data_ptr(), 0, 256, qt.qtype, 0)
+    torch.cuda.synchronize()
+    assert torch.all(y == 7.0)  # n = 0 writes nothing
+    with pytest.raises(ValueError):
+        _lib.call("vb_gemv", qt.ptr(), x.data_ptr(), y.data_ptr(), 4, 100, qt.qtype, 0)
+
+
+def test_gemv_extreme_activations():
+    """Outliers, zeros and tiny values in x still meet the bound."""
+    k = 4096
+    qt = QTensor.quantize(rand_weights(64, k, 4), ggml.GGML_TYPE_Q4_K)
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal(k).astype(np.float32)
+    x[:64] = 0.0
+    x[100] = 300.0
+    x[2000:2032] = 1e-30
+    y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy()
+    want = O.gemv(qt.to_numpy_bytes(), x, 64, k, qt.qtype)
+    assert O.rel_l2(y, want) <= GEMV_TOL
+
+
+CONFIG_SHAPES = [
+    (ggml.GGML_TYPE_Q8_0, 4096, 4096),     # Q8_0 GEMV 4096x4096
+    (ggml.GGML_TYPE_Q4_K, 14336, 4096),    # Q4_K gate/up
+    (ggml.GGML_TYPE_Q4_K, 4096, 14336),    # Q4_K down
+    (ggml.GGML_TYPE_Q6_K, 128256, 4096),   # Q6_K lm_head
+]
+
+
+@pytest.mark.parametrize("qtype,rows,k", CONFIG_SHAPES)
+def test_gemv_config_shapes(qtype, rows, k):
+    gen = torch.Generator(device="cuda").manual_seed(rows + k)
+    w = torch.randn((rows, k), generator=gen, device="cuda") * 0.02
+    qt = QTensor.quantize(w, qtype)
+    del w
+    x = torch.randn(k, generator=gen, device="cuda")
+    y = gemv(qt, x).cpu().numpy()
+    want = O.gemv(qt.to_numpy_bytes(), x.cpu().numpy(), rows, k, qtype)
+    assert O.rel_l2(y, want) <= GEMV_TOL
+    # the decode of the same bytes is bit-exact at full size too
+    if rows * k <= 14336 * 4096:
+        got = qt.dequantize().cpu().numpy()
+        assert np.array_equal(bits(got), bits(O.dequantize(qt.to_numpy_bytes(), k, qtype)))

@@ -1,0 +1,316 @@
+"""Pins the CPU oracle before anything is compared against it (CPU only).
+
+Each decoder is checked against something independent of its own code:
+golden vectors from the compiled reference, the reference's known-answer
+tests, closed forms on blocks whose decoded values are known integers, or
+the published ggml loop form of the layout.
+"""
+import os
+import struct
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden", "ref_vectors.npz")
+
+
+@pytest.fixture(scope="module")
+def gold():
+    return np.load(GOLD, allow_pickle=False)
+
+
+def bits(a):
+    return np.asarray(a, dtype=np.float32).view(np.uint32)
+
+
+# ---- fp16 ------------------------------------------------------------------
+
+def test_f16_to_f32_exact_for_all_patterns():
+    allbits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    exact = allbits.view(np.float16).astype(np.float32)
+    mine = np.array([O.f16_to_f32(int(b)) for b in allbits], dtype=np.float32)
+    nan = np.isnan(exact)
+    assert np.array_equal(np.isnan(mine), nan)
+    assert np.array_equal(bits(mine[~nan]), bits(exact[~nan]))
+
+
+def test_reference_f16_doubles_subnormals(gold):
+    """cpp/src/fp16_compat.cpp:13-35 returns 2x the value of every fp16
+    subnormal; normals and infinities are exact.  The oracle and the GPU follow
+    IEEE (v_cvt_f32_f16), i.e. what GGUF files mean."""
+    b = gold["f16_bits"]
+    ref = gold["f16_ref"]
+    exact = b.view(np.float16).astype(np.float32)
+    sub = ((b & 0x7C00) == 0) & ((b & 0x3FF) != 0)
+    assert np.array_equal(bits(ref[~sub]), bits(exact[~sub]))
+    assert np.array_equal(ref[sub], 2.0 * exact[sub])
+
+
+def test_f32_to_f16_round_to_nearest_even():
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal(5000) * 10.0 ** rng.integers(-9, 5, 5000)).astype(np.float32)
+    x = np.concatenate([x, np.float32([0.0, -0.0, 65504.0, 65520.0, 1e-8, 6e-8, 3e-8, np.inf])])
+    mine = np.array([O.f32_to_f16(float(v)) for v in x], dtype=np.uint16)
+    assert np.array_equal(mine, x.astype(np.float16).view(np.uint16))
+
+
+# ---- Q4_K --------------------------------------------------------------------
+
+def test_q4k_matches_compiled_reference(gold):
+    blocks, want = gold["q4k_blocks"], gold["q4k_out"]
+    got = O.dequantize(blocks.reshape(1, -1), blocks.shape[0] * 256, O.TYPE_Q4_K)
+    assert np.array_equal(bits(got.ravel()), bits(want.ravel()))
+
+
+def _q4k_unit_block(qs):
+    b = bytearray(144)
+    b[0:2] = struct.pack("<e", 1.0)
+    b[2:4] = struct.pack("<e", 0.0)
+    b[4:16] = bytes([1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1])  # sc_j = 1, m_j = 0
+    b[16:144] = bytes(qs)
+    return np.frombuffer(bytes(b), dtype=np.uint8)
+
+
+def test_q4k_index_map_single_nibble():
+    """d=1, dmin=0, every sc=1: y is the nibble itself.  One non-zero nibble
+    per position checks the element -> (byte, nibble) map of
+    cpp/src/dequant.cpp:289-296."""
+    for byte in range(128):
+        for hi in range(2):
+            qs = [0] * 128
+            qs[byte] = 5 << (4 * hi)
+            y = O.dequantize(_q4k_unit_block(qs).reshape(1, -1), 256, O.TYPE_Q4_K).ravel()
+            c, l = byte // 32, byte % 32
+            e = 64 * c + 32 * hi + l
+            want = np.zeros(256, np.float32)
+            want[e] = 5.0
+            assert np.array_equal(y, want), (byte, hi)
+
+
+def test_q4k_min_term():
+    b = bytearray(_q4k_unit_block([0x33] * 128).tobytes())
+    b[2:4] = struct.pack("<e", 0.5)
+    b[4:16] = bytes([2, 2, 2, 2, 3, 3, 3, 3, 0x32, 0x32, 0x32, 0x32])  # sc=2, m=3 everywhere
+    y = O.dequantize(np.frombuffer(bytes(b), np.uint8).reshape(1, -1), 256, O.TYPE_Q4_K)
+    assert np.all(y == 2.0 * 3 - 0.5 * 3)
+
+
+# ---- Q6_K --------------------------------------------------------------------
+
+def _q6k_block(fill_ql, fill_qh, scale=1, d=1.0):
+    b = bytearray(210)
+    b[0:128] = bytes([fill_ql]) * 128
+    b[128:192] = bytes([fill_qh]) * 64
+    b[192:208] = bytes([scale & 0xFF]) * 16
+    b[208:210] = struct.pack("<e", d)
+    return np.frombuffer(bytes(b), dtype=np.uint8)
+
+
+@pytest.mark.parametrize("qtype", [O.TYPE_Q6_K, O.TYPE_Q6_K_VBREF])
+def test_q6k_reference_known_answers(qtype):
+    """The layout-invariant known answers of tests/test_kquants.py:134-175."""
+    y = O.dequantize(_q6k_block(0xFF, 0xFF).reshape(1, -1), 256, qtype)
+    assert np.all(y == 31.0)
+    y = O.dequantize(_q6k_block(0x00, 0x00).reshape(1, -1), 256, qtype)
+    assert np.all(y == -32.0)
+    y = O.dequantize(_q6k_block(0x00, 0x55).reshape(1, -1), 256, qtype)
+    assert np.all(y == -16.0)
+
+
+def test_q6k_vbref_matches_compiled_reference(gold):
+    blocks, want = gold["q6k_blocks"], gold["q6k_vbref_out"]
+    got = O.dequantize(blocks.reshape(1, -1), blocks.shape[0] * 256, O.TYPE_Q6_K_VBREF)
+    assert np.array_equal(bits(got.ravel()), bits(want.ravel()))
+
+
+def _ggml_q6k_loop(block):
+    """ggml's published dequantize_row_q6_K loop form (two halves of 128, four
+    strided outputs per l), an independent statement of the GGUF layout."""
+    ql = block[0:128].astype(np.int32)
+    qh = block[128:192].astype(np.int32)
+    sc = block[192:208].view(np.int8).astype(np.float32)
+    d = np.float32(np.frombuffer(block[208:210].tobytes(), np.float16)[0])
+    y = np.zeros(256, np.float32)
+    for n in range(2):
+        qlp, qhp, scp, yp = ql[64 * n:], qh[32 * n:], sc[8 * n:], 128 * n
+        for l in range(32):
+            i = l // 16
+            q1 = ((qlp[l] & 0xF) | (((qhp[l] >> 0) & 3) << 4)) - 32
+            q2 = ((qlp[l + 32] & 0xF) | (((qhp[l] >> 2) & 3) << 4)) - 32
+            q3 = ((qlp[l] >> 4) | (((qhp[l] >> 4) & 3) << 4)) - 32
+            q4 = ((qlp[l + 32] >> 4) | (((qhp[l] >> 6) & 3) << 4)) - 32
+            y[yp + l] = d * scp[i + 0] * q1
+            y[yp + l + 32] = d * scp[i + 2] * q2
+            y[yp + l + 64] = d * scp[i + 4] * q3
+            y[yp + l + 96] = d * scp[i + 6] * q4
+    return y
+
+
+def test_q6k_gguf_layout_against_ggml_loop_form():
+    rng = np.random.default_rng(11)
+    for _ in range(16):
+        blk = rng.integers(0, 256, 210, dtype=np.uint8)
+        blk[208:210] = np.frombuffer(np.float16(rng.uniform(1e-3, 2)).tobytes(), np.uint8)
+        got = O.dequantize(blk.reshape(1, -1), 256, O.TYPE_Q6_K).ravel()
+        assert np.array_equal(bits(got), bits(_ggml_q6k_loop(blk)))
+
+
+def test_q6k_gguf_and_vbref_differ():
+    """Single-position blocks separate the two gathers (the reference's C++
+    decoder is not the GGUF one)."""
+    blk = _q6k_block(0x00, 0x00).copy()
+    blk[0] = 0x0F  # ql[0] low nibble
+    g = O.dequantize(blk.reshape(1, -1), 256, O.TYPE_Q6_K).ravel()
+    v = O.dequantize(blk.reshape(1, -1), 256, O.TYPE_Q6_K_VBREF).ravel()
+    assert g[0] == -17.0 and v[0] == -17.0
+    blk = _q6k_block(0x00, 0x00).copy()
+    blk[1] = 0xF0  # ql[1] high nibble
+    g = O.dequantize(blk.reshape(1, -1), 256, O.TYPE_Q6_K).ravel()
+    v = O.dequantize(blk.reshape(1, -1), 256, O.TYPE_Q6_K_VBREF).ravel()
+    assert np.flatnonzero(g != -32.0).tolist() == [65]   # GGUF: h=0,t=2,l=1
+    assert np.flatnonzero(v != -32.0).tolist() == [3]    # VBREF: e/2=1, odd
+
+
+# ---- Q8_0 ----------------------------------------------------------------------
+
+def _q8_block(d, q):
+    return np.frombuffer(struct.pack("<e", d) + np.asarray(q, np.int8).tobytes(), np.uint8)
+
+
+def test_q8_0_closed_forms():
+    q = np.arange(-16, 16, dtype=np.int8)
+    y = O.dequantize(_q8_block(1.0, q).reshape(1, -1), 32, O.TYPE_Q8_0).ravel()
+    assert np.array_equal(y, q.astype(np.float32))
+    y = O.dequantize(_q8_block(0.0, q).reshape(1, -1), 32, O.TYPE_Q8_0).ravel()
+    assert np.all(y == 0.0)
+
+
+def test_q8_0_loader_semantics():
+    """vibeblade/loader.py:129-133: fp16 scale at [0:2], int8 at [2:34]."""
+    rng = np.random.default_rng(5)
+    blocks = rng.integers(0, 256, (40, 34), dtype=np.uint8)
+    blocks[:, 0:2] = np.frombuffer(np.float16(rng.uniform(-2, 2, 40)).tobytes(), np.uint8).reshape(40, 2)
+    want = np.concatenate([
+        np.frombuffer(b[2:34].tobytes(), np.int8).astype(np.float32)
+        * np.frombuffer(b[:2].tobytes(), np.float16).astype(np.float32)[0] for b in blocks])
+    got = O.dequantize(blocks.reshape(1, -1), 40 * 32, O.TYPE_Q8_0).ravel()
+    assert np.array_equal(bits(got), bits(want))
+
+
+# ---- quantizers ------------------------------------------------------------------
+
+@pytest.mark.parametrize("qtype,tol", [(O.TYPE_Q8_0, 0.01), (O.TYPE_Q4_K, 0.12), (O.TYPE_Q6_K, 0.03)])
+def test_quantizer_roundtrip(qtype, tol):
+    rng = np.random.default_rng(7)
+    w = (rng.standard_normal((8, 1024)) * 0.02).astype(np.float32)
+    wq = O.quantize(w, qtype)
+    assert wq.shape == (8, O.row_bytes(qtype, 1024))
+    back = O.dequantize(wq, 1024, qtype)
+    assert O.rel_l2(back, w) < tol
+
+
+def test_quantized_q4k_decodes_identically_in_reference():
+    if not O.ref_available():
+        pytest.skip("compiled reference not built (no reference tree)")
+    rng = np.random.default_rng(8)
+    w = (rng.standard_normal((4, 2048)) * 0.02).astype(np.float32)
+    wq = O.quantize(w, O.TYPE_Q4_K)
+    mine = O.dequantize(wq, 2048, O.TYPE_Q4_K).ravel()
+    ref = O.ref_dequantize(wq.ravel(), 4 * 2048, O.TYPE_Q4_K)
+    assert np.array_equal(bits(mine), bits(ref))
+
+
+# ---- products ----------------------------------------------------------------------
+
+def _integer_matrix(qtype, rows, k, rng):
+    """GGUF bytes whose decoded values are known integers, plus those values."""
+    if qtype == O.TYPE_Q8_0:
+        q = rng.integers(-127, 128, (rows, k)).astype(np.int8)
+        raw = b"".join(_q8_block(1.0, q[r, 32 * i:32 * i + 32]).tobytes()
+                       for r in range(rows) for i in range(k // 32))
+        return np.frombuffer(raw, np.uint8).reshape(rows, -1), q.astype(np.float64)
+    if qtype == O.TYPE_Q4_K:
+        nib = rng.integers(0, 16, (rows, k))
+        out = []
+        for r in range(rows):
+            for s in range(k // 256):
+                blk = nib[r, 256 * s:256 * s + 256]
+                qs = [(blk[64 * c + l] | (blk[64 * c + 32 + l] << 4)) for c in range(4) for l in range(32)]
+                out.append(_q4k_unit_block(qs).tobytes())
+        return np.frombuffer(b"".join(out), np.uint8).reshape(rows, -1), nib.astype(np.float64)
+    raise ValueError(qtype)
+
+
+@pytest.mark.parametrize("qtype", [O.TYPE_Q8_0, O.TYPE_Q4_K])
+def test_gemv_gemm_brute_force(qtype):
+    rng = np.random.default_rng(9)
+    rows, k = 6, 512
+    wq, wint = _integer_matrix(qtype, rows, k, rng)
+    assert np.array_equal(O.dequantize(wq, k, qtype), wint.astype(np.float32))
+    x = rng.standard_normal((3, k)).astype(np.float32)
+    want = x.astype(np.float64) @ wint.T
+    assert np.allclose(O.gemv(wq, x[0], rows, k, qtype), want[0], rtol=1e-6, atol=1e-6)
+    assert np.allclose(O.gemm(wq, x, rows, k, qtype), want, rtol=1e-6, atol=1e-6)
+
+
+def test_gemv_kn_restates_reference_loop(gold):
+    K, N = (int(v) for v in gold["kn_shape"])
+    got = O.gemv_kn(gold["kn_x"], gold["kn_w"], K, N, O.TYPE_Q4_K)
+    assert np.allclose(got, gold["kn_out"], rtol=1e-6, atol=1e-7)
+
+
+# ---- FFN compositions -----------------------------------------------------------------
+
+def _ffn_weights(rng, H=64, I=256):
+    g = (rng.standard_normal((I, H)) * 0.1).astype(np.float32)
+    u = (rng.standard_normal((I, H)) * 0.1).astype(np.float32)
+    d = (rng.standard_normal((H, I)) * 0.1).astype(np.float32)
+    return g, u, d
+
+
+@pytest.mark.parametrize("act", [O.ACT_SILU, O.ACT_DRELU])
+def test_sparse_ffn_invariants(act):
+    rng = np.random.default_rng(12)
+    g, u, d = _ffn_weights(rng)
+    x = rng.standard_normal((2, 64)).astype(np.float32)
+    x64 = x.astype(np.float64)
+    gd, ud = x64 @ g.T.astype(np.float64), x64 @ u.T.astype(np.float64)
+    h = O.silu64(gd) * ud if act == O.ACT_SILU else np.maximum(gd, 0) * np.maximum(ud, 0)
+    dense = h @ d.T.astype(np.float64)
+    allidx = np.arange(256)
+    assert np.allclose(O.sparse_ffn(g, u, d, x, allidx, act), dense, rtol=1e-12, atol=1e-12)
+    assert np.all(O.sparse_ffn(g, u, d, x, np.array([], np.int64), act) == 0)
+    s = np.sort(rng.choice(256, 40, replace=False))
+    masked = (h * np.isin(allidx, s)) @ d.T.astype(np.float64)
+    assert np.allclose(O.sparse_ffn(g, u, d, x, s, act), masked, rtol=1e-12, atol=1e-12)
+    assert np.allclose(O.sparse_ffn(g, u, d, x, s[::-1], act), masked, rtol=1e-12, atol=1e-12)
+
+
+def test_moe_invariants():
+    rng = np.random.default_rng(13)
+    E, H, I, T = 4, 32, 64, 6
+    gates = [(rng.standard_normal((I, H)) * 0.1).astype(np.float32) for _ in range(E)]
+    ups = [(rng.standard_normal((I, H)) * 0.1).astype(np.float32) for _ in range(E)]
+    downs = [(rng.standard_normal((H, I)) * 0.1).astype(np.float32) for _ in range(E)]
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    y, idx, w = O.moe_ffn(gates, ups, downs, x, logits, 2)
+    assert np.allclose(w.sum(axis=1), 1.0)
+    assert np.all(idx[:, 0] != idx[:, 1])
+    # every token routed to expert 2 first and expert 0 second
+    logits2 = np.full((T, E), -5.0, np.float32)
+    logits2[:, 2], logits2[:, 0] = 3.0, 1.0
+    y2, idx2, w2 = O.moe_ffn(gates, ups, downs, x, logits2, 2)
+    x64 = x.astype(np.float64)
+
+    def ffn(e):
+        return (O.silu64(x64 @ gates[e].T) * (x64 @ ups[e].T)) @ downs[e].T.astype(np.float64)
+    assert np.allclose(y2, w2[:, :1] * ffn(2) + w2[:, 1:] * ffn(0), rtol=1e-12)
+    # relabelling experts relabels the routing consistently
+    perm = np.array([3, 1, 0, 2])
+    y3, idx3, _ = O.moe_ffn([gates[p] for p in perm], [ups[p] for p in perm],
+                            [downs[p] for p in perm], x, logits[:, perm], 2)
+    assert np.allclose(y3, y, rtol=1e-12)
+    assert np.array_equal(perm[idx3], idx)

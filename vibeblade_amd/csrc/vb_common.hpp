@@ -1,0 +1,110 @@
+// Shared definitions for the gfx950 GGUF quantized-matmul library (libvbhip).
+//
+// GGUF block geometry follows cpp/include/ggml_types.h:11-71 (type ids,
+// elements and bytes per block) with the on-disk layouts of the GGUF standard:
+//   Q8_0  34 B / 32 elem : fp16 d, int8 qs[32]
+//   Q4_K 144 B / 256 elem: fp16 d, fp16 dmin, u8 scales[12], u8 qs[128]
+//   Q6_K 210 B / 256 elem: u8 ql[128], u8 qh[64], i8 scales[16], fp16 d
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+namespace vb {
+
+enum : int32_t {
+    TYPE_F32 = 0,
+    TYPE_F16 = 1,
+    TYPE_Q8_0 = 8,
+    TYPE_Q4_K = 12,
+    TYPE_Q6_K = 14,
+};
+
+enum : int32_t {
+    OK = 0,
+    E_INVAL = -1,        // bad argument (shape, null pointer, bad enum)
+    E_UNSUPPORTED = -2,  // type / variant not implemented
+    E_HIP = -3,          // HIP runtime error
+    E_NOMEM = -4,        // workspace too small
+};
+
+__host__ __device__ constexpr int64_t block_elems(int32_t t) {
+    return t == TYPE_F32 || t == TYPE_F16 ? 1 : t == TYPE_Q8_0 ? 32
+         : (t == TYPE_Q4_K || t == TYPE_Q6_K) ? 256 : -1;
+}
+
+__host__ __device__ constexpr int64_t block_bytes(int32_t t) {
+    return t == TYPE_F32 ? 4 : t == TYPE_F16 ? 2 : t == TYPE_Q8_0 ? 34
+         : t == TYPE_Q4_K ? 144 : t == TYPE_Q6_K ? 210 : -1;
+}
+
+// Bytes of one row of k elements; -1 when the type is unknown or k is not a
+// whole number of blocks.
+inline int64_t row_bytes(int32_t t, int64_t k) {
+    const int64_t be = block_elems(t), bb = block_bytes(t);
+    if (be <= 0 || k <= 0 || k % be != 0) return -1;
+    return (k / be) * bb;
+}
+
+// Thread-local error text behind vb_last_error().
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+const char* last_error();
+
+// Returns E_HIP (with the message recorded) when the previous launch failed.
+int check_launch(const char* what);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---- device helpers ------------------------------------------------------
+
+// Exact fp16 -> fp32 (v_cvt_f32_f16 is exact for every input, subnormals
+// included).
+__device__ __forceinline__ float f16lo(uint32_t w) {
+    return __half2float(__ushort_as_half(static_cast<unsigned short>(w & 0xffffu)));
+}
+__device__ __forceinline__ float f16hi(uint32_t w) {
+    return __half2float(__ushort_as_half(static_cast<unsigned short>(w >> 16)));
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
+}
+
+// 16 bytes from a 4-byte-aligned address (one global_load_dwordx4).
+__device__ __forceinline__ uint4 ld_b128_a4(const uint8_t* p) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4), aligned(4)));
+    const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint32_t ld_b32(const uint8_t* p) {
+    return *reinterpret_cast<const uint32_t*>(p);
+}
+
+// 16 bytes from a 2-byte-aligned address p.  Reads the dwords covering
+// [p & ~3, (p & ~3) + 20): the caller guarantees that window is in bounds.
+__device__ __forceinline__ uint4 ld_b128_a2(const uint8_t* p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint8_t* q = reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3));
+    const uint32_t sh = static_cast<uint32_t>(a & 3u);
+    const uint4 w = ld_b128_a4(q);
+    const uint32_t w4 = ld_b32(q + 16);
+    uint4 r;
+    r.x = __builtin_amdgcn_alignbyte(w.y, w.x, sh);
+    r.y = __builtin_amdgcn_alignbyte(w.z, w.y, sh);
+    r.z = __builtin_amdgcn_alignbyte(w.w, w.z, sh);
+    r.w = __builtin_amdgcn_alignbyte(w4, w.w, sh);
+    return r;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+}  // namespace vb
