@@ -36,6 +36,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_FP16_PEAK_TFS = 2500.0  # dense fp16 MFMA, MI355X
 NCOPIES = 16
 SEED = 1234
 
@@ -68,28 +69,21 @@ def make_copies(qtype, n, k, ncopies, gen):
     return copies
 
 
-def time_gemv(qtype, n, k, steps, warmup, ncopies=NCOPIES):
-    """Returns (ms_per_step, graph_used, copies, x, ys)."""
+def time_launches(launch_fns, steps, warmup):
+    """Capture one call of every closure in `launch_fns` (each takes a stream
+    handle) in a HIP graph and replay it; returns (ms per launch, graph used,
+    launches timed).  HIP events on the replay stream bracket the timed region."""
     import torch
-    from vibeblade_amd import _lib
-    gen = torch.Generator(device="cuda").manual_seed(SEED)
-    copies = make_copies(qtype, n, k, ncopies, gen)
-    x = torch.randn(k, generator=gen, device="cuda")
-    ys = torch.empty((ncopies, n), dtype=torch.float32, device="cuda")
-    lib = _lib.load()
-
     stream = torch.cuda.Stream()
-    launches = [(c.ptr(), x.data_ptr(), ys[i].data_ptr(), n, k, qtype) for i, c in enumerate(copies)]
+    nl = len(launch_fns)
 
     def launch_all(s):
-        for a in launches:
-            rc = lib.vb_gemv(*a, s)
-            if rc != 0:
-                _lib.check("vb_gemv", rc)
+        for f in launch_fns:
+            f(s)
 
     graph = None
     with torch.cuda.stream(stream):
-        launch_all(stream.cuda_stream)  # warm the code object
+        launch_all(stream.cuda_stream)  # warm the code objects
         stream.synchronize()
         try:
             graph = torch.cuda.CUDAGraph()
@@ -98,8 +92,8 @@ def time_gemv(qtype, n, k, steps, warmup, ncopies=NCOPIES):
         except Exception as e:  # graph capture unavailable: direct launches
             print(f"[bench] graph capture failed ({e}); timing direct launches", file=sys.stderr)
             graph = None
-    reps_w = max(1, warmup // ncopies)
-    reps = max(1, (steps + ncopies - 1) // ncopies)
+    reps_w = max(1, warmup // nl)
+    reps = max(1, (steps + nl - 1) // nl)
 
     def run(nrep):
         with torch.cuda.stream(stream):
@@ -117,7 +111,57 @@ def time_gemv(qtype, n, k, steps, warmup, ncopies=NCOPIES):
     end.record(stream)
     torch.cuda.synchronize()
     ms = start.elapsed_time(end)
-    return ms / (reps * ncopies), graph is not None, reps * ncopies, copies, x, ys
+    return ms / (reps * nl), graph is not None, reps * nl
+
+
+def time_gemv(qtype, n, k, steps, warmup, ncopies=NCOPIES):
+    """Returns (ms_per_step, graph_used, steps_timed, copies, x, ys)."""
+    import torch
+    from vibeblade_amd import _lib
+    gen = torch.Generator(device="cuda").manual_seed(SEED)
+    copies = make_copies(qtype, n, k, ncopies, gen)
+    x = torch.randn(k, generator=gen, device="cuda")
+    ys = torch.empty((ncopies, n), dtype=torch.float32, device="cuda")
+    lib = _lib.load()
+
+    def mk(i, c):
+        args = (c.ptr(), x.data_ptr(), ys[i].data_ptr(), n, k, qtype)
+
+        def f(s):
+            rc = lib.vb_gemv(*args, s)
+            if rc != 0:
+                _lib.check("vb_gemv", rc)
+        return f
+    ms, graph_used, nsteps = time_launches([mk(i, c) for i, c in enumerate(copies)], steps, warmup)
+    return ms, graph_used, nsteps, copies, x, ys
+
+
+def time_gemm(m, n, k, steps, warmup, ncopies):
+    """Q4_K GEMM with fp16 X (0.1% outliers x20); returns (ms, rel-L2 of copy 0)."""
+    import torch
+    import oracle as O
+    from vibeblade_amd import _lib, ggml
+    gen = torch.Generator(device="cuda").manual_seed(SEED + m)
+    copies = make_copies(ggml.GGML_TYPE_Q4_K, n, k, ncopies, gen)
+    x = torch.randn((m, k), generator=gen, device="cuda")
+    x[torch.rand((m, k), generator=gen, device="cuda") < 0.001] *= 20.0
+    xh = x.half().contiguous()
+    ys = torch.empty((ncopies, m, n), dtype=torch.float32, device="cuda")
+    lib = _lib.load()
+
+    def mk(i, c):
+        args = (c.ptr(), xh.data_ptr(), 1, ys[i].data_ptr(), m, n, k, c.qtype, 0)
+
+        def f(s):
+            rc = lib.vb_gemm(*args, s)
+            if rc != 0:
+                _lib.check("vb_gemm", rc)
+        return f
+    ms, _, _ = time_launches([mk(i, c) for i, c in enumerate(copies)], steps, warmup)
+    w = O.dequantize(copies[0].to_numpy_bytes(), k, copies[0].qtype).astype(np.float64)
+    want = xh.float().cpu().numpy().astype(np.float64) @ w.T
+    err = O.rel_l2(ys[0].cpu().numpy(), want)
+    return ms, err
 
 
 def check_parity(qtype, n, k, copies, x, ys):
@@ -206,6 +250,18 @@ def main():
                               "frac_hbm": round(b2 / (ms2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                               "rel_l2": e2}), file=sys.stderr, flush=True)
             del cps, yy
+            torch.cuda.empty_cache()
+        for m, ncop in ((8, NCOPIES), (512, 4)):
+            ms3, e3 = time_gemm(m, 14336, 4096, 400 if m == 8 else 100, 40, ncop)
+            flops = 2.0 * m * 14336 * 4096
+            b3 = 14336 * 2304 + 2 * m * 4096 + 4 * m * 14336
+            print(json.dumps({"workload": f"Q4_K GEMM M={m} N=14336 K=4096 fp16 X",
+                              "us_per_call": round(ms3 * 1e3, 3),
+                              "TFLOP/s": round(flops / (ms3 * 1e-3) / 1e12, 2),
+                              "frac_mfma_fp16": round(flops / (ms3 * 1e-3) / 1e12 / MFMA_FP16_PEAK_TFS, 4),
+                              "GB/s": round(b3 / (ms3 * 1e-3) / 1e9, 1),
+                              "frac_hbm": round(b3 / (ms3 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                              "rel_l2": e3}), file=sys.stderr, flush=True)
             torch.cuda.empty_cache()
 
     cpu = None

@@ -1,0 +1,99 @@
+"""GPU parity of the MFMA GEMM (Q4_K weights, fp16 / fp32 activations).
+
+Bar: rel-L2 <= 5e-3 against the fp64 product of the oracle-decoded weights
+(the fp16 MFMA path rounds each weight once to fp16).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from vibeblade_amd import ggml
+from vibeblade_amd.tensor import QTensor, gemm, GEMM_SKINNY, GEMM_TILED
+
+pytestmark = pytest.mark.gpu
+
+TOL = 5e-3
+Q4K = ggml.GGML_TYPE_Q4_K
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    yield
+
+
+def ref_gemm(qt, x):
+    w = O.dequantize(qt.to_numpy_bytes(), qt.k, qt.qtype).astype(np.float64)
+    return x.astype(np.float64) @ w.T
+
+
+def make(m, n, k, seed, outliers=True):
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    if outliers:
+        mask = rng.random((m, k)) < 0.001
+        x[mask] *= 20.0
+    return QTensor.quantize(w, Q4K), x
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("m,n,k", [(1, 16, 256), (3, 50, 512), (8, 300, 1024), (16, 64, 4096),
+                                   (5, 33, 14336)])
+def test_skinny(dtype, m, n, k):
+    qt, x = make(m, n, k, m * 7 + n)
+    xt = torch.from_numpy(x).to("cuda", dtype)
+    y = gemm(qt, xt, variant=GEMM_SKINNY).cpu().numpy()
+    want = ref_gemm(qt, xt.float().cpu().numpy())
+    assert y.shape == (m, n)
+    assert O.rel_l2(y, want) <= TOL
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("m,n,k", [(17, 16, 256), (40, 130, 512), (300, 257, 1024), (256, 128, 4096),
+                                   (513, 200, 768)])
+def test_tiled(dtype, m, n, k):
+    qt, x = make(m, n, k, m + n * 3)
+    xt = torch.from_numpy(x).to("cuda", dtype)
+    y = gemm(qt, xt, variant=GEMM_TILED).cpu().numpy()
+    want = ref_gemm(qt, xt.float().cpu().numpy())
+    assert y.shape == (m, n)
+    assert O.rel_l2(y, want) <= TOL
+    # every row of the output is populated
+    assert np.all(np.abs(y).sum(axis=1) > 0)
+
+
+def test_tiled_matches_skinny_on_overlap():
+    qt, x = make(16, 96, 1024, 5)
+    xt = torch.from_numpy(x).to("cuda", torch.float16)
+    a = gemm(qt, xt, variant=GEMM_SKINNY).cpu().numpy()
+    b = gemm(qt, xt, variant=GEMM_TILED).cpu().numpy()
+    assert O.rel_l2(a, b) <= 1e-5
+
+
+def test_gemm_rejects_bad_shapes():
+    qt, x = make(4, 16, 256, 1)
+    with pytest.raises(ValueError):
+        gemm(qt, torch.zeros((4, 255), device="cuda"))
+    with pytest.raises(ValueError):
+        gemm(qt, torch.zeros((17, 256), device="cuda"), variant=GEMM_SKINNY)
+
+
+@pytest.mark.parametrize("m", [8, 512])
+def test_config_shapes(m):
+    """Q4_K GEMM at M in {8, 512}, N=14336, K=4096, fp16 X ~ N(0,1) with 0.1%
+    outliers x20, fp32 output."""
+    n, k = 14336, 4096
+    gen = torch.Generator(device="cuda").manual_seed(m)
+    w = torch.randn((n, k), generator=gen, device="cuda") * 0.02
+    qt = QTensor.quantize(w, Q4K)
+    del w
+    x = torch.randn((m, k), generator=gen, device="cuda")
+    mask = torch.rand((m, k), generator=gen, device="cuda") < 0.001
+    x[mask] *= 20.0
+    xh = x.half()
+    y = gemm(qt, xh).cpu().numpy()
+    want = ref_gemm(qt, xh.float().cpu().numpy())
+    assert O.rel_l2(y, want) <= TOL

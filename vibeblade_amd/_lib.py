@@ -36,6 +36,7 @@ SIGNATURES = {
     "vb_dequant_rows": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _vp]),
     "vb_quantize_rows": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _vp]),
     "vb_gemv": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i32, _vp]),
+    "vb_gemm": (ctypes.c_int, [_vp, _vp, _i32, _vp, _i64, _i64, _i64, _i32, _i32, _vp]),
 }
 
 _lib = None

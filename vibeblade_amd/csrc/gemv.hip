@@ -5,10 +5,10 @@
 // ever materialised: each lane owns a 64-element "unit" of a row and streams
 // the packed bytes of that unit straight into integer dot products.
 //
-// Activation encoding.  Each lane loads the 64 fp32 activations of its unit
-// once, splits them into runs (32 elements for Q4_K / Q8_0, 16 for Q6_K: the
-// weight sub-block size) and encodes every run as 16-bit fixed point with a
-// per-run fp32 scale:  x ~= s * x16,  |x16| <= 32512,  x16 = 256*xh + xl with
+// Activation encoding.  The workgroup encodes x once into LDS: the 64
+// activations of every unit are split into runs (32 elements for Q4_K / Q8_0,
+// 16 for Q6_K: the weight sub-block size) and every run becomes 16-bit fixed
+// point with a per-run fp32 scale:  x ~= s * x16,  |x16| <= 32512,  x16 = 256*xh + xl with
 // xh, xl signed bytes.  A run's dot product with the integer weight codes q
 // is then  s * (256 * sdot4(q, xh) + sdot4(q, xl))  -- exact integer
 // arithmetic on v_dot4_i32_i8, about one VALU op per weight element.  The
@@ -28,8 +28,8 @@
 // Launch shape.  A wave covers 64 consecutive units of a row ("k-tile").
 // Rows with more than one k-tile are split over `wpr` waves of the same
 // workgroup (partial sums meet in LDS); a workgroup of `wpg` waves holds
-// wpg/wpr row groups, each streaming R rows at a time so that every lane has
-// R * (row bytes per unit) in flight before it computes.
+// wpg/wpr row groups, each streaming R rows at a time with the next R rows
+// already in flight.  The grid is about one workgroup per CU.
 #include <cstdlib>
 
 #include "vb_common.hpp"
@@ -47,62 +47,6 @@ struct XSlice {
     float sum[4];    // per-run sum of the fp32 activations
     int isum[4];     // per-run sum of x16
 };
-
-// Encode 64 activations: 4 segments of 16 at x + seg*seg_stride.
-template <int RUNLEN>
-__device__ __forceinline__ void load_xslice(const float* __restrict__ x, int seg_stride, bool valid,
-                                            XSlice& xs) {
-    float v[64];
-#pragma unroll
-    for (int seg = 0; seg < 4; seg++) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (valid) f = *reinterpret_cast<const float4*>(x + seg * seg_stride + 4 * i);
-            v[16 * seg + 4 * i + 0] = f.x;
-            v[16 * seg + 4 * i + 1] = f.y;
-            v[16 * seg + 4 * i + 2] = f.z;
-            v[16 * seg + 4 * i + 3] = f.w;
-        }
-    }
-    constexpr int NRUN = 64 / RUNLEN;
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        xs.s[r] = 0.f;
-        xs.sum[r] = 0.f;
-        xs.isum[r] = 0;
-    }
-#pragma unroll
-    for (int r = 0; r < NRUN; r++) {
-        float amax = 0.f, sum = 0.f;
-#pragma unroll
-        for (int i = 0; i < RUNLEN; i++) {
-            amax = fmaxf(amax, fabsf(v[r * RUNLEN + i]));
-            sum += v[r * RUNLEN + i];
-        }
-        const float inv = amax > 0.f ? static_cast<float>(X16_MAX) / amax : 0.f;
-        xs.s[r] = amax / static_cast<float>(X16_MAX);
-        xs.sum[r] = sum;
-        int isum = 0;
-#pragma unroll
-        for (int d = 0; d < RUNLEN / 4; d++) {
-            uint32_t ph = 0, pl = 0;
-#pragma unroll
-            for (int b = 0; b < 4; b++) {
-                int q = static_cast<int>(rintf(v[r * RUNLEN + 4 * d + b] * inv));
-                q = q > X16_MAX ? X16_MAX : (q < -X16_MAX ? -X16_MAX : q);
-                isum += q;
-                const int lo = ((q + 128) & 255) - 128;
-                const int hi = (q - lo) >> 8;
-                ph |= static_cast<uint32_t>(hi & 255) << (8 * b);
-                pl |= static_cast<uint32_t>(lo & 255) << (8 * b);
-            }
-            xs.h[r * (RUNLEN / 4) + d] = ph;
-            xs.l[r * (RUNLEN / 4) + d] = pl;
-        }
-        xs.isum[r] = isum;
-    }
-}
 
 // ---- per-type unit loaders and dot products -------------------------------
 
@@ -231,78 +175,254 @@ __device__ __forceinline__ int64_t unit_x_offset(int u, int& seg_stride) {
     }
 }
 
+// ---- shared activation encoding (LDS) -------------------------------------
+//
+// The encoded slice of unit u lives in LDS as 11 uint4 "quads" at
+// xq[(kt * XQ_QUADS + q) * 64 + lane], kt = u / 64, lane = u % 64:
+// quads 0-3 = h[0..15], 4-7 = l[0..15], 8 = s[0..3], 9 = sum[0..3],
+// 10 = isum[0..3].  Consecutive lanes read consecutive 16-byte words, so the
+// per-lane ds_read_b128 loads are bank-conflict free.
+constexpr int XQ_QUADS = 11;
+constexpr int XQ_MAX_KTILES = 8;  // LDS encoding up to k = 32768
+
+// All threads of the workgroup encode the activations of k-tiles [0, nkt):
+// one task = 8 consecutive elements of a unit; the 2 (Q6_K) or 4 tasks of a
+// run sit on adjacent lanes and combine their max / sums with shuffles.
+// Loading is split from encoding so the caller can put the weight loads in
+// between: loads return in issue order, so x must be requested first or its
+// encode would wait for the weights.
+constexpr int XT_MAX = 4;  // tasks per thread held in registers
+
+struct XTasks {
+    float v[XT_MAX][8];
+};
+
 template <int TYPE>
-__device__ __forceinline__ void load_unit_x(const float* x, int u, bool valid, XSlice& xs) {
-    int seg_stride;
-    const int64_t off = unit_x_offset<TYPE>(u, seg_stride);
-    load_xslice<TYPE == TYPE_Q6_K ? 16 : 32>(x + off, seg_stride, valid, xs);
+__device__ __forceinline__ int64_t task_x_offset(int u, int p) {
+    if constexpr (TYPE == TYPE_Q6_K) {
+        int seg_stride;
+        return unit_x_offset<TYPE>(u, seg_stride) + (p >> 1) * 32 + 8 * (p & 1);
+    } else {
+        return static_cast<int64_t>(u) * 64 + 8 * p;
+    }
 }
 
+// Loads are branch-free (clamped address; the value is masked later, in
+// encode_x_task): a load under a branch makes the compiler's wait-count
+// merge fall back to vmcnt(0), and masking here would wait for the load.
+template <int TYPE>
+__device__ __forceinline__ void load_x_task(const float* __restrict__ x, int units, int task, float* v) {
+    const int u = task >> 3, p = task & 7;
+    const int64_t off = task_x_offset<TYPE>(u < units ? u : units - 1, p);
+    const float4 a = *reinterpret_cast<const float4*>(x + off);
+    const float4 b = *reinterpret_cast<const float4*>(x + off + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+template <int TYPE>
+__device__ __forceinline__ void encode_x_task(int task, int units, const float* vin, uint4* xq) {
+    constexpr int RUNLEN = TYPE == TYPE_Q6_K ? 16 : 32;
+    constexpr int TPR = RUNLEN / 8;
+    const int u = task >> 3, p = task & 7;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = u < units ? vin[i] : 0.f;
+    float amax = 0.f, sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        amax = fmaxf(amax, fabsf(v[i]));
+        sum += v[i];
+    }
+#pragma unroll
+    for (int m = 1; m < TPR; m <<= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+        sum += __shfl_xor(sum, m, 64);
+    }
+    const float inv = amax > 0.f ? static_cast<float>(X16_MAX) / amax : 0.f;
+    uint32_t ph[2] = {0, 0}, pl[2] = {0, 0};
+    int isum = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        int q = static_cast<int>(rintf(v[i] * inv));
+        q = q > X16_MAX ? X16_MAX : (q < -X16_MAX ? -X16_MAX : q);
+        isum += q;
+        const int lo = ((q + 128) & 255) - 128;
+        const int hi = (q - lo) >> 8;
+        ph[i >> 2] |= static_cast<uint32_t>(hi & 255) << (8 * (i & 3));
+        pl[i >> 2] |= static_cast<uint32_t>(lo & 255) << (8 * (i & 3));
+    }
+#pragma unroll
+    for (int m = 1; m < TPR; m <<= 1) isum += __shfl_xor(isum, m, 64);
+    const int kt = u >> 6, ln = u & 63;
+    uint4* base = xq + static_cast<size_t>(kt) * XQ_QUADS * 64 + ln;
+    reinterpret_cast<uint2*>(&base[(p >> 1) * 64])[p & 1] = make_uint2(ph[0], ph[1]);
+    reinterpret_cast<uint2*>(&base[(4 + (p >> 1)) * 64])[p & 1] = make_uint2(pl[0], pl[1]);
+    if (p % TPR == 0) {
+        const int r = p / TPR;
+        reinterpret_cast<float*>(&base[8 * 64])[r] = amax / static_cast<float>(X16_MAX);
+        reinterpret_cast<float*>(&base[9 * 64])[r] = sum;
+        reinterpret_cast<int*>(&base[10 * 64])[r] = isum;
+    }
+}
+
+// Register path: at most XT_MAX tasks per thread.  The task count (nkt*512)
+// and the thread count are multiples of 64, so each wave's shuffles see all
+// 64 lanes active.
+template <int TYPE>
+__device__ __forceinline__ void prefetch_x(const float* __restrict__ x, int units, int nkt, XTasks& t) {
+    const int ntasks = nkt * 64 * 8;
+#pragma unroll
+    for (int i = 0; i < XT_MAX; i++) {
+        const int task = threadIdx.x + i * blockDim.x;
+        load_x_task<TYPE>(x, units, task < ntasks ? task : ntasks - 1, t.v[i]);
+    }
+}
+
+template <int TYPE>
+__device__ __forceinline__ void encode_x_regs(int units, int nkt, const XTasks& t, uint4* xq) {
+    const int ntasks = nkt * 64 * 8;
+#pragma unroll
+    for (int i = 0; i < XT_MAX; i++) {
+        const int task = threadIdx.x + i * blockDim.x;
+        if (task < ntasks) encode_x_task<TYPE>(task, units, t.v[i], xq);
+    }
+}
+
+// Loop path for more tasks than fit in registers.
+template <int TYPE>
+__device__ void encode_x_loop(const float* __restrict__ x, int units, int nkt, uint4* xq) {
+    const int ntasks = nkt * 64 * 8;
+    for (int task = threadIdx.x; task < ntasks; task += blockDim.x) {
+        float v[8];
+        load_x_task<TYPE>(x, units, task, v);
+        encode_x_task<TYPE>(task, units, v, xq);
+    }
+}
+
+__device__ __forceinline__ void read_xslice(const uint4* xq, int kt, int lane, XSlice& xs) {
+    const uint4* q = xq + static_cast<size_t>(kt) * XQ_QUADS * 64 + lane;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint4 h = q[i * 64], l = q[(4 + i) * 64];
+        xs.h[4 * i] = h.x; xs.h[4 * i + 1] = h.y; xs.h[4 * i + 2] = h.z; xs.h[4 * i + 3] = h.w;
+        xs.l[4 * i] = l.x; xs.l[4 * i + 1] = l.y; xs.l[4 * i + 2] = l.z; xs.l[4 * i + 3] = l.w;
+    }
+    const uint4 s = q[8 * 64], sm = q[9 * 64], is = q[10 * 64];
+    xs.s[0] = __uint_as_float(s.x); xs.s[1] = __uint_as_float(s.y);
+    xs.s[2] = __uint_as_float(s.z); xs.s[3] = __uint_as_float(s.w);
+    xs.sum[0] = __uint_as_float(sm.x); xs.sum[1] = __uint_as_float(sm.y);
+    xs.sum[2] = __uint_as_float(sm.z); xs.sum[3] = __uint_as_float(sm.w);
+    xs.isum[0] = static_cast<int>(is.x); xs.isum[1] = static_cast<int>(is.y);
+    xs.isum[2] = static_cast<int>(is.z); xs.isum[3] = static_cast<int>(is.w);
+}
+
+// One workgroup: `wpg` waves = (wpg / wpr) row groups x wpr k-waves.  A row
+// group walks its rows in NB batches of R; k-wave kw covers k-tiles kw,
+// kw + wpr, ...  Work is flattened into steps (batch, tile); the loads of
+// step s+1 are issued before step s is computed, and the loads of step 0
+// before the activations are encoded, so HBM latency overlaps both.
 template <int TYPE, int R>
 __global__ void __launch_bounds__(512) gemv_q_kernel(const uint8_t* __restrict__ w,
                                                      const float* __restrict__ x,
                                                      float* __restrict__ y, int64_t n, int64_t rb,
-                                                     int units, int n_ktiles, int wpr,
-                                                     int rows_per_group) {
+                                                     int units, int n_ktiles, int wpr, int nb) {
     using Unit = typename UnitOf<TYPE>::T;
+    extern __shared__ uint4 xq[];
     __shared__ float red[8][R];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int groups = (blockDim.x >> 6) / wpr;
     const int g = wave / wpr, kw = wave - g * wpr;
-    const int64_t row0 =
-        (static_cast<int64_t>(blockIdx.x) * groups + g) * static_cast<int64_t>(rows_per_group);
-    const bool one_tile = n_ktiles <= wpr;
+    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * groups + g) * static_cast<int64_t>(R) * nb;
+    const int ntw = (n_ktiles + wpr - 1) / wpr;  // tiles per k-wave (uniform loop bound)
+    const int nsteps = nb * ntw;
+
+    // Branch-free: out-of-range units and rows load clamped (valid) addresses
+    // and are masked in compute().
+    auto issue = [&](Unit* v, int step) {
+        const int b = step / ntw, i = step - (step / ntw) * ntw;
+        int u = (kw + i * wpr) * 64 + lane;
+        u = u < units ? u : units - 1;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            int64_t row = row0 + static_cast<int64_t>(b) * R + r;
+            row = row < n ? row : n - 1;
+            load_unit(w + row * rb, u, v[r]);
+        }
+    };
+
+    // x first, then the first two steps of weights, then the encode: the
+    // encode only waits for x, and the weights are in flight meanwhile.
+    Unit va[R], vb[R];
+    const bool x_in_regs = n_ktiles * 512 <= XT_MAX * static_cast<int>(blockDim.x);
+    XTasks xt;
+    if (x_in_regs) prefetch_x<TYPE>(x, units, n_ktiles, xt);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(va, 0);
+    issue(vb, nsteps > 1 ? 1 : 0);  // a repeat of step 0 when there is no step 1 (cache hits)
+    __builtin_amdgcn_sched_barrier(0);  // keep the weight loads ahead of the encode
+    if (x_in_regs)
+        encode_x_regs<TYPE>(units, n_ktiles, xt, xq);
+    else
+        encode_x_loop<TYPE>(x, units, n_ktiles, xq);
+    __syncthreads();
 
     XSlice xs;
-    if (one_tile) {
-        const int u = kw * 64 + lane;
-        load_unit_x<TYPE>(x, u, kw < n_ktiles && u < units, xs);
-    }
-    for (int rr = 0; rr < rows_per_group; rr += R) {
-        float acc[R];
+    if (ntw == 1 && kw < n_ktiles) read_xslice(xq, kw, lane, xs);
+    float acc[R];
 #pragma unroll
-        for (int r = 0; r < R; r++) acc[r] = 0.f;
-        for (int kt = kw; kt < n_ktiles; kt += wpr) {
-            const int u = kt * 64 + lane;
-            const bool valid = u < units;
-            if (!one_tile) load_unit_x<TYPE>(x, u, valid, xs);
-            if (valid) {
-                Unit v[R];
+    for (int r = 0; r < R; r++) acc[r] = 0.f;
+
+    auto compute = [&](const Unit* v, int step) {
+        const int b = step / ntw, i = step - (step / ntw) * ntw;
+        const int kt = kw + i * wpr;
+        const int u = kt * 64 + lane;
+        if (ntw > 1 && kt < n_ktiles) read_xslice(xq, kt, lane, xs);
+        if (kt < n_ktiles && u < units) {
 #pragma unroll
-                for (int r = 0; r < R; r++) {
-                    int64_t row = row0 + rr + r;
-                    row = row < n ? row : n - 1;
-                    load_unit(w + row * rb, u, v[r]);
+            for (int r = 0; r < R; r++) acc[r] += unit_dot(v[r], xs, u);
+        }
+        if (i == ntw - 1) {  // batch complete: reduce and store
+            const int64_t rbase = row0 + static_cast<int64_t>(b) * R;
+            float tot[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                tot[r] = wave_sum_dpp(acc[r]);
+                acc[r] = 0.f;
+            }
+            if (wpr == 1) {
+                if (lane == 0) {
+#pragma unroll
+                    for (int r = 0; r < R; r++)
+                        if (rbase + r < n) y[rbase + r] = tot[r];
                 }
+            } else {
+                if (lane == 0) {
 #pragma unroll
-                for (int r = 0; r < R; r++) acc[r] += unit_dot(v[r], xs, u);
+                    for (int r = 0; r < R; r++) red[wave][r] = tot[r];
+                }
+                __syncthreads();
+                if (kw == 0 && lane < R) {
+                    float s2 = 0.f;
+                    for (int j = 0; j < wpr; j++) s2 += red[wave + j][lane];
+                    if (rbase + lane < n) y[rbase + lane] = s2;
+                }
+                __syncthreads();
             }
         }
-#pragma unroll
-        for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
-        if (wpr == 1) {
-            if (lane == 0) {
-#pragma unroll
-                for (int r = 0; r < R; r++) {
-                    const int64_t row = row0 + rr + r;
-                    if (row < n) y[row] = acc[r];
-                }
-            }
-        } else {
-            if (lane == 0) {
-#pragma unroll
-                for (int r = 0; r < R; r++) red[wave][r] = acc[r];
-            }
-            __syncthreads();
-            if (kw == 0 && lane < R) {
-                float s = 0.f;
-                for (int j = 0; j < wpr; j++) s += red[wave + j][lane];
-                const int64_t row = row0 + rr + lane;
-                if (row < n) y[row] = s;
-            }
-            __syncthreads();
-        }
+    };
+
+    // Two steps in flight.  The refill of vb near the end repeats the last
+    // step instead of branching (a branch around loads costs the overlap).
+    int s = 0;
+    for (; s + 2 < nsteps; s += 2) {
+        compute(va, s);
+        issue(va, s + 2);
+        compute(vb, s + 1);
+        issue(vb, s + 3 < nsteps ? s + 3 : nsteps - 1);
     }
+    compute(va, s);
+    if (s + 1 < nsteps) compute(vb, s + 1);
 }
 
 // F32 / F16 weights: plain fp32 dot products, one wave per R rows.
@@ -339,45 +459,86 @@ __global__ void __launch_bounds__(256) gemv_plain_kernel(const uint8_t* __restri
     }
 }
 
-constexpr int GEMV_R = 4;
-
 struct GemvShape {
-    int units, n_ktiles, wpr, wpg, rows_per_group;
+    int units, n_ktiles, wpr, wpg, r, nb;
     int64_t grid;
+    size_t lds;
 };
 
-// Launch geometry for n rows of `units` 64-element units.  VB_GEMV_CFG="wpg,nb"
-// overrides the waves per workgroup and the R-row batches per row group (for
-// tuning sweeps).
-GemvShape gemv_shape(int64_t n, int units) {
+constexpr int kNumCUs = 256;
+// rows per step (two steps are in flight); Q6_K units are larger, and R = 4
+// would spill
+template <int TYPE>
+constexpr int max_rows() { return TYPE == TYPE_Q6_K ? 3 : 4; }
+
+// Launch geometry: for each candidate workgroup size (waves), rows are split
+// so the grid covers the CUs about once with R <= 4 rows per step; the
+// candidate with the fewest rows per CU wins (ties: more waves).
+// VB_GEMV_CFG="wpg,r,nb" overrides (tuning sweeps).
+GemvShape gemv_shape(int64_t n, int units, int max_r) {
     GemvShape s;
     s.units = units;
     s.n_ktiles = (units + 63) / 64;
     s.wpr = s.n_ktiles <= 1 ? 1 : (s.n_ktiles <= 2 ? 2 : 4);
-    int wpg = 4, nb = 1;
-    if (const char* cfg = std::getenv("VB_GEMV_CFG")) {
-        int a = 0, b = 0;
-        if (std::sscanf(cfg, "%d,%d", &a, &b) == 2 && a >= 1 && a <= 8 && b >= 1) {
-            wpg = a;
-            nb = b;
+    int64_t best_cost = -1;
+    for (int wpg = 8; wpg >= 4; wpg--) {
+        if (wpg % s.wpr) continue;
+        const int groups = wpg / s.wpr;
+        int64_t per_group = (n + static_cast<int64_t>(kNumCUs) * groups - 1) /
+                            (static_cast<int64_t>(kNumCUs) * groups);
+        if (per_group < 1) per_group = 1;
+        const int r = static_cast<int>(per_group < max_r ? per_group : max_r);
+        const int nb = static_cast<int>((per_group + r - 1) / r);
+        const int64_t rows_per_wg = static_cast<int64_t>(groups) * r * nb;
+        const int64_t grid = (n + rows_per_wg - 1) / rows_per_wg;
+        const int64_t cost = ((grid + kNumCUs - 1) / kNumCUs) * rows_per_wg;
+        if (best_cost < 0 || cost < best_cost) {
+            best_cost = cost;
+            s.wpg = wpg;
+            s.r = r;
+            s.nb = nb;
         }
     }
-    if (wpg % s.wpr != 0) wpg = s.wpr * ((wpg + s.wpr - 1) / s.wpr);
-    if (wpg > 8) wpg = 8;
-    s.wpg = wpg;
-    s.rows_per_group = GEMV_R * nb;
-    const int64_t rows_per_wg = static_cast<int64_t>(wpg / s.wpr) * s.rows_per_group;
+    if (const char* cfg = std::getenv("VB_GEMV_CFG")) {
+        int a = 0, b = 0, c = 0;
+        if (std::sscanf(cfg, "%d,%d,%d", &a, &b, &c) == 3 && a >= 1 && a <= 8 && b >= 1 && b <= max_r &&
+            c >= 1 && a % s.wpr == 0) {
+            s.wpg = a;
+            s.r = b;
+            s.nb = c;
+        }
+    }
+    const int64_t rows_per_wg = static_cast<int64_t>(s.wpg / s.wpr) * s.r * s.nb;
     s.grid = (n + rows_per_wg - 1) / rows_per_wg;
+    s.lds = static_cast<size_t>(s.n_ktiles) * XQ_QUADS * 64 * sizeof(uint4);
     return s;
+}
+
+template <int TYPE, int R>
+int launch_gemv_r(const GemvShape& s, const void* w, const float* x, float* y, int64_t n, int64_t rb,
+                  hipStream_t st) {
+    gemv_q_kernel<TYPE, R><<<dim3(static_cast<uint32_t>(s.grid)), dim3(64 * s.wpg), s.lds, st>>>(
+        static_cast<const uint8_t*>(w), x, y, n, rb, s.units, s.n_ktiles, s.wpr, s.nb);
+    return check_launch("vb_gemv");
 }
 
 template <int TYPE>
 int launch_gemv_q(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t rb,
                   hipStream_t st) {
-    const GemvShape s = gemv_shape(n, static_cast<int>(k / 64));
-    gemv_q_kernel<TYPE, GEMV_R><<<dim3(static_cast<uint32_t>(s.grid)), dim3(64 * s.wpg), 0, st>>>(
-        static_cast<const uint8_t*>(w), x, y, n, rb, s.units, s.n_ktiles, s.wpr, s.rows_per_group);
-    return check_launch("vb_gemv");
+    const GemvShape s = gemv_shape(n, static_cast<int>(k / 64), max_rows<TYPE>());
+    if (s.n_ktiles > XQ_MAX_KTILES) {
+        set_error("vb_gemv: k=%lld exceeds the supported maximum of %d", static_cast<long long>(k),
+                  XQ_MAX_KTILES * 64 * 64);
+        return E_UNSUPPORTED;
+    }
+    switch (s.r) {
+    case 1: return launch_gemv_r<TYPE, 1>(s, w, x, y, n, rb, st);
+    case 2: return launch_gemv_r<TYPE, 2>(s, w, x, y, n, rb, st);
+    case 3: return launch_gemv_r<TYPE, 3>(s, w, x, y, n, rb, st);
+    default:
+        if constexpr (max_rows<TYPE>() >= 4) return launch_gemv_r<TYPE, 4>(s, w, x, y, n, rb, st);
+        return launch_gemv_r<TYPE, 3>(s, w, x, y, n, rb, st);
+    }
 }
 
 }  // namespace

@@ -1,0 +1,103 @@
+// Building blocks for the Q4_K x fp16 MFMA kernels (gemm.hip, moe.hip).
+//
+// Instruction: v_mfma_f32_16x16x32_f16 (gfx950), D[16x16] += A[16x32] B[32x16]
+// with fp32 accumulation.  Operand layout for lane l (0..63):
+//   A: row i = l % 16, k = 8 * (l / 16) + 0..7  (8 halves, 4 VGPRs)
+//   B: col j = l % 16, k = 8 * (l / 16) + 0..7
+//   D: col j = l % 16, rows i = 4 * (l / 16) + 0..3 (4 floats)
+// The k order inside a lane's 8 halves is irrelevant to the product as long
+// as A and B agree, so both use the order sigma = (0, 2, 1, 3, 4, 6, 5, 7):
+// it lets the weight nibbles of a byte pair land in one half2 with one
+// mask-and-or (see q4k_bfrags).
+//
+// Q4_K B fragments.  A 32-element MFMA k-step is exactly one Q4_K sub-block.
+// Lane group g = l / 16 loads the 8 bytes qs[32c + 8g, +8) of chunk c; their
+// low nibbles are elements 8g..8g+7 of sub-block 2c, their high nibbles the
+// same elements of sub-block 2c+1, so one 8-byte load feeds two k-steps.  A
+// nibble q becomes the half 1024 + q by or-ing in 0x6400 (exact), then
+// w = (h - 1024) * (d*sc) - dmin*m with packed fp16 ops: the weight is
+// rounded once to fp16 (rel. error <= 2^-11).
+#pragma once
+
+#include "vb_common.hpp"
+
+namespace vb {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+union Frag {
+    half8_t h;
+    uint32_t u[4];
+};
+
+__device__ __forceinline__ float4_t mfma16x16x32(const Frag& a, const Frag& b, float4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, b.h, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t h2bits(half2_t v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ half2_t bits2h(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
+
+// Apply sigma to 8 consecutive halves held as 4 dwords (x01, x23, x45, x67).
+__device__ __forceinline__ void sigma_permute(uint32_t x01, uint32_t x23, uint32_t x45, uint32_t x67,
+                                              uint32_t* o) {
+    o[0] = __builtin_amdgcn_perm(x23, x01, 0x05040100u);  // (x0, x2)
+    o[1] = __builtin_amdgcn_perm(x23, x01, 0x07060302u);  // (x1, x3)
+    o[2] = __builtin_amdgcn_perm(x67, x45, 0x05040100u);  // (x4, x6)
+    o[3] = __builtin_amdgcn_perm(x67, x45, 0x07060302u);  // (x5, x7)
+}
+
+// 8 fp32 -> 8 fp16 (round to nearest even), sigma order.
+__device__ __forceinline__ void f32x8_to_frag(const float4& a, const float4& b, uint32_t* o) {
+    auto pk = [](float lo, float hi) {
+        const uint32_t l = __half_as_ushort(__float2half_rn(lo));
+        const uint32_t h = __half_as_ushort(__float2half_rn(hi));
+        return l | (h << 16);
+    };
+    o[0] = pk(a.x, a.z);
+    o[1] = pk(a.y, a.w);
+    o[2] = pk(b.x, b.z);
+    o[3] = pk(b.y, b.w);
+}
+
+// Per-row scale pair of Q4_K sub-blocks 2c and 2c+1 as fp16 half2 splats:
+// ds[i] = d * sc_(2c+i), nm[i] = -(dmin * m_(2c+i)).  hd = the 16-byte block
+// header (d, dmin, scales[12]); c is uniform across the wave.
+__device__ __forceinline__ void q4k_chunk_scales(const uint4& hd, int c, half2_t* ds, half2_t* nm) {
+    const uint32_t sh = 16u * static_cast<uint32_t>(c & 1);
+    const uint32_t A = hd.y >> sh, B = hd.z >> sh, C = hd.w >> sh;
+    uint32_t SC, M;
+    if (c < 2) {
+        SC = A & 0x3F3Fu;
+        M = B & 0x3F3Fu;
+    } else {
+        SC = (C & 0x0F0Fu) | ((A >> 2) & 0x3030u);
+        M = ((C >> 4) & 0x0F0Fu) | ((B >> 2) & 0x3030u);
+    }
+    const float d = f16lo(hd.x), dmin = f16hi(hd.x);
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const _Float16 s = static_cast<_Float16>(d * static_cast<float>((SC >> (8 * i)) & 0xFFu));
+        const _Float16 m = static_cast<_Float16>(-(dmin * static_cast<float>((M >> (8 * i)) & 0xFFu)));
+        ds[i] = half2_t{s, s};
+        nm[i] = half2_t{m, m};
+    }
+}
+
+// Dequantize the two B fragments (sub-blocks 2c, 2c+1) of one lane from its
+// 8 qs bytes (q0 = bytes 0-3, q1 = bytes 4-7).
+__device__ __forceinline__ void q4k_bfrags(uint32_t q0, uint32_t q1, const half2_t* ds,
+                                           const half2_t* nm, Frag& lo, Frag& hi) {
+    const half2_t k1024 = half2_t{static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+    const uint32_t src[4] = {q0, q0 >> 8, q1, q1 >> 8};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const half2_t a = bits2h((src[i] & 0x000F000Fu) | 0x64006400u) - k1024;
+        const half2_t b = bits2h(((src[i] >> 4) & 0x000F000Fu) | 0x64006400u) - k1024;
+        lo.u[i] = h2bits(__builtin_elementwise_fma(a, ds[0], nm[0]));
+        hi.u[i] = h2bits(__builtin_elementwise_fma(b, ds[1], nm[1]));
+    }
+}
+
+}  // namespace vb

@@ -107,4 +107,24 @@ __device__ __forceinline__ T wave_sum(T v) {
     return v;
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 64 lanes of a wave; the result is wave-uniform.  Quad
+// butterflies, then half-row and row mirrors (DPP, no LDS traffic), then the
+// four row sums through v_readlane.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);  // row_half_mirror
+    v += dpp_f<0x140>(v);  // row_mirror
+    const int b = __float_as_int(v);
+    return (__int_as_float(__builtin_amdgcn_readlane(b, 0)) +
+            __int_as_float(__builtin_amdgcn_readlane(b, 16))) +
+           (__int_as_float(__builtin_amdgcn_readlane(b, 32)) +
+            __int_as_float(__builtin_amdgcn_readlane(b, 48)));
+}
+
 }  // namespace vb

@@ -116,3 +116,29 @@ def gemv(w: QTensor, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.
         out = torch.empty(w.rows, dtype=torch.float32, device=w.device)
     _lib.call("vb_gemv", w.ptr(), x.data_ptr(), out.data_ptr(), w.rows, w.k, w.qtype, _stream())
     return out
+
+
+X_F32 = 0
+X_F16 = 1
+GEMM_AUTO, GEMM_SKINNY, GEMM_TILED = 0, 1, 2
+
+
+def gemm(w: QTensor, x: torch.Tensor, out: torch.Tensor | None = None,
+         variant: int = GEMM_AUTO) -> torch.Tensor:
+    """Y = X W^T for a batch of activations X (m, k) fp16 or fp32 -> (m, rows) fp32
+    (MFMA path; fp16 operands, fp32 accumulation)."""
+    if not isinstance(x, torch.Tensor):
+        x = torch.from_numpy(np.ascontiguousarray(x))
+    x = x.to(w.device)
+    if x.dtype not in (torch.float16, torch.float32):
+        x = x.to(torch.float32)
+    x = x.contiguous()
+    if x.dim() != 2 or x.shape[1] != w.k:
+        raise ValueError(f"gemm: x must be (m, {w.k}), got {tuple(x.shape)}")
+    m = x.shape[0]
+    if out is None:
+        out = torch.empty((m, w.rows), dtype=torch.float32, device=w.device)
+    xdt = X_F16 if x.dtype == torch.float16 else X_F32
+    _lib.call("vb_gemm", w.ptr(), x.data_ptr(), xdt, out.data_ptr(), m, w.rows, w.k, w.qtype,
+              variant, _stream())
+    return out
