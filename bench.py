@@ -164,6 +164,81 @@ def time_gemm(m, n, k, steps, warmup, ncopies):
     return ms, err
 
 
+def time_sparse(layout, steps, warmup, ncopies=8):
+    """TurboSparse FFN, H=4096, I=14336, Q4_K, S ~ Bernoulli(0.1), relu(g)*relu(u).
+    Returns (ms per call, |S|, algorithmic bytes)."""
+    import torch
+    from vibeblade_amd import _lib, ggml
+    from vibeblade_amd.tensor import QTensor, ACT_RELU2
+    h, i = 4096, 14336
+    gen = torch.Generator(device="cuda").manual_seed(SEED + 4)
+    sets = []
+    for _ in range(ncopies):
+        g = QTensor.quantize(torch.randn((i, h), generator=gen, device="cuda") * 0.02, ggml.GGML_TYPE_Q4_K)
+        u = QTensor.quantize(torch.randn((i, h), generator=gen, device="cuda") * 0.02, ggml.GGML_TYPE_Q4_K)
+        dshape = (h, i) if layout == 0 else (i, h)
+        d = QTensor.quantize(torch.randn(dshape, generator=gen, device="cuda") * 0.02, ggml.GGML_TYPE_Q4_K)
+        sets.append((g, u, d))
+    rng = np.random.default_rng(42)
+    s = torch.from_numpy(np.flatnonzero(rng.random(i) < 0.10).astype(np.int32)).cuda()
+    x = torch.randn(h, generator=gen, device="cuda")
+    y = torch.empty(h, device="cuda")
+    lib = _lib.load()
+    nbytes = lib.vb_sparse_ffn_workspace(h, i, s.numel(), layout)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+
+    def mk(g, u, d):
+        def f(st):
+            rc = lib.vb_sparse_ffn(g.ptr(), u.ptr(), d.ptr(), layout, x.data_ptr(), s.data_ptr(), s.numel(),
+                                   ACT_RELU2, y.data_ptr(), h, i, g.qtype, ws.data_ptr(), ws.numel(), st)
+            if rc != 0:
+                _lib.check("vb_sparse_ffn", rc)
+        return f
+    ms, _, _ = time_launches([mk(*t) for t in sets], steps, warmup)
+    n_s = int(s.numel())
+    rb = 2304
+    down_b = h * 8064 if layout == 0 else n_s * rb
+    ab = 2 * n_s * rb + down_b + 4 * h + 4 * h + 4 * n_s
+    return ms, n_s, ab
+
+
+def time_moe(steps, warmup):
+    """8 Q4_K experts (gate/up 14336x4096, down 4096x14336), 16 tokens, top-2.
+    Returns (ms per call, experts hit, algorithmic bytes)."""
+    import torch
+    from vibeblade_amd import ggml
+    from vibeblade_amd.tensor import QTensor, moe_grouped_ffn
+    import ctypes
+    from vibeblade_amd import _lib
+    e_n, h, i, t, topk = 8, 4096, 14336, 16, 2
+    gen = torch.Generator(device="cuda").manual_seed(SEED + 5)
+    q = lambda shape: QTensor.quantize(torch.randn(shape, generator=gen, device="cuda") * 0.02, ggml.GGML_TYPE_Q4_K)
+    gates = [q((i, h)) for _ in range(e_n)]
+    ups = [q((i, h)) for _ in range(e_n)]
+    downs = [q((h, i)) for _ in range(e_n)]
+    x = torch.randn((t, h), generator=gen, device="cuda")
+    logits = torch.randn((t, e_n), generator=gen, device="cuda")
+    y, idx, w = moe_grouped_ffn(gates, ups, downs, x, logits, topk)
+    hit = len(set(idx.cpu().numpy().ravel().tolist()))
+    lib = _lib.load()
+    arr = ctypes.c_void_p * e_n
+    pg, pu, pd = arr(*[g.ptr() for g in gates]), arr(*[u.ptr() for u in ups]), arr(*[d.ptr() for d in downs])
+    nbytes = lib.vb_moe_workspace(t, topk, h, i)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    yo = torch.empty((t, h), device="cuda")
+    vp = ctypes.c_void_p
+
+    def f(st):
+        rc = lib.vb_moe_grouped_ffn(ctypes.cast(pg, vp), ctypes.cast(pu, vp), ctypes.cast(pd, vp), e_n,
+                                    x.data_ptr(), t, logits.data_ptr(), topk, yo.data_ptr(), None, None, h, i,
+                                    ggml.GGML_TYPE_Q4_K, ws.data_ptr(), ws.numel(), st)
+        if rc != 0:
+            _lib.check("vb_moe_grouped_ffn", rc)
+    ms, _, _ = time_launches([f], steps, warmup)
+    ab = hit * 3 * i * 2304 + t * h * 4 * 2 + t * e_n * 4
+    return ms, hit, ab
+
+
 def check_parity(qtype, n, k, copies, x, ys):
     """Oracle check of the first copy's output (the timed results)."""
     import oracle as O
@@ -251,6 +326,21 @@ def main():
                               "rel_l2": e2}), file=sys.stderr, flush=True)
             del cps, yy
             torch.cuda.empty_cache()
+        for layout in (1, 0):
+            ms4, n_s, b4 = time_sparse(layout, 400, 40)
+            print(json.dumps({"workload": f"TurboSparse FFN H=4096 I=14336 |S|={n_s} down_layout={layout}",
+                              "us_per_call": round(ms4 * 1e3, 3), "alg_bytes": b4,
+                              "GB/s": round(b4 / (ms4 * 1e-3) / 1e9, 1),
+                              "frac_hbm": round(b4 / (ms4 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}),
+                  file=sys.stderr, flush=True)
+            torch.cuda.empty_cache()
+        ms5, hit, b5 = time_moe(50, 5)
+        print(json.dumps({"workload": f"MoE 8x Q4_K experts, 16 tokens top-2 ({hit} experts hit)",
+                          "us_per_call": round(ms5 * 1e3, 3), "alg_bytes": b5,
+                          "GB/s": round(b5 / (ms5 * 1e-3) / 1e9, 1),
+                          "frac_hbm": round(b5 / (ms5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}),
+              file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
         for m, ncop in ((8, NCOPIES), (512, 4)):
             ms3, e3 = time_gemm(m, 14336, 4096, 400 if m == 8 else 100, 40, ncop)
             flops = 2.0 * m * 14336 * 4096

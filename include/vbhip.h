@@ -100,6 +100,65 @@ int vb_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k,
 int vb_gemm(const void* w, const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n,
             int64_t k, int32_t ggml_type, int32_t variant, void* stream);
 
+/* ---- TurboSparse activation-sparse FFN, one token ------------------------
+ * y[h] = sum_{r < n_active} act(g_r, u_r) * Wd[:, active[r]] with
+ * g_r = Wg[active[r], :] . x, u_r = Wu[active[r], :] . x; only the rows of
+ * the active set are read from Wg / Wu.  active: sorted ascending, unique,
+ * within [0, i) (indices outside are clamped, never dereferenced).
+ * act_kind: 0 = silu(g) * u (vibeblade/sparse.py:269-272),
+ *           1 = relu(g) * relu(u) (ReLU after both projections).
+ * down_layout: 0 = GGUF down, Wd is h rows x i (all of Wd is read);
+ *              1 = neuron-major down, Wd holds W_down^T as i rows x h and
+ *                  only the active rows are read (Q4_K only).
+ * Wg / Wu: i rows x h.  Replaces sparse_ffn_silu's up / down steps
+ * (vibeblade/sparse.py:261-276) and ffn_silu(sparse_mask=)
+ * (vibeblade/transformer.py:177-208).  workspace: at least
+ * vb_sparse_ffn_workspace(h, i, n_active, down_layout) bytes. */
+int64_t vb_sparse_ffn_workspace(int64_t h, int64_t i, int32_t n_active, int32_t down_layout);
+int vb_sparse_ffn(const void* wg, const void* wu, const void* wd, int32_t down_layout,
+                  const float* x, const int32_t* active, int32_t n_active, int32_t act_kind,
+                  float* y, int64_t h, int64_t i, int32_t ggml_type, void* workspace,
+                  size_t workspace_bytes, void* stream);
+
+/* out_idx[0..k) = indices of the k largest v[i], ascending index order (ties
+ * at the threshold resolve to the lowest indices).  The top-k neuron
+ * prediction of sparse_ffn_silu (vibeblade/sparse.py:250-261) and
+ * topk_activation_mask (:142-168), on the device. */
+int vb_topk_indices(const float* v, int64_t n, int32_t k, int32_t* out_idx, void* stream);
+
+/* ---- MoE expert-grouped FFN ---------------------------------------------
+ * For each of n_tokens tokens: p = softmax(clamp(logits_t, -50, 50)), top-k
+ * experts by p, weights renormalised to sum 1 (vibeblade/moe.py:170-206,
+ * cpp/src/fast_model.cpp:534-548); y_t = sum_k w_tk *
+ * Wd_e (silu(Wg_e x_t) * (Wu_e x_t)) with e = e_tk
+ * (vibeblade/moe_executor.py:331-344, vibeblade/moe.py:457-482,
+ * cpp/src/fast_model.cpp:552-572).  wg / wu / wd: host arrays of n_exp
+ * device pointers; Wg_e, Wu_e: i rows x h, Wd_e: h rows x i (GGUF layout,
+ * Q4_K).  x: n_tokens x h fp32; router_logits: n_tokens x n_exp fp32;
+ * y: n_tokens x h fp32; out_idx / out_w (optional, may be NULL):
+ * n_tokens x topk routing result.  Experts may also be F32 (same shapes).
+ * Replaces HotColdExecutor.dispatch's
+ * per-expert loop (vibeblade/moe_executor.py:139-329) and the engine's MoE
+ * branch (cpp/src/fast_model.cpp:844-902).  Limits: n_exp <= 64,
+ * topk <= 8, n_tokens * topk <= 1024.  workspace: at least
+ * vb_moe_workspace(n_tokens, topk, h, i) bytes. */
+int64_t vb_moe_workspace(int32_t n_tokens, int32_t topk, int64_t h, int64_t i);
+int vb_moe_grouped_ffn(const void* const* wg, const void* const* wu, const void* const* wd,
+                       int32_t n_exp, const float* x, int32_t n_tokens, const float* router_logits,
+                       int32_t topk, float* y, int32_t* out_idx, float* out_w, int64_t h, int64_t i,
+                       int32_t ggml_type, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Routing only: out_idx / out_w (n_tokens x topk) as vb_moe_grouped_ffn
+ * computes them (ExpertRouter.route, vibeblade/moe.py:170-206, with the
+ * selected experts ordered by descending weight). */
+int vb_moe_route(const float* router_logits, int32_t n_tokens, int32_t n_exp, int32_t topk,
+                 int32_t* out_idx, float* out_w, void* stream);
+
+/* ---- elementwise ----------------------------------------------------------
+ * y = silu(x) (kind 0) or max(x, 0) (kind 1); GPUBackend.silu / .drelu
+ * (vibeblade/gpu.py:100-124). */
+int vb_activation(const float* x, float* y, int64_t n, int32_t kind, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -37,6 +37,15 @@ SIGNATURES = {
     "vb_quantize_rows": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _vp]),
     "vb_gemv": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i32, _vp]),
     "vb_gemm": (ctypes.c_int, [_vp, _vp, _i32, _vp, _i64, _i64, _i64, _i32, _i32, _vp]),
+    "vb_sparse_ffn_workspace": (_i64, [_i64, _i64, _i32, _i32]),
+    "vb_sparse_ffn": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _vp, _i64, _i64, _i32,
+                                     _vp, _sz, _vp]),
+    "vb_topk_indices": (ctypes.c_int, [_vp, _i64, _i32, _vp, _vp]),
+    "vb_moe_workspace": (_i64, [_i32, _i32, _i64, _i64]),
+    "vb_moe_grouped_ffn": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _i64,
+                                          _i64, _i32, _vp, _sz, _vp]),
+    "vb_moe_route": (ctypes.c_int, [_vp, _i32, _i32, _i32, _vp, _vp, _vp]),
+    "vb_activation": (ctypes.c_int, [_vp, _vp, _i64, _i32, _vp]),
 }
 
 _lib = None

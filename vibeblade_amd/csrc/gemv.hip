@@ -33,6 +33,7 @@
 #include <cstdlib>
 
 #include "vb_common.hpp"
+#include "vb_internal.hpp"
 #include "../../include/vbhip.h"
 
 namespace vb {
@@ -319,14 +320,49 @@ __device__ __forceinline__ void read_xslice(const uint4* xq, int kt, int lane, X
 
 // One workgroup: `wpg` waves = (wpg / wpr) row groups x wpr k-waves.  A row
 // group walks its rows in NB batches of R; k-wave kw covers k-tiles kw,
-// kw + wpr, ...  Work is flattened into steps (batch, tile); the loads of
-// step s+1 are issued before step s is computed, and the loads of step 0
-// before the activations are encoded, so HBM latency overlaps both.
-template <int TYPE, int R>
+// kw + wpr, ...  Work is flattened into steps (batch, tile) and streamed
+// through a ring of D register buffers: the loads of step s + D are issued as
+// soon as step s has been computed, so D steps are always in flight and the
+// arithmetic of one step overlaps the HBM latency of the next ones.  The
+// step count is padded to a multiple of D; padding steps load the last real
+// step again (cache hits) and compute nothing, which keeps every load outside
+// branches (a branch around loads makes the compiler's wait counts
+// conservative).
+constexpr int kDepth = 4;
+
+// Row sources.  ROWS_PLAIN: row r of w.  ROWS_PAIRS: row r is row gidx[r/2]
+// of w (r even) or of w2 (r odd) -- gate/up pairs of the active neurons of a
+// sparse FFN, one launch and one activation encode for both matrices.
+constexpr int ROWS_PLAIN = 0;
+constexpr int ROWS_PAIRS = 1;
+
+template <int MODE>
+__device__ __forceinline__ const uint8_t* row_ptr(const uint8_t* w, const uint8_t* w2,
+                                                  const int32_t* gidx, int64_t nsrc, int64_t row,
+                                                  int64_t rb) {
+    if constexpr (MODE == ROWS_PLAIN) {
+        return w + row * rb;
+    } else {
+        int64_t src = gidx[row >> 1];
+        src = src < 0 ? 0 : (src >= nsrc ? nsrc - 1 : src);  // never read outside the tensor
+        return ((row & 1) ? w2 : w) + src * rb;
+    }
+}
+
+// zbuf / zn: an int buffer the first workgroup clears (the counters of a
+// following kernel; a fill inside this launch keeps memsets out of captured
+// graphs).
+template <int TYPE, int R, int MODE>
 __global__ void __launch_bounds__(512) gemv_q_kernel(const uint8_t* __restrict__ w,
+                                                     const uint8_t* __restrict__ w2,
+                                                     const int32_t* __restrict__ gidx, int64_t nsrc,
                                                      const float* __restrict__ x,
                                                      float* __restrict__ y, int64_t n, int64_t rb,
-                                                     int units, int n_ktiles, int wpr, int nb) {
+                                                     int units, int n_ktiles, int wpr, int nb,
+                                                     int* __restrict__ zbuf, int zn) {
+    if (zn > 0 && blockIdx.x == 0) {
+        for (int i = threadIdx.x; i < zn; i += blockDim.x) zbuf[i] = 0;
+    }
     using Unit = typename UnitOf<TYPE>::T;
     extern __shared__ uint4 xq[];
     __shared__ float red[8][R];
@@ -336,30 +372,32 @@ __global__ void __launch_bounds__(512) gemv_q_kernel(const uint8_t* __restrict__
     const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * groups + g) * static_cast<int64_t>(R) * nb;
     const int ntw = (n_ktiles + wpr - 1) / wpr;  // tiles per k-wave (uniform loop bound)
     const int nsteps = nb * ntw;
+    const int nsteps_p = ((nsteps + kDepth - 1) / kDepth) * kDepth;
 
-    // Branch-free: out-of-range units and rows load clamped (valid) addresses
-    // and are masked in compute().
     auto issue = [&](Unit* v, int step) {
-        const int b = step / ntw, i = step - (step / ntw) * ntw;
+        step = step < nsteps ? step : nsteps - 1;
+        const int b = step / ntw, i = step - b * ntw;
         int u = (kw + i * wpr) * 64 + lane;
         u = u < units ? u : units - 1;
 #pragma unroll
         for (int r = 0; r < R; r++) {
             int64_t row = row0 + static_cast<int64_t>(b) * R + r;
             row = row < n ? row : n - 1;
-            load_unit(w + row * rb, u, v[r]);
+            load_unit(row_ptr<MODE>(w, w2, gidx, nsrc, row, rb), u, v[r]);
         }
     };
 
-    // x first, then the first two steps of weights, then the encode: the
-    // encode only waits for x, and the weights are in flight meanwhile.
-    Unit va[R], vb[R];
+    // x first, then the first D steps of weights, then the encode: the encode
+    // only waits for x, and the weights are in flight meanwhile.
+    Unit v0[R], v1[R], v2[R], v3[R];
     const bool x_in_regs = n_ktiles * 512 <= XT_MAX * static_cast<int>(blockDim.x);
     XTasks xt;
     if (x_in_regs) prefetch_x<TYPE>(x, units, n_ktiles, xt);
     __builtin_amdgcn_sched_barrier(0);
-    issue(va, 0);
-    issue(vb, nsteps > 1 ? 1 : 0);  // a repeat of step 0 when there is no step 1 (cache hits)
+    issue(v0, 0);
+    issue(v1, 1);
+    issue(v2, 2);
+    issue(v3, 3);
     __builtin_amdgcn_sched_barrier(0);  // keep the weight loads ahead of the encode
     if (x_in_regs)
         encode_x_regs<TYPE>(units, n_ktiles, xt, xq);
@@ -374,7 +412,8 @@ __global__ void __launch_bounds__(512) gemv_q_kernel(const uint8_t* __restrict__
     for (int r = 0; r < R; r++) acc[r] = 0.f;
 
     auto compute = [&](const Unit* v, int step) {
-        const int b = step / ntw, i = step - (step / ntw) * ntw;
+        if (step >= nsteps) return;  // padding step (uniform)
+        const int b = step / ntw, i = step - b * ntw;
         const int kt = kw + i * wpr;
         const int u = kt * 64 + lane;
         if (ntw > 1 && kt < n_ktiles) read_xslice(xq, kt, lane, xs);
@@ -412,27 +451,45 @@ __global__ void __launch_bounds__(512) gemv_q_kernel(const uint8_t* __restrict__
         }
     };
 
-    // Two steps in flight.  The refill of vb near the end repeats the last
-    // step instead of branching (a branch around loads costs the overlap).
     int s = 0;
-    for (; s + 2 < nsteps; s += 2) {
-        compute(va, s);
-        issue(va, s + 2);
-        compute(vb, s + 1);
-        issue(vb, s + 3 < nsteps ? s + 3 : nsteps - 1);
+    for (; s + kDepth < nsteps_p; s += kDepth) {
+        compute(v0, s);
+        issue(v0, s + 4);
+        compute(v1, s + 1);
+        issue(v1, s + 5);
+        compute(v2, s + 2);
+        issue(v2, s + 6);
+        compute(v3, s + 3);
+        issue(v3, s + 7);
     }
-    compute(va, s);
-    if (s + 1 < nsteps) compute(vb, s + 1);
+    compute(v0, s);
+    compute(v1, s + 1);
+    compute(v2, s + 2);
+    compute(v3, s + 3);
 }
 
-// F32 / F16 weights: plain fp32 dot products, one wave per R rows.
-template <int TYPE, int R>
+// F32 / F16 weights: plain fp32 dot products, one wave per R rows (rows
+// plain or gathered gate/up pairs, as in the block-quantized kernel).
+template <int TYPE, int R, int MODE>
 __global__ void __launch_bounds__(256) gemv_plain_kernel(const uint8_t* __restrict__ w,
+                                                         const uint8_t* __restrict__ w2,
+                                                         const int32_t* __restrict__ gidx, int64_t nsrc,
                                                          const float* __restrict__ x,
-                                                         float* __restrict__ y, int64_t n,
-                                                         int64_t k) {
+                                                         float* __restrict__ y, int64_t n, int64_t k,
+                                                         int* __restrict__ zbuf, int zn) {
+    if (zn > 0 && blockIdx.x == 0) {
+        for (int i = threadIdx.x; i < zn; i += blockDim.x) zbuf[i] = 0;
+    }
     const int lane = threadIdx.x & 63;
     const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6)) * R;
+    constexpr int64_t ES = TYPE == TYPE_F32 ? 4 : 2;
+    const uint8_t* rp[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        int64_t row = row0 + r;
+        row = row < n ? row : n - 1;
+        rp[r] = row_ptr<MODE>(w, w2, gidx, nsrc, row, k * ES);
+    }
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = 0.f;
@@ -440,18 +497,16 @@ __global__ void __launch_bounds__(256) gemv_plain_kernel(const uint8_t* __restri
         const float xv = x[i];
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            int64_t row = row0 + r;
-            row = row < n ? row : n - 1;
             float wv;
             if constexpr (TYPE == TYPE_F32)
-                wv = reinterpret_cast<const float*>(w)[row * k + i];
+                wv = reinterpret_cast<const float*>(rp[r])[i];
             else
-                wv = __half2float(reinterpret_cast<const __half*>(w)[row * k + i]);
+                wv = __half2float(reinterpret_cast<const __half*>(rp[r])[i]);
             acc[r] += wv * xv;
         }
     }
 #pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
+    for (int r = 0; r < R; r++) acc[r] = wave_sum_dpp(acc[r]);
     if (lane == 0) {
 #pragma unroll
         for (int r = 0; r < R; r++)
@@ -466,13 +521,15 @@ struct GemvShape {
 };
 
 constexpr int kNumCUs = 256;
-// rows per step (two steps are in flight); Q6_K units are larger, and R = 4
-// would spill
+
+// rows per step (kDepth steps are in flight).  One row per step measured
+// fastest for every type and shape (deeper per-row pipelining beats wider
+// steps).
 template <int TYPE>
-constexpr int max_rows() { return TYPE == TYPE_Q6_K ? 3 : 4; }
+constexpr int max_rows() { return 1; }
 
 // Launch geometry: for each candidate workgroup size (waves), rows are split
-// so the grid covers the CUs about once with R <= 4 rows per step; the
+// so the grid covers the CUs about once with R <= max_r rows per step; the
 // candidate with the fewest rows per CU wins (ties: more waves).
 // VB_GEMV_CFG="wpg,r,nb" overrides (tuning sweeps).
 GemvShape gemv_shape(int64_t n, int units, int max_r) {
@@ -488,7 +545,7 @@ GemvShape gemv_shape(int64_t n, int units, int max_r) {
                             (static_cast<int64_t>(kNumCUs) * groups);
         if (per_group < 1) per_group = 1;
         const int r = static_cast<int>(per_group < max_r ? per_group : max_r);
-        const int nb = static_cast<int>((per_group + r - 1) / r);
+        int nb = static_cast<int>((per_group + r - 1) / r);
         const int64_t rows_per_wg = static_cast<int64_t>(groups) * r * nb;
         const int64_t grid = (n + rows_per_wg - 1) / rows_per_wg;
         const int64_t cost = ((grid + kNumCUs - 1) / kNumCUs) * rows_per_wg;
@@ -501,7 +558,7 @@ GemvShape gemv_shape(int64_t n, int units, int max_r) {
     }
     if (const char* cfg = std::getenv("VB_GEMV_CFG")) {
         int a = 0, b = 0, c = 0;
-        if (std::sscanf(cfg, "%d,%d,%d", &a, &b, &c) == 3 && a >= 1 && a <= 8 && b >= 1 && b <= max_r &&
+        if (std::sscanf(cfg, "%d,%d,%d", &a, &b, &c) == 3 && a >= 1 && a <= 8 && b >= 1 && b <= 2 &&
             c >= 1 && a % s.wpr == 0) {
             s.wpg = a;
             s.r = b;
@@ -515,37 +572,39 @@ GemvShape gemv_shape(int64_t n, int units, int max_r) {
 }
 
 template <int TYPE, int R>
-int launch_gemv_r(const GemvShape& s, const void* w, const float* x, float* y, int64_t n, int64_t rb,
-                  hipStream_t st) {
-    gemv_q_kernel<TYPE, R><<<dim3(static_cast<uint32_t>(s.grid)), dim3(64 * s.wpg), s.lds, st>>>(
-        static_cast<const uint8_t*>(w), x, y, n, rb, s.units, s.n_ktiles, s.wpr, s.nb);
+int launch_gemv_r(const GemvShape& s, const void* w, const RowSrc& src, const float* x, float* y, int64_t n,
+                  int64_t rb, hipStream_t st) {
+    const dim3 g(static_cast<uint32_t>(s.grid)), b(64 * s.wpg);
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
+    const uint8_t* w2 = static_cast<const uint8_t*>(src.w2);
+    if (src.gidx)
+        gemv_q_kernel<TYPE, R, ROWS_PAIRS><<<g, b, s.lds, st>>>(wb, w2, src.gidx, src.nsrc, x, y, n, rb, s.units,
+                                                                s.n_ktiles, s.wpr, s.nb, src.zbuf, src.zn);
+    else
+        gemv_q_kernel<TYPE, R, ROWS_PLAIN><<<g, b, s.lds, st>>>(wb, w2, src.gidx, src.nsrc, x, y, n, rb, s.units,
+                                                                s.n_ktiles, s.wpr, s.nb, src.zbuf, src.zn);
     return check_launch("vb_gemv");
 }
 
 template <int TYPE>
-int launch_gemv_q(const void* w, const float* x, float* y, int64_t n, int64_t k, int64_t rb,
-                  hipStream_t st) {
+int launch_gemv_q(const void* w, const RowSrc& src, const float* x, float* y, int64_t n, int64_t k,
+                  int64_t rb, hipStream_t st) {
     const GemvShape s = gemv_shape(n, static_cast<int>(k / 64), max_rows<TYPE>());
     if (s.n_ktiles > XQ_MAX_KTILES) {
         set_error("vb_gemv: k=%lld exceeds the supported maximum of %d", static_cast<long long>(k),
                   XQ_MAX_KTILES * 64 * 64);
         return E_UNSUPPORTED;
     }
-    switch (s.r) {
-    case 1: return launch_gemv_r<TYPE, 1>(s, w, x, y, n, rb, st);
-    case 2: return launch_gemv_r<TYPE, 2>(s, w, x, y, n, rb, st);
-    case 3: return launch_gemv_r<TYPE, 3>(s, w, x, y, n, rb, st);
-    default:
-        if constexpr (max_rows<TYPE>() >= 4) return launch_gemv_r<TYPE, 4>(s, w, x, y, n, rb, st);
-        return launch_gemv_r<TYPE, 3>(s, w, x, y, n, rb, st);
-    }
+    if (s.r == 1) return launch_gemv_r<TYPE, 1>(s, w, src, x, y, n, rb, st);
+    return launch_gemv_r<TYPE, 2>(s, w, src, x, y, n, rb, st);
 }
 
 }  // namespace
 
-// Shared with the other translation units (sparse / moe).
-int gemv_dispatch(const void* w, const float* x, float* y, int64_t n, int64_t k, int32_t type,
-                  hipStream_t st) {
+// Shared with the other translation units (sparse / moe).  `src` selects
+// gathered gate/up pairs and an int buffer to clear (see RowSrc).
+int gemv_dispatch_src(const void* w, const RowSrc& src, const float* x, float* y, int64_t n, int64_t k,
+                      int32_t type, hipStream_t st) {
     const int64_t rb = row_bytes(type, k);
     if (rb < 0) {
         set_error("vb_gemv: unsupported type %d or k=%lld not a whole number of blocks", type,
@@ -570,25 +629,42 @@ int gemv_dispatch(const void* w, const float* x, float* y, int64_t n, int64_t k,
         return E_INVAL;
     }
     switch (type) {
-    case TYPE_Q4_K: return launch_gemv_q<TYPE_Q4_K>(w, x, y, n, k, rb, st);
-    case TYPE_Q6_K: return launch_gemv_q<TYPE_Q6_K>(w, x, y, n, k, rb, st);
-    case TYPE_Q8_0: return launch_gemv_q<TYPE_Q8_0>(w, x, y, n, k, rb, st);
+    case TYPE_Q4_K: return launch_gemv_q<TYPE_Q4_K>(w, src, x, y, n, k, rb, st);
+    case TYPE_Q6_K: return launch_gemv_q<TYPE_Q6_K>(w, src, x, y, n, k, rb, st);
+    case TYPE_Q8_0: return launch_gemv_q<TYPE_Q8_0>(w, src, x, y, n, k, rb, st);
     case TYPE_F32:
     case TYPE_F16: {
         constexpr int R = 4;
         const int64_t grid = (n + 4 * R - 1) / (4 * R);
-        if (type == TYPE_F32)
-            gemv_plain_kernel<TYPE_F32, R><<<dim3(static_cast<uint32_t>(grid)), dim3(256), 0, st>>>(
-                static_cast<const uint8_t*>(w), x, y, n, k);
-        else
-            gemv_plain_kernel<TYPE_F16, R><<<dim3(static_cast<uint32_t>(grid)), dim3(256), 0, st>>>(
-                static_cast<const uint8_t*>(w), x, y, n, k);
+        const dim3 g(static_cast<uint32_t>(grid)), b(256);
+        const uint8_t* wb = static_cast<const uint8_t*>(w);
+        const uint8_t* w2 = static_cast<const uint8_t*>(src.w2);
+        if (type == TYPE_F32) {
+            if (src.gidx)
+                gemv_plain_kernel<TYPE_F32, R, ROWS_PAIRS><<<g, b, 0, st>>>(wb, w2, src.gidx, src.nsrc, x, y, n, k,
+                                                                           src.zbuf, src.zn);
+            else
+                gemv_plain_kernel<TYPE_F32, R, ROWS_PLAIN><<<g, b, 0, st>>>(wb, w2, src.gidx, src.nsrc, x, y, n, k,
+                                                                           src.zbuf, src.zn);
+        } else {
+            if (src.gidx)
+                gemv_plain_kernel<TYPE_F16, R, ROWS_PAIRS><<<g, b, 0, st>>>(wb, w2, src.gidx, src.nsrc, x, y, n, k,
+                                                                           src.zbuf, src.zn);
+            else
+                gemv_plain_kernel<TYPE_F16, R, ROWS_PLAIN><<<g, b, 0, st>>>(wb, w2, src.gidx, src.nsrc, x, y, n, k,
+                                                                           src.zbuf, src.zn);
+        }
         return check_launch("vb_gemv");
     }
     default:
         set_error("vb_gemv: unsupported type %d", type);
         return E_UNSUPPORTED;
     }
+}
+
+int gemv_dispatch(const void* w, const float* x, float* y, int64_t n, int64_t k, int32_t type,
+                  hipStream_t st) {
+    return gemv_dispatch_src(w, RowSrc{}, x, y, n, k, type, st);
 }
 
 }  // namespace vb

@@ -1,0 +1,309 @@
+// TurboSparse activation-sparse FFN (single token) and top-k selection.
+//
+// Reference semantics: vibeblade/sparse.py:199-283 (sparse_ffn_silu: gate ->
+// top-k -> up on the active rows -> silu(gate)*up -> hidden @ down^T[active])
+// and the dense-with-mask form of vibeblade/transformer.py:204-206; the
+// activation is selectable: silu(g)*u, or relu(g)*relu(u) (the native
+// engine's "dReLU" is plain ReLU: src/kernels.cpp:39-57, vibeblade/gpu.py:100).
+//
+// Given the sorted active neuron set S (|S| = n_active) and one token x[h]:
+//   1. gate and up on the rows of S only: one GEMV launch over gathered
+//      gate/up row pairs (gemv.hip, ROWS_PAIRS) -> gu[2r], gu[2r+1];
+//   2. down:
+//      layout 0 (GGUF, W_d is h rows x i): scatter act(gu) into a dense
+//        hidden vector (zeros off S) and run the dense GEMV -- every down
+//        super-block holds an active column at 10 % density, so all of W_d
+//        is read;
+//      layout 1 (neuron-major D = W_d^T, i rows x h, Q4_K): only the |S|
+//        rows of D are read: y = sum_r act_r * D[S_r, :].  Workgroup (u, rs)
+//        owns output unit u (64 columns) and every RS-th active row; row
+//        partials meet in LDS, the RS partials of a unit are summed in fixed
+//        order by the last workgroup to finish it (deterministic, one launch).
+#include "mfma_q4k.hpp"
+#include "vb_internal.hpp"
+#include "../../include/vbhip.h"
+
+namespace vb {
+namespace {
+
+constexpr int ACT_SILU = 0;
+constexpr int ACT_RELU2 = 1;
+
+__device__ __forceinline__ float act_pair(float g, float u, int kind) {
+    if (kind == ACT_SILU) return g / (1.0f + __expf(-g)) * u;
+    return fmaxf(g, 0.f) * fmaxf(u, 0.f);
+}
+
+// layout 0: hid[o] = act(gu[2r], gu[2r+1]) if o == active[r], else 0.
+__global__ void __launch_bounds__(256) scatter_act_kernel(const int32_t* __restrict__ active, int n_active,
+                                                          const float* __restrict__ gu, int kind,
+                                                          float* __restrict__ hid, int64_t i_dim) {
+    const int64_t o = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (o >= i_dim) return;
+    int lo = 0, hi = n_active;  // active is sorted ascending
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (active[mid] < o) lo = mid + 1;
+        else hi = mid;
+    }
+    float v = 0.f;
+    if (lo < n_active && active[lo] == o) v = act_pair(gu[2 * lo], gu[2 * lo + 1], kind);
+    hid[o] = v;
+}
+
+constexpr int DOWN_RS = 4;  // workgroups per output unit
+
+// layout 1, Q4_K: see the header comment.  Thread t = 4*rg + p handles row
+// group rg and quarter p of the unit (16 of its 64 elements: quarter p < 2 =
+// low nibbles of qs bytes 16p.., p >= 2 = high nibbles of bytes 16(p-2)..).
+__global__ void __launch_bounds__(256) down_axpy_q4k_kernel(
+    const uint8_t* __restrict__ d, int64_t rb, int64_t i_dim, const int32_t* __restrict__ active,
+    int n_active, const float* __restrict__ gu, int kind, float* __restrict__ partial,
+    int* __restrict__ cnt, float* __restrict__ y, int64_t h_dim) {
+    __shared__ float red[64][65];
+    __shared__ int last;
+    const int u = blockIdx.x, rs = blockIdx.y;
+    const int t = threadIdx.x, rg = t >> 2, p = t & 3;
+    const int sb = u >> 2, c = u & 3;
+    const int jsub = 2 * c + (p >= 2 ? 1 : 0);
+    float acc[16];
+#pragma unroll
+    for (int e = 0; e < 16; e++) acc[e] = 0.f;
+    float bacc = 0.f;
+    for (int r = rs + DOWN_RS * rg; r < n_active; r += DOWN_RS * 64) {
+        int64_t nr = active[r];
+        nr = nr < 0 ? 0 : (nr >= i_dim ? i_dim - 1 : nr);
+        const uint8_t* blk = d + nr * rb + static_cast<int64_t>(sb) * 144;
+        const uint4 hd = *reinterpret_cast<const uint4*>(blk);
+        const uint4 q = *reinterpret_cast<const uint4*>(blk + 16 + 32 * c + 16 * (p & 1));
+        const float hid = act_pair(gu[2 * r], gu[2 * r + 1], kind);
+        uint8_t s8[12];
+        const uint32_t sw[3] = {hd.y, hd.z, hd.w};
+#pragma unroll
+        for (int b = 0; b < 12; b++) s8[b] = static_cast<uint8_t>(sw[b >> 2] >> (8 * (b & 3)));
+        float sc, m;
+        if (jsub < 4) {
+            sc = static_cast<float>(s8[jsub] & 63);
+            m = static_cast<float>(s8[jsub + 4] & 63);
+        } else {
+            sc = static_cast<float>((s8[jsub + 4] & 0xF) | ((s8[jsub - 4] >> 6) << 4));
+            m = static_cast<float>((s8[jsub + 4] >> 4) | ((s8[jsub] >> 6) << 4));
+        }
+        const float a = hid * (f16lo(hd.x) * sc);
+        bacc += hid * (f16hi(hd.x) * m);
+        const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+        const int shift = p >= 2 ? 4 : 0;
+#pragma unroll
+        for (int e = 0; e < 16; e++)
+            acc[e] += a * static_cast<float>((qw[e >> 2] >> (8 * (e & 3) + shift)) & 0xF);
+    }
+#pragma unroll
+    for (int e = 0; e < 16; e++) red[rg][16 * p + e] = acc[e] - bacc;
+    __syncthreads();
+    if (t < 64) {
+        float s = 0.f;
+        for (int g = 0; g < 64; g++) s += red[g][t];
+        partial[static_cast<int64_t>(rs) * h_dim + 64 * u + t] = s;
+        __threadfence();
+    }
+    __syncthreads();
+    if (t == 0) last = (atomicAdd(&cnt[u], 1) == DOWN_RS - 1) ? 1 : 0;
+    __syncthreads();
+    if (last && t < 64) {
+        __threadfence();
+        float s = 0.f;
+        for (int j = 0; j < DOWN_RS; j++)
+            s += __hip_atomic_load(&partial[static_cast<int64_t>(j) * h_dim + 64 * u + t], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        y[64 * u + t] = s;
+    }
+}
+
+// ---- top-k indices (single workgroup radix select) ---------------------------
+
+__device__ __forceinline__ uint32_t order_key(float f) {
+    const uint32_t b = __float_as_uint(f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);  // ascending key == ascending float
+}
+
+// out[0..k) = indices of the k largest v[i], ascending index order; ties at
+// the threshold value go to the lowest indices.
+__global__ void __launch_bounds__(1024) topk_kernel(const float* __restrict__ v, int n, int k,
+                                                    int32_t* __restrict__ out) {
+    __shared__ int hist[256];
+    __shared__ uint32_t s_prefix, s_mask;
+    __shared__ int s_remaining;
+    __shared__ int wave_cnt[2][16];
+    __shared__ int s_base[2];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) {
+        s_prefix = 0;
+        s_mask = 0;
+        s_remaining = k;
+    }
+    for (int pass = 3; pass >= 0; pass--) {
+        if (tid < 256) hist[tid] = 0;
+        __syncthreads();
+        const uint32_t prefix = s_prefix, mask = s_mask;
+        for (int i = tid; i < n; i += blockDim.x) {
+            const uint32_t key = order_key(v[i]);
+            if ((key & mask) == prefix) atomicAdd(&hist[(key >> (8 * pass)) & 255], 1);
+        }
+        __syncthreads();
+        if (tid == 0) {
+            int rem = s_remaining, cum = 0, b = 255;
+            for (; b > 0; b--) {
+                if (cum + hist[b] >= rem) break;
+                cum += hist[b];
+            }
+            s_prefix = prefix | (static_cast<uint32_t>(b) << (8 * pass));
+            s_mask = mask | (255u << (8 * pass));
+            s_remaining = rem - cum;
+        }
+        __syncthreads();
+    }
+    const uint32_t kth = s_prefix;
+    const int ties = s_remaining;  // elements equal to kth to take
+    if (tid == 0) {
+        s_base[0] = 0;  // selected so far
+        s_base[1] = 0;  // equal-to-kth seen so far
+    }
+    __syncthreads();
+    for (int i0 = 0; i0 < n; i0 += blockDim.x) {
+        const int i = i0 + tid;
+        const uint32_t key = i < n ? order_key(v[i]) : 0u;
+        const bool eq = i < n && key == kth;
+        const bool gt = i < n && key > kth;
+        const uint64_t beq = __ballot(eq);
+        const int eq_rank_w = __popcll(beq & ((1ull << lane) - 1ull));
+        if (lane == 0) wave_cnt[1][wave] = __popcll(beq);
+        __syncthreads();
+        int eq_before = s_base[1];
+        for (int w = 0; w < wave; w++) eq_before += wave_cnt[1][w];
+        const bool sel = gt || (eq && eq_before + eq_rank_w < ties);
+        const uint64_t bsel = __ballot(sel);
+        if (lane == 0) wave_cnt[0][wave] = __popcll(bsel);
+        __syncthreads();
+        int pos = s_base[0] + __popcll(bsel & ((1ull << lane) - 1ull));
+        for (int w = 0; w < wave; w++) pos += wave_cnt[0][w];
+        if (sel && pos < k) out[pos] = i;
+        __syncthreads();
+        if (tid == 0) {
+            int a = 0, b = 0;
+            for (int w = 0; w < static_cast<int>(blockDim.x >> 6); w++) {
+                a += wave_cnt[0][w];
+                b += wave_cnt[1][w];
+            }
+            s_base[0] += a;
+            s_base[1] += b;
+        }
+        __syncthreads();
+    }
+}
+
+size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
+
+struct SparseWs {
+    size_t gu, hid, partial, cnt, total;
+};
+
+SparseWs sparse_ws(int64_t h, int64_t i, int32_t n_active, int32_t layout) {
+    SparseWs w;
+    w.gu = 0;
+    w.hid = align256(static_cast<size_t>(2 * (n_active > 0 ? n_active : 1)) * sizeof(float));
+    size_t off = w.hid + (layout == 0 ? align256(static_cast<size_t>(i) * sizeof(float)) : 0);
+    w.partial = off;
+    off += layout == 1 ? align256(static_cast<size_t>(DOWN_RS) * h * sizeof(float)) : 0;
+    w.cnt = off;
+    off += layout == 1 ? align256(static_cast<size_t>(h / 64) * sizeof(int)) : 0;
+    w.total = off;
+    return w;
+}
+
+__global__ void fill_zero_kernel(float* p, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0.f;
+}
+
+}  // namespace
+}  // namespace vb
+
+using namespace vb;
+
+extern "C" int64_t vb_sparse_ffn_workspace(int64_t h, int64_t i, int32_t n_active, int32_t down_layout) {
+    if (h <= 0 || i <= 0 || n_active < 0 || (down_layout != 0 && down_layout != 1)) return -1;
+    return static_cast<int64_t>(sparse_ws(h, i, n_active, down_layout).total);
+}
+
+extern "C" int vb_sparse_ffn(const void* wg, const void* wu, const void* wd, int32_t down_layout,
+                             const float* x, const int32_t* active, int32_t n_active, int32_t act_kind,
+                             float* y, int64_t h, int64_t i, int32_t ggml_type, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+    hipStream_t st = as_stream(stream);
+    if (h <= 0 || i <= 0 || n_active < 0 || n_active > i || (down_layout != 0 && down_layout != 1) ||
+        (act_kind != ACT_SILU && act_kind != ACT_RELU2) || !wg || !wu || !wd || !x || !y ||
+        (n_active > 0 && !active)) {
+        set_error("vb_sparse_ffn: bad arguments");
+        return E_INVAL;
+    }
+    if (row_bytes(ggml_type, h) < 0 || row_bytes(ggml_type, i) < 0) {
+        set_error("vb_sparse_ffn: type %d unsupported for h=%lld i=%lld", ggml_type, static_cast<long long>(h),
+                  static_cast<long long>(i));
+        return E_UNSUPPORTED;
+    }
+    if (down_layout == 1 && (ggml_type != TYPE_Q4_K || h % 64 != 0)) {
+        set_error("vb_sparse_ffn: neuron-major down (layout 1) needs Q4_K and h %% 64 == 0");
+        return E_UNSUPPORTED;
+    }
+    const SparseWs ws = sparse_ws(h, i, n_active, down_layout);
+    if (!workspace || workspace_bytes < ws.total) {
+        set_error("vb_sparse_ffn: workspace of %zu bytes needed", ws.total);
+        return E_NOMEM;
+    }
+    uint8_t* wsb = static_cast<uint8_t*>(workspace);
+    float* gu = reinterpret_cast<float*>(wsb + ws.gu);
+    int* cnt = reinterpret_cast<int*>(wsb + ws.cnt);
+
+    if (n_active == 0) {  // no active neuron: y = 0
+        fill_zero_kernel<<<dim3(static_cast<uint32_t>((h + 255) / 256)), dim3(256), 0, st>>>(y, h);
+        return check_launch("vb_sparse_ffn");
+    }
+    // 1. gate/up on the active rows (and clear the down counters)
+    RowSrc src;
+    src.w2 = wu;
+    src.gidx = active;
+    src.nsrc = i;
+    if (down_layout == 1) {
+        src.zbuf = cnt;
+        src.zn = static_cast<int>(h / 64);
+    }
+    int rc = gemv_dispatch_src(wg, src, x, gu, 2 * static_cast<int64_t>(n_active), h, ggml_type, st);
+    if (rc != OK) return rc;
+    // 2. down
+    if (down_layout == 0) {
+        float* hid = reinterpret_cast<float*>(wsb + ws.hid);
+        scatter_act_kernel<<<dim3(static_cast<uint32_t>((i + 255) / 256)), dim3(256), 0, st>>>(
+            active, n_active, gu, act_kind, hid, i);
+        if ((rc = check_launch("vb_sparse_ffn")) != OK) return rc;
+        return gemv_dispatch(wd, hid, y, h, i, ggml_type, st);
+    }
+    float* partial = reinterpret_cast<float*>(wsb + ws.partial);
+    down_axpy_q4k_kernel<<<dim3(static_cast<uint32_t>(h / 64), DOWN_RS), dim3(256), 0, st>>>(
+        static_cast<const uint8_t*>(wd), row_bytes(TYPE_Q4_K, h), i, active, n_active, gu, act_kind, partial,
+        cnt, y, h);
+    return check_launch("vb_sparse_ffn");
+}
+
+extern "C" int vb_topk_indices(const float* v, int64_t n, int32_t k, int32_t* out_idx, void* stream) {
+    if (n < 0 || n > 0x7fffffff || k < 0 || (n > 0 && (!v || (k > 0 && !out_idx)))) {
+        set_error("vb_topk_indices: bad arguments");
+        return E_INVAL;
+    }
+    if (k == 0 || n == 0) return OK;
+    if (k > n) {
+        set_error("vb_topk_indices: k=%d > n=%lld", k, static_cast<long long>(n));
+        return E_INVAL;
+    }
+    topk_kernel<<<dim3(1), dim3(1024), 0, as_stream(stream)>>>(v, static_cast<int>(n), k, out_idx);
+    return check_launch("vb_topk_indices");
+}

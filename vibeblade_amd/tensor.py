@@ -142,3 +142,124 @@ def gemm(w: QTensor, x: torch.Tensor, out: torch.Tensor | None = None,
     _lib.call("vb_gemm", w.ptr(), x.data_ptr(), xdt, out.data_ptr(), m, w.rows, w.k, w.qtype,
               variant, _stream())
     return out
+
+
+def as_qtensor(w, device=None) -> QTensor:
+    """A QTensor as is; an fp32 (rows, k) array / tensor uploaded as a GGUF
+    F32 tensor (no quantization: the values stay exact)."""
+    if isinstance(w, QTensor):
+        return w
+    dev = _dev(device if device is not None else
+               (w.device if isinstance(w, torch.Tensor) and w.is_cuda else None))
+    t = _as_f32_dev(w, dev)
+    if t.dim() != 2:
+        raise ValueError(f"expected a 2-D weight matrix, got shape {tuple(t.shape)}")
+    rows, k = t.shape
+    return QTensor(t.contiguous().view(torch.uint8).reshape(-1), ggml.GGML_TYPE_F32, rows, k)
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+ACT_SILU = 0   # silu(g) * u
+ACT_RELU2 = 1  # relu(g) * relu(u)
+DOWN_GGUF = 0          # down weight (h rows x i)
+DOWN_NEURON_MAJOR = 1  # down^T (i rows x h)
+
+
+def topk_indices(v: torch.Tensor, k: int) -> torch.Tensor:
+    """Indices of the k largest entries of a 1-D fp32 device vector, ascending
+    (ties at the threshold go to the lowest indices)."""
+    v = v.to(torch.float32).contiguous().reshape(-1)
+    n = v.numel()
+    k = int(k)
+    if k < 0 or k > n:
+        raise ValueError(f"topk_indices: k={k} out of range for n={n}")
+    out = torch.empty(k, dtype=torch.int32, device=v.device)
+    _lib.call("vb_topk_indices", v.data_ptr(), n, k, out.data_ptr(), _stream())
+    return out
+
+
+def sparse_ffn(gate: QTensor, up: QTensor, down: QTensor, x: torch.Tensor, active: torch.Tensor,
+               act: int = ACT_SILU, down_layout: int = DOWN_GGUF,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """One token through the activation-sparse FFN over the sorted active set."""
+    h, i = gate.k, gate.rows
+    if up.shape != gate.shape or up.qtype != gate.qtype or down.qtype != gate.qtype:
+        raise ValueError("sparse_ffn: gate/up/down must share shape conventions and type")
+    want_down = (h, i) if down_layout == DOWN_GGUF else (i, h)
+    if down.shape != want_down:
+        raise ValueError(f"sparse_ffn: down has shape {down.shape}, expected {want_down}")
+    dev = gate.device
+    x = _as_f32_dev(x, dev).reshape(-1)
+    if x.numel() != h:
+        raise ValueError(f"sparse_ffn: x has {x.numel()} elements, expected {h}")
+    active = active.to(device=dev, dtype=torch.int32).contiguous().reshape(-1)
+    n_active = active.numel()
+    if out is None:
+        out = torch.empty(h, dtype=torch.float32, device=dev)
+    nbytes = _lib.load().vb_sparse_ffn_workspace(h, i, n_active, down_layout)
+    if nbytes < 0:
+        raise ValueError("sparse_ffn: bad shape")
+    ws = _workspace(nbytes, dev)
+    _lib.call("vb_sparse_ffn", gate.ptr(), up.ptr(), down.ptr(), down_layout, x.data_ptr(),
+              active.data_ptr() if n_active else None, n_active, act, out.data_ptr(), h, i, gate.qtype,
+              ws.data_ptr(), ws.numel(), _stream())
+    return out
+
+
+def moe_route(logits: torch.Tensor, topk: int):
+    """(indices int32 (T, topk), weights fp32 (T, topk)) from router logits (T, E)."""
+    logits = logits.to(torch.float32).contiguous()
+    t, e = logits.shape
+    idx = torch.empty((t, topk), dtype=torch.int32, device=logits.device)
+    w = torch.empty((t, topk), dtype=torch.float32, device=logits.device)
+    _lib.call("vb_moe_route", logits.data_ptr(), t, e, topk, idx.data_ptr(), w.data_ptr(), _stream())
+    return idx, w
+
+
+def moe_grouped_ffn(gates, ups, downs, x: torch.Tensor, logits: torch.Tensor, topk: int):
+    """Top-k MoE over experts (lists of QTensors: gate/up i x h, down h x i).
+    Returns (y (T, h) fp32, indices (T, topk) int32, weights (T, topk) fp32)."""
+    import ctypes
+    n_exp = len(gates)
+    if not (len(ups) == len(downs) == n_exp) or n_exp == 0:
+        raise ValueError("moe_grouped_ffn: need the same number of gate/up/down experts")
+    g0 = gates[0]
+    h, i, qtype = g0.k, g0.rows, g0.qtype
+    for e in range(n_exp):
+        if gates[e].shape != (i, h) or ups[e].shape != (i, h) or downs[e].shape != (h, i):
+            raise ValueError(f"moe_grouped_ffn: expert {e} has inconsistent shapes")
+        if not (gates[e].qtype == ups[e].qtype == downs[e].qtype == qtype):
+            raise ValueError("moe_grouped_ffn: experts must share one ggml type")
+    dev = g0.device
+    x = _as_f32_dev(x, dev)
+    if x.dim() == 1:
+        x = x.reshape(1, -1)
+    t = x.shape[0]
+    logits = _as_f32_dev(logits, dev).reshape(t, n_exp)
+    y = torch.empty((t, h), dtype=torch.float32, device=dev)
+    idx = torch.empty((t, topk), dtype=torch.int32, device=dev)
+    w = torch.empty((t, topk), dtype=torch.float32, device=dev)
+    arr = ctypes.c_void_p * n_exp
+    pg = arr(*[g.ptr() for g in gates])
+    pu = arr(*[u.ptr() for u in ups])
+    pd = arr(*[d.ptr() for d in downs])
+    nbytes = _lib.load().vb_moe_workspace(t, topk, h, i)
+    if nbytes < 0:
+        raise ValueError("moe_grouped_ffn: bad shape")
+    ws = _workspace(nbytes, dev)
+    vp = ctypes.c_void_p
+    _lib.call("vb_moe_grouped_ffn", ctypes.cast(pg, vp), ctypes.cast(pu, vp), ctypes.cast(pd, vp), n_exp,
+              x.data_ptr(), t, logits.data_ptr(), topk,
+              y.data_ptr(), idx.data_ptr(), w.data_ptr(), h, i, qtype, ws.data_ptr(), ws.numel(), _stream())
+    return y, idx, w
+
+
+def activation(x: torch.Tensor, kind: int) -> torch.Tensor:
+    """silu (kind 0) or relu (kind 1), elementwise on the device."""
+    x = x.to(torch.float32).contiguous()
+    out = torch.empty_like(x)
+    _lib.call("vb_activation", x.data_ptr(), out.data_ptr(), x.numel(), kind, _stream())
+    return out
