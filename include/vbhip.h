@@ -158,6 +158,13 @@ int vb_moe_route(const float* router_logits, int32_t n_tokens, int32_t n_exp, in
  * y = silu(x) (kind 0) or max(x, 0) (kind 1); GPUBackend.silu / .drelu
  * (vibeblade/gpu.py:100-124). */
 int vb_activation(const float* x, float* y, int64_t n, int32_t kind, void* stream);
+/* y[r] = x[r] / sqrt(mean(x[r]^2) + eps) * w for rows x dim fp32
+ * (GPUBackend.rms_norm, vibeblade/gpu.py:126-146). */
+int vb_rms_norm(const float* x, const float* w, float* y, int64_t rows, int64_t dim, float eps,
+                void* stream);
+/* Row-wise softmax over rows x n fp32 (GPUBackend.softmax,
+ * vibeblade/gpu.py:192-198). */
+int vb_softmax(const float* x, float* y, int64_t rows, int64_t n, void* stream);
 
 #ifdef __cplusplus
 }

@@ -46,6 +46,8 @@ SIGNATURES = {
                                           _i64, _i32, _vp, _sz, _vp]),
     "vb_moe_route": (ctypes.c_int, [_vp, _i32, _i32, _i32, _vp, _vp, _vp]),
     "vb_activation": (ctypes.c_int, [_vp, _vp, _i64, _i32, _vp]),
+    "vb_rms_norm": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp]),
+    "vb_softmax": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp]),
 }
 
 _lib = None

@@ -620,8 +620,10 @@ int gemv_dispatch_src(const void* w, const RowSrc& src, const float* x, float* y
         set_error("vb_gemv: k=%lld must be a multiple of 64 for type %d", static_cast<long long>(k), type);
         return E_UNSUPPORTED;
     }
-    if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 4 != 0) {
-        set_error("vb_gemv: x must be 16-byte and W 4-byte aligned");
+    const bool blockq = type == TYPE_Q4_K || type == TYPE_Q6_K || type == TYPE_Q8_0;
+    if ((blockq && reinterpret_cast<uintptr_t>(x) % 16 != 0) || reinterpret_cast<uintptr_t>(x) % 4 != 0 ||
+        reinterpret_cast<uintptr_t>(w) % 4 != 0) {
+        set_error("vb_gemv: x must be 16-byte aligned for block types (4-byte otherwise), W 4-byte aligned");
         return E_INVAL;
     }
     if (type == TYPE_Q4_K && reinterpret_cast<uintptr_t>(w) % 16 != 0) {
