@@ -68,6 +68,19 @@ def test_sparse_small_all_types(qtype):
         assert O.rel_l2(y, want) <= 1e-3
 
 
+def test_sparse_gathered_rows_on_mfma_path(monkeypatch):
+    """Gathered gate/up row pairs through the int8-MFMA GEMV kernel."""
+    monkeypatch.setenv("VB_GEMV_Q4K_PATH", "mfma")
+    h, i = 1024, 768
+    gq, uq, dq, gd, ud, dd = ffn_weights(h, i, Q4K, 9, DOWN_GGUF)
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal(h).astype(np.float32)
+    for s in (np.sort(rng.choice(i, 77, replace=False)).astype(np.int32), np.array([i - 1], np.int32)):
+        y = sparse_ffn(gq, uq, dq, torch.from_numpy(x), torch.from_numpy(s), ACT_SILU).cpu().numpy()
+        want = O.sparse_ffn(gd, ud, dd, x, s, O.ACT_SILU)[0]
+        assert O.rel_l2(y, want) <= 1e-3
+
+
 def test_sparse_full_set_equals_dense_and_empty_is_zero():
     h, i = 256, 512
     for layout in (DOWN_GGUF, DOWN_NEURON_MAJOR):

@@ -92,6 +92,49 @@ def test_gemv_small_vs_oracle(qtype, rows, k):
     assert np.max(np.abs(y - want)) <= 1e-3 * scale + 1e-6
 
 
+@pytest.fixture
+def q4k_mfma_path(monkeypatch):
+    """Route Q4_K GEMVs through the int8-MFMA kernel (VB_GEMV_Q4K_PATH=mfma)."""
+    monkeypatch.setenv("VB_GEMV_Q4K_PATH", "mfma")
+
+
+@pytest.mark.parametrize("rows,k", [(1, 256), (13, 512), (70, 4096), (37, 14336), (9, 28672), (300, 1280)])
+def test_gemv_q4k_mfma_path_vs_oracle(q4k_mfma_path, rows, k):
+    w = rand_weights(rows, k, rows * 7 + k)
+    qt = QTensor.quantize(w, ggml.GGML_TYPE_Q4_K)
+    x = np.random.default_rng(k + 1).standard_normal(k).astype(np.float32)
+    y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy()
+    want = O.gemv(qt.to_numpy_bytes(), x, rows, k, qt.qtype)
+    assert O.rel_l2(y, want) <= GEMV_TOL
+    assert np.max(np.abs(y - want)) <= 1e-3 * np.abs(want).max() + 1e-6
+
+
+@pytest.mark.parametrize("cfg", ["2,1", "4,4", "8,8", "16,16", "8,2", "6,3"])
+def test_gemv_q4k_mfma_launch_shapes(q4k_mfma_path, monkeypatch, cfg):
+    """Every k-slice / workgroup split gives the same rows (k = 4096: 16
+    super-blocks; "6,3" leaves a ragged last slice)."""
+    monkeypatch.setenv("VB_GEMV_MFMA_CFG", cfg)
+    rows, k = 200, 4096
+    qt = QTensor.quantize(rand_weights(rows, k, 11), ggml.GGML_TYPE_Q4_K)
+    x = np.random.default_rng(12).standard_normal(k).astype(np.float32)
+    y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy()
+    want = O.gemv(qt.to_numpy_bytes(), x, rows, k, qt.qtype)
+    assert O.rel_l2(y, want) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("cfg", ["8,1", "8,3", "16,2", "4,9", "8,7"])
+def test_gemv_dot_launch_shapes(monkeypatch, cfg):
+    """v_dot4 kernel launch overrides (rows per wave, ring depths 2 / 4 / 8)."""
+    monkeypatch.setenv("VB_GEMV_CFG", cfg)
+    for qtype in QTYPES:
+        rows, k = 333, 4096
+        qt = QTensor.quantize(rand_weights(rows, k, 13), qtype)
+        x = np.random.default_rng(14).standard_normal(k).astype(np.float32)
+        y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy()
+        want = O.gemv(qt.to_numpy_bytes(), x, rows, k, qtype)
+        assert O.rel_l2(y, want) <= GEMV_TOL, (cfg, qtype)
+
+
 def test_gemv_zero_rows_and_errors():
     qt = QTensor.quantize(rand_weights(4, 256, 3), ggml.GGML_TYPE_Q4_K)
     x = torch.zeros(256, device="cuda")

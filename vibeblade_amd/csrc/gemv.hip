@@ -25,12 +25,14 @@
 //         Bytes: ql[64h + l0 + [0,16)], ql[64h + 32 + l0 + [0,16)],
 //         qh[32h + l0 + [0,16)], scales[8h + c%2 + 2t], d.
 //
-// Launch shape.  A wave covers 64 consecutive units of a row ("k-tile").
-// Rows with more than one k-tile are split over `wpr` waves of the same
-// workgroup (partial sums meet in LDS); a workgroup of `wpg` waves holds
-// wpg/wpr row groups, each streaming R rows at a time with the next R rows
-// already in flight.  The grid is about one workgroup per CU.
+// Launch shape.  A row's units are split over `wpr` waves ("k-slices" of
+// upw <= 64 units, upw a multiple of 4 so a Q4_K super-block never straddles
+// two lanes' quads); each wave keeps its activation slice in registers for
+// the whole launch and walks `rpg` consecutive rows, with D rows in flight
+// (all of them when rpg <= D).  Per-row wave sums go to LDS; the workgroup
+// writes y (adding the wpr partial sums in a fixed order) at the end.
 #include <cstdlib>
+#include <cstring>
 
 #include "vb_common.hpp"
 #include "vb_internal.hpp"
@@ -51,7 +53,10 @@ struct XSlice {
 
 // ---- per-type unit loaders and dot products -------------------------------
 
-struct Q4KUnit { uint4 hd, qa, qb; };
+// Q4_K: each of the 4 lanes of a super-block loads one dword of the 16-byte
+// header (d|dmin, scales[0:4], scales[4:8], scales[8:12]) and the quad shares
+// them through DPP broadcasts, instead of 4 lanes fetching the same 16 bytes.
+struct Q4KUnit { uint32_t hw; uint4 qa, qb; };
 struct Q8Unit { uint4 a, b, c, d; uint32_t e; };
 struct Q6KUnit { uint4 la, lb, qh; uint32_t sc; uint32_t d; };
 
@@ -63,9 +68,15 @@ template <> struct UnitOf<TYPE_Q6_K> { using T = Q6KUnit; };
 __device__ __forceinline__ void load_unit(const uint8_t* row, int u, Q4KUnit& v) {
     const uint8_t* b = row + (u >> 2) * 144;
     const int c = u & 3;
-    v.hd = *reinterpret_cast<const uint4*>(b);
+    v.hw = ld_b32(b + 4 * c);
     v.qa = *reinterpret_cast<const uint4*>(b + 16 + 32 * c);
     v.qb = *reinterpret_cast<const uint4*>(b + 32 + 32 * c);
+}
+
+// Value of v in lane I of this lane's quad (DPP quad_perm [I,I,I,I]).
+template <int I>
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), I * 0x55, 0xF, 0xF, false));
 }
 
 __device__ __forceinline__ void load_unit(const uint8_t* row, int u, Q8Unit& v) {
@@ -110,9 +121,11 @@ __device__ __forceinline__ float unit_dot(const Q4KUnit& v, const XSlice& xs, in
     }
     const int s0 = run_dot(lo, xs.h, xs.l, 8);
     const int s1 = run_dot(hi, xs.h + 8, xs.l + 8, 8);
-    // 6-bit scales/mins of sub-blocks 2c and 2c+1, two bytes at a time.
+    // 6-bit scales/mins of sub-blocks 2c and 2c+1, two bytes at a time.  The
+    // quad's lanes hold units c = 0..3 of the same super-block.
+    const uint32_t hx = quad_bcast<0>(v.hw);
     const uint32_t sh = 16u * static_cast<uint32_t>(c & 1);
-    const uint32_t A = v.hd.y >> sh, B = v.hd.z >> sh, C = v.hd.w >> sh;
+    const uint32_t A = quad_bcast<1>(v.hw) >> sh, B = quad_bcast<2>(v.hw) >> sh, C = quad_bcast<3>(v.hw) >> sh;
     uint32_t SC, M;
     if (c < 2) {
         SC = A & 0x3F3Fu;
@@ -121,7 +134,7 @@ __device__ __forceinline__ float unit_dot(const Q4KUnit& v, const XSlice& xs, in
         SC = (C & 0x0F0Fu) | ((A >> 2) & 0x3030u);
         M = ((C >> 4) & 0x0F0Fu) | ((B >> 2) & 0x3030u);
     }
-    const float d = f16lo(v.hd.x), dmin = f16hi(v.hd.x);
+    const float d = f16lo(hx), dmin = f16hi(hx);
     const float sc0 = static_cast<float>(SC & 0xFFu), sc1 = static_cast<float>((SC >> 8) & 0xFFu);
     const float m0 = static_cast<float>(M & 0xFFu), m1 = static_cast<float>((M >> 8) & 0xFFu);
     const float dot = sc0 * (xs.s[0] * static_cast<float>(s0)) + sc1 * (xs.s[1] * static_cast<float>(s1));
@@ -179,20 +192,22 @@ __device__ __forceinline__ int64_t unit_x_offset(int u, int& seg_stride) {
 // ---- shared activation encoding (LDS) -------------------------------------
 //
 // The encoded slice of unit u lives in LDS as 11 uint4 "quads" at
-// xq[(kt * XQ_QUADS + q) * 64 + lane], kt = u / 64, lane = u % 64:
-// quads 0-3 = h[0..15], 4-7 = l[0..15], 8 = s[0..3], 9 = sum[0..3],
-// 10 = isum[0..3].  Consecutive lanes read consecutive 16-byte words, so the
-// per-lane ds_read_b128 loads are bank-conflict free.
+// xq[q * slots + u]: quads 0-3 = h[0..15], 4-7 = l[0..15], 8 = s[0..3],
+// 9 = sum[0..3], 10 = isum[0..3].  A wave's lanes read consecutive units, so
+// their ds_read_b128 loads are bank-conflict free.  `slots` (a multiple of 8)
+// covers every unit index a lane may read, idle lanes included; units past
+// the row are encoded as zeros.
 constexpr int XQ_QUADS = 11;
-constexpr int XQ_MAX_KTILES = 8;  // LDS encoding up to k = 32768
+constexpr int kMaxSlots = 520;      // LDS encoding up to k = 32768 (+ idle lanes)
+constexpr int kMaxRedFloats = 8192;  // per-row partial sums kept in LDS
 
-// All threads of the workgroup encode the activations of k-tiles [0, nkt):
-// one task = 8 consecutive elements of a unit; the 2 (Q6_K) or 4 tasks of a
-// run sit on adjacent lanes and combine their max / sums with shuffles.
-// Loading is split from encoding so the caller can put the weight loads in
-// between: loads return in issue order, so x must be requested first or its
-// encode would wait for the weights.
-constexpr int XT_MAX = 4;  // tasks per thread held in registers
+// All threads of the workgroup encode the activations of every slot: one
+// task = 8 consecutive elements of a unit; the 2 (Q6_K) or 4 tasks of a run
+// sit on adjacent lanes and combine their max / sums with shuffles.  Loading
+// is split from encoding so the caller can put the weight loads in between:
+// loads return in issue order, so x must be requested first or its encode
+// would wait for the weights.
+constexpr int XT_MAX = 2;  // tasks per thread held in registers
 
 struct XTasks {
     float v[XT_MAX][8];
@@ -222,7 +237,7 @@ __device__ __forceinline__ void load_x_task(const float* __restrict__ x, int uni
 }
 
 template <int TYPE>
-__device__ __forceinline__ void encode_x_task(int task, int units, const float* vin, uint4* xq) {
+__device__ __forceinline__ void encode_x_task(int task, int units, int slots, const float* vin, uint4* xq) {
     constexpr int RUNLEN = TYPE == TYPE_Q6_K ? 16 : 32;
     constexpr int TPR = RUNLEN / 8;
     const int u = task >> 3, p = task & 7;
@@ -255,24 +270,23 @@ __device__ __forceinline__ void encode_x_task(int task, int units, const float* 
     }
 #pragma unroll
     for (int m = 1; m < TPR; m <<= 1) isum += __shfl_xor(isum, m, 64);
-    const int kt = u >> 6, ln = u & 63;
-    uint4* base = xq + static_cast<size_t>(kt) * XQ_QUADS * 64 + ln;
-    reinterpret_cast<uint2*>(&base[(p >> 1) * 64])[p & 1] = make_uint2(ph[0], ph[1]);
-    reinterpret_cast<uint2*>(&base[(4 + (p >> 1)) * 64])[p & 1] = make_uint2(pl[0], pl[1]);
+    uint4* base = xq + u;
+    reinterpret_cast<uint2*>(&base[(p >> 1) * slots])[p & 1] = make_uint2(ph[0], ph[1]);
+    reinterpret_cast<uint2*>(&base[(4 + (p >> 1)) * slots])[p & 1] = make_uint2(pl[0], pl[1]);
     if (p % TPR == 0) {
         const int r = p / TPR;
-        reinterpret_cast<float*>(&base[8 * 64])[r] = amax / static_cast<float>(X16_MAX);
-        reinterpret_cast<float*>(&base[9 * 64])[r] = sum;
-        reinterpret_cast<int*>(&base[10 * 64])[r] = isum;
+        reinterpret_cast<float*>(&base[8 * slots])[r] = amax / static_cast<float>(X16_MAX);
+        reinterpret_cast<float*>(&base[9 * slots])[r] = sum;
+        reinterpret_cast<int*>(&base[10 * slots])[r] = isum;
     }
 }
 
-// Register path: at most XT_MAX tasks per thread.  The task count (nkt*512)
-// and the thread count are multiples of 64, so each wave's shuffles see all
-// 64 lanes active.
+// Register path: at most XT_MAX tasks per thread.  The task count (8 per
+// slot, slots a multiple of 8) and the thread count are multiples of 64, so
+// each wave's shuffles see all 64 lanes active.
 template <int TYPE>
-__device__ __forceinline__ void prefetch_x(const float* __restrict__ x, int units, int nkt, XTasks& t) {
-    const int ntasks = nkt * 64 * 8;
+__device__ __forceinline__ void prefetch_x(const float* __restrict__ x, int units, int slots, XTasks& t) {
+    const int ntasks = slots * 8;
 #pragma unroll
     for (int i = 0; i < XT_MAX; i++) {
         const int task = threadIdx.x + i * blockDim.x;
@@ -281,35 +295,35 @@ __device__ __forceinline__ void prefetch_x(const float* __restrict__ x, int unit
 }
 
 template <int TYPE>
-__device__ __forceinline__ void encode_x_regs(int units, int nkt, const XTasks& t, uint4* xq) {
-    const int ntasks = nkt * 64 * 8;
+__device__ __forceinline__ void encode_x_regs(int units, int slots, const XTasks& t, uint4* xq) {
+    const int ntasks = slots * 8;
 #pragma unroll
     for (int i = 0; i < XT_MAX; i++) {
         const int task = threadIdx.x + i * blockDim.x;
-        if (task < ntasks) encode_x_task<TYPE>(task, units, t.v[i], xq);
+        if (task < ntasks) encode_x_task<TYPE>(task, units, slots, t.v[i], xq);
     }
 }
 
 // Loop path for more tasks than fit in registers.
 template <int TYPE>
-__device__ void encode_x_loop(const float* __restrict__ x, int units, int nkt, uint4* xq) {
-    const int ntasks = nkt * 64 * 8;
+__device__ void encode_x_loop(const float* __restrict__ x, int units, int slots, uint4* xq) {
+    const int ntasks = slots * 8;
     for (int task = threadIdx.x; task < ntasks; task += blockDim.x) {
         float v[8];
         load_x_task<TYPE>(x, units, task, v);
-        encode_x_task<TYPE>(task, units, v, xq);
+        encode_x_task<TYPE>(task, units, slots, v, xq);
     }
 }
 
-__device__ __forceinline__ void read_xslice(const uint4* xq, int kt, int lane, XSlice& xs) {
-    const uint4* q = xq + static_cast<size_t>(kt) * XQ_QUADS * 64 + lane;
+__device__ __forceinline__ void read_xslice(const uint4* xq, int slots, int u, XSlice& xs) {
+    const uint4* q = xq + u;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const uint4 h = q[i * 64], l = q[(4 + i) * 64];
+        const uint4 h = q[i * slots], l = q[(4 + i) * slots];
         xs.h[4 * i] = h.x; xs.h[4 * i + 1] = h.y; xs.h[4 * i + 2] = h.z; xs.h[4 * i + 3] = h.w;
         xs.l[4 * i] = l.x; xs.l[4 * i + 1] = l.y; xs.l[4 * i + 2] = l.z; xs.l[4 * i + 3] = l.w;
     }
-    const uint4 s = q[8 * 64], sm = q[9 * 64], is = q[10 * 64];
+    const uint4 s = q[8 * slots], sm = q[9 * slots], is = q[10 * slots];
     xs.s[0] = __uint_as_float(s.x); xs.s[1] = __uint_as_float(s.y);
     xs.s[2] = __uint_as_float(s.z); xs.s[3] = __uint_as_float(s.w);
     xs.sum[0] = __uint_as_float(sm.x); xs.sum[1] = __uint_as_float(sm.y);
@@ -318,154 +332,126 @@ __device__ __forceinline__ void read_xslice(const uint4* xq, int kt, int lane, X
     xs.isum[2] = static_cast<int>(is.z); xs.isum[3] = static_cast<int>(is.w);
 }
 
-// One workgroup: `wpg` waves = (wpg / wpr) row groups x wpr k-waves.  A row
-// group walks its rows in NB batches of R; k-wave kw covers k-tiles kw,
-// kw + wpr, ...  Work is flattened into steps (batch, tile) and streamed
-// through a ring of D register buffers: the loads of step s + D are issued as
-// soon as step s has been computed, so D steps are always in flight and the
-// arithmetic of one step overlaps the HBM latency of the next ones.  The
-// step count is padded to a multiple of D; padding steps load the last real
-// step again (cache hits) and compute nothing, which keeps every load outside
-// branches (a branch around loads makes the compiler's wait counts
-// conservative).
-constexpr int kDepth = 4;
-
 // Row sources.  ROWS_PLAIN: row r of w.  ROWS_PAIRS: row r is row gidx[r/2]
 // of w (r even) or of w2 (r odd) -- gate/up pairs of the active neurons of a
 // sparse FFN, one launch and one activation encode for both matrices.
 constexpr int ROWS_PLAIN = 0;
 constexpr int ROWS_PAIRS = 1;
 
+// Row indices are 32-bit (the host checks n and nsrc < 2^31): 64-bit compares
+// have no scalar form on gfx9, and would pull the wave-uniform row
+// addressing onto the VALU.
 template <int MODE>
 __device__ __forceinline__ const uint8_t* row_ptr(const uint8_t* w, const uint8_t* w2,
-                                                  const int32_t* gidx, int64_t nsrc, int64_t row,
-                                                  int64_t rb) {
+                                                  const int32_t* gidx, int nsrc, int row, int64_t rb) {
     if constexpr (MODE == ROWS_PLAIN) {
-        return w + row * rb;
+        return w + static_cast<int64_t>(row) * rb;
     } else {
-        int64_t src = gidx[row >> 1];
+        int src = gidx[row >> 1];
         src = src < 0 ? 0 : (src >= nsrc ? nsrc - 1 : src);  // never read outside the tensor
-        return ((row & 1) ? w2 : w) + src * rb;
+        return ((row & 1) ? w2 : w) + static_cast<int64_t>(src) * rb;
     }
 }
 
+// Register budget: a 16-wave workgroup leaves 128 VGPRs per lane, enough
+// for a ring of 4 Q4_K units (9 VGPRs each) or 2 Q6_K / Q8_0 units (14 / 17);
+// deeper rings run in 8-wave workgroups (256 VGPRs).
+template <int TYPE>
+constexpr int max_d16() { return TYPE == TYPE_Q4_K ? 4 : 2; }
+template <int TYPE, int D>
+constexpr int gemv_max_threads() { return D <= max_d16<TYPE>() ? 1024 : 512; }
+
+// One workgroup: `wpg` waves = (wpg / wpr) row groups x wpr k-slices.  Row
+// group g owns rows [row0, row0 + rpg); k-slice kw covers units
+// [kw*upw, kw*upw + upw) of each of them, lane = unit.  Rows stream through a
+// ring of D register buffers: the loads of row s + D are issued as soon as
+// row s has been computed.  The row count is padded to a multiple of D;
+// padding rows load the last real row again (cache hits) and compute nothing,
+// which keeps every load outside branches (a branch around loads makes the
+// compiler's wait counts conservative).
+//
 // zbuf / zn: an int buffer the first workgroup clears (the counters of a
 // following kernel; a fill inside this launch keeps memsets out of captured
 // graphs).
-template <int TYPE, int R, int MODE>
-__global__ void __launch_bounds__(512) gemv_q_kernel(const uint8_t* __restrict__ w,
-                                                     const uint8_t* __restrict__ w2,
-                                                     const int32_t* __restrict__ gidx, int64_t nsrc,
-                                                     const float* __restrict__ x,
-                                                     float* __restrict__ y, int64_t n, int64_t rb,
-                                                     int units, int n_ktiles, int wpr, int nb,
-                                                     int* __restrict__ zbuf, int zn) {
+template <int TYPE, int D, int MODE>
+__global__ void __launch_bounds__((gemv_max_threads<TYPE, D>())) gemv_q_kernel(
+        const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, const int32_t* __restrict__ gidx,
+        int nsrc, const float* __restrict__ x, float* __restrict__ y, int n, int64_t rb, int units,
+        int slots, int upw, int wpr, int rpg, int* __restrict__ zbuf, int zn) {
     if (zn > 0 && blockIdx.x == 0) {
         for (int i = threadIdx.x; i < zn; i += blockDim.x) zbuf[i] = 0;
     }
     using Unit = typename UnitOf<TYPE>::T;
     extern __shared__ uint4 xq[];
-    __shared__ float red[8][R];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int groups = (blockDim.x >> 6) / wpr;
-    const int g = wave / wpr, kw = wave - g * wpr;
-    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * groups + g) * static_cast<int64_t>(R) * nb;
-    const int ntw = (n_ktiles + wpr - 1) / wpr;  // tiles per k-wave (uniform loop bound)
-    const int nsteps = nb * ntw;
-    const int nsteps_p = ((nsteps + kDepth - 1) / kDepth) * kDepth;
+    const int lane = threadIdx.x & 63;
+    // wave-uniform (readfirstlane): row addressing then runs on the scalar unit
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    // (integer division runs on the VALU: re-assert uniformity afterwards)
+    const int groups = __builtin_amdgcn_readfirstlane(static_cast<int>(blockDim.x >> 6) / wpr);
+    const int g = __builtin_amdgcn_readfirstlane(wave / wpr), kw = wave - g * wpr;
+    const int rows_wg = groups * rpg;
+    float* red = reinterpret_cast<float*>(xq + XQ_QUADS * slots);  // [wpr][rows_wg]
+    const int wg_row0 = static_cast<int>(blockIdx.x) * rows_wg;
+    const int row0 = wg_row0 + g * rpg;
+    const int u = kw * upw + lane;
+    const bool valid = lane < upw && u < units;
+    // Idle lanes load a real unit (discarded).  Q4_K keeps u % 4 == lane % 4
+    // (units and upw are multiples of 4) so every quad reads one super-block.
+    const int uc = valid ? u : units - 4 + (lane & 3);
+    const int nsteps_p = ((rpg + D - 1) / D) * D;
 
-    auto issue = [&](Unit* v, int step) {
-        step = step < nsteps ? step : nsteps - 1;
-        const int b = step / ntw, i = step - b * ntw;
-        int u = (kw + i * wpr) * 64 + lane;
-        u = u < units ? u : units - 1;
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            int64_t row = row0 + static_cast<int64_t>(b) * R + r;
-            row = row < n ? row : n - 1;
-            load_unit(row_ptr<MODE>(w, w2, gidx, nsrc, row, rb), u, v[r]);
-        }
+    auto issue = [&](Unit& v, int step) {
+        step = step < rpg ? step : rpg - 1;
+        int row = row0 + step;
+        row = row < n ? row : n - 1;
+        load_unit(row_ptr<MODE>(w, w2, gidx, nsrc, row, rb), uc, v);
     };
 
-    // x first, then the first D steps of weights, then the encode: the encode
+    // x first, then the first D rows of weights, then the encode: the encode
     // only waits for x, and the weights are in flight meanwhile.
-    Unit v0[R], v1[R], v2[R], v3[R];
-    const bool x_in_regs = n_ktiles * 512 <= XT_MAX * static_cast<int>(blockDim.x);
+    Unit v[D];
+    const bool x_in_regs = slots * 8 <= XT_MAX * static_cast<int>(blockDim.x);
     XTasks xt;
-    if (x_in_regs) prefetch_x<TYPE>(x, units, n_ktiles, xt);
+    if (x_in_regs) prefetch_x<TYPE>(x, units, slots, xt);
     __builtin_amdgcn_sched_barrier(0);
-    issue(v0, 0);
-    issue(v1, 1);
-    issue(v2, 2);
-    issue(v3, 3);
+#pragma unroll
+    for (int j = 0; j < D; j++) issue(v[j], j);
     __builtin_amdgcn_sched_barrier(0);  // keep the weight loads ahead of the encode
     if (x_in_regs)
-        encode_x_regs<TYPE>(units, n_ktiles, xt, xq);
+        encode_x_regs<TYPE>(units, slots, xt, xq);
     else
-        encode_x_loop<TYPE>(x, units, n_ktiles, xq);
+        encode_x_loop<TYPE>(x, units, slots, xq);
     __syncthreads();
 
     XSlice xs;
-    if (ntw == 1 && kw < n_ktiles) read_xslice(xq, kw, lane, xs);
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = 0.f;
+    read_xslice(xq, slots, valid ? u : 0, xs);
+    float* myred = red + kw * rows_wg + g * rpg;
 
-    auto compute = [&](const Unit* v, int step) {
-        if (step >= nsteps) return;  // padding step (uniform)
-        const int b = step / ntw, i = step - b * ntw;
-        const int kt = kw + i * wpr;
-        const int u = kt * 64 + lane;
-        if (ntw > 1 && kt < n_ktiles) read_xslice(xq, kt, lane, xs);
-        if (kt < n_ktiles && u < units) {
-#pragma unroll
-            for (int r = 0; r < R; r++) acc[r] += unit_dot(v[r], xs, u);
-        }
-        if (i == ntw - 1) {  // batch complete: reduce and store
-            const int64_t rbase = row0 + static_cast<int64_t>(b) * R;
-            float tot[R];
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                tot[r] = wave_sum_dpp(acc[r]);
-                acc[r] = 0.f;
-            }
-            if (wpr == 1) {
-                if (lane == 0) {
-#pragma unroll
-                    for (int r = 0; r < R; r++)
-                        if (rbase + r < n) y[rbase + r] = tot[r];
-                }
-            } else {
-                if (lane == 0) {
-#pragma unroll
-                    for (int r = 0; r < R; r++) red[wave][r] = tot[r];
-                }
-                __syncthreads();
-                if (kw == 0 && lane < R) {
-                    float s2 = 0.f;
-                    for (int j = 0; j < wpr; j++) s2 += red[wave + j][lane];
-                    if (rbase + lane < n) y[rbase + lane] = s2;
-                }
-                __syncthreads();
-            }
-        }
+    auto compute = [&](const Unit& vv, int step) {
+        if (step >= rpg) return;  // padding step (uniform)
+        float a = unit_dot(vv, xs, uc);
+        a = valid ? a : 0.f;
+        const float tot = wave_sum_dpp(a);
+        if (lane == 0) myred[step] = tot;
     };
 
     int s = 0;
-    for (; s + kDepth < nsteps_p; s += kDepth) {
-        compute(v0, s);
-        issue(v0, s + 4);
-        compute(v1, s + 1);
-        issue(v1, s + 5);
-        compute(v2, s + 2);
-        issue(v2, s + 6);
-        compute(v3, s + 3);
-        issue(v3, s + 7);
+    for (; s + D < nsteps_p; s += D) {
+#pragma unroll
+        for (int j = 0; j < D; j++) {
+            compute(v[j], s + j);
+            issue(v[j], s + j + D);
+        }
     }
-    compute(v0, s);
-    compute(v1, s + 1);
-    compute(v2, s + 2);
-    compute(v3, s + 3);
+#pragma unroll
+    for (int j = 0; j < D; j++) compute(v[j], s + j);
+
+    __syncthreads();
+    for (int i = threadIdx.x; i < rows_wg; i += blockDim.x) {
+        float t = red[i];
+        for (int k = 1; k < wpr; k++) t += red[k * rows_wg + i];
+        if (wg_row0 + i < n) y[wg_row0 + i] = t;
+    }
 }
 
 // F32 / F16 weights: plain fp32 dot products, one wave per R rows (rows
@@ -473,20 +459,21 @@ __global__ void __launch_bounds__(512) gemv_q_kernel(const uint8_t* __restrict__
 template <int TYPE, int R, int MODE>
 __global__ void __launch_bounds__(256) gemv_plain_kernel(const uint8_t* __restrict__ w,
                                                          const uint8_t* __restrict__ w2,
-                                                         const int32_t* __restrict__ gidx, int64_t nsrc,
+                                                         const int32_t* __restrict__ gidx, int nsrc,
                                                          const float* __restrict__ x,
-                                                         float* __restrict__ y, int64_t n, int64_t k,
+                                                         float* __restrict__ y, int n, int64_t k,
                                                          int* __restrict__ zbuf, int zn) {
     if (zn > 0 && blockIdx.x == 0) {
         for (int i = threadIdx.x; i < zn; i += blockDim.x) zbuf[i] = 0;
     }
     const int lane = threadIdx.x & 63;
-    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6)) * R;
+    const int row0 = (static_cast<int>(blockIdx.x) * static_cast<int>(blockDim.x >> 6) +
+                      __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6))) * R;
     constexpr int64_t ES = TYPE == TYPE_F32 ? 4 : 2;
     const uint8_t* rp[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
-        int64_t row = row0 + r;
+        int row = row0 + r;
         row = row < n ? row : n - 1;
         rp[r] = row_ptr<MODE>(w, w2, gidx, nsrc, row, k * ES);
     }
@@ -515,88 +502,104 @@ __global__ void __launch_bounds__(256) gemv_plain_kernel(const uint8_t* __restri
 }
 
 struct GemvShape {
-    int units, n_ktiles, wpr, wpg, r, nb;
+    int units, slots, upw, wpr, wpg, rpg, depth;
     int64_t grid;
     size_t lds;
 };
 
 constexpr int kNumCUs = 256;
 
-// rows per step (kDepth steps are in flight).  One row per step measured
-// fastest for every type and shape (deeper per-row pipelining beats wider
-// steps).
+// Ring depth for rpg rows per wave: every row in flight when rpg <= 8 (4 for
+// Q6_K / Q8_0, whose units take 14-17 VGPRs), else a ring of 4.
 template <int TYPE>
-constexpr int max_rows() { return 1; }
+int ring_depth(int rpg) {
+    if (rpg <= 2) return 2;
+    if (rpg <= 4 || TYPE != TYPE_Q4_K) return 4;
+    return rpg <= 8 ? 8 : 4;
+}
 
-// Launch geometry: for each candidate workgroup size (waves), rows are split
-// so the grid covers the CUs about once with R <= max_r rows per step; the
-// candidate with the fewest rows per CU wins (ties: more waves).
-// VB_GEMV_CFG="wpg,r,nb" overrides (tuning sweeps).
-GemvShape gemv_shape(int64_t n, int units, int max_r) {
+template <int TYPE>
+int gemv_max_threads_host(int depth) { return depth <= max_d16<TYPE>() ? 1024 : 512; }
+
+// Launch geometry.  k-slices: wpr = ceil(units / 64) waves per row, upw the
+// units per slice rounded up to a multiple of 4.  Rows (rules from sweeps on
+// MI355X, 256 CUs): single-slice rows run in 8-wave workgroups with up to 4
+// rows per wave and up to 2 workgroups per CU, every row in flight at once
+// (e.g. 14336 rows: 4 rows per wave, 448 workgroups); more rows than that
+// stream through one workgroup per CU (Q6_K lm_head, 128256 rows: 63 rows per
+// wave).  Multi-slice rows (k > 4096) use 16-wave workgroups with a ring of
+// 4.  VB_GEMV_CFG="wpg,rpg" overrides (tuning sweeps).
+template <int TYPE>
+GemvShape gemv_shape(int64_t n, int units) {
     GemvShape s;
     s.units = units;
-    s.n_ktiles = (units + 63) / 64;
-    s.wpr = s.n_ktiles <= 1 ? 1 : (s.n_ktiles <= 2 ? 2 : 4);
-    int64_t best_cost = -1;
-    for (int wpg = 8; wpg >= 4; wpg--) {
-        if (wpg % s.wpr) continue;
-        const int groups = wpg / s.wpr;
-        int64_t per_group = (n + static_cast<int64_t>(kNumCUs) * groups - 1) /
-                            (static_cast<int64_t>(kNumCUs) * groups);
-        if (per_group < 1) per_group = 1;
-        const int r = static_cast<int>(per_group < max_r ? per_group : max_r);
-        int nb = static_cast<int>((per_group + r - 1) / r);
-        const int64_t rows_per_wg = static_cast<int64_t>(groups) * r * nb;
-        const int64_t grid = (n + rows_per_wg - 1) / rows_per_wg;
-        const int64_t cost = ((grid + kNumCUs - 1) / kNumCUs) * rows_per_wg;
-        if (best_cost < 0 || cost < best_cost) {
-            best_cost = cost;
-            s.wpg = wpg;
-            s.r = r;
-            s.nb = nb;
-        }
+    s.wpr = (units + 63) / 64;
+    s.upw = ((units + s.wpr - 1) / s.wpr + 3) & ~3;
+    s.slots = (((s.wpr - 1) * s.upw + 64) + 7) & ~7;
+    if (s.wpr == 1) {
+        s.wpg = 8;
+        const int64_t per2 = (n + 2 * kNumCUs * 8 - 1) / (2 * kNumCUs * 8);
+        const int64_t per1 = (n + kNumCUs * 8 - 1) / (kNumCUs * 8);
+        s.rpg = static_cast<int>(per2 <= 4 ? per2 : per1);
+    } else {
+        s.wpg = s.wpr <= 4 ? 16 / s.wpr * s.wpr : s.wpr;
+        if (s.wpg > 16) s.wpg = s.wpr;  // > 4096 * 16 elements: one row group per workgroup
+        const int groups = s.wpg / s.wpr;
+        s.rpg = static_cast<int>((n + static_cast<int64_t>(kNumCUs) * groups - 1) / (static_cast<int64_t>(kNumCUs) * groups));
     }
+    if (s.rpg < 1) s.rpg = 1;
+    const int64_t max_rpg = kMaxRedFloats / (static_cast<int64_t>(s.wpg / s.wpr) * s.wpr);
+    if (s.rpg > max_rpg) s.rpg = static_cast<int>(max_rpg);
+    if (64 * s.wpg > gemv_max_threads_host<TYPE>(ring_depth<TYPE>(s.rpg))) s.wpg = 8 / s.wpr * s.wpr;
+    if (s.wpg < s.wpr) s.wpg = s.wpr;
     if (const char* cfg = std::getenv("VB_GEMV_CFG")) {
-        int a = 0, b = 0, c = 0;
-        if (std::sscanf(cfg, "%d,%d,%d", &a, &b, &c) == 3 && a >= 1 && a <= 8 && b >= 1 && b <= 2 &&
-            c >= 1 && a % s.wpr == 0) {
+        int a = 0, b = 0;
+        if (std::sscanf(cfg, "%d,%d", &a, &b) == 2 && a >= 1 && a <= 16 && b >= 1 && a % s.wpr == 0 &&
+            static_cast<int64_t>(a / s.wpr) * b * s.wpr <= kMaxRedFloats &&
+            64 * a <= gemv_max_threads_host<TYPE>(ring_depth<TYPE>(b))) {
             s.wpg = a;
-            s.r = b;
-            s.nb = c;
+            s.rpg = b;
         }
     }
-    const int64_t rows_per_wg = static_cast<int64_t>(s.wpg / s.wpr) * s.r * s.nb;
-    s.grid = (n + rows_per_wg - 1) / rows_per_wg;
-    s.lds = static_cast<size_t>(s.n_ktiles) * XQ_QUADS * 64 * sizeof(uint4);
+    s.depth = ring_depth<TYPE>(s.rpg);
+    const int64_t rows_wg = static_cast<int64_t>(s.wpg / s.wpr) * s.rpg;
+    s.grid = (n + rows_wg - 1) / rows_wg;
+    s.lds = static_cast<size_t>(s.slots) * XQ_QUADS * sizeof(uint4) + rows_wg * s.wpr * sizeof(float);
     return s;
 }
 
-template <int TYPE, int R>
-int launch_gemv_r(const GemvShape& s, const void* w, const RowSrc& src, const float* x, float* y, int64_t n,
+template <int TYPE, int D>
+int launch_gemv_d(const GemvShape& s, const void* w, const RowSrc& src, const float* x, float* y, int64_t n,
                   int64_t rb, hipStream_t st) {
     const dim3 g(static_cast<uint32_t>(s.grid)), b(64 * s.wpg);
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     const uint8_t* w2 = static_cast<const uint8_t*>(src.w2);
+    const int ni = static_cast<int>(n), nsrc = static_cast<int>(src.nsrc);
     if (src.gidx)
-        gemv_q_kernel<TYPE, R, ROWS_PAIRS><<<g, b, s.lds, st>>>(wb, w2, src.gidx, src.nsrc, x, y, n, rb, s.units,
-                                                                s.n_ktiles, s.wpr, s.nb, src.zbuf, src.zn);
+        gemv_q_kernel<TYPE, D, ROWS_PAIRS><<<g, b, s.lds, st>>>(wb, w2, src.gidx, nsrc, x, y, ni, rb, s.units,
+                                                                s.slots, s.upw, s.wpr, s.rpg, src.zbuf, src.zn);
     else
-        gemv_q_kernel<TYPE, R, ROWS_PLAIN><<<g, b, s.lds, st>>>(wb, w2, src.gidx, src.nsrc, x, y, n, rb, s.units,
-                                                                s.n_ktiles, s.wpr, s.nb, src.zbuf, src.zn);
+        gemv_q_kernel<TYPE, D, ROWS_PLAIN><<<g, b, s.lds, st>>>(wb, w2, src.gidx, nsrc, x, y, ni, rb, s.units,
+                                                                s.slots, s.upw, s.wpr, s.rpg, src.zbuf, src.zn);
     return check_launch("vb_gemv");
 }
 
 template <int TYPE>
 int launch_gemv_q(const void* w, const RowSrc& src, const float* x, float* y, int64_t n, int64_t k,
                   int64_t rb, hipStream_t st) {
-    const GemvShape s = gemv_shape(n, static_cast<int>(k / 64), max_rows<TYPE>());
-    if (s.n_ktiles > XQ_MAX_KTILES) {
-        set_error("vb_gemv: k=%lld exceeds the supported maximum of %d", static_cast<long long>(k),
-                  XQ_MAX_KTILES * 64 * 64);
+    const int units = static_cast<int>(k / 64);
+    const GemvShape s = gemv_shape<TYPE>(n, units);
+    if (s.slots > kMaxSlots) {
+        set_error("vb_gemv: k=%lld exceeds the supported maximum of 32768", static_cast<long long>(k));
         return E_UNSUPPORTED;
     }
-    if (s.r == 1) return launch_gemv_r<TYPE, 1>(s, w, src, x, y, n, rb, st);
-    return launch_gemv_r<TYPE, 2>(s, w, src, x, y, n, rb, st);
+    switch (s.depth) {
+    case 2: return launch_gemv_d<TYPE, 2>(s, w, src, x, y, n, rb, st);
+    case 4: return launch_gemv_d<TYPE, 4>(s, w, src, x, y, n, rb, st);
+    default:
+        if constexpr (TYPE == TYPE_Q4_K) return launch_gemv_d<TYPE, 8>(s, w, src, x, y, n, rb, st);
+        return launch_gemv_d<TYPE, 4>(s, w, src, x, y, n, rb, st);
+    }
 }
 
 }  // namespace
@@ -616,6 +619,10 @@ int gemv_dispatch_src(const void* w, const RowSrc& src, const float* x, float* y
         return E_INVAL;
     }
     if (n == 0) return OK;
+    if (n > INT32_MAX || src.nsrc > INT32_MAX) {
+        set_error("vb_gemv: n=%lld rows exceeds the supported maximum of 2^31-1", static_cast<long long>(n));
+        return E_UNSUPPORTED;
+    }
     if ((type == TYPE_Q4_K || type == TYPE_Q6_K || type == TYPE_Q8_0) && k % 64 != 0) {
         set_error("vb_gemv: k=%lld must be a multiple of 64 for type %d", static_cast<long long>(k), type);
         return E_UNSUPPORTED;
@@ -631,29 +638,36 @@ int gemv_dispatch_src(const void* w, const RowSrc& src, const float* x, float* y
         return E_INVAL;
     }
     switch (type) {
-    case TYPE_Q4_K: return launch_gemv_q<TYPE_Q4_K>(w, src, x, y, n, k, rb, st);
+    case TYPE_Q4_K: {
+        // v_dot4 kernel by default (fastest measured); VB_GEMV_Q4K_PATH=mfma
+        // selects the int8-MFMA kernel (same arithmetic)
+        const char* path = std::getenv("VB_GEMV_Q4K_PATH");
+        if (path && std::strcmp(path, "mfma") == 0) return gemv_q4k_mfma(w, src, x, y, n, k, st);
+        return launch_gemv_q<TYPE_Q4_K>(w, src, x, y, n, k, rb, st);
+    }
     case TYPE_Q6_K: return launch_gemv_q<TYPE_Q6_K>(w, src, x, y, n, k, rb, st);
     case TYPE_Q8_0: return launch_gemv_q<TYPE_Q8_0>(w, src, x, y, n, k, rb, st);
     case TYPE_F32:
     case TYPE_F16: {
         constexpr int R = 4;
         const int64_t grid = (n + 4 * R - 1) / (4 * R);
+        const int ni = static_cast<int>(n), nsrc = static_cast<int>(src.nsrc);
         const dim3 g(static_cast<uint32_t>(grid)), b(256);
         const uint8_t* wb = static_cast<const uint8_t*>(w);
         const uint8_t* w2 = static_cast<const uint8_t*>(src.w2);
         if (type == TYPE_F32) {
             if (src.gidx)
-                gemv_plain_kernel<TYPE_F32, R, ROWS_PAIRS><<<g, b, 0, st>>>(wb, w2, src.gidx, src.nsrc, x, y, n, k,
+                gemv_plain_kernel<TYPE_F32, R, ROWS_PAIRS><<<g, b, 0, st>>>(wb, w2, src.gidx, nsrc, x, y, ni, k,
                                                                            src.zbuf, src.zn);
             else
-                gemv_plain_kernel<TYPE_F32, R, ROWS_PLAIN><<<g, b, 0, st>>>(wb, w2, src.gidx, src.nsrc, x, y, n, k,
+                gemv_plain_kernel<TYPE_F32, R, ROWS_PLAIN><<<g, b, 0, st>>>(wb, w2, src.gidx, nsrc, x, y, ni, k,
                                                                            src.zbuf, src.zn);
         } else {
             if (src.gidx)
-                gemv_plain_kernel<TYPE_F16, R, ROWS_PAIRS><<<g, b, 0, st>>>(wb, w2, src.gidx, src.nsrc, x, y, n, k,
+                gemv_plain_kernel<TYPE_F16, R, ROWS_PAIRS><<<g, b, 0, st>>>(wb, w2, src.gidx, nsrc, x, y, ni, k,
                                                                            src.zbuf, src.zn);
             else
-                gemv_plain_kernel<TYPE_F16, R, ROWS_PLAIN><<<g, b, 0, st>>>(wb, w2, src.gidx, src.nsrc, x, y, n, k,
+                gemv_plain_kernel<TYPE_F16, R, ROWS_PLAIN><<<g, b, 0, st>>>(wb, w2, src.gidx, nsrc, x, y, ni, k,
                                                                            src.zbuf, src.zn);
         }
         return check_launch("vb_gemv");

@@ -85,8 +85,25 @@ __device__ __forceinline__ void q4k_chunk_scales(const uint4& hd, int c, half2_t
     }
 }
 
+// Natural-k-order variant: dword i of a fragment holds elements (2i, 2i+1).
+// v_perm spreads bytes (b0, b1) of a qs dword into the two halves first, so
+// the activation operand needs no reordering (X can be staged as is).
+__device__ __forceinline__ void q4k_bfrags_nat(uint32_t q0, uint32_t q1, const half2_t* ds, const half2_t* nm,
+                                               Frag& lo, Frag& hi) {
+    const half2_t k1024 = half2_t{static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+    const uint32_t src[4] = {__builtin_amdgcn_perm(0u, q0, 0x0C010C00u), __builtin_amdgcn_perm(0u, q0, 0x0C030C02u),
+                             __builtin_amdgcn_perm(0u, q1, 0x0C010C00u), __builtin_amdgcn_perm(0u, q1, 0x0C030C02u)};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const half2_t a = bits2h((src[i] & 0x000F000Fu) | 0x64006400u) - k1024;
+        const half2_t b = bits2h(((src[i] >> 4) & 0x000F000Fu) | 0x64006400u) - k1024;
+        lo.u[i] = h2bits(__builtin_elementwise_fma(a, ds[0], nm[0]));
+        hi.u[i] = h2bits(__builtin_elementwise_fma(b, ds[1], nm[1]));
+    }
+}
+
 // Dequantize the two B fragments (sub-blocks 2c, 2c+1) of one lane from its
-// 8 qs bytes (q0 = bytes 0-3, q1 = bytes 4-7).
+// 8 qs bytes (q0 = bytes 0-3, q1 = bytes 4-7), sigma order.
 __device__ __forceinline__ void q4k_bfrags(uint32_t q0, uint32_t q1, const half2_t* ds,
                                            const half2_t* nm, Frag& lo, Frag& hi) {
     const half2_t k1024 = half2_t{static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};

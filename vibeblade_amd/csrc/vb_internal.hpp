@@ -20,6 +20,10 @@ int gemv_dispatch(const void* w, const float* x, float* y, int64_t n, int64_t k,
                   hipStream_t st);
 int gemv_dispatch_src(const void* w, const RowSrc& src, const float* x, float* y, int64_t n, int64_t k,
                       int32_t type, hipStream_t st);
+// Q4_K M=1 GEMV on the int8 matrix cores (gemv_q4k_mfma.hip); arguments
+// already validated by gemv_dispatch_src.
+int gemv_q4k_mfma(const void* w, const RowSrc& src, const float* x, float* y, int64_t n, int64_t k,
+                  hipStream_t st);
 int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, int64_t N, int64_t K,
                   int32_t type, int32_t variant, hipStream_t st);
 
