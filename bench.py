@@ -36,6 +36,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = os.path.join("profiles", "q4k_gemv_14336x4096_traffic.json")
+GEMV_KERNEL = "gemv_q_kernel<12"  # the Q4_K v_dot4 GEMV instantiations
+CALIB_BYTES = 256 << 20            # bytes read and written by the calibration copy
 MFMA_FP16_PEAK_TFS = 2500.0  # dense fp16 MFMA, MI355X
 NCOPIES = 16
 SEED = 1234
@@ -54,6 +57,12 @@ def parse():
     p.add_argument("--extra", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--pmc-pass", action="store_true",
+                   help="eager launches for rocprofv3 --pmc: 32 headline GEMVs, then a 256 MiB copy "
+                        "(torch.neg) that calibrates FETCH_SIZE / WRITE_SIZE")
+    p.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                   help="turn the counter_collection.csv files of two --pmc-pass runs (FETCH_SIZE, "
+                        "WRITE_SIZE) into " + TRAFFIC_FILE)
     return p.parse_args()
 
 
@@ -69,17 +78,23 @@ def make_copies(qtype, n, k, ncopies, gen):
     return copies
 
 
+GRAPH_LAUNCHES = 128  # launches captured per graph: amortizes the gap between replays
+
+
 def time_launches(launch_fns, steps, warmup):
-    """Capture one call of every closure in `launch_fns` (each takes a stream
-    handle) in a HIP graph and replay it; returns (ms per launch, graph used,
-    launches timed).  HIP events on the replay stream bracket the timed region."""
+    """Capture calls of the closures in `launch_fns` (each takes a stream
+    handle; rounds over the list until about GRAPH_LAUNCHES launches) in a
+    HIP graph and replay it; returns (ms per launch, graph used, launches
+    timed).  HIP events on the replay stream bracket the timed region."""
     import torch
     stream = torch.cuda.Stream()
-    nl = len(launch_fns)
+    rounds = max(1, GRAPH_LAUNCHES // len(launch_fns))
+    nl = rounds * len(launch_fns)
 
     def launch_all(s):
-        for f in launch_fns:
-            f(s)
+        for _ in range(rounds):
+            for f in launch_fns:
+                f(s)
 
     graph = None
     with torch.cuda.stream(stream):
@@ -282,8 +297,92 @@ def cpu_baseline(qtype, n, k, seconds):
     }
 
 
+def pmc_pass():
+    """Launches for counter collection: no graph (per-dispatch counters), no
+    timing.  The GEMVs rotate over 16 weight copies as in the timed run."""
+    import torch
+    from vibeblade_amd import _lib, ggml
+    _lib.init(0)
+    qtype, n, k = ggml.GGML_TYPE_Q4_K, 14336, 4096
+    gen = torch.Generator(device="cuda").manual_seed(SEED)
+    copies = make_copies(qtype, n, k, NCOPIES, gen)
+    x = torch.randn(k, generator=gen, device="cuda")
+    y = torch.empty(n, device="cuda")
+    lib = _lib.load()
+    st = torch.cuda.current_stream().cuda_stream
+    for i in range(32):
+        c = copies[i % NCOPIES]
+        _lib.check("vb_gemv", lib.vb_gemv(c.ptr(), x.data_ptr(), y.data_ptr(), n, k, qtype, st))
+    torch.cuda.synchronize()
+    del copies
+    torch.cuda.empty_cache()
+    src = torch.randn(CALIB_BYTES // 4, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print("[bench] pmc pass done: 32 GEMV dispatches, 4 calibration copies", file=sys.stderr)
+
+
+def _counter_means(path, counter):
+    """Mean counter value per kernel name (all dispatches) from a rocprofv3
+    counter_collection.csv."""
+    import csv
+    sums, cnt = {}, {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] != counter:
+                continue
+            key = (r["Kernel_Name"], r.get("Dispatch_Id", ""))
+            sums[key] = sums.get(key, 0.0) + float(r["Counter_Value"])
+    per_kernel = {}
+    for (name, _), v in sums.items():
+        per_kernel.setdefault(name, []).append(v)
+    return {name: (sum(v) / len(v), len(v)) for name, v in per_kernel.items()}
+
+
+def summarize_pmc(fetch_csv, write_csv):
+    """Traffic per GEMV launch = FETCH_SIZE x read factor + WRITE_SIZE x write
+    factor, the factors being what the calibration copy (CALIB_BYTES read and
+    written) shows for the same counters (KiB per dispatch)."""
+    out = {}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        means = _counter_means(path, counter)
+        gemv = [(v, c, name) for name, (v, c) in means.items() if GEMV_KERNEL in name]
+        calib = [(v, c, name) for name, (v, c) in means.items() if "neg_kernel" in name]
+        if not gemv or not calib:
+            raise SystemExit(f"{path}: no {counter} rows for the GEMV or the calibration copy")
+        g_kib, g_n, g_name = max(gemv, key=lambda t: t[1])
+        c_kib, c_n, _ = max(calib, key=lambda t: t[1])
+        factor = CALIB_BYTES / (c_kib * 1024.0)
+        out[counter] = {"gemv_kib_per_dispatch": round(g_kib, 1), "gemv_dispatches": g_n,
+                        "calib_kib_per_dispatch": round(c_kib, 1), "calib_dispatches": c_n,
+                        "scale_factor": round(factor, 4), "gemv_bytes": round(g_kib * 1024.0 * factor)}
+        out["kernel"] = g_name
+    out["traffic_bytes_per_launch"] = out["FETCH_SIZE"]["gemv_bytes"] + out["WRITE_SIZE"]["gemv_bytes"]
+    out["workload"] = "Q4_K GEMV 14336x4096, M=1"
+    with open(os.path.join(ROOT, TRAFFIC_FILE), "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps(out))
+
+
+def load_traffic():
+    """HBM bytes per launch from the committed counter summary, if any."""
+    try:
+        with open(os.path.join(ROOT, TRAFFIC_FILE)) as f:
+            return int(json.load(f)["traffic_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     args = parse()
+    if args.summarize_pmc:
+        summarize_pmc(*args.summarize_pmc)
+        return
+    if args.pmc_pass:
+        pmc_pass()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(this build has no multi-GPU path)", file=sys.stderr)
@@ -376,7 +475,7 @@ def main():
                    "n": n, "k": k, "m": 1, "weight_copies": NCOPIES, "hip_graph": graph_used,
                    "rel_l2_vs_oracle": float(f"{err:.3e}")},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
                      "alg_bytes_per_launch": ab, "us_per_launch": round(ms * 1e3, 3)},
         "cpu_baseline": cpu,
     }
