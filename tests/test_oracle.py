@@ -89,6 +89,24 @@ def test_q4k_index_map_single_nibble():
             assert np.array_equal(y, want), (byte, hi)
 
 
+@pytest.mark.skipif(not O.ref_available(), reason="compiled reference (oracle/_ref) not built here")
+def test_q4k_every_scale_byte_matches_compiled_reference():
+    """256 blocks in which every one of the 12 scale bytes takes all 256
+    values (so every 6-bit scale / min field of get_scale_min_k4,
+    cpp/src/dequant.cpp:258-266, takes all 64 values in every position),
+    decoded by the oracle and by the compiled reference."""
+    nb = 256
+    rng = np.random.default_rng(7)
+    blk = rng.integers(0, 256, size=(nb, 144), dtype=np.uint8)
+    for i in range(12):
+        blk[:, 4 + i] = (np.arange(nb) * 1 + i * 37) & 255
+    blk[:, 0:2] = np.frombuffer(np.float16(0.75).tobytes(), np.uint8)
+    blk[:, 2:4] = np.frombuffer(np.float16(0.125).tobytes(), np.uint8)
+    got = O.dequantize(blk.reshape(1, -1), nb * 256, O.TYPE_Q4_K)
+    want = O.ref_dequantize(blk.ravel(), nb * 256, O.TYPE_Q4_K)
+    assert np.array_equal(bits(got.ravel()), bits(np.asarray(want).ravel()))
+
+
 def test_q4k_min_term():
     b = bytearray(_q4k_unit_block([0x33] * 128).tobytes())
     b[2:4] = struct.pack("<e", 0.5)
