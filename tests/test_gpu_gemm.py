@@ -65,6 +65,18 @@ def test_tiled(dtype, m, n, k):
     assert np.all(np.abs(y).sum(axis=1) > 0)
 
 
+@pytest.mark.parametrize("nf", ["6", "8"])
+def test_tiled_column_tiles(monkeypatch, nf):
+    """Both workgroup widths (96 and 128 columns), ragged M and N edges."""
+    monkeypatch.setenv("VB_GEMM_NF", nf)
+    qt, x = make(300, 333, 1280, 21)
+    for dtype in (torch.float16, torch.float32):
+        xt = torch.from_numpy(x).to("cuda", dtype)
+        y = gemm(qt, xt, variant=GEMM_TILED).cpu().numpy()
+        want = O.gemm(qt.to_numpy_bytes(), xt.float().cpu().numpy(), 333, 1280, qt.qtype)
+        assert O.rel_l2(y, want) <= TOL, (nf, dtype)
+
+
 def test_tiled_matches_skinny_on_overlap():
     qt, x = make(16, 96, 1024, 5)
     xt = torch.from_numpy(x).to("cuda", torch.float16)

@@ -108,120 +108,247 @@ __global__ void __launch_bounds__(256) gemm_q4k_skinny(const uint8_t* __restrict
 }
 
 // ---- tiled: M > 16 ------------------------------------------------------------
+//
+// Workgroup tile: 256 rows of X x BN = 16 * NF weight rows (output columns),
+// 4 x WN waves; wave (wm, wn) owns X rows [64 wm, +64) x fragment columns
+// [wn * NF / WN, +NF / WN): 4 x NF / WN accumulator fragments, two waves per
+// SIMD with WN = 2.  k advances one Q4_K chunk (64 elements) per step, and
+// both operands of a step are staged in LDS (double-buffered):
+//  * B: the workgroup dequantizes the BN x 64 weight tile once into fp16 B
+//    fragments (natural k order); each of the 4 * BN "units" (8 qs bytes of
+//    one row -> the same lane of the step's two fragments) belongs to one
+//    thread.  Raw weight bytes run PD steps ahead in registers (HBM latency).
+//  * A: the 256 x 64 X tile is loaded with row-contiguous 16-byte pieces
+//    (8 lanes per 128-byte row: 4 x fewer cache-line requests than loading
+//    the fragments directly, and no duplicate loads across wave columns) two
+//    steps ahead, converted to fp16 and stored in rows padded to 144 bytes;
+//    the waves read their A fragments with ds_read_b128.
+// One barrier per step.  The grid is ceil(N / BN) x ceil(M / 256).
+constexpr int TB_M = 256;
+constexpr int XS_STRIDE = 72;  // halves per LDS row of X (64 + 8 padding)
+// weight prefetch distance (steps; K / 64 is a multiple of 4)
+constexpr int PD = 4;
 
-constexpr int BM = 256, BN = 128, BK = 64;
-constexpr int XS_STRIDE = BK + 8;  // halves per LDS row (144 bytes)
-constexpr int MF = 8, NF = 4;      // fragments per wave (128 x 64)
+template <int XT, int NF, int WN>
+__global__ void __launch_bounds__(256 * WN) gemm_q4k_tiled(const uint8_t* __restrict__ w,
+                                                           const void* __restrict__ X, float* __restrict__ Y,
+                                                           int M, int N, int K, int64_t rb) {
+    constexpr int NT = 256 * WN;            // threads
+    constexpr int NU = 4 * 16 * NF;         // dequant units per step
+    constexpr int UPT = (NU + NT - 1) / NT;  // units per thread
+    constexpr int NW = NF / WN;             // B fragments per wave
+    constexpr uint32_t XE = XT == X_F16 ? 2u : 4u;  // bytes per X element
+    constexpr int XPR = 8;                  // 8-element pieces per X row and step
+    constexpr int XPT = TB_M * XPR / NT;    // X pieces per thread and step
+    constexpr int XR = XT == X_F16 ? 1 : 2;  // uint4 per piece
+    static_assert(NF % WN == 0, "NF must split evenly over the wave columns");
+    static_assert(TB_M * XPR % NT == 0, "X pieces must split evenly over the threads");
+    // [buffer][k half][fragment][lane]; fragment NF takes the stores of
+    // threads without a unit (keeps the loop body branch-free)
+    __shared__ uint4 bt[2][2][NF + 1][64];
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2][TB_M * XS_STRIDE];
 
-template <int XT>
-__global__ void __launch_bounds__(256) gemm_q4k_tiled(const uint8_t* __restrict__ w,
-                                                      const void* __restrict__ X, float* __restrict__ Y,
-                                                      int64_t M, int64_t N, int64_t K, int64_t rb) {
-    __shared__ __attribute__((aligned(16))) _Float16 xs[2][BM * XS_STRIDE];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(tid >> 6));
+    const int wm = wave / WN, wn = wave - wm * WN;
     const int j = lane & 15, g = lane >> 4;
-    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * BM;
-    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * BN;
-    const int nchunks = static_cast<int>(K / BK);
+    // Tile of this workgroup.  Workgroups are dealt to the 8 XCDs round
+    // robin (linear id % 8).  With two M-tiles, the XCDs are split between
+    // them so each XCD's L2 holds one M-tile of X.
+    const int nt = static_cast<int>(gridDim.x), mt = static_cast<int>(gridDim.y);
+    int tile_n = static_cast<int>(blockIdx.x), tile_m = static_cast<int>(blockIdx.y);
+    if (mt == 2 && nt % 4 == 0) {
+        const int lin = tile_n + nt * tile_m, xcd = lin & 7, r = lin >> 3;
+        tile_m = xcd >> 2;
+        tile_n = (xcd & 3) * (nt >> 2) + r;
+    }
+    const int mt0 = tile_m * TB_M;
+    const int n0 = tile_n * 16 * NF;
+    const int nsteps = K / 64;
 
-    // weight rows of this lane's 4 B fragments
-    const uint8_t* wrow[NF];
+    // ---- weights: dequant units u = tid + NT i -> row un = u / 4, part ug = u % 4
+    uint32_t urow[UPT];  // byte offset of the unit's weight row in W
+    uint32_t uq[UPT];    // byte offset of the unit's 8 qs bytes within a chunk's 32
+    int uslot[UPT];      // LDS lane slot: fragment un / 16, lane 16 ug + un % 16
 #pragma unroll
-    for (int f = 0; f < NF; f++) {
-        int64_t n = n0 + wn * 64 + 16 * f + j;
+    for (int i = 0; i < UPT; i++) {
+        int u = tid + NT * i;
+        const bool live = u < NU;
+        u = live ? u : NU - 1;
+        const int un = u >> 2, ug = u & 3;
+        int n = n0 + un;
         n = n < N ? n : N - 1;
-        wrow[f] = w + n * rb;
+        urow[i] = static_cast<uint32_t>(n) * static_cast<uint32_t>(rb);
+        uq[i] = 16u + 8u * static_cast<uint32_t>(ug);
+        uslot[i] = live ? (un >> 4) * 64 + 16 * ug + (un & 15) : NF * 64 + lane;
     }
-
-    // X staging: thread owns 8 16-byte pieces (row = q/8, part = q%8).
-    uint32_t xr[8][4];
-    auto load_x = [&](int ch) {
+    uint4 whd[PD][UPT];
+    uint2 wqs[PD][UPT];
+    auto load_w = [&](int step, int slot) {
+        step = step < nsteps ? step : nsteps - 1;
+        const uint32_t sbo = static_cast<uint32_t>(step >> 2) * 144u, co = static_cast<uint32_t>(step & 3) * 32u;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int q = tid + 256 * i;
-            const int r = q >> 3, part = q & 7;
-            const int64_t t = m0 + r;
-            Frag f;
-            load_afrag<XT>(X, K, t < M ? t : 0, static_cast<int64_t>(ch) * BK + 8 * part, t < M, f);
-#pragma unroll
-            for (int e = 0; e < 4; e++) xr[i][e] = f.u[e];
+        for (int i = 0; i < UPT; i++) {
+            whd[slot][i] = *reinterpret_cast<const uint4*>(w + (urow[i] + sbo));
+            wqs[slot][i] = *reinterpret_cast<const uint2*>(w + (urow[i] + sbo + uq[i] + co));
         }
     };
-    auto store_x = [&](int buf) {
+    auto dequant_store = [&](int step, int slot, int buf) {
+        const int c = step & 3;
+        uint4* dst = &bt[buf][0][0][0];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int q = tid + 256 * i;
-            const int r = q >> 3, part = q & 7;
-            *reinterpret_cast<uint4*>(&xs[buf][r * XS_STRIDE + 8 * part]) =
-                make_uint4(xr[i][0], xr[i][1], xr[i][2], xr[i][3]);
-        }
-    };
-    uint4 hd[NF];
-    uint2 qv[NF];
-    auto load_w = [&](int ch) {
-        const int sb = ch >> 2, c = ch & 3;
-#pragma unroll
-        for (int f = 0; f < NF; f++) {
-            const uint8_t* b = wrow[f] + static_cast<int64_t>(sb) * 144;
-            if (c == 0) hd[f] = *reinterpret_cast<const uint4*>(b);
-            qv[f] = *reinterpret_cast<const uint2*>(b + 16 + 32 * c + 8 * g);
-        }
-    };
-
-    float4_t acc[MF][NF];
-#pragma unroll
-    for (int a = 0; a < MF; a++)
-#pragma unroll
-        for (int b = 0; b < NF; b++) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
-
-    load_x(0);
-    load_w(0);
-    store_x(0);
-    for (int ch = 0; ch < nchunks; ch++) {
-        const int buf = ch & 1, c = ch & 3;
-        // dequantize this chunk's B fragments from the registers loaded last step
-        Frag blo[NF], bhi[NF];
-#pragma unroll
-        for (int f = 0; f < NF; f++) {
+        for (int i = 0; i < UPT; i++) {
             half2_t ds[2], nm[2];
-            q4k_chunk_scales(hd[f], c, ds, nm);
-            q4k_bfrags(qv[f].x, qv[f].y, ds, nm, blo[f], bhi[f]);
+            q4k_chunk_scales(whd[slot][i], c, ds, nm);
+            Frag lo, hi;
+            q4k_bfrags_nat(wqs[slot][i].x, wqs[slot][i].y, ds, nm, lo, hi);
+            dst[uslot[i]] = make_uint4(lo.u[0], lo.u[1], lo.u[2], lo.u[3]);
+            dst[(NF + 1) * 64 + uslot[i]] = make_uint4(hi.u[0], hi.u[1], hi.u[2], hi.u[3]);
         }
-        if (ch + 1 < nchunks) {
-            load_x(ch + 1);
-            load_w(ch + 1);
+    };
+
+    // ---- X: piece q = tid + NT i -> row q / 8, elements 8 (q % 8) .. +8 of the step
+    const uint8_t* xb = static_cast<const uint8_t*>(X);
+    uint32_t xoff[XPT];
+    int xlds[XPT];
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+        const int q = tid + NT * i, row = q >> 3, part = q & 7;
+        int r = mt0 + row;
+        r = r < M ? r : M - 1;
+        xoff[i] = (static_cast<uint32_t>(r) * static_cast<uint32_t>(K) + 8u * static_cast<uint32_t>(part)) * XE;
+        xlds[i] = row * XS_STRIDE + 8 * part;
+    }
+    uint4 xr[2][XPT][XR];
+    auto load_x = [&](int step, int slot) {
+        step = step < nsteps ? step : nsteps - 1;
+        const uint32_t ko = static_cast<uint32_t>(step) * 64u * XE;
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            xr[slot][i][0] = *reinterpret_cast<const uint4*>(xb + (xoff[i] + ko));
+            if constexpr (XT == X_F32) xr[slot][i][1] = *reinterpret_cast<const uint4*>(xb + (xoff[i] + ko + 16u));
         }
-        __syncthreads();  // chunk ch of X is in xs[buf]; chunk ch-1 readers are done
-        const _Float16* xb = xs[buf];
+    };
+    auto store_x = [&](int slot, int buf) {
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-#pragma unroll
-            for (int a = 0; a < MF; a++) {
-                Frag af;
-                const int r = wm * 128 + 16 * a + j;
-                const uint4 v = *reinterpret_cast<const uint4*>(&xb[r * XS_STRIDE + 32 * ks + 8 * g]);
-                af.u[0] = v.x; af.u[1] = v.y; af.u[2] = v.z; af.u[3] = v.w;
-#pragma unroll
-                for (int b = 0; b < NF; b++)
-                    acc[a][b] = mfma16x16x32(af, ks == 0 ? blo[b] : bhi[b], acc[a][b]);
+        for (int i = 0; i < XPT; i++) {
+            uint4 v;
+            if constexpr (XT == X_F16) {
+                v = xr[slot][i][0];
+            } else {
+                uint32_t o[4];
+                f32x8_to_frag_nat(*reinterpret_cast<const float4*>(&xr[slot][i][0]),
+                                  *reinterpret_cast<const float4*>(&xr[slot][i][1]), o);
+                v = make_uint4(o[0], o[1], o[2], o[3]);
             }
+            *reinterpret_cast<uint4*>(&xs[buf][xlds[i]]) = v;
         }
-        if (ch + 1 < nchunks) store_x(buf ^ 1);
+    };
+    const int arow = (wm * 64 + j) * XS_STRIDE + 8 * g;  // A fragment of this lane, a = 0, ks = 0
+
+    float4_t acc[4][NW];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int f = 0; f < NW; f++) acc[a][f] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    // prologue: weights of steps 0..PD-1 and X of steps 0..2 in flight; tiles
+    // of step 0 in LDS
+#pragma unroll
+    for (int r = 0; r < PD; r++) load_w(r, r);
+    load_x(0, 0);
+    load_x(1, 1);
+    dequant_store(0, 0, 0);
+    store_x(0, 0);
+    load_x(2, 0);
+    __syncthreads();
+
+    // Loads complete in issue order (one vmcnt queue): the weights of step
+    // s + PD go out at the start of step s and X of step s + 3 at its end
+    // (scheduling fences keep that order); X(s + 1) is consumed at the end of
+    // step s, two steps after its loads went out.
+    for (int s0 = 0; s0 < nsteps; s0 += PD) {
+#pragma unroll
+        for (int r = 0; r < PD; r++) {
+            const int step = s0 + r, buf = r & 1;  // PD is even: buffer = step & 1
+            load_w(step + PD, r);  // slot r held step `step`, dequantized during the previous step
+            __builtin_amdgcn_sched_barrier(0);
+            const uint4* bsrc = &bt[buf][0][wn * NW][0];
+            const _Float16* asrc = &xs[buf][arow];
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                Frag b[NW];
+#pragma unroll
+                for (int f = 0; f < NW; f++) {
+                    const uint4 v = bsrc[(ks * (NF + 1) + f) * 64 + lane];
+                    b[f].u[0] = v.x; b[f].u[1] = v.y; b[f].u[2] = v.z; b[f].u[3] = v.w;
+                }
+#pragma unroll
+                for (int a = 0; a < 4; a++) {
+                    const uint4 v = *reinterpret_cast<const uint4*>(asrc + a * 16 * XS_STRIDE + 32 * ks);
+                    Frag af;
+                    af.u[0] = v.x; af.u[1] = v.y; af.u[2] = v.z; af.u[3] = v.w;
+#pragma unroll
+                    for (int f = 0; f < NW; f++) acc[a][f] = mfma16x16x32(af, b[f], acc[a][f]);
+                }
+            }
+            // next step's tiles into the other buffers: weights of step + 1
+            // (slot (r + 1) % PD), X of step + 1 (register slot (r + 1) % 2),
+            // whose registers then take X of step + 3.  Past the last step the
+            // (clamped) loads repeat the last step and the results are never
+            // read: no branch in the loop body.
+            dequant_store(step + 1, (r + 1) % PD, buf ^ 1);
+            store_x((r + 1) & 1, buf ^ 1);
+            __builtin_amdgcn_sched_barrier(0);
+            load_x(step + 3, (r + 1) & 1);
+            __syncthreads();
+        }
     }
 
 #pragma unroll
-    for (int a = 0; a < MF; a++) {
+    for (int a = 0; a < 4; a++) {
 #pragma unroll
-        for (int b = 0; b < NF; b++) {
-            const int64_t col = n0 + wn * 64 + 16 * b + j;
+        for (int f = 0; f < NW; f++) {
+            const int col = n0 + 16 * (wn * NW + f) + j;
             if (col >= N) continue;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int64_t t = m0 + wm * 128 + 16 * a + 4 * g + r;
-                if (t < M) Y[t * N + col] = acc[a][b][r];
+                const int t = mt0 + wm * 64 + 16 * a + 4 * g + r;
+                if (t < M) Y[static_cast<int64_t>(t) * N + col] = acc[a][f][r];
             }
         }
+    }
+}
+
+// Columns per workgroup (NF fragments of 16) balancing the grid over the
+// CUs; VB_GEMM_NF overrides (6 or 8).
+int tiled_nf(int64_t M, int64_t N) {
+    if (const char* e = std::getenv("VB_GEMM_NF")) {
+        const int v = std::atoi(e);
+        if (v == 6 || v == 8) return v;
+    }
+    constexpr int kCUs = 256;
+    const int64_t mt = (M + TB_M - 1) / TB_M;
+    int best = 8;
+    int64_t best_cost = -1;
+    for (int nf = 8; nf >= 6; nf -= 2) {
+        const int64_t tiles = mt * ((N + 16 * nf - 1) / (16 * nf));
+        const int64_t cost = ((tiles + kCUs - 1) / kCUs) * nf;
+        if (best_cost < 0 || cost < best_cost) {
+            best_cost = cost;
+            best = nf;
+        }
+    }
+    return best;
+}
+
+template <int XT>
+void launch_tiled(int nf, const uint8_t* w, const void* X, float* Y, int M, int N, int K, int64_t rb,
+                  hipStream_t st) {
+    const dim3 grid(static_cast<uint32_t>((N + 16 * nf - 1) / (16 * nf)), static_cast<uint32_t>((M + TB_M - 1) / TB_M));
+    switch (nf) {
+    case 6: gemm_q4k_tiled<XT, 6, 2><<<grid, dim3(512), 0, st>>>(w, X, Y, M, N, K, rb); break;
+    default: gemm_q4k_tiled<XT, 8, 2><<<grid, dim3(512), 0, st>>>(w, X, Y, M, N, K, rb); break;
     }
 }
 
@@ -266,15 +393,19 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
         set_error("vb_gemm: unknown variant %d", variant);
         return E_INVAL;
     }
-    const dim3 grid(static_cast<uint32_t>((N + BN - 1) / BN), static_cast<uint32_t>((M + BM - 1) / BM));
-    if (grid.y > 65535) {
-        set_error("vb_gemm: M too large");
+    const int64_t xbytes = M * K * (x_dtype == X_F16 ? 2 : 4);
+    if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX || (M + TB_M - 1) / TB_M > 65535 ||
+        N * rb >= (int64_t(1) << 32) || xbytes >= (int64_t(1) << 32)) {
+        set_error("vb_gemm: shape too large (M=%lld N=%lld K=%lld)", static_cast<long long>(M),
+                  static_cast<long long>(N), static_cast<long long>(K));
         return E_INVAL;
     }
+    const int nf = tiled_nf(M, N);
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
     if (x_dtype == X_F16)
-        gemm_q4k_tiled<X_F16><<<grid, dim3(256), 0, st>>>(static_cast<const uint8_t*>(w), X, Y, M, N, K, rb);
+        launch_tiled<X_F16>(nf, wb, X, Y, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), rb, st);
     else
-        gemm_q4k_tiled<X_F32><<<grid, dim3(256), 0, st>>>(static_cast<const uint8_t*>(w), X, Y, M, N, K, rb);
+        launch_tiled<X_F32>(nf, wb, X, Y, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), rb, st);
     return check_launch("vb_gemm");
 }
 

@@ -61,6 +61,19 @@ __device__ __forceinline__ void f32x8_to_frag(const float4& a, const float4& b, 
     o[3] = pk(b.y, b.w);
 }
 
+// 8 fp32 -> 8 fp16 (round to nearest even), natural order.
+__device__ __forceinline__ void f32x8_to_frag_nat(const float4& a, const float4& b, uint32_t* o) {
+    auto pk = [](float lo, float hi) {
+        const uint32_t l = __half_as_ushort(__float2half_rn(lo));
+        const uint32_t h = __half_as_ushort(__float2half_rn(hi));
+        return l | (h << 16);
+    };
+    o[0] = pk(a.x, a.y);
+    o[1] = pk(a.z, a.w);
+    o[2] = pk(b.x, b.y);
+    o[3] = pk(b.z, b.w);
+}
+
 // Per-row scale pair of Q4_K sub-blocks 2c and 2c+1 as fp16 half2 splats:
 // ds[i] = d * sc_(2c+i), nm[i] = -(dmin * m_(2c+i)).  hd = the 16-byte block
 // header (d, dmin, scales[12]); c is uniform across the wave.
