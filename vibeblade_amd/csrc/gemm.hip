@@ -117,7 +117,8 @@ __global__ void __launch_bounds__(256) gemm_q4k_skinny(const uint8_t* __restrict
 //  * B: the workgroup dequantizes the BN x 64 weight tile once into fp16 B
 //    fragments (natural k order); each of the 4 * BN "units" (8 qs bytes of
 //    one row -> the same lane of the step's two fragments) belongs to one
-//    thread.  Raw weight bytes run PD steps ahead in registers (HBM latency).
+//    thread, consecutive threads owning consecutive LDS lane slots.  Raw
+//    weight bytes run PD steps ahead in registers (HBM latency).
 //  * A: the 256 x 64 X tile is loaded with row-contiguous 16-byte pieces
 //    (8 lanes per 128-byte row: 4 x fewer cache-line requests than loading
 //    the fragments directly, and no duplicate loads across wave columns) two
@@ -166,21 +167,23 @@ __global__ void __launch_bounds__(256 * WN) gemm_q4k_tiled(const uint8_t* __rest
     const int n0 = tile_n * 16 * NF;
     const int nsteps = K / 64;
 
-    // ---- weights: dequant units u = tid + NT i -> row un = u / 4, part ug = u % 4
+    // ---- weights: dequant unit u = tid + NT i is LDS lane slot u: fragment
+    // u / 64, lane l = u % 64 -> weight row un = 16 (u / 64) + l % 16, qs part
+    // ug = l / 16.  Each wave stores 1 KB contiguous (bank-conflict free).
     uint32_t urow[UPT];  // byte offset of the unit's weight row in W
     uint32_t uq[UPT];    // byte offset of the unit's 8 qs bytes within a chunk's 32
-    int uslot[UPT];      // LDS lane slot: fragment un / 16, lane 16 ug + un % 16
+    int uslot[UPT];      // LDS lane slot
 #pragma unroll
     for (int i = 0; i < UPT; i++) {
         int u = tid + NT * i;
         const bool live = u < NU;
         u = live ? u : NU - 1;
-        const int un = u >> 2, ug = u & 3;
+        const int l = u & 63, un = 16 * (u >> 6) + (l & 15), ug = l >> 4;
         int n = n0 + un;
         n = n < N ? n : N - 1;
         urow[i] = static_cast<uint32_t>(n) * static_cast<uint32_t>(rb);
         uq[i] = 16u + 8u * static_cast<uint32_t>(ug);
-        uslot[i] = live ? (un >> 4) * 64 + 16 * ug + (un & 15) : NF * 64 + lane;
+        uslot[i] = live ? u : NF * 64 + lane;
     }
     uint4 whd[PD][UPT];
     uint2 wqs[PD][UPT];
@@ -275,23 +278,29 @@ __global__ void __launch_bounds__(256 * WN) gemm_q4k_tiled(const uint8_t* __rest
             __builtin_amdgcn_sched_barrier(0);
             const uint4* bsrc = &bt[buf][0][wn * NW][0];
             const _Float16* asrc = &xs[buf][arow];
+            // every fragment of the step is requested before the first MFMA:
+            // one LDS latency per step instead of one per MFMA group
+            Frag b[2][NW], af[2][4];
 #pragma unroll
             for (int ks = 0; ks < 2; ks++) {
-                Frag b[NW];
 #pragma unroll
                 for (int f = 0; f < NW; f++) {
                     const uint4 v = bsrc[(ks * (NF + 1) + f) * 64 + lane];
-                    b[f].u[0] = v.x; b[f].u[1] = v.y; b[f].u[2] = v.z; b[f].u[3] = v.w;
+                    b[ks][f].u[0] = v.x; b[ks][f].u[1] = v.y; b[ks][f].u[2] = v.z; b[ks][f].u[3] = v.w;
                 }
 #pragma unroll
                 for (int a = 0; a < 4; a++) {
                     const uint4 v = *reinterpret_cast<const uint4*>(asrc + a * 16 * XS_STRIDE + 32 * ks);
-                    Frag af;
-                    af.u[0] = v.x; af.u[1] = v.y; af.u[2] = v.z; af.u[3] = v.w;
-#pragma unroll
-                    for (int f = 0; f < NW; f++) acc[a][f] = mfma16x16x32(af, b[f], acc[a][f]);
+                    af[ks][a].u[0] = v.x; af[ks][a].u[1] = v.y; af[ks][a].u[2] = v.z; af[ks][a].u[3] = v.w;
                 }
             }
+            __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+                for (int a = 0; a < 4; a++)
+#pragma unroll
+                    for (int f = 0; f < NW; f++) acc[a][f] = mfma16x16x32(af[ks][a], b[ks][f], acc[a][f]);
             // next step's tiles into the other buffers: weights of step + 1
             // (slot (r + 1) % PD), X of step + 1 (register slot (r + 1) % 2),
             // whose registers then take X of step + 3.  Past the last step the
