@@ -8,18 +8,12 @@
 // in registers, in the B-operand layout of v_mfma_f32_16x16x32_f16
 // (mfma_q4k.hpp), accumulating in fp32.
 //
-// Two kernels:
-//  * skinny (M <= 16: speculative verify, MoE expert groups): one 16-row
-//    M-fragment; a workgroup owns 16 output columns and splits K over its 4
-//    waves (partials meet in LDS).  HBM-bound: the grid has N/16 workgroups.
-//  * tiled (M > 16: chunked prefill): 256 x 128 output tile per workgroup,
-//    2 x 2 waves of 128 x 64.  X is staged through LDS (double-buffered
-//    64-element k-chunks, sigma-permuted, rows padded to 144 B so the
-//    fragment reads are bank-conflict free); each wave dequantizes its 64
-//    weight rows straight into B fragments.  One barrier per k-chunk.
+// M <= 16 goes to the skinny kernel (gemm_skinny.hip); M > 16 (chunked
+// prefill) runs the tiled kernel below.
 #include <cstdlib>
 
 #include "mfma_q4k.hpp"
+#include "vb_internal.hpp"
 #include "../../include/vbhip.h"
 
 namespace vb {
@@ -27,85 +21,6 @@ namespace {
 
 constexpr int X_F32 = 0;
 constexpr int X_F16 = 1;
-
-// A fragment (rows t of X, k0 + 8g .. +8) in sigma order; zeros when !valid.
-template <int XT>
-__device__ __forceinline__ void load_afrag(const void* X, int64_t ldx, int64_t t, int64_t k, bool valid,
-                                           Frag& a) {
-    if (!valid) {
-        a.u[0] = a.u[1] = a.u[2] = a.u[3] = 0u;
-        return;
-    }
-    if constexpr (XT == X_F16) {
-        const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const __half*>(X) + t * ldx + k);
-        sigma_permute(v.x, v.y, v.z, v.w, a.u);
-    } else {
-        const float* p = static_cast<const float*>(X) + t * ldx + k;
-        f32x8_to_frag(*reinterpret_cast<const float4*>(p), *reinterpret_cast<const float4*>(p + 4), a.u);
-    }
-}
-
-// ---- skinny: M <= 16 --------------------------------------------------------
-
-template <int XT>
-__global__ void __launch_bounds__(256) gemm_q4k_skinny(const uint8_t* __restrict__ w,
-                                                       const void* __restrict__ X, float* __restrict__ Y,
-                                                       int M, int64_t N, int64_t K, int64_t rb) {
-    __shared__ float4_t red[4][64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int j = lane & 15, g = lane >> 4;
-    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
-    int64_t n = n0 + j;
-    n = n < N ? n : N - 1;
-    const uint8_t* row = w + n * rb;
-    const int nsb = static_cast<int>(K / 256);
-    const int sb0 = (wave * nsb) / 4, sb1 = ((wave + 1) * nsb) / 4;
-    const bool tvalid = j < M;  // A-fragment row of this lane
-    float4_t acc = {0.f, 0.f, 0.f, 0.f};
-
-    uint4 hd;
-    uint2 qs[4];
-    auto load_w = [&](int sb) {
-        const uint8_t* b = row + static_cast<int64_t>(sb) * 144;
-        hd = *reinterpret_cast<const uint4*>(b);
-#pragma unroll
-        for (int c = 0; c < 4; c++) qs[c] = *reinterpret_cast<const uint2*>(b + 16 + 32 * c + 8 * g);
-    };
-    if (sb0 < sb1) load_w(sb0);
-    for (int sb = sb0; sb < sb1; sb++) {
-        const uint4 hcur = hd;
-        uint2 qcur[4];
-#pragma unroll
-        for (int c = 0; c < 4; c++) qcur[c] = qs[c];
-        if (sb + 1 < sb1) load_w(sb + 1);
-        Frag a[8];
-#pragma unroll
-        for (int sub = 0; sub < 8; sub++)
-            load_afrag<XT>(X, K, j, static_cast<int64_t>(sb) * 256 + 32 * sub + 8 * g, tvalid, a[sub]);
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            half2_t ds[2], nm[2];
-            q4k_chunk_scales(hcur, c, ds, nm);
-            Frag lo, hi;
-            q4k_bfrags(qcur[c].x, qcur[c].y, ds, nm, lo, hi);
-            acc = mfma16x16x32(a[2 * c], lo, acc);
-            acc = mfma16x16x32(a[2 * c + 1], hi, acc);
-        }
-    }
-    red[wave][lane] = acc;
-    __syncthreads();
-    if (wave == 0) {
-        const float4_t s = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
-        const int64_t col = n0 + j;
-        if (col < N) {
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int t = 4 * g + r;
-                if (t < M) Y[static_cast<int64_t>(t) * N + col] = s[r];
-            }
-        }
-    }
-}
 
 // ---- tiled: M > 16 ------------------------------------------------------------
 //
@@ -389,14 +304,7 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
             set_error("vb_gemm: variant 1 (skinny) takes M <= 16, got %lld", static_cast<long long>(M));
             return E_INVAL;
         }
-        const dim3 grid(static_cast<uint32_t>((N + 15) / 16));
-        if (x_dtype == X_F16)
-            gemm_q4k_skinny<X_F16><<<grid, dim3(256), 0, st>>>(static_cast<const uint8_t*>(w), X, Y,
-                                                               static_cast<int>(M), N, K, rb);
-        else
-            gemm_q4k_skinny<X_F32><<<grid, dim3(256), 0, st>>>(static_cast<const uint8_t*>(w), X, Y,
-                                                               static_cast<int>(M), N, K, rb);
-        return check_launch("vb_gemm");
+        return gemm_q4k_skinny(w, X, x_dtype, Y, M, N, K, st);
     }
     if (variant != 0 && variant != 2) {
         set_error("vb_gemm: unknown variant %d", variant);

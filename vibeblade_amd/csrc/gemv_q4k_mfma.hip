@@ -31,6 +31,7 @@
 // ring of D register buffers.  Partial row sums meet in LDS and the
 // workgroup adds the k-slices in a fixed order.
 #include <cstdlib>
+#include <type_traits>
 
 #include "vb_common.hpp"
 #include "vb_internal.hpp"
@@ -210,8 +211,25 @@ __device__ __forceinline__ float sb_dot(const SBUnit& v, const uint8_t* xa_bytes
 // 512 threads); larger k loops.
 constexpr int XT = 2;
 
+// Weight staging.  The MFMA layout makes each lane group of a wave read 16
+// different rows; loaded that way straight from HBM (16 rows per load
+// instruction) the reads run at about two thirds of the row-contiguous
+// pattern's rate.  So a wave loads its 16 rows x 4 super-blocks per step as
+// row-contiguous 16-byte pieces (576 pieces, 9 per lane), stores them into a
+// private LDS area (rows 592 bytes apart: the 16-lane column reads below are
+// bank-conflict free) and reads the MFMA layout back from there.
+constexpr int SB_STEP = 4;                          // super-blocks per step
+constexpr int STAGE_ROW = SB_STEP * 144 + 16;       // bytes per staged row
+constexpr int STAGE_BYTES = 16 * STAGE_ROW;         // per wave
+constexpr int PIECES_PER_ROW = SB_STEP * 144 / 16;  // 36
+constexpr int PPL = 16 * PIECES_PER_ROW / 64;       // pieces per lane: 9
+
+__host__ __device__ constexpr size_t lds_stage_offset(int nsb, int ks, int rows_wg) {
+    return ((static_cast<size_t>(lds_red_offset(nsb)) * 16 + static_cast<size_t>(ks) * rows_wg * 4) + 15) & ~size_t(15);
+}
+
 template <int D>
-constexpr int mfma_max_threads() { return D <= 4 ? 1024 : 512; }
+constexpr int mfma_max_threads() { return D <= 2 ? 512 : 256; }
 
 template <int MODE, int D>
 __global__ void __launch_bounds__(mfma_max_threads<D>()) gemv_q4k_mfma_kernel(
@@ -236,24 +254,46 @@ __global__ void __launch_bounds__(mfma_max_threads<D>()) gemv_q4k_mfma_kernel(
     const int rows_wg = rgs * 16;
     const int wg_row0 = static_cast<int>(blockIdx.x) * rows_wg;
     const int sb0 = kw * nsbw;
-    int nsteps = nsb - sb0;  // super-blocks of this k-slice (the host avoids empty slices)
-    nsteps = nsteps < nsbw ? nsteps : nsbw;
-    nsteps = nsteps > 0 ? nsteps : 1;
+    int nsbk = nsb - sb0;  // super-blocks of this k-slice (the host avoids empty slices)
+    nsbk = nsbk < nsbw ? nsbk : nsbw;
+    nsbk = nsbk > 0 ? nsbk : 1;
+    const int nsteps = (nsbk + SB_STEP - 1) / SB_STEP;
     const int nsteps_p = ((nsteps + D - 1) / D) * D;
+    uint8_t* stage = reinterpret_cast<uint8_t*>(lds) + lds_stage_offset(nsb, ks, rows_wg) +
+                     static_cast<size_t>(wave) * STAGE_BYTES;
 
-    int row = wg_row0 + rgi * 16 + j;
-    row = row < n ? row : n - 1;
-    const uint8_t* rowp = row_ptr<MODE>(w, w2, gidx, nsrc, row, rb) + 32 * g;
-
-    // Issues past the last step reload it (in-bounds, discarded).
-    int isb = sb0;
-    const int sb_last = sb0 + nsteps - 1;
-    auto issue = [&](SBUnit& v) {
-        const uint8_t* p = rowp + static_cast<int64_t>(isb) * 144;
-        v.hd = *reinterpret_cast<const uint4*>(p - 32 * g);
-        v.q0 = *reinterpret_cast<const uint4*>(p + 16);
-        v.q1 = *reinterpret_cast<const uint4*>(p + 32);
-        isb = isb < sb_last ? isb + 1 : sb_last;
+    // pieces of this lane: p = 64 i + lane -> staged row p / 36, piece p % 36
+    // (super-block (p % 36) / 9 of the step, 16-byte word (p % 36) % 9)
+    const uint8_t* prow[PPL];
+    int psb[PPL], pword[PPL], poff[PPL];
+#pragma unroll
+    for (int i = 0; i < PPL; i++) {
+        const int p = 64 * i + lane, r = p / PIECES_PER_ROW, q = p - r * PIECES_PER_ROW;
+        int row = wg_row0 + rgi * 16 + r;
+        row = row < n ? row : n - 1;
+        prow[i] = row_ptr<MODE>(w, w2, gidx, nsrc, row, rb);
+        psb[i] = q / 9;
+        pword[i] = 16 * (q - 9 * (q / 9));
+        poff[i] = r * STAGE_ROW + 144 * psb[i] + pword[i];
+    }
+    // native vector type (HIP's uint4 struct copies become memcpys that keep
+    // the array in scratch)
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 pv[D][PPL];
+    int it = 0;
+    // slots are compile-time constants (std::integral_constant) so pv stays
+    // in registers
+    auto issue = [&](auto slot_c) __attribute__((always_inline)) {
+        constexpr int slot = decltype(slot_c)::value;
+        const int t = it < nsteps ? it : nsteps - 1;
+        const int last = sb0 + nsbk - 1;
+#pragma unroll
+        for (int i = 0; i < PPL; i++) {
+            int sb = sb0 + SB_STEP * t + psb[i];
+            sb = sb < last ? sb : last;
+            pv[slot][i] = *reinterpret_cast<const u32x4*>(prow[i] + static_cast<int64_t>(sb) * 144 + pword[i]);
+        }
+        ++it;
     };
 
     // x first, then the first D steps of weights, then the encode.
@@ -265,9 +305,12 @@ __global__ void __launch_bounds__(mfma_max_threads<D>()) gemv_q4k_mfma_kernel(
         for (int i = 0; i < XT; i++) load_task(x, ntasks, threadIdx.x + i * blockDim.x, xv[i]);
     }
     __builtin_amdgcn_sched_barrier(0);
-    SBUnit v[D];
-#pragma unroll
-    for (int i = 0; i < D; i++) issue(v[i]);
+    issue(std::integral_constant<int, 0>{});
+    issue(std::integral_constant<int, 1>{});
+    if constexpr (D == 4) {
+        issue(std::integral_constant<int, 2>{});
+        issue(std::integral_constant<int, 3>{});
+    }
     __builtin_amdgcn_sched_barrier(0);
     // ntasks and blockDim are multiples of 32: every quad of tasks is complete.
     if (x_in_regs) {
@@ -293,28 +336,52 @@ __global__ void __launch_bounds__(mfma_max_threads<D>()) gemv_q4k_mfma_kernel(
     const uint32_t a_sbmask = a_live ? 0xFFFFFFFFu : 0u;
     const uint8_t* xa_bytes = reinterpret_cast<const uint8_t*>(xa);
     const ScaleSel q = scale_sel(g);
+    const uint8_t* my = stage + j * STAGE_ROW;  // this lane's staged row
     float out = 0.f;
 
-    int csb = sb0;
-    auto compute = [&](const SBUnit& vv, int step) {
-        if (step >= nsteps) return;  // padding step (uniform)
-        const uint32_t a_off = a_lane + ((static_cast<uint32_t>(csb) * 1024u) & a_sbmask);
-        const float* f = xsf + (csb * 4 + g) * 8;
-        const float4 f0 = *reinterpret_cast<const float4*>(f);
-        out += sb_dot(vv, xa_bytes, a_off, f0, f[4], q);
-        ++csb;
+    int ct = 0;
+    auto compute = [&](auto slot_c) __attribute__((always_inline)) {
+        constexpr int slot = decltype(slot_c)::value;
+        if (ct >= nsteps) return;  // padding step (uniform)
+#pragma unroll
+        for (int i = 0; i < PPL; i++) *reinterpret_cast<u32x4*>(stage + poff[i]) = pv[slot][i];
+        const int nsb_here = nsbk - SB_STEP * ct < SB_STEP ? nsbk - SB_STEP * ct : SB_STEP;
+#pragma unroll
+        for (int t = 0; t < SB_STEP; t++) {
+            if (t < nsb_here) {  // uniform
+                const int sb = sb0 + SB_STEP * ct + t;
+                SBUnit v;
+                v.hd = *reinterpret_cast<const uint4*>(my + 144 * t);
+                v.q0 = *reinterpret_cast<const uint4*>(my + 144 * t + 16 + 32 * g);
+                v.q1 = *reinterpret_cast<const uint4*>(my + 144 * t + 32 + 32 * g);
+                const uint32_t a_off = a_lane + ((static_cast<uint32_t>(sb) * 1024u) & a_sbmask);
+                const float* f = xsf + (sb * 4 + g) * 8;
+                const float4 f0 = *reinterpret_cast<const float4*>(f);
+                out += sb_dot(v, xa_bytes, a_off, f0, f[4], q);
+            }
+        }
+        ++ct;
     };
 
-    int s = 0;
-    for (; s + D < nsteps_p; s += D) {
-#pragma unroll
-        for (int i = 0; i < D; i++) {
-            compute(v[i], s + i);
-            issue(v[i]);
+    // ring slots are literal constants (register arrays, no scratch)
+    for (int s = 0; s + D < nsteps_p; s += D) {
+        compute(std::integral_constant<int, 0>{});
+        issue(std::integral_constant<int, 0>{});
+        compute(std::integral_constant<int, 1>{});
+        issue(std::integral_constant<int, 1>{});
+        if constexpr (D == 4) {
+            compute(std::integral_constant<int, 2>{});
+            issue(std::integral_constant<int, 2>{});
+            compute(std::integral_constant<int, 3>{});
+            issue(std::integral_constant<int, 3>{});
         }
     }
-#pragma unroll
-    for (int i = 0; i < D; i++) compute(v[i], s + i);
+    compute(std::integral_constant<int, 0>{});
+    compute(std::integral_constant<int, 1>{});
+    if constexpr (D == 4) {
+        compute(std::integral_constant<int, 2>{});
+        compute(std::integral_constant<int, 3>{});
+    }
 
     // add the 4 chunk lanes of each row, then the k-slices (fixed order)
     out += __shfl_xor(out, 16, 64);
@@ -336,55 +403,61 @@ struct MfmaShape {
 
 constexpr int kNumCUs = 256;
 
-// Ring depth: all of a wave's steps in flight up to 8 (12 VGPRs each).
-int mfma_depth(int nsteps) { return nsteps <= 2 ? 2 : (nsteps <= 4 ? 4 : 8); }
-
-size_t mfma_lds(int nsb, int ks, int64_t rows_wg) {
-    return static_cast<size_t>(lds_red_offset(nsb)) * 16 + static_cast<size_t>(ks * rows_wg) * 4;
+size_t mfma_lds(int nsb, int ks, int wpg) {
+    const int rows_wg = (wpg / ks) * 16;
+    return lds_stage_offset(nsb, ks, rows_wg) + static_cast<size_t>(wpg) * STAGE_BYTES;
 }
 
-// Launch geometry: k-slices of nsbw super-blocks, ks waves per 16-row group,
-// wpg / ks row groups per workgroup.  Candidates are scored by the VALU work
-// of the busiest CU, weighted towards 12-16 resident waves per CU (latency
-// hiding); VB_GEMV_MFMA_CFG="wpg,ks" overrides (tuning sweeps).
+// Launch geometry: k-slices of nsbw super-blocks (a multiple of the 4 of a
+// step), ks waves per 16-row group, wpg / ks row groups per workgroup.  The
+// staging areas make LDS the occupancy limit.  Preferred: every workgroup
+// resident at once, then more waves per CU, then fewer steps per wave.
+// VB_GEMV_MFMA_CFG="wpg,ks" overrides (tuning sweeps).
 MfmaShape mfma_shape(int64_t n, int nsb) {
     MfmaShape best{};
-    double best_score = -1.0;
+    int64_t best_key[3] = {0, 0, 0};
+    bool have = false;
     const int64_t nrg = (n + 15) / 16;
-    for (int ks = 1; ks <= 16 && ks <= nsb; ks++) {
-        const int nsbw = (nsb + ks - 1) / ks;
-        if ((ks - 1) * nsbw >= nsb) continue;  // an empty k-slice
-        const int depth = mfma_depth(nsbw);
-        for (int wpg = 16; wpg >= 2; wpg--) {
+    auto consider = [&](int ks, int wpg) -> MfmaShape {
+        const int nsbw = ((nsb + ks - 1) / ks + SB_STEP - 1) / SB_STEP * SB_STEP;
+        const int steps = nsbw / SB_STEP;
+        const int depth = steps <= 2 ? 2 : 4;
+        const int64_t rows_wg = static_cast<int64_t>(wpg / ks) * 16;
+        const size_t lds = mfma_lds(nsb, ks, wpg);
+        return MfmaShape{nsb, nsbw, ks, wpg, depth, (nrg * 16 + rows_wg - 1) / rows_wg, lds};
+    };
+    for (int ks = 1; ks <= 8 && ks <= nsb; ks++) {
+        for (int wpg = 8; wpg >= ks; wpg--) {
             if (wpg % ks) continue;
-            if (depth == 8 && wpg > 8) continue;  // 8-deep rings: <= 256 VGPRs per lane
-            const int64_t rows_wg = static_cast<int64_t>(wpg / ks) * 16;
-            const int64_t grid = (nrg * 16 + rows_wg - 1) / rows_wg;
-            const size_t lds = mfma_lds(nsb, ks, rows_wg);
-            if (lds > 160 * 1024) continue;
-            const int64_t per_cu = (grid + kNumCUs - 1) / kNumCUs;
-            // VALU work on the busiest CU in units of one wave step (16 rows
-            // x 1 super-block): the steps of every wave plus the activation
-            // encode of each workgroup (about 0.4 step per super-block of k)
-            const double cost = static_cast<double>(per_cu) * (static_cast<double>(wpg) * nsbw + 0.4 * nsb);
-            const int resident = (depth == 8 ? 8 : 16) / wpg;
-            const int64_t waves = (per_cu < resident ? per_cu : resident) * wpg;
-            const double score = cost * (waves >= 12 ? 1.0 : (waves >= 8 ? 1.08 : 1.25));
-            if (best_score < 0 || score < best_score) {
-                best_score = score;
-                best = MfmaShape{nsb, nsbw, ks, wpg, depth, grid, lds};
+            const MfmaShape c = consider(ks, wpg);
+            if ((ks - 1) * c.nsbw >= nsb) continue;  // an empty k-slice
+            if (c.lds > 160 * 1024) continue;
+            if (64 * wpg > (c.depth <= 2 ? 512 : 256)) continue;
+            const int64_t per_lds = static_cast<int64_t>(160 * 1024 / c.lds);
+            const int64_t per_waves = 8 / wpg;
+            const int64_t res = per_lds < per_waves ? per_lds : per_waves;
+            if (res < 1) continue;
+            const int64_t rounds = (c.grid + kNumCUs * res - 1) / (kNumCUs * res);
+            const int64_t wgs_cu = (c.grid + kNumCUs - 1) / kNumCUs;
+            const int64_t waves_cu = (wgs_cu < res ? wgs_cu : res) * wpg;
+            const int64_t key[3] = {rounds, -waves_cu, static_cast<int64_t>(c.nsbw)};
+            bool better = !have;
+            for (int t = 0; t < 3 && !better; t++) {
+                if (key[t] < best_key[t]) better = true;
+                else if (key[t] > best_key[t]) break;
+            }
+            if (better) {
+                have = true;
+                best = c;
+                for (int t = 0; t < 3; t++) best_key[t] = key[t];
             }
         }
     }
     if (const char* cfg = std::getenv("VB_GEMV_MFMA_CFG")) {
         int a = 0, b = 0;
-        if (std::sscanf(cfg, "%d,%d", &a, &b) == 2 && b >= 1 && b <= nsb && a >= b && a % b == 0 && a <= 16) {
-            const int nsbw = (nsb + b - 1) / b;
-            const int depth = mfma_depth(nsbw);
-            const int64_t rows_wg = static_cast<int64_t>(a / b) * 16;
-            const size_t lds = mfma_lds(nsb, b, rows_wg);
-            if ((depth < 8 || a <= 8) && (b - 1) * nsbw < nsb && lds <= 160 * 1024)
-                best = MfmaShape{nsb, nsbw, b, a, depth, (nrg * 16 + rows_wg - 1) / rows_wg, lds};
+        if (std::sscanf(cfg, "%d,%d", &a, &b) == 2 && b >= 1 && b <= nsb && a >= b && a % b == 0 && a <= 8) {
+            const MfmaShape c = consider(b, a);
+            if ((b - 1) * c.nsbw < nsb && c.lds <= 160 * 1024 && 64 * a <= (c.depth <= 2 ? 512 : 256)) best = c;
         }
     }
     return best;
@@ -410,7 +483,7 @@ int gemv_q4k_mfma(const void* w, const RowSrc& src, const float* x, float* y, in
         return E_UNSUPPORTED;
     }
     const MfmaShape s = mfma_shape(n, nsb);
-    if (s.grid <= 0) {
+    if (s.grid <= 0 || s.wpg == 0) {
         set_error("vb_gemv: no launch shape for n=%lld k=%lld", static_cast<long long>(n), static_cast<long long>(k));
         return E_UNSUPPORTED;
     }
@@ -424,8 +497,7 @@ int gemv_q4k_mfma(const void* w, const RowSrc& src, const float* x, float* y, in
            : launch<ROWS_PLAIN, D>(s, wb, w2, src.gidx, nsrc, x, y, ni, rb, src.zbuf, src.zn, st))
     switch (s.depth) {
     case 2: VB_LAUNCH(2); break;
-    case 4: VB_LAUNCH(4); break;
-    default: VB_LAUNCH(8); break;
+    default: VB_LAUNCH(4); break;
     }
 #undef VB_LAUNCH
     return check_launch("vb_gemv");

@@ -24,6 +24,9 @@ int gemv_dispatch_src(const void* w, const RowSrc& src, const float* x, float* y
 // already validated by gemv_dispatch_src.
 int gemv_q4k_mfma(const void* w, const RowSrc& src, const float* x, float* y, int64_t n, int64_t k,
                   hipStream_t st);
+// M <= 16 Q4_K GEMM (gemm_skinny.hip); type, M, alignment already validated.
+int gemm_q4k_skinny(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, int64_t N, int64_t K,
+                    hipStream_t st);
 int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, int64_t N, int64_t K,
                   int32_t type, int32_t variant, hipStream_t st);
 
