@@ -10,18 +10,19 @@
 // (vibeblade/moe_executor.py:210-212); this routes every token.
 //
 // Three launches, no host round trip:
-//   1. gate/up: grid (i/16, E).  Every workgroup recomputes the routing (T x E
-//      logits, cheap), lists the (token, slot) pairs that chose its expert in
-//      token order and, if any, computes the 16 gate and up rows of its tile
-//      for those tokens on v_mfma_f32_16x16x32_f16 (X rows gathered, Q4_K
-//      weights dequantized to fp16 in registers), 4 waves splitting k; the
-//      epilogue writes silu(g) * u for every (slot, row) into hbuf.
-//   2. down: grid (h/16, E), same routing, A rows = hbuf slots of the expert,
+//   1. gate/up: every workgroup recomputes the routing (T x E logits, cheap)
+//      and lists the (token, slot) pairs that chose its expert in token order.
+//      Q4_K experts: grid (i/64, E), skinny tiles (skinny_core.hpp) of 64
+//      gate and 64 up rows per 16 slots, silu(g) * u written as fp16 into
+//      hbuf.  F32 experts: grid (i/16, E), 16-row tiles on
+//      v_mfma_f32_16x16x32_f16, hbuf in fp32.
+//   2. down: same routing, activations = hbuf rows of the expert's slots,
 //      writes the expert output of every slot into obuf.
 //   3. combine: y_t = sum_k w_tk * obuf[t*topk + k] in slot order (fixed
 //      order, deterministic); also writes the routing (indices, weights).
 // Each expert's weights are streamed once per 16 routed slots.
 #include "mfma_q4k.hpp"
+#include "skinny_core.hpp"
 #include "vb_internal.hpp"
 #include "../../include/vbhip.h"
 
@@ -88,8 +89,8 @@ __device__ int expert_slots(const float* __restrict__ logits, int t_n, int e_n, 
     return count;
 }
 
-// One 16-row tile of Q4_K weights times the gathered fp32 activation rows
-// arow[0..nrow) (nrow <= 16), k split over the 4 waves.  NMAT = 1 or 2
+// One 16-row tile of F32 expert weights times the gathered fp32 activation
+// rows arow[0..nrow) (nrow <= 16), k split over the 4 waves.  NMAT = 1 or 2
 // matrices over the same activations.  Returns the per-lane D fragments of
 // the full-k sums in red (LDS, [4 waves][64 lanes] per matrix).
 template <int NMAT, int WT>
@@ -114,29 +115,7 @@ __device__ void tile_mfma(const uint8_t* const* wrow, const float* const* arow, 
             f32x8_to_frag(avalid ? lo4 : make_float4(0.f, 0.f, 0.f, 0.f),
                           avalid ? hi4 : make_float4(0.f, 0.f, 0.f, 0.f), a[sub].u);
         }
-        if constexpr (WT == TYPE_Q4_K) {
-            uint4 hd[NMAT];
-            uint2 qs[NMAT][4];
-#pragma unroll
-            for (int m = 0; m < NMAT; m++) {
-                const uint8_t* b = wrow[m] + static_cast<int64_t>(sb) * 144;
-                hd[m] = *reinterpret_cast<const uint4*>(b);
-#pragma unroll
-                for (int c = 0; c < 4; c++) qs[m][c] = *reinterpret_cast<const uint2*>(b + 16 + 32 * c + 8 * g);
-            }
-#pragma unroll
-            for (int m = 0; m < NMAT; m++) {
-#pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    half2_t ds[2], nm[2];
-                    q4k_chunk_scales(hd[m], c, ds, nm);
-                    Frag lo, hi;
-                    q4k_bfrags(qs[m][c].x, qs[m][c].y, ds, nm, lo, hi);
-                    acc[m] = mfma16x16x32(a[2 * c], lo, acc[m]);
-                    acc[m] = mfma16x16x32(a[2 * c + 1], hi, acc[m]);
-                }
-            }
-        } else {  // F32 weights: row n, k = 256 sb + 32 sub + 8 g .. +8, rounded to fp16
+        {  // F32 weights: row n, k = 256 sb + 32 sub + 8 g .. +8, rounded to fp16
 #pragma unroll
             for (int m = 0; m < NMAT; m++) {
                 const float* wp = reinterpret_cast<const float*>(wrow[m]) + static_cast<int64_t>(sb) * 256 + 8 * g;
@@ -232,6 +211,155 @@ __global__ void __launch_bounds__(256) moe_down_kernel(ExpertPtrs wd, const floa
     }
 }
 
+// ---- Q4_K experts: skinny tiles (skinny_core.hpp) --------------------------
+//
+// prep: block 0 routes every token once and writes the routing (ridx, rw)
+// and the slots of each expert in slot order (elist[eoff[e] .. eoff[e+1]));
+// the other blocks round x to fp16 (xh) -- the MFMA path rounds its
+// activations to fp16 anyway, and fp16 halves the activation traffic of the
+// expert kernels.
+constexpr int PREP_THREADS = 1024;
+
+__global__ void __launch_bounds__(PREP_THREADS) moe_prep_kernel(
+        const float* __restrict__ x, const float* __restrict__ logits, int t_n, int e_n, int topk, int64_t nx,
+        _Float16* __restrict__ xh, int32_t* __restrict__ ridx, float* __restrict__ rw, int32_t* __restrict__ eoff,
+        int32_t* __restrict__ elist) {
+    if (blockIdx.x > 0) {
+        const int64_t i8 = (static_cast<int64_t>(blockIdx.x - 1) * PREP_THREADS + threadIdx.x) * 8;
+        if (i8 < nx) {  // nx = t_n * h, a multiple of 256
+            const float4 a = *reinterpret_cast<const float4*>(x + i8);
+            const float4 b = *reinterpret_cast<const float4*>(x + i8 + 4);
+            uint32_t o[4];
+            f32x8_to_frag_nat(a, b, o);
+            *reinterpret_cast<uint4*>(xh + i8) = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+        return;
+    }
+    __shared__ int sexp[MOE_MAX_SLOTS];
+    __shared__ int scnt[MOE_MAX_EXPERTS + 1];
+    const int nslots = t_n * topk;
+    for (int t = threadIdx.x; t < t_n; t += PREP_THREADS) {
+        int idx[MOE_MAX_TOPK];
+        float w[MOE_MAX_TOPK];
+        route_token(logits + static_cast<int64_t>(t) * e_n, e_n, topk, idx, w);
+        for (int k = 0; k < topk; k++) {
+            ridx[t * topk + k] = idx[k];
+            rw[t * topk + k] = w[k];
+            sexp[t * topk + k] = idx[k];
+        }
+    }
+    __syncthreads();
+    // counts per expert, then exclusive offsets (slots with no expert -- NaN
+    // logits -- are in no list)
+    if (threadIdx.x < e_n) {
+        int c = 0;
+        for (int q = 0; q < nslots; q++) c += sexp[q] == static_cast<int>(threadIdx.x);
+        scnt[threadIdx.x + 1] = c;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        scnt[0] = 0;
+        for (int e = 0; e < e_n; e++) scnt[e + 1] += scnt[e];
+        for (int e = 0; e <= e_n; e++) eoff[e] = scnt[e];
+    }
+    __syncthreads();
+    for (int q = threadIdx.x; q < nslots; q += PREP_THREADS) {
+        const int e = sexp[q];
+        if (e < 0 || e >= e_n) continue;
+        int pos = 0;
+        for (int r = 0; r < q; r++) pos += sexp[r] == e;
+        elist[scnt[e] + pos] = q;
+    }
+}
+
+// gate/up: grid (ceil(i / 64), E), 8 waves.  A workgroup streams 64 rows of
+// the expert's gate and up matrices once per group of 16 routed slots (the
+// two matrices alternate in the tile's unit ring and share the activation
+// fragments) and writes silu(g) * u for every (slot, row) into hbuf as fp16
+// -- the down kernel rounds its activations to fp16 anyway.
+__global__ void __launch_bounds__(64 * skinny::WAVES) moe_gate_up_q4k(
+        ExpertPtrs wg, ExpertPtrs wu, const _Float16* __restrict__ xh, const int32_t* __restrict__ eoff,
+        const int32_t* __restrict__ elist, int topk, int h, int i_dim, int rb, uint32_t wbytes, uint32_t xbytes,
+        _Float16* __restrict__ hbuf) {
+    extern __shared__ skinny::u32x4 moe_lds[];
+    const int e = blockIdx.y;
+    const int base = eoff[e], cnt = eoff[e + 1] - base;
+    if (cnt <= 0) return;
+    const int32_t* slots = elist + base;
+    const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+    skinny::TileArgs<2> ta;
+    ta.w[0] = skinny::make_rsrc(wg.p[e], wbytes);
+    ta.w[1] = skinny::make_rsrc(wu.p[e], wbytes);
+    ta.x = skinny::make_rsrc(xh, xbytes);
+    ta.row0 = static_cast<int>(blockIdx.x) * skinny::ROWS;
+    ta.rows = i_dim - ta.row0 < skinny::ROWS ? i_dim - ta.row0 : skinny::ROWS;
+    ta.nrows = i_dim;
+    ta.rb = rb;
+    ta.nsb = h / 256;
+    for (int m0 = 0; m0 < cnt; m0 += 16) {
+        const int nrow = cnt - m0 < 16 ? cnt - m0 : 16;
+        ta.xoff = j < nrow ? (static_cast<uint32_t>(slots[m0 + j] / topk) * static_cast<uint32_t>(h) + 64u * g) * 2u
+                           : skinny::X_NONE;
+        float4_t s[2];
+        skinny::tile<skinny::X_F16, 2>(ta, reinterpret_cast<uint8_t*>(moe_lds), s);
+        if (threadIdx.x < 256) {
+            const int q = threadIdx.x >> 6, l = threadIdx.x & 63;
+            const int r = 16 * q + (l & 15), n = ta.row0 + r;
+            if (r < ta.rows) {
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int t = 4 * (l >> 4) + v;
+                    if (t < nrow) {
+                        const float gv = s[0][v], uv = s[1][v];
+                        hbuf[static_cast<int64_t>(slots[m0 + t]) * i_dim + n] =
+                                static_cast<_Float16>(gv / (1.0f + __expf(-gv)) * uv);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// down: grid (ceil(h / 64), E); activations = the fp16 hbuf rows of the
+// expert's slots; writes the expert output of every slot into obuf.
+__global__ void __launch_bounds__(64 * skinny::WAVES) moe_down_q4k(
+        ExpertPtrs wd, const _Float16* __restrict__ hbuf, const int32_t* __restrict__ eoff,
+        const int32_t* __restrict__ elist, int h, int i_dim, int rb, uint32_t wbytes, uint32_t hbytes,
+        float* __restrict__ obuf) {
+    extern __shared__ skinny::u32x4 moe_lds[];
+    const int e = blockIdx.y;
+    const int base = eoff[e], cnt = eoff[e + 1] - base;
+    if (cnt <= 0) return;
+    const int32_t* slots = elist + base;
+    const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+    skinny::TileArgs<1> ta;
+    ta.w[0] = skinny::make_rsrc(wd.p[e], wbytes);
+    ta.x = skinny::make_rsrc(hbuf, hbytes);
+    ta.row0 = static_cast<int>(blockIdx.x) * skinny::ROWS;
+    ta.rows = h - ta.row0 < skinny::ROWS ? h - ta.row0 : skinny::ROWS;
+    ta.nrows = h;
+    ta.rb = rb;
+    ta.nsb = i_dim / 256;
+    for (int m0 = 0; m0 < cnt; m0 += 16) {
+        const int nrow = cnt - m0 < 16 ? cnt - m0 : 16;
+        ta.xoff = j < nrow ? (static_cast<uint32_t>(slots[m0 + j]) * static_cast<uint32_t>(i_dim) + 64u * g) * 2u
+                           : skinny::X_NONE;
+        float4_t s[1];
+        skinny::tile<skinny::X_F16, 1>(ta, reinterpret_cast<uint8_t*>(moe_lds), s);
+        if (threadIdx.x < 256) {
+            const int q = threadIdx.x >> 6, l = threadIdx.x & 63;
+            const int r = 16 * q + (l & 15), n = ta.row0 + r;
+            if (r < ta.rows) {
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int t = 4 * (l >> 4) + v;
+                    if (t < nrow) obuf[static_cast<int64_t>(slots[m0 + t]) * h + n] = s[0][v];
+                }
+            }
+        }
+    }
+}
+
 __global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restrict__ obuf,
                                                           const float* __restrict__ logits, int e_n, int topk,
                                                           int64_t h, float* __restrict__ y,
@@ -254,21 +382,31 @@ __global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restric
     __syncthreads();
     for (int64_t o = threadIdx.x; o < h; o += blockDim.x) {
         float s = 0.f;
-        for (int k = 0; k < topk; k++) s += sw[k] * obuf[(static_cast<int64_t>(t) * topk + k) * h + o];
+        for (int k = 0; k < topk; k++)
+            if (sidx[k] >= 0) s += sw[k] * obuf[(static_cast<int64_t>(t) * topk + k) * h + o];
         y[static_cast<int64_t>(t) * h + o] = s;
     }
 }
 
+// Workspace: hbuf (slots x i, fp32 for F32 experts, fp16 for Q4_K), obuf
+// (slots x h fp32); Q4_K only: xh (tokens x h fp16), routing (ridx, rw),
+// per-expert slot lists (eoff, elist).
 struct MoeWs {
-    size_t hbuf, obuf, total;
+    size_t hbuf, obuf, xh, ridx, rw, eoff, elist, total;
 };
 
 MoeWs moe_ws(int64_t t, int32_t topk, int64_t h, int64_t i) {
     MoeWs w;
     auto al = [](size_t b) { return (b + 255) & ~size_t(255); };
+    const size_t slots = static_cast<size_t>(t) * topk;
     w.hbuf = 0;
-    w.obuf = al(static_cast<size_t>(t) * topk * i * sizeof(float));
-    w.total = w.obuf + al(static_cast<size_t>(t) * topk * h * sizeof(float));
+    w.obuf = al(slots * i * sizeof(float));
+    w.xh = w.obuf + al(slots * h * sizeof(float));
+    w.ridx = w.xh + al(static_cast<size_t>(t) * h * 2);
+    w.rw = w.ridx + al(slots * sizeof(int32_t));
+    w.eoff = w.rw + al(slots * sizeof(float));
+    w.elist = w.eoff + al((MOE_MAX_EXPERTS + 1) * sizeof(int32_t));
+    w.total = w.elist + al(slots * sizeof(int32_t));
     return w;
 }
 
@@ -322,22 +460,46 @@ extern "C" int vb_moe_grouped_ffn(const void* const* wg, const void* const* wu, 
     }
     float* hbuf = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + ws.hbuf);
     float* obuf = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + ws.obuf);
-    const dim3 gu_grid(static_cast<uint32_t>((i + 15) / 16), n_exp), dn_grid(static_cast<uint32_t>((h + 15) / 16), n_exp);
-    if (ggml_type == TYPE_Q4_K)
-        moe_gate_up_kernel<TYPE_Q4_K><<<gu_grid, dim3(256), 0, st>>>(pg, pu, x, router_logits, n_tokens, n_exp, topk,
-                                                                     h, i, row_bytes(ggml_type, h), hbuf);
-    else
+    int rc = OK;
+    if (ggml_type == TYPE_Q4_K) {
+        const int64_t rb_gu = row_bytes(ggml_type, h), rb_d = row_bytes(ggml_type, i);
+        const int64_t slots = static_cast<int64_t>(n_tokens) * topk;
+        if (h > INT32_MAX || i > INT32_MAX || i * rb_gu >= (int64_t(1) << 32) || h * rb_d >= (int64_t(1) << 32) ||
+            static_cast<int64_t>(n_tokens) * h * 2 >= (int64_t(1) << 31) || slots * i * 2 >= (int64_t(1) << 31)) {
+            set_error("vb_moe_grouped_ffn: expert or activation tensors too large for 32-bit offsets");
+            return E_INVAL;
+        }
+        uint8_t* wsb = static_cast<uint8_t*>(workspace);
+        _Float16* hb16 = reinterpret_cast<_Float16*>(hbuf);
+        _Float16* xh = reinterpret_cast<_Float16*>(wsb + ws.xh);
+        int32_t* ridx = reinterpret_cast<int32_t*>(wsb + ws.ridx);
+        float* rw = reinterpret_cast<float*>(wsb + ws.rw);
+        int32_t* eoff = reinterpret_cast<int32_t*>(wsb + ws.eoff);
+        int32_t* elist = reinterpret_cast<int32_t*>(wsb + ws.elist);
+        const int64_t nx = static_cast<int64_t>(n_tokens) * h;
+        const dim3 prep(static_cast<uint32_t>(1 + (nx / 8 + PREP_THREADS - 1) / PREP_THREADS));
+        moe_prep_kernel<<<prep, dim3(PREP_THREADS), 0, st>>>(x, router_logits, n_tokens, n_exp, topk, nx, xh, ridx, rw,
+                                                             eoff, elist);
+        if ((rc = check_launch("vb_moe_grouped_ffn")) != OK) return rc;
+        const dim3 gu(static_cast<uint32_t>((i + skinny::ROWS - 1) / skinny::ROWS), n_exp);
+        const dim3 dn(static_cast<uint32_t>((h + skinny::ROWS - 1) / skinny::ROWS), n_exp);
+        moe_gate_up_q4k<<<gu, dim3(64 * skinny::WAVES), skinny::LDS_BYTES, st>>>(
+                pg, pu, xh, eoff, elist, topk, static_cast<int>(h), static_cast<int>(i), static_cast<int>(rb_gu),
+                static_cast<uint32_t>(i * rb_gu), static_cast<uint32_t>(nx * 2), hb16);
+        if ((rc = check_launch("vb_moe_grouped_ffn")) != OK) return rc;
+        moe_down_q4k<<<dn, dim3(64 * skinny::WAVES), skinny::LDS_BYTES, st>>>(
+                pd, hb16, eoff, elist, static_cast<int>(h), static_cast<int>(i), static_cast<int>(rb_d),
+                static_cast<uint32_t>(h * rb_d), static_cast<uint32_t>(slots * i * 2), obuf);
+        if ((rc = check_launch("vb_moe_grouped_ffn")) != OK) return rc;
+    } else {
+        const dim3 gu_grid(static_cast<uint32_t>((i + 15) / 16), n_exp), dn_grid(static_cast<uint32_t>((h + 15) / 16), n_exp);
         moe_gate_up_kernel<TYPE_F32><<<gu_grid, dim3(256), 0, st>>>(pg, pu, x, router_logits, n_tokens, n_exp, topk,
                                                                     h, i, row_bytes(ggml_type, h), hbuf);
-    int rc = check_launch("vb_moe_grouped_ffn");
-    if (rc != OK) return rc;
-    if (ggml_type == TYPE_Q4_K)
-        moe_down_kernel<TYPE_Q4_K><<<dn_grid, dim3(256), 0, st>>>(pd, hbuf, router_logits, n_tokens, n_exp, topk, h, i,
-                                                                  row_bytes(ggml_type, i), obuf);
-    else
+        if ((rc = check_launch("vb_moe_grouped_ffn")) != OK) return rc;
         moe_down_kernel<TYPE_F32><<<dn_grid, dim3(256), 0, st>>>(pd, hbuf, router_logits, n_tokens, n_exp, topk, h, i,
                                                                  row_bytes(ggml_type, i), obuf);
-    if ((rc = check_launch("vb_moe_grouped_ffn")) != OK) return rc;
+        if ((rc = check_launch("vb_moe_grouped_ffn")) != OK) return rc;
+    }
     moe_combine_kernel<<<dim3(static_cast<uint32_t>(n_tokens)), dim3(256), 0, st>>>(obuf, router_logits, n_exp,
                                                                                   topk, h, y, out_idx, out_w);
     return check_launch("vb_moe_grouped_ffn");
