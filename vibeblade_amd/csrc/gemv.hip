@@ -110,30 +110,53 @@ __device__ __forceinline__ int run_dot(const uint32_t* q, const uint32_t* xh, co
     return ah * 256 + al;
 }
 
-__device__ __forceinline__ float unit_dot(const Q4KUnit& v, const XSlice& xs, int u) {
-    const int c = u & 3;
+// Lane-constant selectors of the 6-bit scale / min of sub-blocks 2c, 2c+1
+// (c = the lane's chunk; get_scale_min_k4, cpp/src/dequant.cpp:258-266),
+// with sh = 16 (c & 1) and A, B, C = scales[0:4], [4:8], [8:12]:
+//   c < 2:  sc = (A >> sh) & 0x3F3F,  m = (B >> sh) & 0x3F3F
+//   c >= 2: sc = ((C >> sh) & 0x0F0F) | ((A >> (sh + 2)) & 0x3030)
+//           m  = ((C >> (sh + 4)) & 0x0F0F) | ((B >> (sh + 2)) & 0x3030)
+struct Q4KSel {
+    uint32_t sh, sh2, shm, m1, m2;
+    bool hi;
+};
+
+template <int TYPE>
+__device__ __forceinline__ auto make_unit_sel(int u) {
+    if constexpr (TYPE == TYPE_Q4_K) {
+        const int c = u & 3;
+        Q4KSel q;
+        q.hi = c >= 2;
+        q.sh = 16u * static_cast<uint32_t>(c & 1);
+        q.sh2 = q.sh + 2u;
+        q.shm = q.hi ? q.sh + 4u : q.sh;
+        q.m1 = q.hi ? 0x0F0Fu : 0x3F3Fu;
+        q.m2 = q.hi ? 0x3030u : 0u;
+        return q;
+    } else {
+        return u;
+    }
+}
+
+// High nibbles enter the dot products as (q ^ 0x80) & 0xF0 = 16 (q - 8), a
+// signed byte, with one v_bitop3 per 4 bytes instead of a shift and a mask:
+//   sum x16 q = (sum x16 16 (q - 8) + 128 isum) / 16   (exact; isum = sum x16)
+__device__ __forceinline__ float unit_dot(const Q4KUnit& v, const XSlice& xs, const Q4KSel& q) {
     const uint32_t qd[8] = {v.qa.x, v.qa.y, v.qa.z, v.qa.w, v.qb.x, v.qb.y, v.qb.z, v.qb.w};
     uint32_t lo[8], hi[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         lo[i] = qd[i] & 0x0F0F0F0Fu;
-        hi[i] = (qd[i] >> 4) & 0x0F0F0F0Fu;
+        hi[i] = (qd[i] ^ 0x80808080u) & 0xF0F0F0F0u;
     }
     const int s0 = run_dot(lo, xs.h, xs.l, 8);
-    const int s1 = run_dot(hi, xs.h + 8, xs.l + 8, 8);
-    // 6-bit scales/mins of sub-blocks 2c and 2c+1, two bytes at a time.  The
-    // quad's lanes hold units c = 0..3 of the same super-block.
+    const int s1 = (run_dot(hi, xs.h + 8, xs.l + 8, 8) + 128 * xs.isum[1]) >> 4;
+    // The quad's lanes hold units c = 0..3 of the same super-block and share
+    // its 16-byte header through DPP broadcasts.
     const uint32_t hx = quad_bcast<0>(v.hw);
-    const uint32_t sh = 16u * static_cast<uint32_t>(c & 1);
-    const uint32_t A = quad_bcast<1>(v.hw) >> sh, B = quad_bcast<2>(v.hw) >> sh, C = quad_bcast<3>(v.hw) >> sh;
-    uint32_t SC, M;
-    if (c < 2) {
-        SC = A & 0x3F3Fu;
-        M = B & 0x3F3Fu;
-    } else {
-        SC = (C & 0x0F0Fu) | ((A >> 2) & 0x3030u);
-        M = ((C >> 4) & 0x0F0Fu) | ((B >> 2) & 0x3030u);
-    }
+    const uint32_t A = quad_bcast<1>(v.hw), B = quad_bcast<2>(v.hw), C = quad_bcast<3>(v.hw);
+    const uint32_t SC = (((q.hi ? C : A) >> q.sh) & q.m1) | ((A >> q.sh2) & q.m2);
+    const uint32_t M = (((q.hi ? C : B) >> q.shm) & q.m1) | ((B >> q.sh2) & q.m2);
     const float d = f16lo(hx), dmin = f16hi(hx);
     const float sc0 = static_cast<float>(SC & 0xFFu), sc1 = static_cast<float>((SC >> 8) & 0xFFu);
     const float m0 = static_cast<float>(M & 0xFFu), m1 = static_cast<float>((M >> 8) & 0xFFu);
@@ -398,6 +421,7 @@ __global__ void __launch_bounds__((gemv_max_threads<TYPE, D>())) gemv_q_kernel(
     // Idle lanes load a real unit (discarded).  Q4_K keeps u % 4 == lane % 4
     // (units and upw are multiples of 4) so every quad reads one super-block.
     const int uc = valid ? u : units - 4 + (lane & 3);
+    const auto usel = make_unit_sel<TYPE>(uc);
     const int nsteps_p = ((rpg + D - 1) / D) * D;
 
     auto issue = [&](Unit& v, int step) {
@@ -429,7 +453,7 @@ __global__ void __launch_bounds__((gemv_max_threads<TYPE, D>())) gemv_q_kernel(
 
     auto compute = [&](const Unit& vv, int step) {
         if (step >= rpg) return;  // padding step (uniform)
-        float a = unit_dot(vv, xs, uc);
+        float a = unit_dot(vv, xs, usel);
         a = valid ? a : 0.f;
         const float tot = wave_sum_dpp(a);
         if (lane == 0) myred[step] = tot;

@@ -156,7 +156,7 @@ struct TileArgs {
 // the sums of weight row row0 + 16 q + l % 16 with activation rows
 // 4 (l / 16) + 0..3 of every matrix.  All threads of the workgroup must call
 // it (it synchronises); `lds` = the launch's dynamic LDS (LDS_BYTES).
-template <int XT, int NMAT>
+template <int XT, int NMAT, int RING = 2>
 __device__ __forceinline__ void tile(const TileArgs<NMAT>& ta, uint8_t* lds, float4_t* out) {
     const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -193,18 +193,26 @@ __device__ __forceinline__ void tile(const TileArgs<NMAT>& ta, uint8_t* lds, flo
     // their super-block starts, after which their buffer is free again.
     constexpr int XB = XT == X_F16 ? 2 : 1;
     constexpr int P = 2 * NMAT;  // units per unrolled period (ring slot and buffer parities repeat)
-    u32x4 pv[2][PPL];
+    u32x4 pv[RING][PPL];
     XWords<XT> xw[XB];
     Frag a[XT == X_F32 ? 8 : 1];  // converted fp32 activations of the current super-block
     int itw = 0, itx = 0;
     // Ring slots are compile-time constants so the buffers stay in registers.
     auto issue_w = [&](auto slot_c) __attribute__((always_inline)) {
-        constexpr int slot = decltype(slot_c)::value;  // unit parity; with NMAT = 2 also the matrix
+        constexpr int slot = decltype(slot_c)::value;  // ring slot
         int sb = sb0 + itw / NMAT;
         sb = sb < nsb - 1 ? sb : nsb - 1;  // padding units reload the last super-block
+        if constexpr (NMAT == 1 || RING == 2) {
+            // NMAT = 2 with a ring of two: the slot is the unit parity, i.e. the matrix
 #pragma unroll
-        for (int i = 0; i < PPL; i++)
-            pv[slot][i] = buf_ld128(ta.w[slot % NMAT], poff[i], static_cast<uint32_t>(sb) * 144u);
+            for (int i = 0; i < PPL; i++)
+                pv[slot][i] = buf_ld128(ta.w[slot % NMAT], poff[i], static_cast<uint32_t>(sb) * 144u);
+        } else {
+            // one slot for both matrices: pick the resource by the unit's parity
+            const __amdgpu_buffer_rsrc_t r = (itw & 1) ? ta.w[NMAT - 1] : ta.w[0];
+#pragma unroll
+            for (int i = 0; i < PPL; i++) pv[slot][i] = buf_ld128(r, poff[i], static_cast<uint32_t>(sb) * 144u);
+        }
         ++itw;
     };
     auto issue_x = [&](auto buf_c) __attribute__((always_inline)) {
@@ -223,7 +231,7 @@ __device__ __forceinline__ void tile(const TileArgs<NMAT>& ta, uint8_t* lds, flo
     int ct = 0;
     auto compute = [&](auto u_c) __attribute__((always_inline)) {
         constexpr int u = decltype(u_c)::value;  // position in the period
-        constexpr int slot = u % 2, m = u % NMAT, xb = (u / NMAT) % 2;
+        constexpr int slot = RING == 1 ? 0 : u % 2, m = u % NMAT, xb = (u / NMAT) % 2;
         if (ct >= nunits) return;  // padding unit (uniform)
         if constexpr (m == 0) {
             if constexpr (XT == X_F32) xwords_to_frags<XT>(xw[0], a);
@@ -245,6 +253,10 @@ __device__ __forceinline__ void tile(const TileArgs<NMAT>& ta, uint8_t* lds, flo
         };
 #pragma unroll
         for (int i = 0; i < PPL; i++) *reinterpret_cast<u32x4*>(stage + soff[i]) = pv[slot][i];
+        if constexpr (RING == 1) {
+            // the unit is in LDS: its registers take the next unit now
+            if (ct + 1 < nunits) issue_w(std::integral_constant<int, 0>{});
+        }
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const uint8_t* rp = stage + (16 * q + j) * 144;
@@ -269,6 +281,19 @@ __device__ __forceinline__ void tile(const TileArgs<NMAT>& ta, uint8_t* lds, flo
     // computes P units and refills the ring two units ahead; the last period
     // issues nothing past the end.
     const int nunits_p = nunits <= P ? P : ((nunits + P - 1) / P) * P;
+    if constexpr (RING == 1) {
+        // one unit in flight per wave, refilled as soon as it is staged
+        issue_w(std::integral_constant<int, 0>{});
+        issue_x(std::integral_constant<int, 0>{});
+        for (int u0 = 0; u0 < nunits_p; u0 += P) {
+            compute(std::integral_constant<int, 0>{});
+            compute(std::integral_constant<int, 1>{});
+            if constexpr (NMAT == 2) {
+                compute(std::integral_constant<int, 2>{});
+                compute(std::integral_constant<int, 3>{});
+            }
+        }
+    } else {
     issue_w(std::integral_constant<int, 0>{});
     issue_x(std::integral_constant<int, 0>{});
     issue_w(std::integral_constant<int, 1>{});
@@ -294,6 +319,7 @@ __device__ __forceinline__ void tile(const TileArgs<NMAT>& ta, uint8_t* lds, flo
     } else {
         compute(std::integral_constant<int, 0>{});
         compute(std::integral_constant<int, 1>{});
+    }
     }
 
     // k-range partials meet in LDS (over the staging areas), fixed order.

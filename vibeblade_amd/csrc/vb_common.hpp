@@ -107,24 +107,32 @@ __device__ __forceinline__ T wave_sum(T v) {
     return v;
 }
 
+// old = 0 (the identity of the add that follows) lets the compiler fold the
+// move into v_add_f32_dpp.
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// v from the DPP source lane in the rows of ROW_MASK, 0 in the other rows.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_rows_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
 }
 
 // Sum over the 64 lanes of a wave; the result is wave-uniform.  Quad
-// butterflies, then half-row and row mirrors (DPP, no LDS traffic), then the
-// four row sums through v_readlane.
+// butterflies and half-row / row mirrors give every lane its 16-lane row's
+// sum; row_bcast:15 then adds row 0 into row 1 and row 2 into row 3, and
+// row_bcast:31 adds lane 31 (rows 0 + 1) into rows 2 and 3, so lane 63 holds
+// the total (DPP only, no LDS traffic).
 __device__ __forceinline__ float wave_sum_dpp(float v) {
     v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
     v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
     v += dpp_f<0x141>(v);  // row_half_mirror
     v += dpp_f<0x140>(v);  // row_mirror
-    const int b = __float_as_int(v);
-    return (__int_as_float(__builtin_amdgcn_readlane(b, 0)) +
-            __int_as_float(__builtin_amdgcn_readlane(b, 16))) +
-           (__int_as_float(__builtin_amdgcn_readlane(b, 32)) +
-            __int_as_float(__builtin_amdgcn_readlane(b, 48)));
+    v += dpp_rows_f<0x142, 0xA>(v);  // row_bcast:15 into rows 1, 3
+    v += dpp_rows_f<0x143, 0xC>(v);  // row_bcast:31 into rows 2, 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 }  // namespace vb
