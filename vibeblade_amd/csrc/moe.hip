@@ -9,17 +9,18 @@
 // reference's HotColdExecutor.dispatch routes only the first token of a batch
 // (vibeblade/moe_executor.py:210-212); this routes every token.
 //
-// Three launches, no host round trip:
-//   1. gate/up: every workgroup recomputes the routing (T x E logits, cheap)
-//      and lists the (token, slot) pairs that chose its expert in token order.
-//      Q4_K experts: grid (i/64, E), skinny tiles (skinny_core.hpp) of 64
-//      gate and 64 up rows per 16 slots, silu(g) * u written as fp16 into
-//      hbuf.  F32 experts: grid (i/16, E), 16-row tiles on
+// Four launches, no host round trip:
+//   1. prep: routes every token once (routing written for the combine and the
+//      caller), lists the slots (token * topk + k) of each expert in slot
+//      order, and rounds x to fp16.
+//   2. gate/up.  Q4_K experts: grid (i/64, E), skinny tiles (skinny_core.hpp)
+//      of 64 gate and 64 up rows per 16 slots, silu(g) * u written as fp16
+//      into hbuf.  F32 experts: grid (i/16, E), 16-row tiles on
 //      v_mfma_f32_16x16x32_f16, hbuf in fp32.
-//   2. down: same routing, activations = hbuf rows of the expert's slots,
-//      writes the expert output of every slot into obuf.
-//   3. combine: y_t = sum_k w_tk * obuf[t*topk + k] in slot order (fixed
-//      order, deterministic); also writes the routing (indices, weights).
+//   3. down: activations = hbuf rows of the expert's slots, writes the expert
+//      output of every slot into obuf.
+//   4. combine: y_t = sum_k w_tk * obuf[t*topk + k] in slot order (fixed
+//      order, deterministic); also copies the routing to (indices, weights).
 // Each expert's weights are streamed once per 16 routed slots.
 #include "mfma_q4k.hpp"
 #include "skinny_core.hpp"
@@ -38,55 +39,57 @@ struct ExpertPtrs {
 };
 
 // Route token t: top-k of softmax(clamp(logits, -50, 50)), renormalised.
-// Ties go to the lower expert id.
-__device__ void route_token(const float* __restrict__ logits, int e_n, int topk, int* idx, float* w) {
+// Ties go to the lower expert id.  The clamped logits are read once into
+// registers (one round of loads instead of one per pass).
+__device__ __forceinline__ void route_token(const float* __restrict__ logits, int e_n, int topk, int* idx, float* w) {
+    float lg[MOE_MAX_EXPERTS];
+#pragma unroll
+    for (int e = 0; e < MOE_MAX_EXPERTS; e++)
+        lg[e] = e < e_n ? fminf(fmaxf(logits[e], -50.f), 50.f) : -INFINITY;
     float mx = -INFINITY;
-    for (int e = 0; e < e_n; e++) mx = fmaxf(mx, fminf(fmaxf(logits[e], -50.f), 50.f));
+#pragma unroll
+    for (int e = 0; e < MOE_MAX_EXPERTS; e++)
+        if (e < e_n) mx = fmaxf(mx, lg[e]);
     float denom = 0.f;
-    for (int e = 0; e < e_n; e++) denom += __expf(fminf(fmaxf(logits[e], -50.f), 50.f) - mx);
-    for (int k = 0; k < topk; k++) {
-        idx[k] = -1;
-        w[k] = -1.f;
+#pragma unroll
+    for (int e = 0; e < MOE_MAX_EXPERTS; e++)
+        if (e < e_n) denom += __expf(lg[e] - mx);
+    // top-k kept in descending order in fixed-size arrays (static indices,
+    // registers): inserting p puts it after every weight >= p, so ties keep
+    // the lower expert id first; the smallest weight drops out.
+    float tw[MOE_MAX_TOPK];
+    int ti[MOE_MAX_TOPK];
+#pragma unroll
+    for (int k = 0; k < MOE_MAX_TOPK; k++) {
+        tw[k] = -1.f;
+        ti[k] = -1;
     }
-    for (int e = 0; e < e_n; e++) {
-        const float p = __expf(fminf(fmaxf(logits[e], -50.f), 50.f) - mx) / denom;
-        int pos = topk;
-        while (pos > 0 && p > w[pos - 1]) pos--;
-        if (pos < topk) {
-            for (int j = topk - 1; j > pos; j--) {
-                w[j] = w[j - 1];
-                idx[j] = idx[j - 1];
+#pragma unroll
+    for (int e = 0; e < MOE_MAX_EXPERTS; e++) {
+        if (e < e_n) {
+            const float p = __expf(lg[e] - mx) / denom;
+#pragma unroll
+            for (int j = MOE_MAX_TOPK - 1; j >= 0; j--) {
+                if (j < topk && p > tw[j]) {
+                    const bool here = j == 0 || !(p > tw[j > 0 ? j - 1 : 0]);
+                    tw[j] = here ? p : tw[j > 0 ? j - 1 : 0];
+                    ti[j] = here ? e : ti[j > 0 ? j - 1 : 0];
+                }
             }
-            w[pos] = p;
-            idx[pos] = e;
         }
     }
     float s = 0.f;
-    for (int k = 0; k < topk; k++) s += w[k];
+#pragma unroll
+    for (int k = 0; k < MOE_MAX_TOPK; k++)
+        if (k < topk) s += tw[k];
     s = s < 1e-12f ? 1.f : s;
-    for (int k = 0; k < topk; k++) w[k] /= s;
-}
-
-// Slots (t*topk + k) routed to expert `e`, in slot order, into slots[];
-// returns the count.  Uses the first T threads; all threads must call.
-__device__ int expert_slots(const float* __restrict__ logits, int t_n, int e_n, int topk, int e,
-                            int* slots, int* flags) {
-    for (int t = threadIdx.x; t < t_n; t += blockDim.x) {
-        int idx[MOE_MAX_TOPK];
-        float w[MOE_MAX_TOPK];
-        route_token(logits + static_cast<int64_t>(t) * e_n, e_n, topk, idx, w);
-        for (int k = 0; k < topk; k++) flags[t * topk + k] = idx[k] == e ? 1 : 0;
+#pragma unroll
+    for (int k = 0; k < MOE_MAX_TOPK; k++) {
+        if (k < topk) {
+            idx[k] = ti[k];
+            w[k] = tw[k] / s;
+        }
     }
-    __syncthreads();
-    __shared__ int count;
-    if (threadIdx.x == 0) {
-        int c = 0;
-        for (int s = 0; s < t_n * topk; s++)
-            if (flags[s]) slots[c++] = s;
-        count = c;
-    }
-    __syncthreads();
-    return count;
 }
 
 // One 16-row tile of F32 expert weights times the gathered fp32 activation
@@ -136,15 +139,15 @@ __device__ void tile_mfma(const uint8_t* const* wrow, const float* const* arow, 
 
 template <int WT>
 __global__ void __launch_bounds__(256) moe_gate_up_kernel(ExpertPtrs wg, ExpertPtrs wu, const float* __restrict__ x,
-                                                          const float* __restrict__ logits, int t_n, int e_n,
-                                                          int topk, int64_t h, int64_t i_dim, int64_t rb,
-                                                          float* __restrict__ hbuf) {
-    __shared__ int slots[MOE_MAX_SLOTS], flags[MOE_MAX_SLOTS];
+                                                          const int32_t* __restrict__ eoff,
+                                                          const int32_t* __restrict__ elist, int topk, int64_t h,
+                                                          int64_t i_dim, int64_t rb, float* __restrict__ hbuf) {
     __shared__ float4_t red[2][4][64];
     const int e = blockIdx.y;
     const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
-    const int cnt = expert_slots(logits, t_n, e_n, topk, e, slots, flags);
-    if (cnt == 0) return;
+    const int cnt = eoff[e + 1] - eoff[e];
+    if (cnt <= 0) return;
+    const int32_t* slots = elist + eoff[e];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = lane & 15, g = lane >> 4;
     int64_t n = n0 + j;
@@ -178,15 +181,15 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(ExpertPtrs wg, ExpertP
 
 template <int WT>
 __global__ void __launch_bounds__(256) moe_down_kernel(ExpertPtrs wd, const float* __restrict__ hbuf,
-                                                       const float* __restrict__ logits, int t_n, int e_n,
-                                                       int topk, int64_t h, int64_t i_dim, int64_t rb,
-                                                       float* __restrict__ obuf) {
-    __shared__ int slots[MOE_MAX_SLOTS], flags[MOE_MAX_SLOTS];
+                                                       const int32_t* __restrict__ eoff,
+                                                       const int32_t* __restrict__ elist, int64_t h, int64_t i_dim,
+                                                       int64_t rb, float* __restrict__ obuf) {
     __shared__ float4_t red[1][4][64];
     const int e = blockIdx.y;
     const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
-    const int cnt = expert_slots(logits, t_n, e_n, topk, e, slots, flags);
-    if (cnt == 0) return;
+    const int cnt = eoff[e + 1] - eoff[e];
+    if (cnt <= 0) return;
+    const int32_t* slots = elist + eoff[e];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = lane & 15, g = lane >> 4;
     int64_t n = n0 + j;
@@ -218,7 +221,7 @@ __global__ void __launch_bounds__(256) moe_down_kernel(ExpertPtrs wd, const floa
 // the other blocks round x to fp16 (xh) -- the MFMA path rounds its
 // activations to fp16 anyway, and fp16 halves the activation traffic of the
 // expert kernels.
-constexpr int PREP_THREADS = 1024;
+constexpr int PREP_THREADS = 256;
 
 __global__ void __launch_bounds__(PREP_THREADS) moe_prep_kernel(
         const float* __restrict__ x, const float* __restrict__ logits, int t_n, int e_n, int topk, int64_t nx,
@@ -242,10 +245,13 @@ __global__ void __launch_bounds__(PREP_THREADS) moe_prep_kernel(
         int idx[MOE_MAX_TOPK];
         float w[MOE_MAX_TOPK];
         route_token(logits + static_cast<int64_t>(t) * e_n, e_n, topk, idx, w);
-        for (int k = 0; k < topk; k++) {
-            ridx[t * topk + k] = idx[k];
-            rw[t * topk + k] = w[k];
-            sexp[t * topk + k] = idx[k];
+#pragma unroll
+        for (int k = 0; k < MOE_MAX_TOPK; k++) {
+            if (k < topk) {
+                ridx[t * topk + k] = idx[k];
+                rw[t * topk + k] = w[k];
+                sexp[t * topk + k] = idx[k];
+            }
         }
     }
     __syncthreads();
@@ -360,32 +366,31 @@ __global__ void __launch_bounds__(64 * skinny::WAVES) moe_down_q4k(
     }
 }
 
-__global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restrict__ obuf,
-                                                          const float* __restrict__ logits, int e_n, int topk,
-                                                          int64_t h, float* __restrict__ y,
-                                                          int32_t* __restrict__ out_idx,
+// combine from the prep kernel's routing: grid (T, ceil(h / 1024)), four
+// outputs per thread; y_t = sum_k w_tk * obuf[t*topk + k] in slot order.
+__global__ void __launch_bounds__(256) moe_combine_routed(const float* __restrict__ obuf,
+                                                          const int32_t* __restrict__ ridx,
+                                                          const float* __restrict__ rw, int topk, int64_t h,
+                                                          float* __restrict__ y, int32_t* __restrict__ out_idx,
                                                           float* __restrict__ out_w) {
     const int t = blockIdx.x;
-    __shared__ int sidx[MOE_MAX_TOPK];
-    __shared__ float sw[MOE_MAX_TOPK];
-    if (threadIdx.x == 0) {
-        int idx[MOE_MAX_TOPK];
-        float w[MOE_MAX_TOPK];
-        route_token(logits + static_cast<int64_t>(t) * e_n, e_n, topk, idx, w);
-        for (int k = 0; k < topk; k++) {
-            sidx[k] = idx[k];
-            sw[k] = w[k];
-            if (out_idx) out_idx[t * topk + k] = idx[k];
-            if (out_w) out_w[t * topk + k] = w[k];
-        }
+    if (blockIdx.y == 0 && static_cast<int>(threadIdx.x) < topk) {
+        if (out_idx) out_idx[t * topk + threadIdx.x] = ridx[t * topk + threadIdx.x];
+        if (out_w) out_w[t * topk + threadIdx.x] = rw[t * topk + threadIdx.x];
     }
-    __syncthreads();
-    for (int64_t o = threadIdx.x; o < h; o += blockDim.x) {
-        float s = 0.f;
-        for (int k = 0; k < topk; k++)
-            if (sidx[k] >= 0) s += sw[k] * obuf[(static_cast<int64_t>(t) * topk + k) * h + o];
-        y[static_cast<int64_t>(t) * h + o] = s;
+    const int64_t o = (static_cast<int64_t>(blockIdx.y) * 256 + threadIdx.x) * 4;
+    if (o >= h) return;  // h is a multiple of 256
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k = 0; k < topk; k++) {
+        if (ridx[t * topk + k] < 0) continue;
+        const float wk = rw[t * topk + k];
+        const float4 v = *reinterpret_cast<const float4*>(obuf + (static_cast<int64_t>(t) * topk + k) * h + o);
+        s.x += wk * v.x;
+        s.y += wk * v.y;
+        s.z += wk * v.z;
+        s.w += wk * v.w;
     }
+    *reinterpret_cast<float4*>(y + static_cast<int64_t>(t) * h + o) = s;
 }
 
 // Workspace: hbuf (slots x i, fp32 for F32 experts, fp16 for Q4_K), obuf
@@ -460,27 +465,32 @@ extern "C" int vb_moe_grouped_ffn(const void* const* wg, const void* const* wu, 
     }
     float* hbuf = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + ws.hbuf);
     float* obuf = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + ws.obuf);
-    int rc = OK;
+    const int64_t slots = static_cast<int64_t>(n_tokens) * topk;
+    const int64_t nx = static_cast<int64_t>(n_tokens) * h;
+    if (h > INT32_MAX || i > INT32_MAX || nx * 2 >= (int64_t(1) << 31) || slots * i * 2 >= (int64_t(1) << 31)) {
+        set_error("vb_moe_grouped_ffn: activation tensors too large for 32-bit offsets");
+        return E_INVAL;
+    }
+    uint8_t* wsb = static_cast<uint8_t*>(workspace);
+    _Float16* xh = reinterpret_cast<_Float16*>(wsb + ws.xh);
+    int32_t* ridx = reinterpret_cast<int32_t*>(wsb + ws.ridx);
+    float* rw = reinterpret_cast<float*>(wsb + ws.rw);
+    int32_t* eoff = reinterpret_cast<int32_t*>(wsb + ws.eoff);
+    int32_t* elist = reinterpret_cast<int32_t*>(wsb + ws.elist);
+    // 1. routing, per-expert slot lists, fp16 activations
+    const dim3 prep(static_cast<uint32_t>(1 + (nx / 8 + PREP_THREADS - 1) / PREP_THREADS));
+    moe_prep_kernel<<<prep, dim3(PREP_THREADS), 0, st>>>(x, router_logits, n_tokens, n_exp, topk, nx, xh, ridx, rw,
+                                                         eoff, elist);
+    int rc = check_launch("vb_moe_grouped_ffn");
+    if (rc != OK) return rc;
+    // 2, 3. experts
     if (ggml_type == TYPE_Q4_K) {
         const int64_t rb_gu = row_bytes(ggml_type, h), rb_d = row_bytes(ggml_type, i);
-        const int64_t slots = static_cast<int64_t>(n_tokens) * topk;
-        if (h > INT32_MAX || i > INT32_MAX || i * rb_gu >= (int64_t(1) << 32) || h * rb_d >= (int64_t(1) << 32) ||
-            static_cast<int64_t>(n_tokens) * h * 2 >= (int64_t(1) << 31) || slots * i * 2 >= (int64_t(1) << 31)) {
-            set_error("vb_moe_grouped_ffn: expert or activation tensors too large for 32-bit offsets");
+        if (i * rb_gu >= (int64_t(1) << 32) || h * rb_d >= (int64_t(1) << 32)) {
+            set_error("vb_moe_grouped_ffn: expert tensors too large for 32-bit offsets");
             return E_INVAL;
         }
-        uint8_t* wsb = static_cast<uint8_t*>(workspace);
         _Float16* hb16 = reinterpret_cast<_Float16*>(hbuf);
-        _Float16* xh = reinterpret_cast<_Float16*>(wsb + ws.xh);
-        int32_t* ridx = reinterpret_cast<int32_t*>(wsb + ws.ridx);
-        float* rw = reinterpret_cast<float*>(wsb + ws.rw);
-        int32_t* eoff = reinterpret_cast<int32_t*>(wsb + ws.eoff);
-        int32_t* elist = reinterpret_cast<int32_t*>(wsb + ws.elist);
-        const int64_t nx = static_cast<int64_t>(n_tokens) * h;
-        const dim3 prep(static_cast<uint32_t>(1 + (nx / 8 + PREP_THREADS - 1) / PREP_THREADS));
-        moe_prep_kernel<<<prep, dim3(PREP_THREADS), 0, st>>>(x, router_logits, n_tokens, n_exp, topk, nx, xh, ridx, rw,
-                                                             eoff, elist);
-        if ((rc = check_launch("vb_moe_grouped_ffn")) != OK) return rc;
         const dim3 gu(static_cast<uint32_t>((i + skinny::ROWS - 1) / skinny::ROWS), n_exp);
         const dim3 dn(static_cast<uint32_t>((h + skinny::ROWS - 1) / skinny::ROWS), n_exp);
         moe_gate_up_q4k<<<gu, dim3(64 * skinny::WAVES), skinny::LDS_BYTES, st>>>(
@@ -490,18 +500,18 @@ extern "C" int vb_moe_grouped_ffn(const void* const* wg, const void* const* wu, 
         moe_down_q4k<<<dn, dim3(64 * skinny::WAVES), skinny::LDS_BYTES, st>>>(
                 pd, hb16, eoff, elist, static_cast<int>(h), static_cast<int>(i), static_cast<int>(rb_d),
                 static_cast<uint32_t>(h * rb_d), static_cast<uint32_t>(slots * i * 2), obuf);
-        if ((rc = check_launch("vb_moe_grouped_ffn")) != OK) return rc;
     } else {
         const dim3 gu_grid(static_cast<uint32_t>((i + 15) / 16), n_exp), dn_grid(static_cast<uint32_t>((h + 15) / 16), n_exp);
-        moe_gate_up_kernel<TYPE_F32><<<gu_grid, dim3(256), 0, st>>>(pg, pu, x, router_logits, n_tokens, n_exp, topk,
-                                                                    h, i, row_bytes(ggml_type, h), hbuf);
+        moe_gate_up_kernel<TYPE_F32><<<gu_grid, dim3(256), 0, st>>>(pg, pu, x, eoff, elist, topk, h, i,
+                                                                    row_bytes(ggml_type, h), hbuf);
         if ((rc = check_launch("vb_moe_grouped_ffn")) != OK) return rc;
-        moe_down_kernel<TYPE_F32><<<dn_grid, dim3(256), 0, st>>>(pd, hbuf, router_logits, n_tokens, n_exp, topk, h, i,
-                                                                 row_bytes(ggml_type, i), obuf);
-        if ((rc = check_launch("vb_moe_grouped_ffn")) != OK) return rc;
+        moe_down_kernel<TYPE_F32><<<dn_grid, dim3(256), 0, st>>>(pd, hbuf, eoff, elist, h, i, row_bytes(ggml_type, i),
+                                                                 obuf);
     }
-    moe_combine_kernel<<<dim3(static_cast<uint32_t>(n_tokens)), dim3(256), 0, st>>>(obuf, router_logits, n_exp,
-                                                                                  topk, h, y, out_idx, out_w);
+    if ((rc = check_launch("vb_moe_grouped_ffn")) != OK) return rc;
+    // 4. weighted combine
+    moe_combine_routed<<<dim3(static_cast<uint32_t>(n_tokens), static_cast<uint32_t>((h + 1023) / 1024)), dim3(256), 0,
+                         st>>>(obuf, ridx, rw, topk, h, y, out_idx, out_w);
     return check_launch("vb_moe_grouped_ffn");
 }
 
@@ -514,9 +524,12 @@ __global__ void __launch_bounds__(256) moe_route_kernel(const float* __restrict_
     int idx[MOE_MAX_TOPK];
     float w[MOE_MAX_TOPK];
     route_token(logits + static_cast<int64_t>(t) * e_n, e_n, topk, idx, w);
-    for (int k = 0; k < topk; k++) {
-        out_idx[t * topk + k] = idx[k];
-        out_w[t * topk + k] = w[k];
+#pragma unroll
+    for (int k = 0; k < MOE_MAX_TOPK; k++) {
+        if (k < topk) {
+            out_idx[t * topk + k] = idx[k];
+            out_w[t * topk + k] = w[k];
+        }
     }
 }
 }  // namespace
