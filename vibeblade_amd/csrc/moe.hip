@@ -42,10 +42,13 @@ struct ExpertPtrs {
 // Ties go to the lower expert id.  The clamped logits are read once into
 // registers (one round of loads instead of one per pass).
 __device__ __forceinline__ void route_token(const float* __restrict__ logits, int e_n, int topk, int* idx, float* w) {
+    // Branch-free loads (clamped index, masked after the load): a load under
+    // a branch makes the compiler wait for it on the spot, one latency each.
     float lg[MOE_MAX_EXPERTS];
 #pragma unroll
-    for (int e = 0; e < MOE_MAX_EXPERTS; e++)
-        lg[e] = e < e_n ? fminf(fmaxf(logits[e], -50.f), 50.f) : -INFINITY;
+    for (int e = 0; e < MOE_MAX_EXPERTS; e++) lg[e] = logits[e < e_n ? e : e_n - 1];
+#pragma unroll
+    for (int e = 0; e < MOE_MAX_EXPERTS; e++) lg[e] = e < e_n ? fminf(fmaxf(lg[e], -50.f), 50.f) : -INFINITY;
     float mx = -INFINITY;
 #pragma unroll
     for (int e = 0; e < MOE_MAX_EXPERTS; e++)
