@@ -286,7 +286,12 @@ __global__ void __launch_bounds__(PREP_THREADS) moe_prep_kernel(
 // two matrices alternate in the tile's unit ring and share the activation
 // fragments) and writes silu(g) * u for every (slot, row) into hbuf as fp16
 // -- the down kernel rounds its activations to fp16 anyway.
-__global__ void __launch_bounds__(64 * skinny::WAVES) moe_gate_up_q4k(
+// Four-wave workgroups with at most 256 VGPRs, so two run on each CU: one's
+// start-up and reduction overlap the other's weight stream.
+constexpr int MOE_WAVES = 4;
+
+template <int NW>
+__global__ void __launch_bounds__(64 * NW, NW <= 4 ? 2 : 1) moe_gate_up_q4k(
         ExpertPtrs wg, ExpertPtrs wu, const _Float16* __restrict__ xh, const int32_t* __restrict__ eoff,
         const int32_t* __restrict__ elist, int topk, int h, int i_dim, int rb, uint32_t wbytes, uint32_t xbytes,
         _Float16* __restrict__ hbuf) {
@@ -310,7 +315,7 @@ __global__ void __launch_bounds__(64 * skinny::WAVES) moe_gate_up_q4k(
         ta.xoff = j < nrow ? (static_cast<uint32_t>(slots[m0 + j] / topk) * static_cast<uint32_t>(h) + 64u * g) * 2u
                            : skinny::X_NONE;
         float4_t s[2];
-        skinny::tile<skinny::X_F16, 2>(ta, reinterpret_cast<uint8_t*>(moe_lds), s);
+        skinny::tile<skinny::X_F16, 2, 2, NW>(ta, reinterpret_cast<uint8_t*>(moe_lds), s);
         if (threadIdx.x < 256) {
             const int q = threadIdx.x >> 6, l = threadIdx.x & 63;
             const int r = 16 * q + (l & 15), n = ta.row0 + r;
@@ -331,7 +336,8 @@ __global__ void __launch_bounds__(64 * skinny::WAVES) moe_gate_up_q4k(
 
 // down: grid (ceil(h / 64), E); activations = the fp16 hbuf rows of the
 // expert's slots; writes the expert output of every slot into obuf.
-__global__ void __launch_bounds__(64 * skinny::WAVES) moe_down_q4k(
+template <int NW>
+__global__ void __launch_bounds__(64 * NW, NW <= 4 ? 2 : 1) moe_down_q4k(
         ExpertPtrs wd, const _Float16* __restrict__ hbuf, const int32_t* __restrict__ eoff,
         const int32_t* __restrict__ elist, int h, int i_dim, int rb, uint32_t wbytes, uint32_t hbytes,
         float* __restrict__ obuf) {
@@ -354,7 +360,7 @@ __global__ void __launch_bounds__(64 * skinny::WAVES) moe_down_q4k(
         ta.xoff = j < nrow ? (static_cast<uint32_t>(slots[m0 + j]) * static_cast<uint32_t>(i_dim) + 64u * g) * 2u
                            : skinny::X_NONE;
         float4_t s[1];
-        skinny::tile<skinny::X_F16, 1>(ta, reinterpret_cast<uint8_t*>(moe_lds), s);
+        skinny::tile<skinny::X_F16, 1, 2, NW>(ta, reinterpret_cast<uint8_t*>(moe_lds), s);
         if (threadIdx.x < 256) {
             const int q = threadIdx.x >> 6, l = threadIdx.x & 63;
             const int r = 16 * q + (l & 15), n = ta.row0 + r;
@@ -496,13 +502,13 @@ extern "C" int vb_moe_grouped_ffn(const void* const* wg, const void* const* wu, 
         _Float16* hb16 = reinterpret_cast<_Float16*>(hbuf);
         const dim3 gu(static_cast<uint32_t>((i + skinny::ROWS - 1) / skinny::ROWS), n_exp);
         const dim3 dn(static_cast<uint32_t>((h + skinny::ROWS - 1) / skinny::ROWS), n_exp);
-        moe_gate_up_q4k<<<gu, dim3(64 * skinny::WAVES), skinny::LDS_BYTES, st>>>(
-                pg, pu, xh, eoff, elist, topk, static_cast<int>(h), static_cast<int>(i), static_cast<int>(rb_gu),
-                static_cast<uint32_t>(i * rb_gu), static_cast<uint32_t>(nx * 2), hb16);
+        moe_gate_up_q4k<MOE_WAVES><<<gu, dim3(64 * MOE_WAVES), skinny::lds_bytes<MOE_WAVES>(), st>>>(
+            pg, pu, xh, eoff, elist, topk, static_cast<int>(h), static_cast<int>(i), static_cast<int>(rb_gu),
+            static_cast<uint32_t>(i * rb_gu), static_cast<uint32_t>(nx * 2), hb16);
         if ((rc = check_launch("vb_moe_grouped_ffn")) != OK) return rc;
-        moe_down_q4k<<<dn, dim3(64 * skinny::WAVES), skinny::LDS_BYTES, st>>>(
-                pd, hb16, eoff, elist, static_cast<int>(h), static_cast<int>(i), static_cast<int>(rb_d),
-                static_cast<uint32_t>(h * rb_d), static_cast<uint32_t>(slots * i * 2), obuf);
+        moe_down_q4k<MOE_WAVES><<<dn, dim3(64 * MOE_WAVES), skinny::lds_bytes<MOE_WAVES>(), st>>>(
+            pd, hb16, eoff, elist, static_cast<int>(h), static_cast<int>(i), static_cast<int>(rb_d),
+            static_cast<uint32_t>(h * rb_d), static_cast<uint32_t>(slots * i * 2), obuf);
     } else {
         const dim3 gu_grid(static_cast<uint32_t>((i + 15) / 16), n_exp), dn_grid(static_cast<uint32_t>((h + 15) / 16), n_exp);
         moe_gate_up_kernel<TYPE_F32><<<gu_grid, dim3(256), 0, st>>>(pg, pu, x, eoff, elist, topk, h, i,

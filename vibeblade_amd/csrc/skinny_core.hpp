@@ -36,11 +36,15 @@
 namespace vb {
 namespace skinny {
 
-constexpr int WAVES = 8;
+constexpr int WAVES = 8;                   // default waves per workgroup
 constexpr int ROWS = 64;                   // max rows per workgroup: 4 column groups
 constexpr int PPL = ROWS * 9 / 64;         // 16-byte pieces per lane per unit: 9
 constexpr int STAGE = ROWS * 144 + 16;     // per-wave LDS bytes (+ one discard slot)
-constexpr int LDS_BYTES = WAVES * STAGE;   // dynamic LDS of a launch (>= NMAT x 32 KiB of sums)
+// Dynamic LDS of a launch with NW waves: the staging areas, which the final
+// sums (NMAT x NW x 4 KiB, NMAT <= 2) reuse.
+template <int NW = WAVES>
+constexpr int lds_bytes() { return NW * STAGE; }
+constexpr int LDS_BYTES = lds_bytes<WAVES>();
 constexpr int X_F32 = 0;
 constexpr int X_F16 = 1;
 constexpr uint32_t X_NONE = 0x80000000u;   // lane offset of an absent activation row (reads zeros)
@@ -152,17 +156,19 @@ struct TileArgs {
     int rb, nsb;                     // bytes per weight row, super-blocks per row
 };
 
-// Runs the tile and returns, in threads 0..255 (q = tid / 64, l = tid % 64),
-// the sums of weight row row0 + 16 q + l % 16 with activation rows
-// 4 (l / 16) + 0..3 of every matrix.  All threads of the workgroup must call
-// it (it synchronises); `lds` = the launch's dynamic LDS (LDS_BYTES).
-template <int XT, int NMAT, int RING = 2>
+// Runs the tile with NW waves and returns, in threads 0..255 (q = tid / 64,
+// l = tid % 64), the sums of weight row row0 + 16 q + l % 16 with activation
+// rows 4 (l / 16) + 0..3 of every matrix.  All threads of the workgroup must
+// call it (it synchronises); `lds` = the launch's dynamic LDS
+// (lds_bytes<NW>()).
+template <int XT, int NMAT, int RING = 2, int NW = WAVES>
 __device__ __forceinline__ void tile(const TileArgs<NMAT>& ta, uint8_t* lds, float4_t* out) {
+    static_assert(NMAT * 4096 <= STAGE, "the final sums must fit in the staging areas");
     const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int nsb = ta.nsb;
-    const int sb0 = __builtin_amdgcn_readfirstlane((wave * nsb) / WAVES);
-    const int sb1 = __builtin_amdgcn_readfirstlane(((wave + 1) * nsb) / WAVES);
+    const int sb0 = __builtin_amdgcn_readfirstlane((wave * nsb) / NW);
+    const int sb1 = __builtin_amdgcn_readfirstlane(((wave + 1) * nsb) / NW);
     const int nunits = (sb1 - sb0) * NMAT;  // 0 when nsb < 8 for some waves
     uint8_t* stage = lds + wave * STAGE;
 
@@ -328,15 +334,15 @@ __device__ __forceinline__ void tile(const TileArgs<NMAT>& ta, uint8_t* lds, flo
 #pragma unroll
     for (int m = 0; m < NMAT; m++)
 #pragma unroll
-        for (int q = 0; q < 4; q++) red[((m * WAVES + wave) * 4 + q) * 64 + lane] = acc[m][q];
+        for (int q = 0; q < 4; q++) red[((m * NW + wave) * 4 + q) * 64 + lane] = acc[m][q];
     __syncthreads();
     if (threadIdx.x < 256) {
         const int e = threadIdx.x;
 #pragma unroll
         for (int m = 0; m < NMAT; m++) {
-            float4_t s = red[(m * WAVES * 4) * 64 + e];
+            float4_t s = red[(m * NW * 4) * 64 + e];
 #pragma unroll
-            for (int v = 1; v < WAVES; v++) s += red[((m * WAVES + v) * 4) * 64 + e];
+            for (int v = 1; v < NW; v++) s += red[((m * NW + v) * 4) * 64 + e];
             out[m] = s;
         }
     }
