@@ -11,7 +11,8 @@
 //      gate/up row pairs (gemv.hip, ROWS_PAIRS) -> gu[2r], gu[2r+1];
 //   2. down:
 //      layout 0 (GGUF, W_d is h rows x i): scatter act(gu) into a dense
-//        hidden vector (zeros off S) and run the dense GEMV -- every down
+//        hidden vector (cleared by the gate/up launch, so zeros off S) and
+//        run the dense GEMV -- every down
 //        super-block holds an active column at 10 % density, so all of W_d
 //        is read;
 //      layout 1 (neuron-major D = W_d^T, i rows x h, Q4_K): only the |S|
@@ -34,24 +35,22 @@ __device__ __forceinline__ float act_pair(float g, float u, int kind) {
     return fmaxf(g, 0.f) * fmaxf(u, 0.f);
 }
 
-// layout 0: hid[o] = act(gu[2r], gu[2r+1]) if o == active[r], else 0.
+// layout 0: hid[active[r]] = act(gu[2r], gu[2r+1]); the gate/up launch has
+// cleared hid, so positions off S stay 0.  One thread per active entry: one
+// load round, no search.  Indices outside [0, i) are dropped; a repeated
+// index writes the same value from each of its entries (same row, same x).
 __global__ void __launch_bounds__(256) scatter_act_kernel(const int32_t* __restrict__ active, int n_active,
                                                           const float* __restrict__ gu, int kind,
                                                           float* __restrict__ hid, int64_t i_dim) {
-    const int64_t o = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (o >= i_dim) return;
-    int lo = 0, hi = n_active;  // active is sorted ascending
-    while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (active[mid] < o) lo = mid + 1;
-        else hi = mid;
-    }
-    float v = 0.f;
-    if (lo < n_active && active[lo] == o) v = act_pair(gu[2 * lo], gu[2 * lo + 1], kind);
-    hid[o] = v;
+    const int r = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+    if (r >= n_active) return;
+    const int o = active[r];
+    const float2 g = *reinterpret_cast<const float2*>(gu + 2 * static_cast<int64_t>(r));
+    if (o >= 0 && o < i_dim) hid[o] = act_pair(g.x, g.y, kind);
 }
 
-constexpr int DOWN_RS = 4;  // workgroups per output unit
+constexpr int DOWN_RS = 4;     // workgroups per output unit
+constexpr int DOWN_BATCH = 6;  // rows per thread and load batch
 
 // layout 1, Q4_K: see the header comment.  Thread t = 4*rg + p handles row
 // group rg and quarter p of the unit (16 of its 64 elements: quarter p < 2 =
@@ -70,32 +69,60 @@ __global__ void __launch_bounds__(256) down_axpy_q4k_kernel(
 #pragma unroll
     for (int e = 0; e < 16; e++) acc[e] = 0.f;
     float bacc = 0.f;
-    for (int r = rs + DOWN_RS * rg; r < n_active; r += DOWN_RS * 64) {
-        int64_t nr = active[r];
-        nr = nr < 0 ? 0 : (nr >= i_dim ? i_dim - 1 : nr);
-        const uint8_t* blk = d + nr * rb + static_cast<int64_t>(sb) * 144;
-        const uint4 hd = *reinterpret_cast<const uint4*>(blk);
-        const uint4 q = *reinterpret_cast<const uint4*>(blk + 16 + 32 * c + 16 * (p & 1));
-        const float hid = act_pair(gu[2 * r], gu[2 * r + 1], kind);
-        uint8_t s8[12];
-        const uint32_t sw[3] = {hd.y, hd.z, hd.w};
+    // Rows go in batches of DOWN_BATCH per thread with every load of a batch
+    // issued before any use (indices and activations, then the weight
+    // blocks): two memory latencies per batch instead of two per row.  Rows
+    // past the end load row 0 again and contribute 0.
+    constexpr int STRIDE = DOWN_RS * 64;
+    for (int r0 = rs + DOWN_RS * rg; r0 < n_active; r0 += DOWN_BATCH * STRIDE) {
+        int nr[DOWN_BATCH];
+        float2 gv[DOWN_BATCH];
 #pragma unroll
-        for (int b = 0; b < 12; b++) s8[b] = static_cast<uint8_t>(sw[b >> 2] >> (8 * (b & 3)));
-        float sc, m;
-        if (jsub < 4) {
-            sc = static_cast<float>(s8[jsub] & 63);
-            m = static_cast<float>(s8[jsub + 4] & 63);
-        } else {
-            sc = static_cast<float>((s8[jsub + 4] & 0xF) | ((s8[jsub - 4] >> 6) << 4));
-            m = static_cast<float>((s8[jsub + 4] >> 4) | ((s8[jsub] >> 6) << 4));
+        for (int b = 0; b < DOWN_BATCH; b++) {
+            const int r = r0 + b * STRIDE;
+            const int rc = r < n_active ? r : 0;
+            nr[b] = active[rc];
+            gv[b] = *reinterpret_cast<const float2*>(gu + 2 * rc);
         }
-        const float a = hid * (f16lo(hd.x) * sc);
-        bacc += hid * (f16hi(hd.x) * m);
-        const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-        const int shift = p >= 2 ? 4 : 0;
+        __builtin_amdgcn_sched_barrier(0);  // all index / activation loads first
+        float hid[DOWN_BATCH];
 #pragma unroll
-        for (int e = 0; e < 16; e++)
-            acc[e] += a * static_cast<float>((qw[e >> 2] >> (8 * (e & 3) + shift)) & 0xF);
+        for (int b = 0; b < DOWN_BATCH; b++) {
+            const int v = nr[b];
+            nr[b] = v < 0 ? 0 : (v >= i_dim ? static_cast<int>(i_dim) - 1 : v);
+            hid[b] = r0 + b * STRIDE < n_active ? act_pair(gv[b].x, gv[b].y, kind) : 0.f;
+        }
+        uint4 hdv[DOWN_BATCH], qv[DOWN_BATCH];
+#pragma unroll
+        for (int b = 0; b < DOWN_BATCH; b++) {
+            const uint8_t* blk = d + static_cast<int64_t>(nr[b]) * rb + static_cast<int64_t>(sb) * 144;
+            hdv[b] = *reinterpret_cast<const uint4*>(blk);
+            qv[b] = *reinterpret_cast<const uint4*>(blk + 16 + 32 * c + 16 * (p & 1));
+        }
+        __builtin_amdgcn_sched_barrier(0);  // all weight loads before the math
+#pragma unroll
+        for (int b = 0; b < DOWN_BATCH; b++) {
+            const uint4 hd = hdv[b], q = qv[b];
+            uint8_t s8[12];
+            const uint32_t sw[3] = {hd.y, hd.z, hd.w};
+#pragma unroll
+            for (int k = 0; k < 12; k++) s8[k] = static_cast<uint8_t>(sw[k >> 2] >> (8 * (k & 3)));
+            float sc, m;
+            if (jsub < 4) {
+                sc = static_cast<float>(s8[jsub] & 63);
+                m = static_cast<float>(s8[jsub + 4] & 63);
+            } else {
+                sc = static_cast<float>((s8[jsub + 4] & 0xF) | ((s8[jsub - 4] >> 6) << 4));
+                m = static_cast<float>((s8[jsub + 4] >> 4) | ((s8[jsub] >> 6) << 4));
+            }
+            const float a = hid[b] * (f16lo(hd.x) * sc);
+            bacc += hid[b] * (f16hi(hd.x) * m);
+            const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+            const int shift = p >= 2 ? 4 : 0;
+#pragma unroll
+            for (int e = 0; e < 16; e++)
+                acc[e] += a * static_cast<float>((qw[e >> 2] >> (8 * (e & 3) + shift)) & 0xF);
+        }
     }
 #pragma unroll
     for (int e = 0; e < 16; e++) red[rg][16 * p + e] = acc[e] - bacc;
@@ -240,9 +267,9 @@ extern "C" int vb_sparse_ffn(const void* wg, const void* wu, const void* wd, int
                              float* y, int64_t h, int64_t i, int32_t ggml_type, void* workspace,
                              size_t workspace_bytes, void* stream) {
     hipStream_t st = as_stream(stream);
-    if (h <= 0 || i <= 0 || n_active < 0 || n_active > i || (down_layout != 0 && down_layout != 1) ||
-        (act_kind != ACT_SILU && act_kind != ACT_RELU2) || !wg || !wu || !wd || !x || !y ||
-        (n_active > 0 && !active)) {
+    if (h <= 0 || i <= 0 || h > INT32_MAX || i > INT32_MAX || n_active < 0 || n_active > i ||
+        (down_layout != 0 && down_layout != 1) || (act_kind != ACT_SILU && act_kind != ACT_RELU2) || !wg || !wu ||
+        !wd || !x || !y || (n_active > 0 && !active)) {
         set_error("vb_sparse_ffn: bad arguments");
         return E_INVAL;
     }
@@ -273,16 +300,19 @@ extern "C" int vb_sparse_ffn(const void* wg, const void* wu, const void* wd, int
     src.w2 = wu;
     src.gidx = active;
     src.nsrc = i;
+    float* hid = reinterpret_cast<float*>(wsb + ws.hid);
     if (down_layout == 1) {
         src.zbuf = cnt;
         src.zn = static_cast<int>(h / 64);
+    } else {  // the dense hidden vector starts at zero
+        src.zbuf = reinterpret_cast<int*>(hid);
+        src.zn = static_cast<int>(i);
     }
     int rc = gemv_dispatch_src(wg, src, x, gu, 2 * static_cast<int64_t>(n_active), h, ggml_type, st);
     if (rc != OK) return rc;
     // 2. down
     if (down_layout == 0) {
-        float* hid = reinterpret_cast<float*>(wsb + ws.hid);
-        scatter_act_kernel<<<dim3(static_cast<uint32_t>((i + 255) / 256)), dim3(256), 0, st>>>(
+        scatter_act_kernel<<<dim3(static_cast<uint32_t>((n_active + 255) / 256)), dim3(256), 0, st>>>(
             active, n_active, gu, act_kind, hid, i);
         if ((rc = check_launch("vb_sparse_ffn")) != OK) return rc;
         return gemv_dispatch(wd, hid, y, h, i, ggml_type, st);
