@@ -38,60 +38,53 @@ struct ExpertPtrs {
     const uint8_t* p[MOE_MAX_EXPERTS];
 };
 
-// Route token t: top-k of softmax(clamp(logits, -50, 50)), renormalised.
-// Ties go to the lower expert id.  The clamped logits are read once into
-// registers (one round of loads instead of one per pass).
-__device__ __forceinline__ void route_token(const float* __restrict__ logits, int e_n, int topk, int* idx, float* w) {
-    // Branch-free loads (clamped index, masked after the load): a load under
-    // a branch makes the compiler wait for it on the spot, one latency each.
-    float lg[MOE_MAX_EXPERTS];
+// Route one token with one wave, lane e = expert e (e_n <= 64): top-k of
+// softmax(clamp(logits, -50, 50)), renormalised; ties go to the lower expert
+// id.  Max and sum are xor butterflies (every lane ends with the same bits:
+// each step adds the same two values, a + b == b + a); the top k come out
+// one per round of a butterfly argmax over (p desc, id asc), a total order,
+// so every lane agrees on the winner.  Lanes k < topk write slot k.
+// The weight sum runs in rank order.
+__device__ __forceinline__ void route_token_wave(const float* __restrict__ logits, int e_n, int topk,
+                                                 int32_t* __restrict__ out_idx, float* __restrict__ out_w,
+                                                 int* __restrict__ sexp) {
+    const int lane = threadIdx.x & 63;
+    const bool live = lane < e_n;
+    float z = logits[live ? lane : e_n - 1];  // clamped index: the load stays outside any branch
+    z = live ? fminf(fmaxf(z, -50.f), 50.f) : -INFINITY;
+    float mx = z;
 #pragma unroll
-    for (int e = 0; e < MOE_MAX_EXPERTS; e++) lg[e] = logits[e < e_n ? e : e_n - 1];
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    const float ex = live ? __expf(z - mx) : 0.f;
+    float den = ex;
 #pragma unroll
-    for (int e = 0; e < MOE_MAX_EXPERTS; e++) lg[e] = e < e_n ? fminf(fmaxf(lg[e], -50.f), 50.f) : -INFINITY;
-    float mx = -INFINITY;
+    for (int off = 32; off >= 1; off >>= 1) den += __shfl_xor(den, off);
+    float p = live ? ex / den : -1.f;  // absent experts rank below every live one
+    float s = 0.f, myw = 0.f;
+    int myi = -1;
+    for (int k = 0; k < topk; k++) {
+        float bp = p;
+        int bi = lane;
 #pragma unroll
-    for (int e = 0; e < MOE_MAX_EXPERTS; e++)
-        if (e < e_n) mx = fmaxf(mx, lg[e]);
-    float denom = 0.f;
-#pragma unroll
-    for (int e = 0; e < MOE_MAX_EXPERTS; e++)
-        if (e < e_n) denom += __expf(lg[e] - mx);
-    // top-k kept in descending order in fixed-size arrays (static indices,
-    // registers): inserting p puts it after every weight >= p, so ties keep
-    // the lower expert id first; the smallest weight drops out.
-    float tw[MOE_MAX_TOPK];
-    int ti[MOE_MAX_TOPK];
-#pragma unroll
-    for (int k = 0; k < MOE_MAX_TOPK; k++) {
-        tw[k] = -1.f;
-        ti[k] = -1;
-    }
-#pragma unroll
-    for (int e = 0; e < MOE_MAX_EXPERTS; e++) {
-        if (e < e_n) {
-            const float p = __expf(lg[e] - mx) / denom;
-#pragma unroll
-            for (int j = MOE_MAX_TOPK - 1; j >= 0; j--) {
-                if (j < topk && p > tw[j]) {
-                    const bool here = j == 0 || !(p > tw[j > 0 ? j - 1 : 0]);
-                    tw[j] = here ? p : tw[j > 0 ? j - 1 : 0];
-                    ti[j] = here ? e : ti[j > 0 ? j - 1 : 0];
-                }
-            }
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float op = __shfl_xor(bp, off);
+            const int oi = __shfl_xor(bi, off);
+            const bool take = op > bp || (op == bp && oi < bi);
+            bp = take ? op : bp;
+            bi = take ? oi : bi;
         }
+        s += bp;
+        if (lane == k) {
+            myw = bp;
+            myi = bi;
+        }
+        if (lane == bi) p = -2.f;  // taken
     }
-    float s = 0.f;
-#pragma unroll
-    for (int k = 0; k < MOE_MAX_TOPK; k++)
-        if (k < topk) s += tw[k];
     s = s < 1e-12f ? 1.f : s;
-#pragma unroll
-    for (int k = 0; k < MOE_MAX_TOPK; k++) {
-        if (k < topk) {
-            idx[k] = ti[k];
-            w[k] = tw[k] / s;
-        }
+    if (lane < topk) {
+        out_idx[lane] = myi;
+        out_w[lane] = myw / s;
+        if (sexp) sexp[lane] = myi;
     }
 }
 
@@ -224,7 +217,7 @@ __global__ void __launch_bounds__(256) moe_down_kernel(ExpertPtrs wd, const floa
 // the other blocks round x to fp16 (xh) -- the MFMA path rounds its
 // activations to fp16 anyway, and fp16 halves the activation traffic of the
 // expert kernels.
-constexpr int PREP_THREADS = 256;
+constexpr int PREP_THREADS = 1024;
 
 __global__ void __launch_bounds__(PREP_THREADS) moe_prep_kernel(
         const float* __restrict__ x, const float* __restrict__ logits, int t_n, int e_n, int topk, int64_t nx,
@@ -244,19 +237,10 @@ __global__ void __launch_bounds__(PREP_THREADS) moe_prep_kernel(
     __shared__ int sexp[MOE_MAX_SLOTS];
     __shared__ int scnt[MOE_MAX_EXPERTS + 1];
     const int nslots = t_n * topk;
-    for (int t = threadIdx.x; t < t_n; t += PREP_THREADS) {
-        int idx[MOE_MAX_TOPK];
-        float w[MOE_MAX_TOPK];
-        route_token(logits + static_cast<int64_t>(t) * e_n, e_n, topk, idx, w);
-#pragma unroll
-        for (int k = 0; k < MOE_MAX_TOPK; k++) {
-            if (k < topk) {
-                ridx[t * topk + k] = idx[k];
-                rw[t * topk + k] = w[k];
-                sexp[t * topk + k] = idx[k];
-            }
-        }
-    }
+    // one wave per token
+    for (int t = static_cast<int>(threadIdx.x >> 6); t < t_n; t += PREP_THREADS / 64)
+        route_token_wave(logits + static_cast<int64_t>(t) * e_n, e_n, topk, ridx + t * topk, rw + t * topk,
+                         sexp + t * topk);
     __syncthreads();
     // counts per expert, then exclusive offsets (slots with no expert -- NaN
     // logits -- are in no list)
@@ -528,18 +512,10 @@ namespace vb {
 namespace {
 __global__ void __launch_bounds__(256) moe_route_kernel(const float* __restrict__ logits, int t_n, int e_n, int topk,
                                                         int32_t* __restrict__ out_idx, float* __restrict__ out_w) {
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    const int t = static_cast<int>(blockIdx.x) * 4 + static_cast<int>(threadIdx.x >> 6);  // one wave per token
     if (t >= t_n) return;
-    int idx[MOE_MAX_TOPK];
-    float w[MOE_MAX_TOPK];
-    route_token(logits + static_cast<int64_t>(t) * e_n, e_n, topk, idx, w);
-#pragma unroll
-    for (int k = 0; k < MOE_MAX_TOPK; k++) {
-        if (k < topk) {
-            out_idx[t * topk + k] = idx[k];
-            out_w[t * topk + k] = w[k];
-        }
-    }
+    route_token_wave(logits + static_cast<int64_t>(t) * e_n, e_n, topk, out_idx + t * topk, out_w + t * topk,
+                     nullptr);
 }
 }  // namespace
 }  // namespace vb
@@ -552,7 +528,7 @@ extern "C" int vb_moe_route(const float* router_logits, int32_t n_tokens, int32_
         return E_INVAL;
     }
     if (n_tokens == 0) return OK;
-    moe_route_kernel<<<dim3(static_cast<uint32_t>((n_tokens + 255) / 256)), dim3(256), 0, as_stream(stream)>>>(
+    moe_route_kernel<<<dim3(static_cast<uint32_t>((n_tokens + 3) / 4)), dim3(256), 0, as_stream(stream)>>>(
         router_logits, n_tokens, n_exp, topk, out_idx, out_w);
     return check_launch("vb_moe_route");
 }
