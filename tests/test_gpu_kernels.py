@@ -123,16 +123,21 @@ def test_gemv_q4k_mfma_launch_shapes(q4k_mfma_path, monkeypatch, cfg):
 
 
 @pytest.mark.parametrize("cfg", ["8,1", "8,3", "16,2", "4,9", "8,7"])
-def test_gemv_dot_launch_shapes(monkeypatch, cfg):
-    """v_dot4 kernel launch overrides (rows per wave, ring depths 2 / 4 / 8)."""
+@pytest.mark.parametrize("ring", ["", "1", "2", "3", "4"])
+def test_gemv_dot_launch_shapes(monkeypatch, cfg, ring):
+    """v_dot4 kernel launch overrides: rows per wave x ring depth (1-4; rows
+    not a multiple of the depth take padding steps), one k-slice (k = 4096)
+    and four (k = 14336)."""
     monkeypatch.setenv("VB_GEMV_CFG", cfg)
+    if ring:
+        monkeypatch.setenv("VB_GEMV_RING", ring)
     for qtype in QTYPES:
-        rows, k = 333, 4096
-        qt = QTensor.quantize(rand_weights(rows, k, 13), qtype)
-        x = np.random.default_rng(14).standard_normal(k).astype(np.float32)
-        y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy()
-        want = O.gemv(qt.to_numpy_bytes(), x, rows, k, qtype)
-        assert O.rel_l2(y, want) <= GEMV_TOL, (cfg, qtype)
+        for rows, k in ((333, 4096), (70, 14336)):
+            qt = QTensor.quantize(rand_weights(rows, k, 13), qtype)
+            x = np.random.default_rng(14).standard_normal(k).astype(np.float32)
+            y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy()
+            want = O.gemv(qt.to_numpy_bytes(), x, rows, k, qtype)
+            assert O.rel_l2(y, want) <= GEMV_TOL, (cfg, ring, qtype, rows, k)
 
 
 def test_gemv_zero_rows_and_errors():

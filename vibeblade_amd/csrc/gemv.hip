@@ -533,13 +533,16 @@ struct GemvShape {
 
 constexpr int kNumCUs = 256;
 
-// Ring depth for rpg rows per wave: every row in flight when rpg <= 8 (4 for
-// Q6_K / Q8_0, whose units take 14-17 VGPRs), else a ring of 4.
+// Ring depth for rpg rows per wave (sweeps on MI355X).  A ring of 2 keeps
+// each wave's requests spread over the weight stream: when the last bytes
+// arrive, a wave has one row left to compute, not all of them (with every
+// row in flight at once, 14336 x 4096 Q4_K ran 9.6 us against 8.5-8.8 us).
+// One row: no ring.  Q6_K units (14-17 VGPRs) and long row lists: 4.
 template <int TYPE>
 int ring_depth(int rpg) {
-    if (rpg <= 2) return 2;
-    if (rpg <= 4 || TYPE != TYPE_Q4_K) return 4;
-    return rpg <= 8 ? 8 : 4;
+    if (rpg <= 1) return 1;
+    if (TYPE == TYPE_Q6_K || rpg > 8) return rpg <= 2 ? 2 : 4;
+    return 2;
 }
 
 template <int TYPE>
@@ -547,12 +550,13 @@ int gemv_max_threads_host(int depth) { return depth <= max_d16<TYPE>() ? 1024 : 
 
 // Launch geometry.  k-slices: wpr = ceil(units / 64) waves per row, upw the
 // units per slice rounded up to a multiple of 4.  Rows (rules from sweeps on
-// MI355X, 256 CUs): single-slice rows run in 8-wave workgroups with up to 4
-// rows per wave and up to 2 workgroups per CU, every row in flight at once
-// (e.g. 14336 rows: 4 rows per wave, 448 workgroups); more rows than that
-// stream through one workgroup per CU (Q6_K lm_head, 128256 rows: 63 rows per
-// wave).  Multi-slice rows (k > 4096) use 16-wave workgroups with a ring of
-// 4.  VB_GEMV_CFG="wpg,rpg" overrides (tuning sweeps).
+// MI355X, 256 CUs): single-slice rows run in 8-wave workgroups.  Q4_K with
+// 3..8 rows per wave at one workgroup per CU takes that (14336 rows: 7 rows
+// per wave, 256 workgroups); otherwise up to 4 rows per wave at two
+// workgroups per CU, and beyond that one workgroup per CU again (Q6_K
+// lm_head, 128256 rows: 63 rows per wave).  Multi-slice rows (k > 4096) use
+// 16-wave workgroups.  VB_GEMV_CFG="wpg,rpg" and VB_GEMV_RING=d override
+// (tuning sweeps).
 template <int TYPE>
 GemvShape gemv_shape(int64_t n, int units) {
     GemvShape s;
@@ -564,7 +568,10 @@ GemvShape gemv_shape(int64_t n, int units) {
         s.wpg = 8;
         const int64_t per2 = (n + 2 * kNumCUs * 8 - 1) / (2 * kNumCUs * 8);
         const int64_t per1 = (n + kNumCUs * 8 - 1) / (kNumCUs * 8);
-        s.rpg = static_cast<int>(per2 <= 4 ? per2 : per1);
+        if (TYPE == TYPE_Q4_K && per1 >= 3 && per1 <= 8)
+            s.rpg = static_cast<int>(per1);
+        else
+            s.rpg = static_cast<int>(per2 <= 4 ? per2 : per1);
     } else {
         s.wpg = s.wpr <= 4 ? 16 / s.wpr * s.wpr : s.wpr;
         if (s.wpg > 16) s.wpg = s.wpr;  // > 4096 * 16 elements: one row group per workgroup
@@ -574,18 +581,25 @@ GemvShape gemv_shape(int64_t n, int units) {
     if (s.rpg < 1) s.rpg = 1;
     const int64_t max_rpg = kMaxRedFloats / (static_cast<int64_t>(s.wpg / s.wpr) * s.wpr);
     if (s.rpg > max_rpg) s.rpg = static_cast<int>(max_rpg);
-    if (64 * s.wpg > gemv_max_threads_host<TYPE>(ring_depth<TYPE>(s.rpg))) s.wpg = 8 / s.wpr * s.wpr;
+    int ring = 0;  // ring-depth override
+    if (const char* rd = std::getenv("VB_GEMV_RING")) {
+        const int d = std::atoi(rd);
+        if (d >= 1 && d <= 4) ring = d;
+    }
+    auto depth_of = [&](int rpg) { return ring ? ring : ring_depth<TYPE>(rpg); };
+    // the block size must fit the launch bounds of the kernel of that depth
+    if (64 * s.wpg > gemv_max_threads_host<TYPE>(depth_of(s.rpg))) s.wpg = 8 / s.wpr * s.wpr;
     if (s.wpg < s.wpr) s.wpg = s.wpr;
     if (const char* cfg = std::getenv("VB_GEMV_CFG")) {
         int a = 0, b = 0;
         if (std::sscanf(cfg, "%d,%d", &a, &b) == 2 && a >= 1 && a <= 16 && b >= 1 && a % s.wpr == 0 &&
             static_cast<int64_t>(a / s.wpr) * b * s.wpr <= kMaxRedFloats &&
-            64 * a <= gemv_max_threads_host<TYPE>(ring_depth<TYPE>(b))) {
+            64 * a <= gemv_max_threads_host<TYPE>(depth_of(b))) {
             s.wpg = a;
             s.rpg = b;
         }
     }
-    s.depth = ring_depth<TYPE>(s.rpg);
+    s.depth = depth_of(s.rpg);
     const int64_t rows_wg = static_cast<int64_t>(s.wpg / s.wpr) * s.rpg;
     s.grid = (n + rows_wg - 1) / rows_wg;
     s.lds = static_cast<size_t>(s.slots) * XQ_QUADS * sizeof(uint4) + rows_wg * s.wpr * sizeof(float);
@@ -595,6 +609,11 @@ GemvShape gemv_shape(int64_t n, int units) {
 template <int TYPE, int D>
 int launch_gemv_d(const GemvShape& s, const void* w, const RowSrc& src, const float* x, float* y, int64_t n,
                   int64_t rb, hipStream_t st) {
+    if (64 * s.wpg > gemv_max_threads<TYPE, D>()) {  // never launch past the kernel's launch bounds
+        set_error("vb_gemv: %d threads exceed the %d of the depth-%d kernel", 64 * s.wpg,
+                  gemv_max_threads<TYPE, D>(), D);
+        return E_INVAL;
+    }
     const dim3 g(static_cast<uint32_t>(s.grid)), b(64 * s.wpg);
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     const uint8_t* w2 = static_cast<const uint8_t*>(src.w2);
@@ -618,11 +637,10 @@ int launch_gemv_q(const void* w, const RowSrc& src, const float* x, float* y, in
         return E_UNSUPPORTED;
     }
     switch (s.depth) {
+    case 1: return launch_gemv_d<TYPE, 1>(s, w, src, x, y, n, rb, st);
     case 2: return launch_gemv_d<TYPE, 2>(s, w, src, x, y, n, rb, st);
-    case 4: return launch_gemv_d<TYPE, 4>(s, w, src, x, y, n, rb, st);
-    default:
-        if constexpr (TYPE == TYPE_Q4_K) return launch_gemv_d<TYPE, 8>(s, w, src, x, y, n, rb, st);
-        return launch_gemv_d<TYPE, 4>(s, w, src, x, y, n, rb, st);
+    case 3: return launch_gemv_d<TYPE, 3>(s, w, src, x, y, n, rb, st);
+    default: return launch_gemv_d<TYPE, 4>(s, w, src, x, y, n, rb, st);
     }
 }
 
