@@ -49,20 +49,10 @@ constexpr int X_F32 = 0;
 constexpr int X_F16 = 1;
 constexpr uint32_t X_NONE = 0x80000000u;   // lane offset of an absent activation row (reads zeros)
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-// Buffer loads: a wave-uniform resource (base, size) plus a 32-bit per-lane
-// offset and a uniform offset; no 64-bit address arithmetic per lane, and
-// offsets past the resource's size read zeros.  Resource word 3 = 0x00020000
-// (raw untyped access on gfx9).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
-                                             0x00020000);
-}
-
-__device__ __forceinline__ u32x4 buf_ld128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voff), static_cast<int>(soff), 0);
-}
+// buffer-load helpers shared with the GEMV (vb_common.hpp)
+using vb::u32x4;
+using vb::make_rsrc;
+using vb::buf_ld128;
 
 // d * sc and -dmin * m of sub-blocks 2g, 2g+1 as fp16 splats, for a g that
 // varies across the wave (get_scale_min_k4, cpp/src/dequant.cpp:258-266):

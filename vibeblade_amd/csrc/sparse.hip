@@ -16,10 +16,9 @@
 //        super-block holds an active column at 10 % density, so all of W_d
 //        is read;
 //      layout 1 (neuron-major D = W_d^T, i rows x h, Q4_K): only the |S|
-//        rows of D are read: y = sum_r act_r * D[S_r, :].  Workgroup (u, rs)
-//        owns output unit u (64 columns) and every RS-th active row; row
-//        partials meet in LDS, the RS partials of a unit are summed in fixed
-//        order by the last workgroup to finish it (deterministic, one launch).
+//        rows of D are read: y = sum_r act_r * D[S_r, :].  Workgroup u owns
+//        output unit u (64 columns) over every active row; row partials meet
+//        in LDS and are added in fixed order (deterministic, one launch).
 #include "mfma_q4k.hpp"
 #include "vb_internal.hpp"
 #include "../../include/vbhip.h"
@@ -49,19 +48,26 @@ __global__ void __launch_bounds__(256) scatter_act_kernel(const int32_t* __restr
     if (o >= 0 && o < i_dim) hid[o] = act_pair(g.x, g.y, kind);
 }
 
-constexpr int DOWN_RS = 4;     // workgroups per output unit
-constexpr int DOWN_BATCH = 6;  // rows per thread and load batch
+constexpr int DOWN_THREADS = 1024;
+constexpr int DOWN_RG = DOWN_THREADS / 4;  // row groups per workgroup
+constexpr int DOWN_BATCH = 6;              // rows per thread and load batch
 
-// layout 1, Q4_K: see the header comment.  Thread t = 4*rg + p handles row
-// group rg and quarter p of the unit (16 of its 64 elements: quarter p < 2 =
-// low nibbles of qs bytes 16p.., p >= 2 = high nibbles of bytes 16(p-2)..).
-__global__ void __launch_bounds__(256) down_axpy_q4k_kernel(
+// layout 1, Q4_K: workgroup u owns output unit u (64 columns: chunk u % 4 of
+// super-block u / 4 of every row of D) over all active rows, so it writes its
+// 64 outputs itself: no partial sums cross workgroups.  Thread t = 4 rg + p
+// takes quarter p of the unit (16 of its 64 columns: p < 2 = low nibbles of
+// qs bytes 16p .. +16, sub-block 2c; p >= 2 = high nibbles of bytes
+// 16(p-2) .., sub-block 2c+1) of active rows rg, rg + DOWN_RG, ...  Rows go
+// in batches of DOWN_BATCH per thread with every load of a batch issued
+// before any use (indices and activations, then the weight blocks): two
+// memory latencies per batch.  Partial sums meet in LDS and are added in a
+// fixed order (deterministic).
+__global__ void __launch_bounds__(DOWN_THREADS) down_rows_q4k_kernel(
     const uint8_t* __restrict__ d, int64_t rb, int64_t i_dim, const int32_t* __restrict__ active,
-    int n_active, const float* __restrict__ gu, int kind, float* __restrict__ partial,
-    int* __restrict__ cnt, float* __restrict__ y, int64_t h_dim) {
-    __shared__ float red[64][65];
-    __shared__ int last;
-    const int u = blockIdx.x, rs = blockIdx.y;
+    int n_active, const float* __restrict__ gu, int kind, float* __restrict__ y) {
+    __shared__ float red[DOWN_RG][65];
+    __shared__ float red2[DOWN_THREADS / 64][64];
+    const int u = blockIdx.x;
     const int t = threadIdx.x, rg = t >> 2, p = t & 3;
     const int sb = u >> 2, c = u & 3;
     const int jsub = 2 * c + (p >= 2 ? 1 : 0);
@@ -69,12 +75,8 @@ __global__ void __launch_bounds__(256) down_axpy_q4k_kernel(
 #pragma unroll
     for (int e = 0; e < 16; e++) acc[e] = 0.f;
     float bacc = 0.f;
-    // Rows go in batches of DOWN_BATCH per thread with every load of a batch
-    // issued before any use (indices and activations, then the weight
-    // blocks): two memory latencies per batch instead of two per row.  Rows
-    // past the end load row 0 again and contribute 0.
-    constexpr int STRIDE = DOWN_RS * 64;
-    for (int r0 = rs + DOWN_RS * rg; r0 < n_active; r0 += DOWN_BATCH * STRIDE) {
+    constexpr int STRIDE = DOWN_RG;
+    for (int r0 = rg; r0 < n_active; r0 += DOWN_BATCH * STRIDE) {
         int nr[DOWN_BATCH];
         float2 gv[DOWN_BATCH];
 #pragma unroll
@@ -92,17 +94,18 @@ __global__ void __launch_bounds__(256) down_axpy_q4k_kernel(
             nr[b] = v < 0 ? 0 : (v >= i_dim ? static_cast<int>(i_dim) - 1 : v);
             hid[b] = r0 + b * STRIDE < n_active ? act_pair(gv[b].x, gv[b].y, kind) : 0.f;
         }
-        uint4 hdv[DOWN_BATCH], qv[DOWN_BATCH];
+        // native vector type: arrays of HIP's uint4 struct can land in scratch
+        u32x4 hdv[DOWN_BATCH], qv[DOWN_BATCH];
 #pragma unroll
         for (int b = 0; b < DOWN_BATCH; b++) {
             const uint8_t* blk = d + static_cast<int64_t>(nr[b]) * rb + static_cast<int64_t>(sb) * 144;
-            hdv[b] = *reinterpret_cast<const uint4*>(blk);
-            qv[b] = *reinterpret_cast<const uint4*>(blk + 16 + 32 * c + 16 * (p & 1));
+            hdv[b] = *reinterpret_cast<const u32x4*>(blk);
+            qv[b] = *reinterpret_cast<const u32x4*>(blk + 16 + 32 * c + 16 * (p & 1));
         }
         __builtin_amdgcn_sched_barrier(0);  // all weight loads before the math
 #pragma unroll
         for (int b = 0; b < DOWN_BATCH; b++) {
-            const uint4 hd = hdv[b], q = qv[b];
+            const u32x4 hd = hdv[b], q = qv[b];
             uint8_t s8[12];
             const uint32_t sw[3] = {hd.y, hd.z, hd.w};
 #pragma unroll
@@ -127,22 +130,19 @@ __global__ void __launch_bounds__(256) down_axpy_q4k_kernel(
 #pragma unroll
     for (int e = 0; e < 16; e++) red[rg][16 * p + e] = acc[e] - bacc;
     __syncthreads();
-    if (t < 64) {
-        float s = 0.f;
-        for (int g = 0; g < 64; g++) s += red[g][t];
-        partial[static_cast<int64_t>(rs) * h_dim + 64 * u + t] = s;
-        __threadfence();
+    {  // thread t: column t % 64 over row groups 16 (t / 64) .. +16
+        const int col = t & 63, g0 = (t >> 6) * 16;
+        float sum = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; k++) sum += red[g0 + k][col];
+        red2[t >> 6][col] = sum;
     }
     __syncthreads();
-    if (t == 0) last = (atomicAdd(&cnt[u], 1) == DOWN_RS - 1) ? 1 : 0;
-    __syncthreads();
-    if (last && t < 64) {
-        __threadfence();
-        float s = 0.f;
-        for (int j = 0; j < DOWN_RS; j++)
-            s += __hip_atomic_load(&partial[static_cast<int64_t>(j) * h_dim + 64 * u + t], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-        y[64 * u + t] = s;
+    if (t < 64) {
+        float sum = 0.f;
+#pragma unroll
+        for (int k = 0; k < DOWN_THREADS / 64; k++) sum += red2[k][t];
+        y[64 * static_cast<int64_t>(u) + t] = sum;
     }
 }
 
@@ -231,7 +231,7 @@ __global__ void __launch_bounds__(1024) topk_kernel(const float* __restrict__ v,
 size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
 
 struct SparseWs {
-    size_t gu, hid, partial, cnt, total;
+    size_t gu, hid, total;
 };
 
 SparseWs sparse_ws(int64_t h, int64_t i, int32_t n_active, int32_t layout) {
@@ -239,10 +239,6 @@ SparseWs sparse_ws(int64_t h, int64_t i, int32_t n_active, int32_t layout) {
     w.gu = 0;
     w.hid = align256(static_cast<size_t>(2 * (n_active > 0 ? n_active : 1)) * sizeof(float));
     size_t off = w.hid + (layout == 0 ? align256(static_cast<size_t>(i) * sizeof(float)) : 0);
-    w.partial = off;
-    off += layout == 1 ? align256(static_cast<size_t>(DOWN_RS) * h * sizeof(float)) : 0;
-    w.cnt = off;
-    off += layout == 1 ? align256(static_cast<size_t>(h / 64) * sizeof(int)) : 0;
     w.total = off;
     return w;
 }
@@ -289,22 +285,18 @@ extern "C" int vb_sparse_ffn(const void* wg, const void* wu, const void* wd, int
     }
     uint8_t* wsb = static_cast<uint8_t*>(workspace);
     float* gu = reinterpret_cast<float*>(wsb + ws.gu);
-    int* cnt = reinterpret_cast<int*>(wsb + ws.cnt);
 
     if (n_active == 0) {  // no active neuron: y = 0
         fill_zero_kernel<<<dim3(static_cast<uint32_t>((h + 255) / 256)), dim3(256), 0, st>>>(y, h);
         return check_launch("vb_sparse_ffn");
     }
-    // 1. gate/up on the active rows (and clear the down counters)
+    // 1. gate/up on the active rows
     RowSrc src;
     src.w2 = wu;
     src.gidx = active;
     src.nsrc = i;
     float* hid = reinterpret_cast<float*>(wsb + ws.hid);
-    if (down_layout == 1) {
-        src.zbuf = cnt;
-        src.zn = static_cast<int>(h / 64);
-    } else {  // the dense hidden vector starts at zero
+    if (down_layout == 0) {  // the dense hidden vector starts at zero
         src.zbuf = reinterpret_cast<int*>(hid);
         src.zn = static_cast<int>(i);
     }
@@ -317,10 +309,8 @@ extern "C" int vb_sparse_ffn(const void* wg, const void* wu, const void* wd, int
         if ((rc = check_launch("vb_sparse_ffn")) != OK) return rc;
         return gemv_dispatch(wd, hid, y, h, i, ggml_type, st);
     }
-    float* partial = reinterpret_cast<float*>(wsb + ws.partial);
-    down_axpy_q4k_kernel<<<dim3(static_cast<uint32_t>(h / 64), DOWN_RS), dim3(256), 0, st>>>(
-        static_cast<const uint8_t*>(wd), row_bytes(TYPE_Q4_K, h), i, active, n_active, gu, act_kind, partial,
-        cnt, y, h);
+    down_rows_q4k_kernel<<<dim3(static_cast<uint32_t>(h / 64)), dim3(DOWN_THREADS), 0, st>>>(
+        static_cast<const uint8_t*>(wd), row_bytes(TYPE_Q4_K, h), i, active, n_active, gu, act_kind, y);
     return check_launch("vb_sparse_ffn");
 }
 

@@ -69,6 +69,22 @@ __device__ __forceinline__ float f16hi(uint32_t w) {
     return __half2float(__ushort_as_half(static_cast<unsigned short>(w >> 16)));
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer loads: a wave-uniform resource (base, size) plus a 32-bit per-lane
+// offset and a uniform offset; no 64-bit address arithmetic per lane.
+// Resource word 3 = 0x00020000 (raw untyped access on gfx9).  A load that
+// reaches past the resource's size reads zeros; callers keep every load
+// inside the tensor anyway.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                             0x00020000);
+}
+
+__device__ __forceinline__ u32x4 buf_ld128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voff), static_cast<int>(soff), 0);
+}
+
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
 }
