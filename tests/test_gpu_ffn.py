@@ -114,6 +114,24 @@ def test_sparse_layouts_agree():
     assert O.rel_l2(y0, y1) <= 0.2
 
 
+@pytest.mark.parametrize("h,i,fused_env,one", [(4096, 4096, "0", False), (8192, 2048, None, False),
+                                               (4096, 512, None, True)])
+def test_sparse_neuron_major_paths(monkeypatch, h, i, fused_env, one):
+    """Layout 1 on each of its paths: the fused gate/up/down kernel (h <= 4096),
+    the gathered GEMV + down-rows launches (forced with VB_SPARSE_FUSED=0, and
+    for h > 4096), and a single active neuron on the fused path."""
+    if fused_env is not None:
+        monkeypatch.setenv("VB_SPARSE_FUSED", fused_env)
+    gq, uq, dq, gd, ud, dd = ffn_weights(h, i, Q4K, 17, DOWN_NEURON_MAJOR)
+    rng = np.random.default_rng(8)
+    s = np.array([137], np.int32) if one else np.flatnonzero(rng.random(i) < 0.1).astype(np.int32)
+    x = rng.standard_normal(h).astype(np.float32)
+    for act in (ACT_SILU, ACT_RELU2):
+        y = sparse_ffn(gq, uq, dq, torch.from_numpy(x), torch.from_numpy(s), act, DOWN_NEURON_MAJOR).cpu().numpy()
+        want = O.sparse_ffn(gd, ud, dd, x, s, act)[0]
+        assert O.rel_l2(y, want) <= 1e-3
+
+
 def test_sparse_repeatable():
     """Layout 1 sums partials in a fixed order: identical bits run to run."""
     h, i = 4096, 4096

@@ -1,0 +1,347 @@
+// Device building blocks of the dequant-fused M = 1 kernels (gemv.hip, and
+// the fused sparse FFN in sparse.hip): the activation encoding shared by a
+// workgroup through LDS and the per-type unit loads and integer dot products.
+//
+// Activation encoding.  The workgroup encodes x once into LDS: the 64
+// activations of every unit are split into runs (32 elements for Q4_K / Q8_0,
+// 16 for Q6_K: the weight sub-block size) and every run becomes 16-bit fixed
+// point with a per-run fp32 scale:  x ~= s * x16,  |x16| <= 32512,  x16 = 256*xh + xl with
+// xh, xl signed bytes.  A run's dot product with the integer weight codes q
+// is then  s * (256 * sdot4(q, xh) + sdot4(q, xl))  -- exact integer
+// arithmetic on v_dot4_i32_i8, about one VALU op per weight element.  The
+// encoding error is |x - s*x16| <= s/2 = amax/65024 per element, which puts
+// the GEMV rel-L2 error near 1e-5 (the fp32 bound is 1e-3).
+//
+// Unit -> bytes (row of k elements, units_per_row = k/64):
+//   Q4_K  unit u: super-block u/4, chunk c = u%4: header (16 B: d, dmin,
+//         scales) + qs[32c, 32c+32).  Low nibbles = run 0 = sub-block 2c,
+//         high nibbles = run 1 = sub-block 2c+1 (cpp/src/dequant.cpp:278-299).
+//   Q8_0  unit u: blocks 2u, 2u+1 = 68 bytes at 68u (4-byte aligned).
+//   Q6_K  unit u: super-block u/4, c = u%4, h = c/2, l0 = 16*(c%2): the four
+//         16-element runs t = 0..3 at elements 128h + 32t + l0 + [0, 16).
+//         Bytes: ql[64h + l0 + [0,16)], ql[64h + 32 + l0 + [0,16)],
+//         qh[32h + l0 + [0,16)], scales[8h + c%2 + 2t], d.
+#pragma once
+
+#include "vb_common.hpp"
+
+namespace vb {
+namespace gemvc {
+
+constexpr int X16_MAX = 32512;  // 127 * 256: keeps xh within a signed byte
+
+struct XSlice {
+    uint32_t h[16];  // high bytes of x16, 4 per dword, element order
+    uint32_t l[16];  // low bytes (signed), same order
+    float s[4];      // per-run scale
+    float sum[4];    // per-run sum of the fp32 activations
+    int isum[4];     // per-run sum of x16
+};
+
+// ---- per-type unit loaders and dot products -------------------------------
+
+// Q4_K: each of the 4 lanes of a super-block loads one dword of the 16-byte
+// header (d|dmin, scales[0:4], scales[4:8], scales[8:12]) and the quad shares
+// them through DPP broadcasts, instead of 4 lanes fetching the same 16 bytes.
+struct Q4KUnit { uint32_t hw; uint4 qa, qb; };
+struct Q8Unit { uint4 a, b, c, d; uint32_t e; };
+struct Q6KUnit { uint4 la, lb, qh; uint32_t sc; uint32_t d; };
+
+template <int TYPE> struct UnitOf;
+template <> struct UnitOf<TYPE_Q4_K> { using T = Q4KUnit; };
+template <> struct UnitOf<TYPE_Q8_0> { using T = Q8Unit; };
+template <> struct UnitOf<TYPE_Q6_K> { using T = Q6KUnit; };
+
+__device__ __forceinline__ void load_unit(const uint8_t* row, int u, Q4KUnit& v) {
+    const uint8_t* b = row + (u >> 2) * 144;
+    const int c = u & 3;
+    v.hw = ld_b32(b + 4 * c);
+    v.qa = *reinterpret_cast<const uint4*>(b + 16 + 32 * c);
+    v.qb = *reinterpret_cast<const uint4*>(b + 32 + 32 * c);
+}
+
+// Value of v in lane I of this lane's quad (DPP quad_perm [I,I,I,I]).
+template <int I>
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), I * 0x55, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ void load_unit(const uint8_t* row, int u, Q8Unit& v) {
+    const uint8_t* b = row + u * 68;
+    v.a = ld_b128_a4(b);
+    v.b = ld_b128_a4(b + 16);
+    v.c = ld_b128_a4(b + 32);
+    v.d = ld_b128_a4(b + 48);
+    v.e = ld_b32(b + 64);
+}
+
+__device__ __forceinline__ void load_unit(const uint8_t* row, int u, Q6KUnit& v) {
+    const uint8_t* b = row + (u >> 2) * 210;
+    const int c = u & 3, h = c >> 1, l0 = 16 * (c & 1);
+    v.la = ld_b128_a2(b + 64 * h + l0);
+    v.lb = ld_b128_a2(b + 64 * h + 32 + l0);
+    v.qh = ld_b128_a2(b + 128 + 32 * h + l0);
+    const uint8_t* s = b + 192 + 8 * h + (c & 1);
+    v.sc = static_cast<uint32_t>(s[0]) | (static_cast<uint32_t>(s[2]) << 8) |
+           (static_cast<uint32_t>(s[4]) << 16) | (static_cast<uint32_t>(s[6]) << 24);
+    v.d = *reinterpret_cast<const uint16_t*>(b + 208);
+}
+
+__device__ __forceinline__ int run_dot(const uint32_t* q, const uint32_t* xh, const uint32_t* xl, int n) {
+    int ah = 0, al = 0;
+#pragma unroll
+    for (int i = 0; i < n; i++) {
+        ah = sdot4(q[i], xh[i], ah);
+        al = sdot4(q[i], xl[i], al);
+    }
+    return ah * 256 + al;
+}
+
+// Lane-constant selectors of the 6-bit scale / min of sub-blocks 2c, 2c+1
+// (c = the lane's chunk; get_scale_min_k4, cpp/src/dequant.cpp:258-266),
+// with sh = 16 (c & 1) and A, B, C = scales[0:4], [4:8], [8:12]:
+//   c < 2:  sc = (A >> sh) & 0x3F3F,  m = (B >> sh) & 0x3F3F
+//   c >= 2: sc = ((C >> sh) & 0x0F0F) | ((A >> (sh + 2)) & 0x3030)
+//           m  = ((C >> (sh + 4)) & 0x0F0F) | ((B >> (sh + 2)) & 0x3030)
+struct Q4KSel {
+    uint32_t sh, sh2, shm, m1, m2;
+    bool hi;
+};
+
+template <int TYPE>
+__device__ __forceinline__ auto make_unit_sel(int u) {
+    if constexpr (TYPE == TYPE_Q4_K) {
+        const int c = u & 3;
+        Q4KSel q;
+        q.hi = c >= 2;
+        q.sh = 16u * static_cast<uint32_t>(c & 1);
+        q.sh2 = q.sh + 2u;
+        q.shm = q.hi ? q.sh + 4u : q.sh;
+        q.m1 = q.hi ? 0x0F0Fu : 0x3F3Fu;
+        q.m2 = q.hi ? 0x3030u : 0u;
+        return q;
+    } else {
+        return u;
+    }
+}
+
+// High nibbles enter the dot products as (q ^ 0x80) & 0xF0 = 16 (q - 8), a
+// signed byte, with one v_bitop3 per 4 bytes instead of a shift and a mask:
+//   sum x16 q = (sum x16 16 (q - 8) + 128 isum) / 16   (exact; isum = sum x16)
+__device__ __forceinline__ float unit_dot(const Q4KUnit& v, const XSlice& xs, const Q4KSel& q) {
+    const uint32_t qd[8] = {v.qa.x, v.qa.y, v.qa.z, v.qa.w, v.qb.x, v.qb.y, v.qb.z, v.qb.w};
+    uint32_t lo[8], hi[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        lo[i] = qd[i] & 0x0F0F0F0Fu;
+        hi[i] = (qd[i] ^ 0x80808080u) & 0xF0F0F0F0u;
+    }
+    const int s0 = run_dot(lo, xs.h, xs.l, 8);
+    const int s1 = (run_dot(hi, xs.h + 8, xs.l + 8, 8) + 128 * xs.isum[1]) >> 4;
+    // The quad's lanes hold units c = 0..3 of the same super-block and share
+    // its 16-byte header through DPP broadcasts.
+    const uint32_t hx = quad_bcast<0>(v.hw);
+    const uint32_t A = quad_bcast<1>(v.hw), B = quad_bcast<2>(v.hw), C = quad_bcast<3>(v.hw);
+    const uint32_t SC = (((q.hi ? C : A) >> q.sh) & q.m1) | ((A >> q.sh2) & q.m2);
+    const uint32_t M = (((q.hi ? C : B) >> q.shm) & q.m1) | ((B >> q.sh2) & q.m2);
+    const float d = f16lo(hx), dmin = f16hi(hx);
+    const float sc0 = static_cast<float>(SC & 0xFFu), sc1 = static_cast<float>((SC >> 8) & 0xFFu);
+    const float m0 = static_cast<float>(M & 0xFFu), m1 = static_cast<float>((M >> 8) & 0xFFu);
+    const float dot = sc0 * (xs.s[0] * static_cast<float>(s0)) + sc1 * (xs.s[1] * static_cast<float>(s1));
+    const float mins = m0 * xs.sum[0] + m1 * xs.sum[1];
+    return d * dot - dmin * mins;
+}
+
+__device__ __forceinline__ float unit_dot(const Q8Unit& v, const XSlice& xs, int) {
+    const uint32_t w[17] = {v.a.x, v.a.y, v.a.z, v.a.w, v.b.x, v.b.y, v.b.z, v.b.w,
+                            v.c.x, v.c.y, v.c.z, v.c.w, v.d.x, v.d.y, v.d.z, v.d.w, v.e};
+    uint32_t q0[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) q0[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2);
+    const int s0 = run_dot(q0, xs.h, xs.l, 8);
+    const int s1 = run_dot(w + 9, xs.h + 8, xs.l + 8, 8);
+    const float d0 = f16lo(w[0]), d1 = f16hi(w[8]);
+    return d0 * (xs.s[0] * static_cast<float>(s0)) + d1 * (xs.s[1] * static_cast<float>(s1));
+}
+
+__device__ __forceinline__ float unit_dot(const Q6KUnit& v, const XSlice& xs, int) {
+    const uint32_t la[4] = {v.la.x, v.la.y, v.la.z, v.la.w};
+    const uint32_t lb[4] = {v.lb.x, v.lb.y, v.lb.z, v.lb.w};
+    const uint32_t qh[4] = {v.qh.x, v.qh.y, v.qh.z, v.qh.w};
+    float acc = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        uint32_t q[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t src = (t & 1) ? lb[i] : la[i];
+            const uint32_t lo = (src >> (4 * (t >> 1))) & 0x0F0F0F0Fu;
+            const uint32_t hb = (qh[i] >> (2 * t)) & 0x03030303u;
+            q[i] = lo | (hb << 4);  // q6 + 32, in 0..63
+        }
+        const int s = run_dot(q, xs.h + 4 * t, xs.l + 4 * t, 4) - 32 * xs.isum[t];
+        const float sc = static_cast<float>(static_cast<int8_t>((v.sc >> (8 * t)) & 0xFFu));
+        acc += sc * (xs.s[t] * static_cast<float>(s));
+    }
+    return f16lo(v.d) * acc;
+}
+
+// x offset of unit u and the stride between its four 16-element segments.
+template <int TYPE>
+__device__ __forceinline__ int64_t unit_x_offset(int u, int& seg_stride) {
+    if constexpr (TYPE == TYPE_Q6_K) {
+        const int c = u & 3;
+        seg_stride = 32;
+        return static_cast<int64_t>(u >> 2) * 256 + 128 * (c >> 1) + 16 * (c & 1);
+    } else {
+        seg_stride = 16;
+        return static_cast<int64_t>(u) * 64;
+    }
+}
+
+// ---- shared activation encoding (LDS) -------------------------------------
+//
+// The encoded slice of unit u lives in LDS as 11 uint4 "quads" at
+// xq[q * slots + u]: quads 0-3 = h[0..15], 4-7 = l[0..15], 8 = s[0..3],
+// 9 = sum[0..3], 10 = isum[0..3].  A wave's lanes read consecutive units, so
+// their ds_read_b128 loads are bank-conflict free.  `slots` (a multiple of 8)
+// covers every unit index a lane may read, idle lanes included; units past
+// the row are encoded as zeros.
+constexpr int XQ_QUADS = 11;
+constexpr int kMaxSlots = 520;      // LDS encoding up to k = 32768 (+ idle lanes)
+constexpr int kMaxRedFloats = 8192;  // per-row partial sums kept in LDS
+
+// All threads of the workgroup encode the activations of every slot: one
+// task = 8 consecutive elements of a unit; the 2 (Q6_K) or 4 tasks of a run
+// sit on adjacent lanes and combine their max / sums with shuffles.  Loading
+// is split from encoding so the caller can put the weight loads in between:
+// loads return in issue order, so x must be requested first or its encode
+// would wait for the weights.
+constexpr int XT_MAX = 2;  // tasks per thread held in registers
+
+struct XTasks {
+    float v[XT_MAX][8];
+};
+
+template <int TYPE>
+__device__ __forceinline__ int64_t task_x_offset(int u, int p) {
+    if constexpr (TYPE == TYPE_Q6_K) {
+        int seg_stride;
+        return unit_x_offset<TYPE>(u, seg_stride) + (p >> 1) * 32 + 8 * (p & 1);
+    } else {
+        return static_cast<int64_t>(u) * 64 + 8 * p;
+    }
+}
+
+// Loads are branch-free (clamped address; the value is masked later, in
+// encode_x_task): a load under a branch makes the compiler's wait-count
+// merge fall back to vmcnt(0), and masking here would wait for the load.
+template <int TYPE>
+__device__ __forceinline__ void load_x_task(const float* __restrict__ x, int units, int task, float* v) {
+    const int u = task >> 3, p = task & 7;
+    const int64_t off = task_x_offset<TYPE>(u < units ? u : units - 1, p);
+    const float4 a = *reinterpret_cast<const float4*>(x + off);
+    const float4 b = *reinterpret_cast<const float4*>(x + off + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+template <int TYPE>
+__device__ __forceinline__ void encode_x_task(int task, int units, int slots, const float* vin, uint4* xq) {
+    constexpr int RUNLEN = TYPE == TYPE_Q6_K ? 16 : 32;
+    constexpr int TPR = RUNLEN / 8;
+    const int u = task >> 3, p = task & 7;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = u < units ? vin[i] : 0.f;
+    float amax = 0.f, sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        amax = fmaxf(amax, fabsf(v[i]));
+        sum += v[i];
+    }
+#pragma unroll
+    for (int m = 1; m < TPR; m <<= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+        sum += __shfl_xor(sum, m, 64);
+    }
+    const float inv = amax > 0.f ? static_cast<float>(X16_MAX) / amax : 0.f;
+    uint32_t ph[2] = {0, 0}, pl[2] = {0, 0};
+    int isum = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        int q = static_cast<int>(rintf(v[i] * inv));
+        q = q > X16_MAX ? X16_MAX : (q < -X16_MAX ? -X16_MAX : q);
+        isum += q;
+        const int lo = ((q + 128) & 255) - 128;
+        const int hi = (q - lo) >> 8;
+        ph[i >> 2] |= static_cast<uint32_t>(hi & 255) << (8 * (i & 3));
+        pl[i >> 2] |= static_cast<uint32_t>(lo & 255) << (8 * (i & 3));
+    }
+#pragma unroll
+    for (int m = 1; m < TPR; m <<= 1) isum += __shfl_xor(isum, m, 64);
+    uint4* base = xq + u;
+    reinterpret_cast<uint2*>(&base[(p >> 1) * slots])[p & 1] = make_uint2(ph[0], ph[1]);
+    reinterpret_cast<uint2*>(&base[(4 + (p >> 1)) * slots])[p & 1] = make_uint2(pl[0], pl[1]);
+    if (p % TPR == 0) {
+        const int r = p / TPR;
+        reinterpret_cast<float*>(&base[8 * slots])[r] = amax / static_cast<float>(X16_MAX);
+        reinterpret_cast<float*>(&base[9 * slots])[r] = sum;
+        reinterpret_cast<int*>(&base[10 * slots])[r] = isum;
+    }
+}
+
+// Register path: at most XT_MAX tasks per thread.  The task count (8 per
+// slot, slots a multiple of 8) and the thread count are multiples of 64, so
+// each wave's shuffles see all 64 lanes active.
+template <int TYPE>
+__device__ __forceinline__ void prefetch_x(const float* __restrict__ x, int units, int slots, XTasks& t) {
+    const int ntasks = slots * 8;
+#pragma unroll
+    for (int i = 0; i < XT_MAX; i++) {
+        const int task = threadIdx.x + i * blockDim.x;
+        load_x_task<TYPE>(x, units, task < ntasks ? task : ntasks - 1, t.v[i]);
+    }
+}
+
+template <int TYPE>
+__device__ __forceinline__ void encode_x_regs(int units, int slots, const XTasks& t, uint4* xq) {
+    const int ntasks = slots * 8;
+#pragma unroll
+    for (int i = 0; i < XT_MAX; i++) {
+        const int task = threadIdx.x + i * blockDim.x;
+        if (task < ntasks) encode_x_task<TYPE>(task, units, slots, t.v[i], xq);
+    }
+}
+
+// Loop path for more tasks than fit in registers.
+template <int TYPE>
+__device__ void encode_x_loop(const float* __restrict__ x, int units, int slots, uint4* xq) {
+    const int ntasks = slots * 8;
+    for (int task = threadIdx.x; task < ntasks; task += blockDim.x) {
+        float v[8];
+        load_x_task<TYPE>(x, units, task, v);
+        encode_x_task<TYPE>(task, units, slots, v, xq);
+    }
+}
+
+__device__ __forceinline__ void read_xslice(const uint4* xq, int slots, int u, XSlice& xs) {
+    const uint4* q = xq + u;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint4 h = q[i * slots], l = q[(4 + i) * slots];
+        xs.h[4 * i] = h.x; xs.h[4 * i + 1] = h.y; xs.h[4 * i + 2] = h.z; xs.h[4 * i + 3] = h.w;
+        xs.l[4 * i] = l.x; xs.l[4 * i + 1] = l.y; xs.l[4 * i + 2] = l.z; xs.l[4 * i + 3] = l.w;
+    }
+    const uint4 s = q[8 * slots], sm = q[9 * slots], is = q[10 * slots];
+    xs.s[0] = __uint_as_float(s.x); xs.s[1] = __uint_as_float(s.y);
+    xs.s[2] = __uint_as_float(s.z); xs.s[3] = __uint_as_float(s.w);
+    xs.sum[0] = __uint_as_float(sm.x); xs.sum[1] = __uint_as_float(sm.y);
+    xs.sum[2] = __uint_as_float(sm.z); xs.sum[3] = __uint_as_float(sm.w);
+    xs.isum[0] = static_cast<int>(is.x); xs.isum[1] = static_cast<int>(is.y);
+    xs.isum[2] = static_cast<int>(is.z); xs.isum[3] = static_cast<int>(is.w);
+}
+
+
+}  // namespace gemvc
+}  // namespace vb

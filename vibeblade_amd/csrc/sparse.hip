@@ -19,6 +19,9 @@
 //        rows of D are read: y = sum_r act_r * D[S_r, :].  Workgroup u owns
 //        output unit u (64 columns) over every active row; row partials meet
 //        in LDS and are added in fixed order (deterministic, one launch).
+#include <cstdlib>
+
+#include "gemv_core.hpp"
 #include "mfma_q4k.hpp"
 #include "vb_internal.hpp"
 #include "../../include/vbhip.h"
@@ -146,6 +149,178 @@ __global__ void __launch_bounds__(DOWN_THREADS) down_rows_q4k_kernel(
     }
 }
 
+// ---- fused neuron-major path (one launch + a small reduction) ----------------
+//
+// For h <= 4096 (a row of h elements is one wave: lane = 64-element unit) the
+// gate/up dot products and the down rows of an active neuron run in one
+// wave: wave w of workgroup b takes neurons r = b * 8 NPW + w + 8 k, k <
+// NPW.  All of its gate, up and D rows are requested at kernel start (their
+// addresses need only the active indices), the workgroup encodes x into LDS
+// as the GEMV does (gemv_core.hpp), then per neuron: g = gate . x and
+// u = up . x with the integer unit dot products, one pair_sum for both,
+// h = act(g, u), and lane u adds h * D[S_r, 64u .. 64u+63] (decoded: d*sc*q -
+// dmin*m) to its 64 partial outputs.  The 8 waves' partials meet in LDS and
+// the workgroup writes one partial y (4096 floats); sparse_reduce_kernel adds
+// the workgroups' partials in a fixed order (deterministic).
+constexpr int FUSED_NPW = 1;  // neurons per wave (VB_SPARSE_NPW=2 selects 2; 1 measured faster: more
+                              // workgroups, less serial work per wave, at twice the partial sums)
+constexpr int FUSED_STRIDE = 4096;        // floats per partial y (h <= 4096)
+constexpr int FUSED_RED_PITCH = 65;       // LDS row pitch of the wave partials
+
+__device__ __forceinline__ float pair_sum(float a0, float a1) {
+    // lane 31: total of a0, lane 63: total of a1 (see gemv.hip)
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(a0), __float_as_int(a1), false, false);
+    float v = __int_as_float(sw[0]) + __int_as_float(sw[1]);
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);  // row_half_mirror
+    v += dpp_f<0x140>(v);  // row_mirror
+    v += dpp_rows_f<0x142, 0xA>(v);  // row_bcast:15 into rows 1, 3
+    return v;
+}
+
+// yp[e] += h * (d * sc_j) * q_e for the 64 elements of a Q4_K unit (e < 32:
+// low nibbles, sub-block 2c; e >= 32: high nibbles, sub-block 2c+1); the
+// min terms h * dmin * m_j go to mb0 / mb1 (subtracted once at the end).
+// Scale selection as in the unit dot product (get_scale_min_k4,
+// cpp/src/dequant.cpp:258-266).
+__device__ __forceinline__ void unit_axpy(const gemvc::Q4KUnit& v, const gemvc::Q4KSel& q, float h, float* yp,
+                                          float& mb0, float& mb1) {
+    using gemvc::quad_bcast;
+    const uint32_t hx = quad_bcast<0>(v.hw);
+    const uint32_t A = quad_bcast<1>(v.hw), B = quad_bcast<2>(v.hw), C = quad_bcast<3>(v.hw);
+    const uint32_t SC = (((q.hi ? C : A) >> q.sh) & q.m1) | ((A >> q.sh2) & q.m2);
+    const uint32_t M = (((q.hi ? C : B) >> q.shm) & q.m1) | ((B >> q.sh2) & q.m2);
+    const float hd = h * f16lo(hx), hm = h * f16hi(hx);
+    const float a0 = hd * static_cast<float>(SC & 0xFFu), a1 = hd * static_cast<float>((SC >> 8) & 0xFFu);
+    mb0 += hm * static_cast<float>(M & 0xFFu);
+    mb1 += hm * static_cast<float>((M >> 8) & 0xFFu);
+    const uint32_t qd[8] = {v.qa.x, v.qa.y, v.qa.z, v.qa.w, v.qb.x, v.qb.y, v.qb.z, v.qb.w};
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint32_t lo = qd[i] & 0x0F0F0F0Fu, hi = (qd[i] >> 4) & 0x0F0F0F0Fu;
+        yp[4 * i + 0] += a0 * static_cast<float>(lo & 0xFFu);
+        yp[4 * i + 1] += a0 * static_cast<float>((lo >> 8) & 0xFFu);
+        yp[4 * i + 2] += a0 * static_cast<float>((lo >> 16) & 0xFFu);
+        yp[4 * i + 3] += a0 * static_cast<float>(lo >> 24);
+        yp[32 + 4 * i + 0] += a1 * static_cast<float>(hi & 0xFFu);
+        yp[32 + 4 * i + 1] += a1 * static_cast<float>((hi >> 8) & 0xFFu);
+        yp[32 + 4 * i + 2] += a1 * static_cast<float>((hi >> 16) & 0xFFu);
+        yp[32 + 4 * i + 3] += a1 * static_cast<float>(hi >> 24);
+    }
+}
+
+template <int NPW>
+__global__ void __launch_bounds__(512) sparse_fused_q4k_kernel(
+    const uint8_t* __restrict__ wg, const uint8_t* __restrict__ wu, const uint8_t* __restrict__ wd, int64_t rb,
+    int64_t i_dim, const float* __restrict__ x, const int32_t* __restrict__ active, int n_active, int kind,
+    float* __restrict__ partial, int units, int slots) {
+    using namespace gemvc;
+    // the x encoding (slots x 11 uint4), later the 8 waves' partials
+    __shared__ uint4 lds[8 * 64 * FUSED_RED_PITCH / 4];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const bool valid = lane < units;
+    // idle lanes load a real unit (discarded); u % 4 == lane % 4 keeps every
+    // quad on one super-block (units is a multiple of 4)
+    const int uc = valid ? lane : units - 4 + (lane & 3);
+    const Q4KSel usel = make_unit_sel<TYPE_Q4_K>(uc);
+    const int rbase = static_cast<int>(blockIdx.x) * (8 * NPW) + wave;
+
+    int nidx[NPW];
+    bool nval[NPW];
+#pragma unroll
+    for (int k = 0; k < NPW; k++) {
+        const int r = rbase + 8 * k;
+        nval[k] = r < n_active;
+        int v = active[nval[k] ? r : 0];
+        v = v < 0 ? 0 : (v >= i_dim ? static_cast<int>(i_dim) - 1 : v);  // never read outside the tensors
+        nidx[k] = __builtin_amdgcn_readfirstlane(v);
+    }
+    // x first, then every weight row of the wave, then the encode (which
+    // waits for x only)
+    XTasks xt;
+    const bool x_in_regs = slots * 8 <= XT_MAX * static_cast<int>(blockDim.x);
+    if (x_in_regs) prefetch_x<TYPE_Q4_K>(x, units, slots, xt);
+    __builtin_amdgcn_sched_barrier(0);
+    Q4KUnit vg[NPW], vu[NPW], vd[NPW];
+#pragma unroll
+    for (int k = 0; k < NPW; k++) {
+        const int64_t off = static_cast<int64_t>(nidx[k]) * rb;
+        load_unit(wg + off, uc, vg[k]);
+        load_unit(wu + off, uc, vu[k]);
+        load_unit(wd + off, uc, vd[k]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (x_in_regs)
+        encode_x_regs<TYPE_Q4_K>(units, slots, xt, lds);
+    else
+        encode_x_loop<TYPE_Q4_K>(x, units, slots, lds);
+    __syncthreads();
+    XSlice xs;
+    read_xslice(lds, slots, valid ? lane : 0, xs);
+
+    float yp[64];
+#pragma unroll
+    for (int e = 0; e < 64; e++) yp[e] = 0.f;
+    float mb0 = 0.f, mb1 = 0.f;
+#pragma unroll
+    for (int k = 0; k < NPW; k++) {
+        const float g = valid ? unit_dot(vg[k], xs, usel) : 0.f;
+        const float u = valid ? unit_dot(vu[k], xs, usel) : 0.f;
+        const float t = pair_sum(g, u);
+        const float gt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 31));
+        const float ut = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 63));
+        const float h = nval[k] ? act_pair(gt, ut, kind) : 0.f;
+        unit_axpy(vd[k], usel, h, yp, mb0, mb1);
+    }
+    // the 8 waves' partials (lanes >= units hold junk and are never read)
+    __syncthreads();  // the x encoding is dead: LDS now holds the partials
+    float* red = reinterpret_cast<float*>(lds);
+#pragma unroll
+    for (int e = 0; e < 64; e++)
+        red[(wave * 64 + e) * FUSED_RED_PITCH + lane] = yp[e] - (e < 32 ? mb0 : mb1);
+    __syncthreads();
+    float* out = partial + static_cast<int64_t>(blockIdx.x) * FUSED_STRIDE;
+    const int h_dim = 64 * units;
+    for (int col = static_cast<int>(threadIdx.x); col < h_dim; col += static_cast<int>(blockDim.x)) {
+        const int l = col >> 6, e = col & 63;
+        float sum = 0.f;
+#pragma unroll
+        for (int w = 0; w < 8; w++) sum += red[(w * 64 + e) * FUSED_RED_PITCH + l];
+        out[col] = sum;
+    }
+}
+
+// y[64 b + c] = sum over the nblk partials in order; thread t: column c = t %
+// 64, partials t / 64, t / 64 + 16, ...
+__global__ void __launch_bounds__(1024) sparse_reduce_kernel(const float* __restrict__ partial, int nblk,
+                                                             float* __restrict__ y) {
+    __shared__ float red[16][64];
+    const int c = threadIdx.x & 63, bg = threadIdx.x >> 6;
+    const int col = static_cast<int>(blockIdx.x) * 64 + c;
+    // every load of a round of 8 is issued before the adds (fixed order)
+    float sum = 0.f;
+    for (int b0 = bg; b0 < nblk; b0 += 16 * 8) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int b = b0 + 16 * k;
+            v[k] = partial[static_cast<int64_t>(b < nblk ? b : bg) * FUSED_STRIDE + col];
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) sum += b0 + 16 * k < nblk ? v[k] : 0.f;
+    }
+    red[bg][c] = sum;
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        float t = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; k++) t += red[k][c];
+        y[col] = t;
+    }
+}
+
 // ---- top-k indices (single workgroup radix select) ---------------------------
 
 __device__ __forceinline__ uint32_t order_key(float f) {
@@ -234,11 +409,25 @@ struct SparseWs {
     size_t gu, hid, total;
 };
 
+// The fused layout-1 path (h <= 4096) takes ceil(n_active / (8 * neurons per
+// wave)) partial outputs of FUSED_STRIDE floats; the other paths take the gate/up
+// results (and the dense hidden vector for layout 0).
+bool fused_path(int64_t h, int32_t layout) {
+    if (layout != 1 || h > 4096) return false;
+    const char* e = std::getenv("VB_SPARSE_FUSED");
+    return !(e && e[0] == '0');
+}
+
 SparseWs sparse_ws(int64_t h, int64_t i, int32_t n_active, int32_t layout) {
     SparseWs w;
     w.gu = 0;
     w.hid = align256(static_cast<size_t>(2 * (n_active > 0 ? n_active : 1)) * sizeof(float));
     size_t off = w.hid + (layout == 0 ? align256(static_cast<size_t>(i) * sizeof(float)) : 0);
+    if (layout == 1 && h <= 4096) {  // room for the fused path too
+        const size_t nblk = static_cast<size_t>((n_active + 7) / 8);  // the most partials (1 neuron per wave)
+        const size_t fused = align256((nblk > 0 ? nblk : 1) * FUSED_STRIDE * sizeof(float));
+        off = off > fused ? off : fused;
+    }
     w.total = off;
     return w;
 }
@@ -288,6 +477,31 @@ extern "C" int vb_sparse_ffn(const void* wg, const void* wu, const void* wd, int
 
     if (n_active == 0) {  // no active neuron: y = 0
         fill_zero_kernel<<<dim3(static_cast<uint32_t>((h + 255) / 256)), dim3(256), 0, st>>>(y, h);
+        return check_launch("vb_sparse_ffn");
+    }
+    if (fused_path(h, down_layout)) {
+        // one launch for gate/up/act/down, one for the partial sums
+        if (reinterpret_cast<uintptr_t>(x) % 16 != 0) {
+            set_error("vb_sparse_ffn: x must be 16-byte aligned");
+            return E_INVAL;
+        }
+        const int units = static_cast<int>(h / 64);
+        const int slots = (units + 7) & ~7;  // gemv_core.hpp: encoded units, a multiple of 8
+        const char* ne = std::getenv("VB_SPARSE_NPW");
+        const int npw = ne && ne[0] == '2' ? 2 : FUSED_NPW;
+        const int nblk = (n_active + 8 * npw - 1) / (8 * npw);
+        float* part = reinterpret_cast<float*>(wsb);
+        if (npw == 2)
+            sparse_fused_q4k_kernel<2><<<dim3(static_cast<uint32_t>(nblk)), dim3(512), 0, st>>>(
+                static_cast<const uint8_t*>(wg), static_cast<const uint8_t*>(wu), static_cast<const uint8_t*>(wd),
+                row_bytes(TYPE_Q4_K, h), i, x, active, n_active, act_kind, part, units, slots);
+        else
+            sparse_fused_q4k_kernel<FUSED_NPW><<<dim3(static_cast<uint32_t>(nblk)), dim3(512), 0, st>>>(
+                static_cast<const uint8_t*>(wg), static_cast<const uint8_t*>(wu), static_cast<const uint8_t*>(wd),
+                row_bytes(TYPE_Q4_K, h), i, x, active, n_active, act_kind, part, units, slots);
+        int rcf = check_launch("vb_sparse_ffn");
+        if (rcf != OK) return rcf;
+        sparse_reduce_kernel<<<dim3(static_cast<uint32_t>(units)), dim3(1024), 0, st>>>(part, nblk, y);
         return check_launch("vb_sparse_ffn");
     }
     // 1. gate/up on the active rows
