@@ -254,6 +254,68 @@ def time_moe(steps, warmup):
     return ms, hit, ab
 
 
+def time_gguf_ingest(n_tensors=32, reps=3):
+    """GGUF ingestion: a file of n_tensors Q4_K 14336x4096 tensors (random
+    block bytes, 33 MB each) in the page cache, opened and every tensor
+    uploaded to HBM (vb_gguf_open + vb_gguf_upload).  Returns the best
+    rate over reps in GB/s, the bytes moved, the file and the open time."""
+    import tempfile
+    import torch
+    from vibeblade_amd import ggml
+    from vibeblade_amd.gguf import GGUFFile
+    from vibeblade_amd.gguf_write import write_gguf
+    rows, k = 14336, 4096
+    blob = np.random.default_rng(0).integers(0, 256, rows * ggml.row_bytes(ggml.GGML_TYPE_Q4_K, k),
+                                            dtype=np.uint8)
+    fd, path = tempfile.mkstemp(suffix=".gguf")
+    os.close(fd)
+    write_gguf(path, [], [(f"blk.{i}.ffn_up.weight", (k, rows), ggml.GGML_TYPE_Q4_K, blob)
+                          for i in range(n_tensors)])
+    total = n_tensors * blob.size
+    best, t_open = None, None
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        with GGUFFile(path) as f:
+            t1 = time.perf_counter()
+            ws = [f.load_qtensor(f"blk.{i}.ffn_up.weight", "cuda:0") for i in range(n_tensors)]
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t1
+        if best is None or dt < best:
+            best, t_open = dt, t1 - t0
+        ok = bool(torch.equal(ws[-1].data.reshape(-1), torch.from_numpy(blob).cuda()))
+        del ws
+        torch.cuda.empty_cache()
+        if not ok:
+            os.remove(path)
+            raise RuntimeError("GGUF upload: device bytes differ from the file")
+    return total / best / 1e9, total, path, t_open
+
+
+def gguf_reader_cpu_baseline(path):
+    """The reference's GGUFFile (cpp/src/gguf.cpp) opening the same file:
+    it reads the whole file into RAM (gguf.cpp:199-251), the host half of
+    its ingestion.  None where that reader is not built."""
+    import ctypes
+    lib_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "oracle", "_ref", "libvbref_gguf.so")
+    if not os.path.exists(lib_path):
+        return None
+    lib = ctypes.CDLL(lib_path)
+    lib.ref_gguf_open.restype = ctypes.c_void_p
+    lib.ref_gguf_open.argtypes = [ctypes.c_char_p]
+    lib.ref_gguf_close.argtypes = [ctypes.c_void_p]
+    best = None
+    for _ in range(2):
+        t0 = time.perf_counter()
+        h = lib.ref_gguf_open(path.encode())
+        dt = time.perf_counter() - t0
+        if not h:
+            return None
+        lib.ref_gguf_close(h)
+        best = dt if best is None else min(best, dt)
+    return os.path.getsize(path) / best / 1e9
+
+
 def check_parity(qtype, n, k, copies, x, ys):
     """Oracle check of the first copy's output (the timed results)."""
     import oracle as O
@@ -440,6 +502,15 @@ def main():
                           "frac_hbm": round(b5 / (ms5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}),
               file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
+        gbs6, b6, gpath, t_open = time_gguf_ingest()
+        ref_gbs = gguf_reader_cpu_baseline(gpath) if not args.no_cpu_baseline else None
+        os.remove(gpath)
+        print(json.dumps({"workload": "GGUF ingestion: open + upload 32 Q4_K 14336x4096 tensors (page cache)",
+                          "bytes": b6, "GB/s": round(gbs6, 2), "open_ms": round(t_open * 1e3, 3),
+                          "cpu_baseline": None if ref_gbs is None else
+                          {"value": round(ref_gbs, 2), "unit": "GB/s", "cores": 1, "kind": "reference",
+                           "sample": "reference GGUFFile opening the same file (reads it into RAM)"}}),
+              file=sys.stderr, flush=True)
         for m, ncop in ((8, NCOPIES), (512, 4)):
             ms3, e3 = time_gemm(m, 14336, 4096, 400 if m == 8 else 100, 40, ncop)
             flops = 2.0 * m * 14336 * 4096

@@ -166,6 +166,55 @@ int vb_rms_norm(const float* x, const float* w, float* y, int64_t rows, int64_t 
  * vibeblade/gpu.py:192-198). */
 int vb_softmax(const float* x, float* y, int64_t rows, int64_t n, void* stream);
 
+/* ---- GGUF ingestion --------------------------------------------------------
+ * A .gguf file mapped read-only and parsed (header, metadata, tensor table).
+ * Replaces GGUFFile (cpp/include/gguf.h:29-60, cpp/src/gguf.cpp) and the
+ * parsing half of GGUFLoader (vibeblade/loader.py:490-783).  The data
+ * section follows general.alignment when the file sets it (32 otherwise);
+ * the reference always uses 32.  Host-side calls need no GPU; the handle
+ * is read-only after vb_gguf_open and may be shared between threads. */
+typedef struct vb_gguf vb_gguf;
+/* GGUFFile::GGUFFile (gguf.h:30); errors (bad magic, version > 3, reads past
+ * the end, unaligned or out-of-file tensor data, unknown types) return
+ * E_INVAL with the reason in vb_last_error. */
+int vb_gguf_open(const char* path, vb_gguf** out);
+/* GGUFFile::~GGUFFile (gguf.h:31); unmaps the file.  NULL is accepted. */
+int vb_gguf_close(vb_gguf* f);
+/* version(), file_size() (gguf.h:58-59), plus the data alignment and the
+ * absolute offset of the data section. */
+int vb_gguf_info(const vb_gguf* f, uint32_t* version, uint64_t* alignment, uint64_t* data_offset,
+                 uint64_t* file_size);
+/* tensors() (gguf.h:55): count, lookup by name (-1 when absent, as
+ * tensor_info returns nullptr, gguf.h:41), and one entry: name (valid until
+ * vb_gguf_close), ggml type, dims (GGUF order, dims[0] along the row,
+ * unused dims 1), absolute file offset and byte size of the data. */
+int64_t vb_gguf_n_tensors(const vb_gguf* f);
+int64_t vb_gguf_find_tensor(const vb_gguf* f, const char* name);
+int vb_gguf_tensor_info(const vb_gguf* f, int64_t i, const char** name, int32_t* ggml_type, int32_t* n_dims,
+                        int64_t* dims, uint64_t* offset, uint64_t* nbytes);
+/* tensor_data (gguf.h:38): host pointer into the mapping. */
+int vb_gguf_tensor_data(const vb_gguf* f, int64_t i, const void** host_ptr);
+/* Copies tensor i's bytes (GGUF block layout, unchanged) to device memory
+ * dst (at least nbytes) on `stream` through two pinned staging buffers;
+ * returns when the copy has completed.  The buffers (min(8 MiB, largest
+ * tensor) each) are made on the first upload and kept until vb_gguf_close;
+ * uploads from one handle run one at a time. */
+int vb_gguf_upload(const vb_gguf* f, int64_t i, void* dst, void* stream);
+/* Metadata (meta_* accessors, gguf.h:44-52): count, lookup by key (-1 when
+ * absent), the entry's key, value type (GGUF: 0 u8, 1 i8, 2 u16, 3 i16,
+ * 4 u32, 5 i32, 6 f32, 7 bool, 8 string, 9 array, 10 u64, 11 i64, 12 f64),
+ * array element type (-1 for scalars) and element count (1 for scalars),
+ * then element j as an integer (integer and bool types), a double (f32,
+ * f64) or a string (pointer into the mapping, not NUL-terminated, and its
+ * length). */
+int64_t vb_gguf_n_kv(const vb_gguf* f);
+int64_t vb_gguf_find_kv(const vb_gguf* f, const char* key);
+int vb_gguf_kv_info(const vb_gguf* f, int64_t i, const char** key, int32_t* value_type, int32_t* elem_type,
+                    uint64_t* count);
+int vb_gguf_kv_int(const vb_gguf* f, int64_t i, uint64_t j, int64_t* out);
+int vb_gguf_kv_float(const vb_gguf* f, int64_t i, uint64_t j, double* out);
+int vb_gguf_kv_str(const vb_gguf* f, int64_t i, uint64_t j, const char** s, uint64_t* len);
+
 #ifdef __cplusplus
 }
 #endif

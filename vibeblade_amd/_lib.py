@@ -48,6 +48,25 @@ SIGNATURES = {
     "vb_activation": (ctypes.c_int, [_vp, _vp, _i64, _i32, _vp]),
     "vb_rms_norm": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp]),
     "vb_softmax": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp]),
+    "vb_gguf_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "vb_gguf_close": (ctypes.c_int, [_vp]),
+    "vb_gguf_info": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint64),
+                                    ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
+    "vb_gguf_n_tensors": (_i64, [_vp]),
+    "vb_gguf_find_tensor": (_i64, [_vp, ctypes.c_char_p]),
+    "vb_gguf_tensor_info": (ctypes.c_int, [_vp, _i64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_i32),
+                                           ctypes.POINTER(_i32), ctypes.POINTER(_i64),
+                                           ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
+    "vb_gguf_tensor_data": (ctypes.c_int, [_vp, _i64, ctypes.POINTER(_vp)]),
+    "vb_gguf_upload": (ctypes.c_int, [_vp, _i64, _vp, _vp]),
+    "vb_gguf_n_kv": (_i64, [_vp]),
+    "vb_gguf_find_kv": (_i64, [_vp, ctypes.c_char_p]),
+    "vb_gguf_kv_info": (ctypes.c_int, [_vp, _i64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_i32),
+                                       ctypes.POINTER(_i32), ctypes.POINTER(ctypes.c_uint64)]),
+    "vb_gguf_kv_int": (ctypes.c_int, [_vp, _i64, ctypes.c_uint64, ctypes.POINTER(_i64)]),
+    "vb_gguf_kv_float": (ctypes.c_int, [_vp, _i64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_double)]),
+    "vb_gguf_kv_str": (ctypes.c_int, [_vp, _i64, ctypes.c_uint64, ctypes.POINTER(_vp),
+                                      ctypes.POINTER(ctypes.c_uint64)]),
 }
 
 _lib = None

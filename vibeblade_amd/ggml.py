@@ -3,9 +3,10 @@
 Same table as ``ggml_type`` / ``ggml_blck_size`` / ``ggml_type_size`` /
 ``tensor_nbytes`` (cpp/include/ggml_types.h:11-71, :195-199) and the Python
 twins ``_QBLOCK_SIZE`` / ``_QBLOCK_BYTES`` (vibeblade/loader.py:86-115).  The
-loader's Q3_K entry (178 bytes) disagrees with ggml (110); ggml's value is
-used here.  Only the types with device kernels are marked in
-``DEVICE_TYPES``.
+loader's Q3_K entry (178 bytes) disagrees with ggml (110), and the C++
+table's Q8_1 entry (40 bytes, ggml_types.h:62: fp32 d and s) is the older
+ggml layout (fp16 d and s, 36 bytes, since); ggml's current values are used
+here.  Only the types with device kernels are marked in ``DEVICE_TYPES``.
 """
 from __future__ import annotations
 
@@ -35,7 +36,7 @@ BLOCK = {
     GGML_TYPE_Q5_0: (32, 22),
     GGML_TYPE_Q5_1: (32, 24),
     GGML_TYPE_Q8_0: (32, 34),
-    GGML_TYPE_Q8_1: (32, 40),
+    GGML_TYPE_Q8_1: (32, 36),
     GGML_TYPE_Q2_K: (256, 84),
     GGML_TYPE_Q3_K: (256, 110),
     GGML_TYPE_Q4_K: (256, 144),
