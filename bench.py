@@ -217,6 +217,51 @@ def time_sparse(layout, steps, warmup, ncopies=8):
     return ms, n_s, ab
 
 
+def time_ffn_block(down_type, fused, steps, warmup, ncopies=8):
+    """One token through the FFN block, hd=4096, inter=14336, Q4_K gate/up,
+    down Q4_K or Q6_K (the two Q4_K_M mixes), RMSNorm + SiLU + residual.
+    fused: vb_ffn_block (2 launches); else the reference's step order as
+    separate launches (rms_norm, gate GEMV, up GEMV, silu, multiply, down
+    GEMV, residual add).  Returns (ms per call, algorithmic bytes)."""
+    import torch
+    from vibeblade_amd import _lib, ggml
+    from vibeblade_amd.tensor import QTensor, ACT_SILU
+    hd, inter = 4096, 14336
+    gen = torch.Generator(device="cuda").manual_seed(SEED + 6)
+    sets = []
+    for _ in range(ncopies):
+        g = QTensor.quantize(torch.randn((inter, hd), generator=gen, device="cuda") * 0.02, ggml.GGML_TYPE_Q4_K)
+        u = QTensor.quantize(torch.randn((inter, hd), generator=gen, device="cuda") * 0.02, ggml.GGML_TYPE_Q4_K)
+        d = QTensor.quantize(torch.randn((hd, inter), generator=gen, device="cuda") * 0.02, down_type)
+        sets.append((g, u, d))
+    x = torch.randn(hd, generator=gen, device="cuda")
+    nw = 1.0 + 0.1 * torch.randn(hd, generator=gen, device="cuda")
+    y = torch.empty(hd, device="cuda")
+    lib = _lib.load()
+    ws = torch.empty(lib.vb_ffn_block_workspace(hd, inter), dtype=torch.uint8, device="cuda")
+    xn, gb, ub, hb = (torch.empty(n, device="cuda") for n in (hd, inter, inter, inter))
+    db = torch.empty(hd, device="cuda")
+
+    def mk(g, u, d):
+        def f(st):
+            if fused:
+                _lib.check("vb_ffn_block", lib.vb_ffn_block(
+                    x.data_ptr(), nw.data_ptr(), 1e-5, g.ptr(), u.ptr(), g.qtype, d.ptr(), d.qtype, hd, inter,
+                    ACT_SILU, 1, y.data_ptr(), ws.data_ptr(), ws.numel(), st))
+                return
+            _lib.check("vb_rms_norm", lib.vb_rms_norm(x.data_ptr(), nw.data_ptr(), xn.data_ptr(), 1, hd, 1e-5, st))
+            _lib.check("vb_gemv", lib.vb_gemv(g.ptr(), xn.data_ptr(), gb.data_ptr(), inter, hd, g.qtype, st))
+            _lib.check("vb_gemv", lib.vb_gemv(u.ptr(), xn.data_ptr(), ub.data_ptr(), inter, hd, u.qtype, st))
+            _lib.check("vb_activation", lib.vb_activation(gb.data_ptr(), hb.data_ptr(), inter, 0, st))
+            torch.mul(hb, ub, out=hb)
+            _lib.check("vb_gemv", lib.vb_gemv(d.ptr(), hb.data_ptr(), db.data_ptr(), hd, inter, d.qtype, st))
+            torch.add(x, db, out=y)
+        return f
+    ms, _, _ = time_launches([mk(*t) for t in sets], steps, warmup)
+    ab = 2 * inter * 2304 + hd * ggml.row_bytes(down_type, inter) + 4 * hd * 4 + 8 * inter
+    return ms, ab
+
+
 def time_moe(steps, warmup):
     """8 Q4_K experts (gate/up 14336x4096, down 4096x14336), 16 tokens, top-2.
     Returns (ms per call, experts hit, algorithmic bytes)."""
@@ -502,6 +547,16 @@ def main():
                           "frac_hbm": round(b5 / (ms5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}),
               file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
+        for dt_name, dt in (("Q4_K", ggml.GGML_TYPE_Q4_K), ("Q6_K", ggml.GGML_TYPE_Q6_K)):
+            for fused in (True, False):
+                ms7, b7 = time_ffn_block(dt, fused, 400, 40)
+                print(json.dumps({"workload": f"FFN block hd=4096 inter=14336 Q4_K gate/up, {dt_name} down, "
+                                              f"RMSNorm+SiLU+residual, {'fused (2 launches)' if fused else 'unfused (7 launches)'}",
+                                  "us_per_call": round(ms7 * 1e3, 3), "alg_bytes": b7,
+                                  "GB/s": round(b7 / (ms7 * 1e-3) / 1e9, 1),
+                                  "frac_hbm": round(b7 / (ms7 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}),
+                      file=sys.stderr, flush=True)
+                torch.cuda.empty_cache()
         gbs6, b6, gpath, t_open = time_gguf_ingest()
         ref_gbs = gguf_reader_cpu_baseline(gpath) if not args.no_cpu_baseline else None
         os.remove(gpath)

@@ -120,6 +120,26 @@ int vb_sparse_ffn(const void* wg, const void* wu, const void* wd, int32_t down_l
                   float* y, int64_t h, int64_t i, int32_t ggml_type, void* workspace,
                   size_t workspace_bytes, void* stream);
 
+/* ---- FFN block, one token ------------------------------------------------
+ * y = [x +] Wd act(Wg n, Wu n), n = x / sqrt(mean(x^2) + eps) * norm_w
+ * (n = x when norm_w is NULL; the x term when add_residual != 0).
+ * act_kind: 0 = silu(g) * u, 1 = relu(g) * relu(u),
+ *           2 = gelu_tanh(g) * u (GeGLU, cpp/src/fast_model.cpp:943-948).
+ * Wg, Wu: inter rows x hd, one type (gate_up_type); Wd: hd rows x inter
+ * (down_type); GGUF layout.  x, norm_w: hd fp32, 16-byte aligned; y: hd fp32,
+ * may be x (in-place residual update).  Replaces the dense FFN step of the
+ * decoder layer, RMSNorm -> gate/up -> act -> down -> residual
+ * (cpp/src/fast_model.cpp:837-975; vibeblade/transformer.py:789-815 with
+ * ffn_silu, :177-208).  Two launches when gate/up and down are Q4_K / Q6_K /
+ * Q8_0 (norm and activation fused into the gate/up GEMV, residual into the
+ * down GEMV); other type mixes run unfused, on the device.  workspace: at
+ * least vb_ffn_block_workspace(hd, inter) bytes, 16-byte aligned. */
+int64_t vb_ffn_block_workspace(int64_t hd, int64_t inter);
+int vb_ffn_block(const float* x, const float* norm_w, float eps, const void* w_gate, const void* w_up,
+                 int32_t gate_up_type, const void* w_down, int32_t down_type, int64_t hd, int64_t inter,
+                 int32_t act_kind, int32_t add_residual, float* y, void* workspace, size_t workspace_bytes,
+                 void* stream);
+
 /* out_idx[0..k) = indices of the k largest v[i], ascending index order (ties
  * at the threshold resolve to the lowest indices).  The top-k neuron
  * prediction of sparse_ffn_silu (vibeblade/sparse.py:250-261) and

@@ -48,6 +48,9 @@ PARITY = {
     "dequant Q8_0": "pinned: closed forms (d=1 -> q, d=0 -> 0) on loader.py:129-133 layout",
     "gemv / gemm": "pinned: brute force over integer-valued blocks + fp64 numpy",
     "sparse_ffn": "pinned: closed form S=all equals dense, S=empty gives 0, order invariance",
+    "ffn_block": "pinned: rms_norm closed forms (constant rows, scale invariance, eps), "
+                 "activation special values, the tanh-form GeGLU against the identity "
+                 "0.5(1 + tanh z) = 1/(1 + e^-2z), composition = sparse_ffn with S = all plus the residual",
     "moe": "pinned: weights sum to 1, grouped == per-token loop, single-expert == one GEMM",
 }
 
@@ -228,6 +231,42 @@ def relu64(v: np.ndarray) -> np.ndarray:
 
 ACT_SILU = 0   # silu(g) * u         (vibeblade/sparse.py:269-272)
 ACT_DRELU = 1  # relu(g) * relu(u)   (ReLU after both projections, config 4)
+ACT_GELU_TANH = 2  # gelu_tanh(g) * u (cpp/src/fast_model.cpp:943-948)
+
+
+def gelu_tanh64(v: np.ndarray) -> np.ndarray:
+    """0.5 v (1 + tanh(0.7978845608 (v + 0.044715 v^3))), as
+    cpp/src/fast_model.cpp:945-946 writes it."""
+    v = np.asarray(v, dtype=np.float64)
+    return 0.5 * v * (1.0 + np.tanh(0.7978845608 * (v + 0.044715 * v * v * v)))
+
+
+def act_pair(g: np.ndarray, u: np.ndarray, act: int) -> np.ndarray:
+    if act == ACT_SILU:
+        return silu64(g) * u
+    if act == ACT_GELU_TANH:
+        return gelu_tanh64(g) * u
+    return relu64(g) * relu64(u)
+
+
+def rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """x / sqrt(mean(x^2) + eps) * w per row, fp64 (cpp/src/fast_model.cpp:61-71)."""
+    x = np.asarray(x, dtype=np.float64)
+    r = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+    return x * r * np.asarray(w, dtype=np.float64)
+
+
+def ffn_block(gate: np.ndarray, up: np.ndarray, down: np.ndarray, x: np.ndarray, norm_w, eps: float,
+              act: int, add_residual: bool) -> np.ndarray:
+    """One token's FFN block, fp64 over decoded weights (cpp/src/fast_model.cpp:837-975):
+    n = rms_norm(x) (or x when norm_w is None); y = [x +] down @ act(gate @ n, up @ n).
+    gate/up: decoded (I, H); down: decoded (H, I)."""
+    x = np.asarray(x, dtype=np.float64)
+    n = x if norm_w is None else rms_norm(x, norm_w, eps)
+    g = gate.astype(np.float64) @ n
+    u = up.astype(np.float64) @ n
+    y = down.astype(np.float64) @ act_pair(g, u, act)
+    return x + y if add_residual else y
 
 
 def sparse_ffn(gate: np.ndarray, up: np.ndarray, down: np.ndarray, x: np.ndarray,
@@ -243,8 +282,7 @@ def sparse_ffn(gate: np.ndarray, up: np.ndarray, down: np.ndarray, x: np.ndarray
     idx = np.asarray(active, dtype=np.int64)
     g = x @ gate[idx].astype(np.float64).T
     u = x @ up[idx].astype(np.float64).T
-    h = silu64(g) * u if act == ACT_SILU else relu64(g) * relu64(u)
-    return h @ down[:, idx].astype(np.float64).T
+    return act_pair(g, u, act) @ down[:, idx].astype(np.float64).T
 
 
 def route_top_k(logits: np.ndarray, topk: int):

@@ -1,7 +1,7 @@
-"""GPU parity of the TurboSparse FFN, top-k selection and the MoE FFN.
+"""GPU parity of the TurboSparse FFN, the FFN block, top-k selection and the MoE FFN.
 
-Bars: sparse FFN (fp32 accumulation) rel-L2 <= 1e-3 against the fp64 oracle
-on the same decoded weights; MoE (fp16 MFMA products) rel-L2 <= 5e-3;
+Bars: sparse FFN and FFN block (fp32 accumulation) rel-L2 <= 1e-3 against
+the fp64 oracle on the same decoded weights; MoE (fp16 MFMA products) rel-L2 <= 5e-3;
 top-k and routing indices exact.
 """
 import numpy as np
@@ -11,8 +11,8 @@ import torch
 import oracle as O
 from vibeblade_amd import ggml
 from vibeblade_amd.tensor import (QTensor, as_qtensor, sparse_ffn, topk_indices, moe_grouped_ffn,
-                                  moe_route, activation, ACT_SILU, ACT_RELU2, DOWN_GGUF,
-                                  DOWN_NEURON_MAJOR)
+                                  moe_route, activation, ffn_block, ACT_SILU, ACT_RELU2, ACT_GELU_TANH,
+                                  DOWN_GGUF, DOWN_NEURON_MAJOR)
 
 pytestmark = pytest.mark.gpu
 Q4K = ggml.GGML_TYPE_Q4_K
@@ -241,3 +241,88 @@ def test_activation():
     x = torch.randn(10000, device="cuda") * 5
     assert torch.allclose(activation(x, 0), x * torch.sigmoid(x), rtol=1e-5, atol=1e-6)
     assert torch.equal(activation(x, 1), torch.clamp(x, min=0))
+
+
+# ---- FFN block (vb_ffn_block) -------------------------------------------------
+
+def block_weights(hd, inter, gu_type, d_type, seed):
+    rng = np.random.default_rng(seed)
+    g = (rng.standard_normal((inter, hd)) * 0.02).astype(np.float32)
+    u = (rng.standard_normal((inter, hd)) * 0.02).astype(np.float32)
+    d = (rng.standard_normal((hd, inter)) * 0.02).astype(np.float32)
+
+    def q(w, t):
+        if t == ggml.GGML_TYPE_F32:
+            return as_qtensor(w)
+        if t == ggml.GGML_TYPE_F16:
+            return QTensor.from_bytes(w.astype(np.float16).tobytes(), t, *w.shape)
+        return QTensor.quantize(w, t)
+    gq, uq, dq = q(g, gu_type), q(u, gu_type), q(d, d_type)
+    return gq, uq, dq, dec(gq), dec(uq), dec(dq)
+
+
+def run_block(gq, uq, dq, gd, ud, dd, hd, act, norm, residual, seed, inplace=False):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal(hd).astype(np.float32)
+    nw = (1.0 + 0.1 * rng.standard_normal(hd)).astype(np.float32) if norm else None
+    xt = torch.from_numpy(x).cuda()
+    y = ffn_block(gq, uq, dq, xt, None if nw is None else torch.from_numpy(nw), 1e-5, act, residual,
+                  out=xt if inplace else None)
+    if inplace:
+        assert y.data_ptr() == xt.data_ptr()
+    y = y.cpu().numpy()
+    want = O.ffn_block(gd, ud, dd, x, nw, 1e-5, act, residual)
+    # the FFN part alone meets the bar (the residual would hide its error)
+    x0 = x.astype(np.float64) if residual else 0.0
+    assert O.rel_l2(y - x0, want - x0) <= 1e-3
+    return y
+
+
+@pytest.mark.parametrize("gu,dn", [(Q4K, Q4K), (Q4K, ggml.GGML_TYPE_Q6_K), (ggml.GGML_TYPE_Q6_K, Q4K),
+                                   (ggml.GGML_TYPE_Q8_0, ggml.GGML_TYPE_Q8_0)])
+@pytest.mark.parametrize("act", [ACT_SILU, ACT_RELU2, ACT_GELU_TANH])
+def test_ffn_block_llama_shape(gu, dn, act):
+    """hd = 4096, inter = 14336 (Llama-3-8B), every type mix of a Q4_K_M file."""
+    w = block_weights(4096, 14336, gu, dn, 31)
+    run_block(*w, 4096, act, norm=True, residual=True, seed=5)
+
+
+@pytest.mark.parametrize("norm,residual,inplace", [(False, False, False), (True, False, False),
+                                                   (False, True, False), (True, True, True)])
+def test_ffn_block_options(norm, residual, inplace):
+    w = block_weights(1024, 2816, Q4K, ggml.GGML_TYPE_Q6_K, 32)
+    run_block(*w, 1024, ACT_SILU, norm, residual, seed=6, inplace=inplace)
+
+
+@pytest.mark.parametrize("hd,inter,dn", [(20480, 320, ggml.GGML_TYPE_Q8_0), (8192, 3072, Q4K), (256, 256, Q4K),
+                                         (5120, 13824, Q4K)])
+def test_ffn_block_shapes(hd, inter, dn):
+    """hd = 20480: five k-slices per row, one row group per workgroup, the
+    encode's loop path and the even-rows adjustment of the pair epilogue;
+    hd = inter = 256: one super-block per row."""
+    w = block_weights(hd, inter, Q4K, dn, 33)
+    run_block(*w, hd, ACT_SILU, norm=True, residual=True, seed=7)
+
+
+@pytest.mark.parametrize("gu,dn", [(ggml.GGML_TYPE_F16, ggml.GGML_TYPE_F32), (ggml.GGML_TYPE_F32, Q4K),
+                                   (Q4K, ggml.GGML_TYPE_F16)])
+def test_ffn_block_unfused_types(gu, dn):
+    """Type mixes outside the fused path run as separate launches."""
+    w = block_weights(512, 768, gu, dn, 34)
+    run_block(*w, 512, ACT_GELU_TANH, norm=True, residual=True, seed=8)
+    run_block(*w, 512, ACT_SILU, norm=False, residual=False, seed=9)
+
+
+def test_ffn_block_repeatable_and_errors():
+    w = block_weights(1024, 1024, Q4K, Q4K, 35)
+    a = run_block(*w, 1024, ACT_SILU, True, True, seed=10)
+    b = run_block(*w, 1024, ACT_SILU, True, True, seed=10)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    gq, uq, dq = w[:3]
+    x = torch.zeros(1024, device="cuda")
+    with pytest.raises(ValueError):
+        ffn_block(gq, uq, dq, x, act=7)
+    with pytest.raises(ValueError):
+        ffn_block(gq, uq, dq, torch.zeros(1000, device="cuda"))
+    with pytest.raises(ValueError):  # misaligned x
+        ffn_block(gq, uq, dq, torch.zeros(1025, device="cuda")[1:])

@@ -332,3 +332,52 @@ def test_moe_invariants():
                             [downs[p] for p in perm], x, logits[:, perm], 2)
     assert np.allclose(y3, y, rtol=1e-12)
     assert np.array_equal(perm[idx3], idx)
+
+
+def test_rms_norm_closed_forms():
+    w = np.linspace(-2.0, 3.0, 8)
+    # constant row, eps = 0: x / |x| * w
+    assert np.allclose(O.rms_norm(np.full(8, -3.5), w, 0.0), -w, rtol=0, atol=1e-15)
+    # x = (3, 4): mean square 12.5 (a sum instead of a mean, or a product
+    # instead of a quotient, fails here)
+    got = O.rms_norm(np.array([3.0, 4.0]), np.array([1.0, 2.0]), 0.0)
+    assert np.allclose(got, [3.0 / np.sqrt(12.5), 8.0 / np.sqrt(12.5)], rtol=1e-15)
+    # eps enters under the root: x = 0 stays finite, eps = mean square halves the scale^2
+    assert np.all(O.rms_norm(np.zeros(8), w, 1e-5) == 0.0)
+    x = np.array([1.0, -1.0, 1.0, -1.0])
+    assert np.allclose(O.rms_norm(x, np.ones(4), 1.0), x / np.sqrt(2.0), rtol=1e-15)
+    # scale invariance at eps = 0
+    rng = np.random.default_rng(3)
+    v = rng.standard_normal(64)
+    assert np.allclose(O.rms_norm(1e3 * v, np.ones(64), 0.0), O.rms_norm(v, np.ones(64), 0.0), rtol=1e-12)
+
+
+def test_activation_forms():
+    g = np.array([-30.0, -2.0, -0.5, 0.0, 0.5, 1.0, 2.0, 30.0])
+    # GeGLU (tanh form): published value gelu_tanh(1) = 0.8411919906..., zero at 0, identity far right
+    assert abs(O.gelu_tanh64(np.array([1.0]))[0] - 0.8411919906082768) < 1e-12
+    z = 0.7978845608 * (g + 0.044715 * g ** 3)
+    with np.errstate(over="ignore"):  # exp(1972) at g = -30: the quotient is -0
+        assert np.allclose(O.gelu_tanh64(g), g / (1.0 + np.exp(-2.0 * z)), rtol=1e-13, atol=1e-300)
+    assert O.gelu_tanh64(np.array([0.0]))[0] == 0.0 and abs(O.gelu_tanh64(np.array([30.0]))[0] - 30.0) < 1e-12
+    u = np.full_like(g, 3.0)
+    assert np.allclose(O.act_pair(g, u, O.ACT_SILU), 3.0 * g / (1.0 + np.exp(-g)), rtol=1e-15)
+    assert np.array_equal(O.act_pair(g, -u, O.ACT_DRELU), np.zeros_like(g))
+    assert np.array_equal(O.act_pair(g, u, O.ACT_DRELU), 3.0 * np.maximum(g, 0.0))
+
+
+@pytest.mark.parametrize("act", [O.ACT_SILU, O.ACT_DRELU, O.ACT_GELU_TANH])
+def test_ffn_block_composition(act):
+    """No norm, no residual: the dense FFN = sparse_ffn over every neuron;
+    the residual adds x; the norm feeds rms_norm(x) to the same FFN."""
+    rng = np.random.default_rng(14)
+    g, u, d = _ffn_weights(rng)
+    x = rng.standard_normal(64)
+    nw = rng.standard_normal(64)
+    allidx = np.arange(256)
+    plain = O.ffn_block(g, u, d, x, None, 0.0, act, False)
+    assert np.allclose(plain, O.sparse_ffn(g, u, d, x, allidx, act)[0], rtol=1e-12, atol=1e-14)
+    assert np.allclose(O.ffn_block(g, u, d, x, None, 0.0, act, True) - x, plain, rtol=1e-12, atol=1e-14)
+    normed = O.ffn_block(g, u, d, x, nw, 1e-5, act, True)
+    want = x + O.sparse_ffn(g, u, d, O.rms_norm(x, nw, 1e-5), allidx, act)[0]
+    assert np.allclose(normed, want, rtol=1e-12, atol=1e-14)

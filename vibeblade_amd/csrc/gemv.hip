@@ -28,8 +28,11 @@ using namespace gemvc;
 // Row sources.  ROWS_PLAIN: row r of w.  ROWS_PAIRS: row r is row gidx[r/2]
 // of w (r even) or of w2 (r odd) -- gate/up pairs of the active neurons of a
 // sparse FFN, one launch and one activation encode for both matrices.
+// ROWS_DPAIRS: row r is row r/2 of w or w2 -- the gate/up pairs of every
+// neuron (a dense FFN block).
 constexpr int ROWS_PLAIN = 0;
 constexpr int ROWS_PAIRS = 1;
+constexpr int ROWS_DPAIRS = 2;
 
 // Row indices are 32-bit (the host checks n and nsrc < 2^31): 64-bit compares
 // have no scalar form on gfx9, and would pull the wave-uniform row
@@ -39,6 +42,8 @@ __device__ __forceinline__ const uint8_t* row_ptr(const uint8_t* w, const uint8_
                                                   const int32_t* gidx, int nsrc, int row, int64_t rb) {
     if constexpr (MODE == ROWS_PLAIN) {
         return w + static_cast<int64_t>(row) * rb;
+    } else if constexpr (MODE == ROWS_DPAIRS) {
+        return ((row & 1) ? w2 : w) + static_cast<int64_t>(row >> 1) * rb;
     } else {
         int src = gidx[row >> 1];
         src = src < 0 ? 0 : (src >= nsrc ? nsrc - 1 : src);  // never read outside the tensor
@@ -66,11 +71,16 @@ constexpr int gemv_max_threads() { return D <= max_d16<TYPE>() ? 1024 : 512; }
 // zbuf / zn: an int buffer the first workgroup clears (the counters of a
 // following kernel; a fill inside this launch keeps memsets out of captured
 // graphs).
-template <int TYPE, int D, int MODE>
+//
+// FUSE: the GemvFuse work (vb_internal.hpp) -- RMSNorm of x inside the
+// encode, the gate/up activation epilogue (rows_wg even, so a neuron's two
+// rows never straddle workgroups), the residual add.  FUSE = false is the
+// plain GEMV, and its code does not change.
+template <int TYPE, int D, int MODE, bool FUSE>
 __global__ void __launch_bounds__((gemv_max_threads<TYPE, D>())) gemv_q_kernel(
         const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, const int32_t* __restrict__ gidx,
         int nsrc, const float* __restrict__ x, float* __restrict__ y, int n, int64_t rb, int units,
-        int slots, int upw, int wpr, int rpg, int* __restrict__ zbuf, int zn) {
+        int slots, int upw, int wpr, int rpg, int* __restrict__ zbuf, int zn, GemvFuse fz) {
     if (zn > 0 && blockIdx.x == 0) {
         for (int i = threadIdx.x; i < zn; i += blockDim.x) zbuf[i] = 0;
     }
@@ -106,15 +116,39 @@ __global__ void __launch_bounds__((gemv_max_threads<TYPE, D>())) gemv_q_kernel(
     Unit v[D];
     const bool x_in_regs = slots * 8 <= XT_MAX * static_cast<int>(blockDim.x);
     XTasks xt;
+    [[maybe_unused]] XTasks nt;  // norm weights of the same tasks (FUSE)
+    [[maybe_unused]] const bool norm = FUSE && fz.norm_w != nullptr;
     if (x_in_regs) prefetch_x<TYPE>(x, units, slots, xt);
+    if constexpr (FUSE) {
+        if (x_in_regs && norm) prefetch_x<TYPE>(fz.norm_w, units, slots, nt);
+    }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < D; j++) issue(v[j], j);
     __builtin_amdgcn_sched_barrier(0);  // keep the weight loads ahead of the encode
-    if (x_in_regs)
-        encode_x_regs<TYPE>(units, slots, xt, xq);
-    else
-        encode_x_loop<TYPE>(x, units, slots, xq);
+    if constexpr (FUSE) {
+        if (norm) {
+            // red is free until the main loop; it holds >= one float per wave
+            const float ss = wg_sum_fixed(x_in_regs ? sumsq_tasks(units, slots, xt)
+                                                    : sumsq_loop(x, units * 64), red);
+            const float rinv = rms_inv(ss, units * 64, fz.eps);
+            if (x_in_regs) {
+                scale_tasks(xt, nt, rinv);
+                encode_x_regs<TYPE>(units, slots, xt, xq);
+            } else {
+                encode_x_loop_norm<TYPE>(x, fz.norm_w, rinv, units, slots, xq);
+            }
+        } else if (x_in_regs) {
+            encode_x_regs<TYPE>(units, slots, xt, xq);
+        } else {
+            encode_x_loop<TYPE>(x, units, slots, xq);
+        }
+    } else {
+        if (x_in_regs)
+            encode_x_regs<TYPE>(units, slots, xt, xq);
+        else
+            encode_x_loop<TYPE>(x, units, slots, xq);
+    }
     __syncthreads();
 
     XSlice xs;
@@ -141,9 +175,26 @@ __global__ void __launch_bounds__((gemv_max_threads<TYPE, D>())) gemv_q_kernel(
     for (int j = 0; j < D; j++) compute(v[j], s + j);
 
     __syncthreads();
+    if constexpr (FUSE) {
+        if (fz.act >= 0) {  // neuron p = (wg_row0 + 2i) / 2: rows 2p (gate), 2p + 1 (up)
+            for (int i = threadIdx.x; 2 * i < rows_wg; i += blockDim.x) {
+                float g = red[2 * i], uu = red[2 * i + 1];
+                for (int k = 1; k < wpr; k++) {
+                    g += red[k * rows_wg + 2 * i];
+                    uu += red[k * rows_wg + 2 * i + 1];
+                }
+                const int r = wg_row0 + 2 * i;
+                if (r + 1 < n) y[r >> 1] = act_pair(g, uu, fz.act);
+            }
+            return;
+        }
+    }
     for (int i = threadIdx.x; i < rows_wg; i += blockDim.x) {
         float t = red[i];
         for (int k = 1; k < wpr; k++) t += red[k * rows_wg + i];
+        if constexpr (FUSE) {
+            if (fz.resid && wg_row0 + i < n) t += fz.resid[wg_row0 + i];
+        }
         if (wg_row0 + i < n) y[wg_row0 + i] = t;
     }
 }
@@ -228,7 +279,7 @@ int gemv_max_threads_host(int depth) { return depth <= max_d16<TYPE>() ? 1024 : 
 // 16-wave workgroups.  VB_GEMV_CFG="wpg,rpg" and VB_GEMV_RING=d override
 // (tuning sweeps).
 template <int TYPE>
-GemvShape gemv_shape(int64_t n, int units) {
+GemvShape gemv_shape(int64_t n, int units, bool even_rows = false) {
     GemvShape s;
     s.units = units;
     s.wpr = (units + 63) / 64;
@@ -269,6 +320,15 @@ GemvShape gemv_shape(int64_t n, int units) {
             s.rpg = b;
         }
     }
+    // pair epilogue: a neuron's gate and up rows in one workgroup
+    if (even_rows && ((s.wpg / s.wpr) * s.rpg) % 2 != 0) {
+        if (s.rpg > 1 && static_cast<int64_t>(s.wpg / s.wpr) * (s.rpg + 1) * s.wpr > kMaxRedFloats)
+            s.rpg -= 1;
+        else
+            s.rpg += 1;
+        if (64 * s.wpg > gemv_max_threads_host<TYPE>(depth_of(s.rpg))) s.wpg = 8 / s.wpr * s.wpr;
+        if (s.wpg < s.wpr) s.wpg = s.wpr;
+    }
     s.depth = depth_of(s.rpg);
     const int64_t rows_wg = static_cast<int64_t>(s.wpg / s.wpr) * s.rpg;
     s.grid = (n + rows_wg - 1) / rows_wg;
@@ -277,8 +337,8 @@ GemvShape gemv_shape(int64_t n, int units) {
 }
 
 template <int TYPE, int D>
-int launch_gemv_d(const GemvShape& s, const void* w, const RowSrc& src, const float* x, float* y, int64_t n,
-                  int64_t rb, hipStream_t st) {
+int launch_gemv_d(const GemvShape& s, const void* w, const RowSrc& src, const GemvFuse& fz, const float* x,
+                  float* y, int64_t n, int64_t rb, hipStream_t st) {
     if (64 * s.wpg > gemv_max_threads<TYPE, D>()) {  // never launch past the kernel's launch bounds
         set_error("vb_gemv: %d threads exceed the %d of the depth-%d kernel", 64 * s.wpg,
                   gemv_max_threads<TYPE, D>(), D);
@@ -288,38 +348,55 @@ int launch_gemv_d(const GemvShape& s, const void* w, const RowSrc& src, const fl
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     const uint8_t* w2 = static_cast<const uint8_t*>(src.w2);
     const int ni = static_cast<int>(n), nsrc = static_cast<int>(src.nsrc);
-    if (src.gidx)
-        gemv_q_kernel<TYPE, D, ROWS_PAIRS><<<g, b, s.lds, st>>>(wb, w2, src.gidx, nsrc, x, y, ni, rb, s.units,
-                                                                s.slots, s.upw, s.wpr, s.rpg, src.zbuf, src.zn);
-    else
-        gemv_q_kernel<TYPE, D, ROWS_PLAIN><<<g, b, s.lds, st>>>(wb, w2, src.gidx, nsrc, x, y, ni, rb, s.units,
-                                                                s.slots, s.upw, s.wpr, s.rpg, src.zbuf, src.zn);
+#define VB_GEMV_LAUNCH(MODE, FUSE)                                                                      \
+    gemv_q_kernel<TYPE, D, MODE, FUSE><<<g, b, s.lds, st>>>(wb, w2, src.gidx, nsrc, x, y, ni, rb, s.units, \
+                                                            s.slots, s.upw, s.wpr, s.rpg, src.zbuf, src.zn, fz)
+    if (fz.any()) {
+        if (src.dense_pairs)
+            VB_GEMV_LAUNCH(ROWS_DPAIRS, true);
+        else if (src.gidx)
+            VB_GEMV_LAUNCH(ROWS_PAIRS, true);
+        else
+            VB_GEMV_LAUNCH(ROWS_PLAIN, true);
+    } else if (src.dense_pairs) {
+        VB_GEMV_LAUNCH(ROWS_DPAIRS, false);
+    } else if (src.gidx) {
+        VB_GEMV_LAUNCH(ROWS_PAIRS, false);
+    } else {
+        VB_GEMV_LAUNCH(ROWS_PLAIN, false);
+    }
+#undef VB_GEMV_LAUNCH
     return check_launch("vb_gemv");
 }
 
 template <int TYPE>
-int launch_gemv_q(const void* w, const RowSrc& src, const float* x, float* y, int64_t n, int64_t k,
-                  int64_t rb, hipStream_t st) {
+int launch_gemv_q(const void* w, const RowSrc& src, const GemvFuse& fz, const float* x, float* y, int64_t n,
+                  int64_t k, int64_t rb, hipStream_t st) {
     const int units = static_cast<int>(k / 64);
-    const GemvShape s = gemv_shape<TYPE>(n, units);
+    const GemvShape s = gemv_shape<TYPE>(n, units, fz.act >= 0);
     if (s.slots > kMaxSlots) {
         set_error("vb_gemv: k=%lld exceeds the supported maximum of 32768", static_cast<long long>(k));
         return E_UNSUPPORTED;
     }
+    if (fz.act >= 0 && ((s.wpg / s.wpr) * s.rpg) % 2 != 0) {  // never split a neuron's rows
+        set_error("vb_gemv: internal: odd rows per workgroup in a pair epilogue");
+        return E_INVAL;
+    }
     switch (s.depth) {
-    case 1: return launch_gemv_d<TYPE, 1>(s, w, src, x, y, n, rb, st);
-    case 2: return launch_gemv_d<TYPE, 2>(s, w, src, x, y, n, rb, st);
-    case 3: return launch_gemv_d<TYPE, 3>(s, w, src, x, y, n, rb, st);
-    default: return launch_gemv_d<TYPE, 4>(s, w, src, x, y, n, rb, st);
+    case 1: return launch_gemv_d<TYPE, 1>(s, w, src, fz, x, y, n, rb, st);
+    case 2: return launch_gemv_d<TYPE, 2>(s, w, src, fz, x, y, n, rb, st);
+    case 3: return launch_gemv_d<TYPE, 3>(s, w, src, fz, x, y, n, rb, st);
+    default: return launch_gemv_d<TYPE, 4>(s, w, src, fz, x, y, n, rb, st);
     }
 }
 
 }  // namespace
 
-// Shared with the other translation units (sparse / moe).  `src` selects
-// gathered gate/up pairs and an int buffer to clear (see RowSrc).
-int gemv_dispatch_src(const void* w, const RowSrc& src, const float* x, float* y, int64_t n, int64_t k,
-                      int32_t type, hipStream_t st) {
+// Shared with the other translation units (sparse / moe / ffn).  `src`
+// selects gathered or dense gate/up pairs and an int buffer to clear (see
+// RowSrc); `fz` the fused work (see GemvFuse).
+int gemv_dispatch_fused(const void* w, const RowSrc& src, const GemvFuse& fz, const float* x, float* y,
+                        int64_t n, int64_t k, int32_t type, hipStream_t st) {
     const int64_t rb = row_bytes(type, k);
     if (rb < 0) {
         set_error("vb_gemv: unsupported type %d or k=%lld not a whole number of blocks", type,
@@ -349,16 +426,29 @@ int gemv_dispatch_src(const void* w, const RowSrc& src, const float* x, float* y
         set_error("vb_gemv: Q4_K weights must be 16-byte aligned");
         return E_INVAL;
     }
+    if ((fz.any() || src.dense_pairs) && !blockq) {
+        set_error("vb_gemv: fused work and dense pairs need a Q4_K / Q6_K / Q8_0 weight (type %d)", type);
+        return E_UNSUPPORTED;
+    }
+    if ((fz.act >= 0 || src.dense_pairs) && (n % 2 != 0 || !src.w2)) {
+        set_error("vb_gemv: gate/up pairs need an even row count and both matrices");
+        return E_INVAL;
+    }
+    if (fz.norm_w && reinterpret_cast<uintptr_t>(fz.norm_w) % 16 != 0) {
+        set_error("vb_gemv: the norm weight must be 16-byte aligned");
+        return E_INVAL;
+    }
     switch (type) {
     case TYPE_Q4_K: {
         // v_dot4 kernel by default (fastest measured); VB_GEMV_Q4K_PATH=mfma
-        // selects the int8-MFMA kernel (same arithmetic)
+        // selects the int8-MFMA kernel (same arithmetic) for plain launches
         const char* path = std::getenv("VB_GEMV_Q4K_PATH");
-        if (path && std::strcmp(path, "mfma") == 0) return gemv_q4k_mfma(w, src, x, y, n, k, st);
-        return launch_gemv_q<TYPE_Q4_K>(w, src, x, y, n, k, rb, st);
+        if (path && std::strcmp(path, "mfma") == 0 && !fz.any() && !src.dense_pairs)
+            return gemv_q4k_mfma(w, src, x, y, n, k, st);
+        return launch_gemv_q<TYPE_Q4_K>(w, src, fz, x, y, n, k, rb, st);
     }
-    case TYPE_Q6_K: return launch_gemv_q<TYPE_Q6_K>(w, src, x, y, n, k, rb, st);
-    case TYPE_Q8_0: return launch_gemv_q<TYPE_Q8_0>(w, src, x, y, n, k, rb, st);
+    case TYPE_Q6_K: return launch_gemv_q<TYPE_Q6_K>(w, src, fz, x, y, n, k, rb, st);
+    case TYPE_Q8_0: return launch_gemv_q<TYPE_Q8_0>(w, src, fz, x, y, n, k, rb, st);
     case TYPE_F32:
     case TYPE_F16: {
         constexpr int R = 4;
@@ -388,6 +478,11 @@ int gemv_dispatch_src(const void* w, const RowSrc& src, const float* x, float* y
         set_error("vb_gemv: unsupported type %d", type);
         return E_UNSUPPORTED;
     }
+}
+
+int gemv_dispatch_src(const void* w, const RowSrc& src, const float* x, float* y, int64_t n, int64_t k,
+                      int32_t type, hipStream_t st) {
+    return gemv_dispatch_fused(w, src, GemvFuse{}, x, y, n, k, type, st);
 }
 
 int gemv_dispatch(const void* w, const float* x, float* y, int64_t n, int64_t k, int32_t type,

@@ -325,6 +325,80 @@ __device__ void encode_x_loop(const float* __restrict__ x, int units, int slots,
     }
 }
 
+// ---- RMSNorm folded into the encode ----------------------------------------
+//
+// x -> x * rinv * w with rinv = 1 / sqrt(sum(x^2) / k + eps) (the reference's
+// rms_norm, cpp/src/fast_model.cpp:61-71).  The workgroup reduces sum(x^2)
+// itself: the register path from the tasks it already holds (each element of
+// x sits in exactly one valid task), the loop path with a pass over x.
+
+// Sum of one float per thread over the workgroup, in a fixed order (wave
+// sums, then waves 0, 1, ... in turn), so every thread and every workgroup
+// gets the same value.  red: one float per wave of LDS, free until the
+// barrier that follows the caller's next use of it.
+__device__ __forceinline__ float wg_sum_fixed(float v, float* red) {
+    const float t = wave_sum_dpp(v);
+    const int nw = static_cast<int>(blockDim.x >> 6);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = t;
+    __syncthreads();
+    float s = 0.f;
+    for (int i = 0; i < nw; i++) s += red[i];
+    return s;
+}
+
+__device__ __forceinline__ float rms_inv(float sumsq, int k, float eps) {
+    return 1.0f / sqrtf(sumsq / static_cast<float>(k) + eps);
+}
+
+// Register path: this thread's share of sum(x^2) over its valid tasks.
+__device__ __forceinline__ float sumsq_tasks(int units, int slots, const XTasks& t) {
+    const int ntasks = slots * 8;
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < XT_MAX; i++) {
+        const int task = threadIdx.x + i * blockDim.x;
+        if (task < ntasks && (task >> 3) < units) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) s += t.v[i][j] * t.v[i][j];
+        }
+    }
+    return s;
+}
+
+// Register path: t = t * rinv * w, w the norm weights of the same tasks.
+__device__ __forceinline__ void scale_tasks(XTasks& t, const XTasks& w, float rinv) {
+#pragma unroll
+    for (int i = 0; i < XT_MAX; i++) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) t.v[i][j] = t.v[i][j] * rinv * w.v[i][j];
+    }
+}
+
+// Loop path: this thread's share of sum(x^2) over x[0, k) (k a multiple of 4,
+// x 16-byte aligned).
+__device__ __forceinline__ float sumsq_loop(const float* __restrict__ x, int k) {
+    float s = 0.f;
+    for (int i = 4 * static_cast<int>(threadIdx.x); i < k; i += 4 * static_cast<int>(blockDim.x)) {
+        const float4 a = *reinterpret_cast<const float4*>(x + i);
+        s += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+    }
+    return s;
+}
+
+template <int TYPE>
+__device__ void encode_x_loop_norm(const float* __restrict__ x, const float* __restrict__ nw, float rinv,
+                                   int units, int slots, uint4* xq) {
+    const int ntasks = slots * 8;
+    for (int task = threadIdx.x; task < ntasks; task += blockDim.x) {
+        float v[8], w[8];
+        load_x_task<TYPE>(x, units, task, v);
+        load_x_task<TYPE>(nw, units, task, w);
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = v[j] * rinv * w[j];
+        encode_x_task<TYPE>(task, units, slots, v, xq);
+    }
+}
+
 __device__ __forceinline__ void read_xslice(const uint4* xq, int slots, int u, XSlice& xs) {
     const uint4* q = xq + u;
 #pragma unroll

@@ -29,14 +29,6 @@
 namespace vb {
 namespace {
 
-constexpr int ACT_SILU = 0;
-constexpr int ACT_RELU2 = 1;
-
-__device__ __forceinline__ float act_pair(float g, float u, int kind) {
-    if (kind == ACT_SILU) return g / (1.0f + __expf(-g)) * u;
-    return fmaxf(g, 0.f) * fmaxf(u, 0.f);
-}
-
 // layout 0: hid[active[r]] = act(gu[2r], gu[2r+1]); the gate/up launch has
 // cleared hid, so positions off S stay 0.  One thread per active entry: one
 // load round, no search.  Indices outside [0, i) are dropped; a repeated

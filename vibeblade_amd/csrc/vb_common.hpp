@@ -151,4 +151,25 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Gated activations of an FFN neuron, act(g, u) with g = gate row . x and
+// u = up row . x:
+//   ACT_SILU       silu(g) * u = g / (1 + e^-g) * u
+//                  (cpp/src/fast_model.cpp:75, :952; vibeblade/sparse.py:269-272)
+//   ACT_RELU2      relu(g) * relu(u) (dReLU, ReLU after both projections)
+//   ACT_GELU_TANH  gelu_tanh(g) * u, gelu_tanh(g) = 0.5 g (1 + tanh(z)),
+//                  z = 0.7978845608 (g + 0.044715 g^3) (fast_model.cpp:944-948),
+//                  evaluated as g / (1 + e^(-2z)), the same function.
+constexpr int ACT_SILU = 0;
+constexpr int ACT_RELU2 = 1;
+constexpr int ACT_GELU_TANH = 2;
+
+__device__ __forceinline__ float act_pair(float g, float u, int kind) {
+    if (kind == ACT_SILU) return g / (1.0f + __expf(-g)) * u;
+    if (kind == ACT_GELU_TANH) {
+        const float z = 0.7978845608f * (g + 0.044715f * g * g * g);
+        return g / (1.0f + __expf(-2.0f * z)) * u;
+    }
+    return fmaxf(g, 0.f) * fmaxf(u, 0.f);
+}
+
 }  // namespace vb

@@ -14,12 +14,35 @@ struct RowSrc {
     int64_t nsrc = 0;  // rows of w / w2; gathered indices are clamped to [0, nsrc)
     int* zbuf = nullptr;
     int zn = 0;
+    // dense gate/up pairs: row r = row r/2 of w (r even) or of w2 (r odd),
+    // no index list (an FFN block: every neuron)
+    bool dense_pairs = false;
+};
+
+// Work fused into a block-quantized GEMV launch (Q4_K / Q6_K / Q8_0):
+//  norm_w  RMSNorm prologue: x is replaced by x * (1 / sqrt(mean(x^2) + eps))
+//          * norm_w inside the activation encode; every workgroup reduces
+//          sum(x^2) over all of x itself, in a fixed order.
+//  act     >= 0: pair epilogue.  Rows 2p and 2p+1 are the gate and up rows
+//          of neuron p, and the launch writes y[p] = act_pair(dot(2p),
+//          dot(2p+1), act) for p < n/2 instead of n dot products.
+//  resid   y[r] = dot(r) + resid[r] (resid may be y itself).
+struct GemvFuse {
+    const float* norm_w = nullptr;
+    float eps = 0.f;
+    int act = -1;
+    const float* resid = nullptr;
+    bool any() const { return norm_w != nullptr || act >= 0 || resid != nullptr; }
 };
 
 int gemv_dispatch(const void* w, const float* x, float* y, int64_t n, int64_t k, int32_t type,
                   hipStream_t st);
 int gemv_dispatch_src(const void* w, const RowSrc& src, const float* x, float* y, int64_t n, int64_t k,
                       int32_t type, hipStream_t st);
+// gemv_dispatch_src with fused prologue / epilogue work; VB_E_UNSUPPORTED
+// for types without it (F32 / F16) and for the int8-MFMA GEMV path.
+int gemv_dispatch_fused(const void* w, const RowSrc& src, const GemvFuse& fz, const float* x, float* y,
+                        int64_t n, int64_t k, int32_t type, hipStream_t st);
 // Q4_K M=1 GEMV on the int8 matrix cores (gemv_q4k_mfma.hip); arguments
 // already validated by gemv_dispatch_src.
 int gemv_q4k_mfma(const void* w, const RowSrc& src, const float* x, float* y, int64_t n, int64_t k,

@@ -164,6 +164,7 @@ def _workspace(nbytes: int, device) -> torch.Tensor:
 
 ACT_SILU = 0   # silu(g) * u
 ACT_RELU2 = 1  # relu(g) * relu(u)
+ACT_GELU_TANH = 2  # gelu_tanh(g) * u (GeGLU)
 DOWN_GGUF = 0          # down weight (h rows x i)
 DOWN_NEURON_MAJOR = 1  # down^T (i rows x h)
 
@@ -206,6 +207,34 @@ def sparse_ffn(gate: QTensor, up: QTensor, down: QTensor, x: torch.Tensor, activ
     _lib.call("vb_sparse_ffn", gate.ptr(), up.ptr(), down.ptr(), down_layout, x.data_ptr(),
               active.data_ptr() if n_active else None, n_active, act, out.data_ptr(), h, i, gate.qtype,
               ws.data_ptr(), ws.numel(), _stream())
+    return out
+
+
+def ffn_block(gate: QTensor, up: QTensor, down: QTensor, x: torch.Tensor, norm_w=None, eps: float = 1e-5,
+              act: int = ACT_SILU, residual: bool = True, out: torch.Tensor | None = None) -> torch.Tensor:
+    """One token through the FFN block: y = [x +] down(act(gate(n), up(n))),
+    n = rms_norm(x, norm_w, eps) (n = x without norm_w).  Two launches for
+    Q4_K / Q6_K / Q8_0 weights (vb_ffn_block).  ``out`` may be ``x``."""
+    hd, inter = gate.k, gate.rows
+    if up.shape != gate.shape or up.qtype != gate.qtype:
+        raise ValueError("ffn_block: gate and up must have one shape and type")
+    if down.shape != (hd, inter):
+        raise ValueError(f"ffn_block: down has shape {down.shape}, expected {(hd, inter)}")
+    dev = gate.device
+    x = _as_f32_dev(x, dev).reshape(-1)
+    if x.numel() != hd:
+        raise ValueError(f"ffn_block: x has {x.numel()} elements, expected {hd}")
+    nw = None
+    if norm_w is not None:
+        nw = _as_f32_dev(norm_w, dev).reshape(-1)
+        if nw.numel() != hd:
+            raise ValueError(f"ffn_block: norm_w has {nw.numel()} elements, expected {hd}")
+    if out is None:
+        out = torch.empty(hd, dtype=torch.float32, device=dev)
+    ws = _workspace(_lib.load().vb_ffn_block_workspace(hd, inter), dev)
+    _lib.call("vb_ffn_block", x.data_ptr(), None if nw is None else nw.data_ptr(), float(eps), gate.ptr(),
+              up.ptr(), gate.qtype, down.ptr(), down.qtype, hd, inter, int(act), int(bool(residual)),
+              out.data_ptr(), ws.data_ptr(), ws.numel(), _stream())
     return out
 
 
