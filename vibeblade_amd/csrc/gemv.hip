@@ -254,14 +254,18 @@ struct GemvShape {
 
 constexpr int kNumCUs = 256;
 
-// Ring depth for rpg rows per wave (sweeps on MI355X).  A ring of 2 keeps
-// each wave's requests spread over the weight stream: when the last bytes
-// arrive, a wave has one row left to compute, not all of them (with every
-// row in flight at once, 14336 x 4096 Q4_K ran 9.6 us against 8.5-8.8 us).
-// One row: no ring.  Q6_K units (14-17 VGPRs) and long row lists: 4.
+// Ring depth for rpg rows per wave and wpr k-slices per row (sweeps on
+// MI355X).  A ring of 2 keeps each wave's requests spread over the weight
+// stream: when the last bytes arrive, a wave has one row left to compute,
+// not all of them (with every row in flight at once, 14336 x 4096 Q4_K ran
+// 9.6 us against 8.5-8.8 us).  One row: no ring.  Q6_K units (14-17 VGPRs)
+// and long row lists: 4 -- except for split rows (wpr > 1) with up to 8
+// rows per wave, where a ring of 2 keeps the 16-wave workgroup (and its x
+// in registers): Q6_K 4096 x 14336 ran 15.6 us against 23.2 us at 4.
 template <int TYPE>
-int ring_depth(int rpg) {
+int ring_depth(int rpg, int wpr) {
     if (rpg <= 1) return 1;
+    if (wpr > 1 && rpg <= 8) return 2;
     if (TYPE == TYPE_Q6_K || rpg > 8) return rpg <= 2 ? 2 : 4;
     return 2;
 }
@@ -307,7 +311,7 @@ GemvShape gemv_shape(int64_t n, int units, bool even_rows = false) {
         const int d = std::atoi(rd);
         if (d >= 1 && d <= 4) ring = d;
     }
-    auto depth_of = [&](int rpg) { return ring ? ring : ring_depth<TYPE>(rpg); };
+    auto depth_of = [&](int rpg) { return ring ? ring : ring_depth<TYPE>(rpg, s.wpr); };
     // the block size must fit the launch bounds of the kernel of that depth
     if (64 * s.wpg > gemv_max_threads_host<TYPE>(depth_of(s.rpg))) s.wpg = 8 / s.wpr * s.wpr;
     if (s.wpg < s.wpr) s.wpg = s.wpr;
