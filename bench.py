@@ -179,8 +179,9 @@ def time_gemm(m, n, k, steps, warmup, ncopies):
     return ms, err
 
 
-def time_sparse(layout, steps, warmup, ncopies=8):
-    """TurboSparse FFN, H=4096, I=14336, Q4_K, S ~ Bernoulli(0.1), relu(g)*relu(u).
+def time_sparse(layout, steps, warmup, ncopies=8, block=False):
+    """TurboSparse FFN, H=4096, I=14336, Q4_K, S ~ Bernoulli(0.1), relu(g)*relu(u);
+    block: with the pre-FFN RMSNorm and the residual (vb_sparse_ffn_block).
     Returns (ms per call, |S|, algorithmic bytes)."""
     import torch
     from vibeblade_amd import _lib, ggml
@@ -202,8 +203,15 @@ def time_sparse(layout, steps, warmup, ncopies=8):
     nbytes = lib.vb_sparse_ffn_workspace(h, i, s.numel(), layout)
     ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
 
+    nw = 1.0 + 0.1 * torch.randn(h, generator=gen, device="cuda")
+
     def mk(g, u, d):
         def f(st):
+            if block:
+                _lib.check("vb_sparse_ffn_block", lib.vb_sparse_ffn_block(
+                    g.ptr(), u.ptr(), d.ptr(), layout, x.data_ptr(), nw.data_ptr(), 1e-5, s.data_ptr(),
+                    s.numel(), ACT_RELU2, 1, y.data_ptr(), h, i, g.qtype, ws.data_ptr(), ws.numel(), st))
+                return
             rc = lib.vb_sparse_ffn(g.ptr(), u.ptr(), d.ptr(), layout, x.data_ptr(), s.data_ptr(), s.numel(),
                                    ACT_RELU2, y.data_ptr(), h, i, g.qtype, ws.data_ptr(), ws.numel(), st)
             if rc != 0:
@@ -213,7 +221,7 @@ def time_sparse(layout, steps, warmup, ncopies=8):
     n_s = int(s.numel())
     rb = 2304
     down_b = h * 8064 if layout == 0 else n_s * rb
-    ab = 2 * n_s * rb + down_b + 4 * h + 4 * h + 4 * n_s
+    ab = 2 * n_s * rb + down_b + 4 * h + 4 * h + 4 * n_s + (8 * h if block else 0)
     return ms, n_s, ab
 
 
@@ -532,9 +540,10 @@ def main():
                               "rel_l2": e2}), file=sys.stderr, flush=True)
             del cps, yy
             torch.cuda.empty_cache()
-        for layout in (1, 0):
-            ms4, n_s, b4 = time_sparse(layout, 400, 40)
-            print(json.dumps({"workload": f"TurboSparse FFN H=4096 I=14336 |S|={n_s} down_layout={layout}",
+        for layout, block in ((1, False), (0, False), (1, True), (0, True)):
+            ms4, n_s, b4 = time_sparse(layout, 400, 40, block=block)
+            what = "block (RMSNorm + FFN + residual)" if block else "FFN"
+            print(json.dumps({"workload": f"TurboSparse {what} H=4096 I=14336 |S|={n_s} down_layout={layout}",
                               "us_per_call": round(ms4 * 1e3, 3), "alg_bytes": b4,
                               "GB/s": round(b4 / (ms4 * 1e-3) / 1e9, 1),
                               "frac_hbm": round(b4 / (ms4 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}),

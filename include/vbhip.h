@@ -72,6 +72,14 @@ int vb_stream_destroy(void* stream);
 int vb_dequant_rows(const void* w, float* out, int64_t n_rows, int64_t k,
                     int32_t ggml_type, void* stream);
 
+/* out[t, :] = decoded row tokens[t] of table (n_vocab rows x k, GGUF layout)
+ * for t < n_tokens; ids outside [0, n_vocab) give a row of zeros.  The
+ * token-embedding lookup of the decode step, dequantize_row of row token_id
+ * (cpp/src/fast_model.cpp:1042-1046), on the device for device token ids.
+ * Bit-exact as vb_dequant_rows.  out: 16-byte aligned for block types. */
+int vb_embed_rows(const void* table, int32_t ggml_type, int64_t n_vocab, int64_t k, const int32_t* tokens,
+                  int64_t n_tokens, float* out, void* stream);
+
 /* ---- quantize (no reference counterpart: the reference has no
  * quantizer; this writes the same blocks as the CPU oracle's quantizer and
  * exists so callers can build GGUF tensors on the device) ---------------- */
@@ -106,7 +114,8 @@ int vb_gemm(const void* w, const void* x, int32_t x_dtype, float* y, int64_t m, 
  * the active set are read from Wg / Wu.  active: sorted ascending, unique,
  * within [0, i) (indices outside are clamped, never dereferenced).
  * act_kind: 0 = silu(g) * u (vibeblade/sparse.py:269-272),
- *           1 = relu(g) * relu(u) (ReLU after both projections).
+ *           1 = relu(g) * relu(u) (ReLU after both projections),
+ *           2 = gelu_tanh(g) * u (GeGLU, cpp/src/fast_model.cpp:943-948).
  * down_layout: 0 = GGUF down, Wd is h rows x i (all of Wd is read);
  *              1 = neuron-major down, Wd holds W_down^T as i rows x h and
  *                  only the active rows are read (Q4_K only).
@@ -119,6 +128,19 @@ int vb_sparse_ffn(const void* wg, const void* wu, const void* wd, int32_t down_l
                   const float* x, const int32_t* active, int32_t n_active, int32_t act_kind,
                   float* y, int64_t h, int64_t i, int32_t ggml_type, void* workspace,
                   size_t workspace_bytes, void* stream);
+/* The TurboSparse FFN block: vb_sparse_ffn over n = x / sqrt(mean(x^2) +
+ * eps) * norm_w (n = x when norm_w is NULL), plus x when add_residual != 0;
+ * y may be x.  The sparse branch of the decoder layer with its pre-FFN
+ * RMSNorm and residual (vibeblade/transformer.py:789-815 with
+ * _sparse_ffn_layer :211-229; cpp/src/fast_model.cpp:837-840, :915-940,
+ * :966-975).  The norm runs inside the gate/up encode and the residual in
+ * the launch that writes y (neuron-major Q4_K, h <= 4096: 2 launches).
+ * Same workspace as vb_sparse_ffn; x and norm_w 16-byte aligned. */
+int vb_sparse_ffn_block(const void* wg, const void* wu, const void* wd, int32_t down_layout,
+                        const float* x, const float* norm_w, float eps, const int32_t* active,
+                        int32_t n_active, int32_t act_kind, int32_t add_residual, float* y, int64_t h,
+                        int64_t i, int32_t ggml_type, void* workspace, size_t workspace_bytes,
+                        void* stream);
 
 /* ---- FFN block, one token ------------------------------------------------
  * y = [x +] Wd act(Wg n, Wu n), n = x / sqrt(mean(x^2) + eps) * norm_w

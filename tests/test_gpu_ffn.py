@@ -326,3 +326,55 @@ def test_ffn_block_repeatable_and_errors():
         ffn_block(gq, uq, dq, torch.zeros(1000, device="cuda"))
     with pytest.raises(ValueError):  # misaligned x
         ffn_block(gq, uq, dq, torch.zeros(1025, device="cuda")[1:])
+
+
+# ---- TurboSparse block (vb_sparse_ffn_block): RMSNorm + sparse FFN + residual ----
+
+def sparse_block_case(h, i, qtype, layout, act, norm, residual, seed, frac=0.1, inplace=False, empty=False):
+    gq, uq, dq, gd, ud, dd = ffn_weights(h, i, qtype, seed, layout)
+    rng = np.random.default_rng(seed + 1)
+    s = np.zeros(0, np.int32) if empty else np.flatnonzero(rng.random(i) < frac).astype(np.int32)
+    x = rng.standard_normal(h).astype(np.float32)
+    nw = (1.0 + 0.1 * rng.standard_normal(h)).astype(np.float32) if norm else None
+    xt = torch.from_numpy(x).cuda()
+    y = sparse_ffn(gq, uq, dq, xt, torch.from_numpy(s), act, layout, out=xt if inplace else None,
+                   norm_w=None if nw is None else torch.from_numpy(nw), eps=1e-5, residual=residual)
+    y = y.cpu().numpy()
+    xin = x if nw is None else O.rms_norm(x, nw, 1e-5)
+    f = O.sparse_ffn(gd, ud, dd, xin, s, act)[0] if s.size else np.zeros(h)
+    if empty:
+        assert np.array_equal(y, x if residual else np.zeros(h, np.float32))
+    else:
+        assert O.rel_l2(y - (x if residual else 0), f) <= 1e-3
+    return y
+
+
+@pytest.mark.parametrize("layout", [DOWN_GGUF, DOWN_NEURON_MAJOR])
+@pytest.mark.parametrize("act", [ACT_SILU, ACT_RELU2, ACT_GELU_TANH])
+def test_sparse_block_config_shape(layout, act):
+    sparse_block_case(4096, 14336, Q4K, layout, act, norm=True, residual=True, seed=50)
+
+
+@pytest.mark.parametrize("fused_env", [None, "0"])
+@pytest.mark.parametrize("norm,residual,inplace", [(True, False, False), (False, True, True), (True, True, True)])
+def test_sparse_block_options_neuron_major(monkeypatch, fused_env, norm, residual, inplace):
+    if fused_env is not None:
+        monkeypatch.setenv("VB_SPARSE_FUSED", fused_env)
+    sparse_block_case(2048, 4096, Q4K, DOWN_NEURON_MAJOR, ACT_SILU, norm, residual, seed=51, inplace=inplace)
+
+
+@pytest.mark.parametrize("qtype", [Q4K, ggml.GGML_TYPE_Q6_K, ggml.GGML_TYPE_Q8_0, ggml.GGML_TYPE_F32])
+def test_sparse_block_types_gguf_down(qtype):
+    sparse_block_case(512, 1024, qtype, DOWN_GGUF, ACT_SILU, norm=True, residual=True, seed=52, frac=0.3)
+    sparse_block_case(512, 1024, qtype, DOWN_GGUF, ACT_RELU2, norm=True, residual=True, seed=53, frac=0.3,
+                      inplace=True)
+
+
+def test_sparse_block_long_rows_and_empty():
+    """h = 8192: the gathered GEMV path of the neuron-major layout (no fused
+    kernel above h = 4096); an empty active set leaves y = x (or 0)."""
+    sparse_block_case(8192, 2048, Q4K, DOWN_NEURON_MAJOR, ACT_SILU, norm=True, residual=True, seed=54)
+    for layout in (DOWN_GGUF, DOWN_NEURON_MAJOR):
+        for residual in (True, False):
+            sparse_block_case(1024, 512, Q4K, layout, ACT_SILU, True, residual, seed=55, empty=True,
+                              inplace=residual)

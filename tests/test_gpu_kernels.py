@@ -190,3 +190,33 @@ def test_gemv_config_shapes(qtype, rows, k):
     if rows * k <= 14336 * 4096:
         got = qt.dequantize().cpu().numpy()
         assert np.array_equal(bits(got), bits(O.dequantize(qt.to_numpy_bytes(), k, qtype)))
+
+
+@pytest.mark.parametrize("qtype", QTYPES + [ggml.GGML_TYPE_F32, ggml.GGML_TYPE_F16])
+def test_embed_rows_bit_exact(qtype):
+    """Token-embedding rows decoded from device ids: equal to the oracle's
+    decode of the same rows; ids outside the table give zero rows."""
+    from vibeblade_amd.tensor import embed_rows
+    vocab, k = 1000, 512
+    rng = np.random.default_rng(77)
+    if qtype in QTYPES:
+        rb = ggml.row_bytes(qtype, k)
+        raw = rng.integers(0, 256, (vocab, rb), dtype=np.uint8)
+        be, bb = ggml.BLOCK[qtype]
+        blk = raw.reshape(-1, bb)
+        offs = {ggml.GGML_TYPE_Q4_K: [0, 2], ggml.GGML_TYPE_Q6_K: [208], ggml.GGML_TYPE_Q8_0: [0]}[qtype]
+        for o in offs:
+            blk[:, o + 1] &= 0x7B  # finite fp16 scales
+        want_all = O.dequantize(raw, k, qtype)
+    else:
+        w = rand_weights(vocab, k, 5)
+        raw = w if qtype == ggml.GGML_TYPE_F32 else w.astype(np.float16)
+        want_all = raw.astype(np.float32)
+        raw = np.frombuffer(raw.tobytes(), np.uint8).reshape(vocab, -1)
+    table = QTensor.from_bytes(raw, qtype, vocab, k)
+    ids = np.array([0, 999, 17, 17, -1, 1000, 500, 2 ** 31 - 1], np.int32)
+    got = embed_rows(table, torch.from_numpy(ids)).cpu().numpy()
+    for t, i in enumerate(ids):
+        want = want_all[i] if 0 <= i < vocab else np.zeros(k, np.float32)
+        assert np.array_equal(bits(got[t]), bits(want)), (t, i)
+    assert embed_rows(table, torch.zeros(0, dtype=torch.int32)).shape == (0, k)

@@ -35,6 +35,7 @@ SIGNATURES = {
     "vb_stream_destroy": (ctypes.c_int, [_vp]),
     "vb_dequant_rows": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _vp]),
     "vb_quantize_rows": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _vp]),
+    "vb_embed_rows": (ctypes.c_int, [_vp, _i32, _i64, _i64, _vp, _i64, _vp, _vp]),
     "vb_gemv": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i32, _vp]),
     "vb_gemm": (ctypes.c_int, [_vp, _vp, _i32, _vp, _i64, _i64, _i64, _i32, _i32, _vp]),
     "vb_sparse_ffn_workspace": (_i64, [_i64, _i64, _i32, _i32]),
@@ -43,6 +44,8 @@ SIGNATURES = {
     "vb_ffn_block_workspace": (_i64, [_i64, _i64]),
     "vb_ffn_block": (ctypes.c_int, [_vp, _vp, ctypes.c_float, _vp, _vp, _i32, _vp, _i32, _i64, _i64, _i32,
                                     _i32, _vp, _vp, _sz, _vp]),
+    "vb_sparse_ffn_block": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp, _vp, ctypes.c_float, _vp, _i32, _i32, _i32,
+                                           _vp, _i64, _i64, _i32, _vp, _sz, _vp]),
     "vb_topk_indices": (ctypes.c_int, [_vp, _i64, _i32, _vp, _vp]),
     "vb_moe_workspace": (_i64, [_i32, _i32, _i64, _i64]),
     "vb_moe_grouped_ffn": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _i64,

@@ -29,17 +29,9 @@ __device__ __forceinline__ void q4k_scale_min(int j, const uint8_t* s, float& sc
     }
 }
 
-// One thread decodes 4 consecutive elements (e0 .. e0+3) of one row.
+// Elements e0 .. e0+3 of the row at rp (e0 a multiple of 4).
 template <int TYPE>
-__global__ void __launch_bounds__(256) dequant_kernel(const uint8_t* __restrict__ w,
-                                                      float* __restrict__ out, int64_t n_groups,
-                                                      int64_t k, int64_t rb) {
-    const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (g >= n_groups) return;
-    const int64_t gpr = k / 4;
-    const int64_t row = g / gpr;
-    const int64_t e0 = (g - row * gpr) * 4;
-    const uint8_t* rp = w + row * rb;
+__device__ __forceinline__ float4 decode4(const uint8_t* __restrict__ rp, int64_t e0) {
     float4 y;
     if constexpr (TYPE == TYPE_Q4_K) {
         const uint8_t* b = rp + (e0 / 256) * 144;
@@ -82,7 +74,49 @@ __global__ void __launch_bounds__(256) dequant_kernel(const uint8_t* __restrict_
         y.z = static_cast<float>(static_cast<int8_t>((q >> 16) & 0xff)) * d;
         y.w = static_cast<float>(static_cast<int8_t>(q >> 24)) * d;
     }
-    *reinterpret_cast<float4*>(out + row * k + e0) = y;
+    return y;
+}
+
+// One thread decodes 4 consecutive elements (e0 .. e0+3) of one row.
+template <int TYPE>
+__global__ void __launch_bounds__(256) dequant_kernel(const uint8_t* __restrict__ w,
+                                                      float* __restrict__ out, int64_t n_groups,
+                                                      int64_t k, int64_t rb) {
+    const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (g >= n_groups) return;
+    const int64_t gpr = k / 4;
+    const int64_t row = g / gpr;
+    const int64_t e0 = (g - row * gpr) * 4;
+    *reinterpret_cast<float4*>(out + row * k + e0) = decode4<TYPE>(w + row * rb, e0);
+}
+
+// Row gather: out row t = decoded row ids[t] of w (zeros for ids outside
+// [0, n_src)).  Block types: 4 elements per thread; F32 / F16: 1.
+template <int TYPE>
+__global__ void __launch_bounds__(256) gather_rows_kernel(const uint8_t* __restrict__ w,
+                                                          const int32_t* __restrict__ ids, int64_t n_src,
+                                                          float* __restrict__ out, int64_t n_items, int64_t k,
+                                                          int64_t rb) {
+    const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (g >= n_items) return;
+    constexpr int64_t PER = (TYPE == TYPE_F32 || TYPE == TYPE_F16) ? 1 : 4;
+    const int64_t ipr = k / PER;
+    const int64_t t = g / ipr;
+    const int64_t e0 = (g - t * ipr) * PER;
+    const int32_t id = ids[t];
+    const bool ok = id >= 0 && id < n_src;
+    const uint8_t* rp = w + (ok ? static_cast<int64_t>(id) : 0) * rb;
+    if constexpr (PER == 1) {
+        float v;
+        if constexpr (TYPE == TYPE_F32)
+            v = reinterpret_cast<const float*>(rp)[e0];
+        else
+            v = __half2float(reinterpret_cast<const __half*>(rp)[e0]);
+        out[t * k + e0] = ok ? v : 0.f;
+    } else {
+        const float4 y = decode4<TYPE>(rp, e0);
+        *reinterpret_cast<float4*>(out + t * k + e0) = ok ? y : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
 }
 
 // F32 / F16: one thread per element (any k).
@@ -294,4 +328,43 @@ extern "C" int vb_quantize_rows(const float* src, void* w, int64_t n_rows, int64
     case TYPE_F16: return launch_quantize<TYPE_F16>(src, w, n_blocks, st);
     default: set_error("vb_quantize_rows: unsupported type %d", ggml_type); return E_UNSUPPORTED;
     }
+}
+
+extern "C" int vb_embed_rows(const void* table, int32_t ggml_type, int64_t n_vocab, int64_t k,
+                             const int32_t* tokens, int64_t n_tokens, float* out, void* stream) {
+    const int64_t rb = row_bytes(ggml_type, k);
+    if (rb < 0) {
+        set_error("vb_embed_rows: unsupported type %d or k=%lld not a whole number of blocks", ggml_type,
+                  static_cast<long long>(k));
+        return E_INVAL;
+    }
+    if (n_tokens < 0 || n_vocab <= 0 || (n_tokens > 0 && (!table || !tokens || !out))) {
+        set_error("vb_embed_rows: bad arguments (n_vocab=%lld, n_tokens=%lld)", static_cast<long long>(n_vocab),
+                  static_cast<long long>(n_tokens));
+        return E_INVAL;
+    }
+    if (n_tokens == 0) return OK;
+    const bool plain = ggml_type == TYPE_F32 || ggml_type == TYPE_F16;
+    if (!plain && reinterpret_cast<uintptr_t>(out) % 16 != 0) {
+        set_error("vb_embed_rows: out must be 16-byte aligned for block types");
+        return E_INVAL;
+    }
+    const int64_t n_items = n_tokens * (plain ? k : k / 4);
+    const int64_t grid = (n_items + 255) / 256;
+    if (grid > 0x7fffffff) {
+        set_error("vb_embed_rows: too many rows for one launch");
+        return E_INVAL;
+    }
+    hipStream_t st = as_stream(stream);
+    const uint8_t* wb = static_cast<const uint8_t*>(table);
+    const dim3 g(static_cast<uint32_t>(grid)), b(256);
+    switch (ggml_type) {
+    case TYPE_Q4_K: gather_rows_kernel<TYPE_Q4_K><<<g, b, 0, st>>>(wb, tokens, n_vocab, out, n_items, k, rb); break;
+    case TYPE_Q6_K: gather_rows_kernel<TYPE_Q6_K><<<g, b, 0, st>>>(wb, tokens, n_vocab, out, n_items, k, rb); break;
+    case TYPE_Q8_0: gather_rows_kernel<TYPE_Q8_0><<<g, b, 0, st>>>(wb, tokens, n_vocab, out, n_items, k, rb); break;
+    case TYPE_F32: gather_rows_kernel<TYPE_F32><<<g, b, 0, st>>>(wb, tokens, n_vocab, out, n_items, k, rb); break;
+    case TYPE_F16: gather_rows_kernel<TYPE_F16><<<g, b, 0, st>>>(wb, tokens, n_vocab, out, n_items, k, rb); break;
+    default: set_error("vb_embed_rows: unsupported type %d", ggml_type); return E_UNSUPPORTED;
+    }
+    return check_launch("vb_embed_rows");
 }

@@ -59,7 +59,7 @@ constexpr int DOWN_BATCH = 6;              // rows per thread and load batch
 // fixed order (deterministic).
 __global__ void __launch_bounds__(DOWN_THREADS) down_rows_q4k_kernel(
     const uint8_t* __restrict__ d, int64_t rb, int64_t i_dim, const int32_t* __restrict__ active,
-    int n_active, const float* __restrict__ gu, int kind, float* __restrict__ y) {
+    int n_active, const float* __restrict__ gu, int kind, const float* resid, float* y) {
     __shared__ float red[DOWN_RG][65];
     __shared__ float red2[DOWN_THREADS / 64][64];
     const int u = blockIdx.x;
@@ -137,7 +137,8 @@ __global__ void __launch_bounds__(DOWN_THREADS) down_rows_q4k_kernel(
         float sum = 0.f;
 #pragma unroll
         for (int k = 0; k < DOWN_THREADS / 64; k++) sum += red2[k][t];
-        y[64 * static_cast<int64_t>(u) + t] = sum;
+        const int64_t col = 64 * static_cast<int64_t>(u) + t;
+        y[col] = resid ? sum + resid[col] : sum;  // resid may be y: read before the write
     }
 }
 
@@ -202,11 +203,11 @@ __device__ __forceinline__ void unit_axpy(const gemvc::Q4KUnit& v, const gemvc::
     }
 }
 
-template <int NPW>
+template <int NPW, bool NORM>
 __global__ void __launch_bounds__(512) sparse_fused_q4k_kernel(
     const uint8_t* __restrict__ wg, const uint8_t* __restrict__ wu, const uint8_t* __restrict__ wd, int64_t rb,
     int64_t i_dim, const float* __restrict__ x, const int32_t* __restrict__ active, int n_active, int kind,
-    float* __restrict__ partial, int units, int slots) {
+    float* __restrict__ partial, int units, int slots, const float* __restrict__ norm_w, float eps) {
     using namespace gemvc;
     // the x encoding (slots x 11 uint4), later the 8 waves' partials
     __shared__ uint4 lds[8 * 64 * FUSED_RED_PITCH / 4];
@@ -232,8 +233,12 @@ __global__ void __launch_bounds__(512) sparse_fused_q4k_kernel(
     // x first, then every weight row of the wave, then the encode (which
     // waits for x only)
     XTasks xt;
+    [[maybe_unused]] XTasks nt;  // norm weights of the same tasks (NORM)
     const bool x_in_regs = slots * 8 <= XT_MAX * static_cast<int>(blockDim.x);
     if (x_in_regs) prefetch_x<TYPE_Q4_K>(x, units, slots, xt);
+    if constexpr (NORM) {
+        if (x_in_regs) prefetch_x<TYPE_Q4_K>(norm_w, units, slots, nt);
+    }
     __builtin_amdgcn_sched_barrier(0);
     Q4KUnit vg[NPW], vu[NPW], vd[NPW];
 #pragma unroll
@@ -244,10 +249,25 @@ __global__ void __launch_bounds__(512) sparse_fused_q4k_kernel(
         load_unit(wd + off, uc, vd[k]);
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (x_in_regs)
-        encode_x_regs<TYPE_Q4_K>(units, slots, xt, lds);
-    else
-        encode_x_loop<TYPE_Q4_K>(x, units, slots, lds);
+    if constexpr (NORM) {
+        // RMSNorm inside the encode; the reduction's scratch sits past the
+        // x encoding and is read before the barrier after the encode
+        float* scratch = reinterpret_cast<float*>(lds + XQ_QUADS * slots);
+        const float ss = wg_sum_fixed(x_in_regs ? sumsq_tasks(units, slots, xt) : sumsq_loop(x, units * 64),
+                                      scratch);
+        const float rinv = rms_inv(ss, units * 64, eps);
+        if (x_in_regs) {
+            scale_tasks(xt, nt, rinv);
+            encode_x_regs<TYPE_Q4_K>(units, slots, xt, lds);
+        } else {
+            encode_x_loop_norm<TYPE_Q4_K>(x, norm_w, rinv, units, slots, lds);
+        }
+    } else {
+        if (x_in_regs)
+            encode_x_regs<TYPE_Q4_K>(units, slots, xt, lds);
+        else
+            encode_x_loop<TYPE_Q4_K>(x, units, slots, lds);
+    }
     __syncthreads();
     XSlice xs;
     read_xslice(lds, slots, valid ? lane : 0, xs);
@@ -287,7 +307,7 @@ __global__ void __launch_bounds__(512) sparse_fused_q4k_kernel(
 // y[64 b + c] = sum over the nblk partials in order; thread t: column c = t %
 // 64, partials t / 64, t / 64 + 16, ...
 __global__ void __launch_bounds__(1024) sparse_reduce_kernel(const float* __restrict__ partial, int nblk,
-                                                             float* __restrict__ y) {
+                                                             const float* resid, float* y) {
     __shared__ float red[16][64];
     const int c = threadIdx.x & 63, bg = threadIdx.x >> 6;
     const int col = static_cast<int>(blockIdx.x) * 64 + c;
@@ -309,7 +329,7 @@ __global__ void __launch_bounds__(1024) sparse_reduce_kernel(const float* __rest
         float t = 0.f;
 #pragma unroll
         for (int k = 0; k < 16; k++) t += red[k][c];
-        y[col] = t;
+        y[col] = resid ? t + resid[col] : t;  // resid may be y: read before the write
     }
 }
 
@@ -398,7 +418,7 @@ __global__ void __launch_bounds__(1024) topk_kernel(const float* __restrict__ v,
 size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
 
 struct SparseWs {
-    size_t gu, hid, total;
+    size_t gu, hid, xn, total;
 };
 
 // The fused layout-1 path (h <= 4096) takes ceil(n_active / (8 * neurons per
@@ -420,13 +440,159 @@ SparseWs sparse_ws(int64_t h, int64_t i, int32_t n_active, int32_t layout) {
         const size_t fused = align256((nblk > 0 ? nblk : 1) * FUSED_STRIDE * sizeof(float));
         off = off > fused ? off : fused;
     }
-    w.total = off;
+    // the normalised x of the block entry when its types cannot fuse the norm
+    w.xn = off;
+    w.total = off + align256(static_cast<size_t>(h) * sizeof(float));
     return w;
 }
 
 __global__ void fill_zero_kernel(float* p, int64_t n) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i < n) p[i] = 0.f;
+}
+
+// y = a + b (y may be a or b)
+__global__ void add_vec_kernel(const float* a, const float* b, float* y, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = a[i] + b[i];
+}
+
+__global__ void copy_vec_kernel(const float* a, float* y, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = a[i];
+}
+
+bool block_type(int32_t t) { return t == TYPE_Q4_K || t == TYPE_Q6_K || t == TYPE_Q8_0; }
+
+template <int NPW>
+void launch_fused(bool norm, dim3 g, hipStream_t st, const void* wg, const void* wu, const void* wd, int64_t rb,
+                  int64_t i, const float* x, const int32_t* active, int n_active, int act_kind, float* part,
+                  int units, int slots, const float* norm_w, float eps) {
+    const uint8_t* a = static_cast<const uint8_t*>(wg);
+    const uint8_t* b = static_cast<const uint8_t*>(wu);
+    const uint8_t* c = static_cast<const uint8_t*>(wd);
+    if (norm)
+        sparse_fused_q4k_kernel<NPW, true><<<g, dim3(512), 0, st>>>(a, b, c, rb, i, x, active, n_active, act_kind,
+                                                                     part, units, slots, norm_w, eps);
+    else
+        sparse_fused_q4k_kernel<NPW, false><<<g, dim3(512), 0, st>>>(a, b, c, rb, i, x, active, n_active,
+                                                                      act_kind, part, units, slots, norm_w, eps);
+}
+
+// The sparse FFN with an optional RMSNorm of x (norm_w) and residual (the x
+// term added to y).  y may be x.
+int sparse_ffn_impl(const void* wg, const void* wu, const void* wd, int32_t down_layout, const float* x,
+                    const float* norm_w, float eps, const int32_t* active, int32_t n_active, int32_t act_kind,
+                    bool residual, float* y, int64_t h, int64_t i, int32_t ggml_type, void* workspace,
+                    size_t workspace_bytes, hipStream_t st, const char* fn) {
+    if (h <= 0 || i <= 0 || h > INT32_MAX || i > INT32_MAX || n_active < 0 || n_active > i ||
+        (down_layout != 0 && down_layout != 1) ||
+        (act_kind != ACT_SILU && act_kind != ACT_RELU2 && act_kind != ACT_GELU_TANH) || !wg || !wu || !wd || !x ||
+        !y || (n_active > 0 && !active) || !(eps >= 0.f)) {
+        set_error("%s: bad arguments", fn);
+        return E_INVAL;
+    }
+    if (row_bytes(ggml_type, h) < 0 || row_bytes(ggml_type, i) < 0) {
+        set_error("%s: type %d unsupported for h=%lld i=%lld", fn, ggml_type, static_cast<long long>(h),
+                  static_cast<long long>(i));
+        return E_UNSUPPORTED;
+    }
+    if (down_layout == 1 && (ggml_type != TYPE_Q4_K || h % 64 != 0)) {
+        set_error("%s: neuron-major down (layout 1) needs Q4_K and h %% 64 == 0", fn);
+        return E_UNSUPPORTED;
+    }
+    const SparseWs ws = sparse_ws(h, i, n_active, down_layout);
+    if (!workspace || workspace_bytes < ws.total) {
+        set_error("%s: workspace of %zu bytes needed", fn, ws.total);
+        return E_NOMEM;
+    }
+    if (norm_w && (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(norm_w) % 16 != 0)) {
+        set_error("%s: x and norm_w must be 16-byte aligned", fn);
+        return E_INVAL;
+    }
+    uint8_t* wsb = static_cast<uint8_t*>(workspace);
+    float* gu = reinterpret_cast<float*>(wsb + ws.gu);
+    const float* resid = residual ? x : nullptr;
+    const dim3 vec_grid(static_cast<uint32_t>((h + 255) / 256));
+
+    if (n_active == 0) {  // no active neuron: y = x or 0
+        if (residual) {
+            if (y != x) copy_vec_kernel<<<vec_grid, dim3(256), 0, st>>>(x, y, h);
+        } else {
+            fill_zero_kernel<<<vec_grid, dim3(256), 0, st>>>(y, h);
+        }
+        return check_launch(fn);
+    }
+    // a norm the gate/up launch cannot fuse (F32 / F16 weights) runs first
+    const float* xin = x;
+    const float* nw = norm_w;
+    if (norm_w && !block_type(ggml_type)) {
+        float* xn = reinterpret_cast<float*>(wsb + ws.xn);
+        const int rc = vb_rms_norm(x, norm_w, xn, 1, h, eps, st);
+        if (rc != OK) return rc;
+        xin = xn;
+        nw = nullptr;
+    }
+    if (fused_path(h, down_layout)) {
+        // one launch for gate/up/act/down, one for the partial sums
+        if (reinterpret_cast<uintptr_t>(xin) % 16 != 0) {
+            set_error("%s: x must be 16-byte aligned", fn);
+            return E_INVAL;
+        }
+        const int units = static_cast<int>(h / 64);
+        const int slots = (units + 7) & ~7;  // gemv_core.hpp: encoded units, a multiple of 8
+        const char* ne = std::getenv("VB_SPARSE_NPW");
+        const int npw = ne && ne[0] == '2' ? 2 : FUSED_NPW;
+        const int nblk = (n_active + 8 * npw - 1) / (8 * npw);
+        float* part = reinterpret_cast<float*>(wsb);
+        const dim3 g(static_cast<uint32_t>(nblk));
+        const int64_t rb = row_bytes(TYPE_Q4_K, h);
+        if (npw == 2)
+            launch_fused<2>(nw != nullptr, g, st, wg, wu, wd, rb, i, xin, active, n_active, act_kind, part, units,
+                            slots, nw, eps);
+        else
+            launch_fused<FUSED_NPW>(nw != nullptr, g, st, wg, wu, wd, rb, i, xin, active, n_active, act_kind, part,
+                                    units, slots, nw, eps);
+        int rcf = check_launch(fn);
+        if (rcf != OK) return rcf;
+        sparse_reduce_kernel<<<dim3(static_cast<uint32_t>(units)), dim3(1024), 0, st>>>(part, nblk, resid, y);
+        return check_launch(fn);
+    }
+    // 1. gate/up on the active rows (with the norm in the encode)
+    RowSrc src;
+    src.w2 = wu;
+    src.gidx = active;
+    src.nsrc = i;
+    float* hid = reinterpret_cast<float*>(wsb + ws.hid);
+    if (down_layout == 0) {  // the dense hidden vector starts at zero
+        src.zbuf = reinterpret_cast<int*>(hid);
+        src.zn = static_cast<int>(i);
+    }
+    GemvFuse fz;
+    fz.norm_w = nw;
+    fz.eps = eps;
+    int rc = gemv_dispatch_fused(wg, src, fz, xin, gu, 2 * static_cast<int64_t>(n_active), h, ggml_type, st);
+    if (rc != OK) return rc;
+    // 2. down (with the residual in the launch that writes y)
+    if (down_layout == 0) {
+        scatter_act_kernel<<<dim3(static_cast<uint32_t>((n_active + 255) / 256)), dim3(256), 0, st>>>(
+            active, n_active, gu, act_kind, hid, i);
+        if ((rc = check_launch(fn)) != OK) return rc;
+        if (!residual) return gemv_dispatch(wd, hid, y, h, i, ggml_type, st);
+        if (block_type(ggml_type)) {
+            GemvFuse fd;
+            fd.resid = x;
+            return gemv_dispatch_fused(wd, RowSrc{}, fd, hid, y, h, i, ggml_type, st);
+        }
+        // F32 / F16 down: the product into the workspace, then the add
+        float* dn = reinterpret_cast<float*>(wsb + ws.xn);
+        if ((rc = gemv_dispatch(wd, hid, dn, h, i, ggml_type, st)) != OK) return rc;
+        add_vec_kernel<<<vec_grid, dim3(256), 0, st>>>(x, dn, y, h);
+        return check_launch(fn);
+    }
+    down_rows_q4k_kernel<<<dim3(static_cast<uint32_t>(h / 64)), dim3(DOWN_THREADS), 0, st>>>(
+        static_cast<const uint8_t*>(wd), row_bytes(TYPE_Q4_K, h), i, active, n_active, gu, act_kind, resid, y);
+    return check_launch(fn);
 }
 
 }  // namespace
@@ -443,81 +609,17 @@ extern "C" int vb_sparse_ffn(const void* wg, const void* wu, const void* wd, int
                              const float* x, const int32_t* active, int32_t n_active, int32_t act_kind,
                              float* y, int64_t h, int64_t i, int32_t ggml_type, void* workspace,
                              size_t workspace_bytes, void* stream) {
-    hipStream_t st = as_stream(stream);
-    if (h <= 0 || i <= 0 || h > INT32_MAX || i > INT32_MAX || n_active < 0 || n_active > i ||
-        (down_layout != 0 && down_layout != 1) || (act_kind != ACT_SILU && act_kind != ACT_RELU2) || !wg || !wu ||
-        !wd || !x || !y || (n_active > 0 && !active)) {
-        set_error("vb_sparse_ffn: bad arguments");
-        return E_INVAL;
-    }
-    if (row_bytes(ggml_type, h) < 0 || row_bytes(ggml_type, i) < 0) {
-        set_error("vb_sparse_ffn: type %d unsupported for h=%lld i=%lld", ggml_type, static_cast<long long>(h),
-                  static_cast<long long>(i));
-        return E_UNSUPPORTED;
-    }
-    if (down_layout == 1 && (ggml_type != TYPE_Q4_K || h % 64 != 0)) {
-        set_error("vb_sparse_ffn: neuron-major down (layout 1) needs Q4_K and h %% 64 == 0");
-        return E_UNSUPPORTED;
-    }
-    const SparseWs ws = sparse_ws(h, i, n_active, down_layout);
-    if (!workspace || workspace_bytes < ws.total) {
-        set_error("vb_sparse_ffn: workspace of %zu bytes needed", ws.total);
-        return E_NOMEM;
-    }
-    uint8_t* wsb = static_cast<uint8_t*>(workspace);
-    float* gu = reinterpret_cast<float*>(wsb + ws.gu);
+    return sparse_ffn_impl(wg, wu, wd, down_layout, x, nullptr, 0.f, active, n_active, act_kind, false, y, h, i,
+                           ggml_type, workspace, workspace_bytes, as_stream(stream), "vb_sparse_ffn");
+}
 
-    if (n_active == 0) {  // no active neuron: y = 0
-        fill_zero_kernel<<<dim3(static_cast<uint32_t>((h + 255) / 256)), dim3(256), 0, st>>>(y, h);
-        return check_launch("vb_sparse_ffn");
-    }
-    if (fused_path(h, down_layout)) {
-        // one launch for gate/up/act/down, one for the partial sums
-        if (reinterpret_cast<uintptr_t>(x) % 16 != 0) {
-            set_error("vb_sparse_ffn: x must be 16-byte aligned");
-            return E_INVAL;
-        }
-        const int units = static_cast<int>(h / 64);
-        const int slots = (units + 7) & ~7;  // gemv_core.hpp: encoded units, a multiple of 8
-        const char* ne = std::getenv("VB_SPARSE_NPW");
-        const int npw = ne && ne[0] == '2' ? 2 : FUSED_NPW;
-        const int nblk = (n_active + 8 * npw - 1) / (8 * npw);
-        float* part = reinterpret_cast<float*>(wsb);
-        if (npw == 2)
-            sparse_fused_q4k_kernel<2><<<dim3(static_cast<uint32_t>(nblk)), dim3(512), 0, st>>>(
-                static_cast<const uint8_t*>(wg), static_cast<const uint8_t*>(wu), static_cast<const uint8_t*>(wd),
-                row_bytes(TYPE_Q4_K, h), i, x, active, n_active, act_kind, part, units, slots);
-        else
-            sparse_fused_q4k_kernel<FUSED_NPW><<<dim3(static_cast<uint32_t>(nblk)), dim3(512), 0, st>>>(
-                static_cast<const uint8_t*>(wg), static_cast<const uint8_t*>(wu), static_cast<const uint8_t*>(wd),
-                row_bytes(TYPE_Q4_K, h), i, x, active, n_active, act_kind, part, units, slots);
-        int rcf = check_launch("vb_sparse_ffn");
-        if (rcf != OK) return rcf;
-        sparse_reduce_kernel<<<dim3(static_cast<uint32_t>(units)), dim3(1024), 0, st>>>(part, nblk, y);
-        return check_launch("vb_sparse_ffn");
-    }
-    // 1. gate/up on the active rows
-    RowSrc src;
-    src.w2 = wu;
-    src.gidx = active;
-    src.nsrc = i;
-    float* hid = reinterpret_cast<float*>(wsb + ws.hid);
-    if (down_layout == 0) {  // the dense hidden vector starts at zero
-        src.zbuf = reinterpret_cast<int*>(hid);
-        src.zn = static_cast<int>(i);
-    }
-    int rc = gemv_dispatch_src(wg, src, x, gu, 2 * static_cast<int64_t>(n_active), h, ggml_type, st);
-    if (rc != OK) return rc;
-    // 2. down
-    if (down_layout == 0) {
-        scatter_act_kernel<<<dim3(static_cast<uint32_t>((n_active + 255) / 256)), dim3(256), 0, st>>>(
-            active, n_active, gu, act_kind, hid, i);
-        if ((rc = check_launch("vb_sparse_ffn")) != OK) return rc;
-        return gemv_dispatch(wd, hid, y, h, i, ggml_type, st);
-    }
-    down_rows_q4k_kernel<<<dim3(static_cast<uint32_t>(h / 64)), dim3(DOWN_THREADS), 0, st>>>(
-        static_cast<const uint8_t*>(wd), row_bytes(TYPE_Q4_K, h), i, active, n_active, gu, act_kind, y);
-    return check_launch("vb_sparse_ffn");
+extern "C" int vb_sparse_ffn_block(const void* wg, const void* wu, const void* wd, int32_t down_layout,
+                                   const float* x, const float* norm_w, float eps, const int32_t* active,
+                                   int32_t n_active, int32_t act_kind, int32_t add_residual, float* y, int64_t h,
+                                   int64_t i, int32_t ggml_type, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+    return sparse_ffn_impl(wg, wu, wd, down_layout, x, norm_w, eps, active, n_active, act_kind, add_residual != 0,
+                           y, h, i, ggml_type, workspace, workspace_bytes, as_stream(stream), "vb_sparse_ffn_block");
 }
 
 extern "C" int vb_topk_indices(const float* v, int64_t n, int32_t k, int32_t* out_idx, void* stream) {

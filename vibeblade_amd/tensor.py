@@ -107,6 +107,19 @@ class QTensor:
         return self.data.cpu().numpy()
 
 
+def embed_rows(table: QTensor, tokens, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Decoded rows ``tokens`` of an embedding table, (n_tokens, k) fp32 on
+    the device (vb_embed_rows; ids outside the table give zero rows)."""
+    dev = table.device
+    ids = torch.as_tensor(tokens, dtype=torch.int32).to(dev).contiguous().reshape(-1)
+    n = ids.numel()
+    if out is None:
+        out = torch.empty((n, table.k), dtype=torch.float32, device=dev)
+    _lib.call("vb_embed_rows", table.ptr(), table.qtype, table.rows, table.k, ids.data_ptr() if n else None, n,
+              out.data_ptr(), _stream())
+    return out
+
+
 def gemv(w: QTensor, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """y = W x for one activation vector (len k) -> (rows,) fp32."""
     x = _as_f32_dev(x, w.device).reshape(-1)
@@ -184,8 +197,12 @@ def topk_indices(v: torch.Tensor, k: int) -> torch.Tensor:
 
 def sparse_ffn(gate: QTensor, up: QTensor, down: QTensor, x: torch.Tensor, active: torch.Tensor,
                act: int = ACT_SILU, down_layout: int = DOWN_GGUF,
-               out: torch.Tensor | None = None) -> torch.Tensor:
-    """One token through the activation-sparse FFN over the sorted active set."""
+               out: torch.Tensor | None = None, norm_w=None, eps: float = 1e-5,
+               residual: bool = False) -> torch.Tensor:
+    """One token through the activation-sparse FFN over the sorted active set.
+    With ``norm_w`` the FFN input is rms_norm(x, norm_w, eps) (normalised
+    inside the gate/up launch); with ``residual`` y = x + FFN (``out`` may
+    be ``x``)."""
     h, i = gate.k, gate.rows
     if up.shape != gate.shape or up.qtype != gate.qtype or down.qtype != gate.qtype:
         raise ValueError("sparse_ffn: gate/up/down must share shape conventions and type")
@@ -204,9 +221,20 @@ def sparse_ffn(gate: QTensor, up: QTensor, down: QTensor, x: torch.Tensor, activ
     if nbytes < 0:
         raise ValueError("sparse_ffn: bad shape")
     ws = _workspace(nbytes, dev)
-    _lib.call("vb_sparse_ffn", gate.ptr(), up.ptr(), down.ptr(), down_layout, x.data_ptr(),
-              active.data_ptr() if n_active else None, n_active, act, out.data_ptr(), h, i, gate.qtype,
-              ws.data_ptr(), ws.numel(), _stream())
+    if norm_w is None and not residual:
+        _lib.call("vb_sparse_ffn", gate.ptr(), up.ptr(), down.ptr(), down_layout, x.data_ptr(),
+                  active.data_ptr() if n_active else None, n_active, act, out.data_ptr(), h, i, gate.qtype,
+                  ws.data_ptr(), ws.numel(), _stream())
+        return out
+    nw = None
+    if norm_w is not None:
+        nw = _as_f32_dev(norm_w, dev).reshape(-1)
+        if nw.numel() != h:
+            raise ValueError(f"sparse_ffn: norm_w has {nw.numel()} elements, expected {h}")
+    _lib.call("vb_sparse_ffn_block", gate.ptr(), up.ptr(), down.ptr(), down_layout, x.data_ptr(),
+              None if nw is None else nw.data_ptr(), float(eps), active.data_ptr() if n_active else None,
+              n_active, act, int(bool(residual)), out.data_ptr(), h, i, gate.qtype, ws.data_ptr(), ws.numel(),
+              _stream())
     return out
 
 
