@@ -210,7 +210,7 @@ def time_sparse(layout, steps, warmup, ncopies=8, block=False):
             if block:
                 _lib.check("vb_sparse_ffn_block", lib.vb_sparse_ffn_block(
                     g.ptr(), u.ptr(), d.ptr(), layout, x.data_ptr(), nw.data_ptr(), 1e-5, s.data_ptr(),
-                    s.numel(), ACT_RELU2, 1, y.data_ptr(), h, i, g.qtype, ws.data_ptr(), ws.numel(), st))
+                    s.numel(), None, ACT_RELU2, 1, y.data_ptr(), h, i, g.qtype, ws.data_ptr(), ws.numel(), st))
                 return
             rc = lib.vb_sparse_ffn(g.ptr(), u.ptr(), d.ptr(), layout, x.data_ptr(), s.data_ptr(), s.numel(),
                                    ACT_RELU2, y.data_ptr(), h, i, g.qtype, ws.data_ptr(), ws.numel(), st)
@@ -268,6 +268,50 @@ def time_ffn_block(down_type, fused, steps, warmup, ncopies=8):
     ms, _, _ = time_launches([mk(*t) for t in sets], steps, warmup)
     ab = 2 * inter * 2304 + hd * ggml.row_bytes(down_type, inter) + 4 * hd * 4 + 8 * inter
     return ms, ab
+
+
+def time_sparse_predicted(steps, warmup, ncopies=8, predict_only=False):
+    """One TurboSparse token step with the active set predicted on the device:
+    vb_ema_predict (warm EMA state, k = 10 %), vb_sparse_ffn_block over the
+    predicted set through its device count (RMSNorm + relu(g)*relu(u) +
+    residual, neuron-major Q4_K down, H=4096, I=14336) and vb_ema_update with
+    the used mask.  Returns (ms per step, mean |S|)."""
+    import torch
+    from vibeblade_amd import _lib, ggml
+    from vibeblade_amd.tensor import QTensor, ACT_RELU2
+    h, i = 4096, 14336
+    gen = torch.Generator(device="cuda").manual_seed(SEED + 7)
+    sets = []
+    for _ in range(ncopies):
+        g = QTensor.quantize(torch.randn((i, h), generator=gen, device="cuda") * 0.02, ggml.GGML_TYPE_Q4_K)
+        u = QTensor.quantize(torch.randn((i, h), generator=gen, device="cuda") * 0.02, ggml.GGML_TYPE_Q4_K)
+        d = QTensor.quantize(torch.randn((i, h), generator=gen, device="cuda") * 0.02, ggml.GGML_TYPE_Q4_K)
+        sets.append((g, u, d))
+    lib = _lib.load()
+    # a warm EMA state: about 10 % of the neurons at or above the threshold
+    probs = (torch.rand(i, generator=gen, device="cuda") * 0.34).contiguous()
+    x = torch.randn(h, generator=gen, device="cuda")
+    nw = 1.0 + 0.1 * torch.randn(h, generator=gen, device="cuda")
+    y = torch.empty(h, device="cuda")
+    mask = torch.empty(i, dtype=torch.uint8, device="cuda")
+    active = torch.empty(i, dtype=torch.int32, device="cuda")
+    count = torch.empty(1, dtype=torch.int32, device="cuda")
+    ws = torch.empty(lib.vb_sparse_ffn_workspace(h, i, i, 1), dtype=torch.uint8, device="cuda")
+    k = i // 10
+
+    def mk(g, u, d):
+        def f(st):
+            _lib.check("vb_ema_predict", lib.vb_ema_predict(probs.data_ptr(), None, i, k, 0.3, 1, 0, mask.data_ptr(),
+                                                            active.data_ptr(), count.data_ptr(), st))
+            if predict_only:
+                return
+            _lib.check("vb_sparse_ffn_block", lib.vb_sparse_ffn_block(
+                g.ptr(), u.ptr(), d.ptr(), 1, x.data_ptr(), nw.data_ptr(), 1e-5, active.data_ptr(), i,
+                count.data_ptr(), ACT_RELU2, 1, y.data_ptr(), h, i, g.qtype, ws.data_ptr(), ws.numel(), st))
+            _lib.check("vb_ema_update", lib.vb_ema_update(probs.data_ptr(), i, mask.data_ptr(), 0.1, st))
+        return f
+    ms, _, _ = time_launches([mk(*t) for t in sets], steps, warmup)
+    return ms, int(count.item())
 
 
 def time_moe(steps, warmup):
@@ -556,6 +600,14 @@ def main():
                           "frac_hbm": round(b5 / (ms5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}),
               file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
+        for only in (True, False):
+            ms8, n_s8 = time_sparse_predicted(400, 40, predict_only=only)
+            what = ("EMA predict + compaction alone (I=14336, k=1433)" if only else
+                    "TurboSparse token step on the device: EMA predict + sparse block over the device count "
+                    "+ EMA update, H=4096 I=14336")
+            print(json.dumps({"workload": what, "us_per_call": round(ms8 * 1e3, 3), "active": n_s8}),
+                  file=sys.stderr, flush=True)
+            torch.cuda.empty_cache()
         for dt_name, dt in (("Q4_K", ggml.GGML_TYPE_Q4_K), ("Q6_K", ggml.GGML_TYPE_Q6_K)):
             for fused in (True, False):
                 ms7, b7 = time_ffn_block(dt, fused, 400, 40)

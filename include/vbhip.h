@@ -135,12 +135,37 @@ int vb_sparse_ffn(const void* wg, const void* wu, const void* wd, int32_t down_l
  * _sparse_ffn_layer :211-229; cpp/src/fast_model.cpp:837-840, :915-940,
  * :966-975).  The norm runs inside the gate/up encode and the residual in
  * the launch that writes y (neuron-major Q4_K, h <= 4096: 2 launches).
- * Same workspace as vb_sparse_ffn; x and norm_w 16-byte aligned. */
+ * n_active_dev (optional): the active-set size as the device wrote it (an
+ * on-device prediction, vb_ema_predict); n_active is then the host's bound
+ * (launch sizes, workspace) and the kernels stop at the device count, so no
+ * host round trip is needed.  Same workspace as vb_sparse_ffn for n_active;
+ * x and norm_w 16-byte aligned. */
 int vb_sparse_ffn_block(const void* wg, const void* wu, const void* wd, int32_t down_layout,
                         const float* x, const float* norm_w, float eps, const int32_t* active,
-                        int32_t n_active, int32_t act_kind, int32_t add_residual, float* y, int64_t h,
-                        int64_t i, int32_t ggml_type, void* workspace, size_t workspace_bytes,
-                        void* stream);
+                        int32_t n_active, const int32_t* n_active_dev, int32_t act_kind, int32_t add_residual,
+                        float* y, int64_t h, int64_t i, int32_t ggml_type, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/* ---- EMA neuron predictor on the device ------------------------------------
+ * EMANeuronPredictor (vibeblade/sparse.py:431-650) with its per-layer state,
+ * a probs vector of n fp32 per layer, in device memory.
+ * vb_ema_update: probs = alpha * mask + (1 - alpha) * probs (update,
+ * sparse.py:494-515); mask: n bytes, 0 or 1.  Rounded as the reference's
+ * float32 numpy expression: bit-identical. */
+int vb_ema_update(float* probs, int64_t n, const uint8_t* mask, double alpha, void* stream);
+/* vb_ema_predict (predict, sparse.py:517-569; predict_combined :571-598):
+ *   warm != 0 (the layer has more than 5 updates):
+ *       {probs >= threshold}, topped up to k with the most probable neurons
+ *       (= top-k(probs) | {probs >= threshold});
+ *   warm == 0: top-k(gate_values) when given, else neurons 0 .. k-1;
+ *   combined != 0: the prediction without gate values | top-k(gate_values).
+ * Ties at a top-k threshold go to the lowest indices.  Writes mask_out (n
+ * bytes), active_out (the selected indices ascending; room for n) and
+ * count_out (1 int32), all on the device: feed active_out / count_out to
+ * vb_sparse_ffn_block with n_active = n.  1 <= k <= n. */
+int vb_ema_predict(const float* probs, const float* gate_values, int64_t n, int32_t k, float threshold,
+                   int32_t warm, int32_t combined, uint8_t* mask_out, int32_t* active_out, int32_t* count_out,
+                   void* stream);
 
 /* ---- FFN block, one token ------------------------------------------------
  * y = [x +] Wd act(Wg n, Wu n), n = x / sqrt(mean(x^2) + eps) * norm_w

@@ -52,6 +52,9 @@ PARITY = {
                  "activation special values, the tanh-form GeGLU against the identity "
                  "0.5(1 + tanh z) = 1/(1 + e^-2z), composition = sparse_ffn with S = all plus the residual",
     "moe": "pinned: weights sum to 1, grouped == per-token loop, single-expert == one GEMM",
+    "ema_update / ema_predict": "pinned: the reference's own known answers (tests/test_ema_neuron.py: "
+                                "decay, cold start with and without gate values, warm threshold set, "
+                                "combined union), the closed form 1 - (1 - a)^t, brute force on tiny inputs",
 }
 
 
@@ -283,6 +286,50 @@ def sparse_ffn(gate: np.ndarray, up: np.ndarray, down: np.ndarray, x: np.ndarray
     g = x @ gate[idx].astype(np.float64).T
     u = x @ up[idx].astype(np.float64).T
     return act_pair(g, u, act) @ down[:, idx].astype(np.float64).T
+
+
+def ema_update(probs: np.ndarray, mask: np.ndarray, alpha: float) -> np.ndarray:
+    """EMANeuronPredictor.update (vibeblade/sparse.py:494-515): the float32
+    numpy expression alpha * obs + (1 - alpha) * probs, evaluated as numpy
+    evaluates it."""
+    obs = np.asarray(mask).astype(np.float32)
+    return (alpha * obs + (1.0 - alpha) * np.asarray(probs, dtype=np.float32)).astype(np.float32)
+
+
+def _top_k_lowest(values: np.ndarray, k: int) -> np.ndarray:
+    """Indices of the k largest values; ties to the lowest indices."""
+    return np.argsort(-np.asarray(values, dtype=np.float64), kind="stable")[:k]
+
+
+def ema_predict(probs: np.ndarray, k: int, threshold: float, warm: bool, gate=None,
+                combined: bool = False) -> np.ndarray:
+    """EMANeuronPredictor.predict / predict_combined (vibeblade/sparse.py:517-598)
+    as written there: warm -> the threshold mask, topped up to k with the most
+    probable neurons below it; cold -> top-k of the gate values, else the
+    first k; combined -> the gate-less prediction | top-k(gate).  Where the
+    reference's argpartition leaves ties open, the lowest indices win."""
+    p = np.asarray(probs, dtype=np.float32)
+    n = p.size
+
+    def base(g):
+        if warm:
+            m = p >= np.float32(threshold)
+            c = int(m.sum())
+            if c < k:
+                below = np.flatnonzero(~m)
+                m[below[_top_k_lowest(p[below], k - c)]] = True
+            return m
+        m = np.zeros(n, dtype=bool)
+        if g is not None:
+            m[_top_k_lowest(g, k)] = True
+        else:
+            m[:k] = True
+        return m
+    if combined:
+        m = base(None)
+        m[_top_k_lowest(gate, k)] = True
+        return m
+    return base(gate)
 
 
 def route_top_k(logits: np.ndarray, topk: int):

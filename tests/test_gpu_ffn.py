@@ -149,6 +149,8 @@ def test_topk_indices(n, k):
     rng = np.random.default_rng(n + k)
     v = rng.standard_normal(n).astype(np.float32)
     v[::7] = v[3]  # ties
+    v[1::11] = 0.0
+    v[2::13] = -0.0  # signed zeros compare equal: ties, not an order
     got = topk_indices(torch.from_numpy(v).cuda(), k).cpu().numpy()
     order = np.lexsort((np.arange(n), -v.astype(np.float64)))  # value desc, index asc
     want = np.sort(order[:k])

@@ -381,3 +381,62 @@ def test_ffn_block_composition(act):
     normed = O.ffn_block(g, u, d, x, nw, 1e-5, act, True)
     want = x + O.sparse_ffn(g, u, d, O.rms_norm(x, nw, 1e-5), allidx, act)[0]
     assert np.allclose(normed, want, rtol=1e-12, atol=1e-14)
+
+
+def test_ema_update_known_answers():
+    """tests/test_ema_neuron.py:84-97 of the reference (decay), and the closed
+    form p_t = 1 - (1 - a)^t for an always-on neuron, 0 for a never-on one."""
+    p = np.zeros(128, np.float32)
+    mask = np.zeros(128, bool)
+    mask[:10] = True
+    for _ in range(10):
+        p = O.ema_update(p, mask, 0.1)
+    assert p[0] > 0.5 and p[50] < 0.01
+    assert abs(float(p[0]) - (1 - 0.9 ** 10)) < 1e-6 and p[50] == 0.0
+    # one step from p = 1 with the neuron off: 1 - a
+    q = O.ema_update(np.ones(4, np.float32), np.zeros(4, bool), 0.25)
+    assert np.all(q == np.float32(0.75))
+
+
+def test_ema_predict_known_answers():
+    """The reference's tests/test_ema_neuron.py:99-152 cases."""
+    n = 128
+    k = max(1, int(n * 0.1))
+    m = O.ema_predict(np.zeros(n), k, 0.3, warm=False)  # cold, no gate: first k
+    assert m.sum() == 12 and m[:12].all()
+    gate = np.random.default_rng(0).standard_normal(32).astype(np.float32)
+    gate[5] = 100.0
+    assert O.ema_predict(np.zeros(32), 3, 0.3, warm=False, gate=gate)[5]
+    p = np.zeros(64, np.float32)
+    mk = np.zeros(64, bool)
+    mk[:16] = True
+    for _ in range(10):
+        p = O.ema_update(p, mk, 0.1)
+    warm = O.ema_predict(p, 16, 0.2, warm=True)
+    assert warm[:16].all()
+    g2 = np.zeros(64, np.float32)
+    g2[50] = 100.0
+    comb = O.ema_predict(p, 6, 0.3, warm=True, gate=g2, combined=True)
+    assert comb[50] and comb[:6].all()
+
+
+def test_ema_predict_brute_force():
+    """Tiny inputs against an exhaustive reading of the rule: the threshold
+    set, topped up with the largest remaining probabilities (ties: lowest
+    index), has max(k, |{p >= thr}|) members and contains every p >= thr."""
+    rng = np.random.default_rng(9)
+    for _ in range(200):
+        n = int(rng.integers(1, 12))
+        k = int(rng.integers(1, n + 1))
+        p = rng.choice(np.array([0.0, 0.1, 0.25, 0.5, 0.75], np.float32), n)
+        thr = float(rng.choice([0.1, 0.3, 0.6]))
+        m = O.ema_predict(p, k, thr, warm=True)
+        above = p >= np.float32(thr)
+        assert m[above].all() and m.sum() == max(k, int(above.sum()))
+        # every unselected neuron is below every selected one below the threshold,
+        # and among equals the selected ones come first
+        sel_below = np.flatnonzero(m & ~above)
+        unsel = np.flatnonzero(~m)
+        for a in sel_below:
+            for b in unsel:
+                assert p[a] > p[b] or (p[a] == p[b] and a < b)

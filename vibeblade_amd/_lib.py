@@ -44,8 +44,10 @@ SIGNATURES = {
     "vb_ffn_block_workspace": (_i64, [_i64, _i64]),
     "vb_ffn_block": (ctypes.c_int, [_vp, _vp, ctypes.c_float, _vp, _vp, _i32, _vp, _i32, _i64, _i64, _i32,
                                     _i32, _vp, _vp, _sz, _vp]),
-    "vb_sparse_ffn_block": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp, _vp, ctypes.c_float, _vp, _i32, _i32, _i32,
-                                           _vp, _i64, _i64, _i32, _vp, _sz, _vp]),
+    "vb_sparse_ffn_block": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp, _vp, ctypes.c_float, _vp, _i32, _vp, _i32,
+                                           _i32, _vp, _i64, _i64, _i32, _vp, _sz, _vp]),
+    "vb_ema_update": (ctypes.c_int, [_vp, _i64, _vp, ctypes.c_double, _vp]),
+    "vb_ema_predict": (ctypes.c_int, [_vp, _vp, _i64, _i32, ctypes.c_float, _i32, _i32, _vp, _vp, _vp, _vp]),
     "vb_topk_indices": (ctypes.c_int, [_vp, _i64, _i32, _vp, _vp]),
     "vb_moe_workspace": (_i64, [_i32, _i32, _i64, _i64]),
     "vb_moe_grouped_ffn": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _i64,

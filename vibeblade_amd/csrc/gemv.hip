@@ -79,11 +79,15 @@ constexpr int gemv_max_threads() { return D <= max_d16<TYPE>() ? 1024 : 512; }
 template <int TYPE, int D, int MODE, bool FUSE>
 __global__ void __launch_bounds__((gemv_max_threads<TYPE, D>())) gemv_q_kernel(
         const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, const int32_t* __restrict__ gidx,
-        int nsrc, const float* __restrict__ x, float* __restrict__ y, int n, int64_t rb, int units,
-        int slots, int upw, int wpr, int rpg, int* __restrict__ zbuf, int zn, GemvFuse fz) {
+        int nsrc, const float* __restrict__ x, float* __restrict__ y, int n_bound, int64_t rb, int units,
+        int slots, int upw, int wpr, int rpg, int* __restrict__ zbuf, int zn, GemvFuse fz,
+        const int32_t* __restrict__ n_dev) {
     if (zn > 0 && blockIdx.x == 0) {
         for (int i = threadIdx.x; i < zn; i += blockDim.x) zbuf[i] = 0;
     }
+    // gathered pairs with a device count: rows past 2 * count are not computed
+    int n = n_bound;
+    if constexpr (MODE == ROWS_PAIRS) n = 2 * active_count(n_bound / 2, n_dev);
     using Unit = typename UnitOf<TYPE>::T;
     extern __shared__ uint4 xq[];
     const int lane = threadIdx.x & 63;
@@ -95,6 +99,9 @@ __global__ void __launch_bounds__((gemv_max_threads<TYPE, D>())) gemv_q_kernel(
     const int rows_wg = groups * rpg;
     float* red = reinterpret_cast<float*>(xq + XQ_QUADS * slots);  // [wpr][rows_wg]
     const int wg_row0 = static_cast<int>(blockIdx.x) * rows_wg;
+    if constexpr (MODE == ROWS_PAIRS) {
+        if (wg_row0 >= n) return;  // uniform: before any load or barrier
+    }
     const int row0 = wg_row0 + g * rpg;
     const int u = kw * upw + lane;
     const bool valid = lane < upw && u < units;
@@ -354,7 +361,8 @@ int launch_gemv_d(const GemvShape& s, const void* w, const RowSrc& src, const Ge
     const int ni = static_cast<int>(n), nsrc = static_cast<int>(src.nsrc);
 #define VB_GEMV_LAUNCH(MODE, FUSE)                                                                      \
     gemv_q_kernel<TYPE, D, MODE, FUSE><<<g, b, s.lds, st>>>(wb, w2, src.gidx, nsrc, x, y, ni, rb, s.units, \
-                                                            s.slots, s.upw, s.wpr, s.rpg, src.zbuf, src.zn, fz)
+                                                            s.slots, s.upw, s.wpr, s.rpg, src.zbuf, src.zn, fz,  \
+                                                            src.n_dev)
     if (fz.any()) {
         if (src.dense_pairs)
             VB_GEMV_LAUNCH(ROWS_DPAIRS, true);
@@ -447,7 +455,7 @@ int gemv_dispatch_fused(const void* w, const RowSrc& src, const GemvFuse& fz, co
         // v_dot4 kernel by default (fastest measured); VB_GEMV_Q4K_PATH=mfma
         // selects the int8-MFMA kernel (same arithmetic) for plain launches
         const char* path = std::getenv("VB_GEMV_Q4K_PATH");
-        if (path && std::strcmp(path, "mfma") == 0 && !fz.any() && !src.dense_pairs)
+        if (path && std::strcmp(path, "mfma") == 0 && !fz.any() && !src.dense_pairs && !src.n_dev)
             return gemv_q4k_mfma(w, src, x, y, n, k, st);
         return launch_gemv_q<TYPE_Q4_K>(w, src, fz, x, y, n, k, rb, st);
     }

@@ -34,10 +34,11 @@ namespace {
 // load round, no search.  Indices outside [0, i) are dropped; a repeated
 // index writes the same value from each of its entries (same row, same x).
 __global__ void __launch_bounds__(256) scatter_act_kernel(const int32_t* __restrict__ active, int n_active,
+                                                          const int32_t* __restrict__ n_dev,
                                                           const float* __restrict__ gu, int kind,
                                                           float* __restrict__ hid, int64_t i_dim) {
     const int r = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
-    if (r >= n_active) return;
+    if (r >= active_count(n_active, n_dev)) return;
     const int o = active[r];
     const float2 g = *reinterpret_cast<const float2*>(gu + 2 * static_cast<int64_t>(r));
     if (o >= 0 && o < i_dim) hid[o] = act_pair(g.x, g.y, kind);
@@ -59,8 +60,10 @@ constexpr int DOWN_BATCH = 6;              // rows per thread and load batch
 // fixed order (deterministic).
 __global__ void __launch_bounds__(DOWN_THREADS) down_rows_q4k_kernel(
     const uint8_t* __restrict__ d, int64_t rb, int64_t i_dim, const int32_t* __restrict__ active,
-    int n_active, const float* __restrict__ gu, int kind, const float* resid, float* y) {
+    int n_bound, const int32_t* __restrict__ n_dev, const float* __restrict__ gu, int kind, const float* resid,
+    float* y) {
     __shared__ float red[DOWN_RG][65];
+    const int n_active = active_count(n_bound, n_dev);
     __shared__ float red2[DOWN_THREADS / 64][64];
     const int u = blockIdx.x;
     const int t = threadIdx.x, rg = t >> 2, p = t & 3;
@@ -206,9 +209,14 @@ __device__ __forceinline__ void unit_axpy(const gemvc::Q4KUnit& v, const gemvc::
 template <int NPW, bool NORM>
 __global__ void __launch_bounds__(512) sparse_fused_q4k_kernel(
     const uint8_t* __restrict__ wg, const uint8_t* __restrict__ wu, const uint8_t* __restrict__ wd, int64_t rb,
-    int64_t i_dim, const float* __restrict__ x, const int32_t* __restrict__ active, int n_active, int kind,
-    float* __restrict__ partial, int units, int slots, const float* __restrict__ norm_w, float eps) {
+    int64_t i_dim, const float* __restrict__ x, const int32_t* __restrict__ active, int n_bound,
+    const int32_t* __restrict__ n_dev, int kind, float* __restrict__ partial, int units, int slots,
+    const float* __restrict__ norm_w, float eps) {
     using namespace gemvc;
+    // with a device count, workgroups past it do nothing (the reduction reads
+    // the same count and never their partials)
+    const int n_active = active_count(n_bound, n_dev);
+    if (static_cast<int>(blockIdx.x) * (8 * NPW) >= n_active) return;
     // the x encoding (slots x 11 uint4), later the 8 waves' partials
     __shared__ uint4 lds[8 * 64 * FUSED_RED_PITCH / 4];
     const int lane = threadIdx.x & 63;
@@ -306,9 +314,12 @@ __global__ void __launch_bounds__(512) sparse_fused_q4k_kernel(
 
 // y[64 b + c] = sum over the nblk partials in order; thread t: column c = t %
 // 64, partials t / 64, t / 64 + 16, ...
-__global__ void __launch_bounds__(1024) sparse_reduce_kernel(const float* __restrict__ partial, int nblk,
+__global__ void __launch_bounds__(1024) sparse_reduce_kernel(const float* __restrict__ partial, int nblk_bound,
+                                                             const int32_t* __restrict__ n_dev, int per_blk,
                                                              const float* resid, float* y) {
     __shared__ float red[16][64];
+    // partials of the workgroups that ran (all of them without a device count)
+    const int nblk = n_dev ? (active_count(nblk_bound * per_blk, n_dev) + per_blk - 1) / per_blk : nblk_bound;
     const int c = threadIdx.x & 63, bg = threadIdx.x >> 6;
     const int col = static_cast<int>(blockIdx.x) * 64 + c;
     // every load of a round of 8 is issued before the adds (fixed order)
@@ -335,13 +346,80 @@ __global__ void __launch_bounds__(1024) sparse_reduce_kernel(const float* __rest
 
 // ---- top-k indices (single workgroup radix select) ---------------------------
 
+// Ascending key == ascending float; -0.0 and +0.0 share a key, as they
+// compare equal (numpy's orderings, which the top-k rules follow, treat them
+// as ties).
 __device__ __forceinline__ uint32_t order_key(float f) {
-    const uint32_t b = __float_as_uint(f);
-    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);  // ascending key == ascending float
+    uint32_t b = __float_as_uint(f);
+    b = b == 0x80000000u ? 0u : b;
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-// out[0..k) = indices of the k largest v[i], ascending index order; ties at
-// the threshold value go to the lowest indices.
+// The k-th largest key of v[0..n) (1 <= k <= n) by a 4-pass radix select
+// over LDS histograms, and how many elements equal to it belong to the top k
+// (ties go to the lowest indices).  Every thread of the workgroup calls it.
+struct KthKey {
+    uint32_t key;
+    int ties;
+};
+
+__device__ KthKey radix_kth(const float* __restrict__ v, int n, int k) {
+    __shared__ int hist[256];
+    __shared__ uint32_t s_prefix, s_mask;
+    __shared__ int s_remaining;
+    const int tid = threadIdx.x;
+    if (tid == 0) {
+        s_prefix = 0;
+        s_mask = 0;
+        s_remaining = k;
+    }
+    for (int pass = 3; pass >= 0; pass--) {
+        if (tid < 256) hist[tid] = 0;
+        __syncthreads();
+        const uint32_t prefix = s_prefix, mask = s_mask;
+        for (int i = tid; i < n; i += blockDim.x) {
+            const uint32_t key = order_key(v[i]);
+            if ((key & mask) == prefix) atomicAdd(&hist[(key >> (8 * pass)) & 255], 1);
+        }
+        __syncthreads();
+        if (tid == 0) {
+            int rem = s_remaining, cum = 0, b = 255;
+            for (; b > 0; b--) {
+                if (cum + hist[b] >= rem) break;
+                cum += hist[b];
+            }
+            s_prefix = prefix | (static_cast<uint32_t>(b) << (8 * pass));
+            s_mask = mask | (255u << (8 * pass));
+            s_remaining = rem - cum;
+        }
+        __syncthreads();
+    }
+    KthKey r;
+    r.key = s_prefix;
+    r.ties = s_remaining;
+    __syncthreads();  // every thread has read the result before a next call resets it
+    return r;
+}
+
+// Exclusive rank of this thread's flag among the flags of all threads before
+// it in thread order, plus *base; then *base advances by the workgroup's
+// count.  wcnt: one int per wave.  Every thread calls it.
+__device__ int block_rank(bool f, int* wcnt, int* base) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = static_cast<int>(blockDim.x >> 6);
+    const uint64_t b = __ballot(f);
+    if (lane == 0) wcnt[wave] = __popcll(b);
+    __syncthreads();
+    int r = *base + __popcll(b & ((1ull << lane) - 1ull));
+    int tot = 0;
+    for (int w = 0; w < nw; w++) {
+        tot += wcnt[w];
+        if (w < wave) r += wcnt[w];
+    }
+    __syncthreads();  // every thread has read *base and wcnt
+    if (threadIdx.x == 0) *base += tot;
+    return r;
+}
+
 __global__ void __launch_bounds__(1024) topk_kernel(const float* __restrict__ v, int n, int k,
                                                     int32_t* __restrict__ out) {
     __shared__ int hist[256];
@@ -415,6 +493,305 @@ __global__ void __launch_bounds__(1024) topk_kernel(const float* __restrict__ v,
     }
 }
 
+// ---- EMA neuron predictor (EMANeuronPredictor, vibeblade/sparse.py:431-650) ----
+
+// probs = alpha * mask + (1 - alpha) * probs, rounded as the reference's
+// float32 numpy expression (sparse.py:510-512): the product (1 - alpha) * p is
+// rounded, alpha * mask is exact (mask is 0 or 1), then one rounded add.
+// Contraction into a fused multiply-add is switched off (hipcc contracts by
+// default, and an unrounded product changes the result after a few steps),
+// so the result is bit-identical.
+__global__ void __launch_bounds__(256) ema_update_kernel(float* __restrict__ probs, const uint8_t* __restrict__ mask,
+                                                         int64_t n, float alpha, float beta) {
+#pragma clang fp contract(off)
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float t = beta * probs[i];
+    probs[i] = (mask[i] ? alpha : 0.f) + t;
+}
+
+constexpr int PRED_WARM = 1;      // more than 5 updates: select by EMA probability
+constexpr int PRED_GATE = 2;      // gate values given
+constexpr int PRED_COMBINED = 4;  // predict_combined: EMA prediction | gate top-k
+
+// One workgroup.  The selected set (sparse.py:534-569, :571-598):
+//   warm:                    top-k(probs) | {probs >= threshold}
+//                            (equal to the reference's threshold set topped
+//                            up with the most probable neurons to k)
+//   cold, gate, !combined:   top-k(gate)
+//   cold otherwise:          neurons 0 .. k-1
+//   combined:                the above (without gate) | top-k(gate)
+// Top-k ties go to the lowest indices.  Writes mask (n bytes), the selected
+// indices in ascending order (active, room for n) and their count.
+__global__ void __launch_bounds__(1024) ema_predict_kernel(const float* __restrict__ probs,
+                                                           const float* __restrict__ gate, int n, int k,
+                                                           float threshold, int flags,
+                                                           uint8_t* __restrict__ mask, int32_t* __restrict__ active,
+                                                           int32_t* __restrict__ count) {
+    __shared__ int wcnt[3][16];
+    __shared__ int base[3];
+    const bool warm = flags & PRED_WARM, has_gate = flags & PRED_GATE, combined = flags & PRED_COMBINED;
+    const bool use_p = warm;                               // top-k over probs
+    const bool use_g = has_gate && (combined || !warm);    // top-k over gate
+    KthKey kp{0u, 0}, kg{0u, 0};
+    if (use_p) kp = radix_kth(probs, n, k);
+    if (use_g) kg = radix_kth(gate, n, k);
+    if (threadIdx.x < 3) base[threadIdx.x] = 0;
+    __syncthreads();
+    for (int i0 = 0; i0 < n; i0 += blockDim.x) {
+        const int i = i0 + static_cast<int>(threadIdx.x);
+        const bool in = i < n;
+        const float pv = in && use_p ? probs[i] : 0.f;
+        const float gv = in && use_g ? gate[i] : 0.f;
+        const uint32_t pk = order_key(pv), gk = order_key(gv);
+        const bool peq = in && use_p && pk == kp.key, geq = in && use_g && gk == kg.key;
+        const int prank = block_rank(peq, wcnt[0], &base[0]);
+        const int grank = block_rank(geq, wcnt[1], &base[1]);
+        const bool ptop = in && use_p && (pk > kp.key || (peq && prank < kp.ties));
+        const bool gtop = in && use_g && (gk > kg.key || (geq && grank < kg.ties));
+        bool sel;
+        if (warm)
+            sel = ptop || (in && pv >= threshold);
+        else if (has_gate && !combined)
+            sel = gtop;
+        else
+            sel = in && i < k;
+        if (combined) sel = sel || gtop;
+        const int pos = block_rank(sel, wcnt[2], &base[2]);
+        if (in) {
+            mask[i] = sel ? 1 : 0;
+            if (sel) active[pos] = i;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) *count = base[2];
+}
+
+// ---- register-resident predictor (n <= 1024 * PER) ---------------------------
+//
+// Thread t holds elements e = j * 1024 + t, slots j < PER: loads and mask
+// stores are coalesced, and index order is slot-major.  A rank in index
+// order = the count of flags in earlier (slot, wave) cells + the in-wave
+// rank; the cells' counts go through LDS and wave 0 turns them into
+// exclusive prefixes (two barriers for up to two flag sets at once).
+
+// Index-order ranks of the flagged elements of two flag sets (fa, fb: bit j
+// = this thread's slot j).  Phase 1: each (slot, wave) cell's count into LDS;
+// wave 0 turns each set's cells into exclusive prefixes; phase 2 recomputes
+// the in-wave ranks (ballots are cheap; nothing is held across barriers) and
+// hands rank(j) to `use(set, j, rank)`.  cells: PER * 32 + 2 ints of LDS.
+// Returns the totals in *ta / *tb.  Every thread calls it.
+template <int PER, class Use>
+__device__ void slot_ranks(uint32_t fa, uint32_t fb, int* cells, int* ta, int* tb, Use use) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t lt = (1ull << lane) - 1ull;
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const uint64_t ba = __ballot((fa >> j) & 1u), bb = __ballot((fb >> j) & 1u);
+        if (lane == 0) {
+            cells[j * 16 + wave] = __popcll(ba);
+            cells[PER * 16 + j * 16 + wave] = __popcll(bb);
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {  // wave 0: exclusive prefix over each set's PER * 16 cells, in order
+        constexpr int PL = PER * 16 / 64;  // cells per lane
+#pragma unroll
+        for (int set = 0; set < 2; set++) {
+            int* c = cells + set * PER * 16;
+            int v[PL], sum = 0;
+#pragma unroll
+            for (int q = 0; q < PL; q++) {
+                v[q] = c[lane * PL + q];
+                sum += v[q];
+            }
+            int inc = sum;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const int t = __shfl_up(inc, d, 64);
+                if (lane >= d) inc += t;
+            }
+            int run = inc - sum;
+#pragma unroll
+            for (int q = 0; q < PL; q++) {
+                c[lane * PL + q] = run;
+                run += v[q];
+            }
+            if (lane == 63) cells[PER * 32 + set] = inc;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const uint64_t ba = __ballot((fa >> j) & 1u), bb = __ballot((fb >> j) & 1u);
+        if ((fa >> j) & 1u) use(0, j, cells[j * 16 + wave] + __popcll(ba & lt));
+        if ((fb >> j) & 1u) use(1, j, cells[PER * 16 + j * 16 + wave] + __popcll(bb & lt));
+    }
+    *ta = cells[PER * 32];
+    *tb = cells[PER * 32 + 1];
+    __syncthreads();  // cells are free for the next call
+}
+
+// k-th largest key among all threads' values (valid slots: bit j of vmask)
+// and how many keys equal to it are inside the top k.  Three passes over
+// digits of 11, 11 and 10 bits (2048-bin LDS histogram, one atomic per live
+// key: measured faster than aggregating equal digits first); wave 0 finds
+// the digit, lane l scanning bins 32 l .. 32 l + 31.
+template <int PER>
+__device__ KthKey radix_kth_regs(const float* vals, uint32_t vmask, int k) {
+    __shared__ int hist[2048];
+    __shared__ uint32_t s_prefix, s_mask;
+    __shared__ int s_remaining;
+    if (threadIdx.x == 0) {
+        s_prefix = 0;
+        s_mask = 0;
+        s_remaining = k;
+    }
+    constexpr int kShift[3] = {21, 10, 0};
+    constexpr int kBits[3] = {11, 11, 10};
+#pragma unroll
+    for (int pass = 0; pass < 3; pass++) {
+        const int sh = kShift[pass];
+        const uint32_t dmask = (1u << kBits[pass]) - 1u;
+        for (int b = threadIdx.x; b < 2048; b += blockDim.x) hist[b] = 0;
+        __syncthreads();
+        const uint32_t prefix = s_prefix, mask = s_mask;
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+            const uint32_t key = order_key(vals[j * 1024 + static_cast<int>(threadIdx.x)]);
+            if (((vmask >> j) & 1u) && (key & mask) == prefix) atomicAdd(&hist[(key >> sh) & dmask], 1);
+        }
+        __syncthreads();
+        if (threadIdx.x < 64) {  // wave 0: lane l holds bins 32 l .. 32 l + 31
+            const int l = threadIdx.x;
+            int mine = 0;
+            for (int b = 0; b < 32; b++) mine += hist[32 * l + b];
+            int suf = mine;  // sum over lanes >= l
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const int t = __shfl_down(suf, d, 64);
+                if (l + d < 64) suf += t;
+            }
+            const int rem = s_remaining;
+            int cum = suf - mine;  // keys in higher bins
+            if (cum < rem && suf >= rem) {  // the digit is in this lane's bins
+                for (int b = 31; b >= 0; b--) {
+                    const int h = hist[32 * l + b];
+                    if (cum + h >= rem) {
+                        s_prefix = prefix | (static_cast<uint32_t>(32 * l + b) << sh);
+                        s_mask = mask | (dmask << sh);
+                        s_remaining = rem - cum;
+                        break;
+                    }
+                    cum += h;
+                }
+            }
+        }
+        __syncthreads();
+    }
+    KthKey r;
+    r.key = s_prefix;
+    r.ties = s_remaining;
+    __syncthreads();
+    return r;
+}
+
+template <int PER>  // PER <= 32 (a thread's flags fit one word)
+__global__ void __launch_bounds__(1024) ema_predict_reg_kernel(const float* __restrict__ probs,
+                                                               const float* __restrict__ gate, int n, int k,
+                                                               float threshold, int flags,
+                                                               uint8_t* __restrict__ mask,
+                                                               int32_t* __restrict__ active,
+                                                               int32_t* __restrict__ count) {
+    // The values live in LDS (slot-major: thread t's slot j at j * 1024 + t,
+    // conflict-free); registers hold only per-thread flag words.  The gate
+    // array's space takes the active list once the selection is made.
+    __shared__ int cells[PER * 32 + 2];
+    __shared__ float vals_p[PER * 1024];
+    __shared__ float vals_g[PER * 1024];
+    __shared__ uint8_t mask_lds[PER * 1024];
+    const bool warm = flags & PRED_WARM, has_gate = flags & PRED_GATE, combined = flags & PRED_COMBINED;
+    const bool use_p = warm, use_g = has_gate && (combined || !warm);
+    const int t = static_cast<int>(threadIdx.x);
+    uint32_t vmask = 0, above = 0;
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int e = j * 1024 + t;
+        const bool in = e < n;
+        vmask |= (in ? 1u : 0u) << j;
+        const float pv = use_p && in ? probs[e] : 0.f;
+        vals_p[e] = pv;
+        above |= (use_p && in && pv >= threshold ? 1u : 0u) << j;
+        vals_g[e] = use_g && in ? gate[e] : 0.f;
+    }
+    __syncthreads();
+    int ta = 0, tb = 0;
+    auto none = [](int, int, int) {};
+    // warm: when the threshold set holds k or more neurons it contains the
+    // top k, and the selection is that set alone (no select needed)
+    bool need_p = false;
+    if (use_p) {
+        slot_ranks<PER>(above, 0u, cells, &ta, &tb, none);  // the count only
+        need_p = ta < k;
+    }
+    KthKey kp{0xFFFFFFFFu, 0}, kg{0xFFFFFFFFu, 0};
+    if (need_p) kp = radix_kth_regs<PER>(vals_p, vmask, k);
+    if (use_g) kg = radix_kth_regs<PER>(vals_g, vmask, k);
+    // top-k membership, ties to the lowest indices: rank among equal keys
+    uint32_t peq = 0, geq = 0, pgt = 0, ggt = 0;
+    if (need_p || use_g) {
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+            const bool in = (vmask >> j) & 1u;
+            const uint32_t kpj = order_key(vals_p[j * 1024 + t]), kgj = order_key(vals_g[j * 1024 + t]);
+            peq |= (need_p && in && kpj == kp.key ? 1u : 0u) << j;
+            pgt |= (need_p && in && kpj > kp.key ? 1u : 0u) << j;
+            geq |= (use_g && in && kgj == kg.key ? 1u : 0u) << j;
+            ggt |= (use_g && in && kgj > kg.key ? 1u : 0u) << j;
+        }
+    }
+    uint32_t ptie = 0, gtie = 0;  // equal keys inside the top k
+    if (need_p || use_g) {
+        slot_ranks<PER>(peq, geq, cells, &ta, &tb, [&](int set, int j, int r) {
+            if (set == 0 && r < kp.ties) ptie |= 1u << j;
+            if (set == 1 && r < kg.ties) gtie |= 1u << j;
+        });
+    }
+    const uint32_t ptop = pgt | ptie, gtop = ggt | gtie;
+    uint32_t sel;
+    if (warm)
+        sel = ptop | above;
+    else if (has_gate && !combined)
+        sel = gtop;
+    else {
+        sel = 0;
+#pragma unroll
+        for (int j = 0; j < PER; j++) sel |= (((vmask >> j) & 1u) && j * 1024 + t < k ? 1u : 0u) << j;
+    }
+    if (combined) sel |= gtop;
+    // mask and active list staged in LDS, then written with 16-byte stores
+    int32_t* act_lds = reinterpret_cast<int32_t*>(vals_g);  // the gate values are dead
+#pragma unroll
+    for (int j = 0; j < PER; j++) mask_lds[j * 1024 + t] = (sel >> j) & 1u;
+    slot_ranks<PER>(sel, 0u, cells, &ta, &tb, [&](int, int j, int r) { act_lds[r] = j * 1024 + t; });
+    // (slot_ranks ends with a barrier: mask_lds and act_lds are complete)
+    const bool mvec = (reinterpret_cast<uintptr_t>(mask) & 15) == 0;
+    for (int e = 16 * t; e < n; e += 16 * 1024) {
+        if (mvec && e + 16 <= n)
+            *reinterpret_cast<uint4*>(mask + e) = *reinterpret_cast<const uint4*>(mask_lds + e);
+        else
+            for (int q = e; q < e + 16 && q < n; q++) mask[q] = mask_lds[q];
+    }
+    const bool avec = (reinterpret_cast<uintptr_t>(active) & 15) == 0;
+    for (int e = 4 * t; e < ta; e += 4 * 1024) {
+        if (avec && e + 4 <= ta)
+            *reinterpret_cast<int4*>(active + e) = *reinterpret_cast<const int4*>(act_lds + e);
+        else
+            for (int q = e; q < e + 4 && q < ta; q++) active[q] = act_lds[q];
+    }
+    if (t == 0) *count = ta;
+}
+
 size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
 
 struct SparseWs {
@@ -466,25 +843,27 @@ bool block_type(int32_t t) { return t == TYPE_Q4_K || t == TYPE_Q6_K || t == TYP
 
 template <int NPW>
 void launch_fused(bool norm, dim3 g, hipStream_t st, const void* wg, const void* wu, const void* wd, int64_t rb,
-                  int64_t i, const float* x, const int32_t* active, int n_active, int act_kind, float* part,
-                  int units, int slots, const float* norm_w, float eps) {
+                  int64_t i, const float* x, const int32_t* active, int n_active, const int32_t* n_dev, int act_kind,
+                  float* part, int units, int slots, const float* norm_w, float eps) {
     const uint8_t* a = static_cast<const uint8_t*>(wg);
     const uint8_t* b = static_cast<const uint8_t*>(wu);
     const uint8_t* c = static_cast<const uint8_t*>(wd);
     if (norm)
-        sparse_fused_q4k_kernel<NPW, true><<<g, dim3(512), 0, st>>>(a, b, c, rb, i, x, active, n_active, act_kind,
-                                                                     part, units, slots, norm_w, eps);
+        sparse_fused_q4k_kernel<NPW, true><<<g, dim3(512), 0, st>>>(a, b, c, rb, i, x, active, n_active, n_dev,
+                                                                     act_kind, part, units, slots, norm_w, eps);
     else
-        sparse_fused_q4k_kernel<NPW, false><<<g, dim3(512), 0, st>>>(a, b, c, rb, i, x, active, n_active,
+        sparse_fused_q4k_kernel<NPW, false><<<g, dim3(512), 0, st>>>(a, b, c, rb, i, x, active, n_active, n_dev,
                                                                       act_kind, part, units, slots, norm_w, eps);
 }
 
 // The sparse FFN with an optional RMSNorm of x (norm_w) and residual (the x
 // term added to y).  y may be x.
+// n_dev: optional device count of the active set (then n_active is the
+// host's bound: launches are sized by it and the kernels stop at the count).
 int sparse_ffn_impl(const void* wg, const void* wu, const void* wd, int32_t down_layout, const float* x,
-                    const float* norm_w, float eps, const int32_t* active, int32_t n_active, int32_t act_kind,
-                    bool residual, float* y, int64_t h, int64_t i, int32_t ggml_type, void* workspace,
-                    size_t workspace_bytes, hipStream_t st, const char* fn) {
+                    const float* norm_w, float eps, const int32_t* active, int32_t n_active, const int32_t* n_dev,
+                    int32_t act_kind, bool residual, float* y, int64_t h, int64_t i, int32_t ggml_type,
+                    void* workspace, size_t workspace_bytes, hipStream_t st, const char* fn) {
     if (h <= 0 || i <= 0 || h > INT32_MAX || i > INT32_MAX || n_active < 0 || n_active > i ||
         (down_layout != 0 && down_layout != 1) ||
         (act_kind != ACT_SILU && act_kind != ACT_RELU2 && act_kind != ACT_GELU_TANH) || !wg || !wu || !wd || !x ||
@@ -548,14 +927,15 @@ int sparse_ffn_impl(const void* wg, const void* wu, const void* wd, int32_t down
         const dim3 g(static_cast<uint32_t>(nblk));
         const int64_t rb = row_bytes(TYPE_Q4_K, h);
         if (npw == 2)
-            launch_fused<2>(nw != nullptr, g, st, wg, wu, wd, rb, i, xin, active, n_active, act_kind, part, units,
-                            slots, nw, eps);
+            launch_fused<2>(nw != nullptr, g, st, wg, wu, wd, rb, i, xin, active, n_active, n_dev, act_kind, part,
+                            units, slots, nw, eps);
         else
-            launch_fused<FUSED_NPW>(nw != nullptr, g, st, wg, wu, wd, rb, i, xin, active, n_active, act_kind, part,
-                                    units, slots, nw, eps);
+            launch_fused<FUSED_NPW>(nw != nullptr, g, st, wg, wu, wd, rb, i, xin, active, n_active, n_dev, act_kind,
+                                    part, units, slots, nw, eps);
         int rcf = check_launch(fn);
         if (rcf != OK) return rcf;
-        sparse_reduce_kernel<<<dim3(static_cast<uint32_t>(units)), dim3(1024), 0, st>>>(part, nblk, resid, y);
+        sparse_reduce_kernel<<<dim3(static_cast<uint32_t>(units)), dim3(1024), 0, st>>>(part, nblk, n_dev, 8 * npw,
+                                                                                       resid, y);
         return check_launch(fn);
     }
     // 1. gate/up on the active rows (with the norm in the encode)
@@ -563,6 +943,7 @@ int sparse_ffn_impl(const void* wg, const void* wu, const void* wd, int32_t down
     src.w2 = wu;
     src.gidx = active;
     src.nsrc = i;
+    src.n_dev = n_dev;
     float* hid = reinterpret_cast<float*>(wsb + ws.hid);
     if (down_layout == 0) {  // the dense hidden vector starts at zero
         src.zbuf = reinterpret_cast<int*>(hid);
@@ -576,7 +957,7 @@ int sparse_ffn_impl(const void* wg, const void* wu, const void* wd, int32_t down
     // 2. down (with the residual in the launch that writes y)
     if (down_layout == 0) {
         scatter_act_kernel<<<dim3(static_cast<uint32_t>((n_active + 255) / 256)), dim3(256), 0, st>>>(
-            active, n_active, gu, act_kind, hid, i);
+            active, n_active, n_dev, gu, act_kind, hid, i);
         if ((rc = check_launch(fn)) != OK) return rc;
         if (!residual) return gemv_dispatch(wd, hid, y, h, i, ggml_type, st);
         if (block_type(ggml_type)) {
@@ -591,7 +972,8 @@ int sparse_ffn_impl(const void* wg, const void* wu, const void* wd, int32_t down
         return check_launch(fn);
     }
     down_rows_q4k_kernel<<<dim3(static_cast<uint32_t>(h / 64)), dim3(DOWN_THREADS), 0, st>>>(
-        static_cast<const uint8_t*>(wd), row_bytes(TYPE_Q4_K, h), i, active, n_active, gu, act_kind, resid, y);
+        static_cast<const uint8_t*>(wd), row_bytes(TYPE_Q4_K, h), i, active, n_active, n_dev, gu, act_kind, resid,
+        y);
     return check_launch(fn);
 }
 
@@ -609,17 +991,55 @@ extern "C" int vb_sparse_ffn(const void* wg, const void* wu, const void* wd, int
                              const float* x, const int32_t* active, int32_t n_active, int32_t act_kind,
                              float* y, int64_t h, int64_t i, int32_t ggml_type, void* workspace,
                              size_t workspace_bytes, void* stream) {
-    return sparse_ffn_impl(wg, wu, wd, down_layout, x, nullptr, 0.f, active, n_active, act_kind, false, y, h, i,
-                           ggml_type, workspace, workspace_bytes, as_stream(stream), "vb_sparse_ffn");
+    return sparse_ffn_impl(wg, wu, wd, down_layout, x, nullptr, 0.f, active, n_active, nullptr, act_kind, false, y,
+                           h, i, ggml_type, workspace, workspace_bytes, as_stream(stream), "vb_sparse_ffn");
 }
 
 extern "C" int vb_sparse_ffn_block(const void* wg, const void* wu, const void* wd, int32_t down_layout,
                                    const float* x, const float* norm_w, float eps, const int32_t* active,
-                                   int32_t n_active, int32_t act_kind, int32_t add_residual, float* y, int64_t h,
-                                   int64_t i, int32_t ggml_type, void* workspace, size_t workspace_bytes,
-                                   void* stream) {
-    return sparse_ffn_impl(wg, wu, wd, down_layout, x, norm_w, eps, active, n_active, act_kind, add_residual != 0,
-                           y, h, i, ggml_type, workspace, workspace_bytes, as_stream(stream), "vb_sparse_ffn_block");
+                                   int32_t n_active, const int32_t* n_active_dev, int32_t act_kind,
+                                   int32_t add_residual, float* y, int64_t h, int64_t i, int32_t ggml_type,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+    return sparse_ffn_impl(wg, wu, wd, down_layout, x, norm_w, eps, active, n_active, n_active_dev, act_kind,
+                           add_residual != 0, y, h, i, ggml_type, workspace, workspace_bytes, as_stream(stream),
+                           "vb_sparse_ffn_block");
+}
+
+extern "C" int vb_ema_update(float* probs, int64_t n, const uint8_t* mask, double alpha, void* stream) {
+    if (n < 0 || (n > 0 && (!probs || !mask)) || !(alpha >= 0.0 && alpha <= 1.0)) {
+        set_error("vb_ema_update: bad arguments");
+        return E_INVAL;
+    }
+    if (n == 0) return OK;
+    // the reference's scalars as numpy rounds them for float32 arrays: alpha
+    // and (1 - alpha), each computed in double and rounded to fp32 once
+    const float a = static_cast<float>(alpha);
+    const float beta = static_cast<float>(1.0 - alpha);
+    ema_update_kernel<<<dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, as_stream(stream)>>>(
+        probs, mask, n, a, beta);
+    return check_launch("vb_ema_update");
+}
+
+extern "C" int vb_ema_predict(const float* probs, const float* gate_values, int64_t n, int32_t k, float threshold,
+                              int32_t warm, int32_t combined, uint8_t* mask_out, int32_t* active_out,
+                              int32_t* count_out, void* stream) {
+    if (n <= 0 || n > 0x7fffffff || k < 1 || k > n || !mask_out || !active_out || !count_out ||
+        (warm && !probs) || (combined && !gate_values)) {
+        set_error("vb_ema_predict: bad arguments (n=%lld, k=%d)", static_cast<long long>(n), k);
+        return E_INVAL;
+    }
+    const int flags = (warm ? PRED_WARM : 0) | (gate_values ? PRED_GATE : 0) | (combined ? PRED_COMBINED : 0);
+    const int ni = static_cast<int>(n);
+    hipStream_t st = as_stream(stream);
+    // register-resident for n <= 16384 (16 values per thread; 32 would spill
+    // at 1024 threads), the streaming kernel above
+    if (n <= 1024 * 16)
+        ema_predict_reg_kernel<16><<<dim3(1), dim3(1024), 0, st>>>(probs, gate_values, ni, k, threshold, flags,
+                                                                   mask_out, active_out, count_out);
+    else
+        ema_predict_kernel<<<dim3(1), dim3(1024), 0, st>>>(probs, gate_values, ni, k, threshold, flags, mask_out,
+                                                           active_out, count_out);
+    return check_launch("vb_ema_predict");
 }
 
 extern "C" int vb_topk_indices(const float* v, int64_t n, int32_t k, int32_t* out_idx, void* stream) {

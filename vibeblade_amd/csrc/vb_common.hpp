@@ -151,6 +151,14 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Size of an active set: `bound` (known to the host), or the count the
+// device wrote at *n_dev clamped to [0, bound].
+__device__ __forceinline__ int active_count(int bound, const int32_t* n_dev) {
+    if (!n_dev) return bound;
+    const int c = *n_dev;
+    return c < 0 ? 0 : (c > bound ? bound : c);
+}
+
 // Gated activations of an FFN neuron, act(g, u) with g = gate row . x and
 // u = up row . x:
 //   ACT_SILU       silu(g) * u = g / (1 + e^-g) * u

@@ -17,6 +17,10 @@ struct RowSrc {
     // dense gate/up pairs: row r = row r/2 of w (r even) or of w2 (r odd),
     // no index list (an FFN block: every neuron)
     bool dense_pairs = false;
+    // gathered pairs: the number of pairs written by the device (a predicted
+    // active set); n / 2 is then the host's bound and rows past 2 * count
+    // are not computed
+    const int32_t* n_dev = nullptr;
 };
 
 // Work fused into a block-quantized GEMV launch (Q4_K / Q6_K / Q8_0):

@@ -23,7 +23,7 @@ from .tensor import QTensor, as_qtensor, gemv, sparse_ffn, topk_indices, activat
 __all__ = [
     "drelu_activation", "drelu_gate", "predict_activations", "compute_sparsity", "sparse_matmul",
     "topk_activation_mask", "batch_drelu", "sparse_ffn_silu", "silu", "SparsePredictor",
-    "EMANeuronPredictor",
+    "EMANeuronPredictor", "DeviceEMAPredictor",
 ]
 
 
@@ -277,5 +277,108 @@ class EMANeuronPredictor:
 
     def reset(self) -> None:
         self._ema_probs.fill(0)
+        self._update_counts.fill(0)
+        self._total_updates = 0
+
+
+class DeviceEMAPredictor:
+    """EMANeuronPredictor (vibeblade/sparse.py:431-650) with its state on the
+    GPU: the per-layer probabilities live in device memory and update,
+    predict and the active-index compaction are device launches
+    (vb_ema_update, vb_ema_predict), so a decode step hands its predicted
+    active set to the sparse FFN block (``sparse_ffn(..., count=)``) without a
+    host round trip.
+
+    Same constructor arguments, methods and results as ``EMANeuronPredictor``
+    (ties at a top-k threshold go to the lowest indices; the EMA step is
+    bit-identical).  ``predict`` / ``predict_combined`` return numpy bool
+    masks like the reference (one device-to-host copy); ``predict_active``
+    keeps everything on the device.  The warm-up counters stay on the host:
+    they decide which rule a prediction uses."""
+
+    def __init__(self, hidden_dim: int, n_layers: int, ema_decay: float = 0.1, sparse_ratio: float = 0.1,
+                 activation_threshold: float = 0.3, device=None) -> None:
+        from .tensor import _dev
+        self.hidden_dim = hidden_dim
+        self.n_layers = n_layers
+        self.ema_decay = ema_decay
+        self.sparse_ratio = sparse_ratio
+        self.activation_threshold = activation_threshold
+        self.device = _dev(device)
+        self._probs = torch.zeros((n_layers, hidden_dim), dtype=torch.float32, device=self.device)
+        self._update_counts = np.zeros(n_layers, dtype=np.int32)
+        self._total_updates = 0
+
+    def _k(self) -> int:
+        return min(self.hidden_dim, max(1, int(self.hidden_dim * self.sparse_ratio)))
+
+    def update(self, layer_idx: int, activation_mask) -> None:
+        """EMA step with an observed mask: numpy bool array, or a device
+        bool / uint8 tensor (e.g. the mask of ``predict_active``)."""
+        from . import _lib
+        from .tensor import _stream
+        if layer_idx < 0 or layer_idx >= self.n_layers:
+            return
+        m = torch.as_tensor(activation_mask).to(device=self.device, dtype=torch.uint8).contiguous().reshape(-1)
+        if m.numel() != self.hidden_dim:
+            raise ValueError(f"update: mask has {m.numel()} entries, expected {self.hidden_dim}")
+        _lib.call("vb_ema_update", self._probs[layer_idx].data_ptr(), self.hidden_dim, m.data_ptr(),
+                  float(self.ema_decay), _stream())
+        self._update_counts[layer_idx] += 1
+        self._total_updates += 1
+
+    def predict_active(self, layer_idx: int, gate_values=None, combined: bool = False):
+        """(active int32 indices ascending, count int32 (1,), mask uint8) on
+        the device; ``active`` has room for every neuron and is valid up to
+        ``count``.  combined: the ``predict_combined`` rule."""
+        from . import _lib
+        from .tensor import _stream
+        n = self.hidden_dim
+        active = torch.empty(n, dtype=torch.int32, device=self.device)
+        count = torch.empty(1, dtype=torch.int32, device=self.device)
+        mask = torch.empty(n, dtype=torch.uint8, device=self.device)
+        if layer_idx < 0 or layer_idx >= self.n_layers:  # the reference: every neuron
+            torch.arange(n, dtype=torch.int32, device=self.device, out=active)
+            count.fill_(n)
+            mask.fill_(1)
+            return active, count, mask
+        g = None
+        if gate_values is not None:
+            g = torch.as_tensor(gate_values).to(device=self.device, dtype=torch.float32).contiguous().reshape(-1)
+            if g.numel() != n:
+                raise ValueError(f"predict: gate_values has {g.numel()} entries, expected {n}")
+        if combined and g is None:
+            raise ValueError("predict_combined needs gate_values")
+        warm = int(self._update_counts[layer_idx] > 5)
+        _lib.call("vb_ema_predict", self._probs[layer_idx].data_ptr(), None if g is None else g.data_ptr(), n,
+                  self._k(), float(self.activation_threshold), warm, int(bool(combined)), mask.data_ptr(),
+                  active.data_ptr(), count.data_ptr(), _stream())
+        return active, count, mask
+
+    def predict(self, layer_idx: int, gate_values=None) -> np.ndarray:
+        return self.predict_active(layer_idx, gate_values)[2].cpu().numpy().astype(bool)
+
+    def predict_combined(self, layer_idx: int, gate_values) -> np.ndarray:
+        return self.predict_active(layer_idx, gate_values, combined=True)[2].cpu().numpy().astype(bool)
+
+    def get_activation_probabilities(self, layer_idx: int) -> np.ndarray:
+        if 0 <= layer_idx < self.n_layers:
+            return self._probs[layer_idx].cpu().numpy().copy()
+        return np.zeros(self.hidden_dim, dtype=np.float32)
+
+    def get_top_neurons(self, layer_idx: int, k: int = 10) -> np.ndarray:
+        probs = self.get_activation_probabilities(layer_idx)
+        return np.argsort(-probs, kind="stable")[:min(k, self.hidden_dim)]
+
+    @property
+    def total_updates(self) -> int:
+        return self._total_updates
+
+    @property
+    def is_warmed_up(self) -> bool:
+        return bool(np.all(self._update_counts > 5))
+
+    def reset(self) -> None:
+        self._probs.zero_()
         self._update_counts.fill(0)
         self._total_updates = 0

@@ -198,11 +198,12 @@ def topk_indices(v: torch.Tensor, k: int) -> torch.Tensor:
 def sparse_ffn(gate: QTensor, up: QTensor, down: QTensor, x: torch.Tensor, active: torch.Tensor,
                act: int = ACT_SILU, down_layout: int = DOWN_GGUF,
                out: torch.Tensor | None = None, norm_w=None, eps: float = 1e-5,
-               residual: bool = False) -> torch.Tensor:
+               residual: bool = False, count: torch.Tensor | None = None) -> torch.Tensor:
     """One token through the activation-sparse FFN over the sorted active set.
     With ``norm_w`` the FFN input is rms_norm(x, norm_w, eps) (normalised
     inside the gate/up launch); with ``residual`` y = x + FFN (``out`` may
-    be ``x``)."""
+    be ``x``).  ``count``: a device int32 holding the set's size (an on-device
+    prediction); ``active`` is then read up to it, with no host sync."""
     h, i = gate.k, gate.rows
     if up.shape != gate.shape or up.qtype != gate.qtype or down.qtype != gate.qtype:
         raise ValueError("sparse_ffn: gate/up/down must share shape conventions and type")
@@ -221,7 +222,9 @@ def sparse_ffn(gate: QTensor, up: QTensor, down: QTensor, x: torch.Tensor, activ
     if nbytes < 0:
         raise ValueError("sparse_ffn: bad shape")
     ws = _workspace(nbytes, dev)
-    if norm_w is None and not residual:
+    if count is not None:
+        count = count.to(device=dev, dtype=torch.int32)
+    if norm_w is None and not residual and count is None:
         _lib.call("vb_sparse_ffn", gate.ptr(), up.ptr(), down.ptr(), down_layout, x.data_ptr(),
                   active.data_ptr() if n_active else None, n_active, act, out.data_ptr(), h, i, gate.qtype,
                   ws.data_ptr(), ws.numel(), _stream())
@@ -233,8 +236,8 @@ def sparse_ffn(gate: QTensor, up: QTensor, down: QTensor, x: torch.Tensor, activ
             raise ValueError(f"sparse_ffn: norm_w has {nw.numel()} elements, expected {h}")
     _lib.call("vb_sparse_ffn_block", gate.ptr(), up.ptr(), down.ptr(), down_layout, x.data_ptr(),
               None if nw is None else nw.data_ptr(), float(eps), active.data_ptr() if n_active else None,
-              n_active, act, int(bool(residual)), out.data_ptr(), h, i, gate.qtype, ws.data_ptr(), ws.numel(),
-              _stream())
+              n_active, None if count is None else count.data_ptr(), act, int(bool(residual)), out.data_ptr(), h, i,
+              gate.qtype, ws.data_ptr(), ws.numel(), _stream())
     return out
 
 
