@@ -21,6 +21,14 @@
  *     (rows = outputs, blocks along K), accumulated in double.
  *   - quantizers for Q8_0 / Q4_K / Q6_K.  The reference has none; these are
  *     deterministic and only need to produce valid blocks.
+ *   - Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q5_K / BF16 decode with the GGUF layouts.
+ *     The reference's own decoders for the 32-element types
+ *     (cpp/src/dequant.cpp:23-94) interleave the nibbles (element 2j = low
+ *     nibble of byte j), and its Q5_K (:307-353) reads qh bits 7 / 3 and
+ *     advances qh by 32 bytes per 64-element group, past the 32 bytes of qh.
+ *     GGUF files hold elements 0..15 in the low nibbles and 16..31 in the
+ *     high nibbles of qs[0..15], and Q5_K group g takes bits 2g / 2g+1 of
+ *     qh[l]; these decoders follow the files.
  *
  * Parity pins (tests/test_oracle.py): Q4_K and Q6_K_VBREF against golden
  * vectors produced by the compiled reference dequant.cpp; Q6_K against the
@@ -37,9 +45,15 @@
 enum {
     ORC_TYPE_F32 = 0,
     ORC_TYPE_F16 = 1,
+    ORC_TYPE_Q4_0 = 2,
+    ORC_TYPE_Q4_1 = 3,
+    ORC_TYPE_Q5_0 = 6,
+    ORC_TYPE_Q5_1 = 7,
     ORC_TYPE_Q8_0 = 8,
     ORC_TYPE_Q4_K = 12,
+    ORC_TYPE_Q5_K = 13,
     ORC_TYPE_Q6_K = 14,
+    ORC_TYPE_BF16 = 30,
     /* test-only: the reference's own (non-GGUF) gathers */
     ORC_TYPE_Q6_K_VBREF = 1014,
     ORC_TYPE_Q8_0_VBREF = 1008,
@@ -47,9 +61,10 @@ enum {
 
 int64_t orc_block_elems(int type) {
     switch (type) {
-    case ORC_TYPE_F32: case ORC_TYPE_F16: return 1;
-    case ORC_TYPE_Q8_0: case ORC_TYPE_Q8_0_VBREF: return 32;
-    case ORC_TYPE_Q4_K: case ORC_TYPE_Q6_K: case ORC_TYPE_Q6_K_VBREF: return 256;
+    case ORC_TYPE_F32: case ORC_TYPE_F16: case ORC_TYPE_BF16: return 1;
+    case ORC_TYPE_Q8_0: case ORC_TYPE_Q8_0_VBREF: case ORC_TYPE_Q4_0: case ORC_TYPE_Q4_1:
+    case ORC_TYPE_Q5_0: case ORC_TYPE_Q5_1: return 32;
+    case ORC_TYPE_Q4_K: case ORC_TYPE_Q5_K: case ORC_TYPE_Q6_K: case ORC_TYPE_Q6_K_VBREF: return 256;
     default: return -1;
     }
 }
@@ -57,9 +72,14 @@ int64_t orc_block_elems(int type) {
 int64_t orc_block_bytes(int type) {
     switch (type) {
     case ORC_TYPE_F32: return 4;
-    case ORC_TYPE_F16: return 2;
+    case ORC_TYPE_F16: case ORC_TYPE_BF16: return 2;
+    case ORC_TYPE_Q4_0: return 18;
+    case ORC_TYPE_Q4_1: return 20;
+    case ORC_TYPE_Q5_0: return 22;
+    case ORC_TYPE_Q5_1: return 24;
     case ORC_TYPE_Q8_0: case ORC_TYPE_Q8_0_VBREF: return 34;
     case ORC_TYPE_Q4_K: return 144;
+    case ORC_TYPE_Q5_K: return 176;
     case ORC_TYPE_Q6_K: case ORC_TYPE_Q6_K_VBREF: return 210;
     default: return -1;
     }
@@ -176,6 +196,78 @@ static void dec_q4_k(const uint8_t* b, float* y) {
     }
 }
 
+/* 32-element GGUF blocks: element j (j < 16) = low nibble of qs[j], element
+ * j + 16 = high nibble; the fifth bit of element e is bit e of qh (LE). */
+static void dec_q4_0(const uint8_t* b, float* y) {
+    float d = orc_f16_to_f32(rd_u16(b));
+    const uint8_t* qs = b + 2;
+    for (int j = 0; j < 16; j++) {
+        y[j] = (float)((qs[j] & 0xF) - 8) * d;
+        y[j + 16] = (float)((qs[j] >> 4) - 8) * d;
+    }
+}
+
+static void dec_q4_1(const uint8_t* b, float* y) {
+    float d = orc_f16_to_f32(rd_u16(b)), m = orc_f16_to_f32(rd_u16(b + 2));
+    const uint8_t* qs = b + 4;
+    for (int j = 0; j < 16; j++) {
+        y[j] = d * (float)(qs[j] & 0xF) + m;
+        y[j + 16] = d * (float)(qs[j] >> 4) + m;
+    }
+}
+
+static uint32_t rd_u32(const uint8_t* p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+static void dec_q5_0(const uint8_t* b, float* y) {
+    float d = orc_f16_to_f32(rd_u16(b));
+    uint32_t qh = rd_u32(b + 2);
+    const uint8_t* qs = b + 6;
+    for (int j = 0; j < 16; j++) {
+        int q0 = (qs[j] & 0xF) | (int)(((qh >> j) & 1) << 4);
+        int q1 = (qs[j] >> 4) | (int)(((qh >> (j + 16)) & 1) << 4);
+        y[j] = (float)(q0 - 16) * d;
+        y[j + 16] = (float)(q1 - 16) * d;
+    }
+}
+
+static void dec_q5_1(const uint8_t* b, float* y) {
+    float d = orc_f16_to_f32(rd_u16(b)), m = orc_f16_to_f32(rd_u16(b + 2));
+    uint32_t qh = rd_u32(b + 4);
+    const uint8_t* qs = b + 8;
+    for (int j = 0; j < 16; j++) {
+        int q0 = (qs[j] & 0xF) | (int)(((qh >> j) & 1) << 4);
+        int q1 = (qs[j] >> 4) | (int)(((qh >> (j + 16)) & 1) << 4);
+        y[j] = d * (float)q0 + m;
+        y[j + 16] = d * (float)q1 + m;
+    }
+}
+
+/* Q5_K: Q4_K's header and scale packing, qh[32] at 16, qs[128] at 48; group
+ * c (elements 64c .. 64c + 63) adds bit 2c (low nibbles) / 2c+1 (high) of
+ * qh[l] as the fifth bit. */
+static void dec_q5_k(const uint8_t* b, float* y) {
+    float d = orc_f16_to_f32(rd_u16(b));
+    float dmin = orc_f16_to_f32(rd_u16(b + 2));
+    const uint8_t* sc = b + 4;
+    const uint8_t* qh = b + 16;
+    const uint8_t* qs = b + 48;
+    for (int c = 0; c < 4; c++) {
+        uint8_t s0, m0, s1, m1;
+        orc_q4k_scale_min(2 * c, sc, &s0, &m0);
+        orc_q4k_scale_min(2 * c + 1, sc, &s1, &m1);
+        float d0 = d * (float)s0, mm0 = dmin * (float)m0;
+        float d1 = d * (float)s1, mm1 = dmin * (float)m1;
+        for (int l = 0; l < 32; l++) {
+            int q0 = (qs[32 * c + l] & 0xF) | (((qh[l] >> (2 * c)) & 1) << 4);
+            int q1 = (qs[32 * c + l] >> 4) | (((qh[l] >> (2 * c + 1)) & 1) << 4);
+            y[64 * c + l] = d0 * (float)q0 - mm0;
+            y[64 * c + 32 + l] = d1 * (float)q1 - mm1;
+        }
+    }
+}
+
 static void dec_q6_k(const uint8_t* b, float* y) {
     const uint8_t* ql = b;
     const uint8_t* qh = b + 128;
@@ -216,6 +308,16 @@ int orc_dequant_row(const void* row, float* out, int64_t k, int type) {
         switch (type) {
         case ORC_TYPE_F32: memcpy(y, b, 4); break;
         case ORC_TYPE_F16: y[0] = orc_f16_to_f32(rd_u16(b)); break;
+        case ORC_TYPE_BF16: {
+            uint32_t u = (uint32_t)rd_u16(b) << 16;
+            memcpy(y, &u, 4);
+            break;
+        }
+        case ORC_TYPE_Q4_0: dec_q4_0(b, y); break;
+        case ORC_TYPE_Q4_1: dec_q4_1(b, y); break;
+        case ORC_TYPE_Q5_0: dec_q5_0(b, y); break;
+        case ORC_TYPE_Q5_1: dec_q5_1(b, y); break;
+        case ORC_TYPE_Q5_K: dec_q5_k(b, y); break;
         case ORC_TYPE_Q8_0: dec_q8_0(b, y); break;
         case ORC_TYPE_Q8_0_VBREF: dec_q8_0_vbref(b, y); break;
         case ORC_TYPE_Q4_K: dec_q4_k(b, y); break;

@@ -258,6 +258,9 @@ def block_weights(hd, inter, gu_type, d_type, seed):
             return as_qtensor(w)
         if t == ggml.GGML_TYPE_F16:
             return QTensor.from_bytes(w.astype(np.float16).tobytes(), t, *w.shape)
+        if t not in ggml.QUANTIZE_TYPES:  # no quantizer: random blocks of that type
+            from qblocks import rand_qblocks
+            return QTensor.from_bytes(rand_qblocks(t, *w.shape, seed + t + w.shape[0]), t, *w.shape)
         return QTensor.quantize(w, t)
     gq, uq, dq = q(g, gu_type), q(u, gu_type), q(d, d_type)
     return gq, uq, dq, dec(gq), dec(uq), dec(dq)
@@ -281,10 +284,13 @@ def run_block(gq, uq, dq, gd, ud, dd, hd, act, norm, residual, seed, inplace=Fal
 
 
 @pytest.mark.parametrize("gu,dn", [(Q4K, Q4K), (Q4K, ggml.GGML_TYPE_Q6_K), (ggml.GGML_TYPE_Q6_K, Q4K),
-                                   (ggml.GGML_TYPE_Q8_0, ggml.GGML_TYPE_Q8_0)])
+                                   (ggml.GGML_TYPE_Q8_0, ggml.GGML_TYPE_Q8_0),
+                                   (ggml.GGML_TYPE_Q5_K, ggml.GGML_TYPE_Q6_K),
+                                   (ggml.GGML_TYPE_Q4_0, ggml.GGML_TYPE_Q4_1),
+                                   (ggml.GGML_TYPE_Q5_0, ggml.GGML_TYPE_Q5_1)])
 @pytest.mark.parametrize("act", [ACT_SILU, ACT_RELU2, ACT_GELU_TANH])
 def test_ffn_block_llama_shape(gu, dn, act):
-    """hd = 4096, inter = 14336 (Llama-3-8B), every type mix of a Q4_K_M file."""
+    """hd = 4096, inter = 14336 (Llama-3-8B), the type mixes of Q4_K_M, Q5_K_M and legacy files."""
     w = block_weights(4096, 14336, gu, dn, 31)
     run_block(*w, 4096, act, norm=True, residual=True, seed=5)
 

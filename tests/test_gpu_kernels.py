@@ -220,3 +220,56 @@ def test_embed_rows_bit_exact(qtype):
         want = want_all[i] if 0 <= i < vocab else np.zeros(k, np.float32)
         assert np.array_equal(bits(got[t]), bits(want)), (t, i)
     assert embed_rows(table, torch.zeros(0, dtype=torch.int32)).shape == (0, k)
+
+
+# ---- Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q5_K / BF16 -----------------------------------
+
+NEW_TYPES = [ggml.GGML_TYPE_Q4_0, ggml.GGML_TYPE_Q4_1, ggml.GGML_TYPE_Q5_0, ggml.GGML_TYPE_Q5_1, ggml.GGML_TYPE_Q5_K]
+
+
+@pytest.mark.parametrize("qtype", NEW_TYPES)
+@pytest.mark.parametrize("rows,k", [(3, 256), (17, 4096), (5, 14336)])
+def test_new_types_decode_bit_exact(qtype, rows, k):
+    from qblocks import rand_qblocks
+    raw = rand_qblocks(qtype, rows, k, rows * 7 + k + qtype)
+    got = QTensor.from_bytes(raw, qtype, rows, k).dequantize().cpu().numpy()
+    assert np.array_equal(bits(got), bits(O.dequantize(raw, k, qtype)))
+
+
+@pytest.mark.parametrize("qtype", NEW_TYPES + [ggml.GGML_TYPE_Q8_0])
+@pytest.mark.parametrize("rows,k", [(1, 256), (33, 4096), (5, 14336), (300, 1024), (7, 64), (9, 128), (3, 192)])
+def test_new_types_gemv(qtype, rows, k):
+    """Against the fp64 oracle on the same blocks.  Rows of 64 / 128 / 192
+    elements (fewer than 4 lane units) for the 32-element types; Q8_0 is
+    here for those short rows too."""
+    from qblocks import rand_qblocks
+    if k % ggml.BLOCK[qtype][0]:
+        pytest.skip("row not a whole number of blocks")
+    raw = rand_qblocks(qtype, rows, k, rows + k + 3 * qtype)
+    x = np.random.default_rng(k).standard_normal(k).astype(np.float32)
+    y = gemv(QTensor.from_bytes(raw, qtype, rows, k), torch.from_numpy(x).cuda()).cpu().numpy()
+    want = O.gemv(raw, x, rows, k, qtype)
+    assert O.rel_l2(y, want) <= GEMV_TOL
+
+
+def test_bf16_decode_and_gemv():
+    w = rand_weights(9, 100, 8)
+    raw = (w.view(np.uint32) >> 16).astype(np.uint16)
+    wd = (raw.astype(np.uint32) << 16).view(np.float32)
+    qt = QTensor.from_bytes(raw.view(np.uint8), ggml.GGML_TYPE_BF16, 9, 100)
+    assert np.array_equal(bits(qt.dequantize().cpu().numpy()), bits(wd))
+    x = np.random.default_rng(1).standard_normal(100).astype(np.float32)
+    y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy()
+    assert O.rel_l2(y, wd.astype(np.float64) @ x.astype(np.float64)) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("qtype", NEW_TYPES)
+def test_new_types_embed_rows(qtype):
+    from qblocks import rand_qblocks
+    from vibeblade_amd.tensor import embed_rows
+    raw = rand_qblocks(qtype, 300, 512, qtype)
+    ids = np.array([0, 299, 5, -1, 300, 5], np.int32)
+    got = embed_rows(QTensor.from_bytes(raw, qtype, 300, 512), torch.from_numpy(ids)).cpu().numpy()
+    want = O.dequantize(raw, 512, qtype)
+    for t, i in enumerate(ids):
+        assert np.array_equal(bits(got[t]), bits(want[i] if 0 <= i < 300 else np.zeros(512, np.float32)))

@@ -440,3 +440,97 @@ def test_ema_predict_brute_force():
         for a in sel_below:
             for b in unsel:
                 assert p[a] > p[b] or (p[a] == p[b] and a < b)
+
+
+# ---- Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q5_K / BF16 (GGUF layouts) -------------------
+
+_BLK = {O.TYPE_Q4_0: 18, O.TYPE_Q4_1: 20, O.TYPE_Q5_0: 22, O.TYPE_Q5_1: 24, O.TYPE_Q5_K: 176}
+
+
+def _rand_blocks(qtype, nblk, rng, zero_qh=False):
+    """Random blocks with normal (non-subnormal, finite) fp16 scales."""
+    b = rng.integers(0, 256, (nblk, _BLK[qtype]), dtype=np.uint8)
+    scale_offs = {O.TYPE_Q4_0: [0], O.TYPE_Q4_1: [0, 2], O.TYPE_Q5_0: [0], O.TYPE_Q5_1: [0, 2],
+                  O.TYPE_Q5_K: [0, 2]}[qtype]
+    for o in scale_offs:
+        b[:, o + 1] = (b[:, o + 1] & 0x83) | 0x28  # exponent 10..13: normal, modest
+    if zero_qh:
+        qh = {O.TYPE_Q5_0: (2, 6), O.TYPE_Q5_1: (4, 8), O.TYPE_Q5_K: (16, 48)}[qtype]
+        b[:, qh[0]:qh[1]] = 0
+    return b
+
+
+@pytest.mark.parametrize("qtype,zero_qh", [(O.TYPE_Q4_0, False), (O.TYPE_Q4_1, False), (O.TYPE_Q5_0, True),
+                                           (O.TYPE_Q5_1, True)])
+def test_32_element_types_against_reference_order(qtype, zero_qh):
+    """The compiled reference decodes the same values with interleaved
+    nibbles (cpp/src/dequant.cpp:23-94): GGUF element j = its element 2j,
+    GGUF element j + 16 = its element 2j + 1 (with qh = 0 for the 5-bit
+    types, whose fifth bits the two assign differently)."""
+    if not O.ref_available():
+        pytest.skip("compiled reference not built")
+    rng = np.random.default_rng(qtype)
+    blocks = _rand_blocks(qtype, 64, rng, zero_qh)
+    mine = O.dequantize(blocks.reshape(1, -1), 64 * 32, qtype).reshape(64, 32)
+    ref = O.ref_dequantize(blocks.reshape(-1), 64 * 32, qtype).reshape(64, 32)
+    assert np.array_equal(mine[:, :16], ref[:, 0::2]) and np.array_equal(mine[:, 16:], ref[:, 1::2])
+
+
+@pytest.mark.parametrize("qtype", [O.TYPE_Q5_0, O.TYPE_Q5_1])
+def test_5bit_types_fifth_bit_map(qtype):
+    """d = 1 (m = 0), all nibbles 0, one qh bit e set: only element e moves,
+    by exactly 16 (q - 16 for Q5_0: -16 -> 0; d q + m for Q5_1: 0 -> 16)."""
+    qh_off = 2 if qtype == O.TYPE_Q5_0 else 4
+    base = -16.0 if qtype == O.TYPE_Q5_0 else 0.0
+    for e in range(32):
+        b = np.zeros(_BLK[qtype], np.uint8)
+        b[0:2] = [0x00, 0x3C]  # fp16 1.0
+        b[qh_off:qh_off + 4] = np.frombuffer(np.uint32(1 << e).tobytes(), np.uint8)
+        y = O.dequantize(b.reshape(1, -1), 32, qtype)[0]
+        want = np.full(32, base, np.float32)
+        want[e] = base + 16.0
+        assert np.array_equal(y, want), e
+    # closed forms of the nibbles: Q4_0 with d = 2, qs[j] = j | (15 - j) << 4
+    b = np.zeros(18, np.uint8)
+    b[0:2] = [0x00, 0x40]  # fp16 2.0
+    b[2:] = [j | ((15 - j) << 4) for j in range(16)]
+    y = O.dequantize(b.reshape(1, -1), 32, O.TYPE_Q4_0)[0]
+    assert np.array_equal(y, 2.0 * np.array([j - 8 for j in range(16)] + [7 - j for j in range(16)], np.float32))
+
+
+def test_q5k_with_zero_qh_is_q4k_and_bit_map():
+    """A Q5_K block with qh = 0 decodes as the Q4_K block with the same d,
+    dmin, scales and qs (Q4_K is pinned by the reference's golden vectors);
+    each qh bit adds 16 d sc to exactly one element: bit 2c of qh[l] to
+    element 64 c + l, bit 2c + 1 to element 64 c + 32 + l."""
+    rng = np.random.default_rng(5)
+    q5 = _rand_blocks(O.TYPE_Q5_K, 32, rng, zero_qh=True)
+    q4 = np.concatenate([q5[:, :16], q5[:, 48:]], axis=1)
+    assert np.array_equal(O.dequantize(q5.reshape(1, -1), 32 * 256, O.TYPE_Q5_K),
+                          O.dequantize(q4.reshape(1, -1), 32 * 256, O.TYPE_Q4_K))
+    blk = q5[0].copy()
+    blk[0:2] = [0x00, 0x3C]  # d = 1
+    blk[2:4] = 0  # dmin = 0
+    blk[4:16] = 0
+    blk[4:8] = 1  # scales[0..3]: sub-blocks 0..3 scale 1 (their mins, scales[4..7], stay 0)
+    blk[12:16] = 1  # scales[8..11]: sub-blocks 4..7 scale 1 (low nibble), min 0 (high nibble)
+    base = O.dequantize(blk.reshape(1, -1), 256, O.TYPE_Q5_K)[0]
+    for l in (0, 7, 31):
+        for bit in range(8):
+            b2 = blk.copy()
+            b2[16 + l] = 1 << bit
+            y = O.dequantize(b2.reshape(1, -1), 256, O.TYPE_Q5_K)[0]
+            e = 64 * (bit // 2) + 32 * (bit % 2) + l
+            diff = np.flatnonzero(y != base)
+            assert list(diff) == [e] and y[e] - base[e] == 16.0, (l, bit)
+    if O.ref_available():  # the reference's first group (qh = 0) agrees
+        ref = O.ref_dequantize(q5[:4].reshape(-1), 4 * 256, O.TYPE_Q5_K).reshape(4, 256)
+        mine = O.dequantize(q5[:4].reshape(1, -1), 4 * 256, O.TYPE_Q5_K).reshape(4, 256)
+        assert np.array_equal(mine[:, :64], ref[:, :64])
+
+
+def test_bf16_closed_form():
+    v = np.array([1.0, -2.5, 3.0e38, 1e-40, 0.0, -0.0], np.float32)
+    bf = (v.view(np.uint32) >> 16).astype(np.uint16)
+    y = O.dequantize(bf.view(np.uint8).reshape(1, -1), 6, O.TYPE_BF16)[0]
+    assert np.array_equal(y.view(np.uint32), bf.astype(np.uint32) << 16)

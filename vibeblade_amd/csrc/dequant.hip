@@ -4,9 +4,15 @@
 // cpp/src/dequant.cpp:258-301):
 //   Q8_0: y = q * d
 //   Q4_K: y = (d * sc_j) * nib - (dmin * m_j), sub-block j = e / 32
+//   Q5_K: as Q4_K with q5 = nib + 16 * (bit 2c or 2c+1 of qh[l]), c = e / 64
 //   Q6_K: y = (d * sc_s) * (q6 - 32),          sub-block s = e / 16
+//   Q4_0: y = (q - 8) * d;  Q4_1: y = d * q + m   (q: element j < 16 in the
+//         low nibble of qs[j], element j + 16 in its high nibble)
+//   Q5_0: y = (q5 - 16) * d;  Q5_1: y = d * q5 + m (fifth bit of element e:
+//         bit e of the 32-bit qh)
+//   BF16: the 16 bits above 16 zero bits
 // Every product here is exact in fp32 (at most 23 significant bits), so the
-// only rounding is the final subtraction of Q4_K, and the result is
+// only rounding is the final add or subtraction, and the result is
 // bit-identical to any CPU evaluation of the same formula.
 #include "vb_common.hpp"
 #include "../../include/vbhip.h"
@@ -29,10 +35,42 @@ __device__ __forceinline__ void q4k_scale_min(int j, const uint8_t* s, float& sc
     }
 }
 
+// Four 4-bit codes (bytes of n4, low nibbles) and their fifth bits (bits 0..3
+// of h4) as four ints.
+__device__ __forceinline__ void nib4(uint32_t n4, uint32_t h4, int (&q)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) q[i] = static_cast<int>(((n4 >> (8 * i)) & 0xF) | (((h4 >> i) & 1u) << 4));
+}
+
 // Elements e0 .. e0+3 of the row at rp (e0 a multiple of 4).
 template <int TYPE>
 __device__ __forceinline__ float4 decode4(const uint8_t* __restrict__ rp, int64_t e0) {
     float4 y;
+    if constexpr (TYPE == TYPE_Q4_0 || TYPE == TYPE_Q4_1 || TYPE == TYPE_Q5_0 || TYPE == TYPE_Q5_1) {
+        constexpr int BB = static_cast<int>(block_bytes(TYPE));
+        constexpr bool HAS_M = TYPE == TYPE_Q4_1 || TYPE == TYPE_Q5_1;
+        constexpr bool HAS_H = TYPE == TYPE_Q5_0 || TYPE == TYPE_Q5_1;
+        const uint8_t* b = rp + (e0 / 32) * BB;
+        const int i0 = static_cast<int>(e0 % 32);  // 4 elements in one half
+        const float d = f16lo(ld_u16(b));
+        const float m = HAS_M ? f16lo(ld_u16(b + 2)) : 0.f;
+        const int qh_off = HAS_M ? 4 : 2, qs_off = qh_off + (HAS_H ? 4 : 0);
+        const uint32_t qh = HAS_H ? (ld_u16(b + qh_off) | (ld_u16(b + qh_off + 2) << 16)) : 0u;
+        const int j = i0 & 15;
+        const uint32_t bytes = ld_u16(b + qs_off + j) | (ld_u16(b + qs_off + j + 2) << 16);
+        const uint32_t n4 = i0 < 16 ? bytes : bytes >> 4;
+        int q[4];
+        nib4(n4, qh >> i0, q);
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            if constexpr (HAS_M)
+                v[i] = d * static_cast<float>(q[i]) + m;
+            else
+                v[i] = static_cast<float>(q[i] - (HAS_H ? 16 : 8)) * d;
+        }
+        return make_float4(v[0], v[1], v[2], v[3]);
+    }
     if constexpr (TYPE == TYPE_Q4_K) {
         const uint8_t* b = rp + (e0 / 256) * 144;
         const int wi = static_cast<int>(e0 % 256);
@@ -47,6 +85,21 @@ __device__ __forceinline__ float4 decode4(const uint8_t* __restrict__ rp, int64_
         y.y = d1 * static_cast<float>((q >> 8) & 0xF) - m1;
         y.z = d1 * static_cast<float>((q >> 16) & 0xF) - m1;
         y.w = d1 * static_cast<float>((q >> 24) & 0xF) - m1;
+    } else if constexpr (TYPE == TYPE_Q5_K) {
+        const uint8_t* b = rp + (e0 / 256) * 176;
+        const int wi = static_cast<int>(e0 % 256);
+        const int c = wi / 64, l = wi % 32, hi = (wi % 64) / 32;
+        const uint32_t hd = ld_b32(b);
+        const float d = f16lo(hd), dmin = f16hi(hd);
+        float sc, m;
+        q4k_scale_min(2 * c + hi, b + 4, sc, m);
+        const float d1 = d * sc, m1 = dmin * m;
+        const uint32_t q = ld_b32(b + 48 + 32 * c + l) >> (4 * hi);
+        const uint32_t h = ld_b32(b + 16 + l) >> (2 * c + hi);  // bit 0 of each byte
+        y.x = d1 * static_cast<float>((q & 0xF) | ((h & 1u) << 4)) - m1;
+        y.y = d1 * static_cast<float>(((q >> 8) & 0xF) | (((h >> 8) & 1u) << 4)) - m1;
+        y.z = d1 * static_cast<float>(((q >> 16) & 0xF) | (((h >> 16) & 1u) << 4)) - m1;
+        y.w = d1 * static_cast<float>(((q >> 24) & 0xF) | (((h >> 24) & 1u) << 4)) - m1;
     } else if constexpr (TYPE == TYPE_Q6_K) {
         const uint8_t* b = rp + (e0 / 256) * 210;
         const int wi = static_cast<int>(e0 % 256);
@@ -99,7 +152,7 @@ __global__ void __launch_bounds__(256) gather_rows_kernel(const uint8_t* __restr
                                                           int64_t rb) {
     const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (g >= n_items) return;
-    constexpr int64_t PER = (TYPE == TYPE_F32 || TYPE == TYPE_F16) ? 1 : 4;
+    constexpr int64_t PER = (TYPE == TYPE_F32 || TYPE == TYPE_F16 || TYPE == TYPE_BF16) ? 1 : 4;
     const int64_t ipr = k / PER;
     const int64_t t = g / ipr;
     const int64_t e0 = (g - t * ipr) * PER;
@@ -110,6 +163,8 @@ __global__ void __launch_bounds__(256) gather_rows_kernel(const uint8_t* __restr
         float v;
         if constexpr (TYPE == TYPE_F32)
             v = reinterpret_cast<const float*>(rp)[e0];
+        else if constexpr (TYPE == TYPE_BF16)
+            v = __uint_as_float(static_cast<uint32_t>(reinterpret_cast<const uint16_t*>(rp)[e0]) << 16);
         else
             v = __half2float(reinterpret_cast<const __half*>(rp)[e0]);
         out[t * k + e0] = ok ? v : 0.f;
@@ -127,6 +182,8 @@ __global__ void __launch_bounds__(256) dequant_plain_kernel(const uint8_t* __res
     if (i >= n) return;
     if constexpr (TYPE == TYPE_F32)
         out[i] = reinterpret_cast<const float*>(w)[i];
+    else if constexpr (TYPE == TYPE_BF16)
+        out[i] = __uint_as_float(static_cast<uint32_t>(reinterpret_cast<const uint16_t*>(w)[i]) << 16);
     else
         out[i] = __half2float(reinterpret_cast<const __half*>(w)[i]);
 }
@@ -276,13 +333,20 @@ extern "C" int vb_dequant_rows(const void* w, float* out, int64_t n_rows, int64_
     if (n_rows == 0) return OK;
     hipStream_t st = as_stream(stream);
     const uint8_t* wb = static_cast<const uint8_t*>(w);
-    if (ggml_type == TYPE_F32 || ggml_type == TYPE_F16) {
+    if (ggml_type == TYPE_F32 || ggml_type == TYPE_F16 || ggml_type == TYPE_BF16) {
         const int64_t n = n_rows * k;
         const int64_t grid = (n + 255) / 256;
+        if (grid > 0x7fffffff) {
+            set_error("vb_dequant_rows: tensor too large for one launch");
+            return E_INVAL;
+        }
+        const dim3 g(static_cast<uint32_t>(grid)), b(256);
         if (ggml_type == TYPE_F32)
-            dequant_plain_kernel<TYPE_F32><<<dim3(static_cast<uint32_t>(grid)), dim3(256), 0, st>>>(wb, out, n);
+            dequant_plain_kernel<TYPE_F32><<<g, b, 0, st>>>(wb, out, n);
+        else if (ggml_type == TYPE_BF16)
+            dequant_plain_kernel<TYPE_BF16><<<g, b, 0, st>>>(wb, out, n);
         else
-            dequant_plain_kernel<TYPE_F16><<<dim3(static_cast<uint32_t>(grid)), dim3(256), 0, st>>>(wb, out, n);
+            dequant_plain_kernel<TYPE_F16><<<g, b, 0, st>>>(wb, out, n);
         return check_launch("vb_dequant_rows");
     }
     const int64_t n_groups = n_rows * (k / 4);
@@ -296,6 +360,11 @@ extern "C" int vb_dequant_rows(const void* w, float* out, int64_t n_rows, int64_
     case TYPE_Q4_K: dequant_kernel<TYPE_Q4_K><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
     case TYPE_Q6_K: dequant_kernel<TYPE_Q6_K><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
     case TYPE_Q8_0: dequant_kernel<TYPE_Q8_0><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
+    case TYPE_Q5_K: dequant_kernel<TYPE_Q5_K><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
+    case TYPE_Q4_0: dequant_kernel<TYPE_Q4_0><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
+    case TYPE_Q4_1: dequant_kernel<TYPE_Q4_1><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
+    case TYPE_Q5_0: dequant_kernel<TYPE_Q5_0><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
+    case TYPE_Q5_1: dequant_kernel<TYPE_Q5_1><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
     default: set_error("vb_dequant_rows: unsupported type %d", ggml_type); return E_UNSUPPORTED;
     }
     return check_launch("vb_dequant_rows");
@@ -344,7 +413,7 @@ extern "C" int vb_embed_rows(const void* table, int32_t ggml_type, int64_t n_voc
         return E_INVAL;
     }
     if (n_tokens == 0) return OK;
-    const bool plain = ggml_type == TYPE_F32 || ggml_type == TYPE_F16;
+    const bool plain = ggml_type == TYPE_F32 || ggml_type == TYPE_F16 || ggml_type == TYPE_BF16;
     if (!plain && reinterpret_cast<uintptr_t>(out) % 16 != 0) {
         set_error("vb_embed_rows: out must be 16-byte aligned for block types");
         return E_INVAL;
@@ -364,6 +433,12 @@ extern "C" int vb_embed_rows(const void* table, int32_t ggml_type, int64_t n_voc
     case TYPE_Q8_0: gather_rows_kernel<TYPE_Q8_0><<<g, b, 0, st>>>(wb, tokens, n_vocab, out, n_items, k, rb); break;
     case TYPE_F32: gather_rows_kernel<TYPE_F32><<<g, b, 0, st>>>(wb, tokens, n_vocab, out, n_items, k, rb); break;
     case TYPE_F16: gather_rows_kernel<TYPE_F16><<<g, b, 0, st>>>(wb, tokens, n_vocab, out, n_items, k, rb); break;
+    case TYPE_BF16: gather_rows_kernel<TYPE_BF16><<<g, b, 0, st>>>(wb, tokens, n_vocab, out, n_items, k, rb); break;
+    case TYPE_Q5_K: gather_rows_kernel<TYPE_Q5_K><<<g, b, 0, st>>>(wb, tokens, n_vocab, out, n_items, k, rb); break;
+    case TYPE_Q4_0: gather_rows_kernel<TYPE_Q4_0><<<g, b, 0, st>>>(wb, tokens, n_vocab, out, n_items, k, rb); break;
+    case TYPE_Q4_1: gather_rows_kernel<TYPE_Q4_1><<<g, b, 0, st>>>(wb, tokens, n_vocab, out, n_items, k, rb); break;
+    case TYPE_Q5_0: gather_rows_kernel<TYPE_Q5_0><<<g, b, 0, st>>>(wb, tokens, n_vocab, out, n_items, k, rb); break;
+    case TYPE_Q5_1: gather_rows_kernel<TYPE_Q5_1><<<g, b, 0, st>>>(wb, tokens, n_vocab, out, n_items, k, rb); break;
     default: set_error("vb_embed_rows: unsupported type %d", ggml_type); return E_UNSUPPORTED;
     }
     return check_launch("vb_embed_rows");

@@ -36,7 +36,7 @@ __global__ void __launch_bounds__(256) add_kernel(const float* a, const float* b
     if (i < n) y[i] = a[i] + b[i];
 }
 
-bool block_type(int32_t t) { return t == TYPE_Q4_K || t == TYPE_Q6_K || t == TYPE_Q8_0; }
+bool block_type(int32_t t) { return is_block_type(t); }
 
 constexpr int64_t kAlign = 256;
 

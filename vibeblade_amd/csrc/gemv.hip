@@ -105,9 +105,12 @@ __global__ void __launch_bounds__((gemv_max_threads<TYPE, D>())) gemv_q_kernel(
     const int row0 = wg_row0 + g * rpg;
     const int u = kw * upw + lane;
     const bool valid = lane < upw && u < units;
-    // Idle lanes load a real unit (discarded).  Q4_K keeps u % 4 == lane % 4
-    // (units and upw are multiples of 4) so every quad reads one super-block.
-    const int uc = valid ? u : units - 4 + (lane & 3);
+    // Idle lanes load a real unit (discarded).  Q4_K / Q5_K keep u % 4 ==
+    // lane % 4 (units and upw are multiples of 4 there) so every quad reads
+    // one super-block; rows of fewer than 4 units (32-element types, k < 256)
+    // take unit 0.
+    const int ui = units - 4 + (lane & 3);
+    const int uc = valid ? u : (ui < 0 ? 0 : ui);
     const auto usel = make_unit_sel<TYPE>(uc);
     const int nsteps_p = ((rpg + D - 1) / D) * D;
 
@@ -221,7 +224,7 @@ __global__ void __launch_bounds__(256) gemv_plain_kernel(const uint8_t* __restri
     const int lane = threadIdx.x & 63;
     const int row0 = (static_cast<int>(blockIdx.x) * static_cast<int>(blockDim.x >> 6) +
                       __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6))) * R;
-    constexpr int64_t ES = TYPE == TYPE_F32 ? 4 : 2;
+    constexpr int64_t ES = TYPE == TYPE_F32 ? 4 : 2;  // F16 and BF16: 2
     const uint8_t* rp[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
@@ -239,6 +242,8 @@ __global__ void __launch_bounds__(256) gemv_plain_kernel(const uint8_t* __restri
             float wv;
             if constexpr (TYPE == TYPE_F32)
                 wv = reinterpret_cast<const float*>(rp[r])[i];
+            else if constexpr (TYPE == TYPE_BF16)
+                wv = __uint_as_float(static_cast<uint32_t>(reinterpret_cast<const uint16_t*>(rp[r])[i]) << 16);
             else
                 wv = __half2float(reinterpret_cast<const __half*>(rp[r])[i]);
             acc[r] += wv * xv;
@@ -273,6 +278,9 @@ template <int TYPE>
 int ring_depth(int rpg, int wpr) {
     if (rpg <= 1) return 1;
     if (wpr > 1 && rpg <= 8) return 2;
+    // Q6_K single-slice rows, 3..8 per wave: one row in flight (14336 x 4096:
+    // 14.1 us against 19.2 us at a ring of 4)
+    if (TYPE == TYPE_Q6_K && rpg <= 8) return 1;
     if (TYPE == TYPE_Q6_K || rpg > 8) return rpg <= 2 ? 2 : 4;
     return 2;
 }
@@ -282,11 +290,12 @@ int gemv_max_threads_host(int depth) { return depth <= max_d16<TYPE>() ? 1024 : 
 
 // Launch geometry.  k-slices: wpr = ceil(units / 64) waves per row, upw the
 // units per slice rounded up to a multiple of 4.  Rows (rules from sweeps on
-// MI355X, 256 CUs): single-slice rows run in 8-wave workgroups.  Q4_K with
-// 3..8 rows per wave at one workgroup per CU takes that (14336 rows: 7 rows
-// per wave, 256 workgroups); otherwise up to 4 rows per wave at two
-// workgroups per CU, and beyond that one workgroup per CU again (Q6_K
-// lm_head, 128256 rows: 63 rows per wave).  Multi-slice rows (k > 4096) use
+// MI355X, 256 CUs): single-slice rows run in 8-wave workgroups.  When 3..8
+// rows per wave at one workgroup per CU covers the rows, that is the shape
+// (14336 rows: 7 rows per wave, 256 workgroups; best for every type, by
+// 4-26 % over 4 rows per wave at two workgroups per CU); otherwise up to 4
+// rows per wave at two workgroups per CU, and beyond that one workgroup per
+// CU again (Q6_K lm_head, 128256 rows: 63 rows per wave).  Multi-slice rows (k > 4096) use
 // 16-wave workgroups.  VB_GEMV_CFG="wpg,rpg" and VB_GEMV_RING=d override
 // (tuning sweeps).
 template <int TYPE>
@@ -300,7 +309,7 @@ GemvShape gemv_shape(int64_t n, int units, bool even_rows = false) {
         s.wpg = 8;
         const int64_t per2 = (n + 2 * kNumCUs * 8 - 1) / (2 * kNumCUs * 8);
         const int64_t per1 = (n + kNumCUs * 8 - 1) / (kNumCUs * 8);
-        if (TYPE == TYPE_Q4_K && per1 >= 3 && per1 <= 8)
+        if (per1 >= 3 && per1 <= 8)  // every type (Q4_K first; the others measured since)
             s.rpg = static_cast<int>(per1);
         else
             s.rpg = static_cast<int>(per2 <= 4 ? per2 : per1);
@@ -424,18 +433,18 @@ int gemv_dispatch_fused(const void* w, const RowSrc& src, const GemvFuse& fz, co
         set_error("vb_gemv: n=%lld rows exceeds the supported maximum of 2^31-1", static_cast<long long>(n));
         return E_UNSUPPORTED;
     }
-    if ((type == TYPE_Q4_K || type == TYPE_Q6_K || type == TYPE_Q8_0) && k % 64 != 0) {
+    if (is_block_type(type) && k % 64 != 0) {
         set_error("vb_gemv: k=%lld must be a multiple of 64 for type %d", static_cast<long long>(k), type);
         return E_UNSUPPORTED;
     }
-    const bool blockq = type == TYPE_Q4_K || type == TYPE_Q6_K || type == TYPE_Q8_0;
+    const bool blockq = is_block_type(type);
     if ((blockq && reinterpret_cast<uintptr_t>(x) % 16 != 0) || reinterpret_cast<uintptr_t>(x) % 4 != 0 ||
         reinterpret_cast<uintptr_t>(w) % 4 != 0) {
         set_error("vb_gemv: x must be 16-byte aligned for block types (4-byte otherwise), W 4-byte aligned");
         return E_INVAL;
     }
-    if (type == TYPE_Q4_K && reinterpret_cast<uintptr_t>(w) % 16 != 0) {
-        set_error("vb_gemv: Q4_K weights must be 16-byte aligned");
+    if ((type == TYPE_Q4_K || type == TYPE_Q5_K) && reinterpret_cast<uintptr_t>(w) % 16 != 0) {
+        set_error("vb_gemv: Q4_K / Q5_K weights must be 16-byte aligned");
         return E_INVAL;
     }
     if ((fz.any() || src.dense_pairs) && !blockq) {
@@ -461,8 +470,14 @@ int gemv_dispatch_fused(const void* w, const RowSrc& src, const GemvFuse& fz, co
     }
     case TYPE_Q6_K: return launch_gemv_q<TYPE_Q6_K>(w, src, fz, x, y, n, k, rb, st);
     case TYPE_Q8_0: return launch_gemv_q<TYPE_Q8_0>(w, src, fz, x, y, n, k, rb, st);
+    case TYPE_Q5_K: return launch_gemv_q<TYPE_Q5_K>(w, src, fz, x, y, n, k, rb, st);
+    case TYPE_Q4_0: return launch_gemv_q<TYPE_Q4_0>(w, src, fz, x, y, n, k, rb, st);
+    case TYPE_Q4_1: return launch_gemv_q<TYPE_Q4_1>(w, src, fz, x, y, n, k, rb, st);
+    case TYPE_Q5_0: return launch_gemv_q<TYPE_Q5_0>(w, src, fz, x, y, n, k, rb, st);
+    case TYPE_Q5_1: return launch_gemv_q<TYPE_Q5_1>(w, src, fz, x, y, n, k, rb, st);
     case TYPE_F32:
-    case TYPE_F16: {
+    case TYPE_F16:
+    case TYPE_BF16: {
         constexpr int R = 4;
         const int64_t grid = (n + 4 * R - 1) / (4 * R);
         const int ni = static_cast<int>(n), nsrc = static_cast<int>(src.nsrc);
@@ -476,6 +491,13 @@ int gemv_dispatch_fused(const void* w, const RowSrc& src, const GemvFuse& fz, co
             else
                 gemv_plain_kernel<TYPE_F32, R, ROWS_PLAIN><<<g, b, 0, st>>>(wb, w2, src.gidx, nsrc, x, y, ni, k,
                                                                            src.zbuf, src.zn);
+        } else if (type == TYPE_BF16) {
+            if (src.gidx)
+                gemv_plain_kernel<TYPE_BF16, R, ROWS_PAIRS><<<g, b, 0, st>>>(wb, w2, src.gidx, nsrc, x, y, ni, k,
+                                                                            src.zbuf, src.zn);
+            else
+                gemv_plain_kernel<TYPE_BF16, R, ROWS_PLAIN><<<g, b, 0, st>>>(wb, w2, src.gidx, nsrc, x, y, ni, k,
+                                                                            src.zbuf, src.zn);
         } else {
             if (src.gidx)
                 gemv_plain_kernel<TYPE_F16, R, ROWS_PAIRS><<<g, b, 0, st>>>(wb, w2, src.gidx, nsrc, x, y, ni, k,

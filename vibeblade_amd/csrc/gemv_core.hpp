@@ -21,6 +21,13 @@
 //         16-element runs t = 0..3 at elements 128h + 32t + l0 + [0, 16).
 //         Bytes: ql[64h + l0 + [0,16)], ql[64h + 32 + l0 + [0,16)],
 //         qh[32h + l0 + [0,16)], scales[8h + c%2 + 2t], d.
+//   Q5_K  unit u: as Q4_K (header shared by the quad, qs[32c, 32c+32) at 48)
+//         plus the whole qh[32] at 16: bit 2c / 2c+1 of qh[l] is the fifth
+//         bit of the low / high nibble of qs[32c + l].
+//   Q4_0 / Q4_1 / Q5_0 / Q5_1  unit u: blocks 2u, 2u+1 (36 / 40 / 44 / 48
+//         bytes from u * that, 4-byte aligned); element j < 16 of a block is
+//         the low nibble of qs[j], j + 16 the high nibble; the fifth bit of
+//         element e is bit e of the block's 32-bit qh.
 #pragma once
 
 #include "vb_common.hpp"
@@ -44,13 +51,21 @@ struct XSlice {
 // header (d|dmin, scales[0:4], scales[4:8], scales[8:12]) and the quad shares
 // them through DPP broadcasts, instead of 4 lanes fetching the same 16 bytes.
 struct Q4KUnit { uint32_t hw; uint4 qa, qb; };
+struct Q5KUnit { uint32_t hw; uint4 qa, qb, ha, hb; };
 struct Q8Unit { uint4 a, b, c, d; uint32_t e; };
 struct Q6KUnit { uint4 la, lb, qh; uint32_t sc; uint32_t d; };
+// two 32-element blocks of NW dwords in all
+template <int NW> struct LegacyUnit { uint32_t w[NW]; };
 
 template <int TYPE> struct UnitOf;
 template <> struct UnitOf<TYPE_Q4_K> { using T = Q4KUnit; };
+template <> struct UnitOf<TYPE_Q5_K> { using T = Q5KUnit; };
 template <> struct UnitOf<TYPE_Q8_0> { using T = Q8Unit; };
 template <> struct UnitOf<TYPE_Q6_K> { using T = Q6KUnit; };
+template <> struct UnitOf<TYPE_Q4_0> { using T = LegacyUnit<9>; };
+template <> struct UnitOf<TYPE_Q4_1> { using T = LegacyUnit<10>; };
+template <> struct UnitOf<TYPE_Q5_0> { using T = LegacyUnit<11>; };
+template <> struct UnitOf<TYPE_Q5_1> { using T = LegacyUnit<12>; };
 
 __device__ __forceinline__ void load_unit(const uint8_t* row, int u, Q4KUnit& v) {
     const uint8_t* b = row + (u >> 2) * 144;
@@ -73,6 +88,28 @@ __device__ __forceinline__ void load_unit(const uint8_t* row, int u, Q8Unit& v) 
     v.c = ld_b128_a4(b + 32);
     v.d = ld_b128_a4(b + 48);
     v.e = ld_b32(b + 64);
+}
+
+__device__ __forceinline__ void load_unit(const uint8_t* row, int u, Q5KUnit& v) {
+    const uint8_t* b = row + (u >> 2) * 176;
+    const int c = u & 3;
+    v.hw = ld_b32(b + 4 * c);
+    v.ha = *reinterpret_cast<const uint4*>(b + 16);
+    v.hb = *reinterpret_cast<const uint4*>(b + 32);
+    v.qa = *reinterpret_cast<const uint4*>(b + 48 + 32 * c);
+    v.qb = *reinterpret_cast<const uint4*>(b + 64 + 32 * c);
+}
+
+template <int NW>
+__device__ __forceinline__ void load_unit(const uint8_t* row, int u, LegacyUnit<NW>& v) {
+    const uint8_t* b = row + static_cast<int64_t>(u) * (4 * NW);
+#pragma unroll
+    for (int i = 0; i + 4 <= NW; i += 4) {
+        const uint4 t = ld_b128_a4(b + 4 * i);
+        v.w[i] = t.x; v.w[i + 1] = t.y; v.w[i + 2] = t.z; v.w[i + 3] = t.w;
+    }
+#pragma unroll
+    for (int i = NW / 4 * 4; i < NW; i++) v.w[i] = ld_b32(b + 4 * i);
 }
 
 __device__ __forceinline__ void load_unit(const uint8_t* row, int u, Q6KUnit& v) {
@@ -110,7 +147,7 @@ struct Q4KSel {
 
 template <int TYPE>
 __device__ __forceinline__ auto make_unit_sel(int u) {
-    if constexpr (TYPE == TYPE_Q4_K) {
+    if constexpr (TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K) {
         const int c = u & 3;
         Q4KSel q;
         q.hi = c >= 2;
@@ -150,6 +187,93 @@ __device__ __forceinline__ float unit_dot(const Q4KUnit& v, const XSlice& xs, co
     const float dot = sc0 * (xs.s[0] * static_cast<float>(s0)) + sc1 * (xs.s[1] * static_cast<float>(s1));
     const float mins = m0 * xs.sum[0] + m1 * xs.sum[1];
     return d * dot - dmin * mins;
+}
+
+// Q5_K: the Q4_K selectors; q5 = nibble | fifth bit << 4 (0..31) enters
+// the dot products directly.
+__device__ __forceinline__ float unit_dot(const Q5KUnit& v, const XSlice& xs, const Q4KSel& q) {
+    const uint32_t qd[8] = {v.qa.x, v.qa.y, v.qa.z, v.qa.w, v.qb.x, v.qb.y, v.qb.z, v.qb.w};
+    const uint32_t hd[8] = {v.ha.x, v.ha.y, v.ha.z, v.ha.w, v.hb.x, v.hb.y, v.hb.z, v.hb.w};
+    const uint32_t c2 = 2u * ((q.sh >> 4) + (q.hi ? 2u : 0u));  // 2c for chunk c = u % 4
+    uint32_t lo[8], hi[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        lo[i] = (qd[i] & 0x0F0F0F0Fu) | (((hd[i] >> c2) & 0x01010101u) << 4);
+        hi[i] = ((qd[i] >> 4) & 0x0F0F0F0Fu) | (((hd[i] >> (c2 + 1)) & 0x01010101u) << 4);
+    }
+    const int s0 = run_dot(lo, xs.h, xs.l, 8);
+    const int s1 = run_dot(hi, xs.h + 8, xs.l + 8, 8);
+    const uint32_t hx = quad_bcast<0>(v.hw);
+    const uint32_t A = quad_bcast<1>(v.hw), B = quad_bcast<2>(v.hw), C = quad_bcast<3>(v.hw);
+    const uint32_t SC = (((q.hi ? C : A) >> q.sh) & q.m1) | ((A >> q.sh2) & q.m2);
+    const uint32_t M = (((q.hi ? C : B) >> q.shm) & q.m1) | ((B >> q.sh2) & q.m2);
+    const float d = f16lo(hx), dmin = f16hi(hx);
+    const float sc0 = static_cast<float>(SC & 0xFFu), sc1 = static_cast<float>((SC >> 8) & 0xFFu);
+    const float m0 = static_cast<float>(M & 0xFFu), m1 = static_cast<float>((M >> 8) & 0xFFu);
+    const float dot = sc0 * (xs.s[0] * static_cast<float>(s0)) + sc1 * (xs.s[1] * static_cast<float>(s1));
+    const float mins = m0 * xs.sum[0] + m1 * xs.sum[1];
+    return d * dot - dmin * mins;
+}
+
+// Fifth bits b (4 consecutive elements, bits 0..3) moved to bit 4 of each byte.
+__device__ __forceinline__ uint32_t bits_to_bytes4(uint32_t b) {
+    return ((b & 1u) | ((b & 2u) << 7) | ((b & 4u) << 14) | ((b & 8u) << 21)) << 4;
+}
+
+// The 32-element block types.  Block r (r = 0, 1) of the unit is run r:
+// 16 code bytes -> low nibbles = elements 0..15, high = 16..31, each with
+// its fifth bit from qh.  Σ x·y = d·s·(Σ x16·q - off·isum) + m·Σx.
+template <int TYPE, int NW>
+__device__ __forceinline__ float legacy_dot(const LegacyUnit<NW>& v, const XSlice& xs) {
+    constexpr bool HAS_M = TYPE == TYPE_Q4_1 || TYPE == TYPE_Q5_1;
+    constexpr bool HAS_H = TYPE == TYPE_Q5_0 || TYPE == TYPE_Q5_1;
+    constexpr int BB = 2 * NW;                     // block bytes
+    constexpr int QH = HAS_M ? 4 : 2;              // qh offset in a block
+    constexpr int QS = QH + (HAS_H ? 4 : 0);       // qs offset
+    constexpr int OFF = HAS_M ? 0 : (HAS_H ? 16 : 8);
+    float acc = 0.f;
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int base = r * BB;  // byte offset of the block in the unit
+        auto byte_word = [&](int off) -> uint32_t {  // 4 bytes from any 2-byte offset
+            const int o = base + off;
+            if (o % 4 == 0) return v.w[o / 4];
+            return __builtin_amdgcn_alignbyte(v.w[o / 4 + 1], v.w[o / 4], 2);
+        };
+        const uint32_t hdr = byte_word(0);  // d (low half), m (high half, when present)
+        const float d = (base % 4 == 0) ? f16lo(v.w[base / 4]) : f16hi(v.w[base / 4]);
+        const float m = HAS_M ? f16hi(hdr) : 0.f;
+        const uint32_t qh = HAS_H ? byte_word(QH) : 0u;
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t w = byte_word(QS + 4 * i);
+            lo[i] = w & 0x0F0F0F0Fu;
+            hi[i] = (w >> 4) & 0x0F0F0F0Fu;
+            if constexpr (HAS_H) {
+                lo[i] |= bits_to_bytes4((qh >> (4 * i)) & 0xFu);
+                hi[i] |= bits_to_bytes4((qh >> (16 + 4 * i)) & 0xFu);
+            }
+        }
+        int sdot = run_dot(lo, xs.h + 8 * r, xs.l + 8 * r, 4) + run_dot(hi, xs.h + 8 * r + 4, xs.l + 8 * r + 4, 4);
+        if constexpr (OFF != 0) sdot -= OFF * xs.isum[r];
+        acc += d * (xs.s[r] * static_cast<float>(sdot));
+        if constexpr (HAS_M) acc += m * xs.sum[r];
+    }
+    return acc;
+}
+
+__device__ __forceinline__ float unit_dot(const LegacyUnit<9>& v, const XSlice& xs, int) {
+    return legacy_dot<TYPE_Q4_0>(v, xs);
+}
+__device__ __forceinline__ float unit_dot(const LegacyUnit<10>& v, const XSlice& xs, int) {
+    return legacy_dot<TYPE_Q4_1>(v, xs);
+}
+__device__ __forceinline__ float unit_dot(const LegacyUnit<11>& v, const XSlice& xs, int) {
+    return legacy_dot<TYPE_Q5_0>(v, xs);
+}
+__device__ __forceinline__ float unit_dot(const LegacyUnit<12>& v, const XSlice& xs, int) {
+    return legacy_dot<TYPE_Q5_1>(v, xs);
 }
 
 __device__ __forceinline__ float unit_dot(const Q8Unit& v, const XSlice& xs, int) {

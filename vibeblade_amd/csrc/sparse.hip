@@ -839,7 +839,7 @@ __global__ void copy_vec_kernel(const float* a, float* y, int64_t n) {
     if (i < n) y[i] = a[i];
 }
 
-bool block_type(int32_t t) { return t == TYPE_Q4_K || t == TYPE_Q6_K || t == TYPE_Q8_0; }
+bool block_type(int32_t t) { return is_block_type(t); }
 
 template <int NPW>
 void launch_fused(bool norm, dim3 g, hipStream_t st, const void* wg, const void* wu, const void* wd, int64_t rb,
