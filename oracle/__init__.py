@@ -35,6 +35,8 @@ TYPE_Q4_1 = 3
 TYPE_Q5_0 = 6
 TYPE_Q5_1 = 7
 TYPE_Q8_0 = 8
+TYPE_Q2_K = 10
+TYPE_Q3_K = 11
 TYPE_Q4_K = 12
 TYPE_Q5_K = 13
 TYPE_Q6_K = 14
@@ -43,10 +45,12 @@ TYPE_Q6_K_VBREF = 1014   # cpp/src/dequant.cpp:359-402 gather (test only)
 TYPE_Q8_0_VBREF = 1008   # cpp/src/dequant.cpp:99-112 float-scale read (timing only)
 
 BLOCK_ELEMS = {TYPE_F32: 1, TYPE_F16: 1, TYPE_BF16: 1, TYPE_Q4_0: 32, TYPE_Q4_1: 32, TYPE_Q5_0: 32,
-               TYPE_Q5_1: 32, TYPE_Q8_0: 32, TYPE_Q4_K: 256, TYPE_Q5_K: 256, TYPE_Q6_K: 256,
+               TYPE_Q5_1: 32, TYPE_Q8_0: 32, TYPE_Q2_K: 256, TYPE_Q3_K: 256, TYPE_Q4_K: 256, TYPE_Q5_K: 256,
+               TYPE_Q6_K: 256,
                TYPE_Q6_K_VBREF: 256, TYPE_Q8_0_VBREF: 32}
 BLOCK_BYTES = {TYPE_F32: 4, TYPE_F16: 2, TYPE_BF16: 2, TYPE_Q4_0: 18, TYPE_Q4_1: 20, TYPE_Q5_0: 22,
-               TYPE_Q5_1: 24, TYPE_Q8_0: 34, TYPE_Q4_K: 144, TYPE_Q5_K: 176, TYPE_Q6_K: 210,
+               TYPE_Q5_1: 24, TYPE_Q8_0: 34, TYPE_Q2_K: 84, TYPE_Q3_K: 110, TYPE_Q4_K: 144, TYPE_Q5_K: 176,
+               TYPE_Q6_K: 210,
                TYPE_Q6_K_VBREF: 210, TYPE_Q8_0_VBREF: 34}
 
 PARITY = {

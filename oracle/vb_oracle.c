@@ -29,6 +29,14 @@
  *     GGUF files hold elements 0..15 in the low nibbles and 16..31 in the
  *     high nibbles of qs[0..15], and Q5_K group g takes bits 2g / 2g+1 of
  *     qh[l]; these decoders follow the files.
+ *   - Q2_K / Q3_K decode with the GGUF layouts.  The reference's decoders
+ *     (cpp/src/dequant.cpp:128-149, :157-219) take other code bytes, add dmin
+ *     instead of subtracting dmin * min (Q2_K), and unpack the Q3_K scales and
+ *     hmask bits differently.  GGUF: element e = 128 h + 32 j + l takes bits
+ *     2j, 2j+1 of qs[32 h + l] and the scale of sub-block e / 16; Q3_K adds
+ *     bit 4h + j of hmask[l] as the code's third bit (clear: minus 4), with
+ *     6-bit scales (low 4 bits: byte i or the high nibble of byte i - 8;
+ *     high 2 bits: bits 2 (i / 4) of byte 8 + i % 4) minus 32.
  *
  * Parity pins (tests/test_oracle.py): Q4_K and Q6_K_VBREF against golden
  * vectors produced by the compiled reference dequant.cpp; Q6_K against the
@@ -50,6 +58,8 @@ enum {
     ORC_TYPE_Q5_0 = 6,
     ORC_TYPE_Q5_1 = 7,
     ORC_TYPE_Q8_0 = 8,
+    ORC_TYPE_Q2_K = 10,
+    ORC_TYPE_Q3_K = 11,
     ORC_TYPE_Q4_K = 12,
     ORC_TYPE_Q5_K = 13,
     ORC_TYPE_Q6_K = 14,
@@ -64,6 +74,7 @@ int64_t orc_block_elems(int type) {
     case ORC_TYPE_F32: case ORC_TYPE_F16: case ORC_TYPE_BF16: return 1;
     case ORC_TYPE_Q8_0: case ORC_TYPE_Q8_0_VBREF: case ORC_TYPE_Q4_0: case ORC_TYPE_Q4_1:
     case ORC_TYPE_Q5_0: case ORC_TYPE_Q5_1: return 32;
+    case ORC_TYPE_Q2_K: case ORC_TYPE_Q3_K:
     case ORC_TYPE_Q4_K: case ORC_TYPE_Q5_K: case ORC_TYPE_Q6_K: case ORC_TYPE_Q6_K_VBREF: return 256;
     default: return -1;
     }
@@ -78,6 +89,8 @@ int64_t orc_block_bytes(int type) {
     case ORC_TYPE_Q5_0: return 22;
     case ORC_TYPE_Q5_1: return 24;
     case ORC_TYPE_Q8_0: case ORC_TYPE_Q8_0_VBREF: return 34;
+    case ORC_TYPE_Q2_K: return 84;
+    case ORC_TYPE_Q3_K: return 110;
     case ORC_TYPE_Q4_K: return 144;
     case ORC_TYPE_Q5_K: return 176;
     case ORC_TYPE_Q6_K: case ORC_TYPE_Q6_K_VBREF: return 210;
@@ -268,6 +281,39 @@ static void dec_q5_k(const uint8_t* b, float* y) {
     }
 }
 
+/* Q2_K: scales[16] at 0 (low nibble scale, high nibble min, per 16
+ * elements), qs[64] at 16, d at 80, dmin at 82. */
+static void dec_q2_k(const uint8_t* b, float* y) {
+    const uint8_t* sc = b;
+    const uint8_t* qs = b + 16;
+    float d = orc_f16_to_f32(rd_u16(b + 80)), dmin = orc_f16_to_f32(rd_u16(b + 82));
+    for (int e = 0; e < 256; e++) {
+        int h = e / 128, j = (e % 128) / 32, l = e % 32;
+        int q = (qs[32 * h + l] >> (2 * j)) & 3;
+        uint8_t s = sc[e / 16];
+        y[e] = d * (float)(s & 0xF) * (float)q - dmin * (float)(s >> 4);
+    }
+}
+
+/* Q3_K: hmask[32] at 0, qs[64] at 32, scales[12] at 96, d at 108. */
+static int q3k_scale(const uint8_t* sc, int i) {
+    int lo = i < 8 ? (sc[i] & 0xF) : (sc[i - 8] >> 4);
+    int hi = (sc[8 + i % 4] >> (2 * (i / 4))) & 3;
+    return (lo | (hi << 4)) - 32;
+}
+
+static void dec_q3_k(const uint8_t* b, float* y) {
+    const uint8_t* hm = b;
+    const uint8_t* qs = b + 32;
+    const uint8_t* sc = b + 96;
+    float d = orc_f16_to_f32(rd_u16(b + 108));
+    for (int e = 0; e < 256; e++) {
+        int h = e / 128, j = (e % 128) / 32, l = e % 32;
+        int q = ((qs[32 * h + l] >> (2 * j)) & 3) - (((hm[l] >> (4 * h + j)) & 1) ? 0 : 4);
+        y[e] = d * (float)q3k_scale(sc, e / 16) * (float)q;
+    }
+}
+
 static void dec_q6_k(const uint8_t* b, float* y) {
     const uint8_t* ql = b;
     const uint8_t* qh = b + 128;
@@ -318,6 +364,8 @@ int orc_dequant_row(const void* row, float* out, int64_t k, int type) {
         case ORC_TYPE_Q5_0: dec_q5_0(b, y); break;
         case ORC_TYPE_Q5_1: dec_q5_1(b, y); break;
         case ORC_TYPE_Q5_K: dec_q5_k(b, y); break;
+        case ORC_TYPE_Q2_K: dec_q2_k(b, y); break;
+        case ORC_TYPE_Q3_K: dec_q3_k(b, y); break;
         case ORC_TYPE_Q8_0: dec_q8_0(b, y); break;
         case ORC_TYPE_Q8_0_VBREF: dec_q8_0_vbref(b, y); break;
         case ORC_TYPE_Q4_K: dec_q4_k(b, y); break;

@@ -1,5 +1,5 @@
 """Random GGUF blocks for types without a quantizer here (Q4_0, Q4_1, Q5_0,
-Q5_1, Q5_K): random bytes with every fp16 scale / min set to a modest normal
+Q5_1, Q2_K, Q3_K, Q5_K): random bytes with every fp16 scale / min set to a modest normal
 value of random sign, so decoded weights are finite and of moderate size."""
 import numpy as np
 
@@ -9,6 +9,7 @@ from vibeblade_amd import ggml
 SCALE_OFFSETS = {
     ggml.GGML_TYPE_Q4_0: [0], ggml.GGML_TYPE_Q4_1: [0, 2], ggml.GGML_TYPE_Q5_0: [0], ggml.GGML_TYPE_Q5_1: [0, 2],
     ggml.GGML_TYPE_Q8_0: [0], ggml.GGML_TYPE_Q4_K: [0, 2], ggml.GGML_TYPE_Q5_K: [0, 2], ggml.GGML_TYPE_Q6_K: [208],
+    ggml.GGML_TYPE_Q2_K: [80, 82], ggml.GGML_TYPE_Q3_K: [108],
 }
 
 

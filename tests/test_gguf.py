@@ -48,7 +48,7 @@ def rand_tensors(rng):
             ("blk.0.ffn_gate.weight", (256, 6), ggml.GGML_TYPE_Q6_K), ("half", (32, 3), ggml.GGML_TYPE_F16),
             ("bf", (16,), ggml.GGML_TYPE_BF16), ("q8", (64, 2, 3), ggml.GGML_TYPE_Q8_0),
             ("q40", (64, 2), ggml.GGML_TYPE_Q4_0), ("q5k", (256, 2, 1, 2), ggml.GGML_TYPE_Q5_K),
-            ("q2k", (256, 3), ggml.GGML_TYPE_Q2_K)]
+            ("q8k", (256, 3), ggml.GGML_TYPE_Q8_K)]
     return [(n, d, t, raw(t, d)) for n, d, t in spec]
 
 
@@ -136,7 +136,7 @@ def test_loader_surface(sample):
         want = (np.frombuffer(tensors[4][3], np.uint16).astype(np.uint32) << 16).view(np.float32)
         assert np.array_equal(bf.view(np.uint32), want.view(np.uint32))
         with pytest.raises(ValueError):
-            ld.load_tensor("q2k")  # Q2_K: no device kernels
+            ld.load_tensor("q8k")  # Q8_K: no device kernels
         assert ld.metadata["llama.context_length"] == 8192
     assert calls
 

@@ -287,7 +287,8 @@ def run_block(gq, uq, dq, gd, ud, dd, hd, act, norm, residual, seed, inplace=Fal
                                    (ggml.GGML_TYPE_Q8_0, ggml.GGML_TYPE_Q8_0),
                                    (ggml.GGML_TYPE_Q5_K, ggml.GGML_TYPE_Q6_K),
                                    (ggml.GGML_TYPE_Q4_0, ggml.GGML_TYPE_Q4_1),
-                                   (ggml.GGML_TYPE_Q5_0, ggml.GGML_TYPE_Q5_1)])
+                                   (ggml.GGML_TYPE_Q5_0, ggml.GGML_TYPE_Q5_1),
+                                   (ggml.GGML_TYPE_Q3_K, ggml.GGML_TYPE_Q2_K)])
 @pytest.mark.parametrize("act", [ACT_SILU, ACT_RELU2, ACT_GELU_TANH])
 def test_ffn_block_llama_shape(gu, dn, act):
     """hd = 4096, inter = 14336 (Llama-3-8B), the type mixes of Q4_K_M, Q5_K_M and legacy files."""

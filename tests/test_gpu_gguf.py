@@ -46,8 +46,8 @@ def model(tmp_path_factory):
         tensors.append((name, (k, rows), qt, q.tobytes()))
     norm = rng.standard_normal(1024).astype(np.float32)
     tensors.append(("blk.0.ffn_norm.weight", (1024,), ggml.GGML_TYPE_F32, norm.tobytes()))
-    q2k = rng.integers(0, 256, 2 * ggml.row_bytes(ggml.GGML_TYPE_Q2_K, 256), dtype=np.uint8)
-    tensors.append(("blk.0.attn_k.weight", (256, 2), ggml.GGML_TYPE_Q2_K, q2k.tobytes()))
+    q8k = rng.integers(0, 256, 2 * ggml.row_bytes(ggml.GGML_TYPE_Q8_K, 256), dtype=np.uint8)
+    tensors.append(("blk.0.attn_k.weight", (256, 2), ggml.GGML_TYPE_Q8_K, q8k.tobytes()))
     path = tmp_path_factory.mktemp("gguf") / "tiny.gguf"
     write_gguf(path, [("general.architecture", STRING, "llama"), ("llama.block_count", U32, 1)], tensors,
                alignment=64)
@@ -70,7 +70,7 @@ def test_upload_bytes_and_gemv(model):
         assert nw.shape == (1, 1024)
         assert np.array_equal(bits(nw.dequantize().cpu().numpy().ravel()), bits(norm))
         with pytest.raises(ValueError):
-            f.load_qtensor("blk.0.attn_k.weight")  # Q2_K: no device kernels
+            f.load_qtensor("blk.0.attn_k.weight")  # Q8_K: no device kernels
         with pytest.raises(KeyError):
             f.load_qtensor("missing")
 

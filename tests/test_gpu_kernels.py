@@ -222,9 +222,10 @@ def test_embed_rows_bit_exact(qtype):
     assert embed_rows(table, torch.zeros(0, dtype=torch.int32)).shape == (0, k)
 
 
-# ---- Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q5_K / BF16 -----------------------------------
+# ---- Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q2_K / Q3_K / Q5_K / BF16 --------------------
 
-NEW_TYPES = [ggml.GGML_TYPE_Q4_0, ggml.GGML_TYPE_Q4_1, ggml.GGML_TYPE_Q5_0, ggml.GGML_TYPE_Q5_1, ggml.GGML_TYPE_Q5_K]
+NEW_TYPES = [ggml.GGML_TYPE_Q4_0, ggml.GGML_TYPE_Q4_1, ggml.GGML_TYPE_Q5_0, ggml.GGML_TYPE_Q5_1, ggml.GGML_TYPE_Q5_K,
+             ggml.GGML_TYPE_Q2_K, ggml.GGML_TYPE_Q3_K]
 
 
 @pytest.mark.parametrize("qtype", NEW_TYPES)

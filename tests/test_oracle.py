@@ -534,3 +534,74 @@ def test_bf16_closed_form():
     bf = (v.view(np.uint32) >> 16).astype(np.uint16)
     y = O.dequantize(bf.view(np.uint8).reshape(1, -1), 6, O.TYPE_BF16)[0]
     assert np.array_equal(y.view(np.uint32), bf.astype(np.uint32) << 16)
+
+
+def _f16(v):
+    return np.frombuffer(np.float16(v).tobytes(), np.uint8)
+
+
+def test_q2k_code_and_scale_maps():
+    """GGUF Q2_K: element 128 h + 32 j + l = code bits 2j of qs[32 h + l],
+    sub-block e / 16 scale (low nibble) and min (high nibble)."""
+    base = np.zeros(84, np.uint8)
+    base[80:82] = _f16(1.0)
+    base[0:16] = 0x01  # scale 1, min 0
+    for byte in range(64):
+        for j in range(4):
+            b = base.copy()
+            b[16 + byte] = 1 << (2 * j)
+            y = O.dequantize(b.reshape(1, -1), 256, O.TYPE_Q2_K)[0]
+            e = 128 * (byte // 32) + 32 * j + byte % 32
+            assert list(np.flatnonzero(y)) == [e] and y[e] == 1.0, (byte, j)
+    b = base.copy()
+    b[16:80] = 0xFF  # every code 3
+    b[82:84] = _f16(0.5)  # dmin
+    b[0:16] = [((i % 15) + 1) | ((i % 16) << 4) for i in range(16)]
+    y = O.dequantize(b.reshape(1, -1), 256, O.TYPE_Q2_K)[0]
+    want = np.repeat([3.0 * ((i % 15) + 1) - 0.5 * (i % 16) for i in range(16)], 16).astype(np.float32)
+    assert np.array_equal(y, want)
+
+
+def test_q3k_code_hmask_and_scale_maps():
+    """GGUF Q3_K: code bits 2j of qs[32 h + l], third bit = bit 4h + j of
+    hmask[l] (clear: minus 4), 6-bit scales minus 32, each field moving exactly
+    its own element or sub-block."""
+    base = np.zeros(110, np.uint8)
+    base[108:110] = _f16(1.0)
+    base[96:104] = 0x11  # low 4 bits of every scale = 1
+    base[104:108] = 0xAA  # high 2 bits = 2: every scale 33 - 32 = 1
+    base[0:32] = 0xFF  # every third bit set: q = code
+    y0 = O.dequantize(base.reshape(1, -1), 256, O.TYPE_Q3_K)[0]
+    assert np.all(y0 == 0.0)
+    for byte in range(64):
+        for j in range(4):
+            b = base.copy()
+            b[32 + byte] = 1 << (2 * j)
+            y = O.dequantize(b.reshape(1, -1), 256, O.TYPE_Q3_K)[0]
+            e = 128 * (byte // 32) + 32 * j + byte % 32
+            assert list(np.flatnonzero(y)) == [e] and y[e] == 1.0, (byte, j)
+    for l in range(32):
+        for bit in range(8):
+            b = base.copy()
+            b[l] &= ~np.uint8(1 << bit)
+            y = O.dequantize(b.reshape(1, -1), 256, O.TYPE_Q3_K)[0]
+            e = 128 * (bit // 4) + 32 * (bit % 4) + l
+            assert list(np.flatnonzero(y)) == [e] and y[e] == -4.0, (l, bit)
+    ones = base.copy()
+    ones[32:96] = 0x55  # every code 1: y = scale - 32 per sub-block
+    def sub_scales(b):
+        return O.dequantize(b.reshape(1, -1), 256, O.TYPE_Q3_K)[0].reshape(16, 16)[:, 0]
+    assert np.all(sub_scales(ones) == 1.0)
+    for i in range(16):  # the low 4 bits of scale i: byte i (i < 8) or the high nibble of byte i - 8
+        b = ones.copy()
+        b[96 + (i % 8)] = (0x12 if i < 8 else 0x21)
+        want = np.ones(16, np.float32)
+        want[i] = 2.0
+        assert np.array_equal(sub_scales(b), want), i
+    for t in range(4):  # the high 2 bits of scale 4 t + m: bits 2t of byte 8 + m
+        for m in range(4):
+            b = ones.copy()
+            b[104 + m] = 0xAA ^ (0b11 << (2 * t))  # 2 -> 1: scale 17 - 32 = -15
+            want = np.ones(16, np.float32)
+            want[4 * t + m] = -15.0
+            assert np.array_equal(sub_scales(b), want), (t, m)

@@ -10,6 +10,10 @@
 //         low nibble of qs[j], element j + 16 in its high nibble)
 //   Q5_0: y = (q5 - 16) * d;  Q5_1: y = d * q5 + m (fifth bit of element e:
 //         bit e of the 32-bit qh)
+//   Q2_K: y = (d * sc_s) * q2 - (dmin * m_s), s = e / 16, q2 = bits 2j of
+//         qs[32h + l] for e = 128h + 32j + l
+//   Q3_K: y = (d * (sc6_s - 32)) * (q2 + 4 * hbit - 4), hbit = bit 4h + j of
+//         hmask[l]
 //   BF16: the 16 bits above 16 zero bits
 // Every product here is exact in fp32 (at most 23 significant bits), so the
 // only rounding is the final add or subtraction, and the result is
@@ -100,6 +104,30 @@ __device__ __forceinline__ float4 decode4(const uint8_t* __restrict__ rp, int64_
         y.y = d1 * static_cast<float>(((q >> 8) & 0xF) | (((h >> 8) & 1u) << 4)) - m1;
         y.z = d1 * static_cast<float>(((q >> 16) & 0xF) | (((h >> 16) & 1u) << 4)) - m1;
         y.w = d1 * static_cast<float>(((q >> 24) & 0xF) | (((h >> 24) & 1u) << 4)) - m1;
+    } else if constexpr (TYPE == TYPE_Q2_K || TYPE == TYPE_Q3_K) {
+        const uint8_t* b = rp + (e0 / 256) * block_bytes(TYPE);
+        const int wi = static_cast<int>(e0 % 256);
+        const int h = wi / 128, j = (wi % 128) / 32, l = wi % 32, s = wi / 16;
+        float v[4];
+        if constexpr (TYPE == TYPE_Q2_K) {
+            const uint32_t q = (ld_u16(b + 16 + 32 * h + l) | (ld_u16(b + 18 + 32 * h + l) << 16)) >> (2 * j);
+            const uint32_t sm = b[s];
+            const float dd = f16lo(ld_u16(b + 80)), dm = f16lo(ld_u16(b + 82));
+            const float d1 = dd * static_cast<float>(sm & 0xF), m1 = dm * static_cast<float>(sm >> 4);
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = d1 * static_cast<float>((q >> (8 * i)) & 3) - m1;
+        } else {
+            const uint32_t q = (ld_u16(b + 32 + 32 * h + l) | (ld_u16(b + 34 + 32 * h + l) << 16)) >> (2 * j);
+            const uint32_t hb = (ld_u16(b + l) | (ld_u16(b + l + 2) << 16)) >> (4 * h + j);
+            const uint8_t* sc = b + 96;
+            const int lo = s < 8 ? (sc[s] & 0xF) : (sc[s - 8] >> 4);
+            const int hi = (sc[8 + s % 4] >> (2 * (s / 4))) & 3;
+            const float d1 = f16lo(ld_u16(b + 108)) * static_cast<float>((lo | (hi << 4)) - 32);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                v[i] = d1 * static_cast<float>(static_cast<int>((q >> (8 * i)) & 3) + 4 * static_cast<int>((hb >> (8 * i)) & 1) - 4);
+        }
+        return make_float4(v[0], v[1], v[2], v[3]);
     } else if constexpr (TYPE == TYPE_Q6_K) {
         const uint8_t* b = rp + (e0 / 256) * 210;
         const int wi = static_cast<int>(e0 % 256);
@@ -361,6 +389,8 @@ extern "C" int vb_dequant_rows(const void* w, float* out, int64_t n_rows, int64_
     case TYPE_Q6_K: dequant_kernel<TYPE_Q6_K><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
     case TYPE_Q8_0: dequant_kernel<TYPE_Q8_0><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
     case TYPE_Q5_K: dequant_kernel<TYPE_Q5_K><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
+    case TYPE_Q2_K: dequant_kernel<TYPE_Q2_K><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
+    case TYPE_Q3_K: dequant_kernel<TYPE_Q3_K><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
     case TYPE_Q4_0: dequant_kernel<TYPE_Q4_0><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
     case TYPE_Q4_1: dequant_kernel<TYPE_Q4_1><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
     case TYPE_Q5_0: dequant_kernel<TYPE_Q5_0><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
@@ -435,6 +465,8 @@ extern "C" int vb_embed_rows(const void* table, int32_t ggml_type, int64_t n_voc
     case TYPE_F16: gather_rows_kernel<TYPE_F16><<<g, b, 0, st>>>(wb, tokens, n_vocab, out, n_items, k, rb); break;
     case TYPE_BF16: gather_rows_kernel<TYPE_BF16><<<g, b, 0, st>>>(wb, tokens, n_vocab, out, n_items, k, rb); break;
     case TYPE_Q5_K: gather_rows_kernel<TYPE_Q5_K><<<g, b, 0, st>>>(wb, tokens, n_vocab, out, n_items, k, rb); break;
+    case TYPE_Q2_K: gather_rows_kernel<TYPE_Q2_K><<<g, b, 0, st>>>(wb, tokens, n_vocab, out, n_items, k, rb); break;
+    case TYPE_Q3_K: gather_rows_kernel<TYPE_Q3_K><<<g, b, 0, st>>>(wb, tokens, n_vocab, out, n_items, k, rb); break;
     case TYPE_Q4_0: gather_rows_kernel<TYPE_Q4_0><<<g, b, 0, st>>>(wb, tokens, n_vocab, out, n_items, k, rb); break;
     case TYPE_Q4_1: gather_rows_kernel<TYPE_Q4_1><<<g, b, 0, st>>>(wb, tokens, n_vocab, out, n_items, k, rb); break;
     case TYPE_Q5_0: gather_rows_kernel<TYPE_Q5_0><<<g, b, 0, st>>>(wb, tokens, n_vocab, out, n_items, k, rb); break;

@@ -55,7 +55,7 @@ __device__ __forceinline__ const uint8_t* row_ptr(const uint8_t* w, const uint8_
 // for a ring of 4 Q4_K units (9 VGPRs each) or 2 Q6_K / Q8_0 units (14 / 17);
 // deeper rings run in 8-wave workgroups (256 VGPRs).
 template <int TYPE>
-constexpr int max_d16() { return TYPE == TYPE_Q4_K ? 4 : 2; }
+constexpr int max_d16() { return TYPE == TYPE_Q4_K ? 4 : TYPE == TYPE_Q3_K ? 1 : 2; }  // Q3_K units: 20 VGPRs
 template <int TYPE, int D>
 constexpr int gemv_max_threads() { return D <= max_d16<TYPE>() ? 1024 : 512; }
 
@@ -277,6 +277,9 @@ constexpr int kNumCUs = 256;
 template <int TYPE>
 int ring_depth(int rpg, int wpr) {
     if (rpg <= 1) return 1;
+    // Q3_K units (20 VGPRs) keep 16-wave workgroups only without a ring:
+    // 4096 x 14336 13.3 us against 20.1 us at a ring of 2 in 8-wave groups
+    if (TYPE == TYPE_Q3_K) return 1;
     if (wpr > 1 && rpg <= 8) return 2;
     // Q6_K single-slice rows, 3..8 per wave: one row in flight (14336 x 4096:
     // 14.1 us against 19.2 us at a ring of 4)
@@ -471,6 +474,8 @@ int gemv_dispatch_fused(const void* w, const RowSrc& src, const GemvFuse& fz, co
     case TYPE_Q6_K: return launch_gemv_q<TYPE_Q6_K>(w, src, fz, x, y, n, k, rb, st);
     case TYPE_Q8_0: return launch_gemv_q<TYPE_Q8_0>(w, src, fz, x, y, n, k, rb, st);
     case TYPE_Q5_K: return launch_gemv_q<TYPE_Q5_K>(w, src, fz, x, y, n, k, rb, st);
+    case TYPE_Q2_K: return launch_gemv_q<TYPE_Q2_K>(w, src, fz, x, y, n, k, rb, st);
+    case TYPE_Q3_K: return launch_gemv_q<TYPE_Q3_K>(w, src, fz, x, y, n, k, rb, st);
     case TYPE_Q4_0: return launch_gemv_q<TYPE_Q4_0>(w, src, fz, x, y, n, k, rb, st);
     case TYPE_Q4_1: return launch_gemv_q<TYPE_Q4_1>(w, src, fz, x, y, n, k, rb, st);
     case TYPE_Q5_0: return launch_gemv_q<TYPE_Q5_0>(w, src, fz, x, y, n, k, rb, st);

@@ -24,6 +24,10 @@
 //   Q5_K  unit u: as Q4_K (header shared by the quad, qs[32c, 32c+32) at 48)
 //         plus the whole qh[32] at 16: bit 2c / 2c+1 of qh[l] is the fifth
 //         bit of the low / high nibble of qs[32c + l].
+//   Q2_K / Q3_K  unit u: super-block u/4, c = u%4, h = c/2, j0 = 2 (c%2):
+//         four 16-element runs t, codes = bits 2 (j0 + t/2) of qs[32h + 16 (t%2)
+//         + i], scales of sub-blocks 4c + t; Q3_K adds bit 4h + j of hmask[l]
+//         as the third code bit (clear: minus 4).
 //   Q4_0 / Q4_1 / Q5_0 / Q5_1  unit u: blocks 2u, 2u+1 (36 / 40 / 44 / 48
 //         bytes from u * that, 4-byte aligned); element j < 16 of a block is
 //         the low nibble of qs[j], j + 16 the high nibble; the fifth bit of
@@ -56,12 +60,16 @@ struct Q8Unit { uint4 a, b, c, d; uint32_t e; };
 struct Q6KUnit { uint4 la, lb, qh; uint32_t sc; uint32_t d; };
 // two 32-element blocks of NW dwords in all
 template <int NW> struct LegacyUnit { uint32_t w[NW]; };
+struct Q2KUnit { uint4 qa, qb; uint32_t sc, dd; };
+struct Q3KUnit { uint4 qa, qb, ha, hb; uint32_t s0, s1, s2, d; };
 
 template <int TYPE> struct UnitOf;
 template <> struct UnitOf<TYPE_Q4_K> { using T = Q4KUnit; };
 template <> struct UnitOf<TYPE_Q5_K> { using T = Q5KUnit; };
 template <> struct UnitOf<TYPE_Q8_0> { using T = Q8Unit; };
 template <> struct UnitOf<TYPE_Q6_K> { using T = Q6KUnit; };
+template <> struct UnitOf<TYPE_Q2_K> { using T = Q2KUnit; };
+template <> struct UnitOf<TYPE_Q3_K> { using T = Q3KUnit; };
 template <> struct UnitOf<TYPE_Q4_0> { using T = LegacyUnit<9>; };
 template <> struct UnitOf<TYPE_Q4_1> { using T = LegacyUnit<10>; };
 template <> struct UnitOf<TYPE_Q5_0> { using T = LegacyUnit<11>; };
@@ -110,6 +118,33 @@ __device__ __forceinline__ void load_unit(const uint8_t* row, int u, LegacyUnit<
     }
 #pragma unroll
     for (int i = NW / 4 * 4; i < NW; i++) v.w[i] = ld_b32(b + 4 * i);
+}
+
+__device__ __forceinline__ void load_unit(const uint8_t* row, int u, Q2KUnit& v) {
+    const uint8_t* b = row + (u >> 2) * 84;  // 4-byte aligned
+    const int c = u & 3;
+    v.qa = ld_b128_a4(b + 16 + 32 * (c >> 1));
+    v.qb = ld_b128_a4(b + 32 + 32 * (c >> 1));
+    v.sc = ld_b32(b + 4 * c);
+    v.dd = ld_b32(b + 80);
+}
+
+__device__ __forceinline__ uint32_t ld_b32_a2(const uint8_t* p) {
+    return static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(p)) |
+           (static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(p + 2)) << 16);
+}
+
+__device__ __forceinline__ void load_unit(const uint8_t* row, int u, Q3KUnit& v) {
+    const uint8_t* b = row + (u >> 2) * 110;  // 2-byte aligned
+    const int c = u & 3;
+    v.qa = ld_b128_a2(b + 32 + 32 * (c >> 1));
+    v.qb = ld_b128_a2(b + 48 + 32 * (c >> 1));
+    v.ha = ld_b128_a2(b);
+    v.hb = ld_b128_a2(b + 16);
+    v.s0 = ld_b32_a2(b + 96);
+    v.s1 = ld_b32_a2(b + 100);
+    v.s2 = ld_b32_a2(b + 104);
+    v.d = *reinterpret_cast<const uint16_t*>(b + 108);
 }
 
 __device__ __forceinline__ void load_unit(const uint8_t* row, int u, Q6KUnit& v) {
@@ -213,6 +248,52 @@ __device__ __forceinline__ float unit_dot(const Q5KUnit& v, const XSlice& xs, co
     const float dot = sc0 * (xs.s[0] * static_cast<float>(s0)) + sc1 * (xs.s[1] * static_cast<float>(s1));
     const float mins = m0 * xs.sum[0] + m1 * xs.sum[1];
     return d * dot - dmin * mins;
+}
+
+// Q2_K: sum over the four 16-element runs of d sc_t s_t Σ x16 q2 - dmin m_t Σ x.
+__device__ __forceinline__ float unit_dot(const Q2KUnit& v, const XSlice& xs, int u) {
+    const uint32_t qd[8] = {v.qa.x, v.qa.y, v.qa.z, v.qa.w, v.qb.x, v.qb.y, v.qb.z, v.qb.w};
+    const int j0 = 2 * (u & 1);
+    float acc = 0.f, accm = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int sh = 2 * (j0 + t / 2);
+        uint32_t q[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) q[i] = (qd[4 * (t & 1) + i] >> sh) & 0x03030303u;
+        const int sdot = run_dot(q, xs.h + 4 * t, xs.l + 4 * t, 4);
+        const uint32_t sm = (v.sc >> (8 * t)) & 0xFFu;
+        acc += static_cast<float>(sm & 0xFu) * (xs.s[t] * static_cast<float>(sdot));
+        accm += static_cast<float>(sm >> 4) * xs.sum[t];
+    }
+    return f16lo(v.dd) * acc - f16hi(v.dd) * accm;
+}
+
+// Q3_K: codes q2 | hbit << 2 (0..7), minus 4 through the run's x16 sum; the
+// 6-bit scale of sub-block 4c + t: low 4 bits from byte 4c + t (c < 2) or the
+// high nibble of byte 4(c - 2) + t, high 2 bits from bits 2c of byte 8 + t.
+__device__ __forceinline__ float unit_dot(const Q3KUnit& v, const XSlice& xs, int u) {
+    const uint32_t qd[8] = {v.qa.x, v.qa.y, v.qa.z, v.qa.w, v.qb.x, v.qb.y, v.qb.z, v.qb.w};
+    const uint32_t hd[8] = {v.ha.x, v.ha.y, v.ha.z, v.ha.w, v.hb.x, v.hb.y, v.hb.z, v.hb.w};
+    const int c = u & 3, h = c >> 1, j0 = 2 * (c & 1);
+    const uint32_t lowsrc = (c & 1) ? v.s1 : v.s0;
+    const int lowsh = c >= 2 ? 4 : 0;
+    float acc = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int j = j0 + t / 2;
+        uint32_t q[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int w = 16 * (t & 1) / 4 + i;  // dword of bytes l = 16 (t%2) + 4i ..
+            q[i] = ((qd[w] >> (2 * j)) & 0x03030303u) | (((hd[w] >> (4 * h + j)) & 0x01010101u) << 2);
+        }
+        const int sdot = run_dot(q, xs.h + 4 * t, xs.l + 4 * t, 4) - 4 * xs.isum[t];
+        const int lo = static_cast<int>((lowsrc >> (8 * t + lowsh)) & 0xFu);
+        const int hi = static_cast<int>((v.s2 >> (8 * t + 2 * c)) & 3u);
+        acc += static_cast<float>((lo | (hi << 4)) - 32) * (xs.s[t] * static_cast<float>(sdot));
+    }
+    return f16lo(v.d) * acc;
 }
 
 // Fifth bits b (4 consecutive elements, bits 0..3) moved to bit 4 of each byte.
@@ -372,7 +453,7 @@ __device__ __forceinline__ void load_x_task(const float* __restrict__ x, int uni
 
 template <int TYPE>
 __device__ __forceinline__ void encode_x_task(int task, int units, int slots, const float* vin, uint4* xq) {
-    constexpr int RUNLEN = TYPE == TYPE_Q6_K ? 16 : 32;
+    constexpr int RUNLEN = (TYPE == TYPE_Q6_K || TYPE == TYPE_Q2_K || TYPE == TYPE_Q3_K) ? 16 : 32;
     constexpr int TPR = RUNLEN / 8;
     const int u = task >> 3, p = task & 7;
     float v[8];

@@ -23,6 +23,8 @@ enum : int32_t {
     TYPE_Q5_0 = 6,
     TYPE_Q5_1 = 7,
     TYPE_Q8_0 = 8,
+    TYPE_Q2_K = 10,
+    TYPE_Q3_K = 11,
     TYPE_Q4_K = 12,
     TYPE_Q5_K = 13,
     TYPE_Q6_K = 14,
@@ -40,19 +42,20 @@ enum : int32_t {
 __host__ __device__ constexpr int64_t block_elems(int32_t t) {
     return t == TYPE_F32 || t == TYPE_F16 || t == TYPE_BF16 ? 1
          : (t == TYPE_Q8_0 || t == TYPE_Q4_0 || t == TYPE_Q4_1 || t == TYPE_Q5_0 || t == TYPE_Q5_1) ? 32
-         : (t == TYPE_Q4_K || t == TYPE_Q5_K || t == TYPE_Q6_K) ? 256 : -1;
+         : (t == TYPE_Q2_K || t == TYPE_Q3_K || t == TYPE_Q4_K || t == TYPE_Q5_K || t == TYPE_Q6_K) ? 256 : -1;
 }
 
 __host__ __device__ constexpr int64_t block_bytes(int32_t t) {
     return t == TYPE_F32 ? 4 : (t == TYPE_F16 || t == TYPE_BF16) ? 2 : t == TYPE_Q4_0 ? 18 : t == TYPE_Q4_1 ? 20
-         : t == TYPE_Q5_0 ? 22 : t == TYPE_Q5_1 ? 24 : t == TYPE_Q8_0 ? 34 : t == TYPE_Q4_K ? 144
+         : t == TYPE_Q5_0 ? 22 : t == TYPE_Q5_1 ? 24 : t == TYPE_Q8_0 ? 34 : t == TYPE_Q2_K ? 84
+         : t == TYPE_Q3_K ? 110 : t == TYPE_Q4_K ? 144
          : t == TYPE_Q5_K ? 176 : t == TYPE_Q6_K ? 210 : -1;
 }
 
 // Block-quantized types with dequant-fused GEMV kernels (gemv.hip).
 __host__ __device__ constexpr bool is_block_type(int32_t t) {
     return t == TYPE_Q4_0 || t == TYPE_Q4_1 || t == TYPE_Q5_0 || t == TYPE_Q5_1 || t == TYPE_Q8_0 ||
-           t == TYPE_Q4_K || t == TYPE_Q5_K || t == TYPE_Q6_K;
+           t == TYPE_Q2_K || t == TYPE_Q3_K || t == TYPE_Q4_K || t == TYPE_Q5_K || t == TYPE_Q6_K;
 }
 
 // Bytes of one row of k elements; -1 when the type is unknown or k is not a

@@ -55,7 +55,8 @@ NAMES = {
 
 # Types with gfx950 kernels in libvbhip (decode, embedding rows, GEMV).
 DEVICE_TYPES = (GGML_TYPE_F32, GGML_TYPE_F16, GGML_TYPE_BF16, GGML_TYPE_Q4_0, GGML_TYPE_Q4_1, GGML_TYPE_Q5_0,
-                GGML_TYPE_Q5_1, GGML_TYPE_Q8_0, GGML_TYPE_Q4_K, GGML_TYPE_Q5_K, GGML_TYPE_Q6_K)
+                GGML_TYPE_Q5_1, GGML_TYPE_Q8_0, GGML_TYPE_Q2_K, GGML_TYPE_Q3_K, GGML_TYPE_Q4_K, GGML_TYPE_Q5_K,
+                GGML_TYPE_Q6_K)
 # Of those, the types the quantizer (vb_quantize_rows) writes.
 QUANTIZE_TYPES = (GGML_TYPE_F32, GGML_TYPE_F16, GGML_TYPE_Q8_0, GGML_TYPE_Q4_K, GGML_TYPE_Q6_K)
 

@@ -21,9 +21,9 @@ Differences from the reference, on purpose: the data section follows
 ``general.alignment`` when the file sets it (the reference always uses 32);
 every metadata type is kept (the reference drops 16-bit values and most
 array element types); ``load_tensor`` decodes the quantized types that have
-device kernels (Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K; bit-exact
-GGUF decoding on the GPU) and raises ValueError for the others (Q2_K, Q3_K,
-Q8_1, Q8_K), where the reference's Python decoders use non-GGUF bit layouts
+device kernels (Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K;
+bit-exact GGUF decoding on the GPU) and raises ValueError for the others
+(Q8_1, Q8_K), where the reference's Python decoders use non-GGUF bit layouts
 for several of them.
 """
 from __future__ import annotations
