@@ -57,9 +57,13 @@ def parse():
     p.add_argument("--extra", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--pmc-pass", action="store_true",
-                   help="eager launches for rocprofv3 --pmc: 32 headline GEMVs, then a 256 MiB copy "
-                        "(torch.neg) that calibrates FETCH_SIZE / WRITE_SIZE")
+    p.add_argument("--pmc-pass", nargs="?", const="gemv", choices=["gemv", "gemm8", "gemm512"],
+                   help="eager launches for rocprofv3 --pmc: 32 headline GEMVs (gemv) or 16 Q4_K GEMMs "
+                        "14336x4096 at M=8 / 512 (gemm8, gemm512), then a 256 MiB copy (torch.neg) "
+                        "that calibrates FETCH_SIZE / WRITE_SIZE")
+    p.add_argument("--counter-table", nargs="+", metavar="CSV",
+                   help="per-kernel means of every counter in rocprofv3 counter_collection.csv files, "
+                        "as a markdown table, with the MFMA and traffic figures derived from them")
     p.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                    help="turn the counter_collection.csv files of two --pmc-pass runs (FETCH_SIZE, "
                         "WRITE_SIZE) into " + TRAFFIC_FILE)
@@ -456,22 +460,37 @@ def cpu_baseline(qtype, n, k, seconds):
     }
 
 
-def pmc_pass():
+def pmc_pass(workload="gemv"):
     """Launches for counter collection: no graph (per-dispatch counters), no
-    timing.  The GEMVs rotate over 16 weight copies as in the timed run."""
+    timing.  The GEMVs rotate over 16 weight copies as in the timed run; the
+    GEMMs (fp16 X with 0.1% outliers x20, as timed) over 4."""
     import torch
     from vibeblade_amd import _lib, ggml
     _lib.init(0)
     qtype, n, k = ggml.GGML_TYPE_Q4_K, 14336, 4096
-    gen = torch.Generator(device="cuda").manual_seed(SEED)
-    copies = make_copies(qtype, n, k, NCOPIES, gen)
-    x = torch.randn(k, generator=gen, device="cuda")
-    y = torch.empty(n, device="cuda")
     lib = _lib.load()
     st = torch.cuda.current_stream().cuda_stream
-    for i in range(32):
-        c = copies[i % NCOPIES]
-        _lib.check("vb_gemv", lib.vb_gemv(c.ptr(), x.data_ptr(), y.data_ptr(), n, k, qtype, st))
+    if workload == "gemv":
+        gen = torch.Generator(device="cuda").manual_seed(SEED)
+        copies = make_copies(qtype, n, k, NCOPIES, gen)
+        x = torch.randn(k, generator=gen, device="cuda")
+        y = torch.empty(n, device="cuda")
+        for i in range(32):
+            c = copies[i % NCOPIES]
+            _lib.check("vb_gemv", lib.vb_gemv(c.ptr(), x.data_ptr(), y.data_ptr(), n, k, qtype, st))
+        what = "32 GEMV dispatches"
+    else:
+        m = 8 if workload == "gemm8" else 512
+        gen = torch.Generator(device="cuda").manual_seed(SEED + m)
+        copies = make_copies(qtype, n, k, 4, gen)
+        x = torch.randn((m, k), generator=gen, device="cuda")
+        x[torch.rand((m, k), generator=gen, device="cuda") < 0.001] *= 20.0
+        xh = x.half().contiguous()
+        y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        for i in range(16):
+            c = copies[i % 4]
+            _lib.check("vb_gemm", lib.vb_gemm(c.ptr(), xh.data_ptr(), 1, y.data_ptr(), m, n, k, qtype, 0, st))
+        what = f"16 GEMM dispatches at M={m}"
     torch.cuda.synchronize()
     del copies
     torch.cuda.empty_cache()
@@ -480,7 +499,7 @@ def pmc_pass():
     for _ in range(4):
         torch.neg(src, out=dst)
     torch.cuda.synchronize()
-    print("[bench] pmc pass done: 32 GEMV dispatches, 4 calibration copies", file=sys.stderr)
+    print(f"[bench] pmc pass done: {what}, 4 calibration copies", file=sys.stderr)
 
 
 def _counter_means(path, counter):
@@ -498,6 +517,43 @@ def _counter_means(path, counter):
     for (name, _), v in sums.items():
         per_kernel.setdefault(name, []).append(v)
     return {name: (sum(v) / len(v), len(v)) for name, v in per_kernel.items()}
+
+
+def counter_table(paths):
+    """Markdown table of per-kernel mean counter values (per dispatch) over
+    rocprofv3 counter_collection.csv files, plus derived figures:
+    MFMA FLOPs = SQ_INSTS_VALU_MFMA_MOPS_F16 x 512 (the counter counts units
+    of 512 FLOPs), MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8
+    XCDs x 256 CUs x 4 SIMDs), and FETCH_SIZE / WRITE_SIZE scaled by the calibration
+    copy (CALIB_BYTES read and written) when it is in the same file."""
+    import csv
+    rows = {}
+    for path in paths:
+        with open(path) as f:
+            recs = list(csv.DictReader(f))
+        counters = sorted({r["Counter_Name"] for r in recs})
+        for c in counters:
+            for name, (v, cnt) in _counter_means(path, c).items():
+                rows.setdefault(name, {})[c] = (v, cnt)
+    calib = {c: v for name, d in rows.items() if "neg_kernel" in name for c, (v, _) in d.items()}
+    names = sorted({c for d in rows.values() for c in d})
+    print("| Kernel | dispatches | " + " | ".join(names) + " | derived |")
+    print("|---" * (len(names) + 3) + "|")
+    for kname, d in sorted(rows.items(), key=lambda t: t[0]):
+        short = kname.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0][:80]
+        nd = max(cnt for _, cnt in d.values())
+        cells = [f"{d[c][0]:.4g}" if c in d else "" for c in names]
+        der = []
+        if "SQ_INSTS_VALU_MFMA_MOPS_F16" in d:
+            der.append(f"MFMA f16 {d['SQ_INSTS_VALU_MFMA_MOPS_F16'][0] * 512 / 1e9:.3f} GFLOP")
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in d and "GRBM_GUI_ACTIVE" in d:
+            # GRBM_GUI_ACTIVE comes summed over the 8 XCDs' GRBM instances
+            der.append("MFMA busy {:.1%}".format(
+                d["SQ_VALU_MFMA_BUSY_CYCLES"][0] / (d["GRBM_GUI_ACTIVE"][0] / 8 * 256 * 4)))
+        for c, fac_name in (("FETCH_SIZE", "read"), ("WRITE_SIZE", "write")):
+            if c in d and calib.get(c):
+                der.append(f"{fac_name} {d[c][0] * CALIB_BYTES / calib[c] / 1e6:.2f} MB (copy-scaled)")
+        print(f"| `{short}` | {nd} | " + " | ".join(cells) + " | " + "; ".join(der) + " |")
 
 
 def summarize_pmc(fetch_csv, write_csv):
@@ -539,8 +595,11 @@ def main():
     if args.summarize_pmc:
         summarize_pmc(*args.summarize_pmc)
         return
+    if args.counter_table:
+        counter_table(args.counter_table)
+        return
     if args.pmc_pass:
-        pmc_pass()
+        pmc_pass(args.pmc_pass)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "

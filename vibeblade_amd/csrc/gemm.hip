@@ -37,13 +37,21 @@ constexpr int X_F16 = 1;
 //  * A: the 256 x 64 X tile is loaded with row-contiguous 16-byte pieces
 //    (8 lanes per 128-byte row: 4 x fewer cache-line requests than loading
 //    the fragments directly, and no duplicate loads across wave columns) two
-//    steps ahead, converted to fp16 and stored in rows padded to 144 bytes;
+//    steps ahead, converted to fp16 and stored in swizzled 128-byte rows (below);
 //    the waves read their A fragments with ds_read_b128.
 // One barrier per step.  The grid is ceil(N / BN) x ceil(M / 256).
 constexpr int TB_M = 256;
-constexpr int XS_STRIDE = 72;  // halves per LDS row of X (64 + 8 padding)
+constexpr int XS_ROW = 64;  // halves per LDS row of X (swizzled, no padding)
 // weight prefetch distance (steps; K / 64 is a multiple of 4)
 constexpr int PD = 4;
+
+// X tile in LDS: 128-byte rows (64 halves) whose eight 16-byte pieces are
+// XOR-swizzled by (row / 2) % 8, so the ds_read_b128 of the A fragments (16
+// rows x one piece per lane group) and the row-contiguous tile stores meet
+// no bank conflicts.  Rows padded to 144 bytes instead showed 3.67e6 bank
+// conflict cycles per launch (SQ_LDS_BANK_CONFLICT, M = 512) and ran 2-4 %
+// slower; the swizzle reads 0.
+__device__ __forceinline__ int xswz(int row) { return (row >> 1) & 7; }
 
 template <int XT, int NF, int WN>
 __global__ void __launch_bounds__(256 * WN) gemm_q4k_tiled(const uint8_t* __restrict__ w,
@@ -62,7 +70,7 @@ __global__ void __launch_bounds__(256 * WN) gemm_q4k_tiled(const uint8_t* __rest
     // [buffer][k half][fragment][lane]; fragment NF takes the stores of
     // threads without a unit (keeps the loop body branch-free)
     __shared__ uint4 bt[2][2][NF + 1][64];
-    __shared__ __attribute__((aligned(16))) _Float16 xs[2][TB_M * XS_STRIDE];
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2][TB_M * XS_ROW];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(tid >> 6));
@@ -135,7 +143,7 @@ __global__ void __launch_bounds__(256 * WN) gemm_q4k_tiled(const uint8_t* __rest
         int r = mt0 + row;
         r = r < M ? r : M - 1;
         xoff[i] = (static_cast<uint32_t>(r) * static_cast<uint32_t>(K) + 8u * static_cast<uint32_t>(part)) * XE;
-        xlds[i] = row * XS_STRIDE + 8 * part;
+        xlds[i] = row * XS_ROW + 8 * (part ^ xswz(row));
     }
     uint4 xr[2][XPT][XR];
     auto load_x = [&](int step, int slot) {
@@ -162,7 +170,10 @@ __global__ void __launch_bounds__(256 * WN) gemm_q4k_tiled(const uint8_t* __rest
             *reinterpret_cast<uint4*>(&xs[buf][xlds[i]]) = v;
         }
     };
-    const int arow = (wm * 64 + j) * XS_STRIDE + 8 * g;  // A fragment of this lane, a = 0, ks = 0
+    // A fragment of this lane for a = 0: row wm * 64 + j, 16-byte piece 4 ks + g
+    // (16 a + wm * 64 does not change the row's swizzle)
+    const int arow = (wm * 64 + j) * XS_ROW;
+    const int aoff0 = arow + 8 * (g ^ xswz(j)), aoff1 = arow + 8 * ((4 + g) ^ xswz(j));
 
     float4_t acc[4][NW];
 #pragma unroll
@@ -192,7 +203,8 @@ __global__ void __launch_bounds__(256 * WN) gemm_q4k_tiled(const uint8_t* __rest
             load_w(step + PD, r);  // slot r held step `step`, dequantized during the previous step
             __builtin_amdgcn_sched_barrier(0);
             const uint4* bsrc = &bt[buf][0][wn * NW][0];
-            const _Float16* asrc = &xs[buf][arow];
+            const _Float16* asrc0 = &xs[buf][aoff0];
+            const _Float16* asrc1 = &xs[buf][aoff1];
             // every fragment of the step is requested before the first MFMA:
             // one LDS latency per step instead of one per MFMA group
             Frag b[2][NW], af[2][4];
@@ -205,7 +217,7 @@ __global__ void __launch_bounds__(256 * WN) gemm_q4k_tiled(const uint8_t* __rest
                 }
 #pragma unroll
                 for (int a = 0; a < 4; a++) {
-                    const uint4 v = *reinterpret_cast<const uint4*>(asrc + a * 16 * XS_STRIDE + 32 * ks);
+                    const uint4 v = *reinterpret_cast<const uint4*>((ks ? asrc1 : asrc0) + a * 16 * XS_ROW);
                     af[ks][a].u[0] = v.x; af[ks][a].u[1] = v.y; af[ks][a].u[2] = v.z; af[ks][a].u[3] = v.w;
                 }
             }
