@@ -1,26 +1,33 @@
 """Benchmark: Q4_K GEMV effective HBM GB/s at 14336x4096, M=1, on one MI355X.
 
-One step = one dequant-fused GEMV y = W x with W a GGUF Q4_K 14336x4096 matrix
+Workload: one dequant-fused GEMV y = W x with W a GGUF Q4_K 14336x4096 matrix
 (Llama-3-8B FFN gate/up shape), x fp32 (4096), y fp32 (14336).  Weights are
 drawn N(0, 0.02) from a fixed seed and quantized on the device; 16 distinct
 weight copies (528 MB, more than the 256 MB MALL) are used round robin so
-that every step streams its weights from HBM.  Steps are launched as a HIP
-graph of 16 GEMVs (one per copy) so host launch overhead is off the clock.
-GPU time is taken with HIP events on the launch stream around the K timed
-steps (bracketed by synchronize).
+that every launch streams its weights from HBM.
 
-value = algorithmic bytes per step / (time per step), algorithmic bytes =
-weights read once + x read once + y written once = 33,103,872 B.
+A step is one pass over the 16 copies: 16 GEMV launches, captured once as a
+HIP graph and replayed, so host launch overhead is off the clock.  W
+untimed warmup steps, then exactly K timed steps; a HIP event on the replay
+stream is recorded before the first step and after every step, so each
+step is timed on its own.  The reported time per launch is the median over
+the K steps of (step time / 16); K = 20 is 320 launches.
 
-cpu_baseline: the reference's CPU path (cpp/src/dequant.cpp gemv_dequant,
-compiled from the reference sources into oracle/_ref with its release flags)
-on the same shape, single thread, on a bounded sample (~10 s), reported as
-the same GB/s metric; the oracle's restatement of that loop is used when the
-compiled reference is absent.
+value = algorithmic bytes per launch / median time per launch, algorithmic
+bytes = weights read once + x read once + y written once = 33,103,872 B.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra]
-  --extra also measures the other single-GPU GEMV shapes and prints one JSON
-  line per shape to stderr (the main line stays the headline metric).
+cpu_baseline: the oracle's C restatement of the reference CPU path
+(cpp/src/dequant.cpp:739-780 gemv_dequant: decode each of the K rows into an
+fp32 scratch row, then a saxpy; single thread, like the reference's
+gemv_dequant_mt at :783-792) on the same shape, on a bounded sample (about
+10 s), reported as the same GB/s metric with the host CPU model.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra [LIST]]
+  --extra also measures the other configurations (comma list of gemv,
+  sparse, moe, predict, ffn, gguf, gemm, msweep, cpu; default all) and
+  prints one JSON line per workload to stderr (the main line stays the
+  headline metric).  Every workload rotates more than 512 MB of distinct
+  weights.
 """
 from __future__ import annotations
 
@@ -41,7 +48,11 @@ GEMV_KERNEL = "gemv_q_kernel<12"  # the Q4_K v_dot4 GEMV instantiations
 CALIB_BYTES = 256 << 20            # bytes read and written by the calibration copy
 MFMA_FP16_PEAK_TFS = 2500.0  # dense fp16 MFMA, MI355X
 NCOPIES = 16
+MIN_ROTATION_BYTES = 512 << 20     # every timed rotation touches more than this
 SEED = 1234
+EXTRA_ALL = ("gemv", "sparse", "moe", "predict", "ffn", "gguf", "gemm", "msweep", "cpu")
+DTYPE_GEMV = ("i8 dot (v_dot4_i32_i8) -> i32, f32 scales; x as 16-bit fixed point per 32-element run "
+              "(two int8 halves, per-run f32 scale)")
 
 
 def alg_bytes_gemv(qtype: int, n: int, k: int) -> int:
@@ -52,9 +63,10 @@ def alg_bytes_gemv(qtype: int, n: int, k: int) -> int:
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=2000)
-    p.add_argument("--warmup", type=int, default=200)
-    p.add_argument("--extra", action="store_true")
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--extra", nargs="?", const=",".join(EXTRA_ALL), default=None,
+                   help="comma list of extra workloads: " + ",".join(EXTRA_ALL))
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--pmc-pass", nargs="?", const="gemv", choices=["gemv", "gemm8", "gemm512"],
@@ -70,6 +82,11 @@ def parse():
     return p.parse_args()
 
 
+def copies_for(bytes_per_copy: int, minimum: int = NCOPIES) -> int:
+    """Distinct weight copies so that one rotation touches > MIN_ROTATION_BYTES."""
+    return max(minimum, MIN_ROTATION_BYTES // max(1, bytes_per_copy) + 1)
+
+
 def make_copies(qtype, n, k, ncopies, gen):
     import torch
     from vibeblade_amd.tensor import QTensor
@@ -82,23 +99,36 @@ def make_copies(qtype, n, k, ncopies, gen):
     return copies
 
 
-GRAPH_LAUNCHES = 128  # launches captured per graph: amortizes the gap between replays
+class Timing:
+    """Per-launch times of a timed run: median over steps of (step time /
+    launches per step), the plain mean, and the counts."""
+
+    def __init__(self, step_ms, per_step, total_ms, graph):
+        self.steps = len(step_ms)
+        self.per_step = per_step
+        self.launches = self.steps * per_step
+        self.step_ms = float(np.median(step_ms))
+        self.ms = self.step_ms / per_step               # median per launch
+        self.mean_ms = total_ms / self.launches          # mean per launch
+        self.graph = graph
+
+    def us(self):
+        return round(self.ms * 1e3, 3)
 
 
-def time_launches(launch_fns, steps, warmup):
-    """Capture calls of the closures in `launch_fns` (each takes a stream
-    handle; rounds over the list until about GRAPH_LAUNCHES launches) in a
-    HIP graph and replay it; returns (ms per launch, graph used, launches
-    timed).  HIP events on the replay stream bracket the timed region."""
+def time_launches(launch_fns, steps, warmup, min_launches=200):
+    """One step = one call of every closure in `launch_fns` (each takes a
+    stream handle), captured once as a HIP graph and replayed.  `warmup`
+    untimed steps, then max(steps, ceil(min_launches / len)) timed steps, each
+    bracketed by HIP events on the replay stream.  Returns a Timing."""
     import torch
     stream = torch.cuda.Stream()
-    rounds = max(1, GRAPH_LAUNCHES // len(launch_fns))
-    nl = rounds * len(launch_fns)
+    nl = len(launch_fns)
+    steps = max(steps, -(-min_launches // nl))
 
     def launch_all(s):
-        for _ in range(rounds):
-            for f in launch_fns:
-                f(s)
+        for f in launch_fns:
+            f(s)
 
     graph = None
     with torch.cuda.stream(stream):
@@ -111,32 +141,34 @@ def time_launches(launch_fns, steps, warmup):
         except Exception as e:  # graph capture unavailable: direct launches
             print(f"[bench] graph capture failed ({e}); timing direct launches", file=sys.stderr)
             graph = None
-    reps_w = max(1, warmup // nl)
-    reps = max(1, (steps + nl - 1) // nl)
 
-    def run(nrep):
-        with torch.cuda.stream(stream):
-            for _ in range(nrep):
-                if graph is not None:
-                    graph.replay()
-                else:
-                    launch_all(stream.cuda_stream)
+    def one():
+        if graph is not None:
+            graph.replay()
+        else:
+            launch_all(stream.cuda_stream)
 
-    run(reps_w)
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            one()
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    run(reps)
-    end.record(stream)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    with torch.cuda.stream(stream):
+        evs[0].record(stream)
+        for i in range(steps):
+            one()
+            evs[i + 1].record(stream)
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end)
-    return ms / (reps * nl), graph is not None, reps * nl
+    step_ms = [evs[i].elapsed_time(evs[i + 1]) for i in range(steps)]
+    return Timing(step_ms, nl, evs[0].elapsed_time(evs[-1]), graph is not None)
 
 
-def time_gemv(qtype, n, k, steps, warmup, ncopies=NCOPIES):
-    """Returns (ms_per_step, graph_used, steps_timed, copies, x, ys)."""
+def time_gemv(qtype, n, k, steps, warmup, ncopies=None):
+    """Returns (Timing, copies, x, ys)."""
     import torch
-    from vibeblade_amd import _lib
+    from vibeblade_amd import _lib, ggml
+    if ncopies is None:
+        ncopies = copies_for(n * ggml.row_bytes(qtype, k))
     gen = torch.Generator(device="cuda").manual_seed(SEED)
     copies = make_copies(qtype, n, k, ncopies, gen)
     x = torch.randn(k, generator=gen, device="cuda")
@@ -151,21 +183,29 @@ def time_gemv(qtype, n, k, steps, warmup, ncopies=NCOPIES):
             if rc != 0:
                 _lib.check("vb_gemv", rc)
         return f
-    ms, graph_used, nsteps = time_launches([mk(i, c) for i, c in enumerate(copies)], steps, warmup)
-    return ms, graph_used, nsteps, copies, x, ys
+    tm = time_launches([mk(i, c) for i, c in enumerate(copies)], steps, warmup)
+    return tm, copies, x, ys
 
 
-def time_gemm(m, n, k, steps, warmup, ncopies):
-    """Q4_K GEMM with fp16 X (0.1% outliers x20); returns (ms, rel-L2 of copy 0)."""
+def gemm_inputs(m, k, gen):
+    """fp16 X (m, k) ~ N(0, 1) with 0.1 % of the entries scaled x20."""
+    import torch
+    x = torch.randn((m, k), generator=gen, device="cuda")
+    x[torch.rand((m, k), generator=gen, device="cuda") < 0.001] *= 20.0
+    return x.half().contiguous()
+
+
+def time_gemm(m, n, k, steps, warmup, qtype=None):
+    """Q4_K (or `qtype`) GEMM with fp16 X; weight copies rotate over > 512 MB.
+    Returns (Timing, rel-L2 of copy 0 against the fp64 oracle product)."""
     import torch
     import oracle as O
     from vibeblade_amd import _lib, ggml
+    qtype = ggml.GGML_TYPE_Q4_K if qtype is None else qtype
     gen = torch.Generator(device="cuda").manual_seed(SEED + m)
-    copies = make_copies(ggml.GGML_TYPE_Q4_K, n, k, ncopies, gen)
-    x = torch.randn((m, k), generator=gen, device="cuda")
-    x[torch.rand((m, k), generator=gen, device="cuda") < 0.001] *= 20.0
-    xh = x.half().contiguous()
-    ys = torch.empty((ncopies, m, n), dtype=torch.float32, device="cuda")
+    copies = make_copies(qtype, n, k, copies_for(n * ggml.row_bytes(qtype, k)), gen)
+    xh = gemm_inputs(m, k, gen)
+    ys = torch.empty((len(copies), m, n), dtype=torch.float32, device="cuda")
     lib = _lib.load()
 
     def mk(i, c):
@@ -176,40 +216,47 @@ def time_gemm(m, n, k, steps, warmup, ncopies):
             if rc != 0:
                 _lib.check("vb_gemm", rc)
         return f
-    ms, _, _ = time_launches([mk(i, c) for i, c in enumerate(copies)], steps, warmup)
+    tm = time_launches([mk(i, c) for i, c in enumerate(copies)], steps, warmup)
     w = O.dequantize(copies[0].to_numpy_bytes(), k, copies[0].qtype).astype(np.float64)
     want = xh.float().cpu().numpy().astype(np.float64) @ w.T
     err = O.rel_l2(ys[0].cpu().numpy(), want)
-    return ms, err
+    return tm, err
 
 
-def time_sparse(layout, steps, warmup, ncopies=8, block=False):
-    """TurboSparse FFN, H=4096, I=14336, Q4_K, S ~ Bernoulli(0.1), relu(g)*relu(u);
-    block: with the pre-FFN RMSNorm and the residual (vb_sparse_ffn_block).
-    Returns (ms per call, |S|, algorithmic bytes)."""
+SPARSE_COPIES = 64  # 64 x 9.9 MB (neuron-major) = 634 MB touched per rotation
+
+
+def time_sparse(layout, steps, warmup, block=False):
+    """TurboSparse FFN, H=4096, I=14336, Q4_K, relu(g)*relu(u); block: with the
+    pre-FFN RMSNorm and the residual (vb_sparse_ffn_block).  SPARSE_COPIES
+    weight sets, each with its own active set S ~ Bernoulli(0.1), so one
+    rotation reads more than 512 MB.  Returns (Timing, mean |S|, mean
+    algorithmic bytes per call, rel-L2 of set 0 against the fp64 oracle)."""
     import torch
+    import oracle as O
     from vibeblade_amd import _lib, ggml
     from vibeblade_amd.tensor import QTensor, ACT_RELU2
     h, i = 4096, 14336
     gen = torch.Generator(device="cuda").manual_seed(SEED + 4)
+    rng = np.random.default_rng(42)
     sets = []
-    for _ in range(ncopies):
+    for _ in range(SPARSE_COPIES):
         g = QTensor.quantize(torch.randn((i, h), generator=gen, device="cuda") * 0.02, ggml.GGML_TYPE_Q4_K)
         u = QTensor.quantize(torch.randn((i, h), generator=gen, device="cuda") * 0.02, ggml.GGML_TYPE_Q4_K)
         dshape = (h, i) if layout == 0 else (i, h)
         d = QTensor.quantize(torch.randn(dshape, generator=gen, device="cuda") * 0.02, ggml.GGML_TYPE_Q4_K)
-        sets.append((g, u, d))
-    rng = np.random.default_rng(42)
-    s = torch.from_numpy(np.flatnonzero(rng.random(i) < 0.10).astype(np.int32)).cuda()
+        s = torch.from_numpy(np.flatnonzero(rng.random(i) < 0.10).astype(np.int32)).cuda()
+        sets.append((g, u, d, s))
     x = torch.randn(h, generator=gen, device="cuda")
-    y = torch.empty(h, device="cuda")
+    ys = torch.empty((SPARSE_COPIES, h), device="cuda")
     lib = _lib.load()
-    nbytes = lib.vb_sparse_ffn_workspace(h, i, s.numel(), layout)
+    nbytes = max(lib.vb_sparse_ffn_workspace(h, i, t[3].numel(), layout) for t in sets)
     ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
-
     nw = 1.0 + 0.1 * torch.randn(h, generator=gen, device="cuda")
 
-    def mk(g, u, d):
+    def mk(j, g, u, d, s):
+        y = ys[j]
+
         def f(st):
             if block:
                 _lib.check("vb_sparse_ffn_block", lib.vb_sparse_ffn_block(
@@ -221,20 +268,28 @@ def time_sparse(layout, steps, warmup, ncopies=8, block=False):
             if rc != 0:
                 _lib.check("vb_sparse_ffn", rc)
         return f
-    ms, _, _ = time_launches([mk(*t) for t in sets], steps, warmup)
-    n_s = int(s.numel())
+    tm = time_launches([mk(j, *t) for j, t in enumerate(sets)], steps, warmup)
+    n_s = np.array([t[3].numel() for t in sets], dtype=np.float64)
     rb = 2304
     down_b = h * 8064 if layout == 0 else n_s * rb
-    ab = 2 * n_s * rb + down_b + 4 * h + 4 * h + 4 * n_s + (8 * h if block else 0)
-    return ms, n_s, ab
+    ab = float(np.mean(2 * n_s * rb + down_b + 4 * h + 4 * h + 4 * n_s + (8 * h if block else 0)))
+    err = None
+    if not block:
+        g, u, d, s = sets[0]
+        dec = lambda q: O.dequantize(q.to_numpy_bytes(), q.k, q.qtype)
+        dd = dec(d) if layout == 0 else dec(d).T
+        want = O.sparse_ffn(dec(g), dec(u), dd, x.cpu().numpy(), s.cpu().numpy(), O.ACT_DRELU)
+        err = O.rel_l2(ys[0].cpu().numpy(), want)
+    return tm, float(n_s.mean()), ab, err
 
 
 def time_ffn_block(down_type, fused, steps, warmup, ncopies=8):
     """One token through the FFN block, hd=4096, inter=14336, Q4_K gate/up,
     down Q4_K or Q6_K (the two Q4_K_M mixes), RMSNorm + SiLU + residual.
+    8 weight sets (8 x 99-114 MB per rotation).
     fused: vb_ffn_block (2 launches); else the reference's step order as
     separate launches (rms_norm, gate GEMV, up GEMV, silu, multiply, down
-    GEMV, residual add).  Returns (ms per call, algorithmic bytes)."""
+    GEMV, residual add).  Returns (Timing, algorithmic bytes)."""
     import torch
     from vibeblade_amd import _lib, ggml
     from vibeblade_amd.tensor import QTensor, ACT_SILU
@@ -269,24 +324,25 @@ def time_ffn_block(down_type, fused, steps, warmup, ncopies=8):
             _lib.check("vb_gemv", lib.vb_gemv(d.ptr(), hb.data_ptr(), db.data_ptr(), hd, inter, d.qtype, st))
             torch.add(x, db, out=y)
         return f
-    ms, _, _ = time_launches([mk(*t) for t in sets], steps, warmup)
+    tm = time_launches([mk(*t) for t in sets], steps, warmup)
     ab = 2 * inter * 2304 + hd * ggml.row_bytes(down_type, inter) + 4 * hd * 4 + 8 * inter
-    return ms, ab
+    return tm, ab
 
 
-def time_sparse_predicted(steps, warmup, ncopies=8, predict_only=False):
+def time_sparse_predicted(steps, warmup, predict_only=False):
     """One TurboSparse token step with the active set predicted on the device:
     vb_ema_predict (warm EMA state, k = 10 %), vb_sparse_ffn_block over the
     predicted set through its device count (RMSNorm + relu(g)*relu(u) +
     residual, neuron-major Q4_K down, H=4096, I=14336) and vb_ema_update with
-    the used mask.  Returns (ms per step, mean |S|)."""
+    the used mask.  SPARSE_COPIES weight sets (> 512 MB of active rows per
+    rotation).  Returns (Timing, |S| of the last step)."""
     import torch
     from vibeblade_amd import _lib, ggml
     from vibeblade_amd.tensor import QTensor, ACT_RELU2
     h, i = 4096, 14336
     gen = torch.Generator(device="cuda").manual_seed(SEED + 7)
     sets = []
-    for _ in range(ncopies):
+    for _ in range(1 if predict_only else SPARSE_COPIES):
         g = QTensor.quantize(torch.randn((i, h), generator=gen, device="cuda") * 0.02, ggml.GGML_TYPE_Q4_K)
         u = QTensor.quantize(torch.randn((i, h), generator=gen, device="cuda") * 0.02, ggml.GGML_TYPE_Q4_K)
         d = QTensor.quantize(torch.randn((i, h), generator=gen, device="cuda") * 0.02, ggml.GGML_TYPE_Q4_K)
@@ -314,18 +370,19 @@ def time_sparse_predicted(steps, warmup, ncopies=8, predict_only=False):
                 count.data_ptr(), ACT_RELU2, 1, y.data_ptr(), h, i, g.qtype, ws.data_ptr(), ws.numel(), st))
             _lib.check("vb_ema_update", lib.vb_ema_update(probs.data_ptr(), i, mask.data_ptr(), 0.1, st))
         return f
-    ms, _, _ = time_launches([mk(*t) for t in sets], steps, warmup)
-    return ms, int(count.item())
+    tm = time_launches([mk(*t) for t in sets], steps, warmup)
+    return tm, int(count.item())
 
 
 def time_moe(steps, warmup):
-    """8 Q4_K experts (gate/up 14336x4096, down 4096x14336), 16 tokens, top-2.
-    Returns (ms per call, experts hit, algorithmic bytes)."""
-    import torch
-    from vibeblade_amd import ggml
-    from vibeblade_amd.tensor import QTensor, moe_grouped_ffn
+    """8 Q4_K experts (gate/up 14336x4096, down 4096x14336), 16 tokens, top-2
+    (793 MB of weights per call when all 8 are hit).  Returns (Timing,
+    experts hit, algorithmic bytes, rel-L2 against the fp64 oracle)."""
     import ctypes
-    from vibeblade_amd import _lib
+    import torch
+    import oracle as O
+    from vibeblade_amd import _lib, ggml
+    from vibeblade_amd.tensor import QTensor, moe_grouped_ffn
     e_n, h, i, t, topk = 8, 4096, 14336, 16, 2
     gen = torch.Generator(device="cuda").manual_seed(SEED + 5)
     q = lambda shape: QTensor.quantize(torch.randn(shape, generator=gen, device="cuda") * 0.02, ggml.GGML_TYPE_Q4_K)
@@ -350,9 +407,15 @@ def time_moe(steps, warmup):
                                     ggml.GGML_TYPE_Q4_K, ws.data_ptr(), ws.numel(), st)
         if rc != 0:
             _lib.check("vb_moe_grouped_ffn", rc)
-    ms, _, _ = time_launches([f], steps, warmup)
+    tm = time_launches([f], steps, warmup)
     ab = hit * 3 * i * 2304 + t * h * 4 * 2 + t * e_n * 4
-    return ms, hit, ab
+
+    def expert(e):
+        dec = lambda qt: O.dequantize(qt.to_numpy_bytes(), qt.k, qt.qtype)
+        return dec(gates[e]), dec(ups[e]), dec(downs[e])
+    want, _, _ = O.moe_ffn_grouped(expert, x.cpu().numpy(), logits.cpu().numpy(), topk)
+    err = O.rel_l2(yo.cpu().numpy(), want)
+    return tm, hit, ab, err
 
 
 def time_gguf_ingest(n_tensors=32, reps=3):
@@ -393,30 +456,6 @@ def time_gguf_ingest(n_tensors=32, reps=3):
     return total / best / 1e9, total, path, t_open
 
 
-def gguf_reader_cpu_baseline(path):
-    """The reference's GGUFFile (cpp/src/gguf.cpp) opening the same file:
-    it reads the whole file into RAM (gguf.cpp:199-251), the host half of
-    its ingestion.  None where that reader is not built."""
-    import ctypes
-    lib_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "oracle", "_ref", "libvbref_gguf.so")
-    if not os.path.exists(lib_path):
-        return None
-    lib = ctypes.CDLL(lib_path)
-    lib.ref_gguf_open.restype = ctypes.c_void_p
-    lib.ref_gguf_open.argtypes = [ctypes.c_char_p]
-    lib.ref_gguf_close.argtypes = [ctypes.c_void_p]
-    best = None
-    for _ in range(2):
-        t0 = time.perf_counter()
-        h = lib.ref_gguf_open(path.encode())
-        dt = time.perf_counter() - t0
-        if not h:
-            return None
-        lib.ref_gguf_close(h)
-        best = dt if best is None else min(best, dt)
-    return os.path.getsize(path) / best / 1e9
-
-
 def check_parity(qtype, n, k, copies, x, ys):
     """Oracle check of the first copy's output (the timed results)."""
     import oracle as O
@@ -425,45 +464,133 @@ def check_parity(qtype, n, k, copies, x, ys):
     return O.rel_l2(y, want)
 
 
-def cpu_baseline(qtype, n, k, seconds):
-    """Reference gemv_dequant (its own orientation: K rows of N) on the same
-    bytes count, single thread, 10 % trimmed mean (vibeblade/benchmark.py:61-79)."""
-    import oracle as O
-    rng = np.random.default_rng(SEED)
-    # the reference walks W as k rows of n elements: same bytes, transposed roles
-    w = (rng.standard_normal((k, n)) * 0.02).astype(np.float32)
-    wq = O.quantize(w, qtype)
-    del w
-    x = rng.standard_normal(k).astype(np.float32)
-    scratch = np.empty(n, np.float32)
-    kind = "reference" if O.ref_available() else "port"
-    fn = O.ref_gemv_dequant if kind == "reference" else O.gemv_kn
-    fn(x, wq, k, n, qtype, scratch)  # warmup
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
+def _trimmed_mean(fn, seconds, min_calls=3):
+    """Warmup call, then calls for about `seconds`; 10 % trimmed mean
+    (vibeblade/benchmark.py:61-79).  Returns (seconds per call, calls)."""
+    fn()
     times = []
     t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 3:
+    while time.perf_counter() < t_end or len(times) < min_calls:
         t0 = time.perf_counter()
-        fn(x, wq, k, n, qtype, scratch)
+        fn()
         times.append(time.perf_counter() - t0)
     ts = np.sort(np.array(times))
     trim = int(len(ts) * 0.1)
     ts = ts[trim:len(ts) - trim] if len(ts) > 2 * trim + 1 else ts
-    sec = float(ts.mean())
+    return float(ts.mean()), len(times)
+
+
+def _quantized_kn(qtype, K, N, rng, chunk_rows=256):
+    """GGUF bytes of a K x N matrix (the reference's orientation: K rows of N)
+    of N(0, 0.02) weights, quantized by the oracle in row chunks."""
+    import oracle as O
+    parts = []
+    for r0 in range(0, K, chunk_rows):
+        w = rng.standard_normal((min(chunk_rows, K - r0), N), dtype=np.float32) * np.float32(0.02)
+        parts.append(O.quantize(w, qtype))
+    return np.ascontiguousarray(np.concatenate(parts, axis=0))
+
+
+def cpu_gemv_sample(qtype, K, N, seconds, rng=None):
+    """The oracle's restatement of the reference loop (gemv_dequant,
+    cpp/src/dequant.cpp:739-780) on one K x N matrix: seconds per call."""
+    import oracle as O
+    rng = np.random.default_rng(SEED) if rng is None else rng
+    wq = _quantized_kn(qtype, K, N, rng)
+    x = rng.standard_normal(K).astype(np.float32)
+    scratch = np.empty(N, np.float32)
+    sec, calls = _trimmed_mean(lambda: O.gemv_kn(x, wq, K, N, qtype, scratch), seconds)
+    return sec, calls
+
+
+def cpu_baseline(qtype, n, k, seconds):
+    """The oracle's C restatement of the reference gemv_dequant (its own
+    orientation: k rows of n) on the same bytes, one thread, 10 % trimmed mean."""
+    import oracle as O
+    sec, calls = cpu_gemv_sample(qtype, k, n, seconds)
     return {
         "value": round(alg_bytes_gemv(qtype, n, k) / sec / 1e9, 3),
         "unit": "GB/s",
         "cores": 1,
-        "kind": kind,
-        "sample": (f"{len(times)} calls of gemv_dequant Q4_K (K={k} rows x N={n}), "
-                   f"{O.simd_variant()} build, 10% trimmed mean {sec * 1e3:.2f} ms/call; "
-                   f"host nproc={os.cpu_count()}"),
+        "kind": "port",
+        "sample": (f"{calls} calls of the oracle's restatement of gemv_dequant (cpp/src/dequant.cpp:739-780) "
+                   f"on Q4_K K={k} rows x N={n}, {O.simd_variant()} build (-O3), 10% trimmed mean "
+                   f"{sec * 1e3:.2f} ms/call; host {cpu_model()}, nproc={os.cpu_count()}"),
     }
+
+
+def cpu_table(seconds):
+    """One-core CPU time per call for every configuration: the oracle's
+    restatements of the reference's CPU paths.  GEMV shapes: the gemv_dequant
+    loop; batched M: the reference's per-token loop of it
+    (cpp/src/fast_model.cpp:644-669), timed on a sample of tokens and scaled;
+    TurboSparse and MoE: the reference's numpy steps over fp32 weights
+    (vibeblade/sparse.py:199-283, vibeblade/moe_executor.py:331-344) with
+    BLAS held to one thread.  Yields one dict per configuration."""
+    from vibeblade_amd import ggml
+    from threadpoolctl import threadpool_limits
+    rng = np.random.default_rng(SEED + 11)
+    per = max(1.0, seconds)
+    for name, qt, n, k in (("1: Q8_0 GEMV 4096x4096", ggml.GGML_TYPE_Q8_0, 4096, 4096),
+                           ("2: Q4_K GEMV 14336x4096 (gate/up)", ggml.GGML_TYPE_Q4_K, 14336, 4096),
+                           ("2: Q4_K GEMV 4096x14336 (down)", ggml.GGML_TYPE_Q4_K, 4096, 14336),
+                           ("2: Q6_K GEMV 128256x4096 (lm_head)", ggml.GGML_TYPE_Q6_K, 128256, 4096)):
+        sec, calls = cpu_gemv_sample(qt, k, n, per, rng)
+        yield {"config": name, "cpu_us_per_call": round(sec * 1e6, 1), "calls": calls,
+               "GB/s": round(alg_bytes_gemv(qt, n, k) / sec / 1e9, 3)}
+    sec1, calls = cpu_gemv_sample(ggml.GGML_TYPE_Q4_K, 4096, 14336, per, rng)
+    for m in (8, 512):
+        yield {"config": f"3: Q4_K GEMM M={m} 14336x4096", "cpu_us_per_call": round(m * sec1 * 1e6, 1),
+               "sample": f"per-token loop: {m} x the gate/up GEMV time ({calls} calls timed)"}
+    h, i = 4096, 14336
+    with threadpool_limits(limits=1):
+        w002 = np.float32(0.02)
+        gate = rng.standard_normal((i, h), dtype=np.float32) * w002
+        up = rng.standard_normal((i, h), dtype=np.float32) * w002
+        down = rng.standard_normal((h, i), dtype=np.float32) * w002
+        x = rng.standard_normal((1, h), dtype=np.float32)
+        kk = max(1, int(i * 0.1))
+
+        def sparse_step():
+            g = x @ gate.T
+            top = np.argpartition(g[0], -kk)[-kk:]
+            act = np.sort(top)
+            ua = x @ up[act].T
+            ga = g[:, act]
+            hid = ga * (1.0 / (1.0 + np.exp(-ga))) * ua
+            return hid @ down.T[act]
+        sec, calls = _trimmed_mean(sparse_step, per)
+        yield {"config": "4: TurboSparse FFN H=4096 I=14336 (10% active)", "cpu_us_per_call": round(sec * 1e6, 1),
+               "calls": calls, "sample": "reference sparse_ffn_silu steps in numpy fp32 (dense gate, top-k, "
+                                         "gathered up and down), 1 BLAS thread"}
+        xe = rng.standard_normal((4, h), dtype=np.float32)
+        gt, ut, dt = gate.T, up.T, down.T  # moe convention: no transpose copies
+
+        def expert_step():
+            go = xe @ gt
+            return (go * (1.0 / (1.0 + np.exp(-go))) * (xe @ ut)) @ dt
+        sec, calls = _trimmed_mean(expert_step, per)
+        yield {"config": "5: MoE 8 experts, 16 tokens top-2", "cpu_us_per_call": round(8 * sec * 1e6, 1),
+               "calls": calls, "sample": "8 x one expert's _compute_single_expert_cpu on its 4 tokens "
+                                         "(16 x 2 / 8), numpy fp32, 1 BLAS thread"}
+        del gate, up, down
 
 
 def pmc_pass(workload="gemv"):
     """Launches for counter collection: no graph (per-dispatch counters), no
     timing.  The GEMVs rotate over 16 weight copies as in the timed run; the
-    GEMMs (fp16 X with 0.1% outliers x20, as timed) over 4."""
+    GEMMs (fp16 X with 0.1% outliers x20, as timed) likewise."""
     import torch
     from vibeblade_amd import _lib, ggml
     _lib.init(0)
@@ -482,13 +609,11 @@ def pmc_pass(workload="gemv"):
     else:
         m = 8 if workload == "gemm8" else 512
         gen = torch.Generator(device="cuda").manual_seed(SEED + m)
-        copies = make_copies(qtype, n, k, 4, gen)
-        x = torch.randn((m, k), generator=gen, device="cuda")
-        x[torch.rand((m, k), generator=gen, device="cuda") < 0.001] *= 20.0
-        xh = x.half().contiguous()
+        copies = make_copies(qtype, n, k, NCOPIES, gen)
+        xh = gemm_inputs(m, k, gen)
         y = torch.empty((m, n), dtype=torch.float32, device="cuda")
         for i in range(16):
-            c = copies[i % 4]
+            c = copies[i % NCOPIES]
             _lib.check("vb_gemm", lib.vb_gemm(c.ptr(), xh.data_ptr(), 1, y.data_ptr(), m, n, k, qtype, 0, st))
         what = f"16 GEMM dispatches at M={m}"
     torch.cuda.synchronize()
@@ -590,6 +715,91 @@ def load_traffic():
         return None
 
 
+def emit(d):
+    print(json.dumps(d), file=sys.stderr, flush=True)
+
+
+def run_extra(which, args):
+    """The other configurations, one JSON line each on stderr."""
+    import torch
+    from vibeblade_amd import ggml
+
+    def frac(b, tm):
+        gbs = b / (tm.ms * 1e-3) / 1e9
+        return round(gbs, 1), round(gbs / HBM_PEAK_GBS, 4)
+
+    if "gemv" in which:
+        for name, t, nn, kk in (("1: Q8_0 GEMV 4096x4096", ggml.GGML_TYPE_Q8_0, 4096, 4096),
+                                ("2: Q4_K GEMV 4096x14336 (down)", ggml.GGML_TYPE_Q4_K, 4096, 14336),
+                                ("2: Q6_K GEMV 128256x4096 (lm_head)", ggml.GGML_TYPE_Q6_K, 128256, 4096)):
+            tm, cps, xx, yy = time_gemv(t, nn, kk, 20, 3)
+            e2 = check_parity(t, nn, kk, cps, xx, yy)
+            b2 = alg_bytes_gemv(t, nn, kk)
+            gbs, fr = frac(b2, tm)
+            emit({"workload": name, "us_per_call": tm.us(), "mean_us": round(tm.mean_ms * 1e3, 3),
+                  "launches": tm.launches, "weight_copies": len(cps), "GB/s": gbs, "frac_hbm": fr, "rel_l2": e2})
+            del cps, yy
+            torch.cuda.empty_cache()
+    if "sparse" in which:
+        for layout, block in ((1, False), (0, False), (1, True), (0, True)):
+            tm, n_s, b4, err = time_sparse(layout, 20, 3, block=block)
+            what = "block (RMSNorm + FFN + residual)" if block else "FFN"
+            gbs, fr = frac(b4, tm)
+            emit({"workload": f"4: TurboSparse {what} H=4096 I=14336 mean |S|={n_s:.0f} down_layout={layout}",
+                  "us_per_call": tm.us(), "launches": tm.launches, "weight_sets": SPARSE_COPIES,
+                  "alg_bytes": round(b4), "GB/s": gbs, "frac_hbm": fr, "rel_l2": err})
+            torch.cuda.empty_cache()
+    if "moe" in which:
+        tm, hit, b5, err = time_moe(200, 5)
+        gbs, fr = frac(b5, tm)
+        emit({"workload": f"5: MoE 8x Q4_K experts, 16 tokens top-2 ({hit} experts hit)",
+              "us_per_call": tm.us(), "launches": tm.launches, "alg_bytes": b5, "GB/s": gbs, "frac_hbm": fr,
+              "rel_l2": err, "dtype": "x and the hidden rows rounded to fp16, fp16 MFMA, fp32 accumulate"})
+        torch.cuda.empty_cache()
+    if "predict" in which:
+        for only in (True, False):
+            tm, n_s8 = time_sparse_predicted(20 if not only else 200, 3, predict_only=only)
+            what = ("EMA predict + compaction alone (I=14336, k=1433)" if only else
+                    "TurboSparse token step on the device: EMA predict + sparse block over the device count "
+                    "+ EMA update, H=4096 I=14336")
+            emit({"workload": what, "us_per_call": tm.us(), "launches": tm.launches, "active": n_s8})
+            torch.cuda.empty_cache()
+    if "ffn" in which:
+        for dt_name, dt in (("Q4_K", ggml.GGML_TYPE_Q4_K), ("Q6_K", ggml.GGML_TYPE_Q6_K)):
+            for fused in (True, False):
+                tm, b7 = time_ffn_block(dt, fused, 40, 3)
+                gbs, fr = frac(b7, tm)
+                emit({"workload": f"FFN block hd=4096 inter=14336 Q4_K gate/up, {dt_name} down, RMSNorm+SiLU+"
+                                  f"residual, {'fused (2 launches)' if fused else 'unfused (7 launches)'}",
+                      "us_per_call": tm.us(), "launches": tm.launches, "alg_bytes": b7, "GB/s": gbs, "frac_hbm": fr})
+                torch.cuda.empty_cache()
+    if "gguf" in which:
+        gbs6, b6, gpath, t_open = time_gguf_ingest()
+        os.remove(gpath)
+        emit({"workload": "GGUF ingestion: open + upload 32 Q4_K 14336x4096 tensors (page cache)",
+              "bytes": b6, "GB/s": round(gbs6, 2), "open_ms": round(t_open * 1e3, 3)})
+    ms_list = []
+    if "gemm" in which:
+        ms_list += [8, 512]
+    if "msweep" in which:
+        ms_list += [m for m in (1, 4, 16, 17, 32, 64, 100, 128, 256, 1024) if m not in ms_list]
+    for m in ms_list:
+        tm, e3 = time_gemm(m, 14336, 4096, 20, 2)
+        flops = 2.0 * m * 14336 * 4096
+        b3 = 14336 * 2304 + 2 * m * 4096 + 4 * m * 14336
+        tfs = flops / (tm.ms * 1e-3) / 1e12
+        gbs, fr = frac(b3, tm)
+        emit({"workload": f"3: Q4_K GEMM M={m} N=14336 K=4096 fp16 X", "us_per_call": tm.us(),
+              "launches": tm.launches, "TFLOP/s": round(tfs, 2), "frac_mfma_fp16": round(tfs / MFMA_FP16_PEAK_TFS, 4),
+              "GB/s": gbs, "frac_hbm": fr, "rel_l2": e3})
+        torch.cuda.empty_cache()
+    if "cpu" in which and not args.no_cpu_baseline:
+        for row in cpu_table(min(args.cpu_seconds, 3.0)):
+            row["cores"] = 1
+            row["host"] = cpu_model()
+            emit(row)
+
+
 def main():
     args = parse()
     if args.summarize_pmc:
@@ -614,12 +824,12 @@ def main():
 
     qtype, n, k = ggml.GGML_TYPE_Q4_K, 14336, 4096
     print(f"[bench] Q4_K GEMV {n}x{k}: building {NCOPIES} weight copies", file=sys.stderr, flush=True)
-    ms, graph_used, nsteps, copies, x, ys = time_gemv(qtype, n, k, args.steps, args.warmup)
+    tm, copies, x, ys = time_gemv(qtype, n, k, args.steps, args.warmup, NCOPIES)
     err = check_parity(qtype, n, k, copies, x, ys)
     ab = alg_bytes_gemv(qtype, n, k)
-    gbs = ab / (ms * 1e-3) / 1e9
-    print(f"[bench] {ms * 1e3:.2f} us/step, {gbs:.0f} GB/s, rel-L2 vs oracle {err:.2e}",
-          file=sys.stderr, flush=True)
+    gbs = ab / (tm.ms * 1e-3) / 1e9
+    print(f"[bench] {tm.us():.2f} us per launch (median over {tm.steps} steps of {tm.per_step}; mean "
+          f"{tm.mean_ms * 1e3:.2f}), {gbs:.0f} GB/s, rel-L2 vs oracle {err:.2e}", file=sys.stderr, flush=True)
     if err > 1e-3:
         print("[bench] PARITY FAILURE", file=sys.stderr)
         sys.exit(3)
@@ -627,81 +837,16 @@ def main():
     torch.cuda.empty_cache()
 
     if args.extra:
-        extra_shapes = [
-            ("Q8_0 GEMV 4096x4096", ggml.GGML_TYPE_Q8_0, 4096, 4096),
-            ("Q4_K GEMV 4096x14336 (down)", ggml.GGML_TYPE_Q4_K, 4096, 14336),
-            ("Q6_K GEMV 128256x4096 (lm_head)", ggml.GGML_TYPE_Q6_K, 128256, 4096),
-        ]
-        for name, t, nn, kk in extra_shapes:
-            ncop = 2 if nn * kk > 100e6 else NCOPIES
-            ms2, _, _, cps, xx, yy = time_gemv(t, nn, kk, max(200, args.steps // 4), 50, ncop)
-            e2 = check_parity(t, nn, kk, cps, xx, yy)
-            b2 = alg_bytes_gemv(t, nn, kk)
-            print(json.dumps({"workload": name, "us_per_call": round(ms2 * 1e3, 3),
-                              "GB/s": round(b2 / (ms2 * 1e-3) / 1e9, 1),
-                              "frac_hbm": round(b2 / (ms2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                              "rel_l2": e2}), file=sys.stderr, flush=True)
-            del cps, yy
-            torch.cuda.empty_cache()
-        for layout, block in ((1, False), (0, False), (1, True), (0, True)):
-            ms4, n_s, b4 = time_sparse(layout, 400, 40, block=block)
-            what = "block (RMSNorm + FFN + residual)" if block else "FFN"
-            print(json.dumps({"workload": f"TurboSparse {what} H=4096 I=14336 |S|={n_s} down_layout={layout}",
-                              "us_per_call": round(ms4 * 1e3, 3), "alg_bytes": b4,
-                              "GB/s": round(b4 / (ms4 * 1e-3) / 1e9, 1),
-                              "frac_hbm": round(b4 / (ms4 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}),
-                  file=sys.stderr, flush=True)
-            torch.cuda.empty_cache()
-        ms5, hit, b5 = time_moe(50, 5)
-        print(json.dumps({"workload": f"MoE 8x Q4_K experts, 16 tokens top-2 ({hit} experts hit)",
-                          "us_per_call": round(ms5 * 1e3, 3), "alg_bytes": b5,
-                          "GB/s": round(b5 / (ms5 * 1e-3) / 1e9, 1),
-                          "frac_hbm": round(b5 / (ms5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}),
-              file=sys.stderr, flush=True)
-        torch.cuda.empty_cache()
-        for only in (True, False):
-            ms8, n_s8 = time_sparse_predicted(400, 40, predict_only=only)
-            what = ("EMA predict + compaction alone (I=14336, k=1433)" if only else
-                    "TurboSparse token step on the device: EMA predict + sparse block over the device count "
-                    "+ EMA update, H=4096 I=14336")
-            print(json.dumps({"workload": what, "us_per_call": round(ms8 * 1e3, 3), "active": n_s8}),
-                  file=sys.stderr, flush=True)
-            torch.cuda.empty_cache()
-        for dt_name, dt in (("Q4_K", ggml.GGML_TYPE_Q4_K), ("Q6_K", ggml.GGML_TYPE_Q6_K)):
-            for fused in (True, False):
-                ms7, b7 = time_ffn_block(dt, fused, 400, 40)
-                print(json.dumps({"workload": f"FFN block hd=4096 inter=14336 Q4_K gate/up, {dt_name} down, "
-                                              f"RMSNorm+SiLU+residual, {'fused (2 launches)' if fused else 'unfused (7 launches)'}",
-                                  "us_per_call": round(ms7 * 1e3, 3), "alg_bytes": b7,
-                                  "GB/s": round(b7 / (ms7 * 1e-3) / 1e9, 1),
-                                  "frac_hbm": round(b7 / (ms7 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}),
-                      file=sys.stderr, flush=True)
-                torch.cuda.empty_cache()
-        gbs6, b6, gpath, t_open = time_gguf_ingest()
-        ref_gbs = gguf_reader_cpu_baseline(gpath) if not args.no_cpu_baseline else None
-        os.remove(gpath)
-        print(json.dumps({"workload": "GGUF ingestion: open + upload 32 Q4_K 14336x4096 tensors (page cache)",
-                          "bytes": b6, "GB/s": round(gbs6, 2), "open_ms": round(t_open * 1e3, 3),
-                          "cpu_baseline": None if ref_gbs is None else
-                          {"value": round(ref_gbs, 2), "unit": "GB/s", "cores": 1, "kind": "reference",
-                           "sample": "reference GGUFFile opening the same file (reads it into RAM)"}}),
-              file=sys.stderr, flush=True)
-        for m, ncop in ((8, NCOPIES), (512, 4)):
-            ms3, e3 = time_gemm(m, 14336, 4096, 400 if m == 8 else 100, 40, ncop)
-            flops = 2.0 * m * 14336 * 4096
-            b3 = 14336 * 2304 + 2 * m * 4096 + 4 * m * 14336
-            print(json.dumps({"workload": f"Q4_K GEMM M={m} N=14336 K=4096 fp16 X",
-                              "us_per_call": round(ms3 * 1e3, 3),
-                              "TFLOP/s": round(flops / (ms3 * 1e-3) / 1e12, 2),
-                              "frac_mfma_fp16": round(flops / (ms3 * 1e-3) / 1e12 / MFMA_FP16_PEAK_TFS, 4),
-                              "GB/s": round(b3 / (ms3 * 1e-3) / 1e9, 1),
-                              "frac_hbm": round(b3 / (ms3 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                              "rel_l2": e3}), file=sys.stderr, flush=True)
-            torch.cuda.empty_cache()
+        which = {w.strip() for w in args.extra.split(",") if w.strip()}
+        bad = which - set(EXTRA_ALL)
+        if bad:
+            print(f"unknown --extra workloads: {sorted(bad)}", file=sys.stderr)
+            sys.exit(2)
+        run_extra(which, args)
 
     cpu = None
     if not args.no_cpu_baseline:
-        print("[bench] CPU baseline (reference gemv_dequant, 1 thread)", file=sys.stderr, flush=True)
+        print("[bench] CPU baseline (oracle restatement of gemv_dequant, 1 thread)", file=sys.stderr, flush=True)
         cpu = cpu_baseline(qtype, n, k, args.cpu_seconds)
 
     line = {
@@ -709,20 +854,24 @@ def main():
         "value": round(gbs, 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": nsteps,
+        "steps": tm.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 6),
+        "ms_per_step": round(tm.step_ms, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "i8 dot (v_dot4_i32_i8) -> i32, f32 scales",
-        "data": "synthetic: W ~ N(0,0.02) quantized to GGUF Q4_K on device (16 rotating copies), x ~ N(0,1)",
+        "dtype": DTYPE_GEMV,
+        "data": f"synthetic: W ~ N(0,0.02) quantized to GGUF Q4_K on device ({NCOPIES} rotating copies, "
+                f"{NCOPIES * n * 2304 / 1e6:.0f} MB), x ~ N(0,1)",
         "config": {"workload": "Q4_K GEMV M=1, N=14336 rows x K=4096 (Llama-3-8B FFN gate/up)",
-                   "n": n, "k": k, "m": 1, "weight_copies": NCOPIES, "hip_graph": graph_used,
+                   "n": n, "k": k, "m": 1, "weight_copies": NCOPIES, "hip_graph": tm.graph,
+                   "step": f"one pass over the {NCOPIES} weight copies ({tm.per_step} GEMV launches)",
+                   "launches_timed": tm.launches, "us_per_launch_median": tm.us(),
+                   "us_per_launch_mean": round(tm.mean_ms * 1e3, 3),
                    "rel_l2_vs_oracle": float(f"{err:.3e}")},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
-                     "alg_bytes_per_launch": ab, "us_per_launch": round(ms * 1e3, 3)},
+                     "alg_bytes_per_launch": ab, "us_per_launch": tm.us()},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

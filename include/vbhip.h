@@ -10,8 +10,12 @@
  * workspace, so calls on different streams or threads are independent.
  *
  * Weights are GGUF tensors in the on-disk layout: n rows of k elements, each
- * row a sequence of blocks along k (rows = outputs).  Supported ggml types:
- * F32 (0), F16 (1), Q8_0 (8), Q4_K (12), Q6_K (14).
+ * row a sequence of blocks along k (rows = outputs).  Supported ggml types
+ * (decode, GEMV, FFN block, sparse FFN with GGUF-layout down): F32 (0),
+ * F16 (1), Q4_0 (2), Q4_1 (3), Q5_0 (6), Q5_1 (7), Q8_0 (8), Q2_K (10),
+ * Q3_K (11), Q4_K (12), Q5_K (13), Q6_K (14), BF16 (30).  Each op's comment
+ * lists the subset it takes where that is narrower (vb_gemm, the fused
+ * neuron-major sparse FFN, vb_moe_grouped_ffn, vb_quantize_rows).
  */
 #ifndef VBHIP_H
 #define VBHIP_H
@@ -36,9 +40,17 @@ enum {
 enum {
     VB_TYPE_F32 = 0,
     VB_TYPE_F16 = 1,
+    VB_TYPE_Q4_0 = 2,
+    VB_TYPE_Q4_1 = 3,
+    VB_TYPE_Q5_0 = 6,
+    VB_TYPE_Q5_1 = 7,
     VB_TYPE_Q8_0 = 8,
+    VB_TYPE_Q2_K = 10,
+    VB_TYPE_Q3_K = 11,
     VB_TYPE_Q4_K = 12,
+    VB_TYPE_Q5_K = 13,
     VB_TYPE_Q6_K = 14,
+    VB_TYPE_BF16 = 30,
 };
 
 /* ---- runtime ------------------------------------------------------------
@@ -54,8 +66,16 @@ int vb_version(void);
  * blocks or the type is unknown.  Same table as ggml_blck_size /
  * ggml_type_size / tensor_nbytes (cpp/include/ggml_types.h:30-71, :195-199). */
 int64_t vb_row_bytes(int32_t ggml_type, int64_t k);
-/* Select the device and check that it is a gfx950. */
+/* Select the device and check that it is a gfx950; also reads the launch
+ * tuning overrides (VB_GEMV_RING, VB_GEMV_CFG, VB_GEMV_Q4K_PATH,
+ * VB_GEMV_MFMA_CFG, VB_GEMM_NF, VB_SPARSE_FUSED, VB_SPARSE_NPW) from the
+ * environment, once per process, and the device's compute-unit count. */
 int vb_init(int device);
+/* Re-read the tuning overrides from the environment (for tuning sweeps and
+ * tests).  Not synchronised with op calls running on other threads: their
+ * launches use either the old or the new settings.  No counterpart in the
+ * reference, which has no launch tuning. */
+int vb_tuning_reload(void);
 int vb_malloc(void** ptr, size_t bytes);
 int vb_free(void* ptr);
 int vb_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);

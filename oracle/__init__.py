@@ -373,6 +373,29 @@ def moe_ffn(gates, ups, downs, x: np.ndarray, logits: np.ndarray, topk: int):
     return y, idx, w
 
 
+def moe_ffn_grouped(experts, x: np.ndarray, logits: np.ndarray, topk: int):
+    """moe_ffn with tokens grouped per expert: ``experts(e)`` returns expert e's
+    decoded (gate (I, H), up (I, H), down (H, I)) and is called once per hit
+    expert, so large experts are decoded one at a time.  Same fp64 sums as
+    moe_ffn (each token's slots added in slot order).  Returns (Y, idx, w)."""
+    x = np.asarray(x, dtype=np.float64)
+    idx, w = route_top_k(logits, topk)
+    parts = {}
+    for e in sorted(set(idx.ravel().tolist())):
+        g, u, d = experts(e)
+        rows = [(t, s) for t in range(x.shape[0]) for s in range(topk) if idx[t, s] == e]
+        xe = x[[t for t, _ in rows]]
+        he = silu64(xe @ g.astype(np.float64).T) * (xe @ u.astype(np.float64).T)
+        ye = he @ d.astype(np.float64).T
+        for r, (t, s) in enumerate(rows):
+            parts[(t, s)] = ye[r]
+    y = np.zeros((x.shape[0], parts[(0, 0)].shape[0]), dtype=np.float64)
+    for t in range(x.shape[0]):
+        for s in range(topk):
+            y[t] += w[t, s] * parts[(t, s)]
+    return y, idx, w
+
+
 def rel_l2(a: np.ndarray, b: np.ndarray) -> float:
     a = np.asarray(a, dtype=np.float64)
     b = np.asarray(b, dtype=np.float64)

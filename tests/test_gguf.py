@@ -344,3 +344,22 @@ def test_against_reference_parser(sample):
                     assert list(out[:n]) == v[1] == f.meta_float_array(k)
     finally:
         lib.ref_gguf_close(h)
+
+
+def test_tensor_data_outlives_close(sample):
+    """A tensor_data view keeps the mapping alive after close() and after the
+    GGUFFile is dropped (it used to dangle and crash on access)."""
+    import gc
+    path, tensors, _, _ = sample
+    name, _, _, data = tensors[0]
+    f = GGUFFile(path)
+    view = f.tensor_data(name)
+    f.close()
+    assert view.tobytes() == data
+    with pytest.raises(ValueError):
+        f.load_qtensor(name)
+    view2 = GGUFFile(path).tensor_data(tensors[2][0])
+    gc.collect()
+    assert view2[-1] == tensors[2][3][-1] and view2.tobytes() == tensors[2][3]
+    del view, view2, f
+    gc.collect()

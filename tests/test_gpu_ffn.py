@@ -68,9 +68,9 @@ def test_sparse_small_all_types(qtype):
         assert O.rel_l2(y, want) <= 1e-3
 
 
-def test_sparse_gathered_rows_on_mfma_path(monkeypatch):
+def test_sparse_gathered_rows_on_mfma_path(knob):
     """Gathered gate/up row pairs through the int8-MFMA GEMV kernel."""
-    monkeypatch.setenv("VB_GEMV_Q4K_PATH", "mfma")
+    knob("VB_GEMV_Q4K_PATH", "mfma")
     h, i = 1024, 768
     gq, uq, dq, gd, ud, dd = ffn_weights(h, i, Q4K, 9, DOWN_GGUF)
     rng = np.random.default_rng(9)
@@ -116,12 +116,12 @@ def test_sparse_layouts_agree():
 
 @pytest.mark.parametrize("h,i,fused_env,one", [(4096, 4096, "0", False), (8192, 2048, None, False),
                                                (4096, 512, None, True)])
-def test_sparse_neuron_major_paths(monkeypatch, h, i, fused_env, one):
+def test_sparse_neuron_major_paths(knob, h, i, fused_env, one):
     """Layout 1 on each of its paths: the fused gate/up/down kernel (h <= 4096),
     the gathered GEMV + down-rows launches (forced with VB_SPARSE_FUSED=0, and
     for h > 4096), and a single active neuron on the fused path."""
     if fused_env is not None:
-        monkeypatch.setenv("VB_SPARSE_FUSED", fused_env)
+        knob("VB_SPARSE_FUSED", fused_env)
     gq, uq, dq, gd, ud, dd = ffn_weights(h, i, Q4K, 17, DOWN_NEURON_MAJOR)
     rng = np.random.default_rng(8)
     s = np.array([137], np.int32) if one else np.flatnonzero(rng.random(i) < 0.1).astype(np.int32)
@@ -366,9 +366,9 @@ def test_sparse_block_config_shape(layout, act):
 
 @pytest.mark.parametrize("fused_env", [None, "0"])
 @pytest.mark.parametrize("norm,residual,inplace", [(True, False, False), (False, True, True), (True, True, True)])
-def test_sparse_block_options_neuron_major(monkeypatch, fused_env, norm, residual, inplace):
+def test_sparse_block_options_neuron_major(knob, fused_env, norm, residual, inplace):
     if fused_env is not None:
-        monkeypatch.setenv("VB_SPARSE_FUSED", fused_env)
+        knob("VB_SPARSE_FUSED", fused_env)
     sparse_block_case(2048, 4096, Q4K, DOWN_NEURON_MAJOR, ACT_SILU, norm, residual, seed=51, inplace=inplace)
 
 

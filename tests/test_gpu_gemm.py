@@ -66,9 +66,9 @@ def test_tiled(dtype, m, n, k):
 
 
 @pytest.mark.parametrize("nf", ["6", "8"])
-def test_tiled_column_tiles(monkeypatch, nf):
+def test_tiled_column_tiles(knob, nf):
     """Both workgroup widths (96 and 128 columns), ragged M and N edges."""
-    monkeypatch.setenv("VB_GEMM_NF", nf)
+    knob("VB_GEMM_NF", nf)
     qt, x = make(300, 333, 1280, 21)
     for dtype in (torch.float16, torch.float32):
         xt = torch.from_numpy(x).to("cuda", dtype)

@@ -108,3 +108,25 @@ def test_upload_larger_than_staging(tmp_path):
         assert np.array_equal(ws.to_numpy_bytes().ravel(), small)
         got = wb.data.cpu().numpy()
         assert got.size == big.size and np.array_equal(got.ravel(), big)
+
+
+def test_upload_split_copy_tail(tmp_path):
+    """Chunks of at least 4 MiB are copied by several host threads; a chunk
+    whose size is 1-3 bytes past a multiple of 16 KiB once lost its last
+    bytes to a rounded-down share.  1-D F16 tensors of 4 MiB + 2 and
+    12 MiB + 2 bytes (an 8 MiB chunk, then the ragged one) and of
+    4 MiB + 16 KiB + 2 bytes come back byte for byte."""
+    rng = np.random.default_rng(40)
+    tensors, blobs = [], {}
+    for name, nbytes in (("a", (4 << 20) + 2), ("b", (12 << 20) + 2), ("c", (4 << 20) + (16 << 10) + 2)):
+        blob = rng.integers(0, 256, nbytes, dtype=np.uint8)
+        blobs[name] = blob
+        tensors.append((name, (nbytes // 2,), ggml.GGML_TYPE_F16, blob.tobytes()))
+    path = tmp_path / "tail.gguf"
+    write_gguf(path, [], tensors)
+    with GGUFFile(path) as f:
+        for name, blob in blobs.items():
+            qt = f.load_qtensor(name, "cuda:0")
+            torch.cuda.synchronize()
+            got = qt.data.cpu().numpy().ravel()
+            assert got.size == blob.size and np.array_equal(got, blob), name

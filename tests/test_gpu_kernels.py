@@ -93,9 +93,9 @@ def test_gemv_small_vs_oracle(qtype, rows, k):
 
 
 @pytest.fixture
-def q4k_mfma_path(monkeypatch):
+def q4k_mfma_path(knob):
     """Route Q4_K GEMVs through the int8-MFMA kernel (VB_GEMV_Q4K_PATH=mfma)."""
-    monkeypatch.setenv("VB_GEMV_Q4K_PATH", "mfma")
+    knob("VB_GEMV_Q4K_PATH", "mfma")
 
 
 @pytest.mark.parametrize("rows,k", [(1, 256), (13, 512), (70, 4096), (37, 14336), (9, 28672), (300, 1280)])
@@ -110,10 +110,10 @@ def test_gemv_q4k_mfma_path_vs_oracle(q4k_mfma_path, rows, k):
 
 
 @pytest.mark.parametrize("cfg", ["2,1", "4,4", "8,8", "16,16", "8,2", "6,3"])
-def test_gemv_q4k_mfma_launch_shapes(q4k_mfma_path, monkeypatch, cfg):
+def test_gemv_q4k_mfma_launch_shapes(q4k_mfma_path, knob, cfg):
     """Every k-slice / workgroup split gives the same rows (k = 4096: 16
     super-blocks; "6,3" leaves a ragged last slice)."""
-    monkeypatch.setenv("VB_GEMV_MFMA_CFG", cfg)
+    knob("VB_GEMV_MFMA_CFG", cfg)
     rows, k = 200, 4096
     qt = QTensor.quantize(rand_weights(rows, k, 11), ggml.GGML_TYPE_Q4_K)
     x = np.random.default_rng(12).standard_normal(k).astype(np.float32)
@@ -124,13 +124,13 @@ def test_gemv_q4k_mfma_launch_shapes(q4k_mfma_path, monkeypatch, cfg):
 
 @pytest.mark.parametrize("cfg", ["8,1", "8,3", "16,2", "4,9", "8,7"])
 @pytest.mark.parametrize("ring", ["", "1", "2", "3", "4"])
-def test_gemv_dot_launch_shapes(monkeypatch, cfg, ring):
+def test_gemv_dot_launch_shapes(knob, cfg, ring):
     """v_dot4 kernel launch overrides: rows per wave x ring depth (1-4; rows
     not a multiple of the depth take padding steps), one k-slice (k = 4096)
     and four (k = 14336)."""
-    monkeypatch.setenv("VB_GEMV_CFG", cfg)
+    knob("VB_GEMV_CFG", cfg)
     if ring:
-        monkeypatch.setenv("VB_GEMV_RING", ring)
+        knob("VB_GEMV_RING", ring)
     for qtype in QTYPES:
         for rows, k in ((333, 4096), (70, 14336)):
             qt = QTensor.quantize(rand_weights(rows, k, 13), qtype)

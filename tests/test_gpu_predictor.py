@@ -117,12 +117,12 @@ def _weights(h, i, layout, seed):
                                                   (4096, 14336, DOWN_GGUF, None),
                                                   (2048, 4096, DOWN_NEURON_MAJOR, "0"),
                                                   (8192, 2048, DOWN_NEURON_MAJOR, None)])
-def test_sparse_block_with_device_count(monkeypatch, h, i, layout, fused_env):
+def test_sparse_block_with_device_count(knob, h, i, layout, fused_env):
     """The predicted set through its device count gives the same bits as the
     same set passed from the host (every path: fused neuron-major, GGUF down,
     gathered neuron-major)."""
     if fused_env is not None:
-        monkeypatch.setenv("VB_SPARSE_FUSED", fused_env)
+        knob("VB_SPARSE_FUSED", fused_env)
     gq, uq, dq = _weights(h, i, layout, 11)
     rng = np.random.default_rng(12)
     x = torch.from_numpy(rng.standard_normal(h).astype(np.float32)).cuda()

@@ -332,6 +332,16 @@ def test_moe_invariants():
                             [downs[p] for p in perm], x, logits[:, perm], 2)
     assert np.allclose(y3, y, rtol=1e-12)
     assert np.array_equal(perm[idx3], idx)
+    # grouped per expert (the bench's form for full-size experts) = per-token loop
+    calls = []
+
+    def expert(e):
+        calls.append(e)
+        return gates[e], ups[e], downs[e]
+    yg, idxg, wg = O.moe_ffn_grouped(expert, x, logits, 2)
+    assert np.array_equal(idxg, idx) and np.array_equal(wg, w)
+    assert np.allclose(yg, y, rtol=1e-12, atol=1e-14)
+    assert sorted(calls) == sorted(set(idx.ravel().tolist())) and len(calls) == len(set(calls))
 
 
 def test_rms_norm_closed_forms():

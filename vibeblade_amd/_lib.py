@@ -26,6 +26,7 @@ SIGNATURES = {
     "vb_version": (ctypes.c_int, []),
     "vb_row_bytes": (_i64, [_i32, _i64]),
     "vb_init": (ctypes.c_int, [ctypes.c_int]),
+    "vb_tuning_reload": (ctypes.c_int, []),
     "vb_malloc": (ctypes.c_int, [ctypes.POINTER(_vp), _sz]),
     "vb_free": (ctypes.c_int, [_vp]),
     "vb_memcpy_h2d": (ctypes.c_int, [_vp, _vp, _sz, _vp]),

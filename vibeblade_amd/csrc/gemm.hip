@@ -259,11 +259,8 @@ __global__ void __launch_bounds__(256 * WN) gemm_q4k_tiled(const uint8_t* __rest
 // Columns per workgroup (NF fragments of 16) balancing the grid over the
 // CUs; VB_GEMM_NF overrides (6 or 8).
 int tiled_nf(int64_t M, int64_t N) {
-    if (const char* e = std::getenv("VB_GEMM_NF")) {
-        const int v = std::atoi(e);
-        if (v == 6 || v == 8) return v;
-    }
-    constexpr int kCUs = 256;
+    if (knobs().gemm_nf) return knobs().gemm_nf;
+    const int64_t kCUs = num_cus();
     const int64_t mt = (M + TB_M - 1) / TB_M;
     int best = 8;
     int64_t best_cost = -1;

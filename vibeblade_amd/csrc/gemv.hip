@@ -264,8 +264,6 @@ struct GemvShape {
     size_t lds;
 };
 
-constexpr int kNumCUs = 256;
-
 // Ring depth for rpg rows per wave and wpr k-slices per row (sweeps on
 // MI355X).  A ring of 2 keeps each wave's requests spread over the weight
 // stream: when the last bytes arrive, a wave has one row left to compute,
@@ -300,7 +298,7 @@ int gemv_max_threads_host(int depth) { return depth <= max_d16<TYPE>() ? 1024 : 
 // rows per wave at two workgroups per CU, and beyond that one workgroup per
 // CU again (Q6_K lm_head, 128256 rows: 63 rows per wave).  Multi-slice rows (k > 4096) use
 // 16-wave workgroups.  VB_GEMV_CFG="wpg,rpg" and VB_GEMV_RING=d override
-// (tuning sweeps).
+// (tuning sweeps; Knobs).
 template <int TYPE>
 GemvShape gemv_shape(int64_t n, int units, bool even_rows = false) {
     GemvShape s;
@@ -310,8 +308,9 @@ GemvShape gemv_shape(int64_t n, int units, bool even_rows = false) {
     s.slots = (((s.wpr - 1) * s.upw + 64) + 7) & ~7;
     if (s.wpr == 1) {
         s.wpg = 8;
-        const int64_t per2 = (n + 2 * kNumCUs * 8 - 1) / (2 * kNumCUs * 8);
-        const int64_t per1 = (n + kNumCUs * 8 - 1) / (kNumCUs * 8);
+        const int64_t cus = num_cus();
+        const int64_t per2 = (n + 2 * cus * 8 - 1) / (2 * cus * 8);
+        const int64_t per1 = (n + cus * 8 - 1) / (cus * 8);
         if (per1 >= 3 && per1 <= 8)  // every type (Q4_K first; the others measured since)
             s.rpg = static_cast<int>(per1);
         else
@@ -320,23 +319,20 @@ GemvShape gemv_shape(int64_t n, int units, bool even_rows = false) {
         s.wpg = s.wpr <= 4 ? 16 / s.wpr * s.wpr : s.wpr;
         if (s.wpg > 16) s.wpg = s.wpr;  // > 4096 * 16 elements: one row group per workgroup
         const int groups = s.wpg / s.wpr;
-        s.rpg = static_cast<int>((n + static_cast<int64_t>(kNumCUs) * groups - 1) / (static_cast<int64_t>(kNumCUs) * groups));
+        const int64_t cus = num_cus();
+        s.rpg = static_cast<int>((n + cus * groups - 1) / (cus * groups));
     }
     if (s.rpg < 1) s.rpg = 1;
     const int64_t max_rpg = kMaxRedFloats / (static_cast<int64_t>(s.wpg / s.wpr) * s.wpr);
     if (s.rpg > max_rpg) s.rpg = static_cast<int>(max_rpg);
-    int ring = 0;  // ring-depth override
-    if (const char* rd = std::getenv("VB_GEMV_RING")) {
-        const int d = std::atoi(rd);
-        if (d >= 1 && d <= 4) ring = d;
-    }
+    const int ring = knobs().gemv_ring;  // ring-depth override (0: none)
     auto depth_of = [&](int rpg) { return ring ? ring : ring_depth<TYPE>(rpg, s.wpr); };
     // the block size must fit the launch bounds of the kernel of that depth
     if (64 * s.wpg > gemv_max_threads_host<TYPE>(depth_of(s.rpg))) s.wpg = 8 / s.wpr * s.wpr;
     if (s.wpg < s.wpr) s.wpg = s.wpr;
-    if (const char* cfg = std::getenv("VB_GEMV_CFG")) {
-        int a = 0, b = 0;
-        if (std::sscanf(cfg, "%d,%d", &a, &b) == 2 && a >= 1 && a <= 16 && b >= 1 && a % s.wpr == 0 &&
+    if (knobs().gemv_cfg_wpg > 0) {
+        const int a = knobs().gemv_cfg_wpg, b = knobs().gemv_cfg_rpg;
+        if (a <= 16 && a % s.wpr == 0 &&
             static_cast<int64_t>(a / s.wpr) * b * s.wpr <= kMaxRedFloats &&
             64 * a <= gemv_max_threads_host<TYPE>(depth_of(b))) {
             s.wpg = a;
@@ -466,8 +462,7 @@ int gemv_dispatch_fused(const void* w, const RowSrc& src, const GemvFuse& fz, co
     case TYPE_Q4_K: {
         // v_dot4 kernel by default (fastest measured); VB_GEMV_Q4K_PATH=mfma
         // selects the int8-MFMA kernel (same arithmetic) for plain launches
-        const char* path = std::getenv("VB_GEMV_Q4K_PATH");
-        if (path && std::strcmp(path, "mfma") == 0 && !fz.any() && !src.dense_pairs && !src.n_dev)
+        if (knobs().gemv_q4k_mfma && !fz.any() && !src.dense_pairs && !src.n_dev)
             return gemv_q4k_mfma(w, src, x, y, n, k, st);
         return launch_gemv_q<TYPE_Q4_K>(w, src, fz, x, y, n, k, rb, st);
     }

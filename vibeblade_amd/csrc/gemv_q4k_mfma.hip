@@ -401,7 +401,6 @@ struct MfmaShape {
     size_t lds;
 };
 
-constexpr int kNumCUs = 256;
 
 size_t mfma_lds(int nsb, int ks, int wpg) {
     const int rows_wg = (wpg / ks) * 16;
@@ -418,6 +417,7 @@ MfmaShape mfma_shape(int64_t n, int nsb) {
     int64_t best_key[3] = {0, 0, 0};
     bool have = false;
     const int64_t nrg = (n + 15) / 16;
+    const int64_t cus = num_cus();
     auto consider = [&](int ks, int wpg) -> MfmaShape {
         const int nsbw = ((nsb + ks - 1) / ks + SB_STEP - 1) / SB_STEP * SB_STEP;
         const int steps = nsbw / SB_STEP;
@@ -437,8 +437,8 @@ MfmaShape mfma_shape(int64_t n, int nsb) {
             const int64_t per_waves = 8 / wpg;
             const int64_t res = per_lds < per_waves ? per_lds : per_waves;
             if (res < 1) continue;
-            const int64_t rounds = (c.grid + kNumCUs * res - 1) / (kNumCUs * res);
-            const int64_t wgs_cu = (c.grid + kNumCUs - 1) / kNumCUs;
+            const int64_t rounds = (c.grid + cus * res - 1) / (cus * res);
+            const int64_t wgs_cu = (c.grid + cus - 1) / cus;
             const int64_t waves_cu = (wgs_cu < res ? wgs_cu : res) * wpg;
             const int64_t key[3] = {rounds, -waves_cu, static_cast<int64_t>(c.nsbw)};
             bool better = !have;
@@ -453,9 +453,9 @@ MfmaShape mfma_shape(int64_t n, int nsb) {
             }
         }
     }
-    if (const char* cfg = std::getenv("VB_GEMV_MFMA_CFG")) {
-        int a = 0, b = 0;
-        if (std::sscanf(cfg, "%d,%d", &a, &b) == 2 && b >= 1 && b <= nsb && a >= b && a % b == 0 && a <= 8) {
+    if (knobs().gemv_mfma_wpg > 0) {
+        const int a = knobs().gemv_mfma_wpg, b = knobs().gemv_mfma_ks;
+        if (b <= nsb && a >= b && a % b == 0 && a <= 8) {
             const MfmaShape c = consider(b, a);
             if ((b - 1) * c.nsbw < nsb && c.lds <= 160 * 1024 && 64 * a <= (c.depth <= 2 ? 512 : 256)) best = c;
         }

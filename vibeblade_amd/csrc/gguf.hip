@@ -132,7 +132,8 @@ class CopyPool {
 
     void copy(void* dst, const uint8_t* src, size_t m) {
         const size_t parts = threads_.size() + 1;
-        const size_t part = (m / parts + 4095) & ~size_t(4095);
+        // round the share up before aligning it to pages: parts * part >= m
+        const size_t part = ((m + parts - 1) / parts + 4095) & ~size_t(4095);
         {
             std::lock_guard<std::mutex> lk(mu_);
             dst_ = static_cast<uint8_t*>(dst);

@@ -1,9 +1,13 @@
 // Runtime part of the C ABI: error text, device selection, buffers, streams.
 // The op entry points live next to their kernels (dequant.hip, gemv.hip, ...).
+#include <atomic>
 #include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 
 #include "vb_common.hpp"
+#include "vb_internal.hpp"
 #include "../../include/vbhip.h"
 
 namespace vb {
@@ -20,6 +24,68 @@ void set_error(const char* fmt, ...) {
 }
 
 const char* last_error() { return g_last_error.c_str(); }
+
+namespace {
+Knobs read_knobs() {
+    Knobs k;
+    if (const char* e = std::getenv("VB_GEMV_RING")) {
+        const int d = std::atoi(e);
+        if (d >= 1 && d <= 4) k.gemv_ring = d;
+    }
+    if (const char* e = std::getenv("VB_GEMV_CFG")) {
+        int a = 0, b = 0;
+        if (std::sscanf(e, "%d,%d", &a, &b) == 2 && a >= 1 && b >= 1) {
+            k.gemv_cfg_wpg = a;
+            k.gemv_cfg_rpg = b;
+        }
+    }
+    if (const char* e = std::getenv("VB_GEMV_Q4K_PATH")) k.gemv_q4k_mfma = std::strcmp(e, "mfma") == 0;
+    if (const char* e = std::getenv("VB_GEMV_MFMA_CFG")) {
+        int a = 0, b = 0;
+        if (std::sscanf(e, "%d,%d", &a, &b) == 2 && a >= 1 && b >= 1) {
+            k.gemv_mfma_wpg = a;
+            k.gemv_mfma_ks = b;
+        }
+    }
+    if (const char* e = std::getenv("VB_GEMM_NF")) {
+        const int v = std::atoi(e);
+        if (v == 6 || v == 8) k.gemm_nf = v;
+    }
+    if (const char* e = std::getenv("VB_SPARSE_FUSED")) k.sparse_fused = e[0] != '0';
+    if (const char* e = std::getenv("VB_SPARSE_NPW")) k.sparse_npw = e[0] == '2' ? 2 : 0;
+    return k;
+}
+
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_num_cus[kMaxDevices];
+}  // namespace
+
+// The current overrides: an immutable snapshot behind an atomic pointer,
+// replaced (never freed: a few bytes per reload) by vb_tuning_reload.
+std::atomic<const Knobs*> g_knobs{nullptr};
+
+const Knobs& knobs() {
+    const Knobs* k = g_knobs.load(std::memory_order_acquire);
+    if (!k) {
+        const Knobs* fresh = new Knobs(read_knobs());
+        if (g_knobs.compare_exchange_strong(k, fresh, std::memory_order_acq_rel)) {
+            k = fresh;
+        } else {
+            delete fresh;  // another thread published first; k holds its snapshot
+        }
+    }
+    return *k;
+}
+
+int num_cus() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+    int n = g_num_cus[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    g_num_cus[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
 
 int check_launch(const char* what) {
     const hipError_t e = hipGetLastError();
@@ -66,6 +132,13 @@ int vb_init(int device) {
                   prop.gcnArchName);
         return E_UNSUPPORTED;
     }
+    (void)knobs();
+    (void)num_cus();
+    return OK;
+}
+
+int vb_tuning_reload(void) {
+    g_knobs.store(new Knobs(read_knobs()), std::memory_order_release);
     return OK;
 }
 

@@ -803,8 +803,7 @@ struct SparseWs {
 // results (and the dense hidden vector for layout 0).
 bool fused_path(int64_t h, int32_t layout) {
     if (layout != 1 || h > 4096) return false;
-    const char* e = std::getenv("VB_SPARSE_FUSED");
-    return !(e && e[0] == '0');
+    return knobs().sparse_fused;
 }
 
 SparseWs sparse_ws(int64_t h, int64_t i, int32_t n_active, int32_t layout) {
@@ -920,8 +919,7 @@ int sparse_ffn_impl(const void* wg, const void* wu, const void* wd, int32_t down
         }
         const int units = static_cast<int>(h / 64);
         const int slots = (units + 7) & ~7;  // gemv_core.hpp: encoded units, a multiple of 8
-        const char* ne = std::getenv("VB_SPARSE_NPW");
-        const int npw = ne && ne[0] == '2' ? 2 : FUSED_NPW;
+        const int npw = knobs().sparse_npw == 2 ? 2 : FUSED_NPW;
         const int nblk = (n_active + 8 * npw - 1) / (8 * npw);
         float* part = reinterpret_cast<float*>(wsb);
         const dim3 g(static_cast<uint32_t>(nblk));

@@ -5,6 +5,29 @@
 
 namespace vb {
 
+// Launch-shape overrides for tuning sweeps, read from the environment once
+// per process (vb_init reads them; so does the first op call without it):
+//   VB_GEMV_RING=d, VB_GEMV_CFG="wpg,rpg"   GEMV ring depth / workgroup shape
+//   VB_GEMV_Q4K_PATH=mfma                     Q4_K GEMV on the int8-MFMA kernel
+//   VB_GEMV_MFMA_CFG="wpg,ks"                 that kernel's workgroup shape
+//   VB_GEMM_NF=6|8                            tiled GEMM columns per workgroup
+//   VB_SPARSE_FUSED=0, VB_SPARSE_NPW=2        sparse FFN kernel choice
+// Zero / false means "no override".
+struct Knobs {
+    int gemv_ring = 0;
+    int gemv_cfg_wpg = 0, gemv_cfg_rpg = 0;
+    bool gemv_q4k_mfma = false;
+    int gemv_mfma_wpg = 0, gemv_mfma_ks = 0;
+    int gemm_nf = 0;
+    bool sparse_fused = true;
+    int sparse_npw = 0;
+};
+const Knobs& knobs();
+
+// Compute units of the current device, from its properties (cached per
+// device; 256 on MI355X).
+int num_cus();
+
 // Rows of a GEMV launch: plain (row r of w), or gathered gate/up pairs of a
 // sparse FFN (row r = row gidx[r/2] of w for even r, of w2 for odd r).  zbuf
 // / zn: an int buffer the launch clears (counters of a following kernel).

@@ -68,6 +68,23 @@ class TensorInfo:
         return n
 
 
+class _Mapping:
+    """Owner of the native handle (the file mapping).  ``GGUFFile`` and every
+    ``tensor_data`` view hold a reference, so the mapping outlives
+    ``close()`` for as long as a view of it is alive."""
+
+    def __init__(self, lib, h):
+        self._lib, self.h = lib, h
+
+    def __del__(self) -> None:
+        h, self.h = self.h, None
+        if h is not None and h.value:
+            try:
+                self._lib.vb_gguf_close(h)
+            except Exception:
+                pass
+
+
 class GGUFFile:
     """A parsed .gguf file (see the module docstring)."""
 
@@ -78,6 +95,7 @@ class GGUFFile:
         self._lib = _lib.load()
         h = ctypes.c_void_p()
         _lib.check("vb_gguf_open", self._lib.vb_gguf_open(path.encode(), ctypes.byref(h)))
+        self._map = _Mapping(self._lib, h)
         self._h = h
         self.path = path
         ver, align = ctypes.c_uint32(), ctypes.c_uint64()
@@ -155,14 +173,16 @@ class GGUFFile:
 
     def tensor_data(self, name: str):
         """Read-only numpy uint8 view of the tensor's bytes in the mapping, or
-        None when absent (gguf.h:38)."""
+        None when absent (gguf.h:38).  The view keeps the mapping alive: it
+        stays valid after ``close()`` or after this object is dropped."""
         i = self._by_name.get(name)
         if i is None:
             return None
         p = ctypes.c_void_p()
-        _lib.check("vb_gguf_tensor_data", self._lib.vb_gguf_tensor_data(self._h, i, ctypes.byref(p)))
+        _lib.check("vb_gguf_tensor_data", self._lib.vb_gguf_tensor_data(self._handle(), i, ctypes.byref(p)))
         n = self._tensors[i].size
         buf = (ctypes.c_uint8 * n).from_address(p.value) if n else (ctypes.c_uint8 * 0)()
+        buf._owner = self._map  # the view's base holds the mapping
         arr = np.frombuffer(buf, dtype=np.uint8)
         arr.flags.writeable = False
         return arr
@@ -207,6 +227,7 @@ class GGUFFile:
         import torch
 
         from .tensor import QTensor, _dev, _stream
+        h = self._handle()
         i = self._by_name.get(name)
         if i is None:
             raise KeyError(f"Tensor not found: {name}")
@@ -216,16 +237,21 @@ class GGUFFile:
         dev = _dev(device)
         buf = torch.empty(t.size, dtype=torch.uint8, device=dev)
         with torch.cuda.device(dev):
-            _lib.check("vb_gguf_upload", self._lib.vb_gguf_upload(self._h, i, buf.data_ptr(), _stream()))
+            _lib.check("vb_gguf_upload", self._lib.vb_gguf_upload(h, i, buf.data_ptr(), _stream()))
         return QTensor(buf, t.type, t.rows, t.dims[0])
 
     # ---- lifetime -------------------------------------------------------------
 
+    def _handle(self):
+        if getattr(self, "_h", None) is None:
+            raise ValueError("GGUF file is closed")
+        return self._h
+
     def close(self) -> None:
-        h = getattr(self, "_h", None)
-        if h is not None and h.value:
-            self._lib.vb_gguf_close(h)
-            self._h = None
+        """Release this object's hold on the mapping; it is unmapped once no
+        ``tensor_data`` view of it is left."""
+        self._h = None
+        self._map = None
 
     def __enter__(self):
         return self

@@ -16,7 +16,6 @@ from __future__ import annotations
 
 import threading
 import time
-from dataclasses import dataclass
 
 import numpy as np
 import torch
@@ -26,30 +25,50 @@ from .moe import grouped_ffn, _dense_ffn, _sanitize
 __all__ = ["ExecutorStats", "HotColdExecutor"]
 
 
-@dataclass
-class ExecutorStats:
-    """Per-token execution statistics (vibeblade/moe_executor.py:31-54)."""
+_COUNTS = ("gpu_hits", "cpu_falls")
+_TIMES_MS = ("gpu_latency_ms", "cpu_latency_ms", "sync_latency_ms")
 
-    gpu_hits: int = 0
-    cpu_falls: int = 0
-    gpu_latency_ms: float = 0.0
-    cpu_latency_ms: float = 0.0
-    sync_latency_ms: float = 0.0
+
+class ExecutorStats:
+    """Routed-expert counters and time spent, for one dispatch or summed over
+    dispatches.  Field names, ``hit_rate`` and the ``to_dict`` keys and
+    rounding are the reference's interface (vibeblade/moe_executor.py:31-54)."""
+
+    __slots__ = _COUNTS + _TIMES_MS
+
+    def __init__(self, gpu_hits: int = 0, cpu_falls: int = 0, gpu_latency_ms: float = 0.0,
+                 cpu_latency_ms: float = 0.0, sync_latency_ms: float = 0.0):
+        self.gpu_hits, self.cpu_falls = gpu_hits, cpu_falls
+        self.gpu_latency_ms, self.cpu_latency_ms, self.sync_latency_ms = gpu_latency_ms, cpu_latency_ms, sync_latency_ms
 
     @property
     def hit_rate(self) -> float:
-        total = self.gpu_hits + self.cpu_falls
-        return self.gpu_hits / total if total > 0 else 0.0
+        """Hot share of the routed experts (0 before anything was routed)."""
+        routed = self.gpu_hits + self.cpu_falls
+        return self.gpu_hits / routed if routed else 0.0
+
+    def add(self, other: "ExecutorStats") -> "ExecutorStats":
+        """Accumulate another record into this one (counts and times)."""
+        for name in self.__slots__:
+            setattr(self, name, getattr(self, name) + getattr(other, name))
+        return self
+
+    def copy(self) -> "ExecutorStats":
+        return ExecutorStats().add(self)
 
     def to_dict(self) -> dict:
-        return {
-            "gpu_hits": self.gpu_hits,
-            "cpu_falls": self.cpu_falls,
-            "gpu_latency_ms": round(self.gpu_latency_ms, 3),
-            "cpu_latency_ms": round(self.cpu_latency_ms, 3),
-            "sync_latency_ms": round(self.sync_latency_ms, 3),
-            "hit_rate": round(self.hit_rate, 4),
-        }
+        d = {name: getattr(self, name) for name in _COUNTS}
+        d.update((name, round(getattr(self, name), 3)) for name in _TIMES_MS)
+        d["hit_rate"] = round(self.hit_rate, 4)
+        return d
+
+    def __eq__(self, other) -> bool:
+        if not isinstance(other, ExecutorStats):
+            return NotImplemented
+        return all(getattr(self, n) == getattr(other, n) for n in self.__slots__)
+
+    def __repr__(self) -> str:
+        return "ExecutorStats(" + ", ".join(f"{n}={getattr(self, n)!r}" for n in self.__slots__) + ")"
 
 
 class HotColdExecutor:
@@ -85,8 +104,7 @@ class HotColdExecutor:
     @property
     def stats(self) -> ExecutorStats:
         with self._stats_lock:
-            s = self._total_stats
-            return ExecutorStats(s.gpu_hits, s.cpu_falls, s.gpu_latency_ms, s.cpu_latency_ms, s.sync_latency_ms)
+            return self._total_stats.copy()
 
     def reset_stats(self) -> None:
         with self._stats_lock:
@@ -118,45 +136,44 @@ class HotColdExecutor:
         output = _sanitize(out).astype(np.float32)
         t2 = time.perf_counter()
 
-        hot_ids = set(self._hot_map.hot_experts.get(layer_idx, []))
-        hits = int(sum(1 for e in indices.ravel() if int(e) in hot_ids))
-        falls = int(indices.size - hits)
-        per = ExecutorStats(gpu_hits=hits, cpu_falls=falls, gpu_latency_ms=(t1 - t0) * 1000.0,
+        routed = np.asarray(indices).reshape(-1)
+        hits = int(np.count_nonzero(np.isin(routed, list(self._hot_map.hot_experts.get(layer_idx, ())))))
+        per = ExecutorStats(gpu_hits=hits, cpu_falls=int(routed.size) - hits, gpu_latency_ms=(t1 - t0) * 1000.0,
                             cpu_latency_ms=cpu_ms, sync_latency_ms=(t2 - t1) * 1000.0)
         with self._stats_lock:
-            s = self._total_stats
-            s.gpu_hits += per.gpu_hits
-            s.cpu_falls += per.cpu_falls
-            s.gpu_latency_ms += per.gpu_latency_ms
-            s.cpu_latency_ms += per.cpu_latency_ms
-            s.sync_latency_ms += per.sync_latency_ms
-        stats = {
-            "gpu_hits": per.gpu_hits,
-            "cpu_falls": per.cpu_falls,
-            "hit_rate": per.hit_rate,
-            "gpu_latency_ms": round(per.gpu_latency_ms, 3),
-            "cpu_latency_ms": round(per.cpu_latency_ms, 3),
-            "sync_latency_ms": round(per.sync_latency_ms, 3),
-            "expert_indices": indices[0] if squeeze else indices,
-            "expert_weights": weights[0] if squeeze else weights,
-        }
+            self._total_stats.add(per)
+        # per-dispatch dict: to_dict's keys and rounding, except an unrounded
+        # hit rate, plus the routing of the (first, for 1-D x) token(s)
+        stats = per.to_dict()
+        stats["hit_rate"] = per.hit_rate
+        stats["expert_indices"] = indices[0] if squeeze else indices
+        stats["expert_weights"] = weights[0] if squeeze else weights
         return (output[0] if squeeze else output.reshape(orig_shape)), stats
 
+    def _expert_counts(self, layer_idx=None):
+        """(hot, cold) expert counts of one layer, or of every layer (None)."""
+        maps = (self._hot_map.hot_experts, self._hot_map.cold_experts)
+        if layer_idx is not None:
+            return tuple(len(m.get(layer_idx, ())) for m in maps)
+        return tuple(sum(map(len, m.values())) for m in maps)
+
     def layer_stats(self, layer_idx: int) -> dict:
-        hot = self._hot_map.hot_experts.get(layer_idx, [])
-        cold = self._hot_map.cold_experts.get(layer_idx, [])
-        return {"layer": layer_idx, "hot_experts": len(hot), "cold_experts": len(cold),
-                "hot_pct": len(hot) / max(len(hot) + len(cold), 1) * 100}
+        """Hot and cold expert counts of a layer and the hot share in percent
+        (keys of vibeblade/moe_executor.py:363-372)."""
+        hot, cold = self._expert_counts(layer_idx)
+        return {"layer": layer_idx, "hot_experts": hot, "cold_experts": cold,
+                "hot_pct": 100.0 * hot / max(hot + cold, 1)}
 
     def memory_estimate(self, expert_dim: int, shared_dim: int, bytes_per_param: float = 0.5) -> dict:
-        per_expert = 3 * shared_dim * expert_dim * bytes_per_param
-        total_hot = sum(len(v) for v in self._hot_map.hot_experts.values())
-        total_cold = sum(len(v) for v in self._hot_map.cold_experts.values())
-        return {"hot_vram_gb": total_hot * per_expert / (1024 ** 3),
-                "cold_ram_gb": total_cold * per_expert / (1024 ** 3),
-                "per_expert_mb": per_expert / (1024 ** 2),
-                "total_hot_experts": total_hot,
-                "total_cold_experts": total_cold}
+        """Bytes held by the hot and the cold experts of the whole map; an
+        expert is three shared_dim x expert_dim matrices (gate, up, down) of
+        ``bytes_per_param`` per element (keys of
+        vibeblade/moe_executor.py:374-400; GB and MB are binary)."""
+        expert_bytes = 3.0 * shared_dim * expert_dim * bytes_per_param
+        hot, cold = self._expert_counts()
+        gib, mib = float(1 << 30), float(1 << 20)
+        return {"hot_vram_gb": hot * expert_bytes / gib, "cold_ram_gb": cold * expert_bytes / gib,
+                "per_expert_mb": expert_bytes / mib, "total_hot_experts": hot, "total_cold_experts": cold}
 
     def shutdown(self) -> None:
         """Release host resources (there is no thread pool); dispatch keeps

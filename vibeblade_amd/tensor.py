@@ -37,6 +37,19 @@ def _as_f32_dev(x, device) -> torch.Tensor:
     return t.contiguous()
 
 
+def _check_out(out: torch.Tensor, numel: int, device, what: str) -> torch.Tensor:
+    """A caller-supplied output must be a contiguous fp32 tensor of exactly
+    ``numel`` elements on ``device``: the kernels write through its pointer."""
+    if not isinstance(out, torch.Tensor):
+        raise ValueError(f"{what}: out must be a torch tensor")
+    if out.dtype != torch.float32 or out.device != torch.device(device) or not out.is_contiguous():
+        raise ValueError(f"{what}: out must be a contiguous float32 tensor on {device} "
+                         f"(got {out.dtype} on {out.device}, contiguous={out.is_contiguous()})")
+    if out.numel() != numel:
+        raise ValueError(f"{what}: out has {out.numel()} elements, {numel} expected")
+    return out
+
+
 class QTensor:
     """A GGUF tensor (rows x k, type ``qtype``) resident on one GPU."""
 
@@ -115,6 +128,7 @@ def embed_rows(table: QTensor, tokens, out: torch.Tensor | None = None) -> torch
     n = ids.numel()
     if out is None:
         out = torch.empty((n, table.k), dtype=torch.float32, device=dev)
+    _check_out(out, n * table.k, dev, "embed_rows")
     _lib.call("vb_embed_rows", table.ptr(), table.qtype, table.rows, table.k, ids.data_ptr() if n else None, n,
               out.data_ptr(), _stream())
     return out
@@ -127,6 +141,7 @@ def gemv(w: QTensor, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.
         raise ValueError(f"gemv: x has {x.numel()} elements, W has k={w.k}")
     if out is None:
         out = torch.empty(w.rows, dtype=torch.float32, device=w.device)
+    _check_out(out, w.rows, w.device, "gemv")
     _lib.call("vb_gemv", w.ptr(), x.data_ptr(), out.data_ptr(), w.rows, w.k, w.qtype, _stream())
     return out
 
@@ -151,6 +166,7 @@ def gemm(w: QTensor, x: torch.Tensor, out: torch.Tensor | None = None,
     m = x.shape[0]
     if out is None:
         out = torch.empty((m, w.rows), dtype=torch.float32, device=w.device)
+    _check_out(out, m * w.rows, w.device, "gemm")
     xdt = X_F16 if x.dtype == torch.float16 else X_F32
     _lib.call("vb_gemm", w.ptr(), x.data_ptr(), xdt, out.data_ptr(), m, w.rows, w.k, w.qtype,
               variant, _stream())
@@ -218,6 +234,7 @@ def sparse_ffn(gate: QTensor, up: QTensor, down: QTensor, x: torch.Tensor, activ
     n_active = active.numel()
     if out is None:
         out = torch.empty(h, dtype=torch.float32, device=dev)
+    _check_out(out, h, dev, "sparse_ffn")
     nbytes = _lib.load().vb_sparse_ffn_workspace(h, i, n_active, down_layout)
     if nbytes < 0:
         raise ValueError("sparse_ffn: bad shape")
@@ -262,6 +279,7 @@ def ffn_block(gate: QTensor, up: QTensor, down: QTensor, x: torch.Tensor, norm_w
             raise ValueError(f"ffn_block: norm_w has {nw.numel()} elements, expected {hd}")
     if out is None:
         out = torch.empty(hd, dtype=torch.float32, device=dev)
+    _check_out(out, hd, dev, "ffn_block")
     ws = _workspace(_lib.load().vb_ffn_block_workspace(hd, inter), dev)
     _lib.call("vb_ffn_block", x.data_ptr(), None if nw is None else nw.data_ptr(), float(eps), gate.ptr(),
               up.ptr(), gate.qtype, down.ptr(), down.qtype, hd, inter, int(act), int(bool(residual)),
