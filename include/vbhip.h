@@ -148,6 +148,18 @@ int vb_sparse_ffn(const void* wg, const void* wu, const void* wd, int32_t down_l
                   const float* x, const int32_t* active, int32_t n_active, int32_t act_kind,
                   float* y, int64_t h, int64_t i, int32_t ggml_type, void* workspace,
                   size_t workspace_bytes, void* stream);
+/* vb_sparse_ffn without a workspace argument and without any allocation:
+ * the workspace is a static 8 MiB device array per GPU (held until the
+ * process ends), enough for config-4 shapes (h = 4096, i = 14336) up to
+ * about 4096 active neurons on the fused path; shapes that need more
+ * (vb_sparse_ffn_workspace above 8 MiB) return VB_E_INVAL with a message.
+ * All calls on one GPU share the array: calls that overlap on one GPU (other
+ * streams or threads) race.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). */
+int vb_sparse_ffn_noalloc(const void* wg, const void* wu, const void* wd, int32_t down_layout,
+                          const float* x, const int32_t* active, int32_t n_active, int32_t act_kind,
+                          float* y, int64_t h, int64_t i, int32_t ggml_type, void* stream);
 /* The TurboSparse FFN block: vb_sparse_ffn over n = x / sqrt(mean(x^2) +
  * eps) * norm_w (n = x when norm_w is NULL), plus x when add_residual != 0;
  * y may be x.  The sparse branch of the decoder layer with its pre-FFN

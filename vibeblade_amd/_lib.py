@@ -42,6 +42,8 @@ SIGNATURES = {
     "vb_sparse_ffn_workspace": (_i64, [_i64, _i64, _i32, _i32]),
     "vb_sparse_ffn": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _vp, _i64, _i64, _i32,
                                      _vp, _sz, _vp]),
+    "vb_sparse_ffn_noalloc": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _vp, _i64, _i64, _i32,
+                                             _vp]),
     "vb_ffn_block_workspace": (_i64, [_i64, _i64]),
     "vb_ffn_block": (ctypes.c_int, [_vp, _vp, ctypes.c_float, _vp, _vp, _i32, _vp, _i32, _i64, _i64, _i32,
                                     _i32, _vp, _vp, _sz, _vp]),

@@ -134,7 +134,8 @@ int vb_init(int device) {
     }
     (void)knobs();
     (void)num_cus();
-    return OK;
+    void* scratch_dev = nullptr;  // the allocation-free entry point's scratch on this device
+    return sparse_scratch_ptr(&scratch_dev);
 }
 
 int vb_tuning_reload(void) {

@@ -20,6 +20,7 @@
 //        output unit u (64 columns) over every active row; row partials meet
 //        in LDS and are added in fixed order (deterministic, one launch).
 #include <cstdlib>
+#include <mutex>
 
 #include "gemv_core.hpp"
 #include "mfma_q4k.hpp"
@@ -1001,6 +1002,80 @@ extern "C" int vb_sparse_ffn_block(const void* wg, const void* wu, const void* w
     return sparse_ffn_impl(wg, wu, wd, down_layout, x, norm_w, eps, active, n_active, n_active_dev, act_kind,
                            add_residual != 0, y, h, i, ggml_type, workspace, workspace_bytes, as_stream(stream),
                            "vb_sparse_ffn_block");
+}
+
+// ---- allocation-free variant (static scratch) ------------------------------
+//
+// vb_sparse_ffn_noalloc runs vb_sparse_ffn with its workspace in `scratch`, a
+// file-scope device array of kSparseScratchBytes per GPU (held until the
+// process ends), for callers that cannot allocate device memory.  The array's
+// name is a host-side stand-in: its device address is resolved once per
+// device with hipGetSymbolAddress (vb_init, or the first call on a device)
+// and only that address is handed to kernels.  Every call on one GPU shares
+// the array: calls that overlap on one GPU (different streams or threads)
+// race.  Nothing in it needs clearing between calls: the fused path writes
+// every partial it reads, and the GGUF-down path's hidden vector is cleared
+// inside its gate/up launch.
+namespace {
+constexpr size_t kSparseScratchBytes = size_t(8) << 20;  // 8 MiB
+__device__ __align__(256) uint8_t scratch[kSparseScratchBytes];
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchDevices] = {};
+}  // namespace
+
+namespace vb {
+
+// Device address of `scratch` on the current device (resolved once per device).
+int sparse_scratch_ptr(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        set_error("vb_sparse_ffn_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+        return E_HIP;
+    }
+    if (dev < 0 || dev >= kScratchDevices) {
+        set_error("vb_sparse_ffn_noalloc: device %d beyond the %d supported", dev, kScratchDevices);
+        return E_UNSUPPORTED;
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            set_error("vb_sparse_ffn_noalloc: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+            return E_HIP;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return OK;
+}
+
+}  // namespace vb
+
+extern "C" int vb_sparse_ffn_noalloc(const void* wg, const void* wu, const void* wd, int32_t down_layout,
+                                     const float* x, const int32_t* active, int32_t n_active, int32_t act_kind,
+                                     float* y, int64_t h, int64_t i, int32_t ggml_type, void* stream) {
+    const int64_t need = vb_sparse_ffn_workspace(h, i, n_active, down_layout);
+    if (need < 0) {
+        set_error("vb_sparse_ffn_noalloc: bad shape (h=%lld, i=%lld, n_active=%d, down_layout=%d)",
+                  static_cast<long long>(h), static_cast<long long>(i), n_active, down_layout);
+        return E_INVAL;
+    }
+    if (static_cast<uint64_t>(need) > kSparseScratchBytes) {
+        set_error("vb_sparse_ffn_noalloc: h=%lld, i=%lld, n_active=%d, down_layout=%d needs %lld bytes of "
+                  "scratch, beyond the %zu of the static scratch; use vb_sparse_ffn with a workspace",
+                  static_cast<long long>(h), static_cast<long long>(i), n_active, down_layout,
+                  static_cast<long long>(need), kSparseScratchBytes);
+        return E_INVAL;
+    }
+    void* ws = nullptr;
+    const int rc = sparse_scratch_ptr(&ws);
+    if (rc != OK) return rc;
+    return sparse_ffn_impl(wg, wu, wd, down_layout, x, nullptr, 0.f, active, n_active, nullptr, act_kind, false, y,
+                           h, i, ggml_type, ws, kSparseScratchBytes, as_stream(stream), "vb_sparse_ffn_noalloc");
 }
 
 extern "C" int vb_ema_update(float* probs, int64_t n, const uint8_t* mask, double alpha, void* stream) {

@@ -28,6 +28,10 @@ const Knobs& knobs();
 // device; 256 on MI355X).
 int num_cus();
 
+// Device address of the allocation-free sparse FFN's static scratch on the
+// current device (sparse.hip; resolved once per device).
+int sparse_scratch_ptr(void** out);
+
 // Rows of a GEMV launch: plain (row r of w), or gathered gate/up pairs of a
 // sparse FFN (row r = row gidx[r/2] of w for even r, of w2 for odd r).  zbuf
 // / zn: an int buffer the launch clears (counters of a following kernel).
