@@ -128,6 +128,7 @@ def test_gemv_dot_launch_shapes(knob, cfg, ring):
     """v_dot4 kernel launch overrides: rows per wave x ring depth (1-4; rows
     not a multiple of the depth take padding steps), one k-slice (k = 4096)
     and four (k = 14336)."""
+    knob("VB_GEMV_Q4K_PATH", "dot")  # Q4_K through the general kernel too
     knob("VB_GEMV_CFG", cfg)
     if ring:
         knob("VB_GEMV_RING", ring)
@@ -274,3 +275,64 @@ def test_new_types_embed_rows(qtype):
     want = O.dequantize(raw, 512, qtype)
     for t, i in enumerate(ids):
         assert np.array_equal(bits(got[t]), bits(want[i] if 0 <= i < 300 else np.zeros(512, np.float32)))
+
+
+# ---- the short-row Q4_K kernel (k <= 4096, up to 8 rows per wave) ----------
+
+def _q4k_case(rows, k, seed):
+    qt = QTensor.quantize(rand_weights(rows, k, seed), ggml.GGML_TYPE_Q4_K)
+    x = np.random.default_rng(seed + 1).standard_normal(k).astype(np.float32)
+    return qt, x
+
+
+@pytest.mark.parametrize("wpg", [8, 16])
+@pytest.mark.parametrize("rpw", [1, 2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("ring", ["", "1", "2"])
+def test_gemv_q4k_short_rows_per_wave(knob, wpg, rpw, ring):
+    """Every rows-per-wave count with 8- and 16-wave workgroups (forced with
+    VB_GEMV_CFG), at each ring depth; three full workgroups and a ragged one."""
+    knob("VB_GEMV_CFG", f"{wpg},{rpw}")
+    if ring:
+        knob("VB_GEMV_RING", ring)
+    rows = 3 * wpg * rpw + 5
+    qt, x = _q4k_case(rows, 4096, 10 * wpg + rpw)
+    y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy()
+    want = O.gemv(qt.to_numpy_bytes(), x, rows, 4096, qt.qtype)
+    assert O.rel_l2(y, want) <= GEMV_TOL
+    assert np.max(np.abs(y - want)) <= 1e-3 * np.abs(want).max() + 1e-6  # no row dropped or swapped
+
+
+@pytest.mark.parametrize("rows", [1, 2047, 4096, 14336, 28672, 32768])
+def test_gemv_q4k_short_default_shapes(rows):
+    """The default launch shape at row counts from 1 to the largest it takes
+    (32768 = 256 CUs x 16 waves x 8 rows)."""
+    qt, x = _q4k_case(rows, 4096, rows)
+    y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy()
+    want = O.gemv(qt.to_numpy_bytes(), x, rows, 4096, qt.qtype)
+    assert O.rel_l2(y, want) <= GEMV_TOL
+    assert np.max(np.abs(y - want)) <= 1e-3 * np.abs(want).max() + 1e-6
+
+
+@pytest.mark.parametrize("rows,k", [(1, 256), (3, 256), (17, 768), (64, 1280), (129, 2048), (1, 4096)])
+def test_gemv_q4k_short_k_idle_lanes(rows, k):
+    """k < 4096 leaves lanes idle: they load one of the row's own units (in
+    bounds) and must contribute nothing (counted twice, it would show here)."""
+    qt, x = _q4k_case(rows, k, rows + k)
+    y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy()
+    want = O.gemv(qt.to_numpy_bytes(), x, rows, k, qt.qtype)
+    assert O.rel_l2(y, want) <= GEMV_TOL
+    assert np.max(np.abs(y - want)) <= 1e-3 * np.abs(want).max() + 1e-6
+
+
+def test_gemv_q4k_short_matches_general_kernel(knob):
+    """The short-row kernel and the general v_dot4 kernel agree at the
+    headline shape (both against the oracle; 16-bit vs 15-bit x encodings)."""
+    rows, k = 14336, 4096
+    gen = torch.Generator(device="cuda").manual_seed(77)
+    qt = QTensor.quantize(torch.randn((rows, k), generator=gen, device="cuda") * 0.02, ggml.GGML_TYPE_Q4_K)
+    x = torch.randn(k, generator=gen, device="cuda")
+    y_short = gemv(qt, x).cpu().numpy()
+    knob("VB_GEMV_Q4K_PATH", "dot")
+    y_gen = gemv(qt, x).cpu().numpy()
+    want = O.gemv(qt.to_numpy_bytes(), x.cpu().numpy(), rows, k, qt.qtype)
+    assert O.rel_l2(y_short, want) <= 2e-4 and O.rel_l2(y_gen, want) <= 2e-4

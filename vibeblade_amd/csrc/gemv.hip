@@ -325,7 +325,7 @@ GemvShape gemv_shape(int64_t n, int units, bool even_rows = false) {
     if (s.rpg < 1) s.rpg = 1;
     const int64_t max_rpg = kMaxRedFloats / (static_cast<int64_t>(s.wpg / s.wpr) * s.wpr);
     if (s.rpg > max_rpg) s.rpg = static_cast<int>(max_rpg);
-    const int ring = knobs().gemv_ring;  // ring-depth override (0: none)
+    const int ring = knobs().gemv_ring > 4 ? 4 : knobs().gemv_ring;  // ring-depth override (0: none)
     auto depth_of = [&](int rpg) { return ring ? ring : ring_depth<TYPE>(rpg, s.wpr); };
     // the block size must fit the launch bounds of the kernel of that depth
     if (64 * s.wpg > gemv_max_threads_host<TYPE>(depth_of(s.rpg))) s.wpg = 8 / s.wpr * s.wpr;
@@ -462,8 +462,12 @@ int gemv_dispatch_fused(const void* w, const RowSrc& src, const GemvFuse& fz, co
     case TYPE_Q4_K: {
         // v_dot4 kernel by default (fastest measured); VB_GEMV_Q4K_PATH=mfma
         // selects the int8-MFMA kernel (same arithmetic) for plain launches
+        const bool plain = !fz.any() && !src.dense_pairs && !src.n_dev && !src.gidx && src.zn == 0;
         if (knobs().gemv_q4k_mfma && !fz.any() && !src.dense_pairs && !src.n_dev)
             return gemv_q4k_mfma(w, src, x, y, n, k, st);
+        // short rows (k <= 4096) at <= 8 rows per wave: the dedicated kernel
+        if (plain && !knobs().gemv_q4k_general && k <= 4096 && gemv_q4k_rpw(n) > 0)
+            return gemv_q4k_short(w, x, y, n, k, st);
         return launch_gemv_q<TYPE_Q4_K>(w, src, fz, x, y, n, k, rb, st);
     }
     case TYPE_Q6_K: return launch_gemv_q<TYPE_Q6_K>(w, src, fz, x, y, n, k, rb, st);

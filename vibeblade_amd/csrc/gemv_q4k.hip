@@ -1,0 +1,399 @@
+// Q4_K GEMV for rows of k <= 4096 (one 64-element unit per lane):
+// y[n] = sum_k W[n, k] x[k], W in the GGUF layout.  The headline decode
+// shape (Llama-3-8B FFN gate/up, 14336 x 4096) runs here.
+//
+// Replaces gemv_dequant (cpp/src/dequant.cpp:739-780) for Q4_K weights: no
+// weight is decoded to floats.  Per row and lane the work is integer dot
+// products of the 64 nibbles of one unit against the activation encoding,
+// then one scale/min combination:
+//
+//   unit u (lane), super-block u / 4, chunk c = u % 4: sub-blocks 2c (low
+//   nibbles of qs[32c, 32c + 32)) and 2c + 1 (high nibbles), elements
+//   64u .. 64u + 63 of the row (cpp/src/dequant.cpp:278-299).
+//
+// Activation encoding (one per workgroup, in LDS): x ~= s_u * x16 with one
+// fp32 scale s_u per unit, |x16| <= 16383 (15-bit fixed point), x16 = 256 xh
+// + xl with xh, xl signed bytes, and the integer run sums I0, I1 of x16 over
+// the unit's two 32-element runs.  Then, exactly in integers,
+//   D_r = sum_{e in run r} q_e x16_e   (two v_dot4 per 4 weights: xh and xl)
+//   S   = sc0 D0 + sc1 D1,   M = m0 I0 + m1 I1   (24-bit multiplies: |D_r| <=
+//         32 * 15 * 16383 < 2^23)
+// and the lane's share of the row is s_u (d S - dmin M): 3 fp32 roundings
+// per unit.  The encoding error |x - s_u x16| <= s_u / 2 = amax_u / 32766
+// puts the GEMV rel-L2 near 5e-5 (the fp32-accumulate bar is 1e-3).
+//
+// Schedule.  One workgroup of 8 waves per CU; wave w owns RPW consecutive
+// rows and streams them through a ring of NS register buffers: the loads of
+// row s + NS - 1 are issued before row s is computed, so NS - 1 rows are in
+// flight while the wave computes.
+//
+// Loads.  A row (2304 B at k = 4096) is read contiguously: lane L takes the
+// 16 B at 16 L, 1024 + 16 L and (L < 16) 2048 + 16 L, three buffer loads with
+// the row offset in an SGPR, marked non-temporal (the weights are streamed
+// once).  Every load instruction then covers whole cache lines.  Measured on
+// MI355X with the loads alone (14336 x 4096): 6.6 us per launch, against
+// 7.4 us for per-lane unit loads (a 16 B header and two 16 B pieces of one
+// unit per lane, each instruction touching parts of 16 lines; non-temporal
+// made that pattern slower still, 8.8 us, since the other parts of a line
+// are no longer found in the cache).  The wave writes its row into a private
+// LDS row buffer and reads it back in the unit layout (header, qs[32c, +16),
+// qs[32c + 16, +16)); LDS operations of one wave run in order, so one buffer
+// per wave is enough.
+//
+// Each row leaves one partial per lane in a register; after the last row the
+// wave reduces all RPW rows at once with a transposed butterfly (permlane32
+// / permlane16 swaps, then DPP), about 18 instructions for up to 8 rows, and
+// lanes 8g store y.  No LDS reduction and no barrier at the end.
+#include <cstdint>
+
+#include "vb_common.hpp"
+#include "vb_internal.hpp"
+#include "../../include/vbhip.h"
+
+namespace vb {
+namespace {
+
+constexpr int X15_MAX = 16383;
+constexpr int UNITS_MAX = 64;       // k <= 4096
+constexpr int XQ_UNIT_QUADS = 9;    // xh[16], xl[16] dwords, {s, I0, I1, 128 I1}
+
+struct XU {
+    uint32_t h[16], l[16];
+    float s;
+    int i0, i1, c1;
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+// Task t = 8 consecutive elements (part p = t % 8) of unit t / 8; the 8
+// tasks of a unit sit on adjacent lanes.  Units at or past `units` encode
+// as zeros (their lanes contribute nothing).
+__device__ __forceinline__ void encode_task(const float* v_in, int task, int units, uint4* xq, bool store = true) {
+    const int u = task >> 3, p = task & 7;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = u < units ? v_in[i] : 0.f;
+    // all-reductions over the unit's 8 adjacent lanes with DPP (no LDS round
+    // trip): quad butterflies, then row_half_mirror (lane i <-> 7 - i)
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, dpp_mov_f<0xB1>(amax));   // quad_perm [1,0,3,2]
+    amax = fmaxf(amax, dpp_mov_f<0x4E>(amax));   // quad_perm [2,3,0,1]
+    amax = fmaxf(amax, dpp_mov_f<0x141>(amax));  // row_half_mirror
+    const float inv = amax > 0.f ? static_cast<float>(X15_MAX) / amax : 0.f;
+    uint32_t ph[2] = {0, 0}, pl[2] = {0, 0};
+    int isum = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        int q = static_cast<int>(rintf(v[i] * inv));
+        q = q > X15_MAX ? X15_MAX : (q < -X15_MAX ? -X15_MAX : q);
+        isum += q;
+        const int lo = ((q + 128) & 255) - 128;
+        const int hi = (q - lo) >> 8;
+        ph[i >> 2] |= static_cast<uint32_t>(hi & 255) << (8 * (i & 3));
+        pl[i >> 2] |= static_cast<uint32_t>(lo & 255) << (8 * (i & 3));
+    }
+    isum += dpp_mov_i<0xB1>(isum);
+    isum += dpp_mov_i<0x4E>(isum);              // sum over the run's 4 tasks (a quad)
+    const int isum1 = dpp_mov_i<0x141>(isum);   // part 0 reads run 1's sum from part 7
+    if (!store) return;
+    uint4* b = xq + u;
+    reinterpret_cast<uint2*>(&b[(p >> 1) * UNITS_MAX])[p & 1] = make_uint2(ph[0], ph[1]);
+    reinterpret_cast<uint2*>(&b[(4 + (p >> 1)) * UNITS_MAX])[p & 1] = make_uint2(pl[0], pl[1]);
+    if (p == 0) {
+        uint4 m;
+        m.x = __float_as_uint(amax / static_cast<float>(X15_MAX));
+        m.y = static_cast<uint32_t>(isum);
+        m.z = static_cast<uint32_t>(isum1);
+        m.w = static_cast<uint32_t>(128 * isum1);
+        b[8 * UNITS_MAX] = m;
+    }
+}
+
+__device__ __forceinline__ XU read_unit(const uint4* xq, int u) {
+    XU x;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint4 h = xq[i * UNITS_MAX + u], l = xq[(4 + i) * UNITS_MAX + u];
+        x.h[4 * i] = h.x; x.h[4 * i + 1] = h.y; x.h[4 * i + 2] = h.z; x.h[4 * i + 3] = h.w;
+        x.l[4 * i] = l.x; x.l[4 * i + 1] = l.y; x.l[4 * i + 2] = l.z; x.l[4 * i + 3] = l.w;
+    }
+    const uint4 m = xq[8 * UNITS_MAX + u];
+    x.s = __uint_as_float(m.x);
+    x.i0 = static_cast<int>(m.y);
+    x.i1 = static_cast<int>(m.z);
+    x.c1 = static_cast<int>(m.w);
+    return x;
+}
+
+struct RowBuf { u32x4 hdr, qa, qb; };
+struct RowRaw { u32x4 a, b, c; };  // the row's bytes 16 L, 1024 + 16 L, 2048 + 16 (L % 16)
+
+constexpr int CACHE_NT = 2;  // buffer-load cache policy: non-temporal (streamed once)
+constexpr int ROW_SLOTS = 144;  // 16-byte slots of a k = 4096 row buffer (2304 B)
+
+// Lane-constant selectors of the scale / min bytes of sub-blocks 2c, 2c + 1
+// (get_scale_min_k4, cpp/src/dequant.cpp:258-266).  With A, B, C = scales[0:4],
+// [4:8], [8:12] and c' = c % 2:
+//   P = bytes (A[2c'], A[2c'+1], B[2c'], B[2c'+1]), Q = the same bytes of
+//   (C, C >> 4);  c < 2: R = P & 0x3F3F3F3F;  c >= 2: R = (Q & 0x0F0F0F0F) |
+//   ((P >> 2) & 0x30303030);  R = sc0 | sc1 << 8 | m0 << 16 | m1 << 24.
+struct ScaleSel {
+    uint32_t sel, kq, kp, sp;
+};
+
+__device__ __forceinline__ ScaleSel make_sel(int c) {
+    ScaleSel s;
+    const uint32_t c2 = 2u * static_cast<uint32_t>(c & 1);
+    s.sel = c2 | ((c2 + 1u) << 8) | ((c2 + 4u) << 16) | ((c2 + 5u) << 24);
+    const bool hi = c >= 2;
+    s.kq = hi ? 0x0F0F0F0Fu : 0u;
+    s.kp = hi ? 0x30303030u : 0x3F3F3F3Fu;
+    s.sp = hi ? 2u : 0u;
+    return s;
+}
+
+__device__ __forceinline__ float row_part(const RowBuf& r, const XU& x, const ScaleSel& ss) {
+    const uint32_t qd[8] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w, r.qb.x, r.qb.y, r.qb.z, r.qb.w};
+    int dh0 = 0, dl0 = 0, dh1 = 0, dl1 = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint32_t lo = qd[i] & 0x0F0F0F0Fu;
+        const uint32_t hi = (qd[i] ^ 0x80808080u) & 0xF0F0F0F0u;  // 16 (q - 8), signed bytes
+        dh0 = sdot4(lo, x.h[i], dh0);
+        dl0 = sdot4(lo, x.l[i], dl0);
+        dh1 = sdot4(hi, x.h[8 + i], dh1);
+        dl1 = sdot4(hi, x.l[8 + i], dl1);
+    }
+    const int d0 = dh0 * 256 + dl0;
+    const int d1 = (dh1 * 256 + dl1 + x.c1) >> 4;  // sum 16 (q - 8) x16 = 16 D1 - 128 I1
+    const uint32_t A = r.hdr.y, B = r.hdr.z, C = r.hdr.w;
+    const uint32_t P = __builtin_amdgcn_perm(B, A, ss.sel);
+    const uint32_t Q = __builtin_amdgcn_perm(C >> 4, C, ss.sel);
+    const uint32_t R = (Q & ss.kq) | ((P >> ss.sp) & ss.kp);
+    const int S = __mul24(static_cast<int>(R & 0xFFu), d0) + __mul24(static_cast<int>((R >> 8) & 0xFFu), d1);
+    const int M = __mul24(static_cast<int>((R >> 16) & 0xFFu), x.i0) + __mul24(static_cast<int>(R >> 24), x.i1);
+    const float d = f16lo(r.hdr.x), dmin = f16hi(r.hdr.x);
+    return (d * static_cast<float>(S) - dmin * static_cast<float>(M)) * x.s;
+}
+
+// Sum over the 64 lanes of each of a[0..7]; lanes 8g .. 8g + 7 end with the
+// total of row rows_of(g) = 4 (g % 2) + {0, 2, 1, 3}[g / 2].  Fixed order.
+__device__ __forceinline__ float reduce8(const float (&a)[8]) {
+    float b[4];
+#pragma unroll
+    for (int p = 0; p < 4; p++) {  // lanes < 32: row 2p, lanes >= 32: row 2p + 1
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[2 * p]), __float_as_uint(a[2 * p + 1]),
+                                                         false, false);
+        b[p] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+    float c[2];
+#pragma unroll
+    for (int q = 0; q < 2; q++) {  // 16-lane rows: 4q, 4q + 2, 4q + 1, 4q + 3
+        const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(b[2 * q]), __float_as_uint(b[2 * q + 1]),
+                                                         false, false);
+        c[q] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+    const bool odd8 = (threadIdx.x & 8) != 0;
+    const float own = odd8 ? c[1] : c[0];
+    const float other = odd8 ? c[0] : c[1];
+    // lane i takes `other` from lane i ^ 8 (row_ror:8 within the 16-lane row)
+    float v = own + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(other), 0x128, 0xF, 0xF, false));
+    v += dpp_f<0x141>(v);  // row_half_mirror: i <-> 7 - i within 8 lanes
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    return v;
+}
+
+__device__ __forceinline__ int row_of_group(int g) {
+    return 4 * (g & 1) + ((0x3120 >> (4 * (g >> 1))) & 0xF);
+}
+
+template <int RPW, int NS, int WPG>
+__global__ void __launch_bounds__(64 * WPG) gemv_q4k_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                                            float* __restrict__ y, int n, int units, uint32_t rb) {
+    static_assert(WPG == 8 || WPG == 16, "8 or 16 waves: one encode task per thread for the first 512");
+    __shared__ uint4 xq[XQ_UNIT_QUADS * UNITS_MAX];
+    __shared__ u32x4 rowbuf[WPG][ROW_SLOTS];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int row0 = (static_cast<int>(blockIdx.x) * WPG + wave) * RPW;
+    const int rlast = n - 1;
+    // the wave's rows, clamped into the tensor (rows past n load row n - 1
+    // again and store nothing)
+    const int rbase = row0 < rlast ? row0 : rlast;
+    const uint8_t* wb = w + static_cast<int64_t>(rbase) * rb;
+    const int64_t span64 = static_cast<int64_t>(n - rbase) * rb;
+    const uint32_t span = span64 < 0xFFFFFFFFll ? static_cast<uint32_t>(span64) : 0xFFFFFFFFu;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(wb, span);
+    const bool valid = lane < units;
+    const int u = valid ? lane : (lane & 3);  // idle lanes read unit (lane % 4) of the row, discarded
+    // contiguous pieces of the row (rb = 144 * units / 4 bytes = 16 * slots):
+    // slots lane, 64 + lane, 128 + lane % 16.  A piece past the row's end reads
+    // an in-row address instead (coalesced: nothing extra is read) and lands in
+    // a buffer slot that no unit reads; lanes 16..63 repeat lanes 0..15's
+    // third piece, writing the same value to the same slot.
+    // (a row has at least 9 slots, k >= 256, so lane % 8 is always in it)
+    const int slots = static_cast<int>(rb >> 4);
+    const int pc = 128 + (lane & 15);
+    const uint32_t va = 16u * static_cast<uint32_t>(lane < slots ? lane : lane & 7);
+    const uint32_t vb = 16u * static_cast<uint32_t>(64 + lane < slots ? 64 + lane : lane & 7);
+    const uint32_t vc = 16u * static_cast<uint32_t>(pc < slots ? pc : lane & 7);
+    u32x4* rbuf = rowbuf[wave];
+    const int sh = 9 * (u >> 2), sq = sh + 1 + 2 * (u & 3);  // unit slots: header, qs pieces
+
+    auto soff = [&](int s) -> uint32_t {
+        int r = row0 + s;
+        r = r < rlast ? r : rlast;
+        return static_cast<uint32_t>(r - rbase) * rb;
+    };
+    auto issue = [&](RowRaw& b, int s) {
+        const uint32_t so = soff(s);
+        b.a = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(va), static_cast<int>(so), CACHE_NT);
+        b.b = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(vb), static_cast<int>(so), CACHE_NT);
+        b.c = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(vc), static_cast<int>(so), CACHE_NT);
+    };
+    // the row through the wave's LDS buffer into the unit layout
+    auto stage = [&](const RowRaw& b) -> RowBuf {
+        rbuf[lane] = b.a;
+        rbuf[64 + lane] = b.b;
+        rbuf[pc] = b.c;
+        RowBuf r;
+        r.hdr = rbuf[sh];
+        r.qa = rbuf[sq];
+        r.qb = rbuf[sq + 1];
+        return r;
+    };
+
+    // x first (the encode waits only for it, loads retiring in order), then
+    // the first rows' weights.  Every thread runs one encode task (64 units
+    // x 8 tasks; threads past 512 repeat task t - 512 and store nothing): an
+    // encode under a branch would let the compiler sink the x loads into it,
+    // behind the weight loads.
+    float xv[8];
+    const int task = static_cast<int>(threadIdx.x) & 511;
+    {
+        const int tu = task >> 3;
+        const int off = (tu < units ? tu : units - 1) * 64 + 8 * (task & 7);
+        const float4 a = *reinterpret_cast<const float4*>(x + off);
+        const float4 b = *reinterpret_cast<const float4*>(x + off + 4);
+        xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
+        xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    RowRaw ring[NS];
+#pragma unroll
+    for (int s = 0; s < NS - 1 && s < RPW; s++) issue(ring[s], s);
+    __builtin_amdgcn_sched_barrier(0);
+    encode_task(xv, task, units, xq, WPG == 8 || threadIdx.x < 512);
+    __syncthreads();
+    const XU xu = read_unit(xq, u);
+    const ScaleSel ss = make_sel(u & 3);
+
+    float acc[8];
+#pragma unroll
+    for (int s = 0; s < 8; s++) acc[s] = 0.f;
+#pragma unroll
+    for (int s = 0; s < RPW; s++) {
+        if (s + NS - 1 < RPW) issue(ring[(s + NS - 1) % NS], s + NS - 1);
+        const float part = row_part(stage(ring[s % NS]), xu, ss);
+        acc[s] = valid ? part : 0.f;  // idle lanes: nothing, even from a non-finite scale
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    const float tot = reduce8(acc);
+    const int g = lane >> 3;
+    const int r = row_of_group(g);
+    if ((lane & 7) == 0 && r < RPW && row0 + r < n) y[row0 + r] = tot;
+}
+
+template <int RPW, int NS, int WPG>
+void launch(const void* w, const float* x, float* y, int n, int units, uint32_t rb, hipStream_t st) {
+    const int grid = (n + WPG * RPW - 1) / (WPG * RPW);
+    gemv_q4k_kernel<RPW, NS, WPG><<<dim3(static_cast<uint32_t>(grid)), dim3(64 * WPG), 0, st>>>(
+        static_cast<const uint8_t*>(w), x, y, n, units, rb);
+}
+
+template <int NS, int WPG>
+void launch_rpw(int rpw, const void* w, const float* x, float* y, int n, int units, uint32_t rb, hipStream_t st) {
+    switch (rpw) {
+    case 1: launch<1, NS, WPG>(w, x, y, n, units, rb, st); break;
+    case 2: launch<2, NS, WPG>(w, x, y, n, units, rb, st); break;
+    case 3: launch<3, NS, WPG>(w, x, y, n, units, rb, st); break;
+    case 4: launch<4, NS, WPG>(w, x, y, n, units, rb, st); break;
+    case 5: launch<5, NS, WPG>(w, x, y, n, units, rb, st); break;
+    case 6: launch<6, NS, WPG>(w, x, y, n, units, rb, st); break;
+    case 7: launch<7, NS, WPG>(w, x, y, n, units, rb, st); break;
+    default: launch<8, NS, WPG>(w, x, y, n, units, rb, st); break;
+    }
+}
+
+// Launch shape for n rows: 8-wave workgroups, one per CU, with RPW =
+// ceil(n / (8 CUs)) <= 8 rows per wave (14336 rows: 7); 16-wave workgroups
+// for up to 16 x 8 rows per CU (measured at 14336 x 4096: 16 waves of 4 rows,
+// 224 workgroups, ran 8.1-8.3 us against 7.4 us).  VB_GEMV_CFG="wpg,rpw"
+// overrides (wpg 8 or 16).  rpw 0: more than 8 rows per wave (the caller
+// takes the general kernel).
+struct ShortShape { int wpg, rpw; };
+
+ShortShape short_shape(int64_t n) {
+    const int64_t cus = num_cus();
+    ShortShape s{8, 0};
+    const Knobs& kb = knobs();
+    if (kb.gemv_cfg_wpg == 8 || kb.gemv_cfg_wpg == 16) {
+        s.wpg = kb.gemv_cfg_wpg;
+        s.rpw = kb.gemv_cfg_rpg >= 1 && kb.gemv_cfg_rpg <= 8 ? kb.gemv_cfg_rpg : 0;
+        if (s.rpw) return s;
+    }
+    int64_t rpw = (n + cus * s.wpg - 1) / (cus * s.wpg);
+    if (rpw > 8) {  // past 8 rows per wave: 16-wave workgroups, up to 8 rows each
+        s.wpg = 16;
+        rpw = (n + cus * s.wpg - 1) / (cus * s.wpg);
+        if (rpw > 8) {
+            s.rpw = 0;
+            return s;
+        }
+    }
+    s.rpw = static_cast<int>(rpw < 1 ? 1 : rpw);
+    return s;
+}
+
+}  // namespace
+
+int gemv_q4k_rpw(int64_t n) { return short_shape(n).rpw; }
+
+// Plain Q4_K GEMV, k <= 4096 (k % 256 == 0), at most 8 rows per wave of one
+// workgroup per CU; arguments validated by gemv_dispatch_fused.
+int gemv_q4k_short(const void* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t st) {
+    const ShortShape sh = short_shape(n);
+    const int units = static_cast<int>(k / 64);
+    if (sh.rpw == 0 || units > UNITS_MAX || k % 256 != 0 || n > INT32_MAX) {
+        set_error("vb_gemv: internal: Q4_K short-row kernel shape (n=%lld, k=%lld)", static_cast<long long>(n),
+                  static_cast<long long>(k));
+        return E_INVAL;
+    }
+    const uint32_t rb = static_cast<uint32_t>(row_bytes(TYPE_Q4_K, k));
+    const int ni = static_cast<int>(n);
+    const int ring = knobs().gemv_ring;  // NS - 1 rows in flight while computing (default 3)
+    if (sh.wpg == 8) {
+        if (ring == 1) launch_rpw<2, 8>(sh.rpw, w, x, y, ni, units, rb, st);
+        else if (ring == 2) launch_rpw<3, 8>(sh.rpw, w, x, y, ni, units, rb, st);
+        else if (ring == 4) launch_rpw<5, 8>(sh.rpw, w, x, y, ni, units, rb, st);
+        else if (ring >= 5) launch_rpw<6, 8>(sh.rpw, w, x, y, ni, units, rb, st);
+        else launch_rpw<4, 8>(sh.rpw, w, x, y, ni, units, rb, st);
+    } else {
+        if (ring == 1) launch_rpw<2, 16>(sh.rpw, w, x, y, ni, units, rb, st);
+        else if (ring == 2) launch_rpw<3, 16>(sh.rpw, w, x, y, ni, units, rb, st);
+        else launch_rpw<4, 16>(sh.rpw, w, x, y, ni, units, rb, st);
+    }
+    return check_launch("vb_gemv");
+}
+
+}  // namespace vb

@@ -30,7 +30,7 @@ Knobs read_knobs() {
     Knobs k;
     if (const char* e = std::getenv("VB_GEMV_RING")) {
         const int d = std::atoi(e);
-        if (d >= 1 && d <= 4) k.gemv_ring = d;
+        if (d >= 1 && d <= 6) k.gemv_ring = d;  // the general kernel takes 1..4
     }
     if (const char* e = std::getenv("VB_GEMV_CFG")) {
         int a = 0, b = 0;
@@ -39,7 +39,10 @@ Knobs read_knobs() {
             k.gemv_cfg_rpg = b;
         }
     }
-    if (const char* e = std::getenv("VB_GEMV_Q4K_PATH")) k.gemv_q4k_mfma = std::strcmp(e, "mfma") == 0;
+    if (const char* e = std::getenv("VB_GEMV_Q4K_PATH")) {
+        k.gemv_q4k_mfma = std::strcmp(e, "mfma") == 0;
+        k.gemv_q4k_general = std::strcmp(e, "dot") == 0;
+    }
     if (const char* e = std::getenv("VB_GEMV_MFMA_CFG")) {
         int a = 0, b = 0;
         if (std::sscanf(e, "%d,%d", &a, &b) == 2 && a >= 1 && b >= 1) {

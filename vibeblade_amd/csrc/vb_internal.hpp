@@ -8,7 +8,8 @@ namespace vb {
 // Launch-shape overrides for tuning sweeps, read from the environment once
 // per process (vb_init reads them; so does the first op call without it):
 //   VB_GEMV_RING=d, VB_GEMV_CFG="wpg,rpg"   GEMV ring depth / workgroup shape
-//   VB_GEMV_Q4K_PATH=mfma                     Q4_K GEMV on the int8-MFMA kernel
+//   VB_GEMV_Q4K_PATH=mfma|dot                 Q4_K GEMV on the int8-MFMA kernel, or on
+//                                             the general v_dot4 kernel for every shape
 //   VB_GEMV_MFMA_CFG="wpg,ks"                 that kernel's workgroup shape
 //   VB_GEMM_NF=6|8                            tiled GEMM columns per workgroup
 //   VB_SPARSE_FUSED=0, VB_SPARSE_NPW=2        sparse FFN kernel choice
@@ -17,6 +18,7 @@ struct Knobs {
     int gemv_ring = 0;
     int gemv_cfg_wpg = 0, gemv_cfg_rpg = 0;
     bool gemv_q4k_mfma = false;
+    bool gemv_q4k_general = false;
     int gemv_mfma_wpg = 0, gemv_mfma_ks = 0;
     int gemm_nf = 0;
     bool sparse_fused = true;
@@ -74,6 +76,10 @@ int gemv_dispatch_src(const void* w, const RowSrc& src, const float* x, float* y
 // for types without it (F32 / F16) and for the int8-MFMA GEMV path.
 int gemv_dispatch_fused(const void* w, const RowSrc& src, const GemvFuse& fz, const float* x, float* y,
                         int64_t n, int64_t k, int32_t type, hipStream_t st);
+// Plain Q4_K GEMV for k <= 4096 at up to 8 rows per wave (gemv_q4k.hip);
+// gemv_q4k_rpw(n) is its rows per wave, 0 when n is too large for it.
+int gemv_q4k_rpw(int64_t n);
+int gemv_q4k_short(const void* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t st);
 // Q4_K M=1 GEMV on the int8 matrix cores (gemv_q4k_mfma.hip); arguments
 // already validated by gemv_dispatch_src.
 int gemv_q4k_mfma(const void* w, const RowSrc& src, const float* x, float* y, int64_t n, int64_t k,
