@@ -45,7 +45,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 TRAFFIC_FILE = os.path.join("profiles", "q4k_gemv_14336x4096_traffic.json")
-GEMV_KERNEL = "gemv_q_kernel<12"  # the Q4_K v_dot4 GEMV instantiations
+GEMV_KERNEL = "gemv_q4k_kernel<"  # the Q4_K short-row GEMV instantiations
 CALIB_BYTES = 256 << 20            # bytes read and written by the calibration copy
 MFMA_FP16_PEAK_TFS = 2500.0  # dense fp16 MFMA, MI355X
 NCOPIES = 16

@@ -51,22 +51,49 @@ __device__ __forceinline__ const uint8_t* row_ptr(const uint8_t* w, const uint8_
     }
 }
 
-// Register budget: a 16-wave workgroup leaves 128 VGPRs per lane, enough
-// for a ring of 4 Q4_K units (9 VGPRs each) or 2 Q6_K / Q8_0 units (14 / 17);
-// deeper rings run in 8-wave workgroups (256 VGPRs).
+// Weight loads are staged.  A wave's share of a row (its k-slice: up to 64
+// units, e.g. 2304 B of Q4_K, 3360 B of Q6_K, 4352 B of Q8_0) is read as
+// contiguous 16-byte pieces, piece p of lane L at byte 16 L + 1024 p of the
+// slice, with non-temporal buffer loads (the weights are streamed once), and
+// written to a per-wave LDS buffer; the lanes then read their unit's bytes
+// from LDS with the type's unit loader.  Every load instruction covers whole
+// cache lines, where per-lane unit loads touch parts of many lines per
+// instruction (on MI355X, 14336 x 4096 Q4_K loads alone: 6.6 us per launch
+// against 7.4 us).  A slice that starts 2 bytes past a dword (Q6_K / Q3_K
+// blocks) is read from the dword below, and the LDS copy is addressed with
+// the same shift.  Loads past the slice (and whole padding rows) use a
+// buffer resource that ends there: they return zeros and read nothing (the
+// range check is per dword, measured on MI355X: a 16-byte load straddling the
+// end returns the dwords inside it).
 template <int TYPE>
-constexpr int max_d16() { return TYPE == TYPE_Q4_K ? 4 : TYPE == TYPE_Q3_K ? 1 : 2; }  // Q3_K units: 20 VGPRs
+constexpr int slice_bytes_max() {  // 64 units
+    return TYPE == TYPE_Q4_K ? 2304 : TYPE == TYPE_Q5_K ? 2816 : TYPE == TYPE_Q6_K ? 3360
+         : TYPE == TYPE_Q8_0 ? 4352 : TYPE == TYPE_Q2_K ? 1344 : TYPE == TYPE_Q3_K ? 1760
+         : TYPE == TYPE_Q4_0 ? 2304 : TYPE == TYPE_Q4_1 ? 2560 : TYPE == TYPE_Q5_0 ? 2816 : 3072;
+}
+template <int TYPE>
+constexpr int stage_pieces() {
+    constexpr int slack = (TYPE == TYPE_Q6_K || TYPE == TYPE_Q3_K) ? 2 : 0;
+    return (slice_bytes_max<TYPE>() + slack + 1023) / 1024;
+}
+constexpr int CACHE_NT = 2;  // buffer-load cache policy: non-temporal
+
+// Register budget: a 16-wave workgroup leaves 128 VGPRs per lane, enough
+// for a ring of 4 staged Q4_K row slices (3 pieces = 12 VGPRs each) or 2 of
+// the larger ones; deeper rings run in 8-wave workgroups (256 VGPRs).
+template <int TYPE>
+constexpr int max_d16() { return stage_pieces<TYPE>() <= 3 && TYPE != TYPE_Q3_K ? 4 : 2; }
 template <int TYPE, int D>
 constexpr int gemv_max_threads() { return D <= max_d16<TYPE>() ? 1024 : 512; }
 
 // One workgroup: `wpg` waves = (wpg / wpr) row groups x wpr k-slices.  Row
 // group g owns rows [row0, row0 + rpg); k-slice kw covers units
 // [kw*upw, kw*upw + upw) of each of them, lane = unit.  Rows stream through a
-// ring of D register buffers: the loads of row s + D are issued as soon as
-// row s has been computed.  The row count is padded to a multiple of D;
-// padding rows load the last real row again (cache hits) and compute nothing,
-// which keeps every load outside branches (a branch around loads makes the
-// compiler's wait counts conservative).
+// ring of D register buffers (staged slices, above): the loads of row s + D
+// are issued as soon as row s has been computed.  The row count is padded to
+// a multiple of D; padding rows issue loads of an empty resource (no memory
+// access) and compute nothing, which keeps every load outside branches (a
+// branch around loads makes the compiler's wait counts conservative).
 //
 // zbuf / zn: an int buffer the first workgroup clears (the counters of a
 // following kernel; a fill inside this launch keeps memsets out of captured
@@ -81,7 +108,7 @@ __global__ void __launch_bounds__((gemv_max_threads<TYPE, D>())) gemv_q_kernel(
         const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, const int32_t* __restrict__ gidx,
         int nsrc, const float* __restrict__ x, float* __restrict__ y, int n_bound, int64_t rb, int units,
         int slots, int upw, int wpr, int rpg, int* __restrict__ zbuf, int zn, GemvFuse fz,
-        const int32_t* __restrict__ n_dev) {
+        const int32_t* __restrict__ n_dev, uint32_t slice_stride) {
     if (zn > 0 && blockIdx.x == 0) {
         for (int i = threadIdx.x; i < zn; i += blockDim.x) zbuf[i] = 0;
     }
@@ -89,6 +116,11 @@ __global__ void __launch_bounds__((gemv_max_threads<TYPE, D>())) gemv_q_kernel(
     int n = n_bound;
     if constexpr (MODE == ROWS_PAIRS) n = 2 * active_count(n_bound / 2, n_dev);
     using Unit = typename UnitOf<TYPE>::T;
+    constexpr int P = stage_pieces<TYPE>();
+    struct Raw {
+        u32x4 p[P];
+        uint32_t shift;  // the slice's start past the dword it was read from
+    };
     extern __shared__ uint4 xq[];
     const int lane = threadIdx.x & 63;
     // wave-uniform (readfirstlane): row addressing then runs on the scalar unit
@@ -98,6 +130,9 @@ __global__ void __launch_bounds__((gemv_max_threads<TYPE, D>())) gemv_q_kernel(
     const int g = __builtin_amdgcn_readfirstlane(wave / wpr), kw = wave - g * wpr;
     const int rows_wg = groups * rpg;
     float* red = reinterpret_cast<float*>(xq + XQ_QUADS * slots);  // [wpr][rows_wg]
+    // the wave's LDS slice buffer, after red (padded to 16 bytes)
+    u32x4* stage_buf = reinterpret_cast<u32x4*>(xq + XQ_QUADS * slots + (wpr * rows_wg + 3) / 4) + wave * (P * 64);
+    const uint8_t* stage_bytes = reinterpret_cast<const uint8_t*>(stage_buf);
     const int wg_row0 = static_cast<int>(blockIdx.x) * rows_wg;
     if constexpr (MODE == ROWS_PAIRS) {
         if (wg_row0 >= n) return;  // uniform: before any load or barrier
@@ -112,18 +147,40 @@ __global__ void __launch_bounds__((gemv_max_threads<TYPE, D>())) gemv_q_kernel(
     const int ui = units - 4 + (lane & 3);
     const int uc = valid ? u : (ui < 0 ? 0 : ui);
     const auto usel = make_unit_sel<TYPE>(uc);
+    // the lane's unit inside the slice (idle lanes: one of the slice's first
+    // four, same parity as uc)
+    const int ul = valid ? lane : (lane & 3);
     const int nsteps_p = ((rpg + D - 1) / D) * D;
+    const int64_t slice_off = static_cast<int64_t>(kw) * slice_stride;
+    const int64_t slice_left = rb - slice_off;
+    const uint32_t slice_len = slice_left < slice_stride ? static_cast<uint32_t>(slice_left) : slice_stride;
 
-    auto issue = [&](Unit& v, int step) {
+    auto issue = [&](Raw& r, int step) {
+        const bool live = step < rpg && row0 + step < n;  // wave-uniform
         step = step < rpg ? step : rpg - 1;
         int row = row0 + step;
         row = row < n ? row : n - 1;
-        load_unit(row_ptr<MODE>(w, w2, gidx, nsrc, row, rb), uc, v);
+        const uint8_t* sp = row_ptr<MODE>(w, w2, gidx, nsrc, row, rb) + slice_off;
+        const uint32_t shift = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sp) & 3u);
+        // the range check is per dword: end the resource at the dword that holds
+        // the slice's last byte (at most 3 bytes past it, in the same dword)
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(sp - shift, live ? (slice_len + shift + 3u) & ~3u : 0u);
+#pragma unroll
+        for (int p = 0; p < P; p++)
+            r.p[p] = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(16 * lane + 1024 * p), 0, CACHE_NT);
+        r.shift = shift;
+    };
+    // the slice through the wave's LDS buffer; the lane's unit from there
+    // (LDS operations of one wave run in order: one buffer is enough)
+    auto stage = [&](const Raw& r, Unit& v) {
+#pragma unroll
+        for (int p = 0; p < P; p++) stage_buf[lane + 64 * p] = r.p[p];
+        load_unit(stage_bytes + r.shift, ul, v);
     };
 
     // x first, then the first D rows of weights, then the encode: the encode
     // only waits for x, and the weights are in flight meanwhile.
-    Unit v[D];
+    Raw v[D];
     const bool x_in_regs = slots * 8 <= XT_MAX * static_cast<int>(blockDim.x);
     XTasks xt;
     [[maybe_unused]] XTasks nt;  // norm weights of the same tasks (FUSE)
@@ -165,8 +222,10 @@ __global__ void __launch_bounds__((gemv_max_threads<TYPE, D>())) gemv_q_kernel(
     read_xslice(xq, slots, valid ? u : 0, xs);
     float* myred = red + kw * rows_wg + g * rpg;
 
-    auto compute = [&](const Unit& vv, int step) {
+    auto compute = [&](const Raw& rr, int step) {
         if (step >= rpg) return;  // padding step (uniform)
+        Unit vv;
+        stage(rr, vv);
         float a = unit_dot(vv, xs, usel);
         a = valid ? a : 0.f;
         const float tot = wave_sum_dpp(a);
@@ -258,31 +317,23 @@ __global__ void __launch_bounds__(256) gemv_plain_kernel(const uint8_t* __restri
     }
 }
 
+constexpr size_t kLdsBytes = 160 * 1024;  // LDS per CU (gfx950)
+
 struct GemvShape {
     int units, slots, upw, wpr, wpg, rpg, depth;
     int64_t grid;
     size_t lds;
 };
 
-// Ring depth for rpg rows per wave and wpr k-slices per row (sweeps on
-// MI355X).  A ring of 2 keeps each wave's requests spread over the weight
-// stream: when the last bytes arrive, a wave has one row left to compute,
-// not all of them (with every row in flight at once, 14336 x 4096 Q4_K ran
-// 9.6 us against 8.5-8.8 us).  One row: no ring.  Q6_K units (14-17 VGPRs)
-// and long row lists: 4 -- except for split rows (wpr > 1) with up to 8
-// rows per wave, where a ring of 2 keeps the 16-wave workgroup (and its x
-// in registers): Q6_K 4096 x 14336 ran 15.6 us against 23.2 us at 4.
+// Ring depth for rpg rows per wave (sweeps on MI355X with the staged
+// loads): two rows in flight for every type and shape, one for a single row
+// (no ring) and for Q3_K (its 20-VGPR units keep 16-wave workgroups only
+// without a ring).  Deeper rings slowed every shape: Q6_K lm_head 128256 x
+// 4096 ran 78.1 us at 2 against 86.0 us at 4, Q4_K 4096 x 14336 9.6 against
+// 10.9 us, Q8_0 4096 x 4096 5.35 against 6.5 us at 3.
 template <int TYPE>
-int ring_depth(int rpg, int wpr) {
-    if (rpg <= 1) return 1;
-    // Q3_K units (20 VGPRs) keep 16-wave workgroups only without a ring:
-    // 4096 x 14336 13.3 us against 20.1 us at a ring of 2 in 8-wave groups
-    if (TYPE == TYPE_Q3_K) return 1;
-    if (wpr > 1 && rpg <= 8) return 2;
-    // Q6_K single-slice rows, 3..8 per wave: one row in flight (14336 x 4096:
-    // 14.1 us against 19.2 us at a ring of 4)
-    if (TYPE == TYPE_Q6_K && rpg <= 8) return 1;
-    if (TYPE == TYPE_Q6_K || rpg > 8) return rpg <= 2 ? 2 : 4;
+int ring_depth(int rpg, int) {
+    if (rpg <= 1 || TYPE == TYPE_Q3_K) return 1;
     return 2;
 }
 
@@ -291,13 +342,11 @@ int gemv_max_threads_host(int depth) { return depth <= max_d16<TYPE>() ? 1024 : 
 
 // Launch geometry.  k-slices: wpr = ceil(units / 64) waves per row, upw the
 // units per slice rounded up to a multiple of 4.  Rows (rules from sweeps on
-// MI355X, 256 CUs): single-slice rows run in 8-wave workgroups.  When 3..8
-// rows per wave at one workgroup per CU covers the rows, that is the shape
-// (14336 rows: 7 rows per wave, 256 workgroups; best for every type, by
-// 4-26 % over 4 rows per wave at two workgroups per CU); otherwise up to 4
-// rows per wave at two workgroups per CU, and beyond that one workgroup per
-// CU again (Q6_K lm_head, 128256 rows: 63 rows per wave).  Multi-slice rows (k > 4096) use
-// 16-wave workgroups.  VB_GEMV_CFG="wpg,rpg" and VB_GEMV_RING=d override
+// MI355X, 256 CUs): single-slice rows run in one 8-wave workgroup per CU
+// with ceil(n / (8 CUs)) rows per wave (14336 rows: 7; Q6_K lm_head, 128256
+// rows: 63; Q8_0 4096 rows: 2, 5.35 us against 5.8 us at one row per wave
+// in two workgroups per CU).  Multi-slice rows (k > 4096) use 16-wave
+// workgroups.  VB_GEMV_CFG="wpg,rpg" and VB_GEMV_RING=d override
 // (tuning sweeps; Knobs).
 template <int TYPE>
 GemvShape gemv_shape(int64_t n, int units, bool even_rows = false) {
@@ -306,15 +355,10 @@ GemvShape gemv_shape(int64_t n, int units, bool even_rows = false) {
     s.wpr = (units + 63) / 64;
     s.upw = ((units + s.wpr - 1) / s.wpr + 3) & ~3;
     s.slots = (((s.wpr - 1) * s.upw + 64) + 7) & ~7;
-    if (s.wpr == 1) {
+    if (s.wpr == 1) {  // one 8-wave workgroup per CU, every row count
         s.wpg = 8;
         const int64_t cus = num_cus();
-        const int64_t per2 = (n + 2 * cus * 8 - 1) / (2 * cus * 8);
-        const int64_t per1 = (n + cus * 8 - 1) / (cus * 8);
-        if (per1 >= 3 && per1 <= 8)  // every type (Q4_K first; the others measured since)
-            s.rpg = static_cast<int>(per1);
-        else
-            s.rpg = static_cast<int>(per2 <= 4 ? per2 : per1);
+        s.rpg = static_cast<int>((n + cus * 8 - 1) / (cus * 8));
     } else {
         s.wpg = s.wpr <= 4 ? 16 / s.wpr * s.wpr : s.wpr;
         if (s.wpg > 16) s.wpg = s.wpr;  // > 4096 * 16 elements: one row group per workgroup
@@ -349,9 +393,17 @@ GemvShape gemv_shape(int64_t n, int units, bool even_rows = false) {
         if (s.wpg < s.wpr) s.wpg = s.wpr;
     }
     s.depth = depth_of(s.rpg);
-    const int64_t rows_wg = static_cast<int64_t>(s.wpg / s.wpr) * s.rpg;
+    int64_t rows_wg = static_cast<int64_t>(s.wpg / s.wpr) * s.rpg;
+    auto lds_of = [&](int wpg) {
+        const int64_t rw = static_cast<int64_t>(wpg / s.wpr) * s.rpg;
+        return static_cast<size_t>(s.slots) * XQ_QUADS * sizeof(uint4) + ((rw * s.wpr + 3) / 4) * sizeof(uint4) +
+               static_cast<size_t>(wpg) * stage_pieces<TYPE>() * 1024;
+    };
+    // the per-wave slice buffers must fit the CU's LDS with the encoding
+    while (lds_of(s.wpg) > kLdsBytes && s.wpg > s.wpr) s.wpg -= s.wpr;
+    rows_wg = static_cast<int64_t>(s.wpg / s.wpr) * s.rpg;
     s.grid = (n + rows_wg - 1) / rows_wg;
-    s.lds = static_cast<size_t>(s.slots) * XQ_QUADS * sizeof(uint4) + rows_wg * s.wpr * sizeof(float);
+    s.lds = lds_of(s.wpg);
     return s;
 }
 
@@ -367,10 +419,11 @@ int launch_gemv_d(const GemvShape& s, const void* w, const RowSrc& src, const Ge
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     const uint8_t* w2 = static_cast<const uint8_t*>(src.w2);
     const int ni = static_cast<int>(n), nsrc = static_cast<int>(src.nsrc);
+    const uint32_t stride = static_cast<uint32_t>(row_bytes(TYPE, 64 * static_cast<int64_t>(s.upw)));
 #define VB_GEMV_LAUNCH(MODE, FUSE)                                                                      \
     gemv_q_kernel<TYPE, D, MODE, FUSE><<<g, b, s.lds, st>>>(wb, w2, src.gidx, nsrc, x, y, ni, rb, s.units, \
                                                             s.slots, s.upw, s.wpr, s.rpg, src.zbuf, src.zn, fz,  \
-                                                            src.n_dev)
+                                                            src.n_dev, stride)
     if (fz.any()) {
         if (src.dense_pairs)
             VB_GEMV_LAUNCH(ROWS_DPAIRS, true);
@@ -394,7 +447,7 @@ int launch_gemv_q(const void* w, const RowSrc& src, const GemvFuse& fz, const fl
                   int64_t k, int64_t rb, hipStream_t st) {
     const int units = static_cast<int>(k / 64);
     const GemvShape s = gemv_shape<TYPE>(n, units, fz.act >= 0);
-    if (s.slots > kMaxSlots) {
+    if (s.slots > kMaxSlots || s.lds > kLdsBytes) {
         set_error("vb_gemv: k=%lld exceeds the supported maximum of 32768", static_cast<long long>(k));
         return E_UNSUPPORTED;
     }

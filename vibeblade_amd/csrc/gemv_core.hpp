@@ -451,10 +451,27 @@ __device__ __forceinline__ void load_x_task(const float* __restrict__ x, int uni
     v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
+// Value of v in lane i ^ 1 (M = 1) or i ^ 2 (M = 2) of this lane's quad
+// (DPP quad_perm): the run reductions stay in registers, no LDS round trip.
+template <int M>
+__device__ __forceinline__ float quad_xor(float v) {
+    constexpr int CTRL = M == 1 ? 0xB1 : 0x4E;  // [1,0,3,2] / [2,3,0,1]
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int M>
+__device__ __forceinline__ int quad_xor(int v) {
+    constexpr int CTRL = M == 1 ? 0xB1 : 0x4E;
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+// `store` false: the task only takes part in the run reductions of its
+// neighbours (every lane of the wave must run them); nothing is written.
 template <int TYPE>
-__device__ __forceinline__ void encode_x_task(int task, int units, int slots, const float* vin, uint4* xq) {
+__device__ __forceinline__ void encode_x_task(int task, int units, int slots, const float* vin, uint4* xq,
+                                              bool store = true) {
     constexpr int RUNLEN = (TYPE == TYPE_Q6_K || TYPE == TYPE_Q2_K || TYPE == TYPE_Q3_K) ? 16 : 32;
     constexpr int TPR = RUNLEN / 8;
+    static_assert(TPR == 2 || TPR == 4, "runs of 2 or 4 tasks (one quad)");
     const int u = task >> 3, p = task & 7;
     float v[8];
 #pragma unroll
@@ -465,10 +482,11 @@ __device__ __forceinline__ void encode_x_task(int task, int units, int slots, co
         amax = fmaxf(amax, fabsf(v[i]));
         sum += v[i];
     }
-#pragma unroll
-    for (int m = 1; m < TPR; m <<= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, m, 64));
-        sum += __shfl_xor(sum, m, 64);
+    amax = fmaxf(amax, quad_xor<1>(amax));
+    sum += quad_xor<1>(sum);
+    if constexpr (TPR == 4) {
+        amax = fmaxf(amax, quad_xor<2>(amax));
+        sum += quad_xor<2>(sum);
     }
     const float inv = amax > 0.f ? static_cast<float>(X16_MAX) / amax : 0.f;
     uint32_t ph[2] = {0, 0}, pl[2] = {0, 0};
@@ -483,8 +501,9 @@ __device__ __forceinline__ void encode_x_task(int task, int units, int slots, co
         ph[i >> 2] |= static_cast<uint32_t>(hi & 255) << (8 * (i & 3));
         pl[i >> 2] |= static_cast<uint32_t>(lo & 255) << (8 * (i & 3));
     }
-#pragma unroll
-    for (int m = 1; m < TPR; m <<= 1) isum += __shfl_xor(isum, m, 64);
+    isum += quad_xor<1>(isum);
+    if constexpr (TPR == 4) isum += quad_xor<2>(isum);
+    if (!store) return;
     uint4* base = xq + u;
     reinterpret_cast<uint2*>(&base[(p >> 1) * slots])[p & 1] = make_uint2(ph[0], ph[1]);
     reinterpret_cast<uint2*>(&base[(4 + (p >> 1)) * slots])[p & 1] = make_uint2(pl[0], pl[1]);
@@ -498,7 +517,10 @@ __device__ __forceinline__ void encode_x_task(int task, int units, int slots, co
 
 // Register path: at most XT_MAX tasks per thread.  The task count (8 per
 // slot, slots a multiple of 8) and the thread count are multiples of 64, so
-// each wave's shuffles see all 64 lanes active.
+// each wave's shuffles see all 64 lanes active.  No branch around a task's
+// encode (threads past the task count redo the last task and store
+// nothing): an encode under a branch makes the compiler wait for every load
+// in flight, the weight loads issued after x included.
 template <int TYPE>
 __device__ __forceinline__ void prefetch_x(const float* __restrict__ x, int units, int slots, XTasks& t) {
     const int ntasks = slots * 8;
@@ -515,7 +537,7 @@ __device__ __forceinline__ void encode_x_regs(int units, int slots, const XTasks
 #pragma unroll
     for (int i = 0; i < XT_MAX; i++) {
         const int task = threadIdx.x + i * blockDim.x;
-        if (task < ntasks) encode_x_task<TYPE>(task, units, slots, t.v[i], xq);
+        encode_x_task<TYPE>(task < ntasks ? task : ntasks - 1, units, slots, t.v[i], xq, task < ntasks);
     }
 }
 
