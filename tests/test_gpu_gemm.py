@@ -109,3 +109,33 @@ def test_config_shapes(m):
     y = gemm(qt, xh).cpu().numpy()
     want = ref_gemm(qt, xh.float().cpu().numpy())
     assert O.rel_l2(y, want) <= TOL
+
+
+@pytest.mark.parametrize("cfg", ["4,2,8", "4,2,6", "2,4,8", "2,2,4", "2,2,6", "1,4,4", "1,4,8", "1,2,4"])
+def test_tiled_tile_configs(knob, cfg):
+    """Every tile configuration (VB_GEMM_TILE=wm,wn,nf), ragged M and N edges,
+    fp16 and fp32 X."""
+    knob("VB_GEMM_TILE", cfg)
+    qt, x = make(200, 333, 1280, 23)
+    for dtype in (torch.float16, torch.float32):
+        xt = torch.from_numpy(x).to("cuda", dtype)
+        y = gemm(qt, xt, variant=GEMM_TILED).cpu().numpy()
+        want = O.gemm(qt.to_numpy_bytes(), xt.float().cpu().numpy(), 333, 1280, qt.qtype)
+        assert O.rel_l2(y, want) <= TOL, (cfg, dtype)
+        assert np.all(np.abs(y).sum(axis=1) > 0)
+
+
+@pytest.mark.parametrize("m", [17, 64, 100, 128, 129, 256])
+def test_mid_m_at_config_shape(m):
+    """The mid-M sizes of speculative verify and chunked prefill at
+    N = 14336, K = 4096 (fp16 X with 0.1 % outliers x20), on the default tile
+    for each M."""
+    n, k = 14336, 4096
+    gen = torch.Generator(device="cuda").manual_seed(m)
+    qt = QTensor.quantize(torch.randn((n, k), generator=gen, device="cuda") * 0.02, Q4K)
+    x = torch.randn((m, k), generator=gen, device="cuda")
+    x[torch.rand((m, k), generator=gen, device="cuda") < 0.001] *= 20.0
+    xh = x.half()
+    y = gemm(qt, xh).cpu().numpy()
+    want = ref_gemm(qt, xh.float().cpu().numpy())
+    assert O.rel_l2(y, want) <= TOL

@@ -24,10 +24,12 @@ constexpr int X_F16 = 1;
 
 // ---- tiled: M > 16 ------------------------------------------------------------
 //
-// Workgroup tile: 256 rows of X x BN = 16 * NF weight rows (output columns),
-// 4 x WN waves; wave (wm, wn) owns X rows [64 wm, +64) x fragment columns
-// [wn * NF / WN, +NF / WN): 4 x NF / WN accumulator fragments, two waves per
-// SIMD with WN = 2.  k advances one Q4_K chunk (64 elements) per step, and
+// Workgroup tile: TB_M = 64 WM rows of X x BN = 16 * NF weight rows (output
+// columns), WM x WN waves; wave (wm, wn) owns X rows [64 wm, +64) x fragment
+// columns [wn * NF / WN, +NF / WN): 4 x NF / WN accumulator fragments.  Large
+// M runs 256-row tiles (WM = 4, WN = 2: two waves per SIMD); small M narrower
+// tiles so the grid still covers the CUs (see tiled_cfg).  k advances one
+// Q4_K chunk (64 elements) per step, and
 // both operands of a step are staged in LDS (double-buffered):
 //  * B: the workgroup dequantizes the BN x 64 weight tile once into fp16 B
 //    fragments (natural k order); each of the 4 * BN "units" (8 qs bytes of
@@ -39,8 +41,7 @@ constexpr int X_F16 = 1;
 //    the fragments directly, and no duplicate loads across wave columns) two
 //    steps ahead, converted to fp16 and stored in swizzled 128-byte rows (below);
 //    the waves read their A fragments with ds_read_b128.
-// One barrier per step.  The grid is ceil(N / BN) x ceil(M / 256).
-constexpr int TB_M = 256;
+// One barrier per step.  The grid is ceil(N / BN) x ceil(M / TB_M).
 constexpr int XS_ROW = 64;  // halves per LDS row of X (swizzled, no padding)
 // weight prefetch distance (steps; K / 64 is a multiple of 4)
 constexpr int PD = 4;
@@ -53,11 +54,12 @@ constexpr int PD = 4;
 // slower; the swizzle reads 0.
 __device__ __forceinline__ int xswz(int row) { return (row >> 1) & 7; }
 
-template <int XT, int NF, int WN>
-__global__ void __launch_bounds__(256 * WN) gemm_q4k_tiled(const uint8_t* __restrict__ w,
-                                                           const void* __restrict__ X, float* __restrict__ Y,
-                                                           int M, int N, int K, int64_t rb) {
-    constexpr int NT = 256 * WN;            // threads
+template <int XT, int NF, int WM, int WN>
+__global__ void __launch_bounds__(64 * WM * WN) gemm_q4k_tiled(const uint8_t* __restrict__ w,
+                                                               const void* __restrict__ X, float* __restrict__ Y,
+                                                               int M, int N, int K, int64_t rb) {
+    constexpr int TB_M = 64 * WM;           // X rows per workgroup
+    constexpr int NT = 64 * WM * WN;        // threads
     constexpr int NU = 4 * 16 * NF;         // dequant units per step
     constexpr int UPT = (NU + NT - 1) / NT;  // units per thread
     constexpr int NW = NF / WN;             // B fragments per wave
@@ -256,12 +258,25 @@ __global__ void __launch_bounds__(256 * WN) gemm_q4k_tiled(const uint8_t* __rest
     }
 }
 
-// Columns per workgroup (NF fragments of 16) balancing the grid over the
-// CUs; VB_GEMM_NF overrides (6 or 8).
-int tiled_nf(int64_t M, int64_t N) {
-    if (knobs().gemm_nf) return knobs().gemm_nf;
+// Tile configuration for M rows (sweeps on MI355X at N = 14336, K = 4096,
+// against the 256 x 128 tile alone): M <= 64: 64-row tiles of 64 columns,
+// 4 waves (M = 17: 27.0 us against 59.8 us); 64 < M <= 128: 128 x 64, 4
+// waves (M = 100: 35.2 us against 60.8); 128 < M <= 256: 128 x 128, 8 waves
+// (M = 256: 48.4 against 63.4); above, 256-row tiles of 128 or 96 columns
+// (NF 8 / 6, whichever balances the grid over the CUs; M = 512: 70-72 us).  VB_GEMM_NF (6, 8) overrides NF of the large
+// tiles; VB_GEMM_TILE="wm,wn,nf" (wm 1, 2, 4; wn 2, 4; nf 4, 6, 8 with wn
+// dividing nf) any configuration.
+struct TileCfg { int wm, wn, nf; };
+
+TileCfg tiled_cfg(int64_t M, int64_t N) {
+    const Knobs& kb = knobs();
+    if (kb.gemm_tile_wm) return TileCfg{kb.gemm_tile_wm, kb.gemm_tile_wn, kb.gemm_tile_nf};
+    if (M <= 64) return TileCfg{1, 4, 4};
+    if (M <= 128) return TileCfg{2, 2, 4};
+    if (M <= 256) return TileCfg{2, 4, 8};
+    if (kb.gemm_nf) return TileCfg{4, 2, kb.gemm_nf};
     const int64_t kCUs = num_cus();
-    const int64_t mt = (M + TB_M - 1) / TB_M;
+    const int64_t mt = (M + 255) / 256;
     int best = 8;
     int64_t best_cost = -1;
     for (int nf = 8; nf >= 6; nf -= 2) {
@@ -272,17 +287,39 @@ int tiled_nf(int64_t M, int64_t N) {
             best = nf;
         }
     }
-    return best;
+    return TileCfg{4, 2, best};
+}
+
+template <int XT, int NF, int WM, int WN>
+void launch_tiled_cfg(const uint8_t* w, const void* X, float* Y, int M, int N, int K, int64_t rb, hipStream_t st) {
+    const dim3 grid(static_cast<uint32_t>((N + 16 * NF - 1) / (16 * NF)),
+                    static_cast<uint32_t>((M + 64 * WM - 1) / (64 * WM)));
+    gemm_q4k_tiled<XT, NF, WM, WN><<<grid, dim3(64 * WM * WN), 0, st>>>(w, X, Y, M, N, K, rb);
 }
 
 template <int XT>
-void launch_tiled(int nf, const uint8_t* w, const void* X, float* Y, int M, int N, int K, int64_t rb,
-                  hipStream_t st) {
-    const dim3 grid(static_cast<uint32_t>((N + 16 * nf - 1) / (16 * nf)), static_cast<uint32_t>((M + TB_M - 1) / TB_M));
-    switch (nf) {
-    case 6: gemm_q4k_tiled<XT, 6, 2><<<grid, dim3(512), 0, st>>>(w, X, Y, M, N, K, rb); break;
-    default: gemm_q4k_tiled<XT, 8, 2><<<grid, dim3(512), 0, st>>>(w, X, Y, M, N, K, rb); break;
+int launch_tiled(const TileCfg& c, const uint8_t* w, const void* X, float* Y, int M, int N, int K, int64_t rb,
+                 hipStream_t st) {
+#define VB_TILE(WM_, WN_, NF_)                                                   \
+    if (c.wm == WM_ && c.wn == WN_ && c.nf == NF_) {                            \
+        launch_tiled_cfg<XT, NF_, WM_, WN_>(w, X, Y, M, N, K, rb, st);          \
+        return OK;                                                               \
     }
+    VB_TILE(4, 2, 8)
+    VB_TILE(4, 2, 6)
+    VB_TILE(4, 2, 4)
+    VB_TILE(2, 4, 8)
+    VB_TILE(2, 4, 4)
+    VB_TILE(2, 2, 8)
+    VB_TILE(2, 2, 6)
+    VB_TILE(2, 2, 4)
+    VB_TILE(1, 4, 8)
+    VB_TILE(1, 4, 4)
+    VB_TILE(1, 2, 4)
+    VB_TILE(1, 2, 6)
+#undef VB_TILE
+    set_error("vb_gemm: no tiled kernel for wm=%d wn=%d nf=%d", c.wm, c.wn, c.nf);
+    return E_INVAL;
 }
 
 }  // namespace
@@ -320,18 +357,18 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
         return E_INVAL;
     }
     const int64_t xbytes = M * K * (x_dtype == X_F16 ? 2 : 4);
-    if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX || (M + TB_M - 1) / TB_M > 65535 ||
+    if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX || (M + 63) / 64 > 65535 ||
         N * rb >= (int64_t(1) << 32) || xbytes >= (int64_t(1) << 32)) {
         set_error("vb_gemm: shape too large (M=%lld N=%lld K=%lld)", static_cast<long long>(M),
                   static_cast<long long>(N), static_cast<long long>(K));
         return E_INVAL;
     }
-    const int nf = tiled_nf(M, N);
+    const TileCfg cfg = tiled_cfg(M, N);
     const uint8_t* wb = static_cast<const uint8_t*>(w);
-    if (x_dtype == X_F16)
-        launch_tiled<X_F16>(nf, wb, X, Y, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), rb, st);
-    else
-        launch_tiled<X_F32>(nf, wb, X, Y, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), rb, st);
+    const int rc = x_dtype == X_F16
+        ? launch_tiled<X_F16>(cfg, wb, X, Y, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), rb, st)
+        : launch_tiled<X_F32>(cfg, wb, X, Y, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), rb, st);
+    if (rc != OK) return rc;
     return check_launch("vb_gemm");
 }
 

@@ -54,6 +54,15 @@ Knobs read_knobs() {
         const int v = std::atoi(e);
         if (v == 6 || v == 8) k.gemm_nf = v;
     }
+    if (const char* e = std::getenv("VB_GEMM_TILE")) {
+        int a = 0, b = 0, c = 0;
+        if (std::sscanf(e, "%d,%d,%d", &a, &b, &c) == 3 && (a == 1 || a == 2 || a == 4) && (b == 2 || b == 4) &&
+            (c == 4 || c == 6 || c == 8) && c % b == 0) {
+            k.gemm_tile_wm = a;
+            k.gemm_tile_wn = b;
+            k.gemm_tile_nf = c;
+        }
+    }
     if (const char* e = std::getenv("VB_SPARSE_FUSED")) k.sparse_fused = e[0] != '0';
     if (const char* e = std::getenv("VB_SPARSE_NPW")) k.sparse_npw = e[0] == '2' ? 2 : 0;
     return k;

@@ -12,6 +12,7 @@ namespace vb {
 //                                             the general v_dot4 kernel for every shape
 //   VB_GEMV_MFMA_CFG="wpg,ks"                 that kernel's workgroup shape
 //   VB_GEMM_NF=6|8                            tiled GEMM columns per workgroup
+//   VB_GEMM_TILE="wm,wn,nf"                   tiled GEMM tile configuration
 //   VB_SPARSE_FUSED=0, VB_SPARSE_NPW=2        sparse FFN kernel choice
 // Zero / false means "no override".
 struct Knobs {
@@ -21,6 +22,7 @@ struct Knobs {
     bool gemv_q4k_general = false;
     int gemv_mfma_wpg = 0, gemv_mfma_ks = 0;
     int gemm_nf = 0;
+    int gemm_tile_wm = 0, gemm_tile_wn = 0, gemm_tile_nf = 0;
     bool sparse_fused = true;
     int sparse_npw = 0;
 };
