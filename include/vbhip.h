@@ -120,7 +120,8 @@ int vb_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k,
  * Y[m, n] = sum_k X[m, k] * W[n, k]; X row-major (m x k) in fp32
  * (x_dtype = 0) or fp16 (x_dtype = 1), Y fp32 row-major (m x n).  Products
  * run on v_mfma_f32_16x16x32_f16 with W dequantized to fp16 in registers and
- * fp32 accumulation.  variant: 0 = choose, 1 = skinny (m <= 16), 2 = tiled.
+ * fp32 accumulation.  variant: 0 = choose, 1 = skinny (m <= 16), 2 = tiled,
+ * 3 = role-split (fp16 X only; chosen for 257 <= m <= 768 with fp16 X).
  * Replaces the reference's batched path, a per-token loop of gemv_dequant
  * (cpp/src/fast_model.cpp:644-669, :905-960), and cuda::gemm_f32
  * (cpp/include/cuda_kernels.h, cpp/src/cuda_kernels.cu:184-212).

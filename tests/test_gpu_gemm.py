@@ -9,7 +9,7 @@ import torch
 
 import oracle as O
 from vibeblade_amd import ggml
-from vibeblade_amd.tensor import QTensor, gemm, GEMM_SKINNY, GEMM_TILED
+from vibeblade_amd.tensor import QTensor, gemm, GEMM_SKINNY, GEMM_TILED, GEMM_SPLIT
 
 pytestmark = pytest.mark.gpu
 
@@ -139,3 +139,33 @@ def test_mid_m_at_config_shape(m):
     y = gemm(qt, xh).cpu().numpy()
     want = ref_gemm(qt, xh.float().cpu().numpy())
     assert O.rel_l2(y, want) <= TOL
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 16, 256), (257, 113, 512), (300, 257, 1024), (512, 224, 4096),
+                                   (600, 50, 768), (1000, 333, 256)])
+def test_split(m, n, k):
+    """The role-split kernel (variant 3, fp16 X): ragged M (rows past M) and
+    N (column tiles of 112), one to several M-tiles of 256 rows."""
+    qt, x = make(m, n, k, m * 5 + n)
+    xt = torch.from_numpy(x).to("cuda", torch.float16)
+    y = gemm(qt, xt, variant=GEMM_SPLIT).cpu().numpy()
+    want = ref_gemm(qt, xt.float().cpu().numpy())
+    assert y.shape == (m, n)
+    assert O.rel_l2(y, want) <= TOL
+    assert np.all(np.abs(y).sum(axis=1) > 0)
+
+
+def test_split_matches_tiled():
+    """Same dequantized fragments, same MFMAs in the same order per output:
+    the role-split and tiled kernels agree bit for bit."""
+    qt, x = make(520, 250, 2048, 31)
+    xt = torch.from_numpy(x).to("cuda", torch.float16)
+    a = gemm(qt, xt, variant=GEMM_TILED).cpu().numpy()
+    b = gemm(qt, xt, variant=GEMM_SPLIT).cpu().numpy()
+    assert np.array_equal(a, b)
+
+
+def test_split_rejects_fp32_x():
+    qt, x = make(300, 16, 256, 2)
+    with pytest.raises(ValueError):
+        gemm(qt, torch.from_numpy(x).to("cuda", torch.float32), variant=GEMM_SPLIT)

@@ -352,8 +352,12 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
         }
         return gemm_q4k_skinny(w, X, x_dtype, Y, M, N, K, st);
     }
-    if (variant != 0 && variant != 2) {
+    if (variant < 0 || variant > 3) {
         set_error("vb_gemm: unknown variant %d", variant);
+        return E_INVAL;
+    }
+    if (variant == 3 && x_dtype != X_F16) {
+        set_error("vb_gemm: variant 3 (role-split) takes fp16 X");
         return E_INVAL;
     }
     const int64_t xbytes = M * K * (x_dtype == X_F16 ? 2 : 4);
@@ -362,6 +366,14 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
         set_error("vb_gemm: shape too large (M=%lld N=%lld K=%lld)", static_cast<long long>(M),
                   static_cast<long long>(N), static_cast<long long>(K));
         return E_INVAL;
+    }
+    // 256 < M <= 768, fp16 X: the role-split kernel (gemm_split.hip; at
+    // N = 14336, K = 4096 on MI355X 67.9 / 72.0 us at M = 384 / 512 against
+    // 71.0 / 74.8 tiled, behind at M = 256 and 1024)
+    const int smin = knobs().gemm_split_min_m >= 0 ? knobs().gemm_split_min_m : 257;
+    const bool split_range = smin > 0 && M >= smin && M <= 768;
+    if (variant == 3 || (variant == 0 && x_dtype == X_F16 && split_range)) {
+        return gemm_q4k_split(w, X, Y, M, N, K, st);
     }
     const TileCfg cfg = tiled_cfg(M, N);
     const uint8_t* wb = static_cast<const uint8_t*>(w);

@@ -63,6 +63,10 @@ Knobs read_knobs() {
             k.gemm_tile_nf = c;
         }
     }
+    if (const char* e = std::getenv("VB_GEMM_SPLIT_MIN_M")) {
+        const int v = std::atoi(e);
+        if (v >= 0) k.gemm_split_min_m = v;
+    }
     if (const char* e = std::getenv("VB_SPARSE_FUSED")) k.sparse_fused = e[0] != '0';
     if (const char* e = std::getenv("VB_SPARSE_NPW")) k.sparse_npw = e[0] == '2' ? 2 : 0;
     return k;

@@ -13,6 +13,7 @@ namespace vb {
 //   VB_GEMV_MFMA_CFG="wpg,ks"                 that kernel's workgroup shape
 //   VB_GEMM_NF=6|8                            tiled GEMM columns per workgroup
 //   VB_GEMM_TILE="wm,wn,nf"                   tiled GEMM tile configuration
+//   VB_GEMM_SPLIT_MIN_M=m                     smallest M (up to 768) on the role-split GEMM (0: never)
 //   VB_SPARSE_FUSED=0, VB_SPARSE_NPW=2        sparse FFN kernel choice
 // Zero / false means "no override".
 struct Knobs {
@@ -23,6 +24,7 @@ struct Knobs {
     int gemv_mfma_wpg = 0, gemv_mfma_ks = 0;
     int gemm_nf = 0;
     int gemm_tile_wm = 0, gemm_tile_wn = 0, gemm_tile_nf = 0;
+    int gemm_split_min_m = -1;  // smallest M on the role-split kernel (-1: default)
     bool sparse_fused = true;
     int sparse_npw = 0;
 };
@@ -89,6 +91,9 @@ int gemv_q4k_mfma(const void* w, const RowSrc& src, const float* x, float* y, in
 // M <= 16 Q4_K GEMM (gemm_skinny.hip); type, M, alignment already validated.
 int gemm_q4k_skinny(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, int64_t N, int64_t K,
                     hipStream_t st);
+// Role-split Q4_K GEMM, fp16 X (gemm_split.hip); type, alignment and the
+// 32-bit offset bounds already validated.
+int gemm_q4k_split(const void* w, const void* X, float* Y, int64_t M, int64_t N, int64_t K, hipStream_t st);
 int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, int64_t N, int64_t K,
                   int32_t type, int32_t variant, hipStream_t st);
 

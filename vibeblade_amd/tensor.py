@@ -148,7 +148,7 @@ def gemv(w: QTensor, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.
 
 X_F32 = 0
 X_F16 = 1
-GEMM_AUTO, GEMM_SKINNY, GEMM_TILED = 0, 1, 2
+GEMM_AUTO, GEMM_SKINNY, GEMM_TILED, GEMM_SPLIT = 0, 1, 2, 3
 
 
 def gemm(w: QTensor, x: torch.Tensor, out: torch.Tensor | None = None,
