@@ -800,6 +800,21 @@ def run_extra(which, args):
               "launches": tm.launches, "TFLOP/s": round(tfs, 2), "frac_mfma_fp16": round(tfs / MFMA_FP16_PEAK_TFS, 4),
               "GB/s": gbs, "frac_hbm": fr, "rel_l2": e3})
         torch.cuda.empty_cache()
+    if "gemm" in which:
+        # Q6_K / Q8_0 weights (the down projection of a Q4_K_M / Q8_0 file)
+        from vibeblade_amd import ggml
+        for qtype, name in ((ggml.GGML_TYPE_Q6_K, "Q6_K"), (ggml.GGML_TYPE_Q8_0, "Q8_0")):
+            n, k = 4096, 14336
+            wb = n * ggml.row_bytes(qtype, k)
+            for m in (8, 512):
+                tm, e3 = time_gemm(m, n, k, 20, 2, qtype=qtype)
+                tfs = 2.0 * m * n * k / (tm.ms * 1e-3) / 1e12
+                gbs, fr = frac(wb + 2 * m * k + 4 * m * n, tm)
+                emit({"workload": f"3: {name} GEMM M={m} N={n} K={k} fp16 X", "us_per_call": tm.us(),
+                      "launches": tm.launches, "TFLOP/s": round(tfs, 2),
+                      "frac_mfma_fp16": round(tfs / MFMA_FP16_PEAK_TFS, 4), "GB/s": gbs, "frac_hbm": fr,
+                      "rel_l2": e3})
+                torch.cuda.empty_cache()
     if "cpu" in which and not args.no_cpu_baseline:
         for row in cpu_table(min(args.cpu_seconds, 3.0)):
             row["cores"] = 1

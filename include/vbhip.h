@@ -123,9 +123,11 @@ int vb_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k,
  * fp32 accumulation.  variant: 0 = choose, 1 = skinny (m <= 16), 2 = tiled,
  * 3 = role-split (fp16 X only; chosen for 257 <= m <= 768 with fp16 X).
  * Replaces the reference's batched path, a per-token loop of gemv_dequant
- * (cpp/src/fast_model.cpp:644-669, :905-960), and cuda::gemm_f32
+ * (cpp/src/fast_model.cpp:644-669, :905-960) over rows decoded by
+ * dequantize_row (cpp/src/dequant.cpp:407-425), and cuda::gemm_f32
  * (cpp/include/cuda_kernels.h, cpp/src/cuda_kernels.cu:184-212).
- * Weight type: Q4_K. */
+ * Weight types: Q4_K (variants 0-3), Q6_K and Q8_0 (variant 0; Q8_0 needs
+ * k % 128 == 0).  W and x 16-byte aligned. */
 int vb_gemm(const void* w, const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n,
             int64_t k, int32_t ggml_type, int32_t variant, void* stream);
 

@@ -9,12 +9,15 @@ import torch
 
 import oracle as O
 from vibeblade_amd import ggml
+from vibeblade_amd._lib import VBError
 from vibeblade_amd.tensor import QTensor, gemm, GEMM_SKINNY, GEMM_TILED, GEMM_SPLIT
 
 pytestmark = pytest.mark.gpu
 
 TOL = 5e-3
 Q4K = ggml.GGML_TYPE_Q4_K
+Q6K = ggml.GGML_TYPE_Q6_K
+Q80 = ggml.GGML_TYPE_Q8_0
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -29,14 +32,14 @@ def ref_gemm(qt, x):
     return x.astype(np.float64) @ w.T
 
 
-def make(m, n, k, seed, outliers=True):
+def make(m, n, k, seed, outliers=True, qtype=Q4K):
     rng = np.random.default_rng(seed)
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
     x = rng.standard_normal((m, k)).astype(np.float32)
     if outliers:
         mask = rng.random((m, k)) < 0.001
         x[mask] *= 20.0
-    return QTensor.quantize(w, Q4K), x
+    return QTensor.quantize(w, qtype), x
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
@@ -169,3 +172,86 @@ def test_split_rejects_fp32_x():
     qt, x = make(300, 16, 256, 2)
     with pytest.raises(ValueError):
         gemm(qt, torch.from_numpy(x).to("cuda", torch.float32), variant=GEMM_SPLIT)
+
+
+# ---- Q6_K and Q8_0 weights (gemm_kq.hip) ----------------------------------
+
+@pytest.mark.parametrize("qtype", [Q6K, Q80])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("m,n,k", [(1, 16, 256), (8, 300, 1024), (16, 33, 768), (17, 100, 512),
+                                   (40, 50, 256), (64, 257, 1280), (65, 70, 512), (300, 130, 1024)])
+def test_kq_types(qtype, dtype, m, n, k):
+    """Q6_K and Q8_0 weights at every M tile (16 rows up to M = 16, one tile
+    of 32 / 48 / 64 rows up to 64, 64- or 32-row tiles above), ragged M and N,
+    K split over the 8 waves unevenly (k / 128 steps not a multiple of 8),
+    fp16 and fp32 X."""
+    qt, x = make(m, n, k, m * 11 + n + qtype, qtype=qtype)
+    xt = torch.from_numpy(x).to("cuda", dtype)
+    y = gemm(qt, xt).cpu().numpy()
+    want = ref_gemm(qt, xt.float().cpu().numpy())
+    assert y.shape == (m, n)
+    assert O.rel_l2(y, want) <= TOL, (qtype, dtype, m, n, k)
+    assert np.all(np.abs(y).sum(axis=1) > 0)
+
+
+@pytest.mark.parametrize("qtype", [Q6K, Q80])
+@pytest.mark.parametrize("n", [8192, 16400])
+def test_kq_wide(qtype, n):
+    """Wide weights at small M: two and four 16-row column groups per
+    workgroup."""
+    qt, x = make(5, n, 256, n + qtype, qtype=qtype)
+    xt = torch.from_numpy(x).to("cuda", torch.float16)
+    y = gemm(qt, xt).cpu().numpy()
+    want = ref_gemm(qt, xt.float().cpu().numpy())
+    assert O.rel_l2(y, want) <= TOL
+
+
+def test_kq_rows_misaligned():
+    """Odd row counts of 2-byte-aligned rows: a Q8_0 row of K = 384 is 408
+    bytes and a Q6_K row of K = 256 210 bytes, so every other row starts 2
+    bytes into a dword; the last row's last block ends the tensor."""
+    for qtype, k in ((Q80, 384), (Q6K, 256), (Q6K, 768)):
+        qt, x = make(9, 7, k, k + qtype, qtype=qtype)
+        xt = torch.from_numpy(x).to("cuda", torch.float16)
+        y = gemm(qt, xt).cpu().numpy()
+        want = ref_gemm(qt, xt.float().cpu().numpy())
+        assert O.rel_l2(y, want) <= TOL, (qtype, k)
+
+
+@pytest.mark.parametrize("m", [8, 512])
+def test_kq_q6k_down_shape(m):
+    """Q6_K 4096 x 14336 (the down projection of a Q4_K_M file) at M = 8 and
+    M = 512, fp16 X ~ N(0, 1) with 0.1 % outliers x20."""
+    n, k = 4096, 14336
+    gen = torch.Generator(device="cuda").manual_seed(100 + m)
+    qt = QTensor.quantize(torch.randn((n, k), generator=gen, device="cuda") * 0.02, Q6K)
+    x = torch.randn((m, k), generator=gen, device="cuda")
+    x[torch.rand((m, k), generator=gen, device="cuda") < 0.001] *= 20.0
+    xh = x.half()
+    y = gemm(qt, xh).cpu().numpy()
+    w = O.dequantize(qt.to_numpy_bytes(), k, Q6K).astype(np.float32)
+    want = xh.float().cpu().numpy().astype(np.float64) @ w.T.astype(np.float64)
+    assert O.rel_l2(y, want) <= TOL
+
+
+def test_kq_matches_gemv_rows():
+    """Row r of the Q6_K / Q8_0 GEMM against the GEMV of the same weights
+    with x = X[r] (two independent kernels, fp32 X)."""
+    from vibeblade_amd.tensor import gemv
+    for qtype in (Q6K, Q80):
+        qt, x = make(6, 96, 2048, 77 + qtype, qtype=qtype)
+        xt = torch.from_numpy(x).to("cuda", torch.float32)
+        y = gemm(qt, xt).cpu().numpy()
+        for r in range(6):
+            yr = gemv(qt, xt[r]).cpu().numpy()
+            assert O.rel_l2(y[r], yr) <= TOL, (qtype, r)
+
+
+def test_kq_rejects():
+    qt, x = make(4, 16, 256, 3, qtype=Q80)  # Q8_0 K = 256 is fine
+    gemm(qt, torch.from_numpy(x).to("cuda", torch.float16))
+    q8, x8 = make(4, 16, 96, 3, qtype=Q80)  # K % 128 != 0
+    with pytest.raises(VBError):
+        gemm(q8, torch.from_numpy(x8).to("cuda", torch.float16))
+    with pytest.raises(VBError):
+        gemm(qt, torch.from_numpy(x).to("cuda", torch.float16), variant=GEMM_TILED)

@@ -326,8 +326,8 @@ int launch_tiled(const TileCfg& c, const uint8_t* w, const void* X, float* Y, in
 
 int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, int64_t N, int64_t K,
                   int32_t type, int32_t variant, hipStream_t st) {
-    if (type != TYPE_Q4_K) {
-        set_error("vb_gemm: weight type %d has no MFMA path yet (Q4_K only)", type);
+    if (type != TYPE_Q4_K && type != TYPE_Q6_K && type != TYPE_Q8_0) {
+        set_error("vb_gemm: weight type %d has no MFMA path (Q4_K, Q6_K, Q8_0)", type);
         return E_UNSUPPORTED;
     }
     const int64_t rb = row_bytes(type, K);
@@ -343,6 +343,14 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
     if (reinterpret_cast<uintptr_t>(w) % 16 || reinterpret_cast<uintptr_t>(X) % 16) {
         set_error("vb_gemm: W and X must be 16-byte aligned");
         return E_INVAL;
+    }
+    if (type != TYPE_Q4_K) {
+        // Q6_K / Q8_0: one kernel family for every M (gemm_kq.hip)
+        if (variant != 0) {
+            set_error("vb_gemm: variant %d is Q4_K-only (use 0 for Q6_K / Q8_0)", variant);
+            return E_UNSUPPORTED;
+        }
+        return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
     }
     const bool skinny = variant == 1 || (variant == 0 && M <= 16);
     if (skinny) {

@@ -1,0 +1,386 @@
+// Batched dequant-fused GEMM for Q6_K and Q8_0 weights on MFMA:
+//   Y[M, N] = X[M, K] . W[N, K]^T   (W in GGUF layout, X fp16 or fp32
+//   row-major, Y fp32 row-major).
+//
+// Replaces the reference's batched path for these types, a per-token loop of
+// gemv_dequant over rows decoded by dequantize_row (cpp/src/fast_model.cpp:
+// 905-960, cpp/src/dequant.cpp:407-425): a Q4_K_M file keeps its ffn_down,
+// attn_v and output tensors in Q6_K, and Q8_0 files use Q8_0 throughout.
+//
+// Design.  A workgroup of 8 waves owns a tile of 16 MA activation rows x
+// 16 NCG weight rows and splits K between its waves (contiguous ranges of
+// 128-element steps).  Every wave keeps both operands in registers:
+//  * A: fragment (a, ks) of a step is X[16 a + j][128 s + 32 ks + 8 g, +8)
+//    for lane (j, g), loaded from global memory (L2) at the start of the step;
+//  * B: for each column group the wave decodes one "unit" per lane (weight
+//    row 16 cg + j, the 8 elements 8 g .. of each 32-element k-step of the
+//    128-element step) into four fp16 fragments, w rounded to fp16, from raw
+//    bytes it loaded RD steps earlier.
+// Each weight is therefore decoded once per M-tile and each activation
+// loaded once per N-tile, with no LDS staging; the 8 partial tiles meet in
+// LDS at the end and are added in a fixed order (deterministic output).
+//
+// The k order inside an MFMA is free as long as A and B agree; both use the
+// natural order: lane (j, g) of k-step ks holds elements 32 ks + 8 g + 0..7
+// of the step, and the Q6_K and Q8_0 layouts put exactly those elements in
+// 8 consecutive bytes per lane (below).
+//
+// GGUF rows of these types are only 2-byte aligned (210- and 34-byte
+// blocks), so each 8-byte field is read as the three dwords from its
+// address rounded down to 4 and realigned with v_alignbyte; the weight
+// resource spans the tensor rounded up to whole dwords (the last dword
+// holds tensor bytes, so it is mapped memory).
+#include "mfma_q4k.hpp"
+#include "vb_internal.hpp"
+#include "../../include/vbhip.h"
+
+namespace vb {
+namespace {
+
+constexpr int KQ_WAVES = 8;
+constexpr int KQ_STEP = 128;                 // elements per step: four MFMA k-steps
+constexpr uint32_t KQ_X_NONE = 0x80000000u;  // lane offset of an absent activation row (reads zeros)
+constexpr int KQ_X_F32 = 0;
+constexpr int KQ_X_F16 = 1;
+
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+
+__device__ __forceinline__ u32x3 ld96(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b96(r, static_cast<int>(off), 0, 0);
+}
+__device__ __forceinline__ uint32_t ld32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(off), 0, 0);
+}
+// bytes [sh, sh + 8) of the 12 loaded bytes (sh = 0 or 2)
+__device__ __forceinline__ void realign(const u32x3& v, uint32_t sh, uint32_t& x, uint32_t& y) {
+    x = __builtin_amdgcn_alignbyte(v.y, v.x, sh);
+    y = __builtin_amdgcn_alignbyte(v.z, v.y, sh);
+}
+
+// Constants of the decoders in VGPRs: gfx9 VOP3 takes no literal and one
+// scalar operand at most.
+struct KqConsts {
+    uint32_t m0f, m30, h64, x80;
+};
+__device__ __forceinline__ KqConsts kq_consts() {
+    KqConsts c;
+    asm volatile("v_mov_b32 %0, 0x000F000F" : "=v"(c.m0f));
+    asm volatile("v_mov_b32 %0, 0x00300030" : "=v"(c.m30));
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(c.h64));
+    asm volatile("v_mov_b32 %0, 0x64806480" : "=v"(c.x80));
+    return c;
+}
+
+template <int TYPE> struct Kq;
+
+// Q6_K in the GGUF layout (the layout of real files and of the known answers
+// in tests/test_kquants.py:134-175; cpp/src/dequant.cpp:359-402 gathers the
+// elements in another order): super-block of 256 = two halves h of 128
+// elements; bytes ql[128] @0, qh[64] @128, int8
+// scales[16] @192, fp16 d @208.  In half h, element l + 32 t (l < 32, t < 4)
+// is q - 32 with q = (ql[64 h + l + 32 (t & 1)] >> 4 (t >> 1)) & 15 |
+// ((qh[32 h + l] >> 2 t) & 3) << 4, scaled by d * scales[8 h + l / 16 + 2 t].
+// A step is one half; k-step ks = t, so lane (j, g) needs ql bytes
+// [64 h + 8 g, +8) (t = 0, 2) and [64 h + 32 + 8 g, +8) (t = 1, 3), qh bytes
+// [32 h + 8 g, +8), the scales 8 h + g / 2 + 2 t and d.
+template <>
+struct Kq<TYPE_Q6_K> {
+    struct Raw {
+        u32x3 l0, l1, qh, sc;
+        uint32_t d;
+    };
+    // every field offset is a multiple of 4 from the super-block start, so
+    // one shift (the start's offset within its dword) serves all of them
+    __device__ static __forceinline__ uint32_t shift(uint32_t rowoff, int step) {
+        return (rowoff + static_cast<uint32_t>(step >> 1) * 210u) & 3u;
+    }
+    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t w, uint32_t rowoff, int step, int g,
+                                                 Raw& r) {
+        const uint32_t base = (rowoff + static_cast<uint32_t>(step >> 1) * 210u) & ~3u;
+        const uint32_t h = static_cast<uint32_t>(step & 1), g8 = 8u * static_cast<uint32_t>(g);
+        r.l0 = ld96(w, base + 64u * h + g8);
+        r.l1 = ld96(w, base + 64u * h + 32u + g8);
+        r.qh = ld96(w, base + 128u + 32u * h + g8);
+        r.sc = ld96(w, base + 192u + 8u * h);
+        r.d = ld32(w, base + 208u);
+    }
+    __device__ static __forceinline__ void decode(const Raw& r, uint32_t sh, int g, const KqConsts& kc, Frag* f) {
+        uint32_t l0[2], l1[2], qh[2], sc[2];
+        realign(r.l0, sh, l0[0], l0[1]);
+        realign(r.l1, sh, l1[0], l1[1]);
+        realign(r.qh, sh, qh[0], qh[1]);
+        realign(r.sc, sh, sc[0], sc[1]);
+        const float d = f16lo(r.d >> (8u * sh));
+        // scale bytes g / 2 + {0, 2, 4, 6} of the half's eight
+        const uint32_t P = __builtin_amdgcn_perm(sc[1], sc[0], g >= 2 ? 0x07050301u : 0x06040200u);
+        half2_t dsc[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int8_t s = static_cast<int8_t>((P >> (8 * t)) & 0xFFu);
+            const _Float16 v = static_cast<_Float16>(d * static_cast<float>(s));
+            dsc[t] = half2_t{v, v};
+        }
+        const half2_t k1056 = half2_t{static_cast<_Float16>(1056.0f), static_cast<_Float16>(1056.0f)};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            // elements 2 i, 2 i + 1: halves (ql | qh << 8) of each
+            const uint32_t sel = (i & 1) ? 0x07030602u : 0x05010400u;
+            const uint32_t x = __builtin_amdgcn_perm(qh[i >> 1], l0[i >> 1], sel);
+            const uint32_t y = __builtin_amdgcn_perm(qh[i >> 1], l1[i >> 1], sel);
+            // 1024 + q in each half (exact), q = 6-bit value
+            uint32_t q[4];
+            q[0] = (x & kc.m0f) | (((x >> 4) & kc.m30) | kc.h64);
+            q[2] = ((x >> 4) & kc.m0f) | (((x >> 8) & kc.m30) | kc.h64);
+            q[1] = (y & kc.m0f) | (((y >> 6) & kc.m30) | kc.h64);
+            q[3] = ((y >> 4) & kc.m0f) | (((y >> 10) & kc.m30) | kc.h64);
+#pragma unroll
+            for (int t = 0; t < 4; t++) f[t].u[i] = h2bits((bits2h(q[t]) - k1056) * dsc[t]);
+        }
+    }
+};
+
+// Q8_0 in the GGUF layout (vibeblade/loader.py:129-133,
+// cpp/src/cuda_kernels.cu:718-735): blocks of 32 = fp16 d @0, int8 qs[32]
+// @2.  A
+// step is four blocks; k-step ks = block 4 s + ks, lane (j, g) needs qs
+// bytes [8 g, +8) and d.
+template <>
+struct Kq<TYPE_Q8_0> {
+    struct Raw {
+        u32x3 q[4];
+        uint32_t d[4];
+    };
+    // block 4 s + ks starts at rowoff + 136 s + 34 ks, whose offset within
+    // its dword is (rowoff + 2 ks) & 3; its qs field is 2 bytes further on
+    __device__ static __forceinline__ uint32_t shift(uint32_t rowoff, int) { return rowoff & 3u; }
+    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t w, uint32_t rowoff, int step, int g,
+                                                 Raw& r) {
+        const uint32_t s0 = rowoff + static_cast<uint32_t>(step) * 136u, g8 = 8u * static_cast<uint32_t>(g);
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const uint32_t b = s0 + 34u * ks;
+            r.q[ks] = ld96(w, ((b + 2u) & ~3u) + g8);
+            r.d[ks] = ld32(w, b & ~3u);
+        }
+    }
+    __device__ static __forceinline__ void decode(const Raw& r, uint32_t sh, int, const KqConsts& kc, Frag* f) {
+        const half2_t k1152 = half2_t{static_cast<_Float16>(1152.0f), static_cast<_Float16>(1152.0f)};
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const uint32_t shd = (sh + 2u * ks) & 3u, shq = shd ^ 2u;
+            uint32_t qs[2];
+            realign(r.q[ks], shq, qs[0], qs[1]);
+            const uint32_t d16 = (r.d[ks] >> (8u * shd)) & 0xFFFFu;
+            const half2_t dd = bits2h(d16 | (d16 << 16));
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                // bytes (b0, b1) into the two halves; (b ^ 0x80) | 0x6400 is
+                // the half 1024 + q + 128 (exact)
+                const uint32_t src = __builtin_amdgcn_perm(0u, qs[i >> 1], (i & 1) ? 0x0C030C02u : 0x0C010C00u);
+                f[ks].u[i] = h2bits((bits2h(src ^ kc.x80) - k1152) * dd);
+            }
+        }
+    }
+};
+
+// X fragments of one step: A[ks][a] for activation rows 16 a + j.
+template <int XT, int MA>
+struct XFrags {
+    u32x4 v[4][MA][XT == KQ_X_F16 ? 1 : 2];
+};
+
+template <int TYPE, int XT, int MA, int NCG, int RD>
+__global__ void __launch_bounds__(64 * KQ_WAVES) gemm_kq_kernel(const uint8_t* __restrict__ w, uint32_t wbytes,
+                                                                const uint8_t* __restrict__ X, uint32_t xbytes,
+                                                                float* __restrict__ Y, int M, int N, int K,
+                                                                uint32_t rb) {
+    using T = Kq<TYPE>;
+    extern __shared__ float4_t kq_red[];  // [wave][MA * NCG][lane]
+    constexpr uint32_t ES = XT == KQ_X_F16 ? 2u : 4u;
+    const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int n0 = static_cast<int>(blockIdx.x) * 16 * NCG;
+    const int m0 = static_cast<int>(blockIdx.y) * 16 * MA;
+    const int nsteps = K / KQ_STEP;
+    const int s_beg = __builtin_amdgcn_readfirstlane((wave * nsteps) / KQ_WAVES);
+    const int s_end = __builtin_amdgcn_readfirstlane(((wave + 1) * nsteps) / KQ_WAVES);
+
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(w, wbytes);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(X, xbytes);
+    uint32_t rowoff[NCG];  // weight rows 16 cg + j (rows past N repeat row N - 1; never stored)
+#pragma unroll
+    for (int cg = 0; cg < NCG; cg++) {
+        int n = n0 + 16 * cg + j;
+        n = n < N ? n : N - 1;
+        rowoff[cg] = static_cast<uint32_t>(n) * rb;
+    }
+    uint32_t xoff[MA];  // activation rows 16 a + j (+ 8 g elements); rows past M read zeros
+#pragma unroll
+    for (int a = 0; a < MA; a++) {
+        const int t = m0 + 16 * a + j;
+        xoff[a] = t < M ? (static_cast<uint32_t>(t) * static_cast<uint32_t>(K) + 8u * static_cast<uint32_t>(g)) * ES
+                        : KQ_X_NONE;
+    }
+    const KqConsts kc = kq_consts();
+
+    float4_t acc[MA][NCG];
+#pragma unroll
+    for (int a = 0; a < MA; a++)
+#pragma unroll
+        for (int cg = 0; cg < NCG; cg++) acc[a][cg] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    typename T::Raw raw[RD][NCG];
+    const int last = s_end - 1;
+    auto issue = [&](int slot, int step) {
+        step = step < last ? step : last;  // past the wave's range: repeats its last step, unused
+#pragma unroll
+        for (int cg = 0; cg < NCG; cg++) T::issue(wr, rowoff[cg], step, g, raw[slot][cg]);
+    };
+    if (s_end > s_beg) {
+#pragma unroll
+        for (int r = 0; r < RD; r++) issue(r, s_beg + r);
+        for (int it = s_beg; it < s_end; it += RD) {
+#pragma unroll
+            for (int r = 0; r < RD; r++) {
+                const int step = it + r;
+                if (step >= s_end) break;  // uniform
+                XFrags<XT, MA> xf;
+                const uint32_t so = static_cast<uint32_t>(step) * KQ_STEP * ES;
+#pragma unroll
+                for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+                    for (int a = 0; a < MA; a++) {
+                        xf.v[ks][a][0] = buf_ld128(xr, xoff[a], so + 32u * ES * ks);
+                        if constexpr (XT == KQ_X_F32) xf.v[ks][a][1] = buf_ld128(xr, xoff[a], so + 32u * ES * ks + 16u);
+                    }
+                Frag af[4][MA];
+#pragma unroll
+                for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+                    for (int a = 0; a < MA; a++) {
+                        if constexpr (XT == KQ_X_F16) {
+                            const u32x4 v = xf.v[ks][a][0];
+                            af[ks][a].u[0] = v.x; af[ks][a].u[1] = v.y; af[ks][a].u[2] = v.z; af[ks][a].u[3] = v.w;
+                        } else {
+                            const u32x4 lo = xf.v[ks][a][0], hi = xf.v[ks][a][1];
+                            f32x8_to_frag_nat(make_float4(__uint_as_float(lo.x), __uint_as_float(lo.y),
+                                                          __uint_as_float(lo.z), __uint_as_float(lo.w)),
+                                              make_float4(__uint_as_float(hi.x), __uint_as_float(hi.y),
+                                                          __uint_as_float(hi.z), __uint_as_float(hi.w)),
+                                              af[ks][a].u);
+                        }
+                    }
+#pragma unroll
+                for (int cg = 0; cg < NCG; cg++) {
+                    Frag bf[4];
+                    T::decode(raw[r][cg], T::shift(rowoff[cg], step), g, kc, bf);
+                    T::issue(wr, rowoff[cg], (step + RD) < last ? step + RD : last, g, raw[r][cg]);
+#pragma unroll
+                    for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+                        for (int a = 0; a < MA; a++) acc[a][cg] = mfma16x16x32(af[ks][a], bf[ks], acc[a][cg]);
+                }
+            }
+        }
+    }
+
+    // k-range partials meet in LDS and are added in wave order
+#pragma unroll
+    for (int a = 0; a < MA; a++)
+#pragma unroll
+        for (int cg = 0; cg < NCG; cg++) kq_red[(wave * MA * NCG + a * NCG + cg) * 64 + lane] = acc[a][cg];
+    __syncthreads();
+    for (int e = threadIdx.x; e < MA * NCG * 64; e += 64 * KQ_WAVES) {
+        float4_t s = kq_red[e];
+#pragma unroll
+        for (int v = 1; v < KQ_WAVES; v++) s += kq_red[v * MA * NCG * 64 + e];
+        const int idx = e >> 6, l = e & 63, a = idx / NCG, cg = idx - a * NCG;
+        const int col = n0 + 16 * cg + (l & 15);
+        if (col >= N) continue;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int t = m0 + 16 * a + 4 * (l >> 4) + r;
+            if (t < M) Y[static_cast<int64_t>(t) * N + col] = s[r];
+        }
+    }
+}
+
+template <int TYPE, int XT, int MA, int NCG, int RD>
+void launch_kq(const uint8_t* w, uint32_t wbytes, const uint8_t* X, uint32_t xbytes, float* Y, int M, int N, int K,
+               uint32_t rb, hipStream_t st) {
+    const dim3 grid(static_cast<uint32_t>((N + 16 * NCG - 1) / (16 * NCG)),
+                    static_cast<uint32_t>((M + 16 * MA - 1) / (16 * MA)));
+    const size_t lds = static_cast<size_t>(KQ_WAVES) * MA * NCG * 64 * sizeof(float4_t);
+    gemm_kq_kernel<TYPE, XT, MA, NCG, RD><<<grid, dim3(64 * KQ_WAVES), lds, st>>>(w, wbytes, X, xbytes, Y, M, N, K,
+                                                                                  rb);
+}
+
+// Tile by M.  M <= 16: 16-row M tiles and 16-64 weight rows per workgroup
+// (enough workgroups at N = 4096 to fill the CUs), raw weight bytes two or
+// three steps ahead.  M <= 64: one M tile of 16 ceil(M / 16) rows, so every
+// weight is decoded once, 16 weight rows per workgroup.  Above: 64 x 64 tiles
+// (fp32 X: 32 x 64, its fragments take twice the registers) with the raw
+// bytes one step ahead.
+template <int TYPE, int XT>
+void launch_kq_m(const uint8_t* w, uint32_t wbytes, const uint8_t* X, uint32_t xbytes, float* Y, int M, int N, int K,
+                 uint32_t rb, hipStream_t st) {
+    if (M <= 16) {
+        if (N >= 16384)
+            launch_kq<TYPE, XT, 1, 4, 2>(w, wbytes, X, xbytes, Y, M, N, K, rb, st);
+        else if (N >= 8192)
+            launch_kq<TYPE, XT, 1, 2, 2>(w, wbytes, X, xbytes, Y, M, N, K, rb, st);
+        else
+            launch_kq<TYPE, XT, 1, 1, 3>(w, wbytes, X, xbytes, Y, M, N, K, rb, st);
+    } else if (M <= 32) {
+        launch_kq<TYPE, XT, 2, 1, 2>(w, wbytes, X, xbytes, Y, M, N, K, rb, st);
+    } else if (M <= 48) {
+        launch_kq<TYPE, XT, 3, 1, 2>(w, wbytes, X, xbytes, Y, M, N, K, rb, st);
+    } else if (M <= 64) {
+        launch_kq<TYPE, XT, 4, 1, 2>(w, wbytes, X, xbytes, Y, M, N, K, rb, st);
+    } else if constexpr (XT == KQ_X_F16) {
+        launch_kq<TYPE, XT, 4, 4, 1>(w, wbytes, X, xbytes, Y, M, N, K, rb, st);
+    } else {
+        launch_kq<TYPE, XT, 2, 4, 1>(w, wbytes, X, xbytes, Y, M, N, K, rb, st);
+    }
+}
+
+}  // namespace
+
+// Caller (gemm_dispatch) has checked M, N > 0, pointers, X 16-byte alignment
+// and x_dtype.
+int gemm_kq(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, int64_t N, int64_t K, int32_t type,
+            hipStream_t st) {
+    if (K % KQ_STEP != 0) {
+        set_error("vb_gemm: %s weights need K %% 128 == 0 (K=%lld)", type == TYPE_Q6_K ? "Q6_K" : "Q8_0",
+                  static_cast<long long>(K));
+        return E_UNSUPPORTED;
+    }
+    const int64_t rb = row_bytes(type, K);
+    const int64_t wbytes = (N * rb + 3) & ~int64_t(3);
+    const int64_t xbytes = M * K * (x_dtype == KQ_X_F16 ? 2 : 4);
+    if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX || (M + 15) / 16 > 65535 || wbytes >= (int64_t(1) << 32) ||
+        xbytes >= (int64_t(1) << 31)) {
+        set_error("vb_gemm: shape too large (M=%lld N=%lld K=%lld)", static_cast<long long>(M),
+                  static_cast<long long>(N), static_cast<long long>(K));
+        return E_INVAL;
+    }
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
+    const uint8_t* xb = static_cast<const uint8_t*>(X);
+    const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
+    const uint32_t wby = static_cast<uint32_t>(wbytes), xby = static_cast<uint32_t>(xbytes),
+                   rbu = static_cast<uint32_t>(rb);
+    if (type == TYPE_Q6_K) {
+        if (x_dtype == KQ_X_F16)
+            launch_kq_m<TYPE_Q6_K, KQ_X_F16>(wb, wby, xb, xby, Y, m, n, k, rbu, st);
+        else
+            launch_kq_m<TYPE_Q6_K, KQ_X_F32>(wb, wby, xb, xby, Y, m, n, k, rbu, st);
+    } else {
+        if (x_dtype == KQ_X_F16)
+            launch_kq_m<TYPE_Q8_0, KQ_X_F16>(wb, wby, xb, xby, Y, m, n, k, rbu, st);
+        else
+            launch_kq_m<TYPE_Q8_0, KQ_X_F32>(wb, wby, xb, xby, Y, m, n, k, rbu, st);
+    }
+    return check_launch("vb_gemm");
+}
+
+}  // namespace vb

@@ -94,6 +94,10 @@ int gemm_q4k_skinny(const void* w, const void* X, int32_t x_dtype, float* Y, int
 // Role-split Q4_K GEMM, fp16 X (gemm_split.hip); type, alignment and the
 // 32-bit offset bounds already validated.
 int gemm_q4k_split(const void* w, const void* X, float* Y, int64_t M, int64_t N, int64_t K, hipStream_t st);
+// Q6_K / Q8_0 GEMM, every M (gemm_kq.hip); pointers, alignment, x_dtype and
+// M, N > 0 already validated.
+int gemm_kq(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, int64_t N, int64_t K, int32_t type,
+            hipStream_t st);
 int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, int64_t N, int64_t K,
                   int32_t type, int32_t variant, hipStream_t st);
 
