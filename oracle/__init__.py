@@ -58,6 +58,9 @@ PARITY = {
     "dequant Q6_K": "pinned: layout-invariant KATs (reference tests/test_kquants.py:134-175) "
                     "+ single-position index-map blocks + VBREF golden vectors",
     "dequant Q8_0": "pinned: closed forms (d=1 -> q, d=0 -> 0) on loader.py:129-133 layout",
+    "dequant Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q5_K / Q2_K / Q3_K": "pinned: ggml's published dequantize_row_* "
+        "loop forms restated in the tests (sequential outputs, ggml's own scale / fifth-bit / hmask "
+        "unpacking) on random blocks, plus a moved-code-bit negative control",
     "gemv / gemm": "pinned: brute force over integer-valued blocks + fp64 numpy",
     "sparse_ffn": "pinned: closed form S=all equals dense, S=empty gives 0, order invariance",
     "ffn_block": "pinned: rms_norm closed forms (constant rows, scale invariance, eps), "

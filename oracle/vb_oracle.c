@@ -42,8 +42,10 @@
  * vectors produced by the compiled reference dequant.cpp; Q6_K against the
  * layout-invariant known answers of tests/test_kquants.py:134-175 plus
  * single-position index-map blocks; Q8_0 against closed forms (d=1 gives q,
- * d=0 gives 0) and loader.py semantics; gemv against brute force on blocks
- * whose decoded values are known integers.
+ * d=0 gives 0) and loader.py semantics; Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q5_K /
+ * Q2_K / Q3_K against ggml's published dequantize_row_* loop forms on random
+ * blocks; gemv against brute force on blocks whose decoded values are known
+ * integers.
  */
 #include <math.h>
 #include <stdint.h>

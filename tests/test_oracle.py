@@ -191,6 +191,204 @@ def test_q6k_gguf_and_vbref_differ():
     assert np.flatnonzero(v != -32.0).tolist() == [3]    # VBREF: e/2=1, odd
 
 
+# ---- ggml's published loop forms for the other GGUF types -----------------------
+#
+# Each helper restates ggml's dequantize_row_* loop (ggml-quants.c) in its own
+# shape -- sequential outputs, strided reads, ggml's own scale unpacking -- in
+# float64, which is exact for these products.  The oracle decodes by element
+# index with its own helpers, in float32 (gcc may contract d*q - m into one
+# fma), so the comparison allows a few float32 ulps of the terms: far below one
+# quantization step, which any layout or bit-map mistake moves by.
+
+def _h16(b):
+    return float(np.frombuffer(bytes(b[:2]), np.float16)[0])
+
+
+def _ulp_ok(got, want, scale):
+    """|got - want| within 2^-20 of the per-block magnitude `scale`."""
+    return np.all(np.abs(got.astype(np.float64) - want) <= scale * 2.0 ** -20)
+
+
+def _ggml_scale_min_k4(j, q):
+    if j < 4:
+        return q[j] & 63, q[j + 4] & 63
+    return (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4), (q[j + 4] >> 4) | ((q[j] >> 6) << 4)
+
+
+def _ggml_q4_0(b):
+    d, qs = _h16(b[0:2]), [int(v) for v in b[2:18]]
+    y = np.zeros(32)
+    for j in range(16):
+        y[j] = ((qs[j] & 0x0F) - 8) * d
+        y[j + 16] = ((qs[j] >> 4) - 8) * d
+    return y
+
+
+def _ggml_q4_1(b):
+    d, m, qs = _h16(b[0:2]), _h16(b[2:4]), [int(v) for v in b[4:20]]
+    y = np.zeros(32)
+    for j in range(16):
+        y[j] = (qs[j] & 0x0F) * d + m
+        y[j + 16] = (qs[j] >> 4) * d + m
+    return y
+
+
+def _ggml_q5_0(b):
+    d = _h16(b[0:2])
+    qh = int.from_bytes(bytes(b[2:6]), "little")
+    qs = [int(v) for v in b[6:22]]
+    y = np.zeros(32)
+    for j in range(16):
+        xh_0 = ((qh >> (j + 0)) << 4) & 0x10
+        xh_1 = (qh >> (j + 12)) & 0x10
+        y[j] = (((qs[j] & 0x0F) | xh_0) - 16) * d
+        y[j + 16] = (((qs[j] >> 4) | xh_1) - 16) * d
+    return y
+
+
+def _ggml_q5_1(b):
+    d, m = _h16(b[0:2]), _h16(b[2:4])
+    qh = int.from_bytes(bytes(b[4:8]), "little")
+    qs = [int(v) for v in b[8:24]]
+    y = np.zeros(32)
+    for j in range(16):
+        xh_0 = ((qh >> (j + 0)) << 4) & 0x10
+        xh_1 = (qh >> (j + 12)) & 0x10
+        y[j] = ((qs[j] & 0x0F) | xh_0) * d + m
+        y[j + 16] = ((qs[j] >> 4) | xh_1) * d + m
+    return y
+
+
+def _ggml_q5_k(b):
+    d, dmin = _h16(b[0:2]), _h16(b[2:4])
+    scales = [int(v) for v in b[4:16]]
+    qh = [int(v) for v in b[16:48]]
+    ql = [int(v) for v in b[48:176]]
+    y = np.zeros(256)
+    o, is_, u1, u2 = 0, 0, 1, 2
+    for j in range(0, 256, 64):
+        sc, m = _ggml_scale_min_k4(is_ + 0, scales)
+        d1, m1 = d * sc, dmin * m
+        sc, m = _ggml_scale_min_k4(is_ + 1, scales)
+        d2, m2 = d * sc, dmin * m
+        for l in range(32):
+            y[j + l] = d1 * ((ql[o + l] & 0xF) + (16 if qh[l] & u1 else 0)) - m1
+        for l in range(32):
+            y[j + 32 + l] = d2 * ((ql[o + l] >> 4) + (16 if qh[l] & u2 else 0)) - m2
+        o += 32
+        is_ += 2
+        u1 <<= 2
+        u2 <<= 2
+    return y
+
+
+def _ggml_q2_k(b):
+    scales = [int(v) for v in b[0:16]]
+    q = [int(v) for v in b[16:80]]
+    d, dmin = _h16(b[80:82]), _h16(b[82:84])
+    y, yi, is_ = np.zeros(256), 0, 0
+    for n in range(2):
+        qq = q[32 * n:]
+        shift = 0
+        for _ in range(4):
+            sc = scales[is_]
+            is_ += 1
+            dl, ml = d * (sc & 0xF), dmin * (sc >> 4)
+            for l in range(16):
+                y[yi] = dl * ((qq[l] >> shift) & 3) - ml
+                yi += 1
+            sc = scales[is_]
+            is_ += 1
+            dl, ml = d * (sc & 0xF), dmin * (sc >> 4)
+            for l in range(16):
+                y[yi] = dl * ((qq[l + 16] >> shift) & 3) - ml
+                yi += 1
+            shift += 2
+    return y
+
+
+def _ggml_q3_k(b):
+    hm = [int(v) for v in b[0:32]]
+    q = [int(v) for v in b[32:96]]
+    aux = [int.from_bytes(bytes(b[96 + 4 * i:100 + 4 * i]), "little") for i in range(3)] + [0]
+    d_all = _h16(b[108:110])
+    kmask1, kmask2 = 0x03030303, 0x0F0F0F0F
+    tmp = aux[2]
+    aux[2] = ((aux[0] >> 4) & kmask2) | (((tmp >> 4) & kmask1) << 4)
+    aux[3] = ((aux[1] >> 4) & kmask2) | (((tmp >> 6) & kmask1) << 4)
+    aux[0] = (aux[0] & kmask2) | (((tmp >> 0) & kmask1) << 4)
+    aux[1] = (aux[1] & kmask2) | (((tmp >> 2) & kmask1) << 4)
+    scales = np.array(aux, dtype="<u4").view(np.int8).astype(int)
+    y, yi, is_, m = np.zeros(256), 0, 0, 1
+    for n in range(2):
+        qq = q[32 * n:]
+        shift = 0
+        for _ in range(4):
+            dl = d_all * (scales[is_] - 32)
+            is_ += 1
+            for l in range(16):
+                y[yi] = dl * (((qq[l] >> shift) & 3) - (0 if hm[l] & m else 4))
+                yi += 1
+            dl = d_all * (scales[is_] - 32)
+            is_ += 1
+            for l in range(16):
+                y[yi] = dl * (((qq[l + 16] >> shift) & 3) - (0 if hm[l + 16] & m else 4))
+                yi += 1
+            shift += 2
+            m <<= 1
+    return y
+
+
+# type -> (loop form, byte offsets of the fp16 fields, magnitude bound of a
+# block's terms in units of its fp16 fields: (field offset, bound))
+_LOOP_FORMS = {
+    O.TYPE_Q4_0: (_ggml_q4_0, [(0, 8)]),
+    O.TYPE_Q4_1: (_ggml_q4_1, [(0, 15), (2, 1)]),
+    O.TYPE_Q5_0: (_ggml_q5_0, [(0, 16)]),
+    O.TYPE_Q5_1: (_ggml_q5_1, [(0, 31), (2, 1)]),
+    O.TYPE_Q5_K: (_ggml_q5_k, [(0, 63 * 31), (2, 63)]),
+    O.TYPE_Q2_K: (_ggml_q2_k, [(80, 15 * 3), (82, 15)]),
+    O.TYPE_Q3_K: (_ggml_q3_k, [(108, 32 * 4)]),
+}
+
+
+@pytest.mark.parametrize("qtype", sorted(_LOOP_FORMS))
+def test_gguf_types_against_ggml_loop_forms(qtype):
+    """Oracle decode of Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q5_K / Q2_K / Q3_K equals
+    ggml's published loop form on random blocks (every bit pattern of the
+    codes, scales and fifth / third bits), with finite random fp16 fields."""
+    form, fields = _LOOP_FORMS[qtype]
+    qk, bs = O.BLOCK_ELEMS[qtype], O.BLOCK_BYTES[qtype]
+    rng = np.random.default_rng(1000 + qtype)
+    for _ in range(24):
+        blk = rng.integers(0, 256, bs, dtype=np.uint8)
+        for off, _bound in fields:
+            blk[off:off + 2] = np.frombuffer(np.float16(rng.uniform(-2, 2)).tobytes(), np.uint8)
+        got = O.dequantize(blk.reshape(1, -1), qk, qtype).ravel()
+        want = form(blk)
+        scale = sum(abs(_h16(blk[off:off + 2])) * bound for off, bound in fields)
+        assert _ulp_ok(got, want, scale), (qtype, np.flatnonzero(np.abs(got - want) > scale * 2.0 ** -20)[:8])
+
+
+@pytest.mark.parametrize("qtype", sorted(_LOOP_FORMS))
+def test_ggml_loop_forms_detect_a_moved_bit(qtype):
+    """The comparison has teeth: decoding a block whose codes were changed
+    in one byte differs from the loop form of the original block."""
+    form, fields = _LOOP_FORMS[qtype]
+    qk, bs = O.BLOCK_ELEMS[qtype], O.BLOCK_BYTES[qtype]
+    rng = np.random.default_rng(2000 + qtype)
+    blk = rng.integers(0, 256, bs, dtype=np.uint8)
+    for off, _bound in fields:
+        blk[off:off + 2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    fp16_bytes = {off + i for off, _ in fields for i in (0, 1)}
+    byte = next(i for i in range(bs - 1, -1, -1) if i not in fp16_bytes)
+    moved = blk.copy()
+    moved[byte] ^= 0x11
+    got = O.dequantize(moved.reshape(1, -1), qk, qtype).ravel()
+    scale = sum(bound for _off, bound in fields)
+    assert not _ulp_ok(got, form(blk), scale)
+
+
 # ---- Q8_0 ----------------------------------------------------------------------
 
 def _q8_block(d, q):
