@@ -10,7 +10,7 @@ import torch
 import oracle as O
 from vibeblade_amd import ggml
 from vibeblade_amd._lib import VBError
-from vibeblade_amd.tensor import QTensor, gemm, GEMM_SKINNY, GEMM_TILED, GEMM_SPLIT
+from vibeblade_amd.tensor import QTensor, gemm, GEMM_SKINNY, GEMM_TILED, GEMM_SPLIT, GEMM_KSPLIT
 
 pytestmark = pytest.mark.gpu
 
@@ -255,3 +255,19 @@ def test_kq_rejects():
         gemm(q8, torch.from_numpy(x8).to("cuda", torch.float16))
     with pytest.raises(VBError):
         gemm(qt, torch.from_numpy(x).to("cuda", torch.float16), variant=GEMM_TILED)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("m,n,k", [(1, 16, 256), (8, 300, 1024), (17, 100, 512), (40, 50, 256),
+                                   (64, 257, 1280), (100, 70, 512)])
+def test_ksplit_q4k(dtype, m, n, k):
+    """Q4_K on the K-split kernel (variant 4) at every M tile: against the
+    oracle, and against the default (skinny / tiled) kernel, which rounds the
+    same weights to the same fp16 values and sums in another order."""
+    qt, x = make(m, n, k, m * 13 + n, qtype=Q4K)
+    xt = torch.from_numpy(x).to("cuda", dtype)
+    y = gemm(qt, xt, variant=GEMM_KSPLIT).cpu().numpy()
+    want = ref_gemm(qt, xt.float().cpu().numpy())
+    assert O.rel_l2(y, want) <= TOL
+    other = gemm(qt, xt).cpu().numpy()
+    assert O.rel_l2(y, other) <= 1e-5

@@ -344,14 +344,19 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
         set_error("vb_gemm: W and X must be 16-byte aligned");
         return E_INVAL;
     }
-    if (type != TYPE_Q4_K) {
-        // Q6_K / Q8_0: one kernel family for every M (gemm_kq.hip)
-        if (variant != 0) {
-            set_error("vb_gemm: variant %d is Q4_K-only (use 0 for Q6_K / Q8_0)", variant);
+    if (type != TYPE_Q4_K || variant == 4) {
+        // Q6_K / Q8_0: one kernel family for every M (gemm_kq.hip); Q4_K on
+        // request (variant 4)
+        if (variant != 0 && variant != 4) {
+            set_error("vb_gemm: variant %d is Q4_K-only (use 0 or 4 for Q6_K / Q8_0)", variant);
             return E_UNSUPPORTED;
         }
         return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
     }
+    // 17 <= M <= 32 at N >= 12288: the K-split kernel (gemm_kq.hip; at
+    // N = 14336, K = 4096 on MI355X 21.3 / 24.6 us at M = 17 / 32 against
+    // 27.0 / 27.1 tiled, behind from M = 48)
+    if (variant == 0 && M >= 17 && M <= 32 && N >= 12288) return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
     const bool skinny = variant == 1 || (variant == 0 && M <= 16);
     if (skinny) {
         if (M > 16) {
@@ -360,7 +365,7 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
         }
         return gemm_q4k_skinny(w, X, x_dtype, Y, M, N, K, st);
     }
-    if (variant < 0 || variant > 3) {
+    if (variant < 0 || variant > 4) {
         set_error("vb_gemm: unknown variant %d", variant);
         return E_INVAL;
     }

@@ -73,6 +73,39 @@ __device__ __forceinline__ KqConsts kq_consts() {
 
 template <int TYPE> struct Kq;
 
+// Q4_K (cpp/src/dequant.cpp:258-301; header d, dmin, scales[12] @0, qs[128]
+// @16, rows 16-byte aligned): a step is half a super-block, chunks c = 2 h
+// and 2 h + 1; k-step 2 (c - 2 h) takes the low nibbles of qs bytes
+// [32 c + 8 g, +8) (sub-block 2 c), k-step 2 (c - 2 h) + 1 their high
+// nibbles (sub-block 2 c + 1).
+template <>
+struct Kq<TYPE_Q4_K> {
+    struct Raw {
+        u32x4 hd;
+        uint2 q[2];
+    };
+    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t w, uint32_t rowoff, int step, int g,
+                                                 Raw& r) {
+        const uint32_t base = rowoff + static_cast<uint32_t>(step >> 1) * 144u;
+        const uint32_t qo = base + 16u + 64u * static_cast<uint32_t>(step & 1) + 8u * static_cast<uint32_t>(g);
+        r.hd = buf_ld128(w, base, 0);
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(w, static_cast<int>(qo + 32u * c), 0, 0);
+            r.q[c] = make_uint2(v[0], v[1]);
+        }
+    }
+    __device__ static __forceinline__ void decode(const Raw& r, uint32_t, int step, int, const KqConsts&, Frag* f) {
+        const uint4 hd = make_uint4(r.hd.x, r.hd.y, r.hd.z, r.hd.w);
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            half2_t ds[2], nm[2];
+            q4k_chunk_scales(hd, 2 * (step & 1) + c, ds, nm);
+            q4k_bfrags_nat(r.q[c].x, r.q[c].y, ds, nm, f[2 * c], f[2 * c + 1]);
+        }
+    }
+};
+
 // Q6_K in the GGUF layout (the layout of real files and of the known answers
 // in tests/test_kquants.py:134-175; cpp/src/dequant.cpp:359-402 gathers the
 // elements in another order): super-block of 256 = two halves h of 128
@@ -104,7 +137,9 @@ struct Kq<TYPE_Q6_K> {
         r.sc = ld96(w, base + 192u + 8u * h);
         r.d = ld32(w, base + 208u);
     }
-    __device__ static __forceinline__ void decode(const Raw& r, uint32_t sh, int g, const KqConsts& kc, Frag* f) {
+    __device__ static __forceinline__ void decode(const Raw& r, uint32_t rowoff, int step, int g, const KqConsts& kc,
+                                                  Frag* f) {
+        const uint32_t sh = shift(rowoff, step);
         uint32_t l0[2], l1[2], qh[2], sc[2];
         realign(r.l0, sh, l0[0], l0[1]);
         realign(r.l1, sh, l1[0], l1[1]);
@@ -152,7 +187,6 @@ struct Kq<TYPE_Q8_0> {
     };
     // block 4 s + ks starts at rowoff + 136 s + 34 ks, whose offset within
     // its dword is (rowoff + 2 ks) & 3; its qs field is 2 bytes further on
-    __device__ static __forceinline__ uint32_t shift(uint32_t rowoff, int) { return rowoff & 3u; }
     __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t w, uint32_t rowoff, int step, int g,
                                                  Raw& r) {
         const uint32_t s0 = rowoff + static_cast<uint32_t>(step) * 136u, g8 = 8u * static_cast<uint32_t>(g);
@@ -163,7 +197,9 @@ struct Kq<TYPE_Q8_0> {
             r.d[ks] = ld32(w, b & ~3u);
         }
     }
-    __device__ static __forceinline__ void decode(const Raw& r, uint32_t sh, int, const KqConsts& kc, Frag* f) {
+    __device__ static __forceinline__ void decode(const Raw& r, uint32_t rowoff, int, int, const KqConsts& kc,
+                                                  Frag* f) {
+        const uint32_t sh = rowoff & 3u;
         const half2_t k1152 = half2_t{static_cast<_Float16>(1152.0f), static_cast<_Float16>(1152.0f)};
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
@@ -273,7 +309,7 @@ __global__ void __launch_bounds__(64 * KQ_WAVES) gemm_kq_kernel(const uint8_t* _
 #pragma unroll
                 for (int cg = 0; cg < NCG; cg++) {
                     Frag bf[4];
-                    T::decode(raw[r][cg], T::shift(rowoff[cg], step), g, kc, bf);
+                    T::decode(raw[r][cg], rowoff[cg], step, g, kc, bf);
                     T::issue(wr, rowoff[cg], (step + RD) < last ? step + RD : last, g, raw[r][cg]);
 #pragma unroll
                     for (int ks = 0; ks < 4; ks++)
@@ -315,12 +351,24 @@ void launch_kq(const uint8_t* w, uint32_t wbytes, const uint8_t* X, uint32_t xby
                                                                                   rb);
 }
 
-// Tile by M.  M <= 16: 16-row M tiles and 16-64 weight rows per workgroup
-// (enough workgroups at N = 4096 to fill the CUs), raw weight bytes two or
-// three steps ahead.  M <= 64: one M tile of 16 ceil(M / 16) rows, so every
-// weight is decoded once, 16 weight rows per workgroup.  Above: 64 x 64 tiles
-// (fp32 X: 32 x 64, its fragments take twice the registers) with the raw
-// bytes one step ahead.
+// Tile by M and N.  M <= 16: 16-row M tiles and 16-64 weight rows per
+// workgroup (enough workgroups at N = 4096 to fill the CUs), raw weight bytes
+// two or three steps ahead.  M <= 64: one M tile of 16 ceil(M / 16) rows, so
+// every weight is decoded once; at N >= 12288 64 weight rows per workgroup
+// (X re-read N / 64 times, at least 192 workgroups) with the raw bytes one
+// step ahead, below 16 (two steps ahead).  Above: 64 x 64 tiles (fp32 X:
+// 32 x 64, its fragments take twice the registers), one step ahead.  Deeper
+// rings measured slower on MI355X at every M (Q4_K 14336 x 4096, M = 17:
+// 28.6 us at four steps against 21.3 at one).
+template <int TYPE, int XT, int MA>
+void launch_kq_mid(const uint8_t* w, uint32_t wbytes, const uint8_t* X, uint32_t xbytes, float* Y, int M, int N,
+                   int K, uint32_t rb, hipStream_t st) {
+    if (N >= 12288)
+        launch_kq<TYPE, XT, MA, 4, 1>(w, wbytes, X, xbytes, Y, M, N, K, rb, st);
+    else
+        launch_kq<TYPE, XT, MA, 1, 2>(w, wbytes, X, xbytes, Y, M, N, K, rb, st);
+}
+
 template <int TYPE, int XT>
 void launch_kq_m(const uint8_t* w, uint32_t wbytes, const uint8_t* X, uint32_t xbytes, float* Y, int M, int N, int K,
                  uint32_t rb, hipStream_t st) {
@@ -332,11 +380,11 @@ void launch_kq_m(const uint8_t* w, uint32_t wbytes, const uint8_t* X, uint32_t x
         else
             launch_kq<TYPE, XT, 1, 1, 3>(w, wbytes, X, xbytes, Y, M, N, K, rb, st);
     } else if (M <= 32) {
-        launch_kq<TYPE, XT, 2, 1, 2>(w, wbytes, X, xbytes, Y, M, N, K, rb, st);
+        launch_kq_mid<TYPE, XT, 2>(w, wbytes, X, xbytes, Y, M, N, K, rb, st);
     } else if (M <= 48) {
-        launch_kq<TYPE, XT, 3, 1, 2>(w, wbytes, X, xbytes, Y, M, N, K, rb, st);
+        launch_kq_mid<TYPE, XT, 3>(w, wbytes, X, xbytes, Y, M, N, K, rb, st);
     } else if (M <= 64) {
-        launch_kq<TYPE, XT, 4, 1, 2>(w, wbytes, X, xbytes, Y, M, N, K, rb, st);
+        launch_kq_mid<TYPE, XT, 4>(w, wbytes, X, xbytes, Y, M, N, K, rb, st);
     } else if constexpr (XT == KQ_X_F16) {
         launch_kq<TYPE, XT, 4, 4, 1>(w, wbytes, X, xbytes, Y, M, N, K, rb, st);
     } else {
@@ -351,8 +399,7 @@ void launch_kq_m(const uint8_t* w, uint32_t wbytes, const uint8_t* X, uint32_t x
 int gemm_kq(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, int64_t N, int64_t K, int32_t type,
             hipStream_t st) {
     if (K % KQ_STEP != 0) {
-        set_error("vb_gemm: %s weights need K %% 128 == 0 (K=%lld)", type == TYPE_Q6_K ? "Q6_K" : "Q8_0",
-                  static_cast<long long>(K));
+        set_error("vb_gemm: Q8_0 weights need K %% 128 == 0 (K=%lld)", static_cast<long long>(K));
         return E_UNSUPPORTED;
     }
     const int64_t rb = row_bytes(type, K);
@@ -369,7 +416,12 @@ int gemm_kq(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, 
     const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
     const uint32_t wby = static_cast<uint32_t>(wbytes), xby = static_cast<uint32_t>(xbytes),
                    rbu = static_cast<uint32_t>(rb);
-    if (type == TYPE_Q6_K) {
+    if (type == TYPE_Q4_K) {
+        if (x_dtype == KQ_X_F16)
+            launch_kq_m<TYPE_Q4_K, KQ_X_F16>(wb, wby, xb, xby, Y, m, n, k, rbu, st);
+        else
+            launch_kq_m<TYPE_Q4_K, KQ_X_F32>(wb, wby, xb, xby, Y, m, n, k, rbu, st);
+    } else if (type == TYPE_Q6_K) {
         if (x_dtype == KQ_X_F16)
             launch_kq_m<TYPE_Q6_K, KQ_X_F16>(wb, wby, xb, xby, Y, m, n, k, rbu, st);
         else

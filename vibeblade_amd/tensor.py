@@ -148,7 +148,7 @@ def gemv(w: QTensor, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.
 
 X_F32 = 0
 X_F16 = 1
-GEMM_AUTO, GEMM_SKINNY, GEMM_TILED, GEMM_SPLIT = 0, 1, 2, 3
+GEMM_AUTO, GEMM_SKINNY, GEMM_TILED, GEMM_SPLIT, GEMM_KSPLIT = 0, 1, 2, 3, 4
 
 
 def gemm(w: QTensor, x: torch.Tensor, out: torch.Tensor | None = None,
