@@ -10,19 +10,20 @@
 // of them removed alone saves 8-16 us of ~72 us).  Here the eight waves of
 // a workgroup take two roles, one of each on every SIMD:
 //  * producers (waves 4-7) stream the raw Q4_K bytes of the workgroup's
-//    BN = 16 NF weight rows PD steps ahead, dequantize each 64-element chunk
-//    into fp16 B fragments (natural k order, mfma_q4k.hpp) and store them
-//    into a ring of three LDS buffers, two k-steps ahead of the consumers;
-//  * consumers (waves 0-3) own 64 X rows each: they load their A fragments
-//    straight from global memory (L2) one step ahead into registers, read
-//    the B fragments of the step from LDS (the ks = 1 half under the ks = 0
-//    MFMAs, the next step's ks = 0 half under the ks = 1 MFMAs) and issue
-//    4 x NF MFMAs per 32-element half step.
-// One barrier per step orders the ring: the buffer written during step s
+//    BN = 16 NF weight rows PD steps ahead (a super-block's header once per
+//    four steps), dequantize each 64-element chunk into fp16 B fragments
+//    (natural k order, mfma_q4k.hpp), and stage the workgroup's X tile
+//    (256 rows x 64 fp16 per step, whole 128-byte rows, loaded two steps
+//    ahead into registers); both go into rings of three LDS buffers, two
+//    k-steps ahead of the consumers;
+//  * consumers (waves 0-3) own 64 X rows each: they read the A and B
+//    fragments of a step from LDS (the ks = 1 half under the ks = 0 MFMAs,
+//    the next step's ks = 0 half under the ks = 1 MFMAs) and issue 4 x NF
+//    MFMAs per 32-element half step.
+// One barrier per step orders the rings: the buffer written during step s
 // (that of step s + 2) was last read during steps s - 2 and s - 1, before
 // the barrier that ends step s - 1, and is read from step s + 1 on, after
-// the barrier that ends step s.  The MFMA pipe of each SIMD is fed by its
-// consumer while the producer's VALU work and memory traffic run beside it.
+// the barrier that ends step s.
 //
 // Tile: 256 X rows x 112 weight rows (NF = 7): at N = 14336 that is 128
 // column tiles, so M = 512 runs exactly 256 workgroups, one per CU.
@@ -49,9 +50,9 @@ __global__ void __launch_bounds__(NTHR) gemm_q4k_split_kernel(const uint8_t* __r
     constexpr int BUF = 2 * (NF + 1) * 64;     // uint4 per ring buffer: [ks][fragment][lane]
     // fragment NF of each half takes the stores of producer threads without
     // a unit (keeps their code branch-free)
-    constexpr int XBUF = 64 * 128;            // bytes of one consumer's X ring buffer
+    constexpr int XBUF = TM * 128;            // bytes of one X ring buffer (256 rows x 64 fp16)
     __shared__ uint4 bt[3 * BUF];
-    __shared__ uint4 xring[CW * 3 * XBUF / 16];
+    __shared__ uint4 xring[3 * XBUF / 16];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(tid >> 6));
@@ -70,38 +71,9 @@ __global__ void __launch_bounds__(NTHR) gemm_q4k_split_kernel(const uint8_t* __r
     const int nsteps = K / 64;  // a multiple of 4
 
     if (wave < CW) {
-        // ---- consumer: X rows mt0 + 64 wave + [0, 64) ----
-        // X reaches the MFMAs through a wave-private ring of three LDS
-        // buffers (64 rows x 128 bytes each, 16-byte pieces XOR-swizzled by
-        // (row / 2) % 8): whole 128-byte rows are loaded two steps ahead
-        // (lane L of load i: row 8 i + L / 8, piece L % 8), stored at the end
-        // of the step, and read back as A fragments.  Only this wave touches
-        // its ring, and one wave's LDS operations complete in order, so the
-        // ring needs no barrier.
+        // ---- consumer: X rows mt0 + 64 wave + [0, 64) of the X ring ----
         const int j = lane & 15, g = lane >> 4;
-        uint8_t* const xs = reinterpret_cast<uint8_t*>(xring) + wave * (3 * XBUF);
-        // rows past M read zeros (the resource ends at row M) and are never stored
-        const int xr0 = mt0 + 64 * wave;
-        const int xrows = M - xr0 < 64 ? M - xr0 : 64;
-        const __amdgpu_buffer_rsrc_t xrs =
-            make_rsrc(xrows > 0 ? X + static_cast<uint32_t>(xr0) * static_cast<uint32_t>(K) * 2u : X,
-                      xrows > 0 ? static_cast<uint32_t>(xrows) * static_cast<uint32_t>(K) * 2u : 0u);
-        const int lr = lane >> 3, p = lane & 7;
-        const uint32_t xv = (static_cast<uint32_t>(lr) * static_cast<uint32_t>(K) + 8u * static_cast<uint32_t>(p)) * 2u;
-        // row 8 i + lr: its swizzle (4 i + lr / 2) % 8 is lr / 2, xor 4 for odd i
-        const int xst0 = 128 * lr + 16 * (p ^ (lr >> 1)), xst1 = 128 * lr + 16 * (p ^ (lr >> 1) ^ 4);
-        u32x4 xr[8];
-        auto load_x = [&](int step) {
-            step = step < nsteps ? step : nsteps - 1;
-            const uint32_t ko = static_cast<uint32_t>(step) * 128u;
-#pragma unroll
-            for (int i = 0; i < 8; i++) xr[i] = buf_ld128(xrs, xv, ko + static_cast<uint32_t>(i) * 16u * static_cast<uint32_t>(K));
-        };
-        auto store_x = [&](int buf) {
-#pragma unroll
-            for (int i = 0; i < 8; i++)
-                *reinterpret_cast<u32x4*>(xs + buf * XBUF + 1024 * i + ((i & 1) ? xst1 : xst0)) = xr[i];
-        };
+        const uint8_t* const xs = reinterpret_cast<const uint8_t*>(xring) + wave * (64 * 128);
         // A fragment (a, ks): row 16 a + j, piece 4 ks + g; (16 a + j) / 2 % 8
         // does not depend on a
         const int aoff[2] = {16 * (j * 8 + (g ^ ((j >> 1) & 7))), 16 * (j * 8 + ((4 + g) ^ ((j >> 1) & 7)))};
@@ -132,20 +104,15 @@ __global__ void __launch_bounds__(NTHR) gemm_q4k_split_kernel(const uint8_t* __r
                 for (int f = 0; f < NF; f++) acc[a][f] = mfma16x16x32(af[a], b[f], acc[a][f]);
         };
 
-        load_x(0);
-        store_x(0);
-        load_x(1);
-        store_x(1);
-        __syncthreads();  // B ring buffers 0 and 1 (steps 0, 1) written
+        __syncthreads();  // ring buffers 0 and 1 (steps 0, 1) written
         Frag b0[NF], a0[4];
         read_b(0, 0, b0);
         read_a(0, 0, a0);
-        int bc = 0, bn = 1, bw = 2;  // ring buffers of steps s, s + 1, s + 2
+        int bc = 0, bn = 1;  // ring buffers of steps s, s + 1
         for (int step = 0; step < nsteps; step++) {
             // fences keep each group of reads ahead of the MFMAs it is meant
             // to overlap (the scheduler would sink them) and the MFMAs ahead
             // of the barrier (it would hoist them past)
-            load_x(step + 2);  // past the last step: repeats it, unused
             Frag b1[NF], a1[4];
             read_b(bc, 1, b1);
             read_a(bc, 1, a1);
@@ -157,11 +124,9 @@ __global__ void __launch_bounds__(NTHR) gemm_q4k_split_kernel(const uint8_t* __r
             __builtin_amdgcn_sched_barrier(0);
             mfmas(a1, b1);
             __builtin_amdgcn_sched_barrier(0);
-            store_x(bw);
             __syncthreads();
             bc = bn;
-            bn = bw;
-            bw = bw == 2 ? 0 : bw + 1;
+            bn = bn == 2 ? 0 : bn + 1;
         }
 
 #pragma unroll
@@ -226,10 +191,40 @@ __global__ void __launch_bounds__(NTHR) gemm_q4k_split_kernel(const uint8_t* __r
                 dst[(NF + 1) * 64 + uslot[i]] = make_uint4(hi.u[0], hi.u[1], hi.u[2], hi.u[3]);
             }
         };
+        // X tile pieces q = ptid + PT i (i < 8): row q / 8 = ptid / 8 + 32 i,
+        // 16-byte piece q % 8; rows past M read zeros (the resource ends at
+        // row M).  Ring layout: 128-byte rows, pieces XOR-swizzled by
+        // (row / 2) % 8 = (ptid / 16) % 8 for every i.
+        const int xrows = M - mt0 < TM ? M - mt0 : TM;
+        const __amdgpu_buffer_rsrc_t xrs =
+            make_rsrc(X + static_cast<uint32_t>(mt0) * static_cast<uint32_t>(K) * 2u,
+                      static_cast<uint32_t>(xrows) * static_cast<uint32_t>(K) * 2u);
+        const int xp = ptid & 7;
+        const uint32_t xv = (static_cast<uint32_t>(ptid >> 3) * static_cast<uint32_t>(K) + 8u * static_cast<uint32_t>(xp)) * 2u;
+        const int xst = (ptid >> 3) * 128 + 16 * (xp ^ ((ptid >> 4) & 7));
+        u32x4 xr[2][8];
+        auto load_x = [&](int step, int slot) {
+            step = step < nsteps ? step : nsteps - 1;
+            const uint32_t ko = static_cast<uint32_t>(step) * 128u;
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                xr[slot][i] = buf_ld128(xrs, xv, ko + static_cast<uint32_t>(i) * 64u * static_cast<uint32_t>(K));
+        };
+        auto store_x = [&](int slot, int buf) {
+            uint8_t* xs = reinterpret_cast<uint8_t*>(xring) + buf * XBUF;
+#pragma unroll
+            for (int i = 0; i < 8; i++) *reinterpret_cast<u32x4*>(xs + xst + i * 32 * 128) = xr[slot][i];
+        };
+        load_x(0, 0);
+        load_x(1, 1);
         load_hd(0, 0);
         load_hd(1, 1);
 #pragma unroll
         for (int r = 0; r < PD; r++) load_qs(r, r);
+        store_x(0, 0);
+        load_x(2, 0);
+        store_x(1, 1);
+        load_x(3, 1);
         dequant_store(0, 0, 0, 0);
         load_qs(PD, 0);
         dequant_store(1, 0, 1, 1);
@@ -251,6 +246,8 @@ __global__ void __launch_bounds__(NTHR) gemm_q4k_split_kernel(const uint8_t* __r
                 // step's dequant in its step: hoisted together, the steps'
                 // dequant would wait for all the prefetched loads.
                 __builtin_amdgcn_sched_barrier(0);
+                store_x(r & 1, bw);  // X of step + 2 sits in register slot (step + 2) % 2 = r % 2
+                load_x(step + 4, r & 1);
                 dequant_store((r + 2) & 3, ((r + 2) >> 2) & 1, (r + 2) % PD, bw);
                 load_qs(step + 2 + PD, (r + 2) % PD);
                 if (r == 2) load_hd((s0 >> 2) + 2, 0);
