@@ -70,7 +70,7 @@ def parse():
                    help="comma list of extra workloads: " + ",".join(EXTRA_ALL))
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--pmc-pass", nargs="?", const="gemv", choices=["gemv", "gemm8", "gemm512"],
+    p.add_argument("--pmc-pass", nargs="?", const="gemv", choices=["gemv", "lmhead", "down", "gemm8", "gemm512"],
                    help="eager launches for rocprofv3 --pmc: 32 headline GEMVs (gemv) or 16 Q4_K GEMMs "
                         "14336x4096 at M=8 / 512 (gemm8, gemm512), then a 256 MiB copy (torch.neg) "
                         "that calibrates FETCH_SIZE / WRITE_SIZE")
@@ -604,15 +604,22 @@ def pmc_pass(workload="gemv"):
     qtype, n, k = ggml.GGML_TYPE_Q4_K, 14336, 4096
     lib = _lib.load()
     st = torch.cuda.current_stream().cuda_stream
-    if workload == "gemv":
+    if workload in ("gemv", "lmhead", "down"):
+        if workload == "lmhead":  # Q6_K output projection 128256 x 4096, 2 copies (862 MB)
+            qtype, n, ncop = ggml.GGML_TYPE_Q6_K, 128256, 2
+        elif workload == "down":  # Q4_K 4096 x 14336
+            n, k, ncop = 4096, 14336, NCOPIES
+        else:
+            ncop = NCOPIES
         gen = torch.Generator(device="cuda").manual_seed(SEED)
-        copies = make_copies(qtype, n, k, NCOPIES, gen)
+        copies = make_copies(qtype, n, k, ncop, gen)
         x = torch.randn(k, generator=gen, device="cuda")
         y = torch.empty(n, device="cuda")
-        for i in range(32):
-            c = copies[i % NCOPIES]
+        ndisp = 8 if workload == "lmhead" else 32
+        for i in range(ndisp):
+            c = copies[i % ncop]
             _lib.check("vb_gemv", lib.vb_gemv(c.ptr(), x.data_ptr(), y.data_ptr(), n, k, qtype, st))
-        what = "32 GEMV dispatches"
+        what = f"{ndisp} GEMV dispatches ({workload})"
     else:
         m = 8 if workload == "gemm8" else 512
         gen = torch.Generator(device="cuda").manual_seed(SEED + m)
