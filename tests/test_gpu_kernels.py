@@ -324,6 +324,49 @@ def test_gemv_q4k_short_k_idle_lanes(rows, k):
     assert np.max(np.abs(y - want)) <= 1e-3 * np.abs(want).max() + 1e-6
 
 
+# ---- the split-row Q4_K kernel (4096 < k <= 16384, rows over 2/4/8 waves) --
+
+# (rows, k): 2 slices per row up to 112 units (k = 7168), 4 up to 224
+# (k = 14336), 8 above; rows per wave from 1 to 8 on 256 CUs (2048, 1024 and
+# 512 row groups), ragged row counts, a last slice of 4 units (k = 14592)
+SPLIT_SHAPES = [(1, 4352), (2049, 4352), (16384, 7168), (10000, 7168), (7, 7424), (3000, 7424),
+                (4096, 14336), (8192, 14336), (1000, 14592), (513, 16384), (4096, 16384)]
+
+
+@pytest.mark.parametrize("rows,k", SPLIT_SHAPES)
+def test_gemv_q4k_split_rows(rows, k):
+    qt, x = _q4k_case(rows, k, rows + k)
+    y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy()
+    want = O.gemv(qt.to_numpy_bytes(), x, rows, k, qt.qtype)
+    assert O.rel_l2(y, want) <= GEMV_TOL
+    assert np.max(np.abs(y - want)) <= 1e-3 * np.abs(want).max() + 1e-6  # no row or slice dropped
+
+
+@pytest.mark.parametrize("rows,k", [(8193, 14336), (300, 16640)])
+def test_gemv_q4k_split_declines(rows, k):
+    """Past 8 rows per wave or 256 units the general kernel takes the launch."""
+    qt, x = _q4k_case(rows, k, rows + k)
+    y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy()
+    want = O.gemv(qt.to_numpy_bytes(), x, rows, k, qt.qtype)
+    assert O.rel_l2(y, want) <= GEMV_TOL
+
+
+def test_gemv_q4k_split_matches_general_kernel(knob):
+    """The split-row kernel and the general v_dot4 kernel agree at the FFN
+    down shape (4096 x 14336), both close to the oracle; repeated launches
+    are bit-identical (fixed-order slice sums)."""
+    rows, k = 4096, 14336
+    gen = torch.Generator(device="cuda").manual_seed(78)
+    qt = QTensor.quantize(torch.randn((rows, k), generator=gen, device="cuda") * 0.02, ggml.GGML_TYPE_Q4_K)
+    x = torch.randn(k, generator=gen, device="cuda")
+    y_split = gemv(qt, x).cpu().numpy()
+    assert np.array_equal(bits(gemv(qt, x).cpu().numpy()), bits(y_split))
+    knob("VB_GEMV_Q4K_PATH", "dot")
+    y_gen = gemv(qt, x).cpu().numpy()
+    want = O.gemv(qt.to_numpy_bytes(), x.cpu().numpy(), rows, k, qt.qtype)
+    assert O.rel_l2(y_split, want) <= 2e-4 and O.rel_l2(y_gen, want) <= 2e-4
+
+
 def test_gemv_q4k_short_matches_general_kernel(knob):
     """The short-row kernel and the general v_dot4 kernel agree at the
     headline shape (both against the oracle; 16-bit vs 15-bit x encodings)."""

@@ -521,6 +521,11 @@ int gemv_dispatch_fused(const void* w, const RowSrc& src, const GemvFuse& fz, co
         // short rows (k <= 4096) at <= 8 rows per wave: the dedicated kernel
         if (plain && !knobs().gemv_q4k_general && k <= 4096 && gemv_q4k_rpw(n) > 0)
             return gemv_q4k_short(w, x, y, n, k, st);
+        // split rows (4096 < k <= 16384), plain or with the residual epilogue
+        const bool resid_only = !fz.norm_w && fz.act < 0 && !src.dense_pairs && !src.n_dev && !src.gidx &&
+                                src.zn == 0;
+        if (resid_only && !knobs().gemv_q4k_general && k > 4096 && k % 256 == 0 && gemv_q4k_split_rpw(n, k) > 0)
+            return gemv_q4k_split(w, x, y, fz.resid, n, k, st);
         return launch_gemv_q<TYPE_Q4_K>(w, src, fz, x, y, n, k, rb, st);
     }
     case TYPE_Q6_K: return launch_gemv_q<TYPE_Q6_K>(w, src, fz, x, y, n, k, rb, st);

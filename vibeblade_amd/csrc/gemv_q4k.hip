@@ -74,7 +74,9 @@ __device__ __forceinline__ int dpp_mov_i(int v) {
 
 // Task t = 8 consecutive elements (part p = t % 8) of unit t / 8; the 8
 // tasks of a unit sit on adjacent lanes.  Units at or past `units` encode
-// as zeros (their lanes contribute nothing).
+// as zeros (their lanes contribute nothing).  US is the unit stride of the
+// encoding (the most units it holds).
+template <int US = UNITS_MAX>
 __device__ __forceinline__ void encode_task(const float* v_in, int task, int units, uint4* xq, bool store = true) {
     const int u = task >> 3, p = task & 7;
     float v[8];
@@ -106,27 +108,28 @@ __device__ __forceinline__ void encode_task(const float* v_in, int task, int uni
     const int isum1 = dpp_mov_i<0x141>(isum);   // part 0 reads run 1's sum from part 7
     if (!store) return;
     uint4* b = xq + u;
-    reinterpret_cast<uint2*>(&b[(p >> 1) * UNITS_MAX])[p & 1] = make_uint2(ph[0], ph[1]);
-    reinterpret_cast<uint2*>(&b[(4 + (p >> 1)) * UNITS_MAX])[p & 1] = make_uint2(pl[0], pl[1]);
+    reinterpret_cast<uint2*>(&b[(p >> 1) * US])[p & 1] = make_uint2(ph[0], ph[1]);
+    reinterpret_cast<uint2*>(&b[(4 + (p >> 1)) * US])[p & 1] = make_uint2(pl[0], pl[1]);
     if (p == 0) {
         uint4 m;
         m.x = __float_as_uint(amax / static_cast<float>(X15_MAX));
         m.y = static_cast<uint32_t>(isum);
         m.z = static_cast<uint32_t>(isum1);
         m.w = static_cast<uint32_t>(128 * isum1);
-        b[8 * UNITS_MAX] = m;
+        b[8 * US] = m;
     }
 }
 
+template <int US = UNITS_MAX>
 __device__ __forceinline__ XU read_unit(const uint4* xq, int u) {
     XU x;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const uint4 h = xq[i * UNITS_MAX + u], l = xq[(4 + i) * UNITS_MAX + u];
+        const uint4 h = xq[i * US + u], l = xq[(4 + i) * US + u];
         x.h[4 * i] = h.x; x.h[4 * i + 1] = h.y; x.h[4 * i + 2] = h.z; x.h[4 * i + 3] = h.w;
         x.l[4 * i] = l.x; x.l[4 * i + 1] = l.y; x.l[4 * i + 2] = l.z; x.l[4 * i + 3] = l.w;
     }
-    const uint4 m = xq[8 * UNITS_MAX + u];
+    const uint4 m = xq[8 * US + u];
     x.s = __uint_as_float(m.x);
     x.i0 = static_cast<int>(m.y);
     x.i1 = static_cast<int>(m.z);
@@ -314,6 +317,148 @@ __global__ void __launch_bounds__(64 * WPG) gemv_q4k_kernel(const uint8_t* __res
     if ((lane & 7) == 0 && r < RPW && row0 + r < n) y[row0 + r] = tot;
 }
 
+// ---- split rows: 64 < units <= 256 (4096 < k <= 16384) ------------------------
+//
+// A row is split into SL slices of upw units (upw a multiple of 4, so slices
+// start on super-block boundaries, 36 upw bytes each, upw <= 56); a 16-wave
+// workgroup is 16 / SL row groups x SL slices, and wave (group, slice) takes
+// slice `slice` of the group's RPW rows.  Per row the wave reads its slice
+// contiguously (two 16-byte pieces per lane: at most 128 slots, 2016 B for 56
+// units, fill the wave's 128-slot buffer), stages it through its
+// LDS buffer and computes one unit per lane with the short kernel's
+// arithmetic; the activation encoding covers all units of x.  Each wave
+// reduces its rows at once (reduce8), the slices of a row meet in LDS and are
+// added in slice order, and resid (optional, may be y) is added as y is
+// written.
+constexpr int SPLIT_US = 256;  // unit stride of the encoding (units <= 256)
+
+template <int RPW, int NS, int SL>
+__global__ void __launch_bounds__(1024) gemv_q4k_split_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                                              float* y, const float* resid, int n, int units, int upw,
+                                                              uint32_t rb) {
+    constexpr int WPG = 16;
+    constexpr int NG = WPG / SL;  // row groups per workgroup
+    __shared__ uint4 xq[XQ_UNIT_QUADS * SPLIT_US];
+    __shared__ u32x4 rowbuf[WPG][128];
+    __shared__ float red[NG][SL][8];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int grp = wave / SL, slc = wave - grp * SL;
+    const int row0 = (static_cast<int>(blockIdx.x) * NG + grp) * RPW;
+    const int rlast = n - 1;
+    const int rbase = row0 < rlast ? row0 : rlast;
+    // this wave's slice: units [u0, u0 + su) of each row, bytes [36 u0, +36 su)
+    const int u0 = slc * upw;
+    const int su = units - u0 < upw ? units - u0 : upw;  // >= 4 by the host's choice of SL
+    const uint8_t* wb = w + static_cast<int64_t>(rbase) * rb + 36u * static_cast<uint32_t>(u0);
+    const int64_t span64 = static_cast<int64_t>(n - rbase) * rb - 36 * static_cast<int64_t>(u0);
+    const uint32_t span = span64 < 0xFFFFFFFFll ? static_cast<uint32_t>(span64) : 0xFFFFFFFFu;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(wb, span);
+    const bool valid = lane < su;
+    const int u = valid ? lane : (lane & 3);  // idle lanes read unit (lane % 4) of the slice, discarded
+    const int sslots = 9 * su / 4;            // 16-byte slots of the slice
+    const uint32_t va = 16u * static_cast<uint32_t>(lane < sslots ? lane : lane & 7);
+    const uint32_t vb = 16u * static_cast<uint32_t>(64 + lane < sslots ? 64 + lane : lane & 7);
+    u32x4* rbuf = rowbuf[wave];
+    const int sh = 9 * (u >> 2), sq = sh + 1 + 2 * (u & 3);
+
+    auto soff = [&](int s) -> uint32_t {
+        int r = row0 + s;
+        r = r < rlast ? r : rlast;
+        return static_cast<uint32_t>(r - rbase) * rb;
+    };
+    struct Raw2 { u32x4 a, b; };
+    auto issue = [&](Raw2& b, int s) {
+        const uint32_t so = soff(s);
+        b.a = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(va), static_cast<int>(so), CACHE_NT);
+        b.b = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(vb), static_cast<int>(so), CACHE_NT);
+    };
+    auto stage = [&](const Raw2& b) -> RowBuf {
+        rbuf[lane] = b.a;
+        rbuf[64 + lane] = b.b;
+        RowBuf r;
+        r.hdr = rbuf[sh];
+        r.qa = rbuf[sq];
+        r.qb = rbuf[sq + 1];
+        return r;
+    };
+
+    // x first (8 tasks per unit, up to 2048 tasks: 2 per thread), then the
+    // first rows' weights, then the branch-free encode
+    float xv[2][8];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const int task = static_cast<int>(threadIdx.x) + 1024 * t;
+        const int tu = task >> 3;
+        const int off = (tu < units ? tu : units - 1) * 64 + 8 * (task & 7);
+        const float4 a = *reinterpret_cast<const float4*>(x + off);
+        const float4 b = *reinterpret_cast<const float4*>(x + off + 4);
+        xv[t][0] = a.x; xv[t][1] = a.y; xv[t][2] = a.z; xv[t][3] = a.w;
+        xv[t][4] = b.x; xv[t][5] = b.y; xv[t][6] = b.z; xv[t][7] = b.w;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    Raw2 ring[NS];
+#pragma unroll
+    for (int s = 0; s < NS - 1 && s < RPW; s++) issue(ring[s], s);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < 2; t++) encode_task<SPLIT_US>(xv[t], static_cast<int>(threadIdx.x) + 1024 * t, units, xq);
+    __syncthreads();
+    const XU xu = read_unit<SPLIT_US>(xq, u0 + u);
+    const ScaleSel ss = make_sel(u & 3);
+
+    float acc[8];
+#pragma unroll
+    for (int s = 0; s < 8; s++) acc[s] = 0.f;
+#pragma unroll
+    for (int s = 0; s < RPW; s++) {
+        if (s + NS - 1 < RPW) issue(ring[(s + NS - 1) % NS], s + NS - 1);
+        const float part = row_part(stage(ring[s % NS]), xu, ss);
+        acc[s] = valid ? part : 0.f;  // idle lanes: nothing, even from a non-finite scale
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    const float tot = reduce8(acc);
+    const int g8 = lane >> 3;
+    const int rr = row_of_group(g8);
+    if ((lane & 7) == 0 && rr < RPW) red[grp][slc][rr] = tot;
+    __syncthreads();
+    if (threadIdx.x < NG * RPW) {
+        const int gq = static_cast<int>(threadIdx.x) / RPW, r = static_cast<int>(threadIdx.x) - gq * RPW;
+        const int row = (static_cast<int>(blockIdx.x) * NG + gq) * RPW + r;
+        if (row < n) {
+            float v = 0.f;
+#pragma unroll
+            for (int j = 0; j < SL; j++) v += red[gq][j][r];
+            y[row] = resid ? v + resid[row] : v;  // resid may be y: read before the write
+        }
+    }
+}
+
+template <int RPW, int SL>
+void launch_split(const void* w, const float* x, float* y, const float* resid, int n, int units, int upw,
+                  uint32_t rb, hipStream_t st) {
+    constexpr int NG = 16 / SL;
+    constexpr int NS = RPW < 3 ? RPW + 1 : 3;  // ring: NS - 1 rows in flight while computing
+    const int grid = (n + NG * RPW - 1) / (NG * RPW);
+    gemv_q4k_split_kernel<RPW, NS, SL><<<dim3(static_cast<uint32_t>(grid)), dim3(1024), 0, st>>>(
+        static_cast<const uint8_t*>(w), x, y, resid, n, units, upw, rb);
+}
+
+template <int SL>
+void launch_split_rpw(int rpw, const void* w, const float* x, float* y, const float* resid, int n, int units,
+                      int upw, uint32_t rb, hipStream_t st) {
+    switch (rpw) {
+    case 1: launch_split<1, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 2: launch_split<2, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 3: launch_split<3, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 4: launch_split<4, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 5: launch_split<5, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 6: launch_split<6, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 7: launch_split<7, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    default: launch_split<8, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    }
+}
+
 template <int RPW, int NS, int WPG>
 void launch(const void* w, const float* x, float* y, int n, int units, uint32_t rb, hipStream_t st) {
     const int grid = (n + WPG * RPW - 1) / (WPG * RPW);
@@ -393,6 +538,50 @@ int gemv_q4k_short(const void* w, const float* x, float* y, int64_t n, int64_t k
         else if (ring == 2) launch_rpw<3, 16>(sh.rpw, w, x, y, ni, units, rb, st);
         else launch_rpw<4, 16>(sh.rpw, w, x, y, ni, units, rb, st);
     }
+    return check_launch("vb_gemv");
+}
+
+// Split-row shape: slices per row (2 up to 112 units, 4 up to 224, 8 above,
+// so that a slice is at most 56 units; 16-wave workgroups of 8, 4 or 2 row
+// groups) and rows per wave, one workgroup per CU when that covers n; 0 rows
+// per wave past 8 or for a last slice under 4 units (the caller then takes
+// the general kernel).
+struct SplitShape { int sl, upw, rpw; };
+
+SplitShape split_shape(int64_t n, int units) {
+    SplitShape s{units <= 112 ? 2 : (units <= 224 ? 4 : 8), 0, 0};
+    s.upw = ((units + s.sl - 1) / s.sl + 3) & ~3;
+    const int64_t groups = static_cast<int64_t>(num_cus()) * (16 / s.sl);
+    const int64_t rpw = (n + groups - 1) / groups;
+    s.rpw = rpw <= 8 ? static_cast<int>(rpw < 1 ? 1 : rpw) : 0;
+    if (s.upw > 56 || units - (s.sl - 1) * s.upw < 4) s.rpw = 0;
+    return s;
+}
+
+int gemv_q4k_split_rpw(int64_t n, int64_t k) {
+    const int units = static_cast<int>(k / 64);
+    return units > UNITS_MAX && units <= SPLIT_US ? split_shape(n, units).rpw : 0;
+}
+
+// Plain or residual-epilogue Q4_K GEMV, 4096 < k <= 16384, k % 256 == 0, at
+// most 8 rows per wave; arguments validated by gemv_dispatch_fused.
+int gemv_q4k_split(const void* w, const float* x, float* y, const float* resid, int64_t n, int64_t k,
+                   hipStream_t st) {
+    const int units = static_cast<int>(k / 64);
+    const SplitShape sh = split_shape(n, units);
+    if (sh.rpw == 0 || units <= UNITS_MAX || units > SPLIT_US || k % 256 != 0 || n > INT32_MAX) {
+        set_error("vb_gemv: internal: Q4_K split-row kernel shape (n=%lld, k=%lld)", static_cast<long long>(n),
+                  static_cast<long long>(k));
+        return E_INVAL;
+    }
+    const uint32_t rb = static_cast<uint32_t>(row_bytes(TYPE_Q4_K, k));
+    const int ni = static_cast<int>(n);
+    if (sh.sl == 2)
+        launch_split_rpw<2>(sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
+    else if (sh.sl == 4)
+        launch_split_rpw<4>(sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
+    else
+        launch_split_rpw<8>(sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
     return check_launch("vb_gemv");
 }
 

@@ -84,6 +84,11 @@ int gemv_dispatch_fused(const void* w, const RowSrc& src, const GemvFuse& fz, co
 // gemv_q4k_rpw(n) is its rows per wave, 0 when n is too large for it.
 int gemv_q4k_rpw(int64_t n);
 int gemv_q4k_short(const void* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t st);
+// Plain or residual-epilogue Q4_K GEMV for 4096 < k <= 16384, rows split over
+// 2, 4 or 8 waves (gemv_q4k.hip); gemv_q4k_split_rpw is 0 for shapes it does not take.
+int gemv_q4k_split_rpw(int64_t n, int64_t k);
+int gemv_q4k_split(const void* w, const float* x, float* y, const float* resid, int64_t n, int64_t k,
+                   hipStream_t st);
 // Q4_K M=1 GEMV on the int8 matrix cores (gemv_q4k_mfma.hip); arguments
 // already validated by gemv_dispatch_src.
 int gemv_q4k_mfma(const void* w, const RowSrc& src, const float* x, float* y, int64_t n, int64_t k,
