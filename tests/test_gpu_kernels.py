@@ -342,6 +342,20 @@ def test_gemv_q4k_split_rows(rows, k):
     assert np.max(np.abs(y - want)) <= 1e-3 * np.abs(want).max() + 1e-6  # no row or slice dropped
 
 
+@pytest.mark.parametrize("cfg", ["2,1", "2,3", "4,1", "4,4", "8,2", "8,3"])
+def test_gemv_q4k_split_knob(knob, cfg):
+    """VB_GEMV_SPLIT="slices,rows in flight": every ring depth at 2, 4 and 8
+    slices per row (2 slices of 112-unit rows exceed a 56-unit slice, so
+    k = 14336 then takes the general kernel)."""
+    knob("VB_GEMV_SPLIT", cfg)
+    for rows, k in ((5000, 7168), (4096, 14336)):
+        qt, x = _q4k_case(rows, k, rows + k + 1)
+        y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy()
+        want = O.gemv(qt.to_numpy_bytes(), x, rows, k, qt.qtype)
+        assert O.rel_l2(y, want) <= GEMV_TOL, (cfg, rows, k)
+        assert np.max(np.abs(y - want)) <= 1e-3 * np.abs(want).max() + 1e-6
+
+
 @pytest.mark.parametrize("rows,k", [(8193, 14336), (300, 16640)])
 def test_gemv_q4k_split_declines(rows, k):
     """Past 8 rows per wave or 256 units the general kernel takes the launch."""

@@ -434,28 +434,39 @@ __global__ void __launch_bounds__(1024) gemv_q4k_split_kernel(const uint8_t* __r
     }
 }
 
-template <int RPW, int SL>
+template <int RPW, int D, int SL>
 void launch_split(const void* w, const float* x, float* y, const float* resid, int n, int units, int upw,
                   uint32_t rb, hipStream_t st) {
     constexpr int NG = 16 / SL;
-    constexpr int NS = RPW < 3 ? RPW + 1 : 3;  // ring: NS - 1 rows in flight while computing
+    constexpr int NS = (RPW < D ? RPW : D) + 1;  // ring: NS - 1 (at most D) rows in flight while computing
     const int grid = (n + NG * RPW - 1) / (NG * RPW);
     gemv_q4k_split_kernel<RPW, NS, SL><<<dim3(static_cast<uint32_t>(grid)), dim3(1024), 0, st>>>(
         static_cast<const uint8_t*>(w), x, y, resid, n, units, upw, rb);
 }
 
-template <int SL>
+template <int D, int SL>
 void launch_split_rpw(int rpw, const void* w, const float* x, float* y, const float* resid, int n, int units,
                       int upw, uint32_t rb, hipStream_t st) {
     switch (rpw) {
-    case 1: launch_split<1, SL>(w, x, y, resid, n, units, upw, rb, st); break;
-    case 2: launch_split<2, SL>(w, x, y, resid, n, units, upw, rb, st); break;
-    case 3: launch_split<3, SL>(w, x, y, resid, n, units, upw, rb, st); break;
-    case 4: launch_split<4, SL>(w, x, y, resid, n, units, upw, rb, st); break;
-    case 5: launch_split<5, SL>(w, x, y, resid, n, units, upw, rb, st); break;
-    case 6: launch_split<6, SL>(w, x, y, resid, n, units, upw, rb, st); break;
-    case 7: launch_split<7, SL>(w, x, y, resid, n, units, upw, rb, st); break;
-    default: launch_split<8, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 1: launch_split<1, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 2: launch_split<2, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 3: launch_split<3, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 4: launch_split<4, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 5: launch_split<5, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 6: launch_split<6, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 7: launch_split<7, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    default: launch_split<8, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    }
+}
+
+template <int SL>
+void launch_split_d(int d, int rpw, const void* w, const float* x, float* y, const float* resid, int n, int units,
+                    int upw, uint32_t rb, hipStream_t st) {
+    switch (d) {
+    case 1: launch_split_rpw<1, SL>(rpw, w, x, y, resid, n, units, upw, rb, st); break;
+    case 3: launch_split_rpw<3, SL>(rpw, w, x, y, resid, n, units, upw, rb, st); break;
+    case 4: launch_split_rpw<4, SL>(rpw, w, x, y, resid, n, units, upw, rb, st); break;
+    default: launch_split_rpw<2, SL>(rpw, w, x, y, resid, n, units, upw, rb, st); break;
     }
 }
 
@@ -550,6 +561,7 @@ struct SplitShape { int sl, upw, rpw; };
 
 SplitShape split_shape(int64_t n, int units) {
     SplitShape s{units <= 112 ? 2 : (units <= 224 ? 4 : 8), 0, 0};
+    if (knobs().gemv_split_sl) s.sl = knobs().gemv_split_sl;
     s.upw = ((units + s.sl - 1) / s.sl + 3) & ~3;
     const int64_t groups = static_cast<int64_t>(num_cus()) * (16 / s.sl);
     const int64_t rpw = (n + groups - 1) / groups;
@@ -576,12 +588,13 @@ int gemv_q4k_split(const void* w, const float* x, float* y, const float* resid, 
     }
     const uint32_t rb = static_cast<uint32_t>(row_bytes(TYPE_Q4_K, k));
     const int ni = static_cast<int>(n);
+    const int d = knobs().gemv_split_d;
     if (sh.sl == 2)
-        launch_split_rpw<2>(sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
+        launch_split_d<2>(d, sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
     else if (sh.sl == 4)
-        launch_split_rpw<4>(sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
+        launch_split_d<4>(d, sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
     else
-        launch_split_rpw<8>(sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
+        launch_split_d<8>(d, sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
     return check_launch("vb_gemv");
 }
 

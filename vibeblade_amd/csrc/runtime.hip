@@ -63,6 +63,13 @@ Knobs read_knobs() {
             k.gemm_tile_nf = c;
         }
     }
+    if (const char* e = std::getenv("VB_GEMV_SPLIT")) {
+        int a = 0, b = 0;
+        if (std::sscanf(e, "%d,%d", &a, &b) == 2 && (a == 2 || a == 4 || a == 8) && b >= 1 && b <= 4) {
+            k.gemv_split_sl = a;
+            k.gemv_split_d = b;
+        }
+    }
     if (const char* e = std::getenv("VB_GEMM_SPLIT_MIN_M")) {
         const int v = std::atoi(e);
         if (v >= 0) k.gemm_split_min_m = v;

@@ -14,6 +14,7 @@ namespace vb {
 //   VB_GEMM_NF=6|8                            tiled GEMM columns per workgroup
 //   VB_GEMM_TILE="wm,wn,nf"                   tiled GEMM tile configuration
 //   VB_GEMM_SPLIT_MIN_M=m                     smallest M (up to 768) on the role-split GEMM (0: never)
+//   VB_GEMV_SPLIT="sl,d"                      split-row Q4_K GEMV: slices per row (2, 4, 8), rows in flight (1-4)
 //   VB_SPARSE_FUSED=0, VB_SPARSE_NPW=2        sparse FFN kernel choice
 // Zero / false means "no override".
 struct Knobs {
@@ -25,6 +26,7 @@ struct Knobs {
     int gemm_nf = 0;
     int gemm_tile_wm = 0, gemm_tile_wn = 0, gemm_tile_nf = 0;
     int gemm_split_min_m = -1;  // smallest M on the role-split kernel (-1: default)
+    int gemv_split_sl = 0, gemv_split_d = 0;  // split-row Q4_K GEMV: slices per row, rows in flight
     bool sparse_fused = true;
     int sparse_npw = 0;
 };
