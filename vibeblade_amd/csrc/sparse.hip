@@ -323,17 +323,19 @@ __global__ void __launch_bounds__(1024) sparse_reduce_kernel(const float* __rest
     const int nblk = n_dev ? (active_count(nblk_bound * per_blk, n_dev) + per_blk - 1) / per_blk : nblk_bound;
     const int c = threadIdx.x & 63, bg = threadIdx.x >> 6;
     const int col = static_cast<int>(blockIdx.x) * 64 + c;
-    // every load of a round of 8 is issued before the adds (fixed order)
+    // every load of a round of 16 (up to 256 partials: one round at config
+    // shapes) is issued before the adds, which run in partial order
+    // bg, bg + 16, ... (fixed)
     float sum = 0.f;
-    for (int b0 = bg; b0 < nblk; b0 += 16 * 8) {
-        float v[8];
+    for (int b0 = bg; b0 < nblk; b0 += 16 * 16) {
+        float v[16];
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
+        for (int k = 0; k < 16; k++) {
             const int b = b0 + 16 * k;
             v[k] = partial[static_cast<int64_t>(b < nblk ? b : bg) * FUSED_STRIDE + col];
         }
 #pragma unroll
-        for (int k = 0; k < 8; k++) sum += b0 + 16 * k < nblk ? v[k] : 0.f;
+        for (int k = 0; k < 16; k++) sum += b0 + 16 * k < nblk ? v[k] : 0.f;
     }
     red[bg][c] = sum;
     __syncthreads();
