@@ -120,10 +120,11 @@ int vb_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k,
  * Y[m, n] = sum_k X[m, k] * W[n, k]; X row-major (m x k) in fp32
  * (x_dtype = 0) or fp16 (x_dtype = 1), Y fp32 row-major (m x n).  Products
  * run on v_mfma_f32_16x16x32_f16 with W dequantized to fp16 in registers and
- * fp32 accumulation.  variant: 0 = choose, 1 = skinny (m <= 16), 2 = tiled,
+ * fp32 accumulation.  variant: 0 = choose, 1 = skinny (m <= 32), 2 = tiled,
  * 3 = role-split (fp16 X only; chosen for 257 <= m <= 768 with fp16 X),
  * 4 = K-split (every type; chosen for Q6_K / Q8_0, and for Q4_K at
- * 17 <= m <= 32 with n >= 12288).  Variants 1-3 are Q4_K-only.
+ * 17 <= m <= 32 with fp32 X and n < 12288).  Variant 1 is chosen for Q4_K
+ * at m <= 32 otherwise.  Variants 1-3 are Q4_K-only.
  * Replaces the reference's batched path, a per-token loop of gemv_dequant
  * (cpp/src/fast_model.cpp:644-669, :905-960) over rows decoded by
  * dequantize_row (cpp/src/dequant.cpp:407-425), and cuda::gemm_f32

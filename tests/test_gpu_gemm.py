@@ -80,6 +80,21 @@ def test_tiled_column_tiles(knob, nf):
         assert O.rel_l2(y, want) <= TOL, (nf, dtype)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("m,n,k", [(17, 16, 256), (24, 300, 1024), (32, 64, 4096), (20, 33, 14336),
+                                   (32, 4100, 4096)])
+def test_skinny_two_tiles(dtype, m, n, k):
+    """17 <= M <= 32: two activation tiles share every dequantized weight
+    fragment (4-wave workgroups); ragged row counts and tokens past M."""
+    qt, x = make(m, n, k, m * 11 + n)
+    xt = torch.from_numpy(x).to("cuda", dtype)
+    y = gemm(qt, xt, variant=GEMM_SKINNY).cpu().numpy()
+    want = ref_gemm(qt, xt.float().cpu().numpy())
+    assert y.shape == (m, n)
+    assert O.rel_l2(y, want) <= TOL
+    assert np.all(np.abs(y).sum(axis=1) > 0)  # every token row written
+
+
 def test_tiled_matches_skinny_on_overlap():
     qt, x = make(16, 96, 1024, 5)
     xt = torch.from_numpy(x).to("cuda", torch.float16)
@@ -93,7 +108,7 @@ def test_gemm_rejects_bad_shapes():
     with pytest.raises(ValueError):
         gemm(qt, torch.zeros((4, 255), device="cuda"))
     with pytest.raises(ValueError):
-        gemm(qt, torch.zeros((17, 256), device="cuda"), variant=GEMM_SKINNY)
+        gemm(qt, torch.zeros((33, 256), device="cuda"), variant=GEMM_SKINNY)
 
 
 @pytest.mark.parametrize("m", [8, 512])

@@ -8,7 +8,7 @@
 // in registers, in the B-operand layout of v_mfma_f32_16x16x32_f16
 // (mfma_q4k.hpp), accumulating in fp32.
 //
-// M <= 16 goes to the skinny kernel (gemm_skinny.hip); M > 16 (chunked
+// M <= 32 goes to the skinny kernel (gemm_skinny.hip); M > 32 (chunked
 // prefill) runs the tiled kernel below.
 #include <cstdlib>
 
@@ -353,14 +353,17 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
         }
         return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
     }
-    // 17 <= M <= 32 at N >= 12288: the K-split kernel (gemm_kq.hip; at
-    // N = 14336, K = 4096 on MI355X 21.3 / 24.6 us at M = 17 / 32 against
-    // 27.0 / 27.1 tiled, behind from M = 48)
-    if (variant == 0 && M >= 17 && M <= 32 && N >= 12288) return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
-    const bool skinny = variant == 1 || (variant == 0 && M <= 16);
+    // 17 <= M <= 32: skinny tiles with two activation tiles per wave for fp16
+    // X or N >= 12288, else the K-split kernel (gemm_kq.hip).  On MI355X, fp16
+    // X: 14.5 / 17.5 us at M = 17 / 32 for N = 14336, K = 4096 (K-split 21.5 /
+    // 24.8, tiled 27.0 / 27.1); 11.5 / 13.3 us at 4096 x 4096 (tiled 26.6);
+    // fp32 X at N = 4096 the K-split kernel is 5 % ahead.
+    if (variant == 0 && M >= 17 && M <= 32 && x_dtype != X_F16 && N < 12288)
+        return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
+    const bool skinny = variant == 1 || (variant == 0 && M <= 32);
     if (skinny) {
-        if (M > 16) {
-            set_error("vb_gemm: variant 1 (skinny) takes M <= 16, got %lld", static_cast<long long>(M));
+        if (M > 32) {
+            set_error("vb_gemm: variant 1 (skinny) takes M <= 32, got %lld", static_cast<long long>(M));
             return E_INVAL;
         }
         return gemm_q4k_skinny(w, X, x_dtype, Y, M, N, K, st);

@@ -296,7 +296,7 @@ __global__ void __launch_bounds__(64 * NW, NW <= 4 ? 2 : 1) moe_gate_up_q4k(
     ta.nsb = h / 256;
     for (int m0 = 0; m0 < cnt; m0 += 16) {
         const int nrow = cnt - m0 < 16 ? cnt - m0 : 16;
-        ta.xoff = j < nrow ? (static_cast<uint32_t>(slots[m0 + j] / topk) * static_cast<uint32_t>(h) + 64u * g) * 2u
+        ta.xoff[0] = j < nrow ? (static_cast<uint32_t>(slots[m0 + j] / topk) * static_cast<uint32_t>(h) + 64u * g) * 2u
                            : skinny::X_NONE;
         float4_t s[2];
         skinny::tile<skinny::X_F16, 2, 2, NW>(ta, reinterpret_cast<uint8_t*>(moe_lds), s);
@@ -341,7 +341,7 @@ __global__ void __launch_bounds__(64 * NW, NW <= 4 ? 2 : 1) moe_down_q4k(
     ta.nsb = i_dim / 256;
     for (int m0 = 0; m0 < cnt; m0 += 16) {
         const int nrow = cnt - m0 < 16 ? cnt - m0 : 16;
-        ta.xoff = j < nrow ? (static_cast<uint32_t>(slots[m0 + j]) * static_cast<uint32_t>(i_dim) + 64u * g) * 2u
+        ta.xoff[0] = j < nrow ? (static_cast<uint32_t>(slots[m0 + j]) * static_cast<uint32_t>(i_dim) + 64u * g) * 2u
                            : skinny::X_NONE;
         float4_t s[1];
         skinny::tile<skinny::X_F16, 1, 2, NW>(ta, reinterpret_cast<uint8_t*>(moe_lds), s);

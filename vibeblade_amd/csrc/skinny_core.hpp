@@ -1,5 +1,6 @@
-// Skinny Q4_K x activations tile on MFMA (M <= 16 activation rows), shared by
-// the M <= 16 GEMM (gemm_skinny.hip) and the MoE expert kernels (moe.hip).
+// Skinny Q4_K x activations tile on MFMA (16 activation rows per tile, MT
+// tiles), shared by the M <= 32 GEMM (gemm_skinny.hip) and the MoE expert
+// kernels (moe.hip).
 //
 // A workgroup of 8 waves computes, for `rows` (<= 64) consecutive weight rows
 // of NMAT matrices with the same shape (MoE gate and up: NMAT = 2), the dot
@@ -137,23 +138,25 @@ __device__ __forceinline__ void xwords_to_frags(const XWords<XT>& xw, Frag* a) {
     }
 }
 
-template <int NMAT>
+template <int NMAT, int MT = 1>
 struct TileArgs {
     __amdgpu_buffer_rsrc_t w[NMAT];  // the weight matrices (same shape)
     __amdgpu_buffer_rsrc_t x;        // activations
-    uint32_t xoff;                   // this lane's activation row offset in bytes (+ 64 g elements), or X_NONE
+    uint32_t xoff[MT];               // per 16-row activation tile: this lane's row offset in bytes
+                                     // (+ 64 g elements), or X_NONE
     int row0, rows, nrows;           // rows [row0, row0 + rows) of nrows
     int rb, nsb;                     // bytes per weight row, super-blocks per row
 };
 
 // Runs the tile with NW waves and returns, in threads 0..255 (q = tid / 64,
 // l = tid % 64), the sums of weight row row0 + 16 q + l % 16 with activation
-// rows 4 (l / 16) + 0..3 of every matrix.  All threads of the workgroup must
-// call it (it synchronises); `lds` = the launch's dynamic LDS
-// (lds_bytes<NW>()).
-template <int XT, int NMAT, int RING = 2, int NW = WAVES>
-__device__ __forceinline__ void tile(const TileArgs<NMAT>& ta, uint8_t* lds, float4_t* out) {
-    static_assert(NMAT * 4096 <= STAGE, "the final sums must fit in the staging areas");
+// rows 4 (l / 16) + 0..3 of every matrix and activation tile: out[mt * NMAT
+// + m].  MT activation tiles (16 rows each) share every dequantized weight
+// fragment.  All threads of the workgroup must call it (it synchronises);
+// `lds` = the launch's dynamic LDS (lds_bytes<NW>()).
+template <int XT, int NMAT, int RING = 2, int NW = WAVES, int MT = 1>
+__device__ __forceinline__ void tile(const TileArgs<NMAT, MT>& ta, uint8_t* lds, float4_t* out) {
+    static_assert(MT * NMAT * 4096 <= STAGE, "the final sums must fit in the staging areas");
     const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int nsb = ta.nsb;
@@ -190,8 +193,8 @@ __device__ __forceinline__ void tile(const TileArgs<NMAT>& ta, uint8_t* lds, flo
     constexpr int XB = XT == X_F16 ? 2 : 1;
     constexpr int P = 2 * NMAT;  // units per unrolled period (ring slot and buffer parities repeat)
     u32x4 pv[RING][PPL];
-    XWords<XT> xw[XB];
-    Frag a[XT == X_F32 ? 8 : 1];  // converted fp32 activations of the current super-block
+    XWords<XT> xw[MT][XB];
+    Frag a[MT][XT == X_F32 ? 8 : 1];  // converted fp32 activations of the current super-block
     int itw = 0, itx = 0;
     // Ring slots are compile-time constants so the buffers stay in registers.
     auto issue_w = [&](auto slot_c) __attribute__((always_inline)) {
@@ -215,36 +218,43 @@ __device__ __forceinline__ void tile(const TileArgs<NMAT>& ta, uint8_t* lds, flo
         constexpr int buf = decltype(buf_c)::value % XB;
         int sb = sb0 + itx;
         sb = sb < nsb - 1 ? sb : nsb - 1;
-        load_xwords<XT>(ta.x, ta.xoff, static_cast<uint32_t>(sb) * 256u * ES, xw[buf]);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+            load_xwords<XT>(ta.x, ta.xoff[mt], static_cast<uint32_t>(sb) * 256u * ES, xw[mt][buf]);
         ++itx;
     };
 
-    float4_t acc[NMAT][4];
+    float4_t acc[MT][NMAT][4];
 #pragma unroll
-    for (int m = 0; m < NMAT; m++)
+    for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-        for (int q = 0; q < 4; q++) acc[m][q] = float4_t{0.f, 0.f, 0.f, 0.f};
+        for (int m = 0; m < NMAT; m++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) acc[mt][m][q] = float4_t{0.f, 0.f, 0.f, 0.f};
     int ct = 0;
     auto compute = [&](auto u_c) __attribute__((always_inline)) {
         constexpr int u = decltype(u_c)::value;  // position in the period
         constexpr int slot = RING == 1 ? 0 : u % 2, m = u % NMAT, xb = (u / NMAT) % 2;
         if (ct >= nunits) return;  // padding unit (uniform)
         if constexpr (m == 0) {
-            if constexpr (XT == X_F32) xwords_to_frags<XT>(xw[0], a);
+            if constexpr (XT == X_F32) {
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) xwords_to_frags<XT>(xw[mt][0], a[mt]);
+            }
             issue_x(std::integral_constant<int, xb ^ 1>{});  // next super-block's activations
         }
         // fp16 activations are read in place: no copy lives across units
-        auto afrag = [&](int s) __attribute__((always_inline)) -> Frag {
+        auto afrag = [&](int mt, int s) __attribute__((always_inline)) -> Frag {
             if constexpr (XT == X_F16) {
                 Frag f;
-                const u32x4 v = xw[xb % XB].v[s];
+                const u32x4 v = xw[mt][xb % XB].v[s];
                 f.u[0] = v.x;
                 f.u[1] = v.y;
                 f.u[2] = v.z;
                 f.u[3] = v.w;
                 return f;
             } else {
-                return a[s];
+                return a[mt][s];
             }
         };
 #pragma unroll
@@ -266,8 +276,11 @@ __device__ __forceinline__ void tile(const TileArgs<NMAT>& ta, uint8_t* lds, flo
             for (int s = 0; s < 4; s++) {
                 Frag lo, hi;
                 q4k_bfrags_nat2(qd[2 * s], qd[2 * s + 1], ds, nm, kc, lo, hi);
-                acc[m][q] = mfma16x16x32(afrag(s), lo, acc[m][q]);
-                acc[m][q] = mfma16x16x32(afrag(4 + s), hi, acc[m][q]);
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) {
+                    acc[mt][m][q] = mfma16x16x32(afrag(mt, s), lo, acc[mt][m][q]);
+                    acc[mt][m][q] = mfma16x16x32(afrag(mt, 4 + s), hi, acc[mt][m][q]);
+                }
             }
         }
         ++ct;
@@ -320,20 +333,23 @@ __device__ __forceinline__ void tile(const TileArgs<NMAT>& ta, uint8_t* lds, flo
 
     // k-range partials meet in LDS (over the staging areas), fixed order.
     __syncthreads();
-    float4_t* red = reinterpret_cast<float4_t*>(lds);  // [m][wave][q][lane]
+    float4_t* red = reinterpret_cast<float4_t*>(lds);  // [mt * NMAT + m][wave][q][lane]
 #pragma unroll
-    for (int m = 0; m < NMAT; m++)
+    for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-        for (int q = 0; q < 4; q++) red[((m * NW + wave) * 4 + q) * 64 + lane] = acc[m][q];
+        for (int m = 0; m < NMAT; m++)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                red[(((mt * NMAT + m) * NW + wave) * 4 + q) * 64 + lane] = acc[mt][m][q];
     __syncthreads();
     if (threadIdx.x < 256) {
         const int e = threadIdx.x;
 #pragma unroll
-        for (int m = 0; m < NMAT; m++) {
-            float4_t s = red[(m * NW * 4) * 64 + e];
+        for (int mm = 0; mm < MT * NMAT; mm++) {
+            float4_t s = red[(mm * NW * 4) * 64 + e];
 #pragma unroll
-            for (int v = 1; v < NW; v++) s += red[((m * NW + v) * 4) * 64 + e];
-            out[m] = s;
+            for (int v = 1; v < NW; v++) s += red[((mm * NW + v) * 4) * 64 + e];
+            out[mm] = s;
         }
     }
     __syncthreads();  // the next tile may overwrite the sums

@@ -95,7 +95,7 @@ int gemv_q4k_split(const void* w, const float* x, float* y, const float* resid, 
 // already validated by gemv_dispatch_src.
 int gemv_q4k_mfma(const void* w, const RowSrc& src, const float* x, float* y, int64_t n, int64_t k,
                   hipStream_t st);
-// M <= 16 Q4_K GEMM (gemm_skinny.hip); type, M, alignment already validated.
+// M <= 32 Q4_K GEMM (gemm_skinny.hip); type, M, alignment already validated.
 int gemm_q4k_skinny(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, int64_t N, int64_t K,
                     hipStream_t st);
 // Role-split Q4_K GEMM, fp16 X (gemm_split.hip); type, alignment and the
