@@ -158,11 +158,15 @@ __global__ void __launch_bounds__(DOWN_THREADS) down_rows_q4k_kernel(
 // h = act(g, u), and lane u adds h * D[S_r, 64u .. 64u+63] (decoded: d*sc*q -
 // dmin*m) to its 64 partial outputs.  The 8 waves' partials meet in LDS and
 // the workgroup writes one partial y (4096 floats); sparse_reduce_kernel adds
-// the workgroups' partials in a fixed order (deterministic).
+// the workgroups' partials in a fixed order (deterministic).  The partials
+// go through LDS in 16-byte accesses: 32 LDS instructions per thread where
+// 4-byte accesses take 128.
 constexpr int FUSED_NPW = 1;  // neurons per wave (VB_SPARSE_NPW=2 selects 2; 1 measured faster: more
                               // workgroups, less serial work per wave, at twice the partial sums)
 constexpr int FUSED_STRIDE = 4096;        // floats per partial y (h <= 4096)
-constexpr int FUSED_RED_PITCH = 65;       // LDS row pitch of the wave partials
+// LDS row of one lane's 64 partials (floats): 16-byte writes of 16 lanes at
+// a pitch of 68 floats (4 mod 64 dwords) fall on distinct banks
+constexpr int FUSED_RED_PITCH = 68;
 
 __device__ __forceinline__ float pair_sum(float a0, float a1) {
     // lane 31: total of a0, lane 63: total of a1 (see gemv.hip)
@@ -219,7 +223,7 @@ __global__ void __launch_bounds__(512) sparse_fused_q4k_kernel(
     const int n_active = active_count(n_bound, n_dev);
     if (static_cast<int>(blockIdx.x) * (8 * NPW) >= n_active) return;
     // the x encoding (slots x 11 uint4), later the 8 waves' partials
-    __shared__ uint4 lds[8 * 64 * FUSED_RED_PITCH / 4];
+    __shared__ uint4 lds[8 * 64 * FUSED_RED_PITCH / 4];  // 139,264 B
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const bool valid = lane < units;
@@ -297,19 +301,32 @@ __global__ void __launch_bounds__(512) sparse_fused_q4k_kernel(
     }
     // the 8 waves' partials (lanes >= units hold junk and are never read)
     __syncthreads();  // the x encoding is dead: LDS now holds the partials
+    // row (wave, lane): the lane's 64 partials (columns 64 lane + e), four per
+    // 16-byte write
     float* red = reinterpret_cast<float*>(lds);
 #pragma unroll
-    for (int e = 0; e < 64; e++)
-        red[(wave * 64 + e) * FUSED_RED_PITCH + lane] = yp[e] - (e < 32 ? mb0 : mb1);
+    for (int i = 0; i < 16; i++) {
+        const float m = i < 8 ? mb0 : mb1;
+        *reinterpret_cast<float4*>(red + (wave * 64 + lane) * FUSED_RED_PITCH + 4 * i) =
+            make_float4(yp[4 * i] - m, yp[4 * i + 1] - m, yp[4 * i + 2] - m, yp[4 * i + 3] - m);
+    }
     __syncthreads();
+    // column quad q = (unit q / 16, columns 4 (q % 16) ..): the 8 waves' rows
+    // added in wave order, one 16-byte store
     float* out = partial + static_cast<int64_t>(blockIdx.x) * FUSED_STRIDE;
-    const int h_dim = 64 * units;
-    for (int col = static_cast<int>(threadIdx.x); col < h_dim; col += static_cast<int>(blockDim.x)) {
-        const int l = col >> 6, e = col & 63;
-        float sum = 0.f;
+    const int nquads = 16 * units;
+    for (int q = static_cast<int>(threadIdx.x); q < nquads; q += static_cast<int>(blockDim.x)) {
+        const int l = q >> 4, e0 = 4 * (q & 15);
+        float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int w = 0; w < 8; w++) sum += red[(w * 64 + e) * FUSED_RED_PITCH + l];
-        out[col] = sum;
+        for (int w = 0; w < 8; w++) {
+            const float4 v = *reinterpret_cast<const float4*>(red + (w * 64 + l) * FUSED_RED_PITCH + e0);
+            sum.x += v.x;
+            sum.y += v.y;
+            sum.z += v.z;
+            sum.w += v.w;
+        }
+        *reinterpret_cast<float4*>(out + 64 * l + e0) = sum;
     }
 }
 
