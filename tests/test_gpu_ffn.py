@@ -322,6 +322,21 @@ def test_ffn_block_unfused_types(gu, dn):
     run_block(*w, 512, ACT_SILU, norm=False, residual=False, seed=9)
 
 
+@pytest.mark.parametrize("hd,inter", [(4096, 14336), (1024, 2816), (256, 512)])
+@pytest.mark.parametrize("norm", [False, True])
+def test_ffn_block_pairs_kernel(knob, hd, inter, norm):
+    """Q4_K gate/up with hd <= 4096 runs the short-row pairs kernel (8 to 1
+    neurons per wave here); the general kernel (VB_GEMV_Q4K_PATH=dot) gives
+    the same result to the bar, both against the oracle, every activation."""
+    w = block_weights(hd, inter, Q4K, Q4K, 36)
+    for act in (ACT_SILU, ACT_RELU2, ACT_GELU_TANH):
+        run_block(*w, hd, act, norm=norm, residual=False, seed=11)
+    y_pairs = run_block(*w, hd, ACT_SILU, norm=norm, residual=True, seed=12)
+    knob("VB_GEMV_Q4K_PATH", "dot")
+    y_gen = run_block(*w, hd, ACT_SILU, norm=norm, residual=True, seed=12)
+    assert O.rel_l2(y_pairs, y_gen) <= 1e-3
+
+
 def test_ffn_block_repeatable_and_errors():
     w = block_weights(1024, 1024, Q4K, Q4K, 35)
     a = run_block(*w, 1024, ACT_SILU, True, True, seed=10)

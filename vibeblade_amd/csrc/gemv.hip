@@ -521,6 +521,11 @@ int gemv_dispatch_fused(const void* w, const RowSrc& src, const GemvFuse& fz, co
         // short rows (k <= 4096) at <= 8 rows per wave: the dedicated kernel
         if (plain && !knobs().gemv_q4k_general && k <= 4096 && gemv_q4k_rpw(n) > 0)
             return gemv_q4k_short(w, x, y, n, k, st);
+        // dense gate/up pairs with the activation epilogue (FFN block launch
+        // 1), k <= 4096: the short-row arithmetic, RMSNorm in its encode
+        if (src.dense_pairs && fz.act >= 0 && !fz.resid && !src.n_dev && !src.gidx && src.zn == 0 &&
+            !knobs().gemv_q4k_general && k <= 4096 && k % 256 == 0 && gemv_q4k_pairs_npw(n / 2) > 0)
+            return gemv_q4k_pairs(w, src.w2, x, fz.norm_w, fz.eps, fz.act, y, n / 2, k, st);
         // split rows (4096 < k <= 16384), plain or with the residual epilogue
         const bool resid_only = !fz.norm_w && fz.act < 0 && !src.dense_pairs && !src.n_dev && !src.gidx &&
                                 src.zn == 0;

@@ -317,6 +317,164 @@ __global__ void __launch_bounds__(64 * WPG) gemv_q4k_kernel(const uint8_t* __res
     if ((lane & 7) == 0 && r < RPW && row0 + r < n) y[row0 + r] = tot;
 }
 
+// ---- gate/up pairs with the activation epilogue (FFN block launch 1) ---------
+//
+// y[p] = act(gate_p . n, up_p . n) for neurons p, n = x (or RMSNorm(x) * norm_w
+// with NORM), k <= 4096.  The short-row kernel's arithmetic and loads; wave w
+// of workgroup b owns neurons (8 b + w) NPW + [0, NPW) and streams each
+// neuron's gate row and up row through the same LDS row buffer, NS - 1
+// neurons in flight.  NORM: every workgroup reduces sum(x^2) over all of x in
+// a fixed order (same bits in every workgroup) and scales x by rinv * norm_w
+// before the encode.  The gate and up partials are reduced at once per wave
+// (two reduce8) and lanes 8g write act(g, u) of their neuron.
+template <int NPW, int NS, bool NORM>
+__global__ void __launch_bounds__(512) gemv_q4k_pairs_kernel(const uint8_t* __restrict__ wg,
+                                                             const uint8_t* __restrict__ wu,
+                                                             const float* __restrict__ x,
+                                                             const float* __restrict__ norm_w, float eps, int kind,
+                                                             float* __restrict__ y, int n, int units, uint32_t rb) {
+    __shared__ uint4 xq[XQ_UNIT_QUADS * UNITS_MAX];
+    __shared__ u32x4 rowbuf[8][ROW_SLOTS];
+    __shared__ float wsum[8];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int p0 = (static_cast<int>(blockIdx.x) * 8 + wave) * NPW;
+    const int plast = n - 1;
+    const int pbase = p0 < plast ? p0 : plast;
+    const int64_t span64 = static_cast<int64_t>(n - pbase) * rb;
+    const uint32_t span = span64 < 0xFFFFFFFFll ? static_cast<uint32_t>(span64) : 0xFFFFFFFFu;
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(wg + static_cast<int64_t>(pbase) * rb, span);
+    const __amdgpu_buffer_rsrc_t ru = make_rsrc(wu + static_cast<int64_t>(pbase) * rb, span);
+    const bool valid = lane < units;
+    const int u = valid ? lane : (lane & 3);
+    const int slots = static_cast<int>(rb >> 4);
+    const int pc = 128 + (lane & 15);
+    const uint32_t va = 16u * static_cast<uint32_t>(lane < slots ? lane : lane & 7);
+    const uint32_t vb = 16u * static_cast<uint32_t>(64 + lane < slots ? 64 + lane : lane & 7);
+    const uint32_t vc = 16u * static_cast<uint32_t>(pc < slots ? pc : lane & 7);
+    u32x4* rbuf = rowbuf[wave];
+    const int sh = 9 * (u >> 2), sq = sh + 1 + 2 * (u & 3);
+
+    struct Pair { RowRaw g, u; };
+    auto soff = [&](int s) -> uint32_t {
+        int p = p0 + s;
+        p = p < plast ? p : plast;
+        return static_cast<uint32_t>(p - pbase) * rb;
+    };
+    auto issue1 = [&](RowRaw& b, __amdgpu_buffer_rsrc_t r, uint32_t so) {
+        b.a = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(va), static_cast<int>(so), CACHE_NT);
+        b.b = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(vb), static_cast<int>(so), CACHE_NT);
+        b.c = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(vc), static_cast<int>(so), CACHE_NT);
+    };
+    auto issue = [&](Pair& b, int s) {
+        const uint32_t so = soff(s);
+        issue1(b.g, rg, so);
+        issue1(b.u, ru, so);
+    };
+    auto stage = [&](const RowRaw& b) -> RowBuf {
+        rbuf[lane] = b.a;
+        rbuf[64 + lane] = b.b;
+        rbuf[pc] = b.c;
+        RowBuf r;
+        r.hdr = rbuf[sh];
+        r.qa = rbuf[sq];
+        r.qb = rbuf[sq + 1];
+        return r;
+    };
+
+    // x (and the norm weights) first, then the first neurons' rows, then the
+    // norm and the encode
+    float xv[8];
+    [[maybe_unused]] float nv[8];
+    const int task = static_cast<int>(threadIdx.x);
+    const int tu = task >> 3;
+    {
+        const int off = (tu < units ? tu : units - 1) * 64 + 8 * (task & 7);
+        const float4 a = *reinterpret_cast<const float4*>(x + off);
+        const float4 b = *reinterpret_cast<const float4*>(x + off + 4);
+        xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
+        xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+        if constexpr (NORM) {
+            const float4 c = *reinterpret_cast<const float4*>(norm_w + off);
+            const float4 d = *reinterpret_cast<const float4*>(norm_w + off + 4);
+            nv[0] = c.x; nv[1] = c.y; nv[2] = c.z; nv[3] = c.w;
+            nv[4] = d.x; nv[5] = d.y; nv[6] = d.z; nv[7] = d.w;
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    Pair ring[NS];
+#pragma unroll
+    for (int s = 0; s < NS - 1 && s < NPW; s++) issue(ring[s], s);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (NORM) {
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) ss += xv[i] * xv[i];
+        ss = wave_sum_dpp(tu < units ? ss : 0.f);
+        if (lane == 0) wsum[wave] = ss;
+        __syncthreads();
+        float tot = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) tot += wsum[i];
+        const float rinv = 1.0f / sqrtf(tot / static_cast<float>(units * 64) + eps);
+#pragma unroll
+        for (int i = 0; i < 8; i++) xv[i] = xv[i] * rinv * nv[i];
+    }
+    encode_task(xv, task, units, xq);
+    __syncthreads();
+    const XU xu = read_unit(xq, u);
+    const ScaleSel ss = make_sel(u & 3);
+
+    float ag[8], au[8];
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        ag[s] = 0.f;
+        au[s] = 0.f;
+    }
+#pragma unroll
+    for (int s = 0; s < NPW; s++) {
+        if (s + NS - 1 < NPW) issue(ring[(s + NS - 1) % NS], s + NS - 1);
+        const float pg = row_part(stage(ring[s % NS].g), xu, ss);
+        const float pu = row_part(stage(ring[s % NS].u), xu, ss);
+        ag[s] = valid ? pg : 0.f;
+        au[s] = valid ? pu : 0.f;
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    const float tg = reduce8(ag);
+    const float tv = reduce8(au);
+    const int r = row_of_group(lane >> 3);
+    if ((lane & 7) == 0 && r < NPW && p0 + r < n) y[p0 + r] = act_pair(tg, tv, kind);
+}
+
+template <int NPW, int NS>
+void launch_pairs(bool norm, const void* wg, const void* wu, const float* x, const float* norm_w, float eps,
+                  int kind, float* y, int n, int units, uint32_t rb, hipStream_t st) {
+    const int grid = (n + 8 * NPW - 1) / (8 * NPW);
+    const uint8_t* a = static_cast<const uint8_t*>(wg);
+    const uint8_t* b = static_cast<const uint8_t*>(wu);
+    if (norm)
+        gemv_q4k_pairs_kernel<NPW, NS, true><<<dim3(static_cast<uint32_t>(grid)), dim3(512), 0, st>>>(
+            a, b, x, norm_w, eps, kind, y, n, units, rb);
+    else
+        gemv_q4k_pairs_kernel<NPW, NS, false><<<dim3(static_cast<uint32_t>(grid)), dim3(512), 0, st>>>(
+            a, b, x, norm_w, eps, kind, y, n, units, rb);
+}
+
+template <int NS>
+void launch_pairs_npw(int npw, bool norm, const void* wg, const void* wu, const float* x, const float* norm_w,
+                      float eps, int kind, float* y, int n, int units, uint32_t rb, hipStream_t st) {
+    switch (npw) {
+    case 1: launch_pairs<1, NS < 2 ? NS : 2>(norm, wg, wu, x, norm_w, eps, kind, y, n, units, rb, st); break;
+    case 2: launch_pairs<2, NS < 3 ? NS : 3>(norm, wg, wu, x, norm_w, eps, kind, y, n, units, rb, st); break;
+    case 3: launch_pairs<3, NS>(norm, wg, wu, x, norm_w, eps, kind, y, n, units, rb, st); break;
+    case 4: launch_pairs<4, NS>(norm, wg, wu, x, norm_w, eps, kind, y, n, units, rb, st); break;
+    case 5: launch_pairs<5, NS>(norm, wg, wu, x, norm_w, eps, kind, y, n, units, rb, st); break;
+    case 6: launch_pairs<6, NS>(norm, wg, wu, x, norm_w, eps, kind, y, n, units, rb, st); break;
+    case 7: launch_pairs<7, NS>(norm, wg, wu, x, norm_w, eps, kind, y, n, units, rb, st); break;
+    default: launch_pairs<8, NS>(norm, wg, wu, x, norm_w, eps, kind, y, n, units, rb, st); break;
+    }
+}
+
 // ---- split rows: 64 < units <= 256 (4096 < k <= 16384) ------------------------
 //
 // A row is split into SL slices of upw units (upw a multiple of 4, so slices
@@ -595,6 +753,39 @@ int gemv_q4k_split(const void* w, const float* x, float* y, const float* resid, 
         launch_split_d<4>(d, sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
     else
         launch_split_d<8>(d, sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
+    return check_launch("vb_gemv");
+}
+
+// Neurons per wave of the pairs kernel: one 8-wave workgroup per CU when that
+// covers n neurons at up to 8 per wave, else 0 (the caller takes the general
+// kernel).
+int gemv_q4k_pairs_npw(int64_t n) {
+    const int64_t groups = static_cast<int64_t>(num_cus()) * 8;
+    const int64_t npw = (n + groups - 1) / groups;
+    return npw <= 8 ? static_cast<int>(npw < 1 ? 1 : npw) : 0;
+}
+
+// FFN block launch 1 for Q4_K gate/up with k <= 4096 (k % 256 == 0): y[p] =
+// act(gate_p . n, up_p . n), p < n_neurons; arguments validated by
+// gemv_dispatch_fused.
+int gemv_q4k_pairs(const void* wg, const void* wu, const float* x, const float* norm_w, float eps, int kind,
+                   float* y, int64_t n, int64_t k, hipStream_t st) {
+    const int npw = gemv_q4k_pairs_npw(n);
+    const int units = static_cast<int>(k / 64);
+    if (npw == 0 || units > UNITS_MAX || k % 256 != 0 || n > INT32_MAX) {
+        set_error("vb_gemv: internal: Q4_K pairs kernel shape (n=%lld, k=%lld)", static_cast<long long>(n),
+                  static_cast<long long>(k));
+        return E_INVAL;
+    }
+    const uint32_t rb = static_cast<uint32_t>(row_bytes(TYPE_Q4_K, k));
+    const int ring = knobs().gemv_ring;  // neurons in flight while computing (default 2)
+    const int ni = static_cast<int>(n);
+    if (ring == 1)
+        launch_pairs_npw<2>(npw, norm_w != nullptr, wg, wu, x, norm_w, eps, kind, y, ni, units, rb, st);
+    else if (ring >= 3)
+        launch_pairs_npw<4>(npw, norm_w != nullptr, wg, wu, x, norm_w, eps, kind, y, ni, units, rb, st);
+    else
+        launch_pairs_npw<3>(npw, norm_w != nullptr, wg, wu, x, norm_w, eps, kind, y, ni, units, rb, st);
     return check_launch("vb_gemv");
 }
 
