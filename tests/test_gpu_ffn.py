@@ -132,6 +132,30 @@ def test_sparse_neuron_major_paths(knob, h, i, fused_env, one):
         assert O.rel_l2(y, want) <= 1e-3
 
 
+@pytest.mark.parametrize("h,i", [(4096, 14336), (1024, 2048)])
+def test_sparse_gguf_down_one_launch_hidden(knob, h, i):
+    """GGUF-layout down with Q4_K gate/up (h <= 4096): one launch writes the
+    whole hidden vector, act(g, u) on the set and zeros between.  Sets with
+    the first or the last neuron alone, a dense call right before a sparse
+    one (a position left unwritten would keep the dense call's value), and
+    the general three-launch path (VB_GEMV_Q4K_PATH=dot) on the same sets."""
+    gq, uq, dq, gd, ud, dd = ffn_weights(h, i, Q4K, 21, DOWN_GGUF)
+    rng = np.random.default_rng(h + 3)
+    x = torch.from_numpy(rng.standard_normal(h).astype(np.float32))
+    sets = [np.array([0], np.int32), np.array([i - 1], np.int32),
+            np.flatnonzero(rng.random(i) < 0.5).astype(np.int32), np.flatnonzero(rng.random(i) < 0.02).astype(np.int32)]
+    got = []
+    for s in sets:
+        y = sparse_ffn(gq, uq, dq, x, torch.from_numpy(s), ACT_SILU, DOWN_GGUF).cpu().numpy()
+        want = O.sparse_ffn(gd, ud, dd, x.numpy(), s, ACT_SILU)[0]
+        assert O.rel_l2(y, want) <= 1e-3, s.size
+        got.append(y)
+    knob("VB_GEMV_Q4K_PATH", "dot")
+    for s, y in zip(sets, got):
+        y_gen = sparse_ffn(gq, uq, dq, x, torch.from_numpy(s), ACT_SILU, DOWN_GGUF).cpu().numpy()
+        assert O.rel_l2(y, y_gen) <= 1e-3
+
+
 def test_sparse_repeatable():
     """Layout 1 sums partials in a fixed order: identical bits run to run."""
     h, i = 4096, 4096

@@ -327,24 +327,66 @@ __global__ void __launch_bounds__(64 * WPG) gemv_q4k_kernel(const uint8_t* __res
 // a fixed order (same bits in every workgroup) and scales x by rinv * norm_w
 // before the encode.  The gate and up partials are reduced at once per wave
 // (two reduce8) and lanes 8g write act(g, u) of their neuron.
-template <int NPW, int NS, bool NORM>
+//
+// GATHER (the sparse FFN with a GGUF-layout down): neuron p is row active[p]
+// of both matrices, for p below the active count (n, or the device count at
+// n_dev), and the launch writes the whole hidden vector y[0, i_dim) that the
+// down GEMV reads: y[active[p]] = act(g, u), zeros elsewhere.  The active
+// set is sorted ascending and unique, so workgroup b owns the positions
+// from its first neuron's index (0 for b = 0) up to the next workgroup's
+// first index (i_dim for the last one) and writes every one of them once.
+template <int NPW, int NS, bool NORM, bool GATHER>
 __global__ void __launch_bounds__(512) gemv_q4k_pairs_kernel(const uint8_t* __restrict__ wg,
                                                              const uint8_t* __restrict__ wu,
                                                              const float* __restrict__ x,
                                                              const float* __restrict__ norm_w, float eps, int kind,
-                                                             float* __restrict__ y, int n, int units, uint32_t rb) {
+                                                             float* __restrict__ y, int n, int units, uint32_t rb,
+                                                             const int32_t* __restrict__ active,
+                                                             const int32_t* __restrict__ n_dev, int i_dim) {
     __shared__ uint4 xq[XQ_UNIT_QUADS * UNITS_MAX];
     __shared__ u32x4 rowbuf[8][ROW_SLOTS];
     __shared__ float wsum[8];
+    [[maybe_unused]] __shared__ int gid[8 * NPW];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int p0 = (static_cast<int>(blockIdx.x) * 8 + wave) * NPW;
-    const int plast = n - 1;
+    int n_act = n;
+    if constexpr (GATHER) {
+        n_act = active_count(n, n_dev);
+        const int e0 = static_cast<int>(blockIdx.x) * 8 * NPW;
+        // no neuron here, and no hidden position either (workgroup 0 zeroes
+        // the whole vector when the count is 0)
+        if (e0 >= n_act && !(e0 == 0 && n_act == 0)) return;
+        // the workgroup's hidden positions [lo, hi): zeros where no neuron of
+        // it sits (its neurons' indices, clamped, in LDS for the lookup)
+        const int e1 = e0 + 8 * NPW < n_act ? e0 + 8 * NPW : n_act;
+        auto idx = [&](int e) {
+            const int v = active[e];
+            return v < 0 ? 0 : (v > i_dim ? i_dim : v);
+        };
+        if (static_cast<int>(threadIdx.x) < e1 - e0) gid[threadIdx.x] = idx(e0 + threadIdx.x);
+        const int lo = e0 == 0 ? 0 : idx(e0);
+        const int hi = e1 < n_act ? idx(e1) : i_dim;
+        __syncthreads();
+        for (int q = lo + static_cast<int>(threadIdx.x); q < hi; q += 512) {
+            int a = 0, b = e1 - e0;  // first neuron index >= q
+            while (a < b) {
+                const int m = (a + b) >> 1;
+                if (gid[m] < q) a = m + 1; else b = m;
+            }
+            if (a == e1 - e0 || gid[a] != q) y[q] = 0.f;
+        }
+        if (n_act == 0) return;
+    }
+    const int plast = n_act - 1;
     const int pbase = p0 < plast ? p0 : plast;
-    const int64_t span64 = static_cast<int64_t>(n - pbase) * rb;
+    // dense: the wave's rows from pbase on; gathered: the whole matrices,
+    // row offsets from the active list
+    const int64_t span64 = GATHER ? static_cast<int64_t>(i_dim) * rb : static_cast<int64_t>(n - pbase) * rb;
     const uint32_t span = span64 < 0xFFFFFFFFll ? static_cast<uint32_t>(span64) : 0xFFFFFFFFu;
-    const __amdgpu_buffer_rsrc_t rg = make_rsrc(wg + static_cast<int64_t>(pbase) * rb, span);
-    const __amdgpu_buffer_rsrc_t ru = make_rsrc(wu + static_cast<int64_t>(pbase) * rb, span);
+    const int64_t base = GATHER ? 0 : static_cast<int64_t>(pbase) * rb;
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(wg + base, span);
+    const __amdgpu_buffer_rsrc_t ru = make_rsrc(wu + base, span);
     const bool valid = lane < units;
     const int u = valid ? lane : (lane & 3);
     const int slots = static_cast<int>(rb >> 4);
@@ -359,7 +401,13 @@ __global__ void __launch_bounds__(512) gemv_q4k_pairs_kernel(const uint8_t* __re
     auto soff = [&](int s) -> uint32_t {
         int p = p0 + s;
         p = p < plast ? p : plast;
-        return static_cast<uint32_t>(p - pbase) * rb;
+        if constexpr (GATHER) {
+            int v = active[p];
+            v = v < 0 ? 0 : (v >= i_dim ? i_dim - 1 : v);  // never read outside the matrices
+            return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(v)) * rb;
+        } else {
+            return static_cast<uint32_t>(p - pbase) * rb;
+        }
     };
     auto issue1 = [&](RowRaw& b, __amdgpu_buffer_rsrc_t r, uint32_t so) {
         b.a = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(va), static_cast<int>(so), CACHE_NT);
@@ -443,35 +491,56 @@ __global__ void __launch_bounds__(512) gemv_q4k_pairs_kernel(const uint8_t* __re
     const float tg = reduce8(ag);
     const float tv = reduce8(au);
     const int r = row_of_group(lane >> 3);
-    if ((lane & 7) == 0 && r < NPW && p0 + r < n) y[p0 + r] = act_pair(tg, tv, kind);
+    if ((lane & 7) == 0 && r < NPW && p0 + r < n_act) {
+        if constexpr (GATHER) {
+            const int v = active[p0 + r];
+            if (v >= 0 && v < i_dim) y[v] = act_pair(tg, tv, kind);
+        } else {
+            y[p0 + r] = act_pair(tg, tv, kind);
+        }
+    }
+}
+
+struct PairsArgs {
+    const void *wg, *wu;
+    const float *x, *norm_w;
+    float eps;
+    int kind;
+    float* y;
+    int n, units;
+    uint32_t rb;
+    const int32_t *active, *n_dev;  // gathered rows (active != nullptr)
+    int i_dim;
+};
+
+template <int NPW, int NS, bool NORM, bool GATHER>
+void launch_pairs_k(const PairsArgs& a, hipStream_t st) {
+    const int grid = (a.n + 8 * NPW - 1) / (8 * NPW);
+    gemv_q4k_pairs_kernel<NPW, NS, NORM, GATHER><<<dim3(static_cast<uint32_t>(grid)), dim3(512), 0, st>>>(
+        static_cast<const uint8_t*>(a.wg), static_cast<const uint8_t*>(a.wu), a.x, a.norm_w, a.eps, a.kind, a.y, a.n,
+        a.units, a.rb, a.active, a.n_dev, a.i_dim);
 }
 
 template <int NPW, int NS>
-void launch_pairs(bool norm, const void* wg, const void* wu, const float* x, const float* norm_w, float eps,
-                  int kind, float* y, int n, int units, uint32_t rb, hipStream_t st) {
-    const int grid = (n + 8 * NPW - 1) / (8 * NPW);
-    const uint8_t* a = static_cast<const uint8_t*>(wg);
-    const uint8_t* b = static_cast<const uint8_t*>(wu);
-    if (norm)
-        gemv_q4k_pairs_kernel<NPW, NS, true><<<dim3(static_cast<uint32_t>(grid)), dim3(512), 0, st>>>(
-            a, b, x, norm_w, eps, kind, y, n, units, rb);
+void launch_pairs(const PairsArgs& a, hipStream_t st) {
+    const bool norm = a.norm_w != nullptr, gather = a.active != nullptr;
+    if (gather)
+        norm ? launch_pairs_k<NPW, NS, true, true>(a, st) : launch_pairs_k<NPW, NS, false, true>(a, st);
     else
-        gemv_q4k_pairs_kernel<NPW, NS, false><<<dim3(static_cast<uint32_t>(grid)), dim3(512), 0, st>>>(
-            a, b, x, norm_w, eps, kind, y, n, units, rb);
+        norm ? launch_pairs_k<NPW, NS, true, false>(a, st) : launch_pairs_k<NPW, NS, false, false>(a, st);
 }
 
 template <int NS>
-void launch_pairs_npw(int npw, bool norm, const void* wg, const void* wu, const float* x, const float* norm_w,
-                      float eps, int kind, float* y, int n, int units, uint32_t rb, hipStream_t st) {
+void launch_pairs_npw(int npw, const PairsArgs& a, hipStream_t st) {
     switch (npw) {
-    case 1: launch_pairs<1, NS < 2 ? NS : 2>(norm, wg, wu, x, norm_w, eps, kind, y, n, units, rb, st); break;
-    case 2: launch_pairs<2, NS < 3 ? NS : 3>(norm, wg, wu, x, norm_w, eps, kind, y, n, units, rb, st); break;
-    case 3: launch_pairs<3, NS>(norm, wg, wu, x, norm_w, eps, kind, y, n, units, rb, st); break;
-    case 4: launch_pairs<4, NS>(norm, wg, wu, x, norm_w, eps, kind, y, n, units, rb, st); break;
-    case 5: launch_pairs<5, NS>(norm, wg, wu, x, norm_w, eps, kind, y, n, units, rb, st); break;
-    case 6: launch_pairs<6, NS>(norm, wg, wu, x, norm_w, eps, kind, y, n, units, rb, st); break;
-    case 7: launch_pairs<7, NS>(norm, wg, wu, x, norm_w, eps, kind, y, n, units, rb, st); break;
-    default: launch_pairs<8, NS>(norm, wg, wu, x, norm_w, eps, kind, y, n, units, rb, st); break;
+    case 1: launch_pairs<1, NS < 2 ? NS : 2>(a, st); break;
+    case 2: launch_pairs<2, NS < 3 ? NS : 3>(a, st); break;
+    case 3: launch_pairs<3, NS>(a, st); break;
+    case 4: launch_pairs<4, NS>(a, st); break;
+    case 5: launch_pairs<5, NS>(a, st); break;
+    case 6: launch_pairs<6, NS>(a, st); break;
+    case 7: launch_pairs<7, NS>(a, st); break;
+    default: launch_pairs<8, NS>(a, st); break;
     }
 }
 
@@ -766,26 +835,29 @@ int gemv_q4k_pairs_npw(int64_t n) {
 }
 
 // FFN block launch 1 for Q4_K gate/up with k <= 4096 (k % 256 == 0): y[p] =
-// act(gate_p . n, up_p . n), p < n_neurons; arguments validated by
-// gemv_dispatch_fused.
+// act(gate_p . n, up_p . n), p < n neurons; with `active`, the gathered
+// form (y is the hidden vector of i_dim entries, above).  Arguments
+// validated by the callers.
 int gemv_q4k_pairs(const void* wg, const void* wu, const float* x, const float* norm_w, float eps, int kind,
-                   float* y, int64_t n, int64_t k, hipStream_t st) {
+                   float* y, int64_t n, int64_t k, hipStream_t st, const int32_t* active, const int32_t* n_dev,
+                   int64_t i_dim) {
     const int npw = gemv_q4k_pairs_npw(n);
     const int units = static_cast<int>(k / 64);
-    if (npw == 0 || units > UNITS_MAX || k % 256 != 0 || n > INT32_MAX) {
+    if (npw == 0 || units > UNITS_MAX || k % 256 != 0 || n > INT32_MAX || i_dim > INT32_MAX ||
+        (active && i_dim * row_bytes(TYPE_Q4_K, k) >= (int64_t(1) << 32))) {
         set_error("vb_gemv: internal: Q4_K pairs kernel shape (n=%lld, k=%lld)", static_cast<long long>(n),
                   static_cast<long long>(k));
         return E_INVAL;
     }
-    const uint32_t rb = static_cast<uint32_t>(row_bytes(TYPE_Q4_K, k));
+    PairsArgs a{wg, wu, x, norm_w, eps, kind, y, static_cast<int>(n), units,
+                static_cast<uint32_t>(row_bytes(TYPE_Q4_K, k)), active, n_dev, static_cast<int>(i_dim)};
     const int ring = knobs().gemv_ring;  // neurons in flight while computing (default 2)
-    const int ni = static_cast<int>(n);
     if (ring == 1)
-        launch_pairs_npw<2>(npw, norm_w != nullptr, wg, wu, x, norm_w, eps, kind, y, ni, units, rb, st);
+        launch_pairs_npw<2>(npw, a, st);
     else if (ring >= 3)
-        launch_pairs_npw<4>(npw, norm_w != nullptr, wg, wu, x, norm_w, eps, kind, y, ni, units, rb, st);
+        launch_pairs_npw<4>(npw, a, st);
     else
-        launch_pairs_npw<3>(npw, norm_w != nullptr, wg, wu, x, norm_w, eps, kind, y, ni, units, rb, st);
+        launch_pairs_npw<3>(npw, a, st);
     return check_launch("vb_gemv");
 }
 

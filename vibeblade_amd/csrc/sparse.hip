@@ -956,6 +956,20 @@ int sparse_ffn_impl(const void* wg, const void* wu, const void* wd, int32_t down
                                                                                        resid, y);
         return check_launch(fn);
     }
+    // GGUF down, Q4_K gate/up with h <= 4096: one launch writes the whole
+    // hidden vector (act(g, u) on the active set, zeros elsewhere) on the
+    // short-row arithmetic, then the down GEMV (with the residual)
+    if (down_layout == 0 && ggml_type == TYPE_Q4_K && h <= 4096 && h % 256 == 0 && !knobs().gemv_q4k_general &&
+        gemv_q4k_pairs_npw(n_active) > 0 && reinterpret_cast<uintptr_t>(xin) % 16 == 0 &&
+        reinterpret_cast<uintptr_t>(wg) % 16 == 0 && reinterpret_cast<uintptr_t>(wu) % 16 == 0) {
+        float* hid = reinterpret_cast<float*>(wsb + ws.hid);
+        int rc = gemv_q4k_pairs(wg, wu, xin, nw, eps, act_kind, hid, n_active, h, st, active, n_dev, i);
+        if (rc != OK) return rc;
+        if (!residual) return gemv_dispatch(wd, hid, y, h, i, ggml_type, st);
+        GemvFuse fd;
+        fd.resid = x;
+        return gemv_dispatch_fused(wd, RowSrc{}, fd, hid, y, h, i, ggml_type, st);
+    }
     // 1. gate/up on the active rows (with the norm in the encode)
     RowSrc src;
     src.w2 = wu;

@@ -92,10 +92,13 @@ int gemv_q4k_split_rpw(int64_t n, int64_t k);
 // Q4_K gate/up pairs with the activation epilogue (and an optional RMSNorm of
 // x) for k <= 4096 on the short-row arithmetic (gemv_q4k.hip): y[p] =
 // act(gate_p . n, up_p . n) for p < n neurons; gemv_q4k_pairs_npw is 0 for
-// neuron counts it does not take.
+// neuron counts it does not take.  With `active` (sorted, unique): neuron p
+// is row active[p] (p below the device count n_dev when given) and y is the
+// whole hidden vector of i_dim entries, zeros off the active set.
 int gemv_q4k_pairs_npw(int64_t n);
 int gemv_q4k_pairs(const void* wg, const void* wu, const float* x, const float* norm_w, float eps, int kind,
-                   float* y, int64_t n, int64_t k, hipStream_t st);
+                   float* y, int64_t n, int64_t k, hipStream_t st, const int32_t* active = nullptr,
+                   const int32_t* n_dev = nullptr, int64_t i_dim = 0);
 int gemv_q4k_split(const void* w, const float* x, float* y, const float* resid, int64_t n, int64_t k,
                    hipStream_t st);
 // Q4_K M=1 GEMV on the int8 matrix cores (gemv_q4k_mfma.hip); arguments
