@@ -128,7 +128,8 @@ def test_gemv_dot_launch_shapes(knob, cfg, ring):
     """v_dot4 kernel launch overrides: rows per wave x ring depth (1-4; rows
     not a multiple of the depth take padding steps), one k-slice (k = 4096)
     and four (k = 14336)."""
-    knob("VB_GEMV_Q4K_PATH", "dot")  # Q4_K through the general kernel too
+    knob("VB_GEMV_Q4K_PATH", "dot")  # Q4_K and Q6_K through the general kernel too
+    knob("VB_GEMV_Q6K_PATH", "dot")
     knob("VB_GEMV_CFG", cfg)
     if ring:
         knob("VB_GEMV_RING", ring)
@@ -322,6 +323,86 @@ def test_gemv_q4k_short_k_idle_lanes(rows, k):
     want = O.gemv(qt.to_numpy_bytes(), x, rows, k, qt.qtype)
     assert O.rel_l2(y, want) <= GEMV_TOL
     assert np.max(np.abs(y - want)) <= 1e-3 * np.abs(want).max() + 1e-6
+
+
+# ---- the short-row Q6_K kernel (k = 2048 / 4096, the lm_head shape) ---------
+
+def _q6k_case(rows, k, seed):
+    qt = QTensor.quantize(rand_weights(rows, k, seed), ggml.GGML_TYPE_Q6_K)
+    x = np.random.default_rng(seed + 1).standard_normal(k).astype(np.float32)
+    return qt, x
+
+
+@pytest.mark.parametrize("rpw", [1, 2, 3, 5, 7, 8, 9, 16, 63])
+@pytest.mark.parametrize("ring", ["", "1", "2"])
+def test_gemv_q6k_short_rows_per_wave(knob, rpw, ring):
+    """Rows per wave forced with VB_GEMV_CFG: one group of up to 8 rows, or
+    8-row groups with a ragged last group (9, 63); each ring depth (ring 2
+    past 8 rows per wave falls back to 3 rows in flight); three full
+    workgroups and a ragged one."""
+    knob("VB_GEMV_CFG", f"8,{rpw}")
+    if ring:
+        knob("VB_GEMV_RING", ring)
+    rows = 3 * 8 * rpw + 5
+    qt, x = _q6k_case(rows, 4096, 100 + rpw)
+    y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy()
+    want = O.gemv(qt.to_numpy_bytes(), x, rows, 4096, qt.qtype)
+    assert O.rel_l2(y, want) <= GEMV_TOL
+    assert np.max(np.abs(y - want)) <= 1e-3 * np.abs(want).max() + 1e-6  # no row dropped or swapped
+
+
+@pytest.mark.parametrize("rows,k", [(1, 2048), (129, 2048), (4096, 2048), (1, 4096), (1024, 4096),
+                                    (14336, 4096), (40000, 4096)])
+def test_gemv_q6k_short_default_shapes(rows, k):
+    """Default shapes: k = 2048 leaves half the lanes idle (they read a unit
+    of their own row and contribute nothing); row counts from 1 to 20 rows
+    per wave."""
+    qt, x = _q6k_case(rows, k, rows + k)
+    y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy()
+    want = O.gemv(qt.to_numpy_bytes(), x, rows, k, qt.qtype)
+    assert O.rel_l2(y, want) <= GEMV_TOL
+    assert np.max(np.abs(y - want)) <= 1e-3 * np.abs(want).max() + 1e-6
+
+
+def test_gemv_q6k_short_integer_range():
+    """Codes and scales at the ends of their ranges: q6 = 0 (q = -32) or 63,
+    scales -128 / 127, and x at a constant magnitude, so every x16 is
+    +-16383 and each run's integer sum reaches 16 * 32 * 16383; the pair
+    sums S_01 / S_23 then sit just below 2^31.  Random bytes in other rows
+    (finite fp16 d)."""
+    k, rows = 4096, 64
+    rng = np.random.default_rng(9)
+    raw = rng.integers(0, 256, (rows, ggml.row_bytes(ggml.GGML_TYPE_Q6_K, k)), dtype=np.uint8)
+    blk = raw.reshape(rows, -1, 210)
+    blk[:, :, 209] &= 0x7B            # fp16 d finite
+    blk[0, :, :192] = 0               # q6 = 0 everywhere: q = -32
+    blk[0, :, 192:208] = 0x80         # scales -128
+    blk[1, :, :192] = 0xFF            # q6 = 63: q = 31
+    blk[1, :, 192:208] = 0x7F         # scales 127
+    blk[2, :, :192] = 0
+    blk[2, :, 192:208] = 0x7F
+    blk[:3, :, 208:210] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    for x in (np.ones(k, np.float32), -np.ones(k, np.float32), np.where(np.arange(k) % 2, 1.0, -1.0).astype(np.float32)):
+        qt = QTensor.from_bytes(raw, ggml.GGML_TYPE_Q6_K, rows, k)
+        y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy()
+        want = O.gemv(raw, x, rows, k, ggml.GGML_TYPE_Q6_K)
+        assert np.allclose(y[:3], want[:3], rtol=1e-5, atol=0), (y[:3], want[:3])
+        assert O.rel_l2(y, want) <= GEMV_TOL
+
+
+def test_gemv_q6k_short_matches_general_kernel(knob):
+    """The short-row kernel and the general kernel agree at the lm_head shape,
+    both close to the oracle; repeated launches are bit-identical."""
+    rows, k = 128256, 4096
+    gen = torch.Generator(device="cuda").manual_seed(79)
+    qt = QTensor.quantize(torch.randn((rows, k), generator=gen, device="cuda") * 0.02, ggml.GGML_TYPE_Q6_K)
+    x = torch.randn(k, generator=gen, device="cuda")
+    y_short = gemv(qt, x).cpu().numpy()
+    assert np.array_equal(bits(gemv(qt, x).cpu().numpy()), bits(y_short))
+    knob("VB_GEMV_Q6K_PATH", "dot")
+    y_gen = gemv(qt, x).cpu().numpy()
+    want = O.gemv(qt.to_numpy_bytes(), x.cpu().numpy(), rows, k, qt.qtype)
+    assert O.rel_l2(y_short, want) <= 2e-4 and O.rel_l2(y_gen, want) <= 2e-4
 
 
 # ---- the split-row Q4_K kernel (4096 < k <= 16384, rows over 2/4/8 waves) --

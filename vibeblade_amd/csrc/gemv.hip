@@ -533,7 +533,14 @@ int gemv_dispatch_fused(const void* w, const RowSrc& src, const GemvFuse& fz, co
             return gemv_q4k_split(w, x, y, fz.resid, n, k, st);
         return launch_gemv_q<TYPE_Q4_K>(w, src, fz, x, y, n, k, rb, st);
     }
-    case TYPE_Q6_K: return launch_gemv_q<TYPE_Q6_K>(w, src, fz, x, y, n, k, rb, st);
+    case TYPE_Q6_K: {
+        // plain rows of k = 2048 / 4096 (the lm_head shape): the short-row kernel
+        const bool plain = !fz.any() && !src.dense_pairs && !src.n_dev && !src.gidx && src.zn == 0;
+        if (plain && !knobs().gemv_q6k_general && reinterpret_cast<uintptr_t>(w) % 16 == 0 &&
+            gemv_q6k_rpw(n, k) > 0)
+            return gemv_q6k_short(w, x, y, n, k, st);
+        return launch_gemv_q<TYPE_Q6_K>(w, src, fz, x, y, n, k, rb, st);
+    }
     case TYPE_Q8_0: return launch_gemv_q<TYPE_Q8_0>(w, src, fz, x, y, n, k, rb, st);
     case TYPE_Q5_K: return launch_gemv_q<TYPE_Q5_K>(w, src, fz, x, y, n, k, rb, st);
     case TYPE_Q2_K: return launch_gemv_q<TYPE_Q2_K>(w, src, fz, x, y, n, k, rb, st);

@@ -1,6 +1,9 @@
 // Q4_K GEMV for rows of k <= 4096 (one 64-element unit per lane):
 // y[n] = sum_k W[n, k] x[k], W in the GGUF layout.  The headline decode
-// shape (Llama-3-8B FFN gate/up, 14336 x 4096) runs here.
+// shape (Llama-3-8B FFN gate/up, 14336 x 4096) runs here.  The same
+// short-row arithmetic serves the Q6_K GEMV for k = 2048 / 4096 (the lm_head),
+// the Q4_K gate/up pairs of the FFN block and the split-row Q4_K GEMV for
+// 4096 < k <= 16384 (further down).
 //
 // Replaces gemv_dequant (cpp/src/dequant.cpp:739-780) for Q4_K weights: no
 // weight is decoded to floats.  Per row and lane the work is integer dot
@@ -315,6 +318,242 @@ __global__ void __launch_bounds__(64 * WPG) gemv_q4k_kernel(const uint8_t* __res
     const int g = lane >> 3;
     const int r = row_of_group(g);
     if ((lane & 7) == 0 && r < RPW && row0 + r < n) y[row0 + r] = tot;
+}
+
+// ---- Q6_K short rows (k = 2048 or 4096): the lm_head shape ------------------
+//
+// Unit u (lane) = quarter c = u % 4 of super-block u / 4 (210 B: ql[128],
+// qh[64], int8 scales[16], fp16 d; the GGUF Q6_K layout), h = c / 2, l0 =
+// 16 (c % 2): four 16-element runs t at super-block elements 128 h + 32 t +
+// l0 + [0, 16), y = d sc_t (q6 - 32) with
+//   q6 = nibble | (qh bits 2t, 2t + 1) << 4,
+//   nibble: low (t < 2) or high (t >= 2) half of ql[64 h + 32 (t % 2) + l0 + i],
+//   qh bits from qh[32 h + l0 + i], sc_t = scales[8 h + c % 2 + 2 t]
+// (the vb_dequant_rows formula; the reference decodes these rows in
+// gemv_dequant, cpp/src/dequant.cpp:739-780, through dequantize_row).
+//
+// Activations: the short-row encoding (one fp32 scale per unit, 15-bit x16
+// split into signed bytes), its element order run-major (element 16 t + i of
+// the unit is run t's element i), and the four run sums I_t kept as 32 I_t.
+// Per run, in integers: D_t = sum (q6 - 32) x16 = sum q6 x16 - 32 I_t, with
+// the unsigned code q6 (0..63) in the v_dot4 bytes (two per 4 weights);
+// |D_t| <= 16 * 32 * 16383 <
+// 2^23, so the 24-bit multiplies give S_01 = sc_0 D_0 + sc_1 D_1 and S_23 =
+// sc_2 D_2 + sc_3 D_3 exactly (each below 2^31), and the lane's share of the
+// row is d s_u (S_01 + S_23).
+//
+// The code bytes come from ql and qh with one bit-select per 4 bytes: qh is
+// split once per unit into its even fields (qh & 0x33333333) and odd fields
+// (qh & 0xCC..), each shifted so field t lands on bits 4-5 of the byte and
+// bits 6-7 stay clear; the select keeps the nibble's bits 0-3.
+//
+// Rows: a 3360 B row is read as contiguous 16-byte pieces (slots L, 64 + L,
+// 128 + L, 192 + L of the row for lane L, the last for L < 18) into the
+// wave's LDS row buffer; units at odd super-blocks sit 2 bytes past a dword
+// there and are read as 20 aligned bytes plus v_alignbyte.  Rows stream
+// through a ring of NS, G rows per batched reduction (reduce8), the wave's
+// rows in ceil(rpw / G) groups.
+constexpr int XQ_Q6_QUADS = 10;    // xh[16], xl[16] dwords, {32 I_t}, {s}
+constexpr int Q6_ROW_SLOTS = 210;  // 16-byte slots of a k = 4096 row (3360 B)
+
+struct XU6 {
+    uint32_t h[16], l[16];
+    int c[4];  // 32 I_t
+    float s;
+};
+
+// Task t = 8 consecutive elements (run p / 2, half p % 2) of unit t / 8; the
+// caller loads them.  Units at or past `units` encode as zeros.
+__device__ __forceinline__ void encode_task_q6(const float* v_in, int task, int units, uint4* xq, bool store) {
+    const int u = task >> 3, p = task & 7;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = u < units ? v_in[i] : 0.f;
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, dpp_mov_f<0xB1>(amax));
+    amax = fmaxf(amax, dpp_mov_f<0x4E>(amax));
+    amax = fmaxf(amax, dpp_mov_f<0x141>(amax));
+    const float inv = amax > 0.f ? static_cast<float>(X15_MAX) / amax : 0.f;
+    uint32_t ph[2] = {0, 0}, pl[2] = {0, 0};
+    int isum = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        int q = static_cast<int>(rintf(v[i] * inv));
+        q = q > X15_MAX ? X15_MAX : (q < -X15_MAX ? -X15_MAX : q);
+        isum += q;
+        const int lo = ((q + 128) & 255) - 128;
+        const int hi = (q - lo) >> 8;
+        ph[i >> 2] |= static_cast<uint32_t>(hi & 255) << (8 * (i & 3));
+        pl[i >> 2] |= static_cast<uint32_t>(lo & 255) << (8 * (i & 3));
+    }
+    isum += dpp_mov_i<0xB1>(isum);  // the run's two tasks (lanes 2t, 2t + 1)
+    if (!store) return;
+    uint4* b = xq + u;
+    reinterpret_cast<uint2*>(&b[(p >> 1) * UNITS_MAX])[p & 1] = make_uint2(ph[0], ph[1]);
+    reinterpret_cast<uint2*>(&b[(4 + (p >> 1)) * UNITS_MAX])[p & 1] = make_uint2(pl[0], pl[1]);
+    if ((p & 1) == 0) reinterpret_cast<uint32_t*>(&b[8 * UNITS_MAX])[p >> 1] = static_cast<uint32_t>(32 * isum);
+    if (p == 0) reinterpret_cast<uint32_t*>(&b[9 * UNITS_MAX])[0] = __float_as_uint(amax / static_cast<float>(X15_MAX));
+}
+
+__device__ __forceinline__ XU6 read_unit_q6(const uint4* xq, int u) {
+    XU6 x;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint4 h = xq[i * UNITS_MAX + u], l = xq[(4 + i) * UNITS_MAX + u];
+        x.h[4 * i] = h.x; x.h[4 * i + 1] = h.y; x.h[4 * i + 2] = h.z; x.h[4 * i + 3] = h.w;
+        x.l[4 * i] = l.x; x.l[4 * i + 1] = l.y; x.l[4 * i + 2] = l.z; x.l[4 * i + 3] = l.w;
+    }
+    const uint4 c = xq[8 * UNITS_MAX + u];
+    x.c[0] = static_cast<int>(c.x); x.c[1] = static_cast<int>(c.y);
+    x.c[2] = static_cast<int>(c.z); x.c[3] = static_cast<int>(c.w);
+    x.s = __uint_as_float(reinterpret_cast<const uint32_t*>(&xq[9 * UNITS_MAX + u])[0]);
+    return x;
+}
+
+struct Q6Row { uint4 la, lb, qh; int sc[4]; uint32_t d; };
+struct Q6Raw { u32x4 a, b, c, e; };
+
+// (a & 0x0F0F0F0F) | (b & 0xF0F0F0F0): one v_bitop3 (0xCA: s0 ? s1 : s2 per
+// bit; written out, the compiler narrows the masks from the known-zero bits
+// of b and emits two instructions)
+__device__ __forceinline__ uint32_t nib_sel(uint32_t a, uint32_t b) {
+    return __builtin_amdgcn_bitop3_b32(0x0F0F0F0Fu, a, b, 0xCA);
+}
+
+__device__ __forceinline__ float row_part_q6(const Q6Row& r, const XU6& x) {
+    const uint32_t la[4] = {r.la.x, r.la.y, r.la.z, r.la.w};
+    const uint32_t lb[4] = {r.lb.x, r.lb.y, r.lb.z, r.lb.w};
+    const uint32_t qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+    int D[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        uint32_t q[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t ev = qh[j] & 0x33333333u, od = qh[j] & 0xCCCCCCCCu;  // fields 0, 2 / 1, 3
+            if (t == 0) q[j] = nib_sel(la[j], ev << 4);
+            else if (t == 1) q[j] = nib_sel(lb[j], od << 2);
+            else if (t == 2) q[j] = nib_sel(la[j] >> 4, ev);
+            else q[j] = nib_sel(lb[j] >> 4, od >> 2);
+        }
+        // one accumulation chain: the xh sum, times 256 minus 32 I_t, then the
+        // xl products (written as 256 dh + dl the compiler rebuilds the sum
+        // from shifts, since the 24-bit multiply reads only 24 bits of it)
+        int a = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) a = sdot4(q[j], x.h[4 * t + j], a);
+        a = (a << 8) - x.c[t];
+#pragma unroll
+        for (int j = 0; j < 4; j++) a = sdot4(q[j], x.l[4 * t + j], a);
+        D[t] = a;
+    }
+    const int s01 = __mul24(r.sc[0], D[0]) + __mul24(r.sc[1], D[1]);
+    const int s23 = __mul24(r.sc[2], D[2]) + __mul24(r.sc[3], D[3]);
+    return (static_cast<float>(s01) + static_cast<float>(s23)) * (f16lo(r.d) * x.s);
+}
+
+template <int G, int NS>
+__global__ void __launch_bounds__(512) gemv_q6k_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                                       float* __restrict__ y, int n, int units, uint32_t rb, int rpw) {
+    static_assert(G >= 1 && G <= 8 && NS >= 2, "up to 8 rows per reduction");
+    __shared__ uint4 xq[XQ_Q6_QUADS * UNITS_MAX];
+    __shared__ u32x4 rowbuf[8][Q6_ROW_SLOTS];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int row0 = (static_cast<int>(blockIdx.x) * 8 + wave) * rpw;
+    // the wave's rows [row0, row0 + nrow); loads of rows past them fall
+    // outside the resource (zeros, no memory access)
+    const int left = n - row0;
+    const int nrow = left < 0 ? 0 : (left < rpw ? left : rpw);
+    const __amdgpu_buffer_rsrc_t rs =
+        make_rsrc(w + static_cast<int64_t>(nrow > 0 ? row0 : 0) * rb, static_cast<uint32_t>(nrow) * rb);
+    const bool valid = lane < units;
+    const int u = valid ? lane : (lane & 3);  // idle lanes read unit (lane % 4), discarded
+    const int slots = static_cast<int>(rb >> 4);
+    const int pd = 192 + (lane < 18 ? lane : (lane & 15));
+    auto vo = [&](int slot) { return 16u * static_cast<uint32_t>(slot < slots ? slot : lane & 7); };
+    const uint32_t v0 = vo(lane), v1 = vo(64 + lane), v2 = vo(128 + lane), v3 = vo(pd);
+    u32x4* rbuf = rowbuf[wave];
+    const uint8_t* rbytes = reinterpret_cast<const uint8_t*>(rbuf);
+    // the unit's bytes in the row buffer: super-block B = 210 (u / 4), 2 bytes
+    // past a dword when u / 4 is odd
+    const int sbo = 210 * (u >> 2), c = u & 3, hh = c >> 1, l0 = 16 * (c & 1);
+    const uint32_t sh = static_cast<uint32_t>(sbo & 2);
+    const uint8_t* pla = rbytes + (sbo + 64 * hh + l0 - static_cast<int>(sh));
+    const uint8_t* plb = pla + 32;
+    const uint8_t* pqh = rbytes + (sbo + 128 + 32 * hh + l0 - static_cast<int>(sh));
+    const int8_t* psc = reinterpret_cast<const int8_t*>(rbytes + sbo + 192 + 8 * hh + (c & 1));
+    const uint16_t* pdd = reinterpret_cast<const uint16_t*>(rbytes + sbo + 208);
+
+    // the row offset goes into the per-lane offset, which the range check covers
+    auto issue = [&](Q6Raw& b, int s) {
+        const uint32_t so = static_cast<uint32_t>(s) * rb;
+        b.a = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(v0 + so), 0, CACHE_NT);
+        b.b = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(v1 + so), 0, CACHE_NT);
+        b.c = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(v2 + so), 0, CACHE_NT);
+        b.e = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(v3 + so), 0, CACHE_NT);
+    };
+    auto realign = [&](const uint8_t* p) {
+        const uint4 a = ld_b128_a4(p);
+        const uint32_t e = ld_b32(p + 16);
+        return make_uint4(__builtin_amdgcn_alignbyte(a.y, a.x, sh), __builtin_amdgcn_alignbyte(a.z, a.y, sh),
+                          __builtin_amdgcn_alignbyte(a.w, a.z, sh), __builtin_amdgcn_alignbyte(e, a.w, sh));
+    };
+    auto stage = [&](const Q6Raw& b) -> Q6Row {
+        rbuf[lane] = b.a;
+        rbuf[64 + lane] = b.b;
+        rbuf[128 + lane] = b.c;
+        rbuf[pd] = b.e;
+        Q6Row r;
+        r.la = realign(pla);
+        r.lb = realign(plb);
+        r.qh = realign(pqh);
+#pragma unroll
+        for (int t = 0; t < 4; t++) r.sc[t] = psc[2 * t];
+        r.d = *pdd;
+        return r;
+    };
+
+    // x first, then the first rows, then the encode (as the Q4_K kernel)
+    float xv[8];
+    const int task = static_cast<int>(threadIdx.x);
+    {
+        const int tu0 = task >> 3, p = task & 7;
+        const int tu = tu0 < units ? tu0 : units - 1;
+        const int off = 256 * (tu >> 2) + 128 * ((tu >> 1) & 1) + 16 * (tu & 1) + 32 * (p >> 1) + 8 * (p & 1);
+        const float4 a = *reinterpret_cast<const float4*>(x + off);
+        const float4 b = *reinterpret_cast<const float4*>(x + off + 4);
+        xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
+        xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    Q6Raw ring[NS];
+#pragma unroll
+    for (int s = 0; s < NS - 1; s++) issue(ring[s], s);
+    __builtin_amdgcn_sched_barrier(0);
+    encode_task_q6(xv, task, units, xq, true);
+    __syncthreads();
+    const XU6 xu = read_unit_q6(xq, u);
+
+    // G % NS == 0 whenever the wave has more than one group (host), so the
+    // ring slot of row g0 + i is i % NS in every group
+    for (int g0 = 0; g0 < nrow; g0 += G) {
+        float acc[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc[i] = 0.f;
+#pragma unroll
+        for (int i = 0; i < G; i++) {
+            issue(ring[(i + NS - 1) % NS], g0 + i + NS - 1);
+            const float part = row_part_q6(stage(ring[i % NS]), xu);
+            acc[i] = valid ? part : 0.f;
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        const float tot = reduce8(acc);
+        const int r = g0 + row_of_group(lane >> 3);
+        if ((lane & 7) == 0 && row_of_group(lane >> 3) < G && r < nrow) y[row0 + r] = tot;
+    }
 }
 
 // ---- gate/up pairs with the activation epilogue (FFN block launch 1) ---------
@@ -718,6 +957,29 @@ void launch_rpw(int rpw, const void* w, const float* x, float* y, int n, int uni
     }
 }
 
+template <int G, int NS>
+void launch_q6(const void* w, const float* x, float* y, int n, int units, uint32_t rb, int rpw, hipStream_t st) {
+    const int grid = (n + 8 * rpw - 1) / (8 * rpw);
+    gemv_q6k_kernel<G, NS><<<dim3(static_cast<uint32_t>(grid)), dim3(512), 0, st>>>(
+        static_cast<const uint8_t*>(w), x, y, n, units, rb, rpw);
+}
+
+// rpw <= 8: one group of rpw rows; above, groups of 8 rows (NS divides 8)
+template <int NS>
+void launch_q6_rpw(int rpw, const void* w, const float* x, float* y, int n, int units, uint32_t rb,
+                   hipStream_t st) {
+    switch (rpw) {
+    case 1: launch_q6<1, NS>(w, x, y, n, units, rb, rpw, st); break;
+    case 2: launch_q6<2, NS>(w, x, y, n, units, rb, rpw, st); break;
+    case 3: launch_q6<3, NS>(w, x, y, n, units, rb, rpw, st); break;
+    case 4: launch_q6<4, NS>(w, x, y, n, units, rb, rpw, st); break;
+    case 5: launch_q6<5, NS>(w, x, y, n, units, rb, rpw, st); break;
+    case 6: launch_q6<6, NS>(w, x, y, n, units, rb, rpw, st); break;
+    case 7: launch_q6<7, NS>(w, x, y, n, units, rb, rpw, st); break;
+    default: launch_q6<8, NS>(w, x, y, n, units, rb, rpw, st); break;
+    }
+}
+
 // Launch shape for n rows: 8-wave workgroups, one per CU, with RPW =
 // ceil(n / (8 CUs)) <= 8 rows per wave (14336 rows: 7); 16-wave workgroups
 // for up to 16 x 8 rows per CU (measured at 14336 x 4096: 16 waves of 4 rows,
@@ -776,6 +1038,41 @@ int gemv_q4k_short(const void* w, const float* x, float* y, int64_t n, int64_t k
         else if (ring == 2) launch_rpw<3, 16>(sh.rpw, w, x, y, ni, units, rb, st);
         else launch_rpw<4, 16>(sh.rpw, w, x, y, ni, units, rb, st);
     }
+    return check_launch("vb_gemv");
+}
+
+// Q6_K short-row kernel: rows per wave for n rows of k = 2048 or 4096
+// elements (one 8-wave workgroup per CU; VB_GEMV_CFG="8,rpw" overrides),
+// 0 for other k.
+int gemv_q6k_rpw(int64_t n, int64_t k) {
+    if ((k != 2048 && k != 4096) || n < 1 || n > INT32_MAX) return 0;
+    const Knobs& kb = knobs();
+    if (kb.gemv_cfg_wpg == 8 && kb.gemv_cfg_rpg >= 1 && kb.gemv_cfg_rpg <= 4096) return kb.gemv_cfg_rpg;
+    const int64_t groups = static_cast<int64_t>(num_cus()) * 8;
+    const int64_t rpw = (n + groups - 1) / groups;
+    return rpw <= 4096 ? static_cast<int>(rpw) : 0;
+}
+
+// Plain Q6_K GEMV, k = 2048 or 4096, 16-byte aligned rows; arguments
+// validated by gemv_dispatch_fused.
+int gemv_q6k_short(const void* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t st) {
+    const int rpw = gemv_q6k_rpw(n, k);
+    if (rpw == 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0) {
+        set_error("vb_gemv: internal: Q6_K short-row kernel shape (n=%lld, k=%lld)", static_cast<long long>(n),
+                  static_cast<long long>(k));
+        return E_INVAL;
+    }
+    const uint32_t rb = static_cast<uint32_t>(row_bytes(TYPE_Q6_K, k));
+    const int ni = static_cast<int>(n), units = static_cast<int>(k / 64);
+    // NS - 1 rows in flight while computing (VB_GEMV_RING; default 1: on
+    // MI355X 65.5 us at 128256 x 4096 against 66.9 us with 2 or 3, 9.4
+    // against 9.8 / 10.1 us at 14336 x 4096); past 8 rows per wave the ring
+    // must divide the 8-row groups
+    int ns = knobs().gemv_ring > 0 ? knobs().gemv_ring + 1 : 2;
+    if (rpw > 8 && ns != 2) ns = 4;
+    if (ns == 2) launch_q6_rpw<2>(rpw, w, x, y, ni, units, rb, st);
+    else if (ns == 3) launch_q6_rpw<3>(rpw, w, x, y, ni, units, rb, st);
+    else launch_q6_rpw<4>(rpw, w, x, y, ni, units, rb, st);
     return check_launch("vb_gemv");
 }
 
