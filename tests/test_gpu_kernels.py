@@ -128,8 +128,9 @@ def test_gemv_dot_launch_shapes(knob, cfg, ring):
     """v_dot4 kernel launch overrides: rows per wave x ring depth (1-4; rows
     not a multiple of the depth take padding steps), one k-slice (k = 4096)
     and four (k = 14336)."""
-    knob("VB_GEMV_Q4K_PATH", "dot")  # Q4_K and Q6_K through the general kernel too
+    knob("VB_GEMV_Q4K_PATH", "dot")  # Q4_K, Q6_K and Q8_0 through the general kernel too
     knob("VB_GEMV_Q6K_PATH", "dot")
+    knob("VB_GEMV_Q8_PATH", "dot")
     knob("VB_GEMV_CFG", cfg)
     if ring:
         knob("VB_GEMV_RING", ring)
@@ -325,17 +326,21 @@ def test_gemv_q4k_short_k_idle_lanes(rows, k):
     assert np.max(np.abs(y - want)) <= 1e-3 * np.abs(want).max() + 1e-6
 
 
-# ---- the short-row Q6_K kernel (k = 2048 / 4096, the lm_head shape) ---------
+# ---- the short-row Q6_K / Q8_0 kernel (rows of whole 16-byte slots, k <= 4096) --
 
-def _q6k_case(rows, k, seed):
-    qt = QTensor.quantize(rand_weights(rows, k, seed), ggml.GGML_TYPE_Q6_K)
+SHORT_TYPES = [ggml.GGML_TYPE_Q6_K, ggml.GGML_TYPE_Q8_0]
+
+
+def _short_case(qtype, rows, k, seed):
+    qt = QTensor.quantize(rand_weights(rows, k, seed), qtype)
     x = np.random.default_rng(seed + 1).standard_normal(k).astype(np.float32)
     return qt, x
 
 
+@pytest.mark.parametrize("qtype", SHORT_TYPES)
 @pytest.mark.parametrize("rpw", [1, 2, 3, 5, 7, 8, 9, 16, 63])
 @pytest.mark.parametrize("ring", ["", "1", "2"])
-def test_gemv_q6k_short_rows_per_wave(knob, rpw, ring):
+def test_gemv_short_rows_per_wave(knob, qtype, rpw, ring):
     """Rows per wave forced with VB_GEMV_CFG: one group of up to 8 rows, or
     8-row groups with a ragged last group (9, 63); each ring depth (ring 2
     past 8 rows per wave falls back to 3 rows in flight); three full
@@ -344,24 +349,48 @@ def test_gemv_q6k_short_rows_per_wave(knob, rpw, ring):
     if ring:
         knob("VB_GEMV_RING", ring)
     rows = 3 * 8 * rpw + 5
-    qt, x = _q6k_case(rows, 4096, 100 + rpw)
+    qt, x = _short_case(qtype, rows, 4096, 100 + rpw)
     y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy()
     want = O.gemv(qt.to_numpy_bytes(), x, rows, 4096, qt.qtype)
     assert O.rel_l2(y, want) <= GEMV_TOL
     assert np.max(np.abs(y - want)) <= 1e-3 * np.abs(want).max() + 1e-6  # no row dropped or swapped
 
 
-@pytest.mark.parametrize("rows,k", [(1, 2048), (129, 2048), (4096, 2048), (1, 4096), (1024, 4096),
-                                    (14336, 4096), (40000, 4096)])
-def test_gemv_q6k_short_default_shapes(rows, k):
-    """Default shapes: k = 2048 leaves half the lanes idle (they read a unit
-    of their own row and contribute nothing); row counts from 1 to 20 rows
-    per wave."""
-    qt, x = _q6k_case(rows, k, rows + k)
+@pytest.mark.parametrize("qtype,rows,k", [(ggml.GGML_TYPE_Q6_K, 1, 2048), (ggml.GGML_TYPE_Q6_K, 129, 2048),
+                                          (ggml.GGML_TYPE_Q6_K, 4096, 2048), (ggml.GGML_TYPE_Q6_K, 1, 4096),
+                                          (ggml.GGML_TYPE_Q6_K, 1024, 4096), (ggml.GGML_TYPE_Q6_K, 14336, 4096),
+                                          (ggml.GGML_TYPE_Q6_K, 40000, 4096), (ggml.GGML_TYPE_Q8_0, 1, 256),
+                                          (ggml.GGML_TYPE_Q8_0, 33, 512), (ggml.GGML_TYPE_Q8_0, 300, 1024),
+                                          (ggml.GGML_TYPE_Q8_0, 129, 2816), (ggml.GGML_TYPE_Q8_0, 4096, 4096),
+                                          (ggml.GGML_TYPE_Q8_0, 14336, 4096), (ggml.GGML_TYPE_Q8_0, 40000, 4096)])
+def test_gemv_short_default_shapes(qtype, rows, k):
+    """Default shapes: k < 4096 leaves lanes idle (they read a unit of their
+    own row and contribute nothing); row counts from 1 to 20 rows per wave."""
+    qt, x = _short_case(qtype, rows, k, rows + k)
     y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy()
     want = O.gemv(qt.to_numpy_bytes(), x, rows, k, qt.qtype)
     assert O.rel_l2(y, want) <= GEMV_TOL
     assert np.max(np.abs(y - want)) <= 1e-3 * np.abs(want).max() + 1e-6
+
+
+def test_gemv_q8_short_integer_range():
+    """Q8_0 codes at -128 / 127 with x at a constant magnitude (every x16 =
+    +-16383): each block's integer sum reaches 32 * 128 * 16383; random bytes
+    in the other rows (finite fp16 d)."""
+    k, rows = 4096, 64
+    rng = np.random.default_rng(10)
+    raw = rng.integers(0, 256, (rows, ggml.row_bytes(ggml.GGML_TYPE_Q8_0, k)), dtype=np.uint8)
+    blk = raw.reshape(rows, -1, 34)
+    blk[:, :, 1] &= 0x7B  # fp16 d finite
+    blk[0, :, 2:] = 0x80  # -128
+    blk[1, :, 2:] = 0x7F  # 127
+    blk[:2, :, 0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    for x in (np.ones(k, np.float32), -np.ones(k, np.float32)):
+        qt = QTensor.from_bytes(raw, ggml.GGML_TYPE_Q8_0, rows, k)
+        y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy()
+        want = O.gemv(raw, x, rows, k, ggml.GGML_TYPE_Q8_0)
+        assert np.allclose(y[:2], want[:2], rtol=1e-5, atol=0), (y[:2], want[:2])
+        assert O.rel_l2(y, want) <= GEMV_TOL
 
 
 def test_gemv_q6k_short_integer_range():
@@ -390,16 +419,19 @@ def test_gemv_q6k_short_integer_range():
         assert O.rel_l2(y, want) <= GEMV_TOL
 
 
-def test_gemv_q6k_short_matches_general_kernel(knob):
-    """The short-row kernel and the general kernel agree at the lm_head shape,
-    both close to the oracle; repeated launches are bit-identical."""
-    rows, k = 128256, 4096
+@pytest.mark.parametrize("qtype,rows,env", [(ggml.GGML_TYPE_Q6_K, 128256, "VB_GEMV_Q6K_PATH"),
+                                            (ggml.GGML_TYPE_Q8_0, 4096, "VB_GEMV_Q8_PATH")])
+def test_gemv_short_matches_general_kernel(knob, qtype, rows, env):
+    """The short-row kernel and the general kernel agree at the lm_head and
+    Q8_0 4096 x 4096 shapes, both close to the oracle; repeated launches are
+    bit-identical."""
+    k = 4096
     gen = torch.Generator(device="cuda").manual_seed(79)
-    qt = QTensor.quantize(torch.randn((rows, k), generator=gen, device="cuda") * 0.02, ggml.GGML_TYPE_Q6_K)
+    qt = QTensor.quantize(torch.randn((rows, k), generator=gen, device="cuda") * 0.02, qtype)
     x = torch.randn(k, generator=gen, device="cuda")
     y_short = gemv(qt, x).cpu().numpy()
     assert np.array_equal(bits(gemv(qt, x).cpu().numpy()), bits(y_short))
-    knob("VB_GEMV_Q6K_PATH", "dot")
+    knob(env, "dot")
     y_gen = gemv(qt, x).cpu().numpy()
     want = O.gemv(qt.to_numpy_bytes(), x.cpu().numpy(), rows, k, qt.qtype)
     assert O.rel_l2(y_short, want) <= 2e-4 and O.rel_l2(y_gen, want) <= 2e-4

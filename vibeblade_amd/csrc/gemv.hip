@@ -533,15 +533,17 @@ int gemv_dispatch_fused(const void* w, const RowSrc& src, const GemvFuse& fz, co
             return gemv_q4k_split(w, x, y, fz.resid, n, k, st);
         return launch_gemv_q<TYPE_Q4_K>(w, src, fz, x, y, n, k, rb, st);
     }
-    case TYPE_Q6_K: {
-        // plain rows of k = 2048 / 4096 (the lm_head shape): the short-row kernel
+    case TYPE_Q6_K:
+    case TYPE_Q8_0: {
+        // plain rows of whole 16-byte slots, k <= 4096 (the lm_head and the
+        // Q8_0 4096 x 4096 shapes): the short-row kernel
         const bool plain = !fz.any() && !src.dense_pairs && !src.n_dev && !src.gidx && src.zn == 0;
-        if (plain && !knobs().gemv_q6k_general && reinterpret_cast<uintptr_t>(w) % 16 == 0 &&
-            gemv_q6k_rpw(n, k) > 0)
-            return gemv_q6k_short(w, x, y, n, k, st);
-        return launch_gemv_q<TYPE_Q6_K>(w, src, fz, x, y, n, k, rb, st);
+        const bool general = type == TYPE_Q6_K ? knobs().gemv_q6k_general : knobs().gemv_q8_general;
+        if (plain && !general && reinterpret_cast<uintptr_t>(w) % 16 == 0 && gemv_short_rpw(type, n, k) > 0)
+            return gemv_short(type, w, x, y, n, k, st);
+        if (type == TYPE_Q6_K) return launch_gemv_q<TYPE_Q6_K>(w, src, fz, x, y, n, k, rb, st);
+        return launch_gemv_q<TYPE_Q8_0>(w, src, fz, x, y, n, k, rb, st);
     }
-    case TYPE_Q8_0: return launch_gemv_q<TYPE_Q8_0>(w, src, fz, x, y, n, k, rb, st);
     case TYPE_Q5_K: return launch_gemv_q<TYPE_Q5_K>(w, src, fz, x, y, n, k, rb, st);
     case TYPE_Q2_K: return launch_gemv_q<TYPE_Q2_K>(w, src, fz, x, y, n, k, rb, st);
     case TYPE_Q3_K: return launch_gemv_q<TYPE_Q3_K>(w, src, fz, x, y, n, k, rb, st);

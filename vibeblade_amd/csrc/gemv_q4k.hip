@@ -354,7 +354,6 @@ __global__ void __launch_bounds__(64 * WPG) gemv_q4k_kernel(const uint8_t* __res
 // through a ring of NS, G rows per batched reduction (reduce8), the wave's
 // rows in ceil(rpw / G) groups.
 constexpr int XQ_Q6_QUADS = 10;    // xh[16], xl[16] dwords, {32 I_t}, {s}
-constexpr int Q6_ROW_SLOTS = 210;  // 16-byte slots of a k = 4096 row (3360 B)
 
 struct XU6 {
     uint32_t h[16], l[16];
@@ -412,9 +411,6 @@ __device__ __forceinline__ XU6 read_unit_q6(const uint4* xq, int u) {
     return x;
 }
 
-struct Q6Row { uint4 la, lb, qh; int sc[4]; uint32_t d; };
-struct Q6Raw { u32x4 a, b, c, e; };
-
 // (a & 0x0F0F0F0F) | (b & 0xF0F0F0F0): one v_bitop3 (0xCA: s0 ? s1 : s2 per
 // bit; written out, the compiler narrows the masks from the known-zero bits
 // of b and emits two instructions)
@@ -422,44 +418,146 @@ __device__ __forceinline__ uint32_t nib_sel(uint32_t a, uint32_t b) {
     return __builtin_amdgcn_bitop3_b32(0x0F0F0F0Fu, a, b, 0xCA);
 }
 
-__device__ __forceinline__ float row_part_q6(const Q6Row& r, const XU6& x) {
-    const uint32_t la[4] = {r.la.x, r.la.y, r.la.z, r.la.w};
-    const uint32_t lb[4] = {r.lb.x, r.lb.y, r.lb.z, r.lb.w};
-    const uint32_t qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
-    int D[4];
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        uint32_t q[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t ev = qh[j] & 0x33333333u, od = qh[j] & 0xCCCCCCCCu;  // fields 0, 2 / 1, 3
-            if (t == 0) q[j] = nib_sel(la[j], ev << 4);
-            else if (t == 1) q[j] = nib_sel(lb[j], od << 2);
-            else if (t == 2) q[j] = nib_sel(la[j] >> 4, ev);
-            else q[j] = nib_sel(lb[j] >> 4, od >> 2);
-        }
-        // one accumulation chain: the xh sum, times 256 minus 32 I_t, then the
-        // xl products (written as 256 dh + dl the compiler rebuilds the sum
-        // from shifts, since the 24-bit multiply reads only 24 bits of it)
-        int a = 0;
-#pragma unroll
-        for (int j = 0; j < 4; j++) a = sdot4(q[j], x.h[4 * t + j], a);
-        a = (a << 8) - x.c[t];
-#pragma unroll
-        for (int j = 0; j < 4; j++) a = sdot4(q[j], x.l[4 * t + j], a);
-        D[t] = a;
-    }
-    const int s01 = __mul24(r.sc[0], D[0]) + __mul24(r.sc[1], D[1]);
-    const int s23 = __mul24(r.sc[2], D[2]) + __mul24(r.sc[3], D[3]);
-    return (static_cast<float>(s01) + static_cast<float>(s23)) * (f16lo(r.d) * x.s);
+// 16 bytes at p + sh (sh 0 or 2) from the 20 bytes at the 4-aligned p
+__device__ __forceinline__ uint4 lds_realign(const uint8_t* p, uint32_t sh) {
+    const uint4 a = ld_b128_a4(p);
+    const uint32_t e = ld_b32(p + 16);
+    return make_uint4(__builtin_amdgcn_alignbyte(a.y, a.x, sh), __builtin_amdgcn_alignbyte(a.z, a.y, sh),
+                      __builtin_amdgcn_alignbyte(a.w, a.z, sh), __builtin_amdgcn_alignbyte(e, a.w, sh));
 }
 
-template <int G, int NS>
-__global__ void __launch_bounds__(512) gemv_q6k_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
-                                                       float* __restrict__ y, int n, int units, uint32_t rb, int rpw) {
+// Per-type parts of the short-row kernel: the row in 16-byte slots (k =
+// 4096), the activation encoding (element offset of task part p of unit u,
+// encode, read), the unit's bytes in the LDS row buffer and its dot product.
+template <int TYPE> struct ShortRow;
+
+template <> struct ShortRow<TYPE_Q6_K> {
+    static constexpr int SLOTS = 210;     // 3360 B
+    static constexpr int XQUADS = XQ_Q6_QUADS;
+    using X = XU6;
+    struct Row { uint4 la, lb, qh; int sc[4]; uint32_t d; };
+    struct Addr { const uint8_t *la, *qh; const int8_t* sc; const uint16_t* d; uint32_t sh; };
+    static __device__ int x_off(int u, int p) {
+        return 256 * (u >> 2) + 128 * ((u >> 1) & 1) + 16 * (u & 1) + 32 * (p >> 1) + 8 * (p & 1);
+    }
+    static __device__ void encode(const float* v, int task, int units, uint4* xq) {
+        encode_task_q6(v, task, units, xq, true);
+    }
+    static __device__ X read_x(const uint4* xq, int u) { return read_unit_q6(xq, u); }
+    // super-block B = 210 (u / 4) of the row buffer, 2 bytes past a dword
+    // when u / 4 is odd
+    static __device__ Addr addr(const uint8_t* rb, int u) {
+        const int sbo = 210 * (u >> 2), c = u & 3, hh = c >> 1, l0 = 16 * (c & 1);
+        Addr a;
+        a.sh = static_cast<uint32_t>(sbo & 2);
+        a.la = rb + (sbo + 64 * hh + l0 - static_cast<int>(a.sh));
+        a.qh = rb + (sbo + 128 + 32 * hh + l0 - static_cast<int>(a.sh));
+        a.sc = reinterpret_cast<const int8_t*>(rb + sbo + 192 + 8 * hh + (c & 1));
+        a.d = reinterpret_cast<const uint16_t*>(rb + sbo + 208);
+        return a;
+    }
+    static __device__ Row read(const Addr& a) {
+        Row r;
+        r.la = lds_realign(a.la, a.sh);
+        r.lb = lds_realign(a.la + 32, a.sh);
+        r.qh = lds_realign(a.qh, a.sh);
+#pragma unroll
+        for (int t = 0; t < 4; t++) r.sc[t] = a.sc[2 * t];
+        r.d = *a.d;
+        return r;
+    }
+    static __device__ float part(const Row& r, const X& x) {
+        const uint32_t la[4] = {r.la.x, r.la.y, r.la.z, r.la.w};
+        const uint32_t lb[4] = {r.lb.x, r.lb.y, r.lb.z, r.lb.w};
+        const uint32_t qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+        int D[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            uint32_t q[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t ev = qh[j] & 0x33333333u, od = qh[j] & 0xCCCCCCCCu;  // fields 0, 2 / 1, 3
+                if (t == 0) q[j] = nib_sel(la[j], ev << 4);
+                else if (t == 1) q[j] = nib_sel(lb[j], od << 2);
+                else if (t == 2) q[j] = nib_sel(la[j] >> 4, ev);
+                else q[j] = nib_sel(lb[j] >> 4, od >> 2);
+            }
+            // one accumulation chain: the xh sum, times 256 minus 32 I_t, then
+            // the xl products (written as 256 dh + dl the compiler rebuilds the
+            // sum from shifts, since the 24-bit multiply reads only 24 bits)
+            int a = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) a = sdot4(q[j], x.h[4 * t + j], a);
+            a = (a << 8) - x.c[t];
+#pragma unroll
+            for (int j = 0; j < 4; j++) a = sdot4(q[j], x.l[4 * t + j], a);
+            D[t] = a;
+        }
+        const int s01 = __mul24(r.sc[0], D[0]) + __mul24(r.sc[1], D[1]);
+        const int s23 = __mul24(r.sc[2], D[2]) + __mul24(r.sc[3], D[3]);
+        return (static_cast<float>(s01) + static_cast<float>(s23)) * (f16lo(r.d) * x.s);
+    }
+};
+
+// Q8_0: unit u = blocks 2u, 2u + 1 (68 B at 68 u, 4-byte aligned in the row
+// buffer): d0 = bytes 0-1, block 0's codes at bytes 2-33 (realigned by 2),
+// d1 = bytes 34-35, block 1's codes at 36-67.  The encoding is the Q4_K one
+// (elements 64 u .. 64 u + 63 in order); per block D = sum q x16 (|D| <=
+// 32 * 128 * 16383 < 2^31) and the lane's share s_u (d0 D0 + d1 D1).
+template <> struct ShortRow<TYPE_Q8_0> {
+    static constexpr int SLOTS = 272;     // 4352 B
+    static constexpr int XQUADS = XQ_UNIT_QUADS;
+    using X = XU;
+    struct Row { uint32_t w[17]; };
+    struct Addr { const uint8_t* p; };
+    static __device__ int x_off(int u, int p) { return 64 * u + 8 * p; }
+    static __device__ void encode(const float* v, int task, int units, uint4* xq) {
+        encode_task(v, task, units, xq, true);
+    }
+    static __device__ X read_x(const uint4* xq, int u) { return read_unit(xq, u); }
+    static __device__ Addr addr(const uint8_t* rb, int u) { return Addr{rb + 68 * u}; }
+    static __device__ Row read(const Addr& a) {
+        Row r;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint4 v = ld_b128_a4(a.p + 16 * i);
+            r.w[4 * i] = v.x; r.w[4 * i + 1] = v.y; r.w[4 * i + 2] = v.z; r.w[4 * i + 3] = v.w;
+        }
+        r.w[16] = ld_b32(a.p + 64);
+        return r;
+    }
+    static __device__ float part(const Row& r, const X& x) {
+        int a0 = 0, a1 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            a0 = sdot4(__builtin_amdgcn_alignbyte(r.w[i + 1], r.w[i], 2), x.h[i], a0);
+            a1 = sdot4(r.w[9 + i], x.h[8 + i], a1);
+        }
+        a0 <<= 8;
+        a1 <<= 8;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            a0 = sdot4(__builtin_amdgcn_alignbyte(r.w[i + 1], r.w[i], 2), x.l[i], a0);
+            a1 = sdot4(r.w[9 + i], x.l[8 + i], a1);
+        }
+        return (f16lo(r.w[0]) * static_cast<float>(a0) + f16hi(r.w[8]) * static_cast<float>(a1)) * x.s;
+    }
+};
+
+// y = W x for plain rows of k <= 4096 elements (units = k / 64 lanes busy)
+// in rows of whole 16-byte slots; wave w of workgroup b owns rows (8 b + w)
+// rpw + [0, rpw).
+template <int TYPE, int G, int NS>
+__global__ void __launch_bounds__(512) gemv_short_kernel(const uint8_t* __restrict__ w,
+                                                         const float* __restrict__ x, float* __restrict__ y, int n,
+                                                         int units, uint32_t rb, int rpw) {
+    using T = ShortRow<TYPE>;
+    constexpr int P = (T::SLOTS + 63) / 64;  // 16-byte pieces per lane
+    constexpr int REM = T::SLOTS - 64 * (P - 1);
     static_assert(G >= 1 && G <= 8 && NS >= 2, "up to 8 rows per reduction");
-    __shared__ uint4 xq[XQ_Q6_QUADS * UNITS_MAX];
-    __shared__ u32x4 rowbuf[8][Q6_ROW_SLOTS];
+    static_assert(REM >= 16, "the last piece's lanes past REM repeat lanes 0-15");
+    __shared__ uint4 xq[T::XQUADS * UNITS_MAX];
+    __shared__ u32x4 rowbuf[8][T::SLOTS];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int row0 = (static_cast<int>(blockIdx.x) * 8 + wave) * rpw;
@@ -471,71 +569,55 @@ __global__ void __launch_bounds__(512) gemv_q6k_kernel(const uint8_t* __restrict
         make_rsrc(w + static_cast<int64_t>(nrow > 0 ? row0 : 0) * rb, static_cast<uint32_t>(nrow) * rb);
     const bool valid = lane < units;
     const int u = valid ? lane : (lane & 3);  // idle lanes read unit (lane % 4), discarded
+    // piece p of lane L: slot 64 p + L (the last piece: L < REM, else L % 16,
+    // the same slot and bytes as lane L % 16); a slot past a shorter row loads
+    // an in-row slot (its lines are being read anyway) into a buffer slot that
+    // no unit reads
     const int slots = static_cast<int>(rb >> 4);
-    const int pd = 192 + (lane < 18 ? lane : (lane & 15));
-    auto vo = [&](int slot) { return 16u * static_cast<uint32_t>(slot < slots ? slot : lane & 7); };
-    const uint32_t v0 = vo(lane), v1 = vo(64 + lane), v2 = vo(128 + lane), v3 = vo(pd);
-    u32x4* rbuf = rowbuf[wave];
-    const uint8_t* rbytes = reinterpret_cast<const uint8_t*>(rbuf);
-    // the unit's bytes in the row buffer: super-block B = 210 (u / 4), 2 bytes
-    // past a dword when u / 4 is odd
-    const int sbo = 210 * (u >> 2), c = u & 3, hh = c >> 1, l0 = 16 * (c & 1);
-    const uint32_t sh = static_cast<uint32_t>(sbo & 2);
-    const uint8_t* pla = rbytes + (sbo + 64 * hh + l0 - static_cast<int>(sh));
-    const uint8_t* plb = pla + 32;
-    const uint8_t* pqh = rbytes + (sbo + 128 + 32 * hh + l0 - static_cast<int>(sh));
-    const int8_t* psc = reinterpret_cast<const int8_t*>(rbytes + sbo + 192 + 8 * hh + (c & 1));
-    const uint16_t* pdd = reinterpret_cast<const uint16_t*>(rbytes + sbo + 208);
-
-    // the row offset goes into the per-lane offset, which the range check covers
-    auto issue = [&](Q6Raw& b, int s) {
-        const uint32_t so = static_cast<uint32_t>(s) * rb;
-        b.a = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(v0 + so), 0, CACHE_NT);
-        b.b = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(v1 + so), 0, CACHE_NT);
-        b.c = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(v2 + so), 0, CACHE_NT);
-        b.e = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(v3 + so), 0, CACHE_NT);
-    };
-    auto realign = [&](const uint8_t* p) {
-        const uint4 a = ld_b128_a4(p);
-        const uint32_t e = ld_b32(p + 16);
-        return make_uint4(__builtin_amdgcn_alignbyte(a.y, a.x, sh), __builtin_amdgcn_alignbyte(a.z, a.y, sh),
-                          __builtin_amdgcn_alignbyte(a.w, a.z, sh), __builtin_amdgcn_alignbyte(e, a.w, sh));
-    };
-    auto stage = [&](const Q6Raw& b) -> Q6Row {
-        rbuf[lane] = b.a;
-        rbuf[64 + lane] = b.b;
-        rbuf[128 + lane] = b.c;
-        rbuf[pd] = b.e;
-        Q6Row r;
-        r.la = realign(pla);
-        r.lb = realign(plb);
-        r.qh = realign(pqh);
+    uint32_t vo[P];
+    int so_lds[P];
 #pragma unroll
-        for (int t = 0; t < 4; t++) r.sc[t] = psc[2 * t];
-        r.d = *pdd;
-        return r;
+    for (int p = 0; p < P; p++) {
+        const int slot = 64 * p + (p < P - 1 || lane < REM ? lane : (lane & 15));
+        so_lds[p] = slot;
+        vo[p] = 16u * static_cast<uint32_t>(slot < slots ? slot : lane & 7);
+    }
+    u32x4* rbuf = rowbuf[wave];
+    const typename T::Addr ad = T::addr(reinterpret_cast<const uint8_t*>(rbuf), u);
+
+    struct Raw { u32x4 p[P]; };
+    // the row offset goes into the per-lane offset, which the range check covers
+    auto issue = [&](Raw& b, int s) {
+        const uint32_t so = static_cast<uint32_t>(s) * rb;
+#pragma unroll
+        for (int p = 0; p < P; p++)
+            b.p[p] = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(vo[p] + so), 0, CACHE_NT);
+    };
+    auto stage = [&](const Raw& b) {
+#pragma unroll
+        for (int p = 0; p < P; p++) rbuf[so_lds[p]] = b.p[p];
+        return T::read(ad);
     };
 
     // x first, then the first rows, then the encode (as the Q4_K kernel)
     float xv[8];
     const int task = static_cast<int>(threadIdx.x);
     {
-        const int tu0 = task >> 3, p = task & 7;
-        const int tu = tu0 < units ? tu0 : units - 1;
-        const int off = 256 * (tu >> 2) + 128 * ((tu >> 1) & 1) + 16 * (tu & 1) + 32 * (p >> 1) + 8 * (p & 1);
+        const int tu0 = task >> 3;
+        const int off = T::x_off(tu0 < units ? tu0 : units - 1, task & 7);
         const float4 a = *reinterpret_cast<const float4*>(x + off);
         const float4 b = *reinterpret_cast<const float4*>(x + off + 4);
         xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
         xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
     }
     __builtin_amdgcn_sched_barrier(0);
-    Q6Raw ring[NS];
+    Raw ring[NS];
 #pragma unroll
     for (int s = 0; s < NS - 1; s++) issue(ring[s], s);
     __builtin_amdgcn_sched_barrier(0);
-    encode_task_q6(xv, task, units, xq, true);
+    T::encode(xv, task, units, xq);
     __syncthreads();
-    const XU6 xu = read_unit_q6(xq, u);
+    const typename T::X xu = T::read_x(xq, u);
 
     // G % NS == 0 whenever the wave has more than one group (host), so the
     // ring slot of row g0 + i is i % NS in every group
@@ -546,7 +628,7 @@ __global__ void __launch_bounds__(512) gemv_q6k_kernel(const uint8_t* __restrict
 #pragma unroll
         for (int i = 0; i < G; i++) {
             issue(ring[(i + NS - 1) % NS], g0 + i + NS - 1);
-            const float part = row_part_q6(stage(ring[i % NS]), xu);
+            const float part = T::part(stage(ring[i % NS]), xu);
             acc[i] = valid ? part : 0.f;
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -957,27 +1039,36 @@ void launch_rpw(int rpw, const void* w, const float* x, float* y, int n, int uni
     }
 }
 
-template <int G, int NS>
-void launch_q6(const void* w, const float* x, float* y, int n, int units, uint32_t rb, int rpw, hipStream_t st) {
+template <int TYPE, int G, int NS>
+void launch_short(const void* w, const float* x, float* y, int n, int units, uint32_t rb, int rpw,
+                  hipStream_t st) {
     const int grid = (n + 8 * rpw - 1) / (8 * rpw);
-    gemv_q6k_kernel<G, NS><<<dim3(static_cast<uint32_t>(grid)), dim3(512), 0, st>>>(
+    gemv_short_kernel<TYPE, G, NS><<<dim3(static_cast<uint32_t>(grid)), dim3(512), 0, st>>>(
         static_cast<const uint8_t*>(w), x, y, n, units, rb, rpw);
 }
 
 // rpw <= 8: one group of rpw rows; above, groups of 8 rows (NS divides 8)
-template <int NS>
-void launch_q6_rpw(int rpw, const void* w, const float* x, float* y, int n, int units, uint32_t rb,
-                   hipStream_t st) {
+template <int TYPE, int NS>
+void launch_short_rpw(int rpw, const void* w, const float* x, float* y, int n, int units, uint32_t rb,
+                      hipStream_t st) {
     switch (rpw) {
-    case 1: launch_q6<1, NS>(w, x, y, n, units, rb, rpw, st); break;
-    case 2: launch_q6<2, NS>(w, x, y, n, units, rb, rpw, st); break;
-    case 3: launch_q6<3, NS>(w, x, y, n, units, rb, rpw, st); break;
-    case 4: launch_q6<4, NS>(w, x, y, n, units, rb, rpw, st); break;
-    case 5: launch_q6<5, NS>(w, x, y, n, units, rb, rpw, st); break;
-    case 6: launch_q6<6, NS>(w, x, y, n, units, rb, rpw, st); break;
-    case 7: launch_q6<7, NS>(w, x, y, n, units, rb, rpw, st); break;
-    default: launch_q6<8, NS>(w, x, y, n, units, rb, rpw, st); break;
+    case 1: launch_short<TYPE, 1, NS>(w, x, y, n, units, rb, rpw, st); break;
+    case 2: launch_short<TYPE, 2, NS>(w, x, y, n, units, rb, rpw, st); break;
+    case 3: launch_short<TYPE, 3, NS>(w, x, y, n, units, rb, rpw, st); break;
+    case 4: launch_short<TYPE, 4, NS>(w, x, y, n, units, rb, rpw, st); break;
+    case 5: launch_short<TYPE, 5, NS>(w, x, y, n, units, rb, rpw, st); break;
+    case 6: launch_short<TYPE, 6, NS>(w, x, y, n, units, rb, rpw, st); break;
+    case 7: launch_short<TYPE, 7, NS>(w, x, y, n, units, rb, rpw, st); break;
+    default: launch_short<TYPE, 8, NS>(w, x, y, n, units, rb, rpw, st); break;
     }
+}
+
+template <int TYPE>
+void launch_short_ns(int ns, int rpw, const void* w, const float* x, float* y, int n, int units, uint32_t rb,
+                     hipStream_t st) {
+    if (ns == 2) launch_short_rpw<TYPE, 2>(rpw, w, x, y, n, units, rb, st);
+    else if (ns == 3) launch_short_rpw<TYPE, 3>(rpw, w, x, y, n, units, rb, st);
+    else launch_short_rpw<TYPE, 4>(rpw, w, x, y, n, units, rb, st);
 }
 
 // Launch shape for n rows: 8-wave workgroups, one per CU, with RPW =
@@ -1041,11 +1132,14 @@ int gemv_q4k_short(const void* w, const float* x, float* y, int64_t n, int64_t k
     return check_launch("vb_gemv");
 }
 
-// Q6_K short-row kernel: rows per wave for n rows of k = 2048 or 4096
-// elements (one 8-wave workgroup per CU; VB_GEMV_CFG="8,rpw" overrides),
-// 0 for other k.
-int gemv_q6k_rpw(int64_t n, int64_t k) {
-    if ((k != 2048 && k != 4096) || n < 1 || n > INT32_MAX) return 0;
+// Short-row Q6_K / Q8_0 kernel: rows per wave for n rows of k elements (one
+// 8-wave workgroup per CU; VB_GEMV_CFG="8,rpw" overrides), 0 for shapes it
+// does not take: rows must be whole 16-byte slots (Q6_K: k = 2048 or 4096;
+// Q8_0: k % 256 == 0, k <= 4096).
+int gemv_short_rpw(int32_t type, int64_t n, int64_t k) {
+    const bool ok = type == TYPE_Q6_K ? (k == 2048 || k == 4096)
+                  : type == TYPE_Q8_0 ? (k % 256 == 0 && k >= 256 && k <= 4096) : false;
+    if (!ok || n < 1 || n > INT32_MAX) return 0;
     const Knobs& kb = knobs();
     if (kb.gemv_cfg_wpg == 8 && kb.gemv_cfg_rpg >= 1 && kb.gemv_cfg_rpg <= 4096) return kb.gemv_cfg_rpg;
     const int64_t groups = static_cast<int64_t>(num_cus()) * 8;
@@ -1053,26 +1147,25 @@ int gemv_q6k_rpw(int64_t n, int64_t k) {
     return rpw <= 4096 ? static_cast<int>(rpw) : 0;
 }
 
-// Plain Q6_K GEMV, k = 2048 or 4096, 16-byte aligned rows; arguments
-// validated by gemv_dispatch_fused.
-int gemv_q6k_short(const void* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t st) {
-    const int rpw = gemv_q6k_rpw(n, k);
+// Plain Q6_K / Q8_0 GEMV on the short-row kernel, 16-byte aligned rows;
+// arguments validated by gemv_dispatch_fused.
+int gemv_short(int32_t type, const void* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t st) {
+    const int rpw = gemv_short_rpw(type, n, k);
     if (rpw == 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0) {
-        set_error("vb_gemv: internal: Q6_K short-row kernel shape (n=%lld, k=%lld)", static_cast<long long>(n),
-                  static_cast<long long>(k));
+        set_error("vb_gemv: internal: short-row kernel shape (type %d, n=%lld, k=%lld)", type,
+                  static_cast<long long>(n), static_cast<long long>(k));
         return E_INVAL;
     }
-    const uint32_t rb = static_cast<uint32_t>(row_bytes(TYPE_Q6_K, k));
+    const uint32_t rb = static_cast<uint32_t>(row_bytes(type, k));
     const int ni = static_cast<int>(n), units = static_cast<int>(k / 64);
-    // NS - 1 rows in flight while computing (VB_GEMV_RING; default 1: on
-    // MI355X 65.5 us at 128256 x 4096 against 66.9 us with 2 or 3, 9.4
-    // against 9.8 / 10.1 us at 14336 x 4096); past 8 rows per wave the ring
-    // must divide the 8-row groups
+    // NS - 1 rows in flight while computing (VB_GEMV_RING).  Q6_K default 1:
+    // on MI355X 65.5 us at 128256 x 4096 against 66.9 us with 2 or 3, 9.4
+    // against 9.8 / 10.1 us at 14336 x 4096.  Past 8 rows per wave the ring
+    // must divide the 8-row groups.
     int ns = knobs().gemv_ring > 0 ? knobs().gemv_ring + 1 : 2;
     if (rpw > 8 && ns != 2) ns = 4;
-    if (ns == 2) launch_q6_rpw<2>(rpw, w, x, y, ni, units, rb, st);
-    else if (ns == 3) launch_q6_rpw<3>(rpw, w, x, y, ni, units, rb, st);
-    else launch_q6_rpw<4>(rpw, w, x, y, ni, units, rb, st);
+    if (type == TYPE_Q6_K) launch_short_ns<TYPE_Q6_K>(ns, rpw, w, x, y, ni, units, rb, st);
+    else launch_short_ns<TYPE_Q8_0>(ns, rpw, w, x, y, ni, units, rb, st);
     return check_launch("vb_gemv");
 }
 

@@ -44,6 +44,7 @@ Knobs read_knobs() {
         k.gemv_q4k_general = std::strcmp(e, "dot") == 0;
     }
     if (const char* e = std::getenv("VB_GEMV_Q6K_PATH")) k.gemv_q6k_general = std::strcmp(e, "dot") == 0;
+    if (const char* e = std::getenv("VB_GEMV_Q8_PATH")) k.gemv_q8_general = std::strcmp(e, "dot") == 0;
     if (const char* e = std::getenv("VB_GEMV_MFMA_CFG")) {
         int a = 0, b = 0;
         if (std::sscanf(e, "%d,%d", &a, &b) == 2 && a >= 1 && b >= 1) {

@@ -10,7 +10,7 @@ namespace vb {
 //   VB_GEMV_RING=d, VB_GEMV_CFG="wpg,rpg"   GEMV ring depth / workgroup shape
 //   VB_GEMV_Q4K_PATH=mfma|dot                 Q4_K GEMV on the int8-MFMA kernel, or on
 //                                             the general v_dot4 kernel for every shape
-//   VB_GEMV_Q6K_PATH=dot                      Q6_K GEMV on the general kernel for every shape
+//   VB_GEMV_Q6K_PATH=dot, VB_GEMV_Q8_PATH=dot  Q6_K / Q8_0 GEMV on the general kernel for every shape
 //   VB_GEMV_MFMA_CFG="wpg,ks"                 that kernel's workgroup shape
 //   VB_GEMM_NF=6|8                            tiled GEMM columns per workgroup
 //   VB_GEMM_TILE="wm,wn,nf"                   tiled GEMM tile configuration
@@ -24,6 +24,7 @@ struct Knobs {
     bool gemv_q4k_mfma = false;
     bool gemv_q4k_general = false;
     bool gemv_q6k_general = false;
+    bool gemv_q8_general = false;
     int gemv_mfma_wpg = 0, gemv_mfma_ks = 0;
     int gemm_nf = 0;
     int gemm_tile_wm = 0, gemm_tile_wn = 0, gemm_tile_nf = 0;
@@ -88,11 +89,11 @@ int gemv_dispatch_fused(const void* w, const RowSrc& src, const GemvFuse& fz, co
 // gemv_q4k_rpw(n) is its rows per wave, 0 when n is too large for it.
 int gemv_q4k_rpw(int64_t n);
 int gemv_q4k_short(const void* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t st);
-// Plain Q6_K GEMV for k = 2048 or 4096 on the short-row arithmetic
-// (gemv_q4k.hip); gemv_q6k_rpw(n, k) is its rows per wave, 0 for shapes it
-// does not take.
-int gemv_q6k_rpw(int64_t n, int64_t k);
-int gemv_q6k_short(const void* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t st);
+// Plain Q6_K (k = 2048 / 4096) and Q8_0 (k % 256 == 0, k <= 4096) GEMV on
+// the short-row arithmetic (gemv_q4k.hip); gemv_short_rpw is its rows per
+// wave, 0 for types and shapes it does not take.
+int gemv_short_rpw(int32_t type, int64_t n, int64_t k);
+int gemv_short(int32_t type, const void* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t st);
 // Plain or residual-epilogue Q4_K GEMV for 4096 < k <= 16384, rows split over
 // 2, 4 or 8 waves (gemv_q4k.hip); gemv_q4k_split_rpw is 0 for shapes it does not take.
 int gemv_q4k_split_rpw(int64_t n, int64_t k);
