@@ -437,6 +437,60 @@ def test_gemv_short_matches_general_kernel(knob, qtype, rows, env):
     assert O.rel_l2(y_short, want) <= 2e-4 and O.rel_l2(y_gen, want) <= 2e-4
 
 
+# ---- the split-row Q6_K / Q8_0 kernel (4096 < k <= 16384) --------------------
+
+# (rows, k): 2 slices per row (Q6_K k = 4608: slices of 40 and 32 units; Q8_0
+# k = 4352: 36 and 32; k = 7168), 4 (k = 14336), 8 with a short last slice
+# (k = 14848: 7 x 32 + 8 units), rows per wave 1 to 8
+TSPLIT_SHAPES = [(1, 4608), (2049, 4608), (3000, 7168), (4096, 14336), (8192, 14336), (1000, 14848),
+                 (513, 16384)]
+
+
+@pytest.mark.parametrize("qtype", SHORT_TYPES)
+@pytest.mark.parametrize("rows,k", TSPLIT_SHAPES + [(77, 4352), (4096, 11264)])
+def test_gemv_split_rows(qtype, rows, k):
+    """Q6_K rows need k % 512 == 0 for the split kernel (Q6_K k = 4352 takes the
+    general kernel); every case against the oracle."""
+    qt, x = _short_case(qtype, rows, k, rows + k + qtype)
+    y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy()
+    want = O.gemv(qt.to_numpy_bytes(), x, rows, k, qt.qtype)
+    assert O.rel_l2(y, want) <= GEMV_TOL
+    assert np.max(np.abs(y - want)) <= 1e-3 * np.abs(want).max() + 1e-6  # no row or slice dropped
+
+
+@pytest.mark.parametrize("cfg", ["2,1", "4,1", "4,3", "8,2", "8,4"])
+def test_gemv_split_knob(knob, cfg):
+    """VB_GEMV_SPLIT="slices,rows in flight" on the Q6_K / Q8_0 split kernel
+    (4 rows in flight run as 3; 2 slices of 112-unit rows exceed a 56-unit
+    slice: the general kernel takes k = 14336 then)."""
+    knob("VB_GEMV_SPLIT", cfg)
+    for qtype in SHORT_TYPES:
+        for rows, k in ((5000, 7168), (4096, 14336)):
+            qt, x = _short_case(qtype, rows, k, rows + k + 2)
+            y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy()
+            want = O.gemv(qt.to_numpy_bytes(), x, rows, k, qt.qtype)
+            assert O.rel_l2(y, want) <= GEMV_TOL, (cfg, qtype, rows, k)
+            assert np.max(np.abs(y - want)) <= 1e-3 * np.abs(want).max() + 1e-6
+
+
+@pytest.mark.parametrize("qtype,env", [(ggml.GGML_TYPE_Q6_K, "VB_GEMV_Q6K_PATH"),
+                                       (ggml.GGML_TYPE_Q8_0, "VB_GEMV_Q8_PATH")])
+def test_gemv_split_matches_general_kernel(knob, qtype, env):
+    """At the FFN down shape (4096 x 14336) the split-row kernel and the
+    general kernel agree, both close to the oracle; repeated launches are
+    bit-identical (fixed-order slice sums)."""
+    rows, k = 4096, 14336
+    gen = torch.Generator(device="cuda").manual_seed(80)
+    qt = QTensor.quantize(torch.randn((rows, k), generator=gen, device="cuda") * 0.02, qtype)
+    x = torch.randn(k, generator=gen, device="cuda")
+    y_split = gemv(qt, x).cpu().numpy()
+    assert np.array_equal(bits(gemv(qt, x).cpu().numpy()), bits(y_split))
+    knob(env, "dot")
+    y_gen = gemv(qt, x).cpu().numpy()
+    want = O.gemv(qt.to_numpy_bytes(), x.cpu().numpy(), rows, k, qt.qtype)
+    assert O.rel_l2(y_split, want) <= 2e-4 and O.rel_l2(y_gen, want) <= 2e-4
+
+
 # ---- the split-row Q4_K kernel (4096 < k <= 16384, rows over 2/4/8 waves) --
 
 # (rows, k): 2 slices per row up to 112 units (k = 7168), 4 up to 224

@@ -541,6 +541,12 @@ int gemv_dispatch_fused(const void* w, const RowSrc& src, const GemvFuse& fz, co
         const bool general = type == TYPE_Q6_K ? knobs().gemv_q6k_general : knobs().gemv_q8_general;
         if (plain && !general && reinterpret_cast<uintptr_t>(w) % 16 == 0 && gemv_short_rpw(type, n, k) > 0)
             return gemv_short(type, w, x, y, n, k, st);
+        // 4096 < k <= 16384 (a Q4_K_M file's Q6_K FFN down), plain or with
+        // the residual epilogue: the split-row kernel
+        const bool resid_only = !fz.norm_w && fz.act < 0 && !src.dense_pairs && !src.n_dev && !src.gidx &&
+                                src.zn == 0;
+        if (resid_only && !general && k > 4096 && gemv_split_rpw(type, n, k) > 0)
+            return gemv_split(type, w, x, y, fz.resid, n, k, st);
         if (type == TYPE_Q6_K) return launch_gemv_q<TYPE_Q6_K>(w, src, fz, x, y, n, k, rb, st);
         return launch_gemv_q<TYPE_Q8_0>(w, src, fz, x, y, n, k, rb, st);
     }

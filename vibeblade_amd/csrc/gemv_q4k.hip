@@ -48,6 +48,7 @@
 // / permlane16 swaps, then DPP), about 18 instructions for up to 8 rows, and
 // lanes 8g store y.  No LDS reduction and no barrier at the end.
 #include <cstdint>
+#include <type_traits>
 
 #include "vb_common.hpp"
 #include "vb_internal.hpp"
@@ -363,6 +364,7 @@ struct XU6 {
 
 // Task t = 8 consecutive elements (run p / 2, half p % 2) of unit t / 8; the
 // caller loads them.  Units at or past `units` encode as zeros.
+template <int US = UNITS_MAX>
 __device__ __forceinline__ void encode_task_q6(const float* v_in, int task, int units, uint4* xq, bool store) {
     const int u = task >> 3, p = task & 7;
     float v[8];
@@ -390,24 +392,25 @@ __device__ __forceinline__ void encode_task_q6(const float* v_in, int task, int 
     isum += dpp_mov_i<0xB1>(isum);  // the run's two tasks (lanes 2t, 2t + 1)
     if (!store) return;
     uint4* b = xq + u;
-    reinterpret_cast<uint2*>(&b[(p >> 1) * UNITS_MAX])[p & 1] = make_uint2(ph[0], ph[1]);
-    reinterpret_cast<uint2*>(&b[(4 + (p >> 1)) * UNITS_MAX])[p & 1] = make_uint2(pl[0], pl[1]);
-    if ((p & 1) == 0) reinterpret_cast<uint32_t*>(&b[8 * UNITS_MAX])[p >> 1] = static_cast<uint32_t>(32 * isum);
-    if (p == 0) reinterpret_cast<uint32_t*>(&b[9 * UNITS_MAX])[0] = __float_as_uint(amax / static_cast<float>(X15_MAX));
+    reinterpret_cast<uint2*>(&b[(p >> 1) * US])[p & 1] = make_uint2(ph[0], ph[1]);
+    reinterpret_cast<uint2*>(&b[(4 + (p >> 1)) * US])[p & 1] = make_uint2(pl[0], pl[1]);
+    if ((p & 1) == 0) reinterpret_cast<uint32_t*>(&b[8 * US])[p >> 1] = static_cast<uint32_t>(32 * isum);
+    if (p == 0) reinterpret_cast<uint32_t*>(&b[9 * US])[0] = __float_as_uint(amax / static_cast<float>(X15_MAX));
 }
 
+template <int US = UNITS_MAX>
 __device__ __forceinline__ XU6 read_unit_q6(const uint4* xq, int u) {
     XU6 x;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const uint4 h = xq[i * UNITS_MAX + u], l = xq[(4 + i) * UNITS_MAX + u];
+        const uint4 h = xq[i * US + u], l = xq[(4 + i) * US + u];
         x.h[4 * i] = h.x; x.h[4 * i + 1] = h.y; x.h[4 * i + 2] = h.z; x.h[4 * i + 3] = h.w;
         x.l[4 * i] = l.x; x.l[4 * i + 1] = l.y; x.l[4 * i + 2] = l.z; x.l[4 * i + 3] = l.w;
     }
-    const uint4 c = xq[8 * UNITS_MAX + u];
+    const uint4 c = xq[8 * US + u];
     x.c[0] = static_cast<int>(c.x); x.c[1] = static_cast<int>(c.y);
     x.c[2] = static_cast<int>(c.z); x.c[3] = static_cast<int>(c.w);
-    x.s = __uint_as_float(reinterpret_cast<const uint32_t*>(&xq[9 * UNITS_MAX + u])[0]);
+    x.s = __uint_as_float(reinterpret_cast<const uint32_t*>(&xq[9 * US + u])[0]);
     return x;
 }
 
@@ -437,13 +440,16 @@ template <> struct ShortRow<TYPE_Q6_K> {
     using X = XU6;
     struct Row { uint4 la, lb, qh; int sc[4]; uint32_t d; };
     struct Addr { const uint8_t *la, *qh; const int8_t* sc; const uint16_t* d; uint32_t sh; };
+    static constexpr int bytes(int units) { return 210 * (units / 4); }
     static __device__ int x_off(int u, int p) {
         return 256 * (u >> 2) + 128 * ((u >> 1) & 1) + 16 * (u & 1) + 32 * (p >> 1) + 8 * (p & 1);
     }
+    template <int US = UNITS_MAX>
     static __device__ void encode(const float* v, int task, int units, uint4* xq) {
-        encode_task_q6(v, task, units, xq, true);
+        encode_task_q6<US>(v, task, units, xq, true);
     }
-    static __device__ X read_x(const uint4* xq, int u) { return read_unit_q6(xq, u); }
+    template <int US = UNITS_MAX>
+    static __device__ X read_x(const uint4* xq, int u) { return read_unit_q6<US>(xq, u); }
     // super-block B = 210 (u / 4) of the row buffer, 2 bytes past a dword
     // when u / 4 is odd
     static __device__ Addr addr(const uint8_t* rb, int u) {
@@ -510,11 +516,14 @@ template <> struct ShortRow<TYPE_Q8_0> {
     using X = XU;
     struct Row { uint32_t w[17]; };
     struct Addr { const uint8_t* p; };
+    static constexpr int bytes(int units) { return 68 * units; }
     static __device__ int x_off(int u, int p) { return 64 * u + 8 * p; }
+    template <int US = UNITS_MAX>
     static __device__ void encode(const float* v, int task, int units, uint4* xq) {
-        encode_task(v, task, units, xq, true);
+        encode_task<US>(v, task, units, xq, true);
     }
-    static __device__ X read_x(const uint4* xq, int u) { return read_unit(xq, u); }
+    template <int US = UNITS_MAX>
+    static __device__ X read_x(const uint4* xq, int u) { return read_unit<US>(xq, u); }
     static __device__ Addr addr(const uint8_t* rb, int u) { return Addr{rb + 68 * u}; }
     static __device__ Row read(const Addr& a) {
         Row r;
@@ -982,6 +991,148 @@ __global__ void __launch_bounds__(1024) gemv_q4k_split_kernel(const uint8_t* __r
     }
 }
 
+// Split rows for Q6_K / Q8_0 (4096 < k <= 16384): the Q4_K split-row kernel's
+// work split with the short-row Q6_K / Q8_0 units (ShortRow).  A slice of
+// upw units starts on a 4-byte boundary (Q6_K: an even super-block), is read
+// as P contiguous 16-byte pieces per lane from there (its last piece may run
+// a few bytes past the slice: unread) and staged in the wave's row buffer.
+template <int TYPE, int RPW, int NS, int SL>
+__global__ void __launch_bounds__(1024) gemv_split_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                                          float* y, const float* resid, int n, int units, int upw,
+                                                          uint32_t rb) {
+    using T = ShortRow<TYPE>;
+    constexpr int WPG = 16;
+    constexpr int NG = WPG / SL;                      // row groups per workgroup
+    constexpr int P = (T::bytes(56) + 15 + 1023) / 1024;  // pieces per lane of a slice of at most 56 units
+    __shared__ uint4 xq[T::XQUADS * SPLIT_US];
+    __shared__ u32x4 rowbuf[WPG][64 * P];
+    __shared__ float red[NG][SL][8];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int grp = wave / SL, slc = wave - grp * SL;
+    const int row0 = (static_cast<int>(blockIdx.x) * NG + grp) * RPW;
+    const int rlast = n - 1;
+    const int rbase = row0 < rlast ? row0 : rlast;
+    // this wave's slice: units [u0, u0 + su) of each row
+    const int u0 = slc * upw;
+    const int su = units - u0 < upw ? units - u0 : upw;  // >= 4 by the host's choice of SL
+    const uint32_t sb0 = static_cast<uint32_t>(T::bytes(u0));
+    const uint8_t* wb = w + static_cast<int64_t>(rbase) * rb + sb0;
+    const int64_t span64 = static_cast<int64_t>(n - rbase) * rb - sb0;
+    const uint32_t span = span64 < 0xFFFFFFFFll ? static_cast<uint32_t>(span64) : 0xFFFFFFFFu;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(wb, span);
+    const bool valid = lane < su;
+    const int u = valid ? lane : (lane & 3);  // idle lanes read unit (lane % 4) of the slice, discarded
+    const int sslots = (T::bytes(su) + 15) / 16;  // 16-byte slots of the slice
+    uint32_t vo[P];
+#pragma unroll
+    for (int p = 0; p < P; p++) vo[p] = 16u * static_cast<uint32_t>(64 * p + lane < sslots ? 64 * p + lane : lane & 7);
+    u32x4* rbuf = rowbuf[wave];
+    const typename T::Addr ad = T::addr(reinterpret_cast<const uint8_t*>(rbuf), u);
+
+    auto soff = [&](int s) -> uint32_t {
+        int r = row0 + s;
+        r = r < rlast ? r : rlast;
+        return static_cast<uint32_t>(r - rbase) * rb;
+    };
+    struct Raw { u32x4 p[P]; };
+    auto issue = [&](Raw& b, int s) {
+        const uint32_t so = soff(s);
+#pragma unroll
+        for (int p = 0; p < P; p++)
+            b.p[p] = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(vo[p]), static_cast<int>(so), CACHE_NT);
+    };
+    auto stage = [&](const Raw& b) {
+#pragma unroll
+        for (int p = 0; p < P; p++) rbuf[64 * p + lane] = b.p[p];
+        return T::read(ad);
+    };
+
+    // x first (8 tasks per unit, up to 2048 tasks: 2 per thread), then the
+    // first rows' weights, then the branch-free encode
+    float xv[2][8];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const int task = static_cast<int>(threadIdx.x) + 1024 * t;
+        const int tu = task >> 3;
+        const int off = T::x_off(tu < units ? tu : units - 1, task & 7);
+        const float4 a = *reinterpret_cast<const float4*>(x + off);
+        const float4 b = *reinterpret_cast<const float4*>(x + off + 4);
+        xv[t][0] = a.x; xv[t][1] = a.y; xv[t][2] = a.z; xv[t][3] = a.w;
+        xv[t][4] = b.x; xv[t][5] = b.y; xv[t][6] = b.z; xv[t][7] = b.w;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    Raw ring[NS];
+#pragma unroll
+    for (int s = 0; s < NS - 1 && s < RPW; s++) issue(ring[s], s);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+        T::template encode<SPLIT_US>(xv[t], static_cast<int>(threadIdx.x) + 1024 * t, units, xq);
+    __syncthreads();
+    const typename T::X xu = T::template read_x<SPLIT_US>(xq, u0 + u);
+
+    float acc[8];
+#pragma unroll
+    for (int s = 0; s < 8; s++) acc[s] = 0.f;
+#pragma unroll
+    for (int s = 0; s < RPW; s++) {
+        if (s + NS - 1 < RPW) issue(ring[(s + NS - 1) % NS], s + NS - 1);
+        const float part = T::part(stage(ring[s % NS]), xu);
+        acc[s] = valid ? part : 0.f;
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    const float tot = reduce8(acc);
+    const int rr = row_of_group(lane >> 3);
+    if ((lane & 7) == 0 && rr < RPW) red[grp][slc][rr] = tot;
+    __syncthreads();
+    if (threadIdx.x < NG * RPW) {
+        const int gq = static_cast<int>(threadIdx.x) / RPW, r = static_cast<int>(threadIdx.x) - gq * RPW;
+        const int row = (static_cast<int>(blockIdx.x) * NG + gq) * RPW + r;
+        if (row < n) {
+            float v = 0.f;
+#pragma unroll
+            for (int j = 0; j < SL; j++) v += red[gq][j][r];
+            y[row] = resid ? v + resid[row] : v;  // resid may be y: read before the write
+        }
+    }
+}
+
+template <int TYPE, int RPW, int D, int SL>
+void launch_tsplit(const void* w, const float* x, float* y, const float* resid, int n, int units, int upw,
+                   uint32_t rb, hipStream_t st) {
+    constexpr int NG = 16 / SL;
+    constexpr int NS = (RPW < D ? RPW : D) + 1;
+    const int grid = (n + NG * RPW - 1) / (NG * RPW);
+    gemv_split_kernel<TYPE, RPW, NS, SL><<<dim3(static_cast<uint32_t>(grid)), dim3(1024), 0, st>>>(
+        static_cast<const uint8_t*>(w), x, y, resid, n, units, upw, rb);
+}
+
+template <int TYPE, int D, int SL>
+void launch_tsplit_rpw(int rpw, const void* w, const float* x, float* y, const float* resid, int n, int units,
+                       int upw, uint32_t rb, hipStream_t st) {
+    switch (rpw) {
+    case 1: launch_tsplit<TYPE, 1, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 2: launch_tsplit<TYPE, 2, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 3: launch_tsplit<TYPE, 3, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 4: launch_tsplit<TYPE, 4, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 5: launch_tsplit<TYPE, 5, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 6: launch_tsplit<TYPE, 6, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 7: launch_tsplit<TYPE, 7, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    default: launch_tsplit<TYPE, 8, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    }
+}
+
+template <int TYPE, int SL>
+void launch_tsplit_d(int d, int rpw, const void* w, const float* x, float* y, const float* resid, int n, int units,
+                     int upw, uint32_t rb, hipStream_t st) {
+    switch (d) {
+    case 1: launch_tsplit_rpw<TYPE, 1, SL>(rpw, w, x, y, resid, n, units, upw, rb, st); break;
+    case 3: launch_tsplit_rpw<TYPE, 3, SL>(rpw, w, x, y, resid, n, units, upw, rb, st); break;
+    default: launch_tsplit_rpw<TYPE, 2, SL>(rpw, w, x, y, resid, n, units, upw, rb, st); break;
+    }
+}
+
 template <int RPW, int D, int SL>
 void launch_split(const void* w, const float* x, float* y, const float* resid, int n, int units, int upw,
                   uint32_t rb, hipStream_t st) {
@@ -1212,6 +1363,58 @@ int gemv_q4k_split(const void* w, const float* x, float* y, const float* resid, 
         launch_split_d<4>(d, sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
     else
         launch_split_d<8>(d, sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
+    return check_launch("vb_gemv");
+}
+
+// Split-row shape for Q6_K / Q8_0: split_shape's, with Q6_K slices a multiple
+// of 8 units (4-byte-aligned slice starts).
+SplitShape split_shape_t(int32_t type, int64_t n, int units) {
+    SplitShape s = split_shape(n, units);
+    if (type == TYPE_Q6_K) {
+        s.upw = ((units + s.sl - 1) / s.sl + 7) & ~7;
+        if (s.upw > 56 || units - (s.sl - 1) * s.upw < 4) s.rpw = 0;
+    }
+    return s;
+}
+
+int gemv_split_rpw(int32_t type, int64_t n, int64_t k) {
+    // Q6_K rows of a whole number of dwords (k % 512 == 0: an even super-block count)
+    if (!((type == TYPE_Q6_K && k % 512 == 0) || (type == TYPE_Q8_0 && k % 256 == 0))) return 0;
+    const int units = static_cast<int>(k / 64);
+    return units > UNITS_MAX && units <= SPLIT_US && n <= INT32_MAX ? split_shape_t(type, n, units).rpw : 0;
+}
+
+// Plain or residual-epilogue Q6_K / Q8_0 GEMV, 4096 < k <= 16384, on the
+// split-row kernel; arguments validated by gemv_dispatch_fused.
+int gemv_split(int32_t type, const void* w, const float* x, float* y, const float* resid, int64_t n, int64_t k,
+               hipStream_t st) {
+    const int units = static_cast<int>(k / 64);
+    const SplitShape sh = split_shape_t(type, n, units);
+    if (gemv_split_rpw(type, n, k) == 0 || sh.rpw == 0) {
+        set_error("vb_gemv: internal: split-row kernel shape (type %d, n=%lld, k=%lld)", type,
+                  static_cast<long long>(n), static_cast<long long>(k));
+        return E_INVAL;
+    }
+    const uint32_t rb = static_cast<uint32_t>(row_bytes(type, k));
+    const int ni = static_cast<int>(n);
+    // rows in flight (VB_GEMV_SPLIT): Q6_K 1, Q8_0 2 by default (on MI355X at
+    // 4096 x 14336: Q6_K 10.7 us against 10.8 at 2 and 12.2 at 3; Q8_0 11.4
+    // against 11.8 at 1); at most 3, 4 would spill registers at 8 rows per wave
+    int d = knobs().gemv_split_d > 3 ? 3 : knobs().gemv_split_d;
+    if (d == 0) d = type == TYPE_Q6_K ? 1 : 2;
+    auto go = [&](auto type_c) {
+        constexpr int TY = decltype(type_c)::value;
+        if (sh.sl == 2)
+            launch_tsplit_d<TY, 2>(d, sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
+        else if (sh.sl == 4)
+            launch_tsplit_d<TY, 4>(d, sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
+        else
+            launch_tsplit_d<TY, 8>(d, sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
+    };
+    if (type == TYPE_Q6_K)
+        go(std::integral_constant<int, TYPE_Q6_K>{});
+    else
+        go(std::integral_constant<int, TYPE_Q8_0>{});
     return check_launch("vb_gemv");
 }
 
