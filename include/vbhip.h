@@ -68,8 +68,10 @@ int vb_version(void);
 int64_t vb_row_bytes(int32_t ggml_type, int64_t k);
 /* Select the device and check that it is a gfx950; also reads the launch
  * tuning overrides (VB_GEMV_RING, VB_GEMV_CFG, VB_GEMV_Q4K_PATH,
- * VB_GEMV_MFMA_CFG, VB_GEMM_NF, VB_SPARSE_FUSED, VB_SPARSE_NPW) from the
- * environment, once per process, and the device's compute-unit count. */
+ * VB_GEMV_Q6K_PATH, VB_GEMV_Q8_PATH, VB_GEMV_SPLIT, VB_GEMV_MFMA_CFG,
+ * VB_GEMM_NF, VB_GEMM_TILE, VB_GEMM_SPLIT_MIN_M, VB_SPARSE_FUSED,
+ * VB_SPARSE_NPW) from the environment, once per process, and the device's
+ * compute-unit count. */
 int vb_init(int device);
 /* Re-read the tuning overrides from the environment (for tuning sweeps and
  * tests).  Not synchronised with op calls running on other threads: their
@@ -112,7 +114,13 @@ int vb_quantize_rows(const float* src, void* w, int64_t n_rows, int64_t k,
  * cpp/src/dequant.cpp:739-792) and cuda::gemv_dequant
  * (cpp/include/cuda_kernels.h:191-199).  Note the reference C++ names the
  * output dimension N and walks W as K rows of N; this entry takes the GGUF
- * orientation (rows = outputs), as real .gguf tensors are stored. */
+ * orientation (rows = outputs), as real .gguf tensors are stored.
+ * Kernels: Q4_K, Q6_K and Q8_0 rows of whole 16-byte slots with k <= 4096
+ * run the short-row kernel (one 64-element unit per lane, whole rows per
+ * wave), 4096 < k <= 16384 the split-row kernel (rows in slices over 2-8
+ * waves); other shapes and types the general kernel.  Activations are
+ * encoded as 15- or 16-bit fixed point per unit or run (rel-L2 near 5e-5
+ * against the fp64 product). */
 int vb_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k,
             int32_t ggml_type, void* stream);
 
