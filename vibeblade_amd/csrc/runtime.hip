@@ -77,7 +77,7 @@ Knobs read_knobs() {
         if (v >= 0) k.gemm_split_min_m = v;
     }
     if (const char* e = std::getenv("VB_SPARSE_FUSED")) k.sparse_fused = e[0] != '0';
-    if (const char* e = std::getenv("VB_SPARSE_NPW")) k.sparse_npw = e[0] == '2' ? 2 : 0;
+    if (const char* e = std::getenv("VB_SPARSE_NPW")) k.sparse_npw = e[0] == '2' ? 2 : (e[0] == '1' ? 1 : 0);
     return k;
 }
 

@@ -161,8 +161,10 @@ __global__ void __launch_bounds__(DOWN_THREADS) down_rows_q4k_kernel(
 // the workgroups' partials in a fixed order (deterministic).  The partials
 // go through LDS in 16-byte accesses: 32 LDS instructions per thread where
 // 4-byte accesses take 128.
-constexpr int FUSED_NPW = 1;  // neurons per wave (VB_SPARSE_NPW=2 selects 2; 1 measured faster: more
-                              // workgroups, less serial work per wave, at twice the partial sums)
+// Neurons per wave of this row-split kernel: 1 (VB_SPARSE_NPW=1) or 2
+// (VB_SPARSE_NPW=2; 1 measured faster: more workgroups, less serial work per
+// wave, at twice the partial sums).  The default is the column-split kernel
+// below.
 constexpr int FUSED_STRIDE = 4096;        // floats per partial y (h <= 4096)
 // LDS row of one lane's 64 partials (floats): 16-byte writes of 16 lanes at
 // a pitch of 68 floats (4 mod 64 dwords) fall on distinct banks
@@ -327,6 +329,155 @@ __global__ void __launch_bounds__(512) sparse_fused_q4k_kernel(
             sum.w += v.w;
         }
         *reinterpret_cast<float4*>(out + 64 * l + e0) = sum;
+    }
+}
+
+// Column-split variant (the default): each wave still computes one neuron's
+// gate and up dot products, but the down rows are split by output columns.
+// Once the 8 h values meet in LDS, wave w adds h_r * D[S_r, 512 w .. 512 w +
+// 511] for the workgroup's 8 neurons r and writes its 512 columns of the
+// partial straight from registers: no LDS sum of 8 partial vectors.  Wave
+// w's slice of a down row is 2 super-blocks (288 B); the 8 slices are read as
+// contiguous 16-byte pieces (requested at kernel start with the gate and up
+// rows) and staged in the wave's LDS area.  Lane L takes unit 8 w + L / 8,
+// qs bytes 4 (L % 8) .. + 3 of it: elements 4 (L % 8) + j (low nibbles,
+// sub-block 2c) and 32 + 4 (L % 8) + j (high nibbles, 2c + 1).
+constexpr int COLS_SLICE = 288;   // bytes of a wave's down-row slice (8 units)
+constexpr int COLS_PIECES = 8 * COLS_SLICE / 16;  // 144 16-byte pieces per wave (8 rows)
+
+template <bool NORM>
+__global__ void __launch_bounds__(512) sparse_fused_cols_kernel(
+    const uint8_t* __restrict__ wg, const uint8_t* __restrict__ wu, const uint8_t* __restrict__ wd, int64_t rb,
+    int64_t i_dim, const float* __restrict__ x, const int32_t* __restrict__ active, int n_bound,
+    const int32_t* __restrict__ n_dev, int kind, float* __restrict__ partial, int units, int slots,
+    const float* __restrict__ norm_w, float eps) {
+    using namespace gemvc;
+    const int n_active = active_count(n_bound, n_dev);
+    if (static_cast<int>(blockIdx.x) * 8 >= n_active) return;
+    __shared__ uint4 lds[XQ_QUADS * 64 + 16];      // the x encoding (slots <= 64) and a norm scratch
+    __shared__ uint4 dst[8][COLS_PIECES];          // the waves' down-row slices
+    __shared__ float hbuf[8];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const bool valid = lane < units;
+    const int uc = valid ? lane : units - 4 + (lane & 3);
+    const Q4KSel usel = make_unit_sel<TYPE_Q4_K>(uc);
+    const int r0 = static_cast<int>(blockIdx.x) * 8;
+
+    // the workgroup's 8 neurons (clamped indices: never read outside the tensors)
+    auto neuron = [&](int r) {
+        int v = active[r < n_active ? r : 0];
+        v = v < 0 ? 0 : (v >= i_dim ? static_cast<int>(i_dim) - 1 : v);
+        return v;
+    };
+    // the 8 indices in one round trip: lanes 0-7 load, the wave reads them
+    // out (wave-uniform, in scalar registers) before any other load is issued
+    const int nl = neuron(r0 + (lane & 7));
+    int nid[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) nid[k] = __builtin_amdgcn_readlane(nl, k);
+    const int nidx = __builtin_amdgcn_readlane(nl, wave);
+    const bool nval = r0 + wave < n_active;
+    // slice pieces of this lane: p = lane + 64 i < 144, row p / 18, part p % 18
+    // (parts past the row, for h < 4096, read the row's start and are never used)
+    int64_t poff[3];
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+        const int p = lane + 64 * i < COLS_PIECES ? lane + 64 * i : lane;
+        const int row = p / 18, part = p - 18 * row;
+        int v = nid[0];
+#pragma unroll
+        for (int k = 1; k < 8; k++) v = row == k ? nid[k] : v;
+        const int64_t b = static_cast<int64_t>(COLS_SLICE) * wave + 16 * part;
+        poff[i] = static_cast<int64_t>(v) * rb + (b + 16 <= rb ? b : 0);
+    }
+
+    XTasks xt;
+    [[maybe_unused]] XTasks nt;
+    const bool x_in_regs = slots * 8 <= XT_MAX * static_cast<int>(blockDim.x);
+    if (x_in_regs) prefetch_x<TYPE_Q4_K>(x, units, slots, xt);
+    if constexpr (NORM) {
+        if (x_in_regs) prefetch_x<TYPE_Q4_K>(norm_w, units, slots, nt);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    Q4KUnit vg, vu;
+    {
+        const int64_t off = static_cast<int64_t>(nidx) * rb;
+        load_unit(wg + off, uc, vg);
+        load_unit(wu + off, uc, vu);
+    }
+    const uint4 dv0 = *reinterpret_cast<const uint4*>(wd + poff[0]);
+    const uint4 dv1 = *reinterpret_cast<const uint4*>(wd + poff[1]);
+    const uint4 dv2 = *reinterpret_cast<const uint4*>(wd + poff[2]);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (NORM) {
+        float* scratch = reinterpret_cast<float*>(lds + XQ_QUADS * slots);
+        const float ss = wg_sum_fixed(x_in_regs ? sumsq_tasks(units, slots, xt) : sumsq_loop(x, units * 64),
+                                      scratch);
+        const float rinv = rms_inv(ss, units * 64, eps);
+        if (x_in_regs) {
+            scale_tasks(xt, nt, rinv);
+            encode_x_regs<TYPE_Q4_K>(units, slots, xt, lds);
+        } else {
+            encode_x_loop_norm<TYPE_Q4_K>(x, norm_w, rinv, units, slots, lds);
+        }
+    } else {
+        if (x_in_regs)
+            encode_x_regs<TYPE_Q4_K>(units, slots, xt, lds);
+        else
+            encode_x_loop<TYPE_Q4_K>(x, units, slots, lds);
+    }
+    __syncthreads();
+    XSlice xs;
+    read_xslice(lds, slots, valid ? lane : 0, xs);
+
+    // this wave's neuron: h into LDS; the slices into the wave's LDS area
+    {
+        const float g = valid ? unit_dot(vg, xs, usel) : 0.f;
+        const float u = valid ? unit_dot(vu, xs, usel) : 0.f;
+        const float t = pair_sum(g, u);
+        const float gt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 31));
+        const float ut = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 63));
+        if (lane == 0) hbuf[wave] = nval ? act_pair(gt, ut, kind) : 0.f;
+    }
+    dst[wave][lane] = dv0;
+    dst[wave][64 + lane] = dv1;
+    if (128 + lane < COLS_PIECES) dst[wave][128 + lane] = dv2;
+    __syncthreads();
+
+    // the wave's 512 columns: unit 8 w + L / 8 of every neuron's row
+    const int ul = lane >> 3, i8 = lane & 7;
+    const int u = 8 * wave + ul;
+    const Q4KSel csel = make_unit_sel<TYPE_Q4_K>(ul & 3);
+    const uint8_t* sb = reinterpret_cast<const uint8_t*>(dst[wave]) + 144 * (ul >> 2);
+    float yp[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) yp[e] = 0.f;
+    float mb0 = 0.f, mb1 = 0.f;
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        const float h = hbuf[r];
+        const uint8_t* rp = sb + COLS_SLICE * r;
+        const uint4 hd = *reinterpret_cast<const uint4*>(rp);
+        const uint32_t q = *reinterpret_cast<const uint32_t*>(rp + 16 + 32 * (ul & 3) + 4 * i8);
+        const uint32_t A = hd.y, B = hd.z, C = hd.w;
+        const uint32_t SC = (((csel.hi ? C : A) >> csel.sh) & csel.m1) | ((A >> csel.sh2) & csel.m2);
+        const uint32_t M = (((csel.hi ? C : B) >> csel.shm) & csel.m1) | ((B >> csel.sh2) & csel.m2);
+        const float hdd = h * f16lo(hd.x), hm = h * f16hi(hd.x);
+        const float a0 = hdd * static_cast<float>(SC & 0xFFu), a1 = hdd * static_cast<float>((SC >> 8) & 0xFFu);
+        mb0 += hm * static_cast<float>(M & 0xFFu);
+        mb1 += hm * static_cast<float>((M >> 8) & 0xFFu);
+        const uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            yp[j] += a0 * static_cast<float>((lo >> (8 * j)) & 0xFFu);
+            yp[4 + j] += a1 * static_cast<float>((hi >> (8 * j)) & 0xFFu);
+        }
+    }
+    if (u < units) {
+        float* out = partial + static_cast<int64_t>(blockIdx.x) * FUSED_STRIDE + 64 * u + 4 * i8;
+        *reinterpret_cast<float4*>(out) = make_float4(yp[0] - mb0, yp[1] - mb0, yp[2] - mb0, yp[3] - mb0);
+        *reinterpret_cast<float4*>(out + 32) = make_float4(yp[4] - mb1, yp[5] - mb1, yp[6] - mb1, yp[7] - mb1);
     }
 }
 
@@ -867,12 +1018,20 @@ void launch_fused(bool norm, dim3 g, hipStream_t st, const void* wg, const void*
     const uint8_t* a = static_cast<const uint8_t*>(wg);
     const uint8_t* b = static_cast<const uint8_t*>(wu);
     const uint8_t* c = static_cast<const uint8_t*>(wd);
-    if (norm)
+    if constexpr (NPW == 0) {  // the column-split kernel (one neuron per wave)
+        if (norm)
+            sparse_fused_cols_kernel<true><<<g, dim3(512), 0, st>>>(a, b, c, rb, i, x, active, n_active, n_dev,
+                                                                    act_kind, part, units, slots, norm_w, eps);
+        else
+            sparse_fused_cols_kernel<false><<<g, dim3(512), 0, st>>>(a, b, c, rb, i, x, active, n_active, n_dev,
+                                                                     act_kind, part, units, slots, norm_w, eps);
+    } else if (norm) {
         sparse_fused_q4k_kernel<NPW, true><<<g, dim3(512), 0, st>>>(a, b, c, rb, i, x, active, n_active, n_dev,
                                                                      act_kind, part, units, slots, norm_w, eps);
-    else
+    } else {
         sparse_fused_q4k_kernel<NPW, false><<<g, dim3(512), 0, st>>>(a, b, c, rb, i, x, active, n_active, n_dev,
                                                                       act_kind, part, units, slots, norm_w, eps);
+    }
 }
 
 // The sparse FFN with an optional RMSNorm of x (norm_w) and residual (the x
@@ -939,17 +1098,23 @@ int sparse_ffn_impl(const void* wg, const void* wu, const void* wd, int32_t down
         }
         const int units = static_cast<int>(h / 64);
         const int slots = (units + 7) & ~7;  // gemv_core.hpp: encoded units, a multiple of 8
-        const int npw = knobs().sparse_npw == 2 ? 2 : FUSED_NPW;
+        // VB_SPARSE_NPW=1 / 2: the row-split kernel with 1 or 2 neurons per wave;
+        // default the column-split kernel (1 neuron per wave)
+        const int npw_knob = knobs().sparse_npw;
+        const int npw = npw_knob == 2 ? 2 : 1;
         const int nblk = (n_active + 8 * npw - 1) / (8 * npw);
         float* part = reinterpret_cast<float*>(wsb);
         const dim3 g(static_cast<uint32_t>(nblk));
         const int64_t rb = row_bytes(TYPE_Q4_K, h);
-        if (npw == 2)
+        if (npw_knob == 2)
             launch_fused<2>(nw != nullptr, g, st, wg, wu, wd, rb, i, xin, active, n_active, n_dev, act_kind, part,
                             units, slots, nw, eps);
+        else if (npw_knob == 1)
+            launch_fused<1>(nw != nullptr, g, st, wg, wu, wd, rb, i, xin, active, n_active, n_dev, act_kind, part,
+                            units, slots, nw, eps);
         else
-            launch_fused<FUSED_NPW>(nw != nullptr, g, st, wg, wu, wd, rb, i, xin, active, n_active, n_dev, act_kind,
-                                    part, units, slots, nw, eps);
+            launch_fused<0>(nw != nullptr, g, st, wg, wu, wd, rb, i, xin, active, n_active, n_dev, act_kind, part,
+                            units, slots, nw, eps);
         int rcf = check_launch(fn);
         if (rcf != OK) return rcf;
         sparse_reduce_kernel<<<dim3(static_cast<uint32_t>(units)), dim3(1024), 0, st>>>(part, nblk, n_dev, 8 * npw,

@@ -16,7 +16,8 @@ namespace vb {
 //   VB_GEMM_TILE="wm,wn,nf"                   tiled GEMM tile configuration
 //   VB_GEMM_SPLIT_MIN_M=m                     smallest M (up to 768) on the role-split GEMM (0: never)
 //   VB_GEMV_SPLIT="sl,d"                      split-row Q4_K GEMV: slices per row (2, 4, 8), rows in flight (1-4)
-//   VB_SPARSE_FUSED=0, VB_SPARSE_NPW=2        sparse FFN kernel choice
+//   VB_SPARSE_FUSED=0, VB_SPARSE_NPW=1|2      sparse FFN kernel choice (NPW: the row-split fused
+//                                             kernel with 1 or 2 neurons per wave)
 // Zero / false means "no override".
 struct Knobs {
     int gemv_ring = 0;
