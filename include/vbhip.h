@@ -124,7 +124,7 @@ int vb_quantize_rows(const float* src, void* w, int64_t n_rows, int64_t k,
 int vb_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k,
             int32_t ggml_type, void* stream);
 
-/* ---- dequant-fused GEMM on MFMA, M >= 2 ---------------------------------
+/* ---- dequant-fused GEMM on MFMA ----------------------------------------
  * Y[m, n] = sum_k X[m, k] * W[n, k]; X row-major (m x k) in fp32
  * (x_dtype = 0) or fp16 (x_dtype = 1), Y fp32 row-major (m x n).  Products
  * run on v_mfma_f32_16x16x32_f16 with W dequantized to fp16 in registers and
@@ -132,7 +132,10 @@ int vb_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k,
  * 3 = role-split (fp16 X only; chosen for 257 <= m <= 768 with fp16 X),
  * 4 = K-split (every type; chosen for Q6_K / Q8_0, and for Q4_K at
  * 17 <= m <= 32 with fp32 X and n < 12288).  Variant 1 is chosen for Q4_K
- * at m <= 32 otherwise.  Variants 1-3 are Q4_K-only.
+ * at m <= 32 otherwise.  Variants 1-3 are Q4_K-only.  With variant 0 and
+ * m == 1 the GEMV runs instead: vb_gemv's kernels for fp32 X (bit-identical
+ * to vb_gemv), and for fp16 X the short-row Q4_K kernel (k <= 4096,
+ * k % 256 == 0) reading the halves directly; other fp16 cases stay on MFMA.
  * Replaces the reference's batched path, a per-token loop of gemv_dequant
  * (cpp/src/fast_model.cpp:644-669, :905-960) over rows decoded by
  * dequantize_row (cpp/src/dequant.cpp:407-425), and cuda::gemm_f32

@@ -10,7 +10,7 @@ import torch
 import oracle as O
 from vibeblade_amd import ggml
 from vibeblade_amd._lib import VBError
-from vibeblade_amd.tensor import QTensor, gemm, GEMM_SKINNY, GEMM_TILED, GEMM_SPLIT, GEMM_KSPLIT
+from vibeblade_amd.tensor import QTensor, gemm, GEMM_AUTO, GEMM_SKINNY, GEMM_TILED, GEMM_SPLIT, GEMM_KSPLIT
 
 pytestmark = pytest.mark.gpu
 
@@ -52,6 +52,27 @@ def test_skinny(dtype, m, n, k):
     want = ref_gemm(qt, xt.float().cpu().numpy())
     assert y.shape == (m, n)
     assert O.rel_l2(y, want) <= TOL
+
+
+@pytest.mark.parametrize("qtype", [Q4K, Q6K, Q80])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("n,k", [(64, 256), (14336, 4096), (4096, 14336), (1000, 2048)])
+def test_one_row_runs_the_gemv(qtype, dtype, n, k):
+    """M = 1 (variant 0) takes the GEMV path: fp32 X for every type, fp16 X on
+    the Q4_K short-row kernel (k <= 4096); other fp16 shapes stay on the MFMA
+    kernels.  Same results as vb_gemv on the same (rounded) activations."""
+    if qtype == Q6K and k % 256 != 0:
+        pytest.skip("k is not a whole number of super-blocks")
+    qt, x = make(1, n, k, n + k + qtype)
+    xt = torch.from_numpy(x).to("cuda", dtype)
+    y = gemm(qt, xt).cpu().numpy()
+    want = ref_gemm(qt, xt.float().cpu().numpy())
+    assert y.shape == (1, n)
+    assert O.rel_l2(y, want) <= TOL
+    if dtype == torch.float32 or (qtype == Q4K and k <= 4096):
+        from vibeblade_amd.tensor import gemv
+        yv = gemv(qt, xt.float().reshape(-1)).cpu().numpy()
+        assert np.array_equal(y.reshape(-1).view(np.uint32), yv.view(np.uint32))
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
@@ -277,12 +298,13 @@ def test_kq_rejects():
                                    (64, 257, 1280), (100, 70, 512)])
 def test_ksplit_q4k(dtype, m, n, k):
     """Q4_K on the K-split kernel (variant 4) at every M tile: against the
-    oracle, and against the default (skinny / tiled) kernel, which rounds the
-    same weights to the same fp16 values and sums in another order."""
+    oracle, and against the skinny / tiled kernel, which rounds the same
+    weights to the same fp16 values and sums in another order (one row goes
+    to the GEMV by default, so the skinny kernel is named for it)."""
     qt, x = make(m, n, k, m * 13 + n, qtype=Q4K)
     xt = torch.from_numpy(x).to("cuda", dtype)
     y = gemm(qt, xt, variant=GEMM_KSPLIT).cpu().numpy()
     want = ref_gemm(qt, xt.float().cpu().numpy())
     assert O.rel_l2(y, want) <= TOL
-    other = gemm(qt, xt).cpu().numpy()
+    other = gemm(qt, xt, variant=GEMM_SKINNY if m == 1 else GEMM_AUTO).cpu().numpy()
     assert O.rel_l2(y, other) <= 1e-5

@@ -224,8 +224,9 @@ __device__ __forceinline__ int row_of_group(int g) {
     return 4 * (g & 1) + ((0x3120 >> (4 * (g >> 1))) & 0xF);
 }
 
-template <int RPW, int NS, int WPG>
-__global__ void __launch_bounds__(64 * WPG) gemv_q4k_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
+// XH: x in fp16 (a one-row GEMM with fp16 activations), converted as loaded.
+template <int RPW, int NS, int WPG, bool XH = false>
+__global__ void __launch_bounds__(64 * WPG) gemv_q4k_kernel(const uint8_t* __restrict__ w, const void* __restrict__ xp,
                                                             float* __restrict__ y, int n, int units, uint32_t rb) {
     static_assert(WPG == 8 || WPG == 16, "8 or 16 waves: one encode task per thread for the first 512");
     __shared__ uint4 xq[XQ_UNIT_QUADS * UNITS_MAX];
@@ -290,10 +291,18 @@ __global__ void __launch_bounds__(64 * WPG) gemv_q4k_kernel(const uint8_t* __res
     {
         const int tu = task >> 3;
         const int off = (tu < units ? tu : units - 1) * 64 + 8 * (task & 7);
-        const float4 a = *reinterpret_cast<const float4*>(x + off);
-        const float4 b = *reinterpret_cast<const float4*>(x + off + 4);
-        xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
-        xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+        if constexpr (XH) {
+            typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+            const h8 hv = *reinterpret_cast<const h8*>(static_cast<const _Float16*>(xp) + off);
+#pragma unroll
+            for (int i = 0; i < 8; i++) xv[i] = static_cast<float>(hv[i]);
+        } else {
+            const float* x = static_cast<const float*>(xp);
+            const float4 a = *reinterpret_cast<const float4*>(x + off);
+            const float4 b = *reinterpret_cast<const float4*>(x + off + 4);
+            xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
+            xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
     RowRaw ring[NS];
@@ -1169,24 +1178,24 @@ void launch_split_d(int d, int rpw, const void* w, const float* x, float* y, con
     }
 }
 
-template <int RPW, int NS, int WPG>
-void launch(const void* w, const float* x, float* y, int n, int units, uint32_t rb, hipStream_t st) {
+template <int RPW, int NS, int WPG, bool XH = false>
+void launch(const void* w, const void* x, float* y, int n, int units, uint32_t rb, hipStream_t st) {
     const int grid = (n + WPG * RPW - 1) / (WPG * RPW);
-    gemv_q4k_kernel<RPW, NS, WPG><<<dim3(static_cast<uint32_t>(grid)), dim3(64 * WPG), 0, st>>>(
+    gemv_q4k_kernel<RPW, NS, WPG, XH><<<dim3(static_cast<uint32_t>(grid)), dim3(64 * WPG), 0, st>>>(
         static_cast<const uint8_t*>(w), x, y, n, units, rb);
 }
 
-template <int NS, int WPG>
-void launch_rpw(int rpw, const void* w, const float* x, float* y, int n, int units, uint32_t rb, hipStream_t st) {
+template <int NS, int WPG, bool XH = false>
+void launch_rpw(int rpw, const void* w, const void* x, float* y, int n, int units, uint32_t rb, hipStream_t st) {
     switch (rpw) {
-    case 1: launch<1, NS, WPG>(w, x, y, n, units, rb, st); break;
-    case 2: launch<2, NS, WPG>(w, x, y, n, units, rb, st); break;
-    case 3: launch<3, NS, WPG>(w, x, y, n, units, rb, st); break;
-    case 4: launch<4, NS, WPG>(w, x, y, n, units, rb, st); break;
-    case 5: launch<5, NS, WPG>(w, x, y, n, units, rb, st); break;
-    case 6: launch<6, NS, WPG>(w, x, y, n, units, rb, st); break;
-    case 7: launch<7, NS, WPG>(w, x, y, n, units, rb, st); break;
-    default: launch<8, NS, WPG>(w, x, y, n, units, rb, st); break;
+    case 1: launch<1, NS, WPG, XH>(w, x, y, n, units, rb, st); break;
+    case 2: launch<2, NS, WPG, XH>(w, x, y, n, units, rb, st); break;
+    case 3: launch<3, NS, WPG, XH>(w, x, y, n, units, rb, st); break;
+    case 4: launch<4, NS, WPG, XH>(w, x, y, n, units, rb, st); break;
+    case 5: launch<5, NS, WPG, XH>(w, x, y, n, units, rb, st); break;
+    case 6: launch<6, NS, WPG, XH>(w, x, y, n, units, rb, st); break;
+    case 7: launch<7, NS, WPG, XH>(w, x, y, n, units, rb, st); break;
+    default: launch<8, NS, WPG, XH>(w, x, y, n, units, rb, st); break;
     }
 }
 
@@ -1258,7 +1267,7 @@ int gemv_q4k_rpw(int64_t n) { return short_shape(n).rpw; }
 
 // Plain Q4_K GEMV, k <= 4096 (k % 256 == 0), at most 8 rows per wave of one
 // workgroup per CU; arguments validated by gemv_dispatch_fused.
-int gemv_q4k_short(const void* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t st) {
+int gemv_q4k_short(const void* w, const void* x, float* y, int64_t n, int64_t k, hipStream_t st, bool x_half) {
     const ShortShape sh = short_shape(n);
     const int units = static_cast<int>(k / 64);
     if (sh.rpw == 0 || units > UNITS_MAX || k % 256 != 0 || n > INT32_MAX) {
@@ -1268,6 +1277,13 @@ int gemv_q4k_short(const void* w, const float* x, float* y, int64_t n, int64_t k
     }
     const uint32_t rb = static_cast<uint32_t>(row_bytes(TYPE_Q4_K, k));
     const int ni = static_cast<int>(n);
+    if (x_half) {  // fp16 x (a one-row GEMM): the default ring only
+        if (sh.wpg == 8)
+            launch_rpw<4, 8, true>(sh.rpw, w, x, y, ni, units, rb, st);
+        else
+            launch_rpw<4, 16, true>(sh.rpw, w, x, y, ni, units, rb, st);
+        return check_launch("vb_gemm");
+    }
     const int ring = knobs().gemv_ring;  // NS - 1 rows in flight while computing (default 3)
     if (sh.wpg == 8) {
         if (ring == 1) launch_rpw<2, 8>(sh.rpw, w, x, y, ni, units, rb, st);

@@ -89,7 +89,9 @@ int gemv_dispatch_fused(const void* w, const RowSrc& src, const GemvFuse& fz, co
 // Plain Q4_K GEMV for k <= 4096 at up to 8 rows per wave (gemv_q4k.hip);
 // gemv_q4k_rpw(n) is its rows per wave, 0 when n is too large for it.
 int gemv_q4k_rpw(int64_t n);
-int gemv_q4k_short(const void* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t st);
+// x_half: x in fp16 (vb_gemm with one fp16 activation row).
+int gemv_q4k_short(const void* w, const void* x, float* y, int64_t n, int64_t k, hipStream_t st,
+                   bool x_half = false);
 // Plain Q6_K (k = 2048 / 4096) and Q8_0 (k % 256 == 0, k <= 4096) GEMV on
 // the short-row arithmetic (gemv_q4k.hip); gemv_short_rpw is its rows per
 // wave, 0 for types and shapes it does not take.
