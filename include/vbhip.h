@@ -128,11 +128,13 @@ int vb_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k,
  * Y[m, n] = sum_k X[m, k] * W[n, k]; X row-major (m x k) in fp32
  * (x_dtype = 0) or fp16 (x_dtype = 1), Y fp32 row-major (m x n).  Products
  * run on v_mfma_f32_16x16x32_f16 with W dequantized to fp16 in registers and
- * fp32 accumulation.  variant: 0 = choose, 1 = skinny (m <= 32), 2 = tiled,
- * 3 = role-split (fp16 X only; chosen for 257 <= m <= 768 with fp16 X),
- * 4 = K-split (every type; chosen for Q6_K / Q8_0, and for Q4_K at
- * 17 <= m <= 32 with fp32 X and n < 12288).  Variant 1 is chosen for Q4_K
- * at m <= 32 otherwise.  Variants 1-3 are Q4_K-only.  With variant 0 and
+ * fp32 accumulation.  variant: 0 = choose, 1 = skinny (m <= 32), 2 = tiled
+ * (every type; Q6_K / Q8_0 need k % 256 == 0), 3 = role-split (fp16 X only;
+ * chosen for 257 <= m <= 768 with fp16 X), 4 = K-split (every type).
+ * Q4_K: variant 1 at m <= 32 (4 at 17 <= m <= 32 with fp32 X and n < 12288),
+ * 2 above (3 in its range).  Q6_K / Q8_0: variant 4 up to m = 64 (Q6_K with
+ * n < 8192: up to m = 256), 2 above.  Variants 1 and 3 are Q4_K-only.  With
+ * variant 0 and
  * m == 1 the GEMV runs instead: vb_gemv's kernels for fp32 X (bit-identical
  * to vb_gemv), and for fp16 X the short-row Q4_K kernel (k <= 4096,
  * k % 256 == 0) reading the halves directly; other fp16 cases stay on MFMA.
@@ -140,8 +142,8 @@ int vb_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k,
  * (cpp/src/fast_model.cpp:644-669, :905-960) over rows decoded by
  * dequantize_row (cpp/src/dequant.cpp:407-425), and cuda::gemm_f32
  * (cpp/include/cuda_kernels.h, cpp/src/cuda_kernels.cu:184-212).
- * Weight types: Q4_K (variants 0-3), Q6_K and Q8_0 (variant 0; Q8_0 needs
- * k % 128 == 0).  W and x 16-byte aligned. */
+ * Weight types: Q4_K (variants 0-4), Q6_K and Q8_0 (variants 0, 2, 4; Q8_0
+ * needs k % 128 == 0).  W and x 16-byte aligned. */
 int vb_gemm(const void* w, const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n,
             int64_t k, int32_t ggml_type, int32_t variant, void* stream);
 

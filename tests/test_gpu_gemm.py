@@ -289,8 +289,96 @@ def test_kq_rejects():
     q8, x8 = make(4, 16, 96, 3, qtype=Q80)  # K % 128 != 0
     with pytest.raises(VBError):
         gemm(q8, torch.from_numpy(x8).to("cuda", torch.float16))
+    for variant in (GEMM_SKINNY, GEMM_SPLIT):  # Q4_K-only kernels
+        with pytest.raises(VBError):
+            gemm(qt, torch.from_numpy(x).to("cuda", torch.float16), variant=variant)
+    q8, x8 = make(4, 16, 384, 3, qtype=Q80)  # the tiled kernel takes K % 256 == 0
     with pytest.raises(VBError):
-        gemm(qt, torch.from_numpy(x).to("cuda", torch.float16), variant=GEMM_TILED)
+        gemm(q8, torch.from_numpy(x8).to("cuda", torch.float16), variant=GEMM_TILED)
+    gemm(q8, torch.from_numpy(x8).to("cuda", torch.float16), variant=GEMM_KSPLIT)
+
+
+# ---- Q6_K and Q8_0 on the LDS-tiled kernel (gemm.hip) ---------------------
+
+@pytest.mark.parametrize("qtype", [Q6K, Q80])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("m,n,k", [(1, 16, 256), (17, 33, 512), (65, 70, 512), (130, 257, 1024),
+                                   (300, 130, 768), (256, 128, 4096), (520, 100, 2304)])
+def test_tiled_types(qtype, dtype, m, n, k):
+    """Q6_K and Q8_0 weights on the tiled kernel (variant 2) at every tile
+    shape the default picks, ragged M and N, Q6_K rows of K = 768 (630 bytes:
+    every other row starts 2 bytes into a dword): against the oracle, and
+    against the K-split kernel, which rounds the same weights to the same fp16
+    values and sums in another order."""
+    qt, x = make(m, n, k, m * 7 + n + qtype, qtype=qtype)
+    xt = torch.from_numpy(x).to("cuda", dtype)
+    y = gemm(qt, xt, variant=GEMM_TILED).cpu().numpy()
+    want = ref_gemm(qt, xt.float().cpu().numpy())
+    assert y.shape == (m, n)
+    assert O.rel_l2(y, want) <= TOL, (qtype, dtype, m, n, k)
+    assert np.all(np.abs(y).sum(axis=1) > 0)
+    other = gemm(qt, xt, variant=GEMM_KSPLIT).cpu().numpy()
+    assert O.rel_l2(y, other) <= 1e-5
+    # the default runs the tiled kernel from M = 65 on (Q6_K at N < 8192:
+    # above M = 256)
+    if m >= 65 and not (qtype == Q6K and n < 8192 and m <= 256):
+        assert np.array_equal(gemm(qt, xt).cpu().numpy(), y)
+
+
+@pytest.mark.parametrize("qtype", [Q6K, Q80])
+@pytest.mark.parametrize("cfg", ["4,2,8", "4,2,6", "4,2,4", "2,4,8", "2,4,4", "2,2,8", "2,2,6", "2,2,4",
+                                 "1,4,8", "1,4,4", "1,2,4", "1,2,6"])
+def test_tiled_types_tile_configs(knob, qtype, cfg):
+    """Every tile configuration with Q6_K / Q8_0 weights, ragged edges, fp16
+    and fp32 X."""
+    knob("VB_GEMM_TILE", cfg)
+    qt, x = make(200, 333, 1280, 29 + qtype, qtype=qtype)
+    for dtype in (torch.float16, torch.float32):
+        xt = torch.from_numpy(x).to("cuda", dtype)
+        y = gemm(qt, xt, variant=GEMM_TILED).cpu().numpy()
+        want = ref_gemm(qt, xt.float().cpu().numpy())
+        assert O.rel_l2(y, want) <= TOL, (cfg, dtype)
+        assert np.all(np.abs(y).sum(axis=1) > 0)
+
+
+@pytest.mark.parametrize("qtype", [Q4K, Q6K, Q80])
+@pytest.mark.parametrize("cfg", ["2,2,4", "1,4,4", "1,4,8", "1,2,4"])
+def test_tiled_k_halves(knob, qtype, cfg):
+    """K halves per workgroup (VB_GEMM_TILE=wm,wn,nf,2): against the oracle
+    and the same tile without halves, which sums the same fp16 products in
+    another order.  K = 1536 (24 steps: 12 a half) and K = 1280 (20 steps: not
+    a whole number of 4-step rounds a half, so the tile runs without
+    halves)."""
+    for k in (1536, 1280):
+        qt, x = make(200, 333, k, 31 + qtype + k, qtype=qtype)
+        for dtype in (torch.float16, torch.float32):
+            xt = torch.from_numpy(x).to("cuda", dtype)
+            knob("VB_GEMM_TILE", cfg + ",2")
+            y = gemm(qt, xt, variant=GEMM_TILED).cpu().numpy()
+            want = ref_gemm(qt, xt.float().cpu().numpy())
+            assert O.rel_l2(y, want) <= TOL, (cfg, dtype, k)
+            assert np.all(np.abs(y).sum(axis=1) > 0)
+            knob("VB_GEMM_TILE", cfg)
+            one = gemm(qt, xt, variant=GEMM_TILED).cpu().numpy()
+            assert O.rel_l2(y, one) <= 1e-5, (cfg, dtype, k)
+
+
+@pytest.mark.parametrize("qtype", [Q6K, Q80])
+def test_tiled_types_down_shape(qtype):
+    """4096 x 14336 Q6_K / Q8_0 weights (the down projection) at M = 512 on
+    the default path (the tiled kernel), against the K-split kernel and the
+    oracle; fp16 X with 0.1 % outliers x20."""
+    n, k, m = 4096, 14336, 512
+    gen = torch.Generator(device="cuda").manual_seed(300 + qtype)
+    qt = QTensor.quantize(torch.randn((n, k), generator=gen, device="cuda") * 0.02, qtype)
+    x = torch.randn((m, k), generator=gen, device="cuda")
+    x[torch.rand((m, k), generator=gen, device="cuda") < 0.001] *= 20.0
+    xh = x.half()
+    y = gemm(qt, xh).cpu().numpy()
+    w = O.dequantize(qt.to_numpy_bytes(), k, qtype).astype(np.float32)
+    want = xh.float().cpu().numpy().astype(np.float64) @ w.T.astype(np.float64)
+    assert O.rel_l2(y, want) <= TOL
+    assert O.rel_l2(y, gemm(qt, xh, variant=GEMM_KSPLIT).cpu().numpy()) <= 1e-5
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])

@@ -1,5 +1,5 @@
-// Dequant-fused GEMM on MFMA:  Y[M, N] = X[M, K] . W[N, K]^T  (W Q4_K, GGUF
-// layout; X fp16 or fp32 row-major; Y fp32 row-major).
+// Dequant-fused GEMM on MFMA:  Y[M, N] = X[M, K] . W[N, K]^T  (W Q4_K, Q6_K
+// or Q8_0 in the GGUF layout; X fp16 or fp32 row-major; Y fp32 row-major).
 //
 // The reference runs batched tokens as a per-token loop of gemv_dequant
 // (cpp/src/fast_model.cpp:644-669, :905-960), re-streaming every weight once
@@ -8,8 +8,9 @@
 // in registers, in the B-operand layout of v_mfma_f32_16x16x32_f16
 // (mfma_q4k.hpp), accumulating in fp32.
 //
-// M <= 32 goes to the skinny kernel (gemm_skinny.hip); M > 32 (chunked
-// prefill) runs the tiled kernel below.
+// Q4_K: M <= 32 goes to the skinny kernel (gemm_skinny.hip); M > 32
+// (chunked prefill) runs the tiled kernel below.  Q6_K / Q8_0 run the
+// K-split kernel (gemm_kq.hip) at small M and the tiled kernel above.
 #include <cstdlib>
 
 #include "mfma_q4k.hpp"
@@ -54,12 +55,126 @@ constexpr int PD = 4;
 // slower; the swizzle reads 0.
 __device__ __forceinline__ int xswz(int row) { return (row >> 1) & 7; }
 
-template <int XT, int NF, int WM, int WN>
-__global__ void __launch_bounds__(64 * WM * WN) gemm_q4k_tiled(const uint8_t* __restrict__ w,
-                                                               const void* __restrict__ X, float* __restrict__ Y,
-                                                               int M, int N, int K, int64_t rb) {
+// ---- weight steps of the 2-byte-aligned GGUF types.  A step is 64
+// elements; dequant unit (row, ug) yields lane (row % 16, ug) of the step's
+// two B fragments: elements 8 ug .. +7 (k-half 0) and 32 + 8 ug .. +7
+// (k-half 1), the natural k order.  issue() loads the raw bytes (buffer
+// loads, 12-byte reads realigned: rows are 2-byte aligned); decode() rounds
+// each weight to fp16 once.  g8 = 8 ug.
+template <int TYPE> struct TiledW {
+    struct Raw {};
+};
+
+// Q6_K in the GGUF layout (super-block of 256: ql[128] @0, qh[64] @128, int8
+// scales[16] @192, fp16 d @208; known answers in tests/test_kquants.py:
+// 134-175).  In half h, element l + 32 t (l < 32, t < 4) is q - 32 with
+// q = (ql[64 h + l + 32 (t & 1)] >> 4 (t >> 1)) & 15 |
+// ((qh[32 h + l] >> 2 t) & 3) << 4, scaled by d * scales[8 h + l / 16 + 2 t].
+// Step 4 sb + 2 h + p covers t = 2 p + ks of half h, so a lane needs the 8
+// ql bytes at 64 h + 8 ug (k-half 0) and 64 h + 32 + 8 ug (k-half 1), nibble
+// p, the qh bytes at 128 + 32 h + 8 ug (bits 4 p + 2 ks), the scales
+// 8 h + 4 p + ug / 2 (+ 2) and d.
+template <>
+struct TiledW<TYPE_Q6_K> {
+    struct Raw {
+        u32x3 l0, l1, qh;
+        uint32_t sc0, sc1, d;
+    };
+    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t w, uint32_t rowoff, int step, uint32_t g8,
+                                                 Raw& r) {
+        const uint32_t base = (rowoff + static_cast<uint32_t>(step >> 2) * 210u) & ~3u;
+        const uint32_t h = (static_cast<uint32_t>(step) >> 1) & 1u, p = static_cast<uint32_t>(step) & 1u;
+        r.l0 = ld96(w, base + 64u * h + g8);
+        r.l1 = ld96(w, base + 64u * h + 32u + g8);
+        r.qh = ld96(w, base + 128u + 32u * h + g8);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(w, static_cast<int>(base + 192u + 8u * h + 4u * p), 0, 0);
+        r.sc0 = v[0];
+        r.sc1 = v[1];
+        r.d = ld32(w, base + 208u);
+    }
+    __device__ static __forceinline__ void decode(const Raw& r, uint32_t rowoff, int step, uint32_t g8,
+                                                  const KqConsts& kc, Frag& lo, Frag& hi) {
+        const uint32_t sh = (rowoff + static_cast<uint32_t>(step >> 2) * 210u) & 3u;
+        const uint32_t sx = 4u * (static_cast<uint32_t>(step) & 1u);  // nibble p
+        uint32_t l0[2], l1[2], qh[2];
+        realign(r.l0, sh, l0[0], l0[1]);
+        realign(r.l1, sh, l1[0], l1[1]);
+        realign(r.qh, sh, qh[0], qh[1]);
+        const uint32_t sc = __builtin_amdgcn_alignbyte(r.sc1, r.sc0, sh);
+        const float d = f16lo(r.d >> (8u * sh));
+        const uint32_t sb = 8u * (g8 >> 4);  // byte of scale ug / 2 within the four
+        const _Float16 v0 = static_cast<_Float16>(d * static_cast<float>(static_cast<int8_t>(sc >> sb)));
+        const _Float16 v1 = static_cast<_Float16>(d * static_cast<float>(static_cast<int8_t>(sc >> (sb + 16u))));
+        const half2_t ds0 = half2_t{v0, v0}, ds1 = half2_t{v1, v1};
+        const half2_t k1056 = half2_t{static_cast<_Float16>(1056.0f), static_cast<_Float16>(1056.0f)};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            // elements 2 i, 2 i + 1: halves (ql | qh << 8); 1024 + q in each half (exact)
+            const uint32_t sel = (i & 1) ? 0x07030602u : 0x05010400u;
+            const uint32_t x = __builtin_amdgcn_perm(qh[i >> 1], l0[i >> 1], sel);
+            const uint32_t y = __builtin_amdgcn_perm(qh[i >> 1], l1[i >> 1], sel);
+            const uint32_t q0 = ((x >> sx) & kc.m0f) | (((x >> (sx + 4u)) & kc.m30) | kc.h64);
+            const uint32_t q1 = ((y >> sx) & kc.m0f) | (((y >> (sx + 6u)) & kc.m30) | kc.h64);
+            lo.u[i] = h2bits((bits2h(q0) - k1056) * ds0);
+            hi.u[i] = h2bits((bits2h(q1) - k1056) * ds1);
+        }
+    }
+};
+
+// Q8_0 in the GGUF layout (vibeblade/loader.py:129-133): blocks of 32 =
+// fp16 d @0, int8 qs[32] @2.  Step s covers blocks 2 s (k-half 0) and
+// 2 s + 1 (k-half 1); a lane needs their qs bytes [8 ug, +8) and d.
+template <>
+struct TiledW<TYPE_Q8_0> {
+    struct Raw {
+        u32x3 q[2];
+        uint32_t d[2];
+    };
+    // block 2 s + ks starts at rowoff + 68 s + 34 ks, whose offset within its
+    // dword is (rowoff + 2 ks) & 3; its qs field is 2 bytes further on
+    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t w, uint32_t rowoff, int step, uint32_t g8,
+                                                 Raw& r) {
+        const uint32_t s0 = rowoff + static_cast<uint32_t>(step) * 68u;
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            const uint32_t b = s0 + 34u * ks;
+            r.q[ks] = ld96(w, ((b + 2u) & ~3u) + g8);
+            r.d[ks] = ld32(w, b & ~3u);
+        }
+    }
+    __device__ static __forceinline__ void decode(const Raw& r, uint32_t rowoff, int, uint32_t, const KqConsts& kc,
+                                                  Frag& lo, Frag& hi) {
+        const uint32_t sh = rowoff & 3u;
+        const half2_t k1152 = half2_t{static_cast<_Float16>(1152.0f), static_cast<_Float16>(1152.0f)};
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            Frag& f = ks ? hi : lo;
+            const uint32_t shd = (sh + 2u * ks) & 3u, shq = shd ^ 2u;
+            uint32_t qs[2];
+            realign(r.q[ks], shq, qs[0], qs[1]);
+            const uint32_t d16 = (r.d[ks] >> (8u * shd)) & 0xFFFFu;
+            const half2_t dd = bits2h(d16 | (d16 << 16));
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                // bytes (b0, b1) into the two halves; (b ^ 0x80) | 0x6400 is
+                // the half 1024 + q + 128 (exact)
+                const uint32_t src = __builtin_amdgcn_perm(0u, qs[i >> 1], (i & 1) ? 0x0C030C02u : 0x0C010C00u);
+                f.u[i] = h2bits((bits2h(src ^ kc.x80) - k1152) * dd);
+            }
+        }
+    }
+};
+
+// KS = 2 splits K in halves between two groups of WM x WN waves, each with
+// its own LDS stage (the tiles below); both run the same number of steps, so
+// the one barrier per step serves both.  At the end group 1 hands its
+// accumulators to group 0 through LDS (fixed order), which stores Y.
+template <int TYPE, int XT, int NF, int WM, int WN, int KS>
+__global__ void __launch_bounds__(64 * WM * WN * KS) gemm_tiled(const uint8_t* __restrict__ w, uint32_t wbytes,
+                                                                const void* __restrict__ X, float* __restrict__ Y,
+                                                                int M, int N, int K, int64_t rb) {
     constexpr int TB_M = 64 * WM;           // X rows per workgroup
-    constexpr int NT = 64 * WM * WN;        // threads
+    constexpr int NT = 64 * WM * WN;        // threads of one K group
     constexpr int NU = 4 * 16 * NF;         // dequant units per step
     constexpr int UPT = (NU + NT - 1) / NT;  // units per thread
     constexpr int NW = NF / WN;             // B fragments per wave
@@ -69,13 +184,22 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_q4k_tiled(const uint8_t* __
     constexpr int XR = XT == X_F16 ? 1 : 2;  // uint4 per piece
     static_assert(NF % WN == 0, "NF must split evenly over the wave columns");
     static_assert(TB_M * XPR % NT == 0, "X pieces must split evenly over the threads");
-    // [buffer][k half][fragment][lane]; fragment NF takes the stores of
-    // threads without a unit (keeps the loop body branch-free)
-    __shared__ uint4 bt[2][2][NF + 1][64];
-    __shared__ __attribute__((aligned(16))) _Float16 xs[2][TB_M * XS_ROW];
+    // Stage of one K group.  bt: [buffer][k half][fragment][lane]; fragment
+    // NF takes the stores of threads without a unit (keeps the loop body
+    // branch-free).
+    struct Stage {
+        uint4 bt[2][2][NF + 1][64];
+        _Float16 xs[2][TB_M * XS_ROW];
+    };
+    static_assert(KS == 1 || sizeof(Stage) >= sizeof(float4_t) * 64 * WM * WN * 4 * (NF / WN),
+                  "group 1's stage must hold its accumulators");
+    __shared__ __attribute__((aligned(16))) Stage stage[KS];
 
-    const int tid = threadIdx.x, lane = tid & 63;
+    const int grp = KS == 1 ? 0 : __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / NT);
+    const int tid = static_cast<int>(threadIdx.x) - grp * NT, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(tid >> 6));
+    auto& bt = stage[grp].bt;
+    auto& xs = stage[grp].xs;
     const int wm = wave / WN, wn = wave - wm * WN;
     const int j = lane & 15, g = lane >> 4;
     // Tile of this workgroup.  Workgroups are dealt to the 8 XCDs round
@@ -91,6 +215,8 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_q4k_tiled(const uint8_t* __
     const int mt0 = tile_m * TB_M;
     const int n0 = tile_n * 16 * NF;
     const int nsteps = K / 64;
+    // this group's steps: [s_base, s_base + nloc); nloc % PD == 0 (host)
+    const int nloc = nsteps / KS, s_base = grp * nloc;
 
     // ---- weights: dequant unit u = tid + NT i is LDS lane slot u: fragment
     // u / 64, lane l = u % 64 -> weight row un = 16 (u / 64) + l % 16, qs part
@@ -107,29 +233,47 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_q4k_tiled(const uint8_t* __
         int n = n0 + un;
         n = n < N ? n : N - 1;
         urow[i] = static_cast<uint32_t>(n) * static_cast<uint32_t>(rb);
-        uq[i] = 16u + 8u * static_cast<uint32_t>(ug);
+        // Q4_K: the unit's qs bytes within a chunk's (after the 16-byte
+        // header); other types: 8 ug
+        uq[i] = (TYPE == TYPE_Q4_K ? 16u : 0u) + 8u * static_cast<uint32_t>(ug);
         uslot[i] = live ? u : NF * 64 + lane;
     }
-    uint4 whd[PD][UPT];
-    uint2 wqs[PD][UPT];
+    [[maybe_unused]] uint4 whd[PD][UPT];
+    [[maybe_unused]] uint2 wqs[PD][UPT];
+    [[maybe_unused]] typename TiledW<TYPE>::Raw wraw[PD][UPT];
+    [[maybe_unused]] const __amdgpu_buffer_rsrc_t wrs = make_rsrc(w, wbytes);
+    [[maybe_unused]] KqConsts kc;
+    if constexpr (TYPE != TYPE_Q4_K) kc = kq_consts();
+    // the lambdas take the group's local step
     auto load_w = [&](int step, int slot) {
+        step += s_base;
         step = step < nsteps ? step : nsteps - 1;
-        const uint32_t sbo = static_cast<uint32_t>(step >> 2) * 144u, co = static_cast<uint32_t>(step & 3) * 32u;
+        if constexpr (TYPE == TYPE_Q4_K) {
+            const uint32_t sbo = static_cast<uint32_t>(step >> 2) * 144u, co = static_cast<uint32_t>(step & 3) * 32u;
 #pragma unroll
-        for (int i = 0; i < UPT; i++) {
-            whd[slot][i] = *reinterpret_cast<const uint4*>(w + (urow[i] + sbo));
-            wqs[slot][i] = *reinterpret_cast<const uint2*>(w + (urow[i] + sbo + uq[i] + co));
+            for (int i = 0; i < UPT; i++) {
+                whd[slot][i] = *reinterpret_cast<const uint4*>(w + (urow[i] + sbo));
+                wqs[slot][i] = *reinterpret_cast<const uint2*>(w + (urow[i] + sbo + uq[i] + co));
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < UPT; i++) TiledW<TYPE>::issue(wrs, urow[i], step, uq[i], wraw[slot][i]);
         }
     };
     auto dequant_store = [&](int step, int slot, int buf) {
-        const int c = step & 3;
+        step += s_base;
         uint4* dst = &bt[buf][0][0][0];
 #pragma unroll
         for (int i = 0; i < UPT; i++) {
-            half2_t ds[2], nm[2];
-            q4k_chunk_scales(whd[slot][i], c, ds, nm);
             Frag lo, hi;
-            q4k_bfrags_nat(wqs[slot][i].x, wqs[slot][i].y, ds, nm, lo, hi);
+            if constexpr (TYPE == TYPE_Q4_K) {
+                half2_t ds[2], nm[2];
+                q4k_chunk_scales(whd[slot][i], step & 3, ds, nm);
+                q4k_bfrags_nat(wqs[slot][i].x, wqs[slot][i].y, ds, nm, lo, hi);
+            } else {
+                // the slot holds the clamped step (past the end: never read)
+                TiledW<TYPE>::decode(wraw[slot][i], urow[i], step < nsteps ? step : nsteps - 1, uq[i], kc, lo, hi);
+            }
             dst[uslot[i]] = make_uint4(lo.u[0], lo.u[1], lo.u[2], lo.u[3]);
             dst[(NF + 1) * 64 + uslot[i]] = make_uint4(hi.u[0], hi.u[1], hi.u[2], hi.u[3]);
         }
@@ -149,6 +293,7 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_q4k_tiled(const uint8_t* __
     }
     uint4 xr[2][XPT][XR];
     auto load_x = [&](int step, int slot) {
+        step += s_base;
         step = step < nsteps ? step : nsteps - 1;
         const uint32_t ko = static_cast<uint32_t>(step) * 64u * XE;
 #pragma unroll
@@ -198,7 +343,7 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_q4k_tiled(const uint8_t* __
     // s + PD go out at the start of step s and X of step s + 3 at its end
     // (scheduling fences keep that order); X(s + 1) is consumed at the end of
     // step s, two steps after its loads went out.
-    for (int s0 = 0; s0 < nsteps; s0 += PD) {
+    for (int s0 = 0; s0 < nloc; s0 += PD) {
 #pragma unroll
         for (int r = 0; r < PD; r++) {
             const int step = s0 + r, buf = r & 1;  // PD is even: buffer = step & 1
@@ -243,6 +388,22 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_q4k_tiled(const uint8_t* __
         }
     }
 
+    if constexpr (KS == 2) {
+        // group 1's stage is free (the last barrier ended every LDS read)
+        float4_t* red = reinterpret_cast<float4_t*>(&stage[1]);
+        if (grp == 1) {
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int f = 0; f < NW; f++) red[((a * NW + f) * (WM * WN) + wave) * 64 + lane] = acc[a][f];
+        }
+        __syncthreads();
+        if (grp == 1) return;
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int f = 0; f < NW; f++) acc[a][f] += red[((a * NW + f) * (WM * WN) + wave) * 64 + lane];
+    }
 #pragma unroll
     for (int a = 0; a < 4; a++) {
 #pragma unroll
@@ -266,16 +427,46 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_q4k_tiled(const uint8_t* __
 // (NF 8 / 6, whichever balances the grid over the CUs; M = 512: 70-72 us).  VB_GEMM_NF (6, 8) overrides NF of the large
 // tiles; VB_GEMM_TILE="wm,wn,nf" (wm 1, 2, 4; wn 2, 4; nf 4, 6, 8 with wn
 // dividing nf) any configuration.
-struct TileCfg { int wm, wn, nf; };
+struct TileCfg { int wm, wn, nf, ks; };
 
-TileCfg tiled_cfg(int64_t M, int64_t N) {
+// Tiles that run with K halves (KS = 2, 512 threads, so at most 256
+// registers a lane): wider ones spill.
+constexpr bool ks2_tile(int wm, int wn, int nf) { return (nf == 4 && wm * wn <= 4) || (wm == 1 && wn == 4 && nf == 8); }
+
+// Q6_K / Q8_0 run the tiled kernel from this M on (variant 0)
+constexpr int64_t kKqTiledMinM = 65;
+
+int64_t tile_count(const TileCfg& c, int64_t M, int64_t N) {
+    return ((N + 16 * c.nf - 1) / (16 * c.nf)) * ((M + 64 * c.wm - 1) / (64 * c.wm));
+}
+
+TileCfg tiled_cfg(int type, int x_dtype, int64_t M, int64_t N, int64_t K) {
     const Knobs& kb = knobs();
-    if (kb.gemm_tile_wm) return TileCfg{kb.gemm_tile_wm, kb.gemm_tile_wn, kb.gemm_tile_nf};
-    if (M <= 64) return TileCfg{1, 4, 4};
-    if (M <= 128) return TileCfg{2, 2, 4};
-    if (M <= 256) return TileCfg{2, 4, 8};
-    if (kb.gemm_nf) return TileCfg{4, 2, kb.gemm_nf};
+    // K halves need a whole number of PD-step rounds per half
+    const bool halves = (K / 64) % (2 * PD) == 0;
+    if (kb.gemm_tile_wm) {
+        const bool ks2 = kb.gemm_tile_ks == 2 && ks2_tile(kb.gemm_tile_wm, kb.gemm_tile_wn, kb.gemm_tile_nf) && halves;
+        return TileCfg{kb.gemm_tile_wm, kb.gemm_tile_wn, kb.gemm_tile_nf, ks2 ? 2 : 1};
+    }
     const int64_t kCUs = num_cus();
+    if (type != TYPE_Q4_K) {
+        // Q6_K / Q8_0: the largest tile whose grid still covers about the CUs
+        // (MI355X: 4096 x 14336 takes 64 x 64 tiles up to M = 256 and
+        // 128 x 64 at M = 512; 14336 x 4096 128 x 64 up to M = 128, 128 x 128
+        // at 256, 256 x 96 or 128 above).  fp32 X keeps 96 columns on the
+        // 256-row tile (128 spill).
+        const int nf_big = x_dtype == X_F16 ? 8 : 6;
+        const TileCfg order[4] = {{4, 2, nf_big, 1}, {2, 4, 8, 1}, {2, 2, 4, 1}, {1, 4, 4, 1}};
+        for (const TileCfg& c : order)
+            if (tile_count(c, M, N) * 8 >= kCUs * 7) return c;
+        return order[3];
+    }
+    // Q4_K, 33 <= M <= 128: K halves (M = 33 / 64 / 100 / 128 at 14336 x
+    // 4096: 24.3 / 25.6 / 30.4 / 31.1 us against 26.9 / 27.3 / 35.4 / 35.6)
+    if (M <= 64) return TileCfg{1, 4, 4, halves ? 2 : 1};
+    if (M <= 128) return TileCfg{2, 2, 4, halves ? 2 : 1};
+    if (M <= 256) return TileCfg{2, 4, 8, 1};
+    if (kb.gemm_nf) return TileCfg{4, 2, kb.gemm_nf, 1};
     const int64_t mt = (M + 255) / 256;
     int best = 8;
     int64_t best_cost = -1;
@@ -287,23 +478,30 @@ TileCfg tiled_cfg(int64_t M, int64_t N) {
             best = nf;
         }
     }
-    return TileCfg{4, 2, best};
+    return TileCfg{4, 2, best, 1};
 }
 
-template <int XT, int NF, int WM, int WN>
-void launch_tiled_cfg(const uint8_t* w, const void* X, float* Y, int M, int N, int K, int64_t rb, hipStream_t st) {
+template <int TYPE, int XT, int NF, int WM, int WN>
+void launch_tiled_cfg(const uint8_t* w, uint32_t wbytes, const void* X, float* Y, int M, int N, int K, int64_t rb,
+                      int ks, hipStream_t st) {
     const dim3 grid(static_cast<uint32_t>((N + 16 * NF - 1) / (16 * NF)),
                     static_cast<uint32_t>((M + 64 * WM - 1) / (64 * WM)));
-    gemm_q4k_tiled<XT, NF, WM, WN><<<grid, dim3(64 * WM * WN), 0, st>>>(w, X, Y, M, N, K, rb);
+    if constexpr (ks2_tile(WM, WN, NF)) {
+        if (ks == 2) {
+            gemm_tiled<TYPE, XT, NF, WM, WN, 2><<<grid, dim3(128 * WM * WN), 0, st>>>(w, wbytes, X, Y, M, N, K, rb);
+            return;
+        }
+    }
+    gemm_tiled<TYPE, XT, NF, WM, WN, 1><<<grid, dim3(64 * WM * WN), 0, st>>>(w, wbytes, X, Y, M, N, K, rb);
 }
 
-template <int XT>
-int launch_tiled(const TileCfg& c, const uint8_t* w, const void* X, float* Y, int M, int N, int K, int64_t rb,
-                 hipStream_t st) {
-#define VB_TILE(WM_, WN_, NF_)                                                   \
-    if (c.wm == WM_ && c.wn == WN_ && c.nf == NF_) {                            \
-        launch_tiled_cfg<XT, NF_, WM_, WN_>(w, X, Y, M, N, K, rb, st);          \
-        return OK;                                                               \
+template <int TYPE, int XT>
+int launch_tiled(const TileCfg& c, const uint8_t* w, uint32_t wbytes, const void* X, float* Y, int M, int N, int K,
+                 int64_t rb, hipStream_t st) {
+#define VB_TILE(WM_, WN_, NF_)                                                        \
+    if (c.wm == WM_ && c.wn == WN_ && c.nf == NF_) {                                 \
+        launch_tiled_cfg<TYPE, XT, NF_, WM_, WN_>(w, wbytes, X, Y, M, N, K, rb, c.ks, st);  \
+        return OK;                                                                    \
     }
     VB_TILE(4, 2, 8)
     VB_TILE(4, 2, 6)
@@ -354,13 +552,27 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
             gemv_q4k_rpw(N) > 0)
             return gemv_q4k_short(w, X, Y, N, K, st, true);
     }
-    if (type != TYPE_Q4_K || variant == 4) {
-        // Q6_K / Q8_0: one kernel family for every M (gemm_kq.hip); Q4_K on
-        // request (variant 4)
-        if (variant != 0 && variant != 4) {
-            set_error("vb_gemm: variant %d is Q4_K-only (use 0 or 4 for Q6_K / Q8_0)", variant);
+    bool tiled = false;
+    if (type != TYPE_Q4_K) {
+        // Q6_K / Q8_0: the K-split kernel (gemm_kq.hip) up to M = 64, where
+        // it decodes each weight once; above, the tiled kernel, which decodes
+        // each weight once per 64-256 rows of M (the K-split kernel once per
+        // 64).  The tiled kernel takes K % 256 == 0.
+        if (variant != 0 && variant != 2 && variant != 4) {
+            set_error("vb_gemm: variant %d is Q4_K-only (use 0, 2 or 4 for Q6_K / Q8_0)", variant);
             return E_UNSUPPORTED;
         }
+        if (variant == 2 && K % 256 != 0) {
+            set_error("vb_gemm: the tiled kernel takes K %% 256 == 0 for Q6_K / Q8_0 (K=%lld)",
+                      static_cast<long long>(K));
+            return E_UNSUPPORTED;
+        }
+        // Q6_K at N < 8192 keeps the K-split kernel up to M = 256 (MI355X,
+        // 4096 x 14336: 88-100 us against 105-112 us tiled)
+        const bool kq_q6k = type == TYPE_Q6_K && N < 8192 && M <= 256;
+        tiled = variant == 2 || (variant == 0 && M >= kKqTiledMinM && K % 256 == 0 && !kq_q6k);
+        if (!tiled) return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
+    } else if (variant == 4) {
         return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
     }
     // 17 <= M <= 32: skinny tiles with two activation tiles per wave for fp16
@@ -368,9 +580,9 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
     // X: 14.5 / 17.5 us at M = 17 / 32 for N = 14336, K = 4096 (K-split 21.5 /
     // 24.8, tiled 27.0 / 27.1); 11.5 / 13.3 us at 4096 x 4096 (tiled 26.6);
     // fp32 X at N = 4096 the K-split kernel is 5 % ahead.
-    if (variant == 0 && M >= 17 && M <= 32 && x_dtype != X_F16 && N < 12288)
+    if (!tiled && variant == 0 && M >= 17 && M <= 32 && x_dtype != X_F16 && N < 12288)
         return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
-    const bool skinny = variant == 1 || (variant == 0 && M <= 32);
+    const bool skinny = !tiled && (variant == 1 || (variant == 0 && M <= 32));
     if (skinny) {
         if (M > 32) {
             set_error("vb_gemm: variant 1 (skinny) takes M <= 32, got %lld", static_cast<long long>(M));
@@ -387,8 +599,9 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
         return E_INVAL;
     }
     const int64_t xbytes = M * K * (x_dtype == X_F16 ? 2 : 4);
+    const int64_t wbytes = (N * rb + 3) & ~int64_t(3);  // whole dwords (buffer resource of Q6_K / Q8_0)
     if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX || (M + 63) / 64 > 65535 ||
-        N * rb >= (int64_t(1) << 32) || xbytes >= (int64_t(1) << 32)) {
+        wbytes >= (int64_t(1) << 32) || xbytes >= (int64_t(1) << 32)) {
         set_error("vb_gemm: shape too large (M=%lld N=%lld K=%lld)", static_cast<long long>(M),
                   static_cast<long long>(N), static_cast<long long>(K));
         return E_INVAL;
@@ -398,14 +611,23 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
     // 71.0 / 74.8 tiled, behind at M = 256 and 1024)
     const int smin = knobs().gemm_split_min_m >= 0 ? knobs().gemm_split_min_m : 257;
     const bool split_range = smin > 0 && M >= smin && M <= 768;
-    if (variant == 3 || (variant == 0 && x_dtype == X_F16 && split_range)) {
+    if (type == TYPE_Q4_K && (variant == 3 || (variant == 0 && x_dtype == X_F16 && split_range))) {
         return gemm_q4k_split(w, X, Y, M, N, K, st);
     }
-    const TileCfg cfg = tiled_cfg(M, N);
+    const TileCfg cfg = tiled_cfg(type, x_dtype, M, N, K);
     const uint8_t* wb = static_cast<const uint8_t*>(w);
-    const int rc = x_dtype == X_F16
-        ? launch_tiled<X_F16>(cfg, wb, X, Y, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), rb, st)
-        : launch_tiled<X_F32>(cfg, wb, X, Y, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), rb, st);
+    const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
+    const uint32_t wby = static_cast<uint32_t>(wbytes);
+    int rc;
+    if (type == TYPE_Q4_K)
+        rc = x_dtype == X_F16 ? launch_tiled<TYPE_Q4_K, X_F16>(cfg, wb, wby, X, Y, m, n, k, rb, st)
+                              : launch_tiled<TYPE_Q4_K, X_F32>(cfg, wb, wby, X, Y, m, n, k, rb, st);
+    else if (type == TYPE_Q6_K)
+        rc = x_dtype == X_F16 ? launch_tiled<TYPE_Q6_K, X_F16>(cfg, wb, wby, X, Y, m, n, k, rb, st)
+                              : launch_tiled<TYPE_Q6_K, X_F32>(cfg, wb, wby, X, Y, m, n, k, rb, st);
+    else
+        rc = x_dtype == X_F16 ? launch_tiled<TYPE_Q8_0, X_F16>(cfg, wb, wby, X, Y, m, n, k, rb, st)
+                              : launch_tiled<TYPE_Q8_0, X_F32>(cfg, wb, wby, X, Y, m, n, k, rb, st);
     if (rc != OK) return rc;
     return check_launch("vb_gemm");
 }

@@ -43,34 +43,6 @@ constexpr uint32_t KQ_X_NONE = 0x80000000u;  // lane offset of an absent activat
 constexpr int KQ_X_F32 = 0;
 constexpr int KQ_X_F16 = 1;
 
-typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
-
-__device__ __forceinline__ u32x3 ld96(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __builtin_amdgcn_raw_buffer_load_b96(r, static_cast<int>(off), 0, 0);
-}
-__device__ __forceinline__ uint32_t ld32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(off), 0, 0);
-}
-// bytes [sh, sh + 8) of the 12 loaded bytes (sh = 0 or 2)
-__device__ __forceinline__ void realign(const u32x3& v, uint32_t sh, uint32_t& x, uint32_t& y) {
-    x = __builtin_amdgcn_alignbyte(v.y, v.x, sh);
-    y = __builtin_amdgcn_alignbyte(v.z, v.y, sh);
-}
-
-// Constants of the decoders in VGPRs: gfx9 VOP3 takes no literal and one
-// scalar operand at most.
-struct KqConsts {
-    uint32_t m0f, m30, h64, x80;
-};
-__device__ __forceinline__ KqConsts kq_consts() {
-    KqConsts c;
-    asm volatile("v_mov_b32 %0, 0x000F000F" : "=v"(c.m0f));
-    asm volatile("v_mov_b32 %0, 0x00300030" : "=v"(c.m30));
-    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(c.h64));
-    asm volatile("v_mov_b32 %0, 0x64806480" : "=v"(c.x80));
-    return c;
-}
-
 template <int TYPE> struct Kq;
 
 // Q4_K (cpp/src/dequant.cpp:258-301; header d, dmin, scales[12] @0, qs[128]

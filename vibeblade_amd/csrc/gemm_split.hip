@@ -4,7 +4,7 @@
 // Replaces, like gemm.hip, the reference's per-token loop of gemv_dequant
 // (cpp/src/fast_model.cpp:644-669, :905-960) for prefill-sized batches.
 //
-// Why a second large-M kernel: in gemm_q4k_tiled every wave of a workgroup
+// Why a second large-M kernel: in gemm_tiled (gemm.hip) every wave of a workgroup
 // loads, dequantizes, stages and multiplies in lockstep behind one barrier
 // per k-step, so those costs add up instead of overlapping (at M = 512 each
 // of them removed alone saves 8-16 us of ~72 us).  Here the eight waves of

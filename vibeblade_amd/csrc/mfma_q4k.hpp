@@ -173,4 +173,36 @@ __device__ __forceinline__ void q4k_bfrags(uint32_t q0, uint32_t q1, const half2
     }
 }
 
+// ---- 2-byte-aligned GGUF rows (Q6_K, Q8_0): 12-byte reads from a field's
+// dword, realigned with v_alignbyte.  The buffer resource spans the tensor
+// rounded up to whole dwords, so the dword past a field's end is either
+// mapped tensor memory or outside the range (reads zero).
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+
+__device__ __forceinline__ u32x3 ld96(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b96(r, static_cast<int>(off), 0, 0);
+}
+__device__ __forceinline__ uint32_t ld32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(off), 0, 0);
+}
+// bytes [sh, sh + 8) of the 12 loaded bytes (sh = 0 or 2)
+__device__ __forceinline__ void realign(const u32x3& v, uint32_t sh, uint32_t& x, uint32_t& y) {
+    x = __builtin_amdgcn_alignbyte(v.y, v.x, sh);
+    y = __builtin_amdgcn_alignbyte(v.z, v.y, sh);
+}
+
+// Constants of the Q6_K / Q8_0 decoders in VGPRs: gfx9 VOP3 takes no
+// literal and one scalar operand at most.
+struct KqConsts {
+    uint32_t m0f, m30, h64, x80;
+};
+__device__ __forceinline__ KqConsts kq_consts() {
+    KqConsts c;
+    asm volatile("v_mov_b32 %0, 0x000F000F" : "=v"(c.m0f));
+    asm volatile("v_mov_b32 %0, 0x00300030" : "=v"(c.m30));
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(c.h64));
+    asm volatile("v_mov_b32 %0, 0x64806480" : "=v"(c.x80));
+    return c;
+}
+
 }  // namespace vb

@@ -57,12 +57,14 @@ Knobs read_knobs() {
         if (v == 6 || v == 8) k.gemm_nf = v;
     }
     if (const char* e = std::getenv("VB_GEMM_TILE")) {
-        int a = 0, b = 0, c = 0;
-        if (std::sscanf(e, "%d,%d,%d", &a, &b, &c) == 3 && (a == 1 || a == 2 || a == 4) && (b == 2 || b == 4) &&
-            (c == 4 || c == 6 || c == 8) && c % b == 0) {
+        int a = 0, b = 0, c = 0, d = 1;
+        const int got = std::sscanf(e, "%d,%d,%d,%d", &a, &b, &c, &d);
+        if ((got == 3 || got == 4) && (a == 1 || a == 2 || a == 4) && (b == 2 || b == 4) &&
+            (c == 4 || c == 6 || c == 8) && c % b == 0 && (d == 1 || d == 2)) {
             k.gemm_tile_wm = a;
             k.gemm_tile_wn = b;
             k.gemm_tile_nf = c;
+            k.gemm_tile_ks = d;
         }
     }
     if (const char* e = std::getenv("VB_GEMV_SPLIT")) {

@@ -13,7 +13,8 @@ namespace vb {
 //   VB_GEMV_Q6K_PATH=dot, VB_GEMV_Q8_PATH=dot  Q6_K / Q8_0 GEMV on the general kernel for every shape
 //   VB_GEMV_MFMA_CFG="wpg,ks"                 that kernel's workgroup shape
 //   VB_GEMM_NF=6|8                            tiled GEMM columns per workgroup
-//   VB_GEMM_TILE="wm,wn,nf"                   tiled GEMM tile configuration
+//   VB_GEMM_TILE="wm,wn,nf[,ks]"              tiled GEMM tile configuration (ks: K halves per
+//                                             workgroup, 1 or 2)
 //   VB_GEMM_SPLIT_MIN_M=m                     smallest M (up to 768) on the role-split GEMM (0: never)
 //   VB_GEMV_SPLIT="sl,d"                      split-row Q4_K GEMV: slices per row (2, 4, 8), rows in flight (1-4)
 //   VB_SPARSE_FUSED=0, VB_SPARSE_NPW=1|2      sparse FFN kernel choice (NPW: the row-split fused
@@ -28,7 +29,7 @@ struct Knobs {
     bool gemv_q8_general = false;
     int gemv_mfma_wpg = 0, gemv_mfma_ks = 0;
     int gemm_nf = 0;
-    int gemm_tile_wm = 0, gemm_tile_wn = 0, gemm_tile_nf = 0;
+    int gemm_tile_wm = 0, gemm_tile_wn = 0, gemm_tile_nf = 0, gemm_tile_ks = 1;
     int gemm_split_min_m = -1;  // smallest M on the role-split kernel (-1: default)
     int gemv_split_sl = 0, gemv_split_d = 0;  // split-row Q4_K GEMV: slices per row, rows in flight
     bool sparse_fused = true;
