@@ -194,9 +194,11 @@ def test_split(m, n, k):
     assert np.all(np.abs(y).sum(axis=1) > 0)
 
 
-def test_split_matches_tiled():
+def test_split_matches_tiled(knob):
     """Same dequantized fragments, same MFMAs in the same order per output:
-    the role-split and tiled kernels agree bit for bit."""
+    the role-split and tiled kernels agree bit for bit (the tiled kernel
+    without K halves, which sum in another order)."""
+    knob("VB_GEMM_TILE", "2,2,4,1")
     qt, x = make(520, 250, 2048, 31)
     xt = torch.from_numpy(x).to("cuda", torch.float16)
     a = gemm(qt, xt, variant=GEMM_TILED).cpu().numpy()
@@ -361,6 +363,20 @@ def test_tiled_k_halves(knob, qtype, cfg):
             knob("VB_GEMM_TILE", cfg)
             one = gemm(qt, xt, variant=GEMM_TILED).cpu().numpy()
             assert O.rel_l2(y, one) <= 1e-5, (cfg, dtype, k)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("m", [40, 200, 512, 1000])
+def test_narrow_n_defaults(dtype, m):
+    """Q4_K at N < 8192 on the default path: the K-split kernel at
+    33 <= M <= 64, 64- and 128-row tiles with K halves up to M = 768, 128 x 128
+    tiles above (K = 1536: 12 steps a half)."""
+    qt, x = make(m, 1000, 1536, 41 + m, qtype=Q4K)
+    xt = torch.from_numpy(x).to("cuda", dtype)
+    y = gemm(qt, xt).cpu().numpy()
+    want = ref_gemm(qt, xt.float().cpu().numpy())
+    assert O.rel_l2(y, want) <= TOL, (dtype, m)
+    assert np.all(np.abs(y).sum(axis=1) > 0)
 
 
 @pytest.mark.parametrize("qtype", [Q6K, Q80])

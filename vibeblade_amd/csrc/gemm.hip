@@ -203,14 +203,16 @@ __global__ void __launch_bounds__(64 * WM * WN * KS) gemm_tiled(const uint8_t* _
     const int wm = wave / WN, wn = wave - wm * WN;
     const int j = lane & 15, g = lane >> 4;
     // Tile of this workgroup.  Workgroups are dealt to the 8 XCDs round
-    // robin (linear id % 8).  With two M-tiles, the XCDs are split between
-    // them so each XCD's L2 holds one M-tile of X.
+    // robin (linear id % 8).  With 2, 4 or 8 M-tiles, each M-tile gets 8 / mt
+    // XCDs of its own, so each XCD's L2 holds one M-tile of X (a bijection
+    // when nt is a multiple of 8 / mt).
     const int nt = static_cast<int>(gridDim.x), mt = static_cast<int>(gridDim.y);
     int tile_n = static_cast<int>(blockIdx.x), tile_m = static_cast<int>(blockIdx.y);
-    if (mt == 2 && nt % 4 == 0) {
+    if ((mt == 2 || mt == 4 || mt == 8) && nt % (8 / mt) == 0) {
+        const int G = 8 / mt;  // XCDs per M-tile
         const int lin = tile_n + nt * tile_m, xcd = lin & 7, r = lin >> 3;
-        tile_m = xcd >> 2;
-        tile_n = (xcd & 3) * (nt >> 2) + r;
+        tile_m = xcd / G;
+        tile_n = (xcd % G) * (nt / G) + r;
     }
     const int mt0 = tile_m * TB_M;
     const int n0 = tile_n * 16 * NF;
@@ -461,6 +463,17 @@ TileCfg tiled_cfg(int type, int x_dtype, int64_t M, int64_t N, int64_t K) {
             if (tile_count(c, M, N) * 8 >= kCUs * 7) return c;
         return order[3];
     }
+    // Q4_K at N < 8192 (the down and attention shapes): narrow tiles with K
+    // halves keep the grid covered (MI355X, 4096 x 14336: M = 128 / 256
+    // 77.6 / 77.7 us on 64 x 64, M = 384 / 512 95.3 / 97.4 on 128 x 64,
+    // against 96.4 / 142 / 210 / 211 with the wide-N choices; 4096 x 4096:
+    // M = 128 / 256 / 512 24.5 / 25.0 / 30.8 against 29.7 / 44.3 / 65.4;
+    // M = 1024 on 128 x 128: 153 against 170)
+    if (N < 8192) {
+        if (M <= 256) return TileCfg{1, 4, 4, halves ? 2 : 1};
+        if (M <= 768) return TileCfg{2, 2, 4, halves ? 2 : 1};
+        return TileCfg{2, 4, 8, 1};
+    }
     // Q4_K, 33 <= M <= 128: K halves (M = 33 / 64 / 100 / 128 at 14336 x
     // 4096: 24.3 / 25.6 / 30.4 / 31.1 us against 26.9 / 27.3 / 35.4 / 35.6)
     if (M <= 64) return TileCfg{1, 4, 4, halves ? 2 : 1};
@@ -582,6 +595,10 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
     // fp32 X at N = 4096 the K-split kernel is 5 % ahead.
     if (!tiled && variant == 0 && M >= 17 && M <= 32 && x_dtype != X_F16 && N < 12288)
         return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
+    // 33 <= M <= 64 at N < 8192: the K-split kernel (4096 x 14336, M = 64:
+    // 63.5 us against 79.3 tiled)
+    if (!tiled && variant == 0 && M >= 33 && M <= 64 && N < 8192)
+        return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
     const bool skinny = !tiled && (variant == 1 || (variant == 0 && M <= 32));
     if (skinny) {
         if (M > 32) {
@@ -610,7 +627,8 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
     // N = 14336, K = 4096 on MI355X 67.9 / 72.0 us at M = 384 / 512 against
     // 71.0 / 74.8 tiled, behind at M = 256 and 1024)
     const int smin = knobs().gemm_split_min_m >= 0 ? knobs().gemm_split_min_m : 257;
-    const bool split_range = smin > 0 && M >= smin && M <= 768;
+    // (at N >= 8192 only: at 4096 x 14336 it ran 211 us against 97 us tiled)
+    const bool split_range = smin > 0 && M >= smin && M <= 768 && N >= 8192;
     if (type == TYPE_Q4_K && (variant == 3 || (variant == 0 && x_dtype == X_F16 && split_range))) {
         return gemm_q4k_split(w, X, Y, M, N, K, st);
     }
