@@ -808,9 +808,11 @@ def run_extra(which, args):
               "GB/s": gbs, "frac_hbm": fr, "rel_l2": e3})
         torch.cuda.empty_cache()
     if "gemm" in which:
-        # Q6_K / Q8_0 weights (the down projection of a Q4_K_M / Q8_0 file)
+        # the down projection: Q6_K in a Q4_K_M file, Q4_K in a Q4_K_S file,
+        # Q8_0 in a Q8_0 file
         from vibeblade_amd import ggml
-        for qtype, name in ((ggml.GGML_TYPE_Q6_K, "Q6_K"), (ggml.GGML_TYPE_Q8_0, "Q8_0")):
+        for qtype, name in ((ggml.GGML_TYPE_Q6_K, "Q6_K"), (ggml.GGML_TYPE_Q4_K, "Q4_K"),
+                            (ggml.GGML_TYPE_Q8_0, "Q8_0")):
             n, k = 4096, 14336
             wb = n * ggml.row_bytes(qtype, k)
             for m in (8, 512):
