@@ -379,6 +379,17 @@ def test_narrow_n_defaults(dtype, m):
     assert np.all(np.abs(y).sum(axis=1) > 0)
 
 
+@pytest.mark.parametrize("m", [2, 5, 8, 16])
+def test_small_m_long_k_runs_ksplit(m):
+    """Q4_K at 2 <= M <= 16, N < 8192, K >= 8192 takes the K-split kernel by
+    default: equal to variant 4 bit for bit, and to the oracle."""
+    qt, x = make(m, 300, 8192, 53 + m, qtype=Q4K)
+    xt = torch.from_numpy(x).to("cuda", torch.float16)
+    y = gemm(qt, xt).cpu().numpy()
+    assert np.array_equal(y, gemm(qt, xt, variant=GEMM_KSPLIT).cpu().numpy())
+    assert O.rel_l2(y, ref_gemm(qt, xt.float().cpu().numpy())) <= TOL
+
+
 @pytest.mark.parametrize("qtype", [Q6K, Q80])
 def test_tiled_types_down_shape(qtype):
     """4096 x 14336 Q6_K / Q8_0 weights (the down projection) at M = 512 on

@@ -596,8 +596,13 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
     if (!tiled && variant == 0 && M >= 17 && M <= 32 && x_dtype != X_F16 && N < 12288)
         return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
     // 33 <= M <= 64 at N < 8192: the K-split kernel (4096 x 14336, M = 64:
-    // 63.5 us against 79.3 tiled)
+    // 63.5 us against 79.3 tiled); M <= 16 there too when K >= 8192 (M = 2 /
+    // 4 / 8 / 9 / 16: 18.1 / 19.5 / 21.8 / 21.9 / 26.6 us against 23.1 / 23.3
+    // / 23.8 / 23.9 / 26.7 skinny; at 4096 x 4096 the skinny kernel stays
+    // ahead, 9.4 against 9.9 at M = 8)
     if (!tiled && variant == 0 && M >= 33 && M <= 64 && N < 8192)
+        return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
+    if (!tiled && variant == 0 && M >= 2 && M <= 16 && N < 8192 && K >= 8192)
         return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
     const bool skinny = !tiled && (variant == 1 || (variant == 0 && M <= 32));
     if (skinny) {
