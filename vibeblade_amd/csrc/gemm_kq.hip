@@ -52,6 +52,7 @@ template <int TYPE> struct Kq;
 // nibbles (sub-block 2 c + 1).
 template <>
 struct Kq<TYPE_Q4_K> {
+    static constexpr bool kBlockLane = false;
     struct Raw {
         u32x4 hd;
         uint2 q[2];
@@ -90,6 +91,7 @@ struct Kq<TYPE_Q4_K> {
 // [32 h + 8 g, +8), the scales 8 h + g / 2 + 2 t and d.
 template <>
 struct Kq<TYPE_Q6_K> {
+    static constexpr bool kBlockLane = false;
     struct Raw {
         u32x3 l0, l1, qh, sc;
         uint32_t d;
@@ -148,38 +150,40 @@ struct Kq<TYPE_Q6_K> {
 
 // Q8_0 in the GGUF layout (vibeblade/loader.py:129-133,
 // cpp/src/cuda_kernels.cu:718-735): blocks of 32 = fp16 d @0, int8 qs[32]
-// @2.  A
-// step is four blocks; k-step ks = block 4 s + ks, lane (j, g) needs qs
-// bytes [8 g, +8) and d.
+// @2.  A step is four blocks.  Lane group g takes block 4 s + g whole (one
+// 34-byte read, one scale) and k-step ks its codes [8 ks, +8): the "block
+// per lane group" k order, which the activation fragments follow (kBlockLane).
+// Rows are whole dwords (K % 128 == 0: 136-byte steps), so block g starts
+// 2 g bytes into a dword modulo 4.
 template <>
 struct Kq<TYPE_Q8_0> {
+    static constexpr bool kBlockLane = true;
     struct Raw {
-        u32x3 q[4];
-        uint32_t d[4];
+        u32x3 q[3];  // 36 bytes from the block's dword
     };
-    // block 4 s + ks starts at rowoff + 136 s + 34 ks, whose offset within
-    // its dword is (rowoff + 2 ks) & 3; its qs field is 2 bytes further on
     __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t w, uint32_t rowoff, int step, int g,
                                                  Raw& r) {
-        const uint32_t s0 = rowoff + static_cast<uint32_t>(step) * 136u, g8 = 8u * static_cast<uint32_t>(g);
+        const uint32_t a = (rowoff + static_cast<uint32_t>(step) * 136u + 34u * static_cast<uint32_t>(g)) & ~3u;
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            const uint32_t b = s0 + 34u * ks;
-            r.q[ks] = ld96(w, ((b + 2u) & ~3u) + g8);
-            r.d[ks] = ld32(w, b & ~3u);
-        }
+        for (int i = 0; i < 3; i++) r.q[i] = ld96(w, a + 12u * i);
     }
-    __device__ static __forceinline__ void decode(const Raw& r, uint32_t rowoff, int, int, const KqConsts& kc,
+    __device__ static __forceinline__ void decode(const Raw& r, uint32_t rowoff, int, int g, const KqConsts& kc,
                                                   Frag* f) {
-        const uint32_t sh = rowoff & 3u;
+        const uint32_t w[9] = {r.q[0].x, r.q[0].y, r.q[0].z, r.q[1].x, r.q[1].y, r.q[1].z, r.q[2].x, r.q[2].y,
+                               r.q[2].z};
+        const bool odd = ((rowoff + 2u * static_cast<uint32_t>(g)) & 3u) != 0;  // block at byte 2 of its dword
+        // d at bytes [0, 2) or [2, 4); codes at byte 2 (realign by 2) or 4 (dword 1)
+        const uint32_t d16 = odd ? (w[0] >> 16) : (w[0] & 0xFFFFu);
+        const half2_t dd = bits2h(d16 | (d16 << 16));
         const half2_t k1152 = half2_t{static_cast<_Float16>(1152.0f), static_cast<_Float16>(1152.0f)};
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
-            const uint32_t shd = (sh + 2u * ks) & 3u, shq = shd ^ 2u;
             uint32_t qs[2];
-            realign(r.q[ks], shq, qs[0], qs[1]);
-            const uint32_t d16 = (r.d[ks] >> (8u * shd)) & 0xFFFFu;
-            const half2_t dd = bits2h(d16 | (d16 << 16));
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int i = 2 * ks + h;
+                qs[h] = odd ? w[i + 1] : __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2u);
+            }
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 // bytes (b0, b1) into the two halves; (b ^ 0x80) | 0x6400 is
@@ -222,11 +226,14 @@ __global__ void __launch_bounds__(64 * KQ_WAVES) gemm_kq_kernel(const uint8_t* _
         n = n < N ? n : N - 1;
         rowoff[cg] = static_cast<uint32_t>(n) * rb;
     }
-    uint32_t xoff[MA];  // activation rows 16 a + j (+ 8 g elements); rows past M read zeros
+    // k order of a step: natural (lane group g holds elements 32 ks + 8 g ..
+    // of k-step ks) or block per lane group (32 g + 8 ks ..)
+    constexpr uint32_t GSTR = T::kBlockLane ? 32u : 8u, KSTR = T::kBlockLane ? 8u : 32u;
+    uint32_t xoff[MA];  // activation rows 16 a + j (+ the lane group's elements); rows past M read zeros
 #pragma unroll
     for (int a = 0; a < MA; a++) {
         const int t = m0 + 16 * a + j;
-        xoff[a] = t < M ? (static_cast<uint32_t>(t) * static_cast<uint32_t>(K) + 8u * static_cast<uint32_t>(g)) * ES
+        xoff[a] = t < M ? (static_cast<uint32_t>(t) * static_cast<uint32_t>(K) + GSTR * static_cast<uint32_t>(g)) * ES
                         : KQ_X_NONE;
     }
     const KqConsts kc = kq_consts();
@@ -258,8 +265,8 @@ __global__ void __launch_bounds__(64 * KQ_WAVES) gemm_kq_kernel(const uint8_t* _
                 for (int ks = 0; ks < 4; ks++)
 #pragma unroll
                     for (int a = 0; a < MA; a++) {
-                        xf.v[ks][a][0] = buf_ld128(xr, xoff[a], so + 32u * ES * ks);
-                        if constexpr (XT == KQ_X_F32) xf.v[ks][a][1] = buf_ld128(xr, xoff[a], so + 32u * ES * ks + 16u);
+                        xf.v[ks][a][0] = buf_ld128(xr, xoff[a], so + KSTR * ES * ks);
+                        if constexpr (XT == KQ_X_F32) xf.v[ks][a][1] = buf_ld128(xr, xoff[a], so + KSTR * ES * ks + 16u);
                     }
                 Frag af[4][MA];
 #pragma unroll
