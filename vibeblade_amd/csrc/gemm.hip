@@ -580,10 +580,12 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
                       static_cast<long long>(K));
             return E_UNSUPPORTED;
         }
-        // Q6_K at N < 8192 keeps the K-split kernel up to M = 256 (MI355X,
-        // 4096 x 14336: 88-100 us against 105-112 us tiled)
-        const bool kq_q6k = type == TYPE_Q6_K && N < 8192 && M <= 256;
-        tiled = variant == 2 || (variant == 0 && M >= kKqTiledMinM && K % 256 == 0 && !kq_q6k);
+        // At N < 8192 the K-split kernel stays ahead up to M = 256 with fp16
+        // X, 128 with fp32 X (MI355X, 4096 x 14336, M = 65-256: Q6_K 88-100
+        // us against 105-112 tiled, Q8_0 94-109 against 114-116; fp32 X at
+        // M = 256 Q8_0 224 against 141)
+        const bool kq_narrow = N < 8192 && M <= (x_dtype == X_F16 ? 256 : 128);
+        tiled = variant == 2 || (variant == 0 && M >= kKqTiledMinM && K % 256 == 0 && !kq_narrow);
         if (!tiled) return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
     } else if (variant == 4) {
         return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
