@@ -59,17 +59,17 @@ def test_skinny(dtype, m, n, k):
 @pytest.mark.parametrize("n,k", [(64, 256), (14336, 4096), (4096, 14336), (1000, 2048)])
 def test_one_row_runs_the_gemv(qtype, dtype, n, k):
     """M = 1 (variant 0) takes the GEMV path: fp32 X for every type, fp16 X on
-    the Q4_K short-row kernel (k <= 4096); other fp16 shapes stay on the MFMA
-    kernels.  Same results as vb_gemv on the same (rounded) activations."""
-    if qtype == Q6K and k % 256 != 0:
-        pytest.skip("k is not a whole number of super-blocks")
-    qt, x = make(1, n, k, n + k + qtype)
+    the short-row kernels (Q4_K k <= 4096, Q6_K k = 2048 / 4096, Q8_0
+    k % 256 == 0 up to 4096); other fp16 shapes stay on the MFMA kernels.
+    Same results as vb_gemv on the same (rounded) activations."""
+    qt, x = make(1, n, k, n + k + qtype, qtype=qtype)
     xt = torch.from_numpy(x).to("cuda", dtype)
     y = gemm(qt, xt).cpu().numpy()
     want = ref_gemm(qt, xt.float().cpu().numpy())
     assert y.shape == (1, n)
     assert O.rel_l2(y, want) <= TOL
-    if dtype == torch.float32 or (qtype == Q4K and k <= 4096):
+    short = {Q4K: k <= 4096, Q6K: k in (2048, 4096), Q80: k % 256 == 0 and k <= 4096}[qtype]
+    if dtype == torch.float32 or short:
         from vibeblade_amd.tensor import gemv
         yv = gemv(qt, xt.float().reshape(-1)).cpu().numpy()
         assert np.array_equal(y.reshape(-1).view(np.uint32), yv.view(np.uint32))

@@ -565,9 +565,11 @@ template <> struct ShortRow<TYPE_Q8_0> {
 // y = W x for plain rows of k <= 4096 elements (units = k / 64 lanes busy)
 // in rows of whole 16-byte slots; wave w of workgroup b owns rows (8 b + w)
 // rpw + [0, rpw).
-template <int TYPE, int G, int NS>
+// XH: x in fp16 (the one-row GEMM with fp16 activations), widened to fp32
+// before the encode.
+template <int TYPE, int G, int NS, bool XH = false>
 __global__ void __launch_bounds__(512) gemv_short_kernel(const uint8_t* __restrict__ w,
-                                                         const float* __restrict__ x, float* __restrict__ y, int n,
+                                                         const void* __restrict__ xp, float* __restrict__ y, int n,
                                                          int units, uint32_t rb, int rpw) {
     using T = ShortRow<TYPE>;
     constexpr int P = (T::SLOTS + 63) / 64;  // 16-byte pieces per lane
@@ -623,10 +625,18 @@ __global__ void __launch_bounds__(512) gemv_short_kernel(const uint8_t* __restri
     {
         const int tu0 = task >> 3;
         const int off = T::x_off(tu0 < units ? tu0 : units - 1, task & 7);
-        const float4 a = *reinterpret_cast<const float4*>(x + off);
-        const float4 b = *reinterpret_cast<const float4*>(x + off + 4);
-        xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
-        xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+        if constexpr (XH) {
+            typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+            const h8 hv = *reinterpret_cast<const h8*>(static_cast<const _Float16*>(xp) + off);
+#pragma unroll
+            for (int i = 0; i < 8; i++) xv[i] = static_cast<float>(hv[i]);
+        } else {
+            const float* x = static_cast<const float*>(xp);
+            const float4 a = *reinterpret_cast<const float4*>(x + off);
+            const float4 b = *reinterpret_cast<const float4*>(x + off + 4);
+            xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
+            xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
     Raw ring[NS];
@@ -1199,32 +1209,32 @@ void launch_rpw(int rpw, const void* w, const void* x, float* y, int n, int unit
     }
 }
 
-template <int TYPE, int G, int NS>
-void launch_short(const void* w, const float* x, float* y, int n, int units, uint32_t rb, int rpw,
+template <int TYPE, int G, int NS, bool XH>
+void launch_short(const void* w, const void* x, float* y, int n, int units, uint32_t rb, int rpw,
                   hipStream_t st) {
     const int grid = (n + 8 * rpw - 1) / (8 * rpw);
-    gemv_short_kernel<TYPE, G, NS><<<dim3(static_cast<uint32_t>(grid)), dim3(512), 0, st>>>(
+    gemv_short_kernel<TYPE, G, NS, XH><<<dim3(static_cast<uint32_t>(grid)), dim3(512), 0, st>>>(
         static_cast<const uint8_t*>(w), x, y, n, units, rb, rpw);
 }
 
 // rpw <= 8: one group of rpw rows; above, groups of 8 rows (NS divides 8)
-template <int TYPE, int NS>
-void launch_short_rpw(int rpw, const void* w, const float* x, float* y, int n, int units, uint32_t rb,
+template <int TYPE, int NS, bool XH = false>
+void launch_short_rpw(int rpw, const void* w, const void* x, float* y, int n, int units, uint32_t rb,
                       hipStream_t st) {
     switch (rpw) {
-    case 1: launch_short<TYPE, 1, NS>(w, x, y, n, units, rb, rpw, st); break;
-    case 2: launch_short<TYPE, 2, NS>(w, x, y, n, units, rb, rpw, st); break;
-    case 3: launch_short<TYPE, 3, NS>(w, x, y, n, units, rb, rpw, st); break;
-    case 4: launch_short<TYPE, 4, NS>(w, x, y, n, units, rb, rpw, st); break;
-    case 5: launch_short<TYPE, 5, NS>(w, x, y, n, units, rb, rpw, st); break;
-    case 6: launch_short<TYPE, 6, NS>(w, x, y, n, units, rb, rpw, st); break;
-    case 7: launch_short<TYPE, 7, NS>(w, x, y, n, units, rb, rpw, st); break;
-    default: launch_short<TYPE, 8, NS>(w, x, y, n, units, rb, rpw, st); break;
+    case 1: launch_short<TYPE, 1, NS, XH>(w, x, y, n, units, rb, rpw, st); break;
+    case 2: launch_short<TYPE, 2, NS, XH>(w, x, y, n, units, rb, rpw, st); break;
+    case 3: launch_short<TYPE, 3, NS, XH>(w, x, y, n, units, rb, rpw, st); break;
+    case 4: launch_short<TYPE, 4, NS, XH>(w, x, y, n, units, rb, rpw, st); break;
+    case 5: launch_short<TYPE, 5, NS, XH>(w, x, y, n, units, rb, rpw, st); break;
+    case 6: launch_short<TYPE, 6, NS, XH>(w, x, y, n, units, rb, rpw, st); break;
+    case 7: launch_short<TYPE, 7, NS, XH>(w, x, y, n, units, rb, rpw, st); break;
+    default: launch_short<TYPE, 8, NS, XH>(w, x, y, n, units, rb, rpw, st); break;
     }
 }
 
 template <int TYPE>
-void launch_short_ns(int ns, int rpw, const void* w, const float* x, float* y, int n, int units, uint32_t rb,
+void launch_short_ns(int ns, int rpw, const void* w, const void* x, float* y, int n, int units, uint32_t rb,
                      hipStream_t st) {
     if (ns == 2) launch_short_rpw<TYPE, 2>(rpw, w, x, y, n, units, rb, st);
     else if (ns == 3) launch_short_rpw<TYPE, 3>(rpw, w, x, y, n, units, rb, st);
@@ -1316,7 +1326,8 @@ int gemv_short_rpw(int32_t type, int64_t n, int64_t k) {
 
 // Plain Q6_K / Q8_0 GEMV on the short-row kernel, 16-byte aligned rows;
 // arguments validated by gemv_dispatch_fused.
-int gemv_short(int32_t type, const void* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t st) {
+int gemv_short(int32_t type, const void* w, const void* x, float* y, int64_t n, int64_t k, hipStream_t st,
+               bool x_half) {
     const int rpw = gemv_short_rpw(type, n, k);
     if (rpw == 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0) {
         set_error("vb_gemv: internal: short-row kernel shape (type %d, n=%lld, k=%lld)", type,
@@ -1331,6 +1342,12 @@ int gemv_short(int32_t type, const void* w, const float* x, float* y, int64_t n,
     // must divide the 8-row groups.
     int ns = knobs().gemv_ring > 0 ? knobs().gemv_ring + 1 : 2;
     if (rpw > 8 && ns != 2) ns = 4;
+    if (x_half) {
+        // fp16 x (the one-row GEMM): the default ring only
+        if (type == TYPE_Q6_K) launch_short_rpw<TYPE_Q6_K, 2, true>(rpw, w, x, y, ni, units, rb, st);
+        else launch_short_rpw<TYPE_Q8_0, 2, true>(rpw, w, x, y, ni, units, rb, st);
+        return check_launch("vb_gemm");
+    }
     if (type == TYPE_Q6_K) launch_short_ns<TYPE_Q6_K>(ns, rpw, w, x, y, ni, units, rb, st);
     else launch_short_ns<TYPE_Q8_0>(ns, rpw, w, x, y, ni, units, rb, st);
     return check_launch("vb_gemv");

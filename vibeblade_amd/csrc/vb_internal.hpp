@@ -95,9 +95,11 @@ int gemv_q4k_short(const void* w, const void* x, float* y, int64_t n, int64_t k,
                    bool x_half = false);
 // Plain Q6_K (k = 2048 / 4096) and Q8_0 (k % 256 == 0, k <= 4096) GEMV on
 // the short-row arithmetic (gemv_q4k.hip); gemv_short_rpw is its rows per
-// wave, 0 for types and shapes it does not take.
+// wave, 0 for types and shapes it does not take.  x_half: x in fp16 (the
+// one-row GEMM).
 int gemv_short_rpw(int32_t type, int64_t n, int64_t k);
-int gemv_short(int32_t type, const void* w, const float* x, float* y, int64_t n, int64_t k, hipStream_t st);
+int gemv_short(int32_t type, const void* w, const void* x, float* y, int64_t n, int64_t k, hipStream_t st,
+               bool x_half = false);
 // Plain or residual-epilogue Q6_K (k % 512 == 0) / Q8_0 GEMV for 4096 < k <=
 // 16384 on the split-row kernel with the short-row units (gemv_q4k.hip);
 // gemv_split_rpw is 0 for types and shapes it does not take.
