@@ -908,8 +908,9 @@ void launch_pairs_npw(int npw, const PairsArgs& a, hipStream_t st) {
 // written.
 constexpr int SPLIT_US = 256;  // unit stride of the encoding (units <= 256)
 
-template <int RPW, int NS, int SL>
-__global__ void __launch_bounds__(1024) gemv_q4k_split_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
+// XH: x in fp16 (the one-row GEMM), widened to fp32 before the encode.
+template <int RPW, int NS, int SL, bool XH = false>
+__global__ void __launch_bounds__(1024) gemv_q4k_split_kernel(const uint8_t* __restrict__ w, const void* __restrict__ xp,
                                                               float* y, const float* resid, int n, int units, int upw,
                                                               uint32_t rb) {
     constexpr int WPG = 16;
@@ -967,10 +968,18 @@ __global__ void __launch_bounds__(1024) gemv_q4k_split_kernel(const uint8_t* __r
         const int task = static_cast<int>(threadIdx.x) + 1024 * t;
         const int tu = task >> 3;
         const int off = (tu < units ? tu : units - 1) * 64 + 8 * (task & 7);
-        const float4 a = *reinterpret_cast<const float4*>(x + off);
-        const float4 b = *reinterpret_cast<const float4*>(x + off + 4);
-        xv[t][0] = a.x; xv[t][1] = a.y; xv[t][2] = a.z; xv[t][3] = a.w;
-        xv[t][4] = b.x; xv[t][5] = b.y; xv[t][6] = b.z; xv[t][7] = b.w;
+        if constexpr (XH) {
+            typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+            const h8 hv = *reinterpret_cast<const h8*>(static_cast<const _Float16*>(xp) + off);
+#pragma unroll
+            for (int i = 0; i < 8; i++) xv[t][i] = static_cast<float>(hv[i]);
+        } else {
+            const float* x = static_cast<const float*>(xp);
+            const float4 a = *reinterpret_cast<const float4*>(x + off);
+            const float4 b = *reinterpret_cast<const float4*>(x + off + 4);
+            xv[t][0] = a.x; xv[t][1] = a.y; xv[t][2] = a.z; xv[t][3] = a.w;
+            xv[t][4] = b.x; xv[t][5] = b.y; xv[t][6] = b.z; xv[t][7] = b.w;
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
     Raw2 ring[NS];
@@ -1152,33 +1161,33 @@ void launch_tsplit_d(int d, int rpw, const void* w, const float* x, float* y, co
     }
 }
 
-template <int RPW, int D, int SL>
-void launch_split(const void* w, const float* x, float* y, const float* resid, int n, int units, int upw,
+template <int RPW, int D, int SL, bool XH>
+void launch_split(const void* w, const void* x, float* y, const float* resid, int n, int units, int upw,
                   uint32_t rb, hipStream_t st) {
     constexpr int NG = 16 / SL;
     constexpr int NS = (RPW < D ? RPW : D) + 1;  // ring: NS - 1 (at most D) rows in flight while computing
     const int grid = (n + NG * RPW - 1) / (NG * RPW);
-    gemv_q4k_split_kernel<RPW, NS, SL><<<dim3(static_cast<uint32_t>(grid)), dim3(1024), 0, st>>>(
+    gemv_q4k_split_kernel<RPW, NS, SL, XH><<<dim3(static_cast<uint32_t>(grid)), dim3(1024), 0, st>>>(
         static_cast<const uint8_t*>(w), x, y, resid, n, units, upw, rb);
 }
 
-template <int D, int SL>
-void launch_split_rpw(int rpw, const void* w, const float* x, float* y, const float* resid, int n, int units,
+template <int D, int SL, bool XH = false>
+void launch_split_rpw(int rpw, const void* w, const void* x, float* y, const float* resid, int n, int units,
                       int upw, uint32_t rb, hipStream_t st) {
     switch (rpw) {
-    case 1: launch_split<1, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
-    case 2: launch_split<2, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
-    case 3: launch_split<3, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
-    case 4: launch_split<4, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
-    case 5: launch_split<5, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
-    case 6: launch_split<6, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
-    case 7: launch_split<7, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
-    default: launch_split<8, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 1: launch_split<1, D, SL, XH>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 2: launch_split<2, D, SL, XH>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 3: launch_split<3, D, SL, XH>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 4: launch_split<4, D, SL, XH>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 5: launch_split<5, D, SL, XH>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 6: launch_split<6, D, SL, XH>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 7: launch_split<7, D, SL, XH>(w, x, y, resid, n, units, upw, rb, st); break;
+    default: launch_split<8, D, SL, XH>(w, x, y, resid, n, units, upw, rb, st); break;
     }
 }
 
 template <int SL>
-void launch_split_d(int d, int rpw, const void* w, const float* x, float* y, const float* resid, int n, int units,
+void launch_split_d(int d, int rpw, const void* w, const void* x, float* y, const float* resid, int n, int units,
                     int upw, uint32_t rb, hipStream_t st) {
     switch (d) {
     case 1: launch_split_rpw<1, SL>(rpw, w, x, y, resid, n, units, upw, rb, st); break;
@@ -1378,8 +1387,8 @@ int gemv_q4k_split_rpw(int64_t n, int64_t k) {
 
 // Plain or residual-epilogue Q4_K GEMV, 4096 < k <= 16384, k % 256 == 0, at
 // most 8 rows per wave; arguments validated by gemv_dispatch_fused.
-int gemv_q4k_split(const void* w, const float* x, float* y, const float* resid, int64_t n, int64_t k,
-                   hipStream_t st) {
+int gemv_q4k_split(const void* w, const void* x, float* y, const float* resid, int64_t n, int64_t k,
+                   hipStream_t st, bool x_half) {
     const int units = static_cast<int>(k / 64);
     const SplitShape sh = split_shape(n, units);
     if (sh.rpw == 0 || units <= UNITS_MAX || units > SPLIT_US || k % 256 != 0 || n > INT32_MAX) {
@@ -1389,6 +1398,16 @@ int gemv_q4k_split(const void* w, const float* x, float* y, const float* resid, 
     }
     const uint32_t rb = static_cast<uint32_t>(row_bytes(TYPE_Q4_K, k));
     const int ni = static_cast<int>(n);
+    if (x_half) {
+        // fp16 x (the one-row GEMM): the default ring only
+        if (sh.sl == 2)
+            launch_split_rpw<2, 2, true>(sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
+        else if (sh.sl == 4)
+            launch_split_rpw<2, 4, true>(sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
+        else
+            launch_split_rpw<2, 8, true>(sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
+        return check_launch("vb_gemm");
+    }
     const int d = knobs().gemv_split_d;
     if (sh.sl == 2)
         launch_split_d<2>(d, sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);

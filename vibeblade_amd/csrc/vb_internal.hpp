@@ -119,8 +119,8 @@ int gemv_q4k_pairs_npw(int64_t n);
 int gemv_q4k_pairs(const void* wg, const void* wu, const float* x, const float* norm_w, float eps, int kind,
                    float* y, int64_t n, int64_t k, hipStream_t st, const int32_t* active = nullptr,
                    const int32_t* n_dev = nullptr, int64_t i_dim = 0);
-int gemv_q4k_split(const void* w, const float* x, float* y, const float* resid, int64_t n, int64_t k,
-                   hipStream_t st);
+int gemv_q4k_split(const void* w, const void* x, float* y, const float* resid, int64_t n, int64_t k,
+                   hipStream_t st, bool x_half = false);
 // Q4_K M=1 GEMV on the int8 matrix cores (gemv_q4k_mfma.hip); arguments
 // already validated by gemv_dispatch_src.
 int gemv_q4k_mfma(const void* w, const RowSrc& src, const float* x, float* y, int64_t n, int64_t k,
