@@ -137,9 +137,9 @@ int vb_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k,
  * with fp16 X, 128 with fp32 X), 2 above.  Variants 1 and 3 are Q4_K-only.  With variant 0 and
  * m == 1 the GEMV runs instead: vb_gemv's kernels for fp32 X (bit-identical
  * to vb_gemv), and for fp16 X the short-row kernels reading the halves
- * directly (Q4_K k <= 4096, and 4096 < k <= 16384 on the split-row
- * kernel; Q6_K k = 2048 / 4096; Q8_0 k % 256 == 0 up to 4096); other fp16
- * cases stay on MFMA.
+ * directly (Q4_K k <= 4096; Q6_K k = 2048 / 4096; Q8_0 k % 256 == 0 up to
+ * 4096), and the split-row kernels for 4096 < k <= 16384 (the shapes vb_gemv
+ * takes there); other fp16 cases stay on MFMA.
  * Replaces the reference's batched path, a per-token loop of gemv_dequant
  * (cpp/src/fast_model.cpp:644-669, :905-960) over rows decoded by
  * dequantize_row (cpp/src/dequant.cpp:407-425), and cuda::gemm_f32

@@ -60,8 +60,8 @@ def test_skinny(dtype, m, n, k):
 def test_one_row_runs_the_gemv(qtype, dtype, n, k):
     """M = 1 (variant 0) takes the GEMV path: fp32 X for every type, fp16 X on
     the short-row kernels (Q4_K k <= 4096, Q6_K k = 2048 / 4096, Q8_0
-    k % 256 == 0 up to 4096) and the Q4_K split-row kernel (k = 14336); other
-    fp16 shapes stay on the MFMA kernels.
+    k % 256 == 0 up to 4096) and the split-row kernels (k = 14336); other fp16
+    shapes stay on the MFMA kernels.
     Same results as vb_gemv on the same (rounded) activations."""
     qt, x = make(1, n, k, n + k + qtype, qtype=qtype)
     xt = torch.from_numpy(x).to("cuda", dtype)
@@ -69,7 +69,7 @@ def test_one_row_runs_the_gemv(qtype, dtype, n, k):
     want = ref_gemm(qt, xt.float().cpu().numpy())
     assert y.shape == (1, n)
     assert O.rel_l2(y, want) <= TOL
-    short = {Q4K: True, Q6K: k in (2048, 4096), Q80: k % 256 == 0 and k <= 4096}[qtype]
+    short = {Q4K: True, Q6K: k in (2048, 4096, 14336), Q80: k % 256 == 0}[qtype]
     if dtype == torch.float32 or short:
         from vibeblade_amd.tensor import gemv
         yv = gemv(qt, xt.float().reshape(-1)).cpu().numpy()

@@ -558,7 +558,7 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
     // one row: the GEMV (the short-row and split-row kernels; rel-L2 near
     // 5e-5, and at 14336 x 4096 on MI355X 7.4 us against 11.8 us for the
     // skinny tile).  fp32 X for every type; fp16 X on the short-row kernels
-    // (k <= 4096) and the Q4_K split-row kernel (4096 < k <= 16384).
+    // (k <= 4096) and the split-row kernels (4096 < k <= 16384).
     if (variant == 0 && M == 1) {
         if (x_dtype == X_F32) return gemv_dispatch(w, static_cast<const float*>(X), Y, N, K, type, st);
         if (type == TYPE_Q4_K && K <= 4096 && K % 256 == 0 && !knobs().gemv_q4k_general && N <= INT32_MAX &&
@@ -573,6 +573,9 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
         const bool general = type == TYPE_Q6_K ? knobs().gemv_q6k_general : knobs().gemv_q8_general;
         if (type != TYPE_Q4_K && !general && gemv_short_rpw(type, N, K) > 0)
             return gemv_short(type, w, X, Y, N, K, st, true);
+        // and 4096 < k <= 16384 on their split-row kernel
+        if (type != TYPE_Q4_K && !general && K > 4096 && gemv_split_rpw(type, N, K) > 0)
+            return gemv_split(type, w, X, Y, nullptr, N, K, st, true);
     }
     bool tiled = false;
     if (type != TYPE_Q4_K) {

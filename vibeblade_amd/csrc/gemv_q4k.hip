@@ -1024,8 +1024,9 @@ __global__ void __launch_bounds__(1024) gemv_q4k_split_kernel(const uint8_t* __r
 // upw units starts on a 4-byte boundary (Q6_K: an even super-block), is read
 // as P contiguous 16-byte pieces per lane from there (its last piece may run
 // a few bytes past the slice: unread) and staged in the wave's row buffer.
-template <int TYPE, int RPW, int NS, int SL>
-__global__ void __launch_bounds__(1024) gemv_split_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
+// XH: x in fp16 (the one-row GEMM), widened to fp32 before the encode.
+template <int TYPE, int RPW, int NS, int SL, bool XH = false>
+__global__ void __launch_bounds__(1024) gemv_split_kernel(const uint8_t* __restrict__ w, const void* __restrict__ xp,
                                                           float* y, const float* resid, int n, int units, int upw,
                                                           uint32_t rb) {
     using T = ShortRow<TYPE>;
@@ -1084,10 +1085,18 @@ __global__ void __launch_bounds__(1024) gemv_split_kernel(const uint8_t* __restr
         const int task = static_cast<int>(threadIdx.x) + 1024 * t;
         const int tu = task >> 3;
         const int off = T::x_off(tu < units ? tu : units - 1, task & 7);
-        const float4 a = *reinterpret_cast<const float4*>(x + off);
-        const float4 b = *reinterpret_cast<const float4*>(x + off + 4);
-        xv[t][0] = a.x; xv[t][1] = a.y; xv[t][2] = a.z; xv[t][3] = a.w;
-        xv[t][4] = b.x; xv[t][5] = b.y; xv[t][6] = b.z; xv[t][7] = b.w;
+        if constexpr (XH) {
+            typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+            const h8 hv = *reinterpret_cast<const h8*>(static_cast<const _Float16*>(xp) + off);
+#pragma unroll
+            for (int i = 0; i < 8; i++) xv[t][i] = static_cast<float>(hv[i]);
+        } else {
+            const float* x = static_cast<const float*>(xp);
+            const float4 a = *reinterpret_cast<const float4*>(x + off);
+            const float4 b = *reinterpret_cast<const float4*>(x + off + 4);
+            xv[t][0] = a.x; xv[t][1] = a.y; xv[t][2] = a.z; xv[t][3] = a.w;
+            xv[t][4] = b.x; xv[t][5] = b.y; xv[t][6] = b.z; xv[t][7] = b.w;
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
     Raw ring[NS];
@@ -1126,33 +1135,33 @@ __global__ void __launch_bounds__(1024) gemv_split_kernel(const uint8_t* __restr
     }
 }
 
-template <int TYPE, int RPW, int D, int SL>
-void launch_tsplit(const void* w, const float* x, float* y, const float* resid, int n, int units, int upw,
+template <int TYPE, int RPW, int D, int SL, bool XH>
+void launch_tsplit(const void* w, const void* x, float* y, const float* resid, int n, int units, int upw,
                    uint32_t rb, hipStream_t st) {
     constexpr int NG = 16 / SL;
     constexpr int NS = (RPW < D ? RPW : D) + 1;
     const int grid = (n + NG * RPW - 1) / (NG * RPW);
-    gemv_split_kernel<TYPE, RPW, NS, SL><<<dim3(static_cast<uint32_t>(grid)), dim3(1024), 0, st>>>(
+    gemv_split_kernel<TYPE, RPW, NS, SL, XH><<<dim3(static_cast<uint32_t>(grid)), dim3(1024), 0, st>>>(
         static_cast<const uint8_t*>(w), x, y, resid, n, units, upw, rb);
 }
 
-template <int TYPE, int D, int SL>
-void launch_tsplit_rpw(int rpw, const void* w, const float* x, float* y, const float* resid, int n, int units,
+template <int TYPE, int D, int SL, bool XH = false>
+void launch_tsplit_rpw(int rpw, const void* w, const void* x, float* y, const float* resid, int n, int units,
                        int upw, uint32_t rb, hipStream_t st) {
     switch (rpw) {
-    case 1: launch_tsplit<TYPE, 1, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
-    case 2: launch_tsplit<TYPE, 2, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
-    case 3: launch_tsplit<TYPE, 3, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
-    case 4: launch_tsplit<TYPE, 4, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
-    case 5: launch_tsplit<TYPE, 5, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
-    case 6: launch_tsplit<TYPE, 6, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
-    case 7: launch_tsplit<TYPE, 7, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
-    default: launch_tsplit<TYPE, 8, D, SL>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 1: launch_tsplit<TYPE, 1, D, SL, XH>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 2: launch_tsplit<TYPE, 2, D, SL, XH>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 3: launch_tsplit<TYPE, 3, D, SL, XH>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 4: launch_tsplit<TYPE, 4, D, SL, XH>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 5: launch_tsplit<TYPE, 5, D, SL, XH>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 6: launch_tsplit<TYPE, 6, D, SL, XH>(w, x, y, resid, n, units, upw, rb, st); break;
+    case 7: launch_tsplit<TYPE, 7, D, SL, XH>(w, x, y, resid, n, units, upw, rb, st); break;
+    default: launch_tsplit<TYPE, 8, D, SL, XH>(w, x, y, resid, n, units, upw, rb, st); break;
     }
 }
 
 template <int TYPE, int SL>
-void launch_tsplit_d(int d, int rpw, const void* w, const float* x, float* y, const float* resid, int n, int units,
+void launch_tsplit_d(int d, int rpw, const void* w, const void* x, float* y, const float* resid, int n, int units,
                      int upw, uint32_t rb, hipStream_t st) {
     switch (d) {
     case 1: launch_tsplit_rpw<TYPE, 1, SL>(rpw, w, x, y, resid, n, units, upw, rb, st); break;
@@ -1438,8 +1447,8 @@ int gemv_split_rpw(int32_t type, int64_t n, int64_t k) {
 
 // Plain or residual-epilogue Q6_K / Q8_0 GEMV, 4096 < k <= 16384, on the
 // split-row kernel; arguments validated by gemv_dispatch_fused.
-int gemv_split(int32_t type, const void* w, const float* x, float* y, const float* resid, int64_t n, int64_t k,
-               hipStream_t st) {
+int gemv_split(int32_t type, const void* w, const void* x, float* y, const float* resid, int64_t n, int64_t k,
+               hipStream_t st, bool x_half) {
     const int units = static_cast<int>(k / 64);
     const SplitShape sh = split_shape_t(type, n, units);
     if (gemv_split_rpw(type, n, k) == 0 || sh.rpw == 0) {
@@ -1456,6 +1465,17 @@ int gemv_split(int32_t type, const void* w, const float* x, float* y, const floa
     if (d == 0) d = type == TYPE_Q6_K ? 1 : 2;
     auto go = [&](auto type_c) {
         constexpr int TY = decltype(type_c)::value;
+        if (x_half) {
+            // fp16 x (the one-row GEMM): the default rows in flight only
+            constexpr int D0 = TY == TYPE_Q6_K ? 1 : 2;
+            if (sh.sl == 2)
+                launch_tsplit_rpw<TY, D0, 2, true>(sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
+            else if (sh.sl == 4)
+                launch_tsplit_rpw<TY, D0, 4, true>(sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
+            else
+                launch_tsplit_rpw<TY, D0, 8, true>(sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
+            return;
+        }
         if (sh.sl == 2)
             launch_tsplit_d<TY, 2>(d, sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
         else if (sh.sl == 4)
@@ -1467,7 +1487,7 @@ int gemv_split(int32_t type, const void* w, const float* x, float* y, const floa
         go(std::integral_constant<int, TYPE_Q6_K>{});
     else
         go(std::integral_constant<int, TYPE_Q8_0>{});
-    return check_launch("vb_gemv");
+    return check_launch(x_half ? "vb_gemm" : "vb_gemv");
 }
 
 // Neurons per wave of the pairs kernel: one 8-wave workgroup per CU when that

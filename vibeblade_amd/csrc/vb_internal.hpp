@@ -104,8 +104,8 @@ int gemv_short(int32_t type, const void* w, const void* x, float* y, int64_t n, 
 // 16384 on the split-row kernel with the short-row units (gemv_q4k.hip);
 // gemv_split_rpw is 0 for types and shapes it does not take.
 int gemv_split_rpw(int32_t type, int64_t n, int64_t k);
-int gemv_split(int32_t type, const void* w, const float* x, float* y, const float* resid, int64_t n, int64_t k,
-               hipStream_t st);
+int gemv_split(int32_t type, const void* w, const void* x, float* y, const float* resid, int64_t n, int64_t k,
+               hipStream_t st, bool x_half = false);
 // Plain or residual-epilogue Q4_K GEMV for 4096 < k <= 16384, rows split over
 // 2, 4 or 8 waves (gemv_q4k.hip); gemv_q4k_split_rpw is 0 for shapes it does not take.
 int gemv_q4k_split_rpw(int64_t n, int64_t k);
