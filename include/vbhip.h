@@ -133,8 +133,8 @@ int vb_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k,
  * 4 = K-split (every type).  Variant 0 for Q4_K: 1 at m <= 32, 2 above, with
  * 4 at 17 <= m <= 32 for fp32 X and n < 12288, and at n < 8192 for
  * 33 <= m <= 64 and (k >= 8192) 2 <= m <= 16; 3 at 257 <= m <= 768 for fp16
- * X and n >= 8192.  Q6_K / Q8_0: 4 up to m = 64 (at n < 8192: up to m = 256
- * with fp16 X, 128 with fp32 X), 2 above.  Variants 1 and 3 are Q4_K-only.  With variant 0 and
+ * X and n >= 8192.  Q6_K / Q8_0: 4 up to m = 64 (at n < 8192: Q6_K up to
+ * m = 256 with fp16 X, both up to 128 with fp32 X), 2 above.  Variants 1 and 3 are Q4_K-only.  With variant 0 and
  * m == 1 the GEMV runs instead: vb_gemv's kernels for fp32 X (bit-identical
  * to vb_gemv), and for fp16 X the short-row kernels reading the halves
  * directly (Q4_K k <= 4096; Q6_K k = 2048 / 4096; Q8_0 k % 256 == 0 up to

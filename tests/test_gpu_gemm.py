@@ -322,9 +322,10 @@ def test_tiled_types(qtype, dtype, m, n, k):
     assert np.all(np.abs(y).sum(axis=1) > 0)
     other = gemm(qt, xt, variant=GEMM_KSPLIT).cpu().numpy()
     assert O.rel_l2(y, other) <= 1e-5
-    # the default runs the tiled kernel from M = 65 on (at N < 8192: above
-    # M = 256 with fp16 X, 128 with fp32 X)
-    if m >= 65 and not (n < 8192 and m <= (256 if dtype == torch.float16 else 128)):
+    # the default runs the tiled kernel from M = 65 on (at N < 8192: Q6_K
+    # above M = 256 with fp16 X, both types above 128 with fp32 X)
+    kq_max = (256 if qtype == Q6K else 0) if dtype == torch.float16 else 128
+    if m >= 65 and not (n < 8192 and m <= kq_max):
         assert np.array_equal(gemm(qt, xt).cpu().numpy(), y)
 
 

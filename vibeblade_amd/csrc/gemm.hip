@@ -62,6 +62,7 @@ __device__ __forceinline__ int xswz(int row) { return (row >> 1) & 7; }
 // loads, 12-byte reads realigned: rows are 2-byte aligned); decode() rounds
 // each weight to fp16 once.  g8 = 8 ug.
 template <int TYPE> struct TiledW {
+    static constexpr bool kPairOrder = false;
     struct Raw {};
 };
 
@@ -76,6 +77,7 @@ template <int TYPE> struct TiledW {
 // 8 h + 4 p + ug / 2 (+ 2) and d.
 template <>
 struct TiledW<TYPE_Q6_K> {
+    static constexpr bool kPairOrder = false;
     struct Raw {
         u32x3 l0, l1, qh;
         uint32_t sc0, sc1, d;
@@ -122,43 +124,51 @@ struct TiledW<TYPE_Q6_K> {
 };
 
 // Q8_0 in the GGUF layout (vibeblade/loader.py:129-133): blocks of 32 =
-// fp16 d @0, int8 qs[32] @2.  Step s covers blocks 2 s (k-half 0) and
-// 2 s + 1 (k-half 1); a lane needs their qs bytes [8 ug, +8) and d.
+// fp16 d @0, int8 qs[32] @2.  Step s covers blocks 2 s and 2 s + 1 in the
+// pair k order (kPairOrder): lane group ug holds the 16 codes
+// [16 (ug & 1), +16) of block 2 s + ug / 2, k-half 0 the first 8 and k-half 1
+// the next 8, i.e. step elements 16 ug .. 16 ug + 15 (the activation
+// fragments read 8-element pieces 2 ug and 2 ug + 1).  One 20-byte code read
+// and one scale read per unit, where the natural order took two of each.
 template <>
 struct TiledW<TYPE_Q8_0> {
+    static constexpr bool kPairOrder = true;
     struct Raw {
-        u32x3 q[2];
-        uint32_t d[2];
+        u32x4 q;
+        uint32_t q4, d;
     };
-    // block 2 s + ks starts at rowoff + 68 s + 34 ks, whose offset within its
-    // dword is (rowoff + 2 ks) & 3; its qs field is 2 bytes further on
+    // block 2 s + ug / 2 starts at rowoff + 68 s + 34 (ug / 2); its codes
+    // [16 (ug & 1), +16) 2 + 16 (ug & 1) bytes further on
     __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t w, uint32_t rowoff, int step, uint32_t g8,
                                                  Raw& r) {
-        const uint32_t s0 = rowoff + static_cast<uint32_t>(step) * 68u;
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-            const uint32_t b = s0 + 34u * ks;
-            r.q[ks] = ld96(w, ((b + 2u) & ~3u) + g8);
-            r.d[ks] = ld32(w, b & ~3u);
-        }
+        const uint32_t ug = g8 >> 3;
+        const uint32_t blk = rowoff + static_cast<uint32_t>(step) * 68u + 34u * (ug >> 1);
+        const uint32_t c = (blk + 2u + 16u * (ug & 1u)) & ~3u;
+        r.q = buf_ld128(w, c, 0);
+        r.q4 = ld32(w, c + 16u);
+        r.d = ld32(w, blk & ~3u);
     }
-    __device__ static __forceinline__ void decode(const Raw& r, uint32_t rowoff, int, uint32_t, const KqConsts& kc,
+    __device__ static __forceinline__ void decode(const Raw& r, uint32_t rowoff, int, uint32_t g8, const KqConsts& kc,
                                                   Frag& lo, Frag& hi) {
-        const uint32_t sh = rowoff & 3u;
+        const uint32_t ug = g8 >> 3;
+        const uint32_t shb = (rowoff + 34u * (ug >> 1)) & 3u;  // block start within its dword
+        const uint32_t shc = (shb + 2u) & 3u;                  // codes start (the odd half: +16, same)
+        const uint32_t w[5] = {r.q.x, r.q.y, r.q.z, r.q.w, r.q4};
+        uint32_t qs[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) qs[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], shc);
+        const uint32_t d16 = (r.d >> (8u * shb)) & 0xFFFFu;
+        const half2_t dd = bits2h(d16 | (d16 << 16));
         const half2_t k1152 = half2_t{static_cast<_Float16>(1152.0f), static_cast<_Float16>(1152.0f)};
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) {
             Frag& f = ks ? hi : lo;
-            const uint32_t shd = (sh + 2u * ks) & 3u, shq = shd ^ 2u;
-            uint32_t qs[2];
-            realign(r.q[ks], shq, qs[0], qs[1]);
-            const uint32_t d16 = (r.d[ks] >> (8u * shd)) & 0xFFFFu;
-            const half2_t dd = bits2h(d16 | (d16 << 16));
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 // bytes (b0, b1) into the two halves; (b ^ 0x80) | 0x6400 is
                 // the half 1024 + q + 128 (exact)
-                const uint32_t src = __builtin_amdgcn_perm(0u, qs[i >> 1], (i & 1) ? 0x0C030C02u : 0x0C010C00u);
+                const uint32_t src =
+                    __builtin_amdgcn_perm(0u, qs[2 * ks + (i >> 1)], (i & 1) ? 0x0C030C02u : 0x0C010C00u);
                 f.u[i] = h2bits((bits2h(src ^ kc.x80) - k1152) * dd);
             }
         }
@@ -321,8 +331,11 @@ __global__ void __launch_bounds__(64 * WM * WN * KS) gemm_tiled(const uint8_t* _
     };
     // A fragment of this lane for a = 0: row wm * 64 + j, 16-byte piece 4 ks + g
     // (16 a + wm * 64 does not change the row's swizzle)
+    // (pair k order: pieces 2 g and 2 g + 1)
     const int arow = (wm * 64 + j) * XS_ROW;
-    const int aoff0 = arow + 8 * (g ^ xswz(j)), aoff1 = arow + 8 * ((4 + g) ^ xswz(j));
+    constexpr bool PAIR = TiledW<TYPE>::kPairOrder;
+    const int pc0 = PAIR ? 2 * g : g, pc1 = PAIR ? 2 * g + 1 : 4 + g;
+    const int aoff0 = arow + 8 * (pc0 ^ xswz(j)), aoff1 = arow + 8 * (pc1 ^ xswz(j));
 
     float4_t acc[4][NW];
 #pragma unroll
@@ -592,11 +605,13 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
                       static_cast<long long>(K));
             return E_UNSUPPORTED;
         }
-        // At N < 8192 the K-split kernel stays ahead up to M = 256 with fp16
-        // X, 128 with fp32 X (MI355X, 4096 x 14336, M = 65-256: Q6_K 88-100
-        // us against 105-112 tiled, Q8_0 94-109 against 114-116; fp32 X at
-        // M = 256 Q8_0 224 against 141)
-        const bool kq_narrow = N < 8192 && M <= (x_dtype == X_F16 ? 256 : 128);
+        // At N < 8192 the K-split kernel stays ahead for Q6_K up to M = 256
+        // with fp16 X (MI355X, 4096 x 14336, M = 65-256: 88-100 us against
+        // 105-112 tiled) and for both types up to M = 128 with fp32 X (Q8_0
+        // M = 65 / 128: 100 / 113 against 107 / 121); Q8_0 with fp16 X runs
+        // tiled from M = 65 (93-95 us against 95-109)
+        const int kq_max = x_dtype == X_F16 ? (type == TYPE_Q6_K ? 256 : 0) : 128;
+        const bool kq_narrow = N < 8192 && M <= kq_max;
         tiled = variant == 2 || (variant == 0 && M >= kKqTiledMinM && K % 256 == 0 && !kq_narrow);
         if (!tiled) return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
     } else if (variant == 4) {
