@@ -93,8 +93,8 @@ template <>
 struct Kq<TYPE_Q6_K> {
     static constexpr bool kBlockLane = false;
     struct Raw {
-        u32x3 l0, l1, qh, sc;
-        uint32_t d;
+        u32x3 l0, l1, qh;
+        uint32_t sd;  // lane group g: dword g of (scales of the half: 12 bytes from their dword, d's dword)
     };
     // every field offset is a multiple of 4 from the super-block start, so
     // one shift (the start's offset within its dword) serves all of them
@@ -108,18 +108,24 @@ struct Kq<TYPE_Q6_K> {
         r.l0 = ld96(w, base + 64u * h + g8);
         r.l1 = ld96(w, base + 64u * h + 32u + g8);
         r.qh = ld96(w, base + 128u + 32u * h + g8);
-        r.sc = ld96(w, base + 192u + 8u * h);
-        r.d = ld32(w, base + 208u);
+        // the four lane groups of a row share its scales and d: one dword each
+        r.sd = ld32(w, g < 3 ? base + 192u + 8u * h + 4u * static_cast<uint32_t>(g) : base + 208u);
     }
     __device__ static __forceinline__ void decode(const Raw& r, uint32_t rowoff, int step, int g, const KqConsts& kc,
                                                   Frag* f) {
         const uint32_t sh = shift(rowoff, step);
+        // scale dwords 0-2 and d's dword from lane groups 0-3: the pair's
+        // even / odd 16-lane rows, then the lower / upper halves of the wave
+        const auto p16 = __builtin_amdgcn_permlane16_swap(r.sd, r.sd, false, false);
+        const auto e32 = __builtin_amdgcn_permlane32_swap(p16[0], p16[0], false, false);
+        const auto o32 = __builtin_amdgcn_permlane32_swap(p16[1], p16[1], false, false);
+        const u32x3 scw = {e32[0], o32[0], e32[1]};
         uint32_t l0[2], l1[2], qh[2], sc[2];
         realign(r.l0, sh, l0[0], l0[1]);
         realign(r.l1, sh, l1[0], l1[1]);
         realign(r.qh, sh, qh[0], qh[1]);
-        realign(r.sc, sh, sc[0], sc[1]);
-        const float d = f16lo(r.d >> (8u * sh));
+        realign(scw, sh, sc[0], sc[1]);
+        const float d = f16lo(o32[1] >> (8u * sh));
         // scale bytes g / 2 + {0, 2, 4, 6} of the half's eight
         const uint32_t P = __builtin_amdgcn_perm(sc[1], sc[0], g >= 2 ? 0x07050301u : 0x06040200u);
         half2_t dsc[4];
