@@ -80,7 +80,7 @@ struct TiledW<TYPE_Q6_K> {
     static constexpr bool kPairOrder = false;
     struct Raw {
         u32x3 l0, l1, qh;
-        uint32_t sc0, sc1, d;
+        uint32_t sd;  // lane group ug: the step's scale dwords (ug 0, 1) or d's dword (ug 2, 3)
     };
     __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t w, uint32_t rowoff, int step, uint32_t g8,
                                                  Raw& r) {
@@ -89,10 +89,9 @@ struct TiledW<TYPE_Q6_K> {
         r.l0 = ld96(w, base + 64u * h + g8);
         r.l1 = ld96(w, base + 64u * h + 32u + g8);
         r.qh = ld96(w, base + 128u + 32u * h + g8);
-        const auto v = __builtin_amdgcn_raw_buffer_load_b64(w, static_cast<int>(base + 192u + 8u * h + 4u * p), 0, 0);
-        r.sc0 = v[0];
-        r.sc1 = v[1];
-        r.d = ld32(w, base + 208u);
+        // the four lane groups of a row share its scales and d: one dword each
+        const uint32_t ug = g8 >> 3;
+        r.sd = ld32(w, ug < 2 ? base + 192u + 8u * h + 4u * p + 4u * ug : base + 208u);
     }
     __device__ static __forceinline__ void decode(const Raw& r, uint32_t rowoff, int step, uint32_t g8,
                                                   const KqConsts& kc, Frag& lo, Frag& hi) {
@@ -102,8 +101,13 @@ struct TiledW<TYPE_Q6_K> {
         realign(r.l0, sh, l0[0], l0[1]);
         realign(r.l1, sh, l1[0], l1[1]);
         realign(r.qh, sh, qh[0], qh[1]);
-        const uint32_t sc = __builtin_amdgcn_alignbyte(r.sc1, r.sc0, sh);
-        const float d = f16lo(r.d >> (8u * sh));
+        // dwords of lane groups 0-2 (the pair's even / odd 16-lane rows, then
+        // the lower / upper halves of the wave)
+        const auto p16 = __builtin_amdgcn_permlane16_swap(r.sd, r.sd, false, false);
+        const auto e32 = __builtin_amdgcn_permlane32_swap(p16[0], p16[0], false, false);
+        const auto o32 = __builtin_amdgcn_permlane32_swap(p16[1], p16[1], false, false);
+        const uint32_t sc = __builtin_amdgcn_alignbyte(o32[0], e32[0], sh);
+        const float d = f16lo(e32[1] >> (8u * sh));
         const uint32_t sb = 8u * (g8 >> 4);  // byte of scale ug / 2 within the four
         const _Float16 v0 = static_cast<_Float16>(d * static_cast<float>(static_cast<int8_t>(sc >> sb)));
         const _Float16 v1 = static_cast<_Float16>(d * static_cast<float>(static_cast<int8_t>(sc >> (sb + 16u))));
