@@ -52,8 +52,17 @@ NCOPIES = 16
 MIN_ROTATION_BYTES = 512 << 20     # every timed rotation touches more than this
 SEED = 1234
 EXTRA_ALL = ("gemv", "sparse", "moe", "predict", "ffn", "gguf", "gemm", "msweep", "cpu")
-DTYPE_GEMV = ("i8 dot (v_dot4_i32_i8) -> i32, f32 scales; x as 16-bit fixed point per 32-element run "
-              "(two int8 halves, per-run f32 scale)")
+# Arithmetic of the GEMV kernels that the GEMV lines time (the short-row Q4_K
+# kernel of the headline, the short-row Q6_K / Q8_0 kernels and the split-row
+# kernels): x encoded per workgroup as 15-bit fixed point (|x16| <= 16383) with
+# one fp32 scale per 64-element unit, each value split into two signed bytes;
+# weights as stored (4-, 6- or 8-bit codes); v_dot4_i32_i8 integer dot
+# products, integer scale/min combination per run, fp32 per unit and row.
+DTYPE_GEMV = ("i8 x i8 dot (v_dot4_i32_i8) -> i32; x as 15-bit fixed point with one f32 scale per "
+              "64-element unit (two int8 halves per value); f32 scale combination per unit, f32 accumulate")
+
+
+DTYPE_GEMM = "fp16 X x W dequantized to fp16 (one rounding) on v_mfma_f32_16x16x32_f16, f32 accumulate"
 
 
 def alg_bytes_gemv(qtype: int, n: int, k: int) -> int:
@@ -214,14 +223,19 @@ def time_gemm(m, n, k, steps, warmup, qtype=None):
     xh = gemm_inputs(m, k, gen)
     ys = torch.empty((len(copies), m, n), dtype=torch.float32, device="cuda")
     lib = _lib.load()
+    # the workspace vb_gemm_ws needs for this shape (the packed-X kernel's X
+    # in fragment order; 0 for the other kernels), allocated once, as a
+    # serving loop would
+    nb = int(lib.vb_gemm_workspace(m, n, k, qtype, 1, 0))
+    ws = torch.empty(max(nb, 16), dtype=torch.uint8, device="cuda")
 
     def mk(i, c):
-        args = (c.ptr(), xh.data_ptr(), 1, ys[i].data_ptr(), m, n, k, c.qtype, 0)
+        args = (c.ptr(), xh.data_ptr(), 1, ys[i].data_ptr(), m, n, k, c.qtype, 0, ws.data_ptr(), nb)
 
         def f(s):
-            rc = lib.vb_gemm(*args, s)
+            rc = lib.vb_gemm_ws(*args, s)
             if rc != 0:
-                _lib.check("vb_gemm", rc)
+                _lib.check("vb_gemm_ws", rc)
         return f
     tm = time_launches([mk(i, c) for i, c in enumerate(copies)], steps, warmup)
     w = O.dequantize(copies[0].to_numpy_bytes(), k, copies[0].qtype).astype(np.float64)
@@ -751,7 +765,8 @@ def run_extra(which, args):
             b2 = alg_bytes_gemv(t, nn, kk)
             gbs, fr = frac(b2, tm)
             emit({"workload": name, "us_per_call": tm.us(), "mean_us": round(tm.mean_ms * 1e3, 3),
-                  "launches": tm.launches, "weight_copies": len(cps), "GB/s": gbs, "frac_hbm": fr, "rel_l2": e2})
+                  "launches": tm.launches, "weight_copies": len(cps), "GB/s": gbs, "frac_hbm": fr, "rel_l2": e2,
+                  "dtype": DTYPE_GEMV})
             del cps, yy
             torch.cuda.empty_cache()
     if "sparse" in which:
@@ -805,7 +820,7 @@ def run_extra(which, args):
         gbs, fr = frac(b3, tm)
         emit({"workload": f"3: Q4_K GEMM M={m} N=14336 K=4096 fp16 X", "us_per_call": tm.us(),
               "launches": tm.launches, "TFLOP/s": round(tfs, 2), "frac_mfma_fp16": round(tfs / MFMA_FP16_PEAK_TFS, 4),
-              "GB/s": gbs, "frac_hbm": fr, "rel_l2": e3})
+              "GB/s": gbs, "frac_hbm": fr, "rel_l2": e3, "dtype": DTYPE_GEMM if m > 1 else DTYPE_GEMV})
         torch.cuda.empty_cache()
     if "gemm" in which:
         # the down projection: Q6_K in a Q4_K_M file, Q4_K in a Q4_K_S file,
@@ -822,7 +837,7 @@ def run_extra(which, args):
                 emit({"workload": f"3: {name} GEMM M={m} N={n} K={k} fp16 X", "us_per_call": tm.us(),
                       "launches": tm.launches, "TFLOP/s": round(tfs, 2),
                       "frac_mfma_fp16": round(tfs / MFMA_FP16_PEAK_TFS, 4), "GB/s": gbs, "frac_hbm": fr,
-                      "rel_l2": e3})
+                      "rel_l2": e3, "dtype": DTYPE_GEMM})
                 torch.cuda.empty_cache()
     if "cpu" in which and not args.no_cpu_baseline:
         for row in cpu_table(min(args.cpu_seconds, 3.0)):

@@ -148,6 +148,18 @@ int vb_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k,
  * needs k % 128 == 0).  W and x 16-byte aligned. */
 int vb_gemm(const void* w, const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n,
             int64_t k, int32_t ggml_type, int32_t variant, void* stream);
+/* vb_gemm with a caller-owned workspace, which lets variant 0 (and variant 5)
+ * use the GEMM that needs one: 5 = X in registers (Q4_K, fp16 X, m >= 256):
+ * a pack pass writes X into the workspace in MFMA fragment order, then the
+ * MFMA waves load their A fragments from it directly and only the
+ * dequantized weight tile goes through LDS.  vb_gemm_workspace returns the
+ * bytes variant `variant` needs for the shape (0: none, then vb_gemm_ws is
+ * vb_gemm); the workspace must be 16-byte aligned.  Same reference path as
+ * vb_gemm (cpp/src/fast_model.cpp:644-669, :905-960); the reference's
+ * batched loop has no workspace (its scratch row is decoded per token). */
+int64_t vb_gemm_workspace(int64_t m, int64_t n, int64_t k, int32_t ggml_type, int32_t x_dtype, int32_t variant);
+int vb_gemm_ws(const void* w, const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n, int64_t k,
+               int32_t ggml_type, int32_t variant, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- TurboSparse activation-sparse FFN, one token ------------------------
  * y[h] = sum_{r < n_active} act(g_r, u_r) * Wd[:, active[r]] with

@@ -10,7 +10,9 @@ import torch
 import oracle as O
 from vibeblade_amd import ggml
 from vibeblade_amd._lib import VBError
-from vibeblade_amd.tensor import QTensor, gemm, GEMM_AUTO, GEMM_SKINNY, GEMM_TILED, GEMM_SPLIT, GEMM_KSPLIT
+from vibeblade_amd import _lib
+from vibeblade_amd.tensor import (QTensor, gemm, GEMM_AUTO, GEMM_SKINNY, GEMM_TILED, GEMM_SPLIT, GEMM_KSPLIT,
+                                  GEMM_XREG)
 
 pytestmark = pytest.mark.gpu
 
@@ -211,6 +213,74 @@ def test_split_rejects_fp32_x():
     qt, x = make(300, 16, 256, 2)
     with pytest.raises(ValueError):
         gemm(qt, torch.from_numpy(x).to("cuda", torch.float32), variant=GEMM_SPLIT)
+
+
+# ---- packed-X kernel (gemm_xr.hip, variant 5 / variant 0 with a workspace) ---
+
+@pytest.mark.parametrize("m,n,k", [(256, 224, 256), (300, 4096, 1024), (512, 14336, 4096), (600, 1136, 512),
+                                   (777, 128, 2048), (256, 16, 768)])
+def test_xreg(m, n, k):
+    """The packed-X kernel: one or several 256-row M-tiles (a last partial
+    tile moved back to end at row M, its shared rows computed twice), ragged
+    N (column tiles of 112, rows past N clamped), K of 1 to 16 super-blocks."""
+    qt, x = make(m, n, k, m * 3 + n + k)
+    xt = torch.from_numpy(x).to("cuda", torch.float16)
+    y = gemm(qt, xt, variant=GEMM_XREG).cpu().numpy()
+    want = ref_gemm(qt, xt.float().cpu().numpy())
+    assert y.shape == (m, n)
+    assert O.rel_l2(y, want) <= TOL
+    assert np.all(np.abs(y).sum(axis=1) > 0)
+
+
+def test_xreg_matches_tiled():
+    """Same fp16 weights and MFMA order per output as the tiled kernel's one
+    k-group configuration: agreement to fp32 rounding of the same sums."""
+    qt, x = make(512, 14336, 4096, 11)
+    xt = torch.from_numpy(x).to("cuda", torch.float16)
+    a = gemm(qt, xt, variant=GEMM_XREG).cpu().numpy()
+    b = gemm(qt, xt, variant=GEMM_TILED).cpu().numpy()
+    assert O.rel_l2(a, b.astype(np.float64)) <= 1e-5
+
+
+def test_xreg_auto_route():
+    """Variant 0 with a workspace takes the packed-X kernel at M > 256, N >=
+    8192 (fp16 X): vb_gemm_workspace says how much, and the result equals an
+    explicit variant 5 call bit for bit."""
+    lib = _lib.load()
+    assert lib.vb_gemm_workspace(512, 14336, 4096, Q4K, 1, 0) == 512 * 4096 * 2
+    assert lib.vb_gemm_workspace(300, 14336, 4096, Q4K, 1, 0) == 512 * 4096 * 2  # whole 256-row tiles
+    assert lib.vb_gemm_workspace(256, 14336, 4096, Q4K, 1, 0) == 0   # M = 256: another kernel
+    assert lib.vb_gemm_workspace(512, 4096, 14336, Q4K, 1, 0) == 0   # N < 8192
+    assert lib.vb_gemm_workspace(512, 14336, 4096, Q4K, 0, 0) == 0   # fp32 X
+    assert lib.vb_gemm_workspace(512, 14336, 4096, Q6K, 1, 0) == 0
+    assert lib.vb_gemm_workspace(256, 64, 256, Q4K, 1, 5) == 256 * 256 * 2
+    qt, x = make(384, 8192, 1024, 5)
+    xt = torch.from_numpy(x).to("cuda", torch.float16)
+    a = gemm(qt, xt).cpu().numpy()
+    b = gemm(qt, xt, variant=GEMM_XREG).cpu().numpy()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert O.rel_l2(a, ref_gemm(qt, xt.float().cpu().numpy())) <= TOL
+
+
+def test_xreg_rejects():
+    lib = _lib.load()
+    qt, x = make(300, 64, 256, 2)
+    with pytest.raises(ValueError):
+        gemm(qt, torch.from_numpy(x).to("cuda", torch.float32), variant=GEMM_XREG)
+    qt, x = make(255, 64, 256, 3)
+    with pytest.raises(ValueError):
+        gemm(qt, torch.from_numpy(x).to("cuda", torch.float16), variant=GEMM_XREG)
+    # variant 5 without a workspace (vb_gemm) or with one that is too small
+    qt, x = make(256, 64, 256, 4)
+    xt = torch.from_numpy(x).to("cuda", torch.float16)
+    y = torch.empty((256, 64), dtype=torch.float32, device="cuda")
+    rc = lib.vb_gemm(qt.ptr(), xt.data_ptr(), 1, y.data_ptr(), 256, 64, 256, Q4K, GEMM_XREG, None)
+    assert rc == -1
+    ws = torch.empty(1024, dtype=torch.uint8, device="cuda")
+    rc = lib.vb_gemm_ws(qt.ptr(), xt.data_ptr(), 1, y.data_ptr(), 256, 64, 256, Q4K, GEMM_XREG, ws.data_ptr(),
+                        1024, None)
+    assert rc == -1
+    assert b"workspace" in lib.vb_last_error()
 
 
 # ---- Q6_K and Q8_0 weights (gemm_kq.hip) ----------------------------------

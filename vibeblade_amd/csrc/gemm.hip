@@ -553,7 +553,7 @@ int launch_tiled(const TileCfg& c, const uint8_t* w, uint32_t wbytes, const void
 }  // namespace
 
 int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, int64_t N, int64_t K,
-                  int32_t type, int32_t variant, hipStream_t st) {
+                  int32_t type, int32_t variant, void* ws, size_t ws_bytes, hipStream_t st) {
     if (type != TYPE_Q4_K && type != TYPE_Q6_K && type != TYPE_Q8_0) {
         set_error("vb_gemm: weight type %d has no MFMA path (Q4_K, Q6_K, Q8_0)", type);
         return E_UNSUPPORTED;
@@ -645,12 +645,12 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
         }
         return gemm_q4k_skinny(w, X, x_dtype, Y, M, N, K, st);
     }
-    if (variant < 0 || variant > 4) {
+    if (variant < 0 || variant > 5) {
         set_error("vb_gemm: unknown variant %d", variant);
         return E_INVAL;
     }
-    if (variant == 3 && x_dtype != X_F16) {
-        set_error("vb_gemm: variant 3 (role-split) takes fp16 X");
+    if ((variant == 3 || variant == 5) && x_dtype != X_F16) {
+        set_error("vb_gemm: variant %d (role-split / X in registers) takes fp16 X", variant);
         return E_INVAL;
     }
     const int64_t xbytes = M * K * (x_dtype == X_F16 ? 2 : 4);
@@ -667,6 +667,28 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
     const int smin = knobs().gemm_split_min_m >= 0 ? knobs().gemm_split_min_m : 257;
     // (at N >= 8192 only: at 4096 x 14336 it ran 211 us against 97 us tiled)
     const bool split_range = smin > 0 && M >= smin && M <= 768 && N >= 8192;
+    // 256 < M, N >= 8192, fp16 X, with a workspace: X packed in fragment
+    // order and loaded straight into registers (gemm_xr.hip; at N = 14336,
+    // K = 4096 on MI355X, pack pass included: M = 384 / 512 / 1024 at 62.8 /
+    // 62.6 / 117.5 us against 68.5 / 70.7 / 139.9 us on the role-split and
+    // tiled kernels; behind at M = 256, 50.8 against 48.5)
+    const bool xr_auto = variant == 0 && type == TYPE_Q4_K && x_dtype == X_F16 && M > 256 && N >= 8192 &&
+                         ws != nullptr && static_cast<int64_t>(ws_bytes) >= gemm_q4k_xr_workspace(M, K) &&
+                         reinterpret_cast<uintptr_t>(ws) % 16 == 0;
+    if (xr_auto) return gemm_q4k_xr(w, X, Y, M, N, K, ws, st);
+    if (type == TYPE_Q4_K && variant == 5) {
+        if (M < 256) {
+            set_error("vb_gemm: variant 5 (X in registers) takes m >= 256, got %lld", static_cast<long long>(M));
+            return E_INVAL;
+        }
+        const int64_t need = gemm_q4k_xr_workspace(M, K);
+        if (!ws || static_cast<int64_t>(ws_bytes) < need || reinterpret_cast<uintptr_t>(ws) % 16) {
+            set_error("vb_gemm: variant 5 needs a 16-byte-aligned workspace of %lld bytes (got %zu)",
+                      static_cast<long long>(need), ws_bytes);
+            return E_INVAL;
+        }
+        return gemm_q4k_xr(w, X, Y, M, N, K, ws, st);
+    }
     if (type == TYPE_Q4_K && (variant == 3 || (variant == 0 && x_dtype == X_F16 && split_range))) {
         return gemm_q4k_split(w, X, Y, M, N, K, st);
     }
@@ -692,5 +714,19 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
 
 extern "C" int vb_gemm(const void* w, const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n,
                        int64_t k, int32_t ggml_type, int32_t variant, void* stream) {
-    return vb::gemm_dispatch(w, x, x_dtype, y, m, n, k, ggml_type, variant, vb::as_stream(stream));
+    return vb::gemm_dispatch(w, x, x_dtype, y, m, n, k, ggml_type, variant, nullptr, 0, vb::as_stream(stream));
+}
+
+extern "C" int64_t vb_gemm_workspace(int64_t m, int64_t n, int64_t k, int32_t ggml_type, int32_t x_dtype,
+                                     int32_t variant) {
+    if (k <= 0 || k % 256 != 0 || ggml_type != vb::TYPE_Q4_K || x_dtype != 1) return 0;
+    // the shapes gemm_dispatch sends to the packed-X kernel
+    if ((variant == 5 && m >= 256) || (variant == 0 && m > 256 && n >= 8192)) return vb::gemm_q4k_xr_workspace(m, k);
+    return 0;
+}
+
+extern "C" int vb_gemm_ws(const void* w, const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n, int64_t k,
+                          int32_t ggml_type, int32_t variant, void* workspace, size_t workspace_bytes, void* stream) {
+    return vb::gemm_dispatch(w, x, x_dtype, y, m, n, k, ggml_type, variant, workspace, workspace_bytes,
+                             vb::as_stream(stream));
 }

@@ -1,0 +1,327 @@
+// Dequant-fused Q4_K GEMM for large M with the activation fragments loaded
+// straight into registers (fp16 X): Y[M, N] = X[M, K] . W[N, K]^T, W in the
+// GGUF Q4_K layout, Y fp32 row-major.
+//
+// Replaces, like gemm.hip, the reference's per-token loop of gemv_dequant
+// (cpp/src/fast_model.cpp:644-669, :905-960) for prefill-sized batches.
+//
+// Why this shape.  A v_mfma_f32_16x16x32_f16 wave tile of m_w x n_w needs
+// (m_w + n_w) x 64 bytes of operands per 32-element k-step.  With the 256 x
+// 112 workgroup tile of 4 MFMA waves (64 x 112 each) and both operands
+// staged through LDS (gemm_split.hip), a CU moves about 150 bytes of LDS
+// traffic per clock at full MFMA rate (the X tile written and read, the B
+// tile written and read four times), which is what its LDS delivers.  Here
+// the MFMA waves load their own 64 X rows straight into A fragments (rows
+// are disjoint between waves: nothing is loaded twice and nothing goes
+// through LDS), and only the dequantized B tile, which all four share, goes
+// through LDS: about 78 bytes per clock at full MFMA rate.
+//
+// X in fragment order.  An A fragment holds 16 rows x 8 halves per lane
+// group; loaded from row-major X every load instruction touches 16 rows (16
+// separate 64-byte pieces, no two adjacent lanes contiguous), and on MI355X
+// such loads kept the texture addresser busy about 60 cycles each: the X
+// stream, not the MFMAs, bounded the kernel (93 us at M = 512, 14336 x
+// 4096; 66 us with the same loads made contiguous).  So a pack pass first
+// writes X into the workspace in the order the fragments are read: per
+// 256-row tile and 64-element step, [ks][wave][a][lane] x 16 bytes, so each
+// A-fragment load is one contiguous 1 KB.  The pack pass reads 2 M K bytes
+// and writes as many (4 MB at M = 512, K = 4096).
+//
+// Roles (8 waves, two per SIMD, so the hardware interleaves one wave's
+// MFMAs with the other's VALU work):
+//  * consumers, waves 0-3: X rows 64 w .. 64 w + 63 of the tile and all 16 NF
+//    columns (4 x NF accumulator tiles).  Per 64-element k-step: the step's B
+//    fragments from LDS, 8 A-fragment loads two steps ahead (two register
+//    slots: the loads of step s + 2 go out as soon as the MFMAs of step s
+//    have read slot s % 2), 8 NF MFMAs.  Nothing but MFMAs and their
+//    operands: VALU work in the same scheduling region as the MFMAs made
+//    the register allocator rotate the accumulators through copies.
+//  * producers, waves 4-7: stage the raw Q4_K bytes of the tile's 16 NF rows
+//    one super-block at a time into LDS with row-contiguous 16-byte loads
+//    (9 lanes per 144-byte block), loaded two super-blocks ahead; and
+//    dequantize super-block sb + 1 from there while the consumers multiply
+//    super-block sb: its 4 NF (chunk, fragment) items are dealt round robin
+//    (item i = p + 4 q: chunk i / NF, fragment i % NF), two per step.
+// LDS: the B ring, two super-blocks x 4 steps x {ks = 0, 1} x NF fragments x
+// 64 lanes x 16 bytes, in the lane order the MFMA reads (every access one
+// contiguous 1 KB per wave instruction), and two raw super-blocks of the
+// tile's rows.  One barrier per super-block (all 8 waves) separates the
+// writes of super-block sb + 1 into the B ring from its reads, the last
+// reads of super-block sb - 1 from the writes of sb + 1 into the same half,
+// and the raw writes from their reads in the same way.
+//
+// A k-step is 64 elements = chunk c of a super-block (Q4_K sub-blocks 2c,
+// 2c + 1); lane (j, g) of 16-row block a holds X[64 w + 16 a + j, 64 s + 32
+// ks + 8 g .. + 8) (natural k order, as q4k_bfrags_nat2 gives the weights).
+#include "mfma_q4k.hpp"
+#include "vb_internal.hpp"
+#include "../../include/vbhip.h"
+
+namespace vb {
+namespace {
+
+constexpr int XR_CW = 4;              // consumer waves
+constexpr int XR_TM = 64 * XR_CW;     // X rows per workgroup
+constexpr int XR_THREADS = 2 * 64 * XR_CW;
+constexpr int XR_STEP_BYTES = XR_TM * 128;  // packed X per 64-element step and tile (32 KB)
+
+// M-tile t covers X rows [t0, t0 + XR_TM) with t0 = min(XR_TM t, M - XR_TM)
+// (M >= XR_TM): a last, partial tile is moved back to end at row M.
+__device__ __forceinline__ int xr_tile_row0(int t, int M) {
+    const int r = t * XR_TM;
+    return r < M - XR_TM ? r : M - XR_TM;
+}
+
+// Pack X (M x K fp16, row-major) into fragment order.  Entry [ks][w][a]
+// [lane] of step s of M-tile t (16 bytes) is X[t0 + 64 w + 16 a + lane % 16,
+// 64 s + 32 ks + 8 (lane / 16) .. + 8).  Workgroup (kb, blk, t) moves the
+// 16 x 256 block of rows t0 + 16 blk .. + 16 and elements 256 kb .. + 256:
+// row-contiguous 16-byte loads (32 lanes per 512-byte row piece), a
+// transpose through LDS (rows padded by 16 bytes: the 16 rows a fragment
+// read gathers fall in distinct banks), and 1 KB contiguous stores (one
+// fragment per 64 threads).
+__global__ void __launch_bounds__(256) xr_pack_kernel(const uint8_t* __restrict__ X, uint4* __restrict__ Xf,
+                                                      int M, int K) {
+    __shared__ uint4 tl[16 * 33];
+    const int kb = static_cast<int>(blockIdx.x), blk = static_cast<int>(blockIdx.y);
+    const int t = static_cast<int>(blockIdx.z), tid = static_cast<int>(threadIdx.x);
+    const int nsteps = K / 64;
+    const int r0 = xr_tile_row0(t, M) + 16 * blk;
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        const int idx = q * 256 + tid, row = idx >> 5, piece = idx & 31;
+        tl[row * 33 + piece] =
+            *reinterpret_cast<const uint4*>(X + (static_cast<int64_t>(r0 + row) * K + 256 * kb + 8 * piece) * 2);
+    }
+    __syncthreads();
+    uint4* dst = Xf + static_cast<int64_t>(t) * nsteps * (XR_STEP_BYTES / 16);
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        const int idx = q * 256 + tid, c = idx >> 6, lane = idx & 63;
+        const int s = 4 * kb + (c >> 1), ks = c & 1;
+        dst[((s * 2 + ks) * 16 + blk) * 64 + lane] = tl[(lane & 15) * 33 + 8 * (c >> 1) + 4 * ks + (lane >> 4)];
+    }
+}
+
+template <int NF>
+__global__ void __launch_bounds__(XR_THREADS) gemm_q4k_xr_kernel(const uint8_t* __restrict__ w, uint32_t wbytes,
+                                                                  const uint8_t* __restrict__ Xf,
+                                                                  float* __restrict__ Y, int M, int N, int K,
+                                                                  uint32_t rb) {
+    constexpr int HS = NF * 64;  // uint4 per (step, ks) half of the B ring
+    constexpr int SS = 2 * HS;   // per step
+    constexpr int SB = 4 * SS;   // per super-block
+    constexpr int RAW = 9 * 16 * NF;          // uint4 of one raw super-block (16 NF rows x 144 B)
+    constexpr int RPT = (RAW + 255) / 256;    // raw pieces per producer thread
+    __shared__ uint4 bt[2 * SB];
+    __shared__ uint4 raw[2 * RAW];
+
+    const int lane = static_cast<int>(threadIdx.x) & 63, j = lane & 15, g = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    // workgroups go to the 8 XCDs round robin (linear id % 8): with two
+    // M-tiles each XCD takes one of them
+    const int nt = static_cast<int>(gridDim.x), mt = static_cast<int>(gridDim.y);
+    int tile_n = static_cast<int>(blockIdx.x), tile_m = static_cast<int>(blockIdx.y);
+    if (mt == 2 && nt % 4 == 0) {
+        const int lin = tile_n + nt * tile_m, xcd = lin & 7, r = lin >> 3;
+        tile_m = xcd >> 2;
+        tile_n = (xcd & 3) * (nt >> 2) + r;
+    }
+    // rows of a moved-back last tile that the tile before also covers are
+    // computed twice, bit-identically (same fragments, same MFMA order), and
+    // written twice with the same values
+    const int mt0 = xr_tile_row0(tile_m, M);
+    const int n0 = tile_n * 16 * NF;
+    const int nsb = K >> 8, nsteps = 4 * nsb;
+
+    if (wave < XR_CW) {
+        // ---------------- consumer ----------------
+        const __amdgpu_buffer_rsrc_t xfs =
+            make_rsrc(Xf + static_cast<int64_t>(tile_m) * nsteps * XR_STEP_BYTES,
+                      static_cast<uint32_t>(nsteps) * XR_STEP_BYTES);
+        const uint32_t xv = 16u * static_cast<uint32_t>(lane);
+        Frag areg[2][2][4];  // [slot][ks][a]
+        auto load_a = [&](int s, int slot, int ks) {
+            s = s < nsteps ? s : nsteps - 1;
+#pragma unroll
+            for (int a = 0; a < 4; a++) {
+                const uint32_t so = static_cast<uint32_t>(((s * 2 + ks) * 16 + wave * 4 + a) * 1024);
+                const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xfs, static_cast<int>(xv), static_cast<int>(so), 0);
+                areg[slot][ks][a].u[0] = v.x;
+                areg[slot][ks][a].u[1] = v.y;
+                areg[slot][ks][a].u[2] = v.z;
+                areg[slot][ks][a].u[3] = v.w;
+            }
+        };
+        auto read_b = [&](int buf, int t, int ks, Frag* b) {
+            const uint4* src = bt + buf * SB + t * SS + ks * HS + lane;
+#pragma unroll
+            for (int f = 0; f < NF; f++) {
+                const uint4 v = src[f * 64];
+                b[f].u[0] = v.x; b[f].u[1] = v.y; b[f].u[2] = v.z; b[f].u[3] = v.w;
+            }
+        };
+        float4_t acc[4][NF];
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int f = 0; f < NF; f++) acc[a][f] = float4_t{0.f, 0.f, 0.f, 0.f};
+        auto mfmas = [&](const Frag* af, const Frag* b) {
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int f = 0; f < NF; f++) acc[a][f] = mfma16x16x32(af[a], b[f], acc[a][f]);
+        };
+
+        load_a(0, 0, 0);
+        load_a(0, 0, 1);
+        load_a(1, 1, 0);
+        load_a(1, 1, 1);
+        __syncthreads();  // raw super-blocks 0 and 1 staged
+        __syncthreads();  // ring half 0 (super-block 0) written
+        Frag b0[NF], b1[NF];
+        read_b(0, 0, 0, b0);
+        for (int sb = 0; sb < nsb; sb++) {
+            const int cur = sb & 1, nxt = cur ^ 1;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int s = 4 * sb + t;
+                const int slot = t & 1;
+                __builtin_amdgcn_sched_barrier(0);
+                read_b(cur, t, 1, b1);
+                __builtin_amdgcn_sched_barrier(0);
+                mfmas(areg[slot][0], b0);
+                __builtin_amdgcn_sched_barrier(0);
+                load_a(s + 2, slot, 0);
+                if (t == 3) __syncthreads();
+                read_b(t == 3 ? nxt : cur, (t + 1) & 3, 0, b0);
+                __builtin_amdgcn_sched_barrier(0);
+                mfmas(areg[slot][1], b1);
+                __builtin_amdgcn_sched_barrier(0);
+                load_a(s + 2, slot, 1);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+#pragma unroll
+            for (int f = 0; f < NF; f++) {
+                const int col = n0 + 16 * f + j;
+                if (col >= N) continue;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int t = mt0 + 64 * wave + 16 * a + 4 * g + r;
+                    Y[static_cast<int64_t>(t) * N + col] = acc[a][f][r];
+                }
+            }
+        }
+    } else {
+        // ---------------- producer ----------------
+        const int pw = wave - XR_CW;
+        const int pt = static_cast<int>(threadIdx.x) - 64 * XR_CW;
+        const __amdgpu_buffer_rsrc_t wrs = make_rsrc(w, wbytes);
+        // raw piece p = pt + 256 i of a super-block: 16-byte piece p % 9 of
+        // tile row p / 9 (rows past N repeat row N - 1, never stored; pieces
+        // past the tile repeat the last one and are not written)
+        uint32_t roff[RPT];
+#pragma unroll
+        for (int i = 0; i < RPT; i++) {
+            int p = pt + 256 * i;
+            p = p < RAW ? p : RAW - 1;
+            int n = n0 + p / 9;
+            n = n < N ? n : N - 1;
+            roff[i] = static_cast<uint32_t>(n) * rb + 16u * static_cast<uint32_t>(p % 9);
+        }
+        u32x4 rr[RPT];
+        auto load_raw = [&](int sb) {
+            sb = sb < nsb ? sb : nsb - 1;
+#pragma unroll
+            for (int i = 0; i < RPT; i++)
+                rr[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, static_cast<int>(roff[i]),
+                                                              static_cast<int>(static_cast<uint32_t>(sb) * 144u), 0);
+        };
+        auto store_raw = [&](int buf) {
+#pragma unroll
+            for (int i = 0; i < RPT; i++) {
+                const int p = pt + 256 * i;
+                if (i + 1 < RPT || p < RAW) raw[buf * RAW + p] = make_uint4(rr[i].x, rr[i].y, rr[i].z, rr[i].w);
+            }
+        };
+        // the wave's dequant items q = 0 .. NF - 1: chunk ic[q], fragment ifr[q]
+        int ic[NF], ifr[NF];
+#pragma unroll
+        for (int q = 0; q < NF; q++) {
+            const int i = pw + 4 * q;
+            ic[q] = i / NF;
+            ifr[q] = i - NF * ic[q];
+        }
+        const NatConsts kc = nat_consts();
+        auto dequant_item = [&](int q, int rbuf, int buf) {
+            const uint8_t* rw = reinterpret_cast<const uint8_t*>(raw + rbuf * RAW) + (16 * ifr[q] + j) * 144;
+            const uint4 h = *reinterpret_cast<const uint4*>(rw);
+            const uint2 qs = *reinterpret_cast<const uint2*>(rw + 16 + 32 * ic[q] + 8 * g);
+            half2_t ds[2], nm[2];
+            q4k_chunk_scales_sel(h, ic[q], ds, nm);
+            Frag lo, hi;
+            q4k_bfrags_nat2(qs.x, qs.y, ds, nm, kc, lo, hi);
+            uint4* dst = bt + buf * SB + ic[q] * SS + ifr[q] * 64 + lane;
+            dst[0] = make_uint4(lo.u[0], lo.u[1], lo.u[2], lo.u[3]);
+            dst[HS] = make_uint4(hi.u[0], hi.u[1], hi.u[2], hi.u[3]);
+        };
+
+        load_raw(0);
+        store_raw(0);
+        load_raw(1);
+        store_raw(1);
+        __syncthreads();  // raw super-blocks 0 and 1 staged
+#pragma unroll
+        for (int q = 0; q < NF; q++) dequant_item(q, 0, 0);
+        load_raw(2);
+        __syncthreads();  // ring half 0 written
+        for (int sb = 0; sb < nsb; sb++) {
+            // dequantize super-block sb + 1 (raw half (sb + 1) % 2) into ring
+            // half (sb + 1) % 2, two items per step; then stage the raw bytes
+            // of super-block sb + 2 (loaded during sb - 1) into raw half sb % 2,
+            // free since super-block sb was dequantized during sb - 1, and
+            // load those of sb + 3.  Past the last super-block: clamped
+            // loads, halves nobody reads.
+            const int nxt = (sb & 1) ^ 1;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int k2 = 0; k2 < 2; k2++)
+                    if (2 * t + k2 < NF) dequant_item(2 * t + k2, nxt, nxt);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            store_raw(sb & 1);
+            load_raw(sb + 3);
+            __syncthreads();
+        }
+    }
+}
+
+}  // namespace
+
+int64_t gemm_q4k_xr_workspace(int64_t M, int64_t K) {
+    return (M + XR_TM - 1) / XR_TM * XR_TM * K * 2;
+}
+
+// Caller (gemm_dispatch) has validated type (Q4_K), alignment (W, X 16 B),
+// the 32-bit offset bounds (N * row bytes, M * K * 2 < 2^32), M >= 256 and
+// the workspace (gemm_q4k_xr_workspace bytes, 16-byte aligned).
+int gemm_q4k_xr(const void* w, const void* X, float* Y, int64_t M, int64_t N, int64_t K, void* ws, hipStream_t st) {
+    constexpr int NF = 7;
+    const int64_t rb = row_bytes(TYPE_Q4_K, K);
+    const uint32_t mtiles = static_cast<uint32_t>((M + XR_TM - 1) / XR_TM);
+    xr_pack_kernel<<<dim3(static_cast<uint32_t>(K / 256), XR_TM / 16, mtiles), dim3(256), 0, st>>>(
+        static_cast<const uint8_t*>(X), static_cast<uint4*>(ws), static_cast<int>(M), static_cast<int>(K));
+    const dim3 grid(static_cast<uint32_t>((N + 16 * NF - 1) / (16 * NF)), mtiles);
+    gemm_q4k_xr_kernel<NF><<<grid, dim3(XR_THREADS), 0, st>>>(
+        static_cast<const uint8_t*>(w), static_cast<uint32_t>(N * rb), static_cast<const uint8_t*>(ws), Y,
+        static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), static_cast<uint32_t>(rb));
+    return check_launch("vb_gemm");
+}
+
+}  // namespace vb

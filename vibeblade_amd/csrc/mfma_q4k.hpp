@@ -98,6 +98,25 @@ __device__ __forceinline__ void q4k_chunk_scales(const uint4& hd, int c, half2_t
     }
 }
 
+// Same values for a chunk index c that varies between waves: selects
+// instead of a branch, so a loop that calls it stays one basic block (the
+// scheduler can then interleave its VALU work with the MFMAs around it).
+__device__ __forceinline__ void q4k_chunk_scales_sel(const uint4& hd, int c, half2_t* ds, half2_t* nm) {
+    const uint32_t sh = 16u * static_cast<uint32_t>(c & 1);
+    const uint32_t A = hd.y >> sh, B = hd.z >> sh, C = hd.w >> sh;
+    const uint32_t lo = c < 2 ? 0xFFFFFFFFu : 0u;
+    const uint32_t SC = (lo & A & 0x3F3Fu) | (~lo & ((C & 0x0F0Fu) | ((A >> 2) & 0x3030u)));
+    const uint32_t M = (lo & B & 0x3F3Fu) | (~lo & (((C >> 4) & 0x0F0Fu) | ((B >> 2) & 0x3030u)));
+    const float d = f16lo(hd.x), dmin = f16hi(hd.x);
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const _Float16 s = static_cast<_Float16>(d * static_cast<float>((SC >> (8 * i)) & 0xFFu));
+        const _Float16 m = static_cast<_Float16>(-(dmin * static_cast<float>((M >> (8 * i)) & 0xFFu)));
+        ds[i] = half2_t{s, s};
+        nm[i] = half2_t{m, m};
+    }
+}
+
 // Natural-k-order variant: dword i of a fragment holds elements (2i, 2i+1).
 // v_perm spreads bytes (b0, b1) of a qs dword into the two halves first, so
 // the activation operand needs no reordering (X can be staged as is).

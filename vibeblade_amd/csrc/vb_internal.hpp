@@ -131,11 +131,19 @@ int gemm_q4k_skinny(const void* w, const void* X, int32_t x_dtype, float* Y, int
 // Role-split Q4_K GEMM, fp16 X (gemm_split.hip); type, alignment and the
 // 32-bit offset bounds already validated.
 int gemm_q4k_split(const void* w, const void* X, float* Y, int64_t M, int64_t N, int64_t K, hipStream_t st);
+// Q4_K GEMM with the activation fragments loaded into registers from X
+// packed in fragment order, fp16 X (gemm_xr.hip): the preconditions of
+// gemm_q4k_split plus M >= 256 and a 16-byte-aligned workspace of
+// gemm_q4k_xr_workspace(M, K) bytes (the packed X).
+int64_t gemm_q4k_xr_workspace(int64_t M, int64_t K);
+int gemm_q4k_xr(const void* w, const void* X, float* Y, int64_t M, int64_t N, int64_t K, void* ws, hipStream_t st);
 // Q6_K / Q8_0 GEMM, every M (gemm_kq.hip); pointers, alignment, x_dtype and
 // M, N > 0 already validated.
 int gemm_kq(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, int64_t N, int64_t K, int32_t type,
             hipStream_t st);
+// ws / ws_bytes: the caller's workspace (may be null / 0: the kernels that
+// need one are then not chosen, and variant 5 is refused).
 int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, int64_t N, int64_t K,
-                  int32_t type, int32_t variant, hipStream_t st);
+                  int32_t type, int32_t variant, void* ws, size_t ws_bytes, hipStream_t st);
 
 }  // namespace vb

@@ -148,7 +148,7 @@ def gemv(w: QTensor, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.
 
 X_F32 = 0
 X_F16 = 1
-GEMM_AUTO, GEMM_SKINNY, GEMM_TILED, GEMM_SPLIT, GEMM_KSPLIT = 0, 1, 2, 3, 4
+GEMM_AUTO, GEMM_SKINNY, GEMM_TILED, GEMM_SPLIT, GEMM_KSPLIT, GEMM_XREG = 0, 1, 2, 3, 4, 5
 
 
 def gemm(w: QTensor, x: torch.Tensor, out: torch.Tensor | None = None,
@@ -168,6 +168,14 @@ def gemm(w: QTensor, x: torch.Tensor, out: torch.Tensor | None = None,
         out = torch.empty((m, w.rows), dtype=torch.float32, device=w.device)
     _check_out(out, m * w.rows, w.device, "gemm")
     xdt = X_F16 if x.dtype == torch.float16 else X_F32
+    lib = _lib.load()
+    nb = int(lib.vb_gemm_workspace(m, w.rows, w.k, w.qtype, xdt, variant))
+    if nb > 0:
+        # the packed-X kernel's workspace, from torch's caching allocator
+        ws = torch.empty(nb, dtype=torch.uint8, device=w.device)
+        _lib.call("vb_gemm_ws", w.ptr(), x.data_ptr(), xdt, out.data_ptr(), m, w.rows, w.k, w.qtype,
+                  variant, ws.data_ptr(), nb, _stream())
+        return out
     _lib.call("vb_gemm", w.ptr(), x.data_ptr(), xdt, out.data_ptr(), m, w.rows, w.k, w.qtype,
               variant, _stream())
     return out
