@@ -86,6 +86,11 @@ def parse():
     p.add_argument("--counter-table", nargs="+", metavar="CSV",
                    help="per-kernel means of every counter in rocprofv3 counter_collection.csv files, "
                         "as a markdown table, with the MFMA and traffic figures derived from them")
+    p.add_argument("--floor", action="store_true",
+                   help="one-launch floor table for the headline shape (same protocol: rotating weight copies, "
+                        "128-launch graph replays): the GEMV beside a read-only probe with its launch shape and "
+                        "loads (vb_stream_read, several rings), torch's reduction and copy over the same bytes, "
+                        "and a one-workgroup launch; one JSON line each on stderr")
     p.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                    help="turn the counter_collection.csv files of two --pmc-pass runs (FETCH_SIZE, "
                         "WRITE_SIZE) into " + TRAFFIC_FILE)
@@ -743,6 +748,63 @@ def load_traffic():
         return None
 
 
+def run_floor(steps, warmup):
+    """The headline GEMV (14336 x 4096 Q4_K) and what one launch over the same
+    33 MB costs without the GEMV's arithmetic, all under the bench protocol
+    (16 rotating weight copies, graphs of 128 launches, HIP events on the
+    replay stream):
+      * vb_stream_read: the GEMV's grid (256 workgroups of 8 waves, 7 rows
+        per wave) and row-contiguous non-temporal loads, nothing computed;
+        ring 3 is the GEMV's schedule, ring 0 issues a wave's 7 rows at once;
+      * torch.sum over the copy viewed as int32 (a vendor reduction kernel);
+      * torch copy_ of the copy into a second buffer (reads and writes 33 MB);
+      * vb_stream_read of one row (one workgroup): the launch cost alone."""
+    import torch
+    from vibeblade_amd import _lib, ggml
+    qtype, n, k = ggml.GGML_TYPE_Q4_K, 14336, 4096
+    rb = ggml.row_bytes(qtype, k)
+    ab = alg_bytes_gemv(qtype, n, k)
+    tm, copies, x, ys = time_gemv(qtype, n, k, steps, warmup, NCOPIES)
+    lib = _lib.load()
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    rows = [("GEMV (vb_gemv, the headline kernel)", tm)]
+
+    def probe(ring, nrows):
+        def mk(c):
+            def f(s):
+                rc = lib.vb_stream_read(c.ptr(), nrows, rb, ring, sink.data_ptr(), s)
+                if rc != 0:
+                    _lib.check("vb_stream_read", rc)
+            return f
+        return time_launches([mk(c) for c in copies], steps, warmup)
+
+    for ring in (3, 1, 2, 4, 6, 0):
+        what = "all 7 rows of a wave at once" if ring == 0 else f"ring {ring}"
+        rows.append((f"read-only probe, GEMV shape and loads, {what}", probe(ring, n)))
+    views = [c.data.reshape(-1).view(torch.int32) for c in copies]
+    out = torch.empty((), dtype=torch.int64, device="cuda")
+
+    def red(v):
+        def f(s):
+            torch.sum(v, dim=0, dtype=torch.int64, out=out)
+        return f
+    rows.append(("torch.sum over the copy (int32 view)", time_launches([red(v) for v in views], steps, warmup)))
+    dst = torch.empty_like(views[0])
+
+    def cp(v):
+        def f(s):
+            dst.copy_(v)
+        return f
+    rows.append(("torch copy_ of the copy (reads + writes 33 MB)", time_launches([cp(v) for v in views], steps,
+                                                                                   warmup)))
+    rows.append(("one-workgroup launch (vb_stream_read of 1 row)", probe(3, 1)))
+    for name, t in rows:
+        gbs = ab / (t.ms * 1e-3) / 1e9
+        emit({"floor": name, "us_per_launch": t.us(), "GB/s_of_33.1MB": round(gbs, 1),
+              "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "launches": t.launches})
+    return rows
+
+
 def emit(d):
     print(json.dumps(d), file=sys.stderr, flush=True)
 
@@ -856,6 +918,12 @@ def main():
         return
     if args.pmc_pass:
         pmc_pass(args.pmc_pass)
+        return
+    if args.floor:
+        import torch
+        from vibeblade_amd import _lib
+        _lib.init(0)
+        run_floor(args.steps, args.warmup)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "

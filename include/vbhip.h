@@ -161,6 +161,18 @@ int64_t vb_gemm_workspace(int64_t m, int64_t n, int64_t k, int32_t ggml_type, in
 int vb_gemm_ws(const void* w, const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n, int64_t k,
                int32_t ggml_type, int32_t variant, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- measurement utility ----------------------------------------------
+ * Reads n rows of row_bytes (a multiple of 16, at most 4096) with the launch
+ * shape and load pattern of the short-row Q4_K GEMV (one 8-wave workgroup
+ * per CU slot, n / (CUs x 8) rows per wave, contiguous 16-byte
+ * non-temporal pieces per row; `ring` rows loaded ahead of the row being
+ * consumed, as the GEMV's ring of 3; 0 = all of a wave's rows at once) and
+ * computes nothing from them: the time one launch
+ * needs to read what the GEMV reads.  sink: 4 bytes of device memory the
+ * kernel may write (it keeps the loads in the program).  No counterpart in
+ * the reference: it exists for the bench's floor table. */
+int vb_stream_read(const void* w, int64_t n, int64_t row_bytes, int32_t ring, uint32_t* sink, void* stream);
+
 /* ---- TurboSparse activation-sparse FFN, one token ------------------------
  * y[h] = sum_{r < n_active} act(g_r, u_r) * Wd[:, active[r]] with
  * g_r = Wg[active[r], :] . x, u_r = Wu[active[r], :] . x; only the rows of

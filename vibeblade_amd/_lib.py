@@ -40,6 +40,7 @@ SIGNATURES = {
     "vb_gemv": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i32, _vp]),
     "vb_gemm": (ctypes.c_int, [_vp, _vp, _i32, _vp, _i64, _i64, _i64, _i32, _i32, _vp]),
     "vb_gemm_workspace": (_i64, [_i64, _i64, _i64, _i32, _i32, _i32]),
+    "vb_stream_read": (ctypes.c_int, [_vp, _i64, _i64, _i32, _vp, _vp]),
     "vb_gemm_ws": (ctypes.c_int, [_vp, _vp, _i32, _vp, _i64, _i64, _i64, _i32, _i32, _vp, _sz, _vp]),
     "vb_sparse_ffn_workspace": (_i64, [_i64, _i64, _i32, _i32]),
     "vb_sparse_ffn": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _vp, _i64, _i64, _i32,
