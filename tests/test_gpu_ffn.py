@@ -181,14 +181,18 @@ def test_topk_indices(n, k):
     assert np.array_equal(got, want)
 
 
-def moe_weights(e_n, h, i, seed, qtype=Q4K):
+def moe_weights(e_n, h, i, seed, qtype=Q4K, down_type=None):
+    """e_n experts, gate/up of qtype and down of down_type (default qtype)."""
     gen = torch.Generator(device="cuda").manual_seed(seed)
-    mk = (lambda w: QTensor.quantize(w, qtype)) if qtype == Q4K else as_qtensor
+    down_type = qtype if down_type is None else down_type
+
+    def mk(t):
+        return as_qtensor if t == ggml.GGML_TYPE_F32 else (lambda w: QTensor.quantize(w, t))
     gates, ups, downs = [], [], []
     for _ in range(e_n):
-        gates.append(mk(torch.randn((i, h), generator=gen, device="cuda") * 0.02))
-        ups.append(mk(torch.randn((i, h), generator=gen, device="cuda") * 0.02))
-        downs.append(mk(torch.randn((h, i), generator=gen, device="cuda") * 0.02))
+        gates.append(mk(qtype)(torch.randn((i, h), generator=gen, device="cuda") * 0.02))
+        ups.append(mk(qtype)(torch.randn((i, h), generator=gen, device="cuda") * 0.02))
+        downs.append(mk(down_type)(torch.randn((h, i), generator=gen, device="cuda") * 0.02))
     return gates, ups, downs
 
 
@@ -250,6 +254,69 @@ def test_moe_small_invariants():
     # routing-only entry point agrees
     ridx, rw = moe_route(torch.from_numpy(logits).cuda(), topk)
     assert np.array_equal(ridx.cpu().numpy(), idx.cpu().numpy())
+
+
+Q6K, Q80 = ggml.GGML_TYPE_Q6_K, ggml.GGML_TYPE_Q8_0
+
+
+def test_moe_mixed_config_shape():
+    """8 experts, Q4_K gate/up (14336x4096) and Q6_K down (4096x14336), as a
+    GGUF MoE layer stores ffn_down_exps (cpp/src/fast_model.cpp:552-572 takes
+    each matrix with its own type); 16 tokens, top-2."""
+    e_n, h, i, t, topk = 8, 4096, 14336, 16, 2
+    gates, ups, downs = moe_weights(e_n, h, i, 15, Q4K, Q6K)
+    assert gates[0].qtype == Q4K and downs[0].qtype == Q6K
+    rng = np.random.default_rng(19)
+    x = rng.standard_normal((t, h)).astype(np.float32)
+    logits = rng.standard_normal((t, e_n)).astype(np.float32)
+    y, idx, w = moe_grouped_ffn(gates, ups, downs, torch.from_numpy(x), torch.from_numpy(logits), topk)
+    want, widx, ww = moe_oracle(gates, ups, downs, x, logits, topk)
+    assert np.array_equal(idx.cpu().numpy(), widx)
+    assert np.allclose(w.cpu().numpy(), ww, rtol=1e-5, atol=1e-6)
+    assert O.rel_l2(y.cpu().numpy(), want) <= 5e-3
+
+
+@pytest.mark.parametrize("gu,dn", [(Q4K, Q6K), (Q4K, Q80), (Q6K, Q4K), (Q80, Q6K), (Q6K, Q6K), (Q80, Q80),
+                                   (Q6K, Q80)])
+def test_moe_mixed_types(gu, dn):
+    """Every gate/up x down pairing of Q4_K / Q6_K / Q8_0 the entry takes,
+    with the routed slot counts the grouped kernels split at: a spread
+    routing, one expert with more than 16 slots, and an idle expert."""
+    e_n, h, i, t, topk = 5, 512, 768, 21, 2
+    gates, ups, downs = moe_weights(e_n, h, i, 30 + gu + dn, gu, dn)
+    rng = np.random.default_rng(gu * 7 + dn)
+    x = rng.standard_normal((t, h)).astype(np.float32)
+    for lg in (rng.standard_normal((t, e_n)).astype(np.float32),
+               np.where(np.arange(e_n) == 1, 3.0, np.where(np.arange(e_n) == 4, 2.0, -1.0))
+               .astype(np.float32)[None, :].repeat(t, 0)):
+        y, idx, _ = moe_grouped_ffn(gates, ups, downs, x, lg, topk)
+        want, widx, _ = moe_oracle(gates, ups, downs, x, lg, topk)
+        assert np.array_equal(idx.cpu().numpy(), widx)
+        assert O.rel_l2(y.cpu().numpy(), want) <= 5e-3, (gu, dn)
+    # the same-type entry is the two-type entry with equal types
+    if gu == dn:
+        from vibeblade_amd import _lib
+        import ctypes
+        idx2 = torch.empty((t, topk), dtype=torch.int32, device="cuda")
+        w2 = torch.empty((t, topk), dtype=torch.float32, device="cuda")
+        y2 = torch.empty((t, h), dtype=torch.float32, device="cuda")
+        xt = torch.from_numpy(x).cuda()
+        lt = torch.from_numpy(lg).cuda()
+        ws = torch.empty(_lib.load().vb_moe_workspace(t, topk, h, i), dtype=torch.uint8, device="cuda")
+        arr = ctypes.c_void_p * e_n
+        ptrs = [ctypes.cast(arr(*[q.ptr() for q in m]), ctypes.c_void_p) for m in (gates, ups, downs)]
+        _lib.call("vb_moe_grouped_ffn", *ptrs, e_n, xt.data_ptr(), t, lt.data_ptr(), topk, y2.data_ptr(),
+                  idx2.data_ptr(), w2.data_ptr(), h, i, gu, ws.data_ptr(), ws.numel(),
+                  torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert torch.equal(y2, y)
+
+
+def test_moe_type_mix_rejected():
+    from vibeblade_amd._lib import VBError
+    gates, ups, downs = moe_weights(2, 256, 256, 3, Q4K, ggml.GGML_TYPE_F32)
+    with pytest.raises(VBError, match="gate/up and down each"):
+        moe_grouped_ffn(gates, ups, downs, np.zeros((1, 256), np.float32), np.zeros((1, 2), np.float32), 1)
 
 
 def test_moe_f32_experts():

@@ -58,6 +58,8 @@ SIGNATURES = {
     "vb_moe_workspace": (_i64, [_i32, _i32, _i64, _i64]),
     "vb_moe_grouped_ffn": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _i64,
                                           _i64, _i32, _vp, _sz, _vp]),
+    "vb_moe_grouped_ffn_types": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _vp, _vp, _vp,
+                                                _i64, _i64, _i32, _i32, _vp, _sz, _vp]),
     "vb_moe_route": (ctypes.c_int, [_vp, _i32, _i32, _i32, _vp, _vp, _vp]),
     "vb_activation": (ctypes.c_int, [_vp, _vp, _i64, _i32, _vp]),
     "vb_rms_norm": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp]),

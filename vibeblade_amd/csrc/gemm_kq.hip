@@ -43,6 +43,10 @@ constexpr uint32_t KQ_X_NONE = 0x80000000u;  // lane offset of an absent activat
 constexpr int KQ_X_F32 = 0;
 constexpr int KQ_X_F16 = 1;
 
+struct KqExperts {
+    const uint8_t* p[MOE_KQ_MAX_EXPERTS];
+};
+
 template <int TYPE> struct Kq;
 
 // Q4_K (cpp/src/dequant.cpp:258-301; header d, dmin, scales[12] @0, qs[128]
@@ -326,6 +330,125 @@ __global__ void __launch_bounds__(64 * KQ_WAVES) gemm_kq_kernel(const uint8_t* _
     }
 }
 
+// Expert-grouped form for the MoE FFN (moe.hip): workgroup (n-tile, expert
+// e) walks expert e's routed slots (elist[eoff[e] .. eoff[e + 1])) 16 at a
+// time, with the same k split, decoders and fixed-order reduction as
+// gemm_kq_kernel.  Activation rows are gathered: slot q reads row q / xdiv of
+// X (fp16; xdiv = topk for the tokens' rows, 1 for the hidden rows of the
+// slots).  NMAT = 2: gate and up weights over the same rows, written as fp16
+// silu(g) * u into hout[slot][n]; NMAT = 1: fp32 into fout[slot][n].
+template <int TYPE, int NMAT, int NCG, int RD>
+__global__ void __launch_bounds__(64 * KQ_WAVES) moe_kq_kernel(KqExperts w0, KqExperts w1, uint32_t wbytes,
+                                                               const uint8_t* __restrict__ X, uint32_t xbytes,
+                                                               int xdiv, const int32_t* __restrict__ eoff,
+                                                               const int32_t* __restrict__ elist, int N, int K,
+                                                               uint32_t rb, _Float16* __restrict__ hout,
+                                                               float* __restrict__ fout) {
+    using T = Kq<TYPE>;
+    extern __shared__ float4_t kq_red[];  // [wave][NMAT * NCG][lane]
+    const int e = static_cast<int>(blockIdx.y);
+    const int base = eoff[e], cnt = eoff[e + 1] - base;
+    if (cnt <= 0) return;
+    const int32_t* slots = elist + base;
+    const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int n0 = static_cast<int>(blockIdx.x) * 16 * NCG;
+    const int nsteps = K / KQ_STEP;
+    const int s_beg = __builtin_amdgcn_readfirstlane((wave * nsteps) / KQ_WAVES);
+    const int s_end = __builtin_amdgcn_readfirstlane(((wave + 1) * nsteps) / KQ_WAVES);
+    __amdgpu_buffer_rsrc_t wr[NMAT];
+    wr[0] = make_rsrc(w0.p[e], wbytes);
+    if constexpr (NMAT == 2) wr[1] = make_rsrc(w1.p[e], wbytes);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(X, xbytes);
+    uint32_t rowoff[NCG];
+#pragma unroll
+    for (int cg = 0; cg < NCG; cg++) {
+        int n = n0 + 16 * cg + j;
+        n = n < N ? n : N - 1;
+        rowoff[cg] = static_cast<uint32_t>(n) * rb;
+    }
+    constexpr uint32_t GSTR = T::kBlockLane ? 32u : 8u, KSTR = T::kBlockLane ? 8u : 32u;
+    const KqConsts kc = kq_consts();
+    const int last = s_end - 1;
+    for (int m0 = 0; m0 < cnt; m0 += 16) {
+        const int nrow = cnt - m0 < 16 ? cnt - m0 : 16;
+        const uint32_t xoff = j < nrow ? (static_cast<uint32_t>(slots[m0 + j] / xdiv) * static_cast<uint32_t>(K) +
+                                          GSTR * static_cast<uint32_t>(g)) * 2u
+                                       : KQ_X_NONE;
+        float4_t acc[NMAT][NCG];
+#pragma unroll
+        for (int mt = 0; mt < NMAT; mt++)
+#pragma unroll
+            for (int cg = 0; cg < NCG; cg++) acc[mt][cg] = float4_t{0.f, 0.f, 0.f, 0.f};
+        typename T::Raw raw[RD][NMAT][NCG];
+        if (s_end > s_beg) {
+#pragma unroll
+            for (int r = 0; r < RD; r++) {
+                const int step = s_beg + r < last ? s_beg + r : last;
+#pragma unroll
+                for (int mt = 0; mt < NMAT; mt++)
+#pragma unroll
+                    for (int cg = 0; cg < NCG; cg++) T::issue(wr[mt], rowoff[cg], step, g, raw[r][mt][cg]);
+            }
+            for (int it = s_beg; it < s_end; it += RD) {
+#pragma unroll
+                for (int r = 0; r < RD; r++) {
+                    const int step = it + r;
+                    if (step >= s_end) break;  // uniform
+                    const uint32_t so = static_cast<uint32_t>(step) * KQ_STEP * 2u;
+                    Frag af[4];
+#pragma unroll
+                    for (int ks = 0; ks < 4; ks++) {
+                        const u32x4 v = buf_ld128(xr, xoff, so + KSTR * 2u * ks);
+                        af[ks].u[0] = v.x; af[ks].u[1] = v.y; af[ks].u[2] = v.z; af[ks].u[3] = v.w;
+                    }
+                    const int nxt = (step + RD) < last ? step + RD : last;
+#pragma unroll
+                    for (int mt = 0; mt < NMAT; mt++)
+#pragma unroll
+                        for (int cg = 0; cg < NCG; cg++) {
+                            Frag bf[4];
+                            T::decode(raw[r][mt][cg], rowoff[cg], step, g, kc, bf);
+                            T::issue(wr[mt], rowoff[cg], nxt, g, raw[r][mt][cg]);
+#pragma unroll
+                            for (int ks = 0; ks < 4; ks++) acc[mt][cg] = mfma16x16x32(af[ks], bf[ks], acc[mt][cg]);
+                        }
+                }
+            }
+        }
+#pragma unroll
+        for (int mt = 0; mt < NMAT; mt++)
+#pragma unroll
+            for (int cg = 0; cg < NCG; cg++) kq_red[(wave * NMAT * NCG + mt * NCG + cg) * 64 + lane] = acc[mt][cg];
+        __syncthreads();
+        for (int q = threadIdx.x; q < NCG * 64; q += 64 * KQ_WAVES) {
+            const int cg = q >> 6, l = q & 63;
+            float4_t s0 = kq_red[cg * 64 + l];
+#pragma unroll
+            for (int v = 1; v < KQ_WAVES; v++) s0 += kq_red[(v * NMAT * NCG + cg) * 64 + l];
+            float4_t s1 = s0;
+            if constexpr (NMAT == 2) {
+                s1 = kq_red[(NCG + cg) * 64 + l];
+#pragma unroll
+                for (int v = 1; v < KQ_WAVES; v++) s1 += kq_red[(v * NMAT * NCG + NCG + cg) * 64 + l];
+            }
+            const int col = n0 + 16 * cg + (l & 15);
+            if (col >= N) continue;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int t = 4 * (l >> 4) + r;
+                if (t >= nrow) continue;
+                const int64_t o = static_cast<int64_t>(slots[m0 + t]) * N + col;
+                if constexpr (NMAT == 2)
+                    hout[o] = static_cast<_Float16>(s0[r] / (1.0f + __expf(-s0[r])) * s1[r]);
+                else
+                    fout[o] = s0[r];
+            }
+        }
+        __syncthreads();  // kq_red is rewritten by the next 16 slots
+    }
+}
+
 template <int TYPE, int XT, int MA, int NCG, int RD>
 void launch_kq(const uint8_t* w, uint32_t wbytes, const uint8_t* X, uint32_t xbytes, float* Y, int M, int N, int K,
                uint32_t rb, hipStream_t st) {
@@ -418,6 +541,43 @@ int gemm_kq(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, 
             launch_kq_m<TYPE_Q8_0, KQ_X_F32>(wb, wby, xb, xby, Y, m, n, k, rbu, st);
     }
     return check_launch("vb_gemm");
+}
+
+// Expert-grouped Q6_K / Q8_0 / Q4_K products for the MoE FFN; the caller
+// (moe.hip) has validated the shapes (K % 128 == 0, 32-bit offsets) and the
+// per-expert pointers.  gate_up: hout = fp16 silu(W0 x) * (W1 x) over
+// rows slot / topk of X (N = i, K = h); else fout = W0 x over rows slot of
+// X (N = h, K = i).
+int moe_kq(int32_t type, bool gate_up, const void* const* w0, const void* const* w1, int n_exp, const void* X,
+           int64_t xbytes, int topk, const int32_t* eoff, const int32_t* elist, int64_t N, int64_t K,
+           _Float16* hout, float* fout, hipStream_t st) {
+    if (n_exp > MOE_KQ_MAX_EXPERTS || K % KQ_STEP != 0) return E_UNSUPPORTED;
+    KqExperts a{}, b{};
+    for (int e = 0; e < n_exp; e++) {
+        a.p[e] = static_cast<const uint8_t*>(w0[e]);
+        b.p[e] = gate_up ? static_cast<const uint8_t*>(w1[e]) : a.p[e];
+    }
+    const int64_t rb = row_bytes(type, K);
+    const uint32_t wbytes = static_cast<uint32_t>((N * rb + 3) & ~int64_t(3));
+    const uint8_t* xb = static_cast<const uint8_t*>(X);
+    const int n = static_cast<int>(N), k = static_cast<int>(K);
+    const uint32_t xby = static_cast<uint32_t>(xbytes), rbu = static_cast<uint32_t>(rb);
+    auto go = [&](auto kernel, int ncg, int nmat) {
+        const dim3 grid(static_cast<uint32_t>((N + 16 * ncg - 1) / (16 * ncg)), static_cast<uint32_t>(n_exp));
+        const size_t lds = static_cast<size_t>(KQ_WAVES) * nmat * ncg * 64 * sizeof(float4_t);
+        kernel<<<grid, dim3(64 * KQ_WAVES), lds, st>>>(a, b, wbytes, xb, xby, gate_up ? topk : 1, eoff, elist, n, k,
+                                                       rbu, hout, fout);
+    };
+    if (gate_up) {
+        if (type == TYPE_Q6_K) go(moe_kq_kernel<TYPE_Q6_K, 2, 2, 2>, 2, 2);
+        else if (type == TYPE_Q8_0) go(moe_kq_kernel<TYPE_Q8_0, 2, 2, 2>, 2, 2);
+        else go(moe_kq_kernel<TYPE_Q4_K, 2, 2, 2>, 2, 2);
+    } else {
+        if (type == TYPE_Q6_K) go(moe_kq_kernel<TYPE_Q6_K, 1, 1, 3>, 1, 1);
+        else if (type == TYPE_Q8_0) go(moe_kq_kernel<TYPE_Q8_0, 1, 1, 3>, 1, 1);
+        else go(moe_kq_kernel<TYPE_Q4_K, 1, 1, 3>, 1, 1);
+    }
+    return check_launch("vb_moe_grouped_ffn");
 }
 
 }  // namespace vb

@@ -418,11 +418,15 @@ extern "C" int64_t vb_moe_workspace(int32_t n_tokens, int32_t topk, int64_t h, i
     return static_cast<int64_t>(moe_ws(n_tokens, topk, h, i).total);
 }
 
-extern "C" int vb_moe_grouped_ffn(const void* const* wg, const void* const* wu, const void* const* wd,
-                                  int32_t n_exp, const float* x, int32_t n_tokens, const float* router_logits,
-                                  int32_t topk, float* y, int32_t* out_idx, float* out_w, int64_t h,
-                                  int64_t i, int32_t ggml_type, void* workspace, size_t workspace_bytes,
-                                  void* stream) {
+namespace {
+bool moe_quant_type(int32_t t) { return t == TYPE_Q4_K || t == TYPE_Q6_K || t == TYPE_Q8_0; }
+}  // namespace
+
+extern "C" int vb_moe_grouped_ffn_types(const void* const* wg, const void* const* wu, const void* const* wd,
+                                        int32_t n_exp, const float* x, int32_t n_tokens, const float* router_logits,
+                                        int32_t topk, float* y, int32_t* out_idx, float* out_w, int64_t h, int64_t i,
+                                        int32_t gate_up_type, int32_t down_type, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
     hipStream_t st = as_stream(stream);
     if (n_exp <= 0 || n_exp > MOE_MAX_EXPERTS || topk <= 0 || topk > MOE_MAX_TOPK || topk > n_exp ||
         n_tokens < 0 || static_cast<int64_t>(n_tokens) * topk > MOE_MAX_SLOTS || h <= 0 || i <= 0 || !wg ||
@@ -431,8 +435,10 @@ extern "C" int vb_moe_grouped_ffn(const void* const* wg, const void* const* wu, 
                   MOE_MAX_TOPK, MOE_MAX_SLOTS);
         return E_INVAL;
     }
-    if ((ggml_type != TYPE_Q4_K && ggml_type != TYPE_F32) || h % 256 != 0 || i % 256 != 0) {
-        set_error("vb_moe_grouped_ffn: Q4_K or F32 experts with h, i multiples of 256 are supported");
+    const bool f32 = gate_up_type == TYPE_F32 && down_type == TYPE_F32;
+    if (!(f32 || (moe_quant_type(gate_up_type) && moe_quant_type(down_type))) || h % 256 != 0 || i % 256 != 0) {
+        set_error("vb_moe_grouped_ffn: experts of Q4_K / Q6_K / Q8_0 (gate/up and down each; or F32 throughout) "
+                  "with h, i multiples of 256 are supported (got gate/up %d, down %d)", gate_up_type, down_type);
         return E_UNSUPPORTED;
     }
     if (n_tokens == 0) return OK;
@@ -477,28 +483,41 @@ extern "C" int vb_moe_grouped_ffn(const void* const* wg, const void* const* wu, 
     int rc = check_launch("vb_moe_grouped_ffn");
     if (rc != OK) return rc;
     // 2, 3. experts
-    if (ggml_type == TYPE_Q4_K) {
-        const int64_t rb_gu = row_bytes(ggml_type, h), rb_d = row_bytes(ggml_type, i);
-        if (i * rb_gu >= (int64_t(1) << 32) || h * rb_d >= (int64_t(1) << 32)) {
+    if (!f32) {
+        const int64_t rb_gu = row_bytes(gate_up_type, h), rb_d = row_bytes(down_type, i);
+        if (i * rb_gu + 4 >= (int64_t(1) << 32) || h * rb_d + 4 >= (int64_t(1) << 32)) {
             set_error("vb_moe_grouped_ffn: expert tensors too large for 32-bit offsets");
             return E_INVAL;
         }
         _Float16* hb16 = reinterpret_cast<_Float16*>(hbuf);
-        const dim3 gu(static_cast<uint32_t>((i + skinny::ROWS - 1) / skinny::ROWS), n_exp);
-        const dim3 dn(static_cast<uint32_t>((h + skinny::ROWS - 1) / skinny::ROWS), n_exp);
-        moe_gate_up_q4k<MOE_WAVES><<<gu, dim3(64 * MOE_WAVES), skinny::lds_bytes<MOE_WAVES>(), st>>>(
-            pg, pu, xh, eoff, elist, topk, static_cast<int>(h), static_cast<int>(i), static_cast<int>(rb_gu),
-            static_cast<uint32_t>(i * rb_gu), static_cast<uint32_t>(nx * 2), hb16);
-        if ((rc = check_launch("vb_moe_grouped_ffn")) != OK) return rc;
-        moe_down_q4k<MOE_WAVES><<<dn, dim3(64 * MOE_WAVES), skinny::lds_bytes<MOE_WAVES>(), st>>>(
-            pd, hb16, eoff, elist, static_cast<int>(h), static_cast<int>(i), static_cast<int>(rb_d),
-            static_cast<uint32_t>(h * rb_d), static_cast<uint32_t>(slots * i * 2), obuf);
+        // Q4_K on the skinny tiles (one activation fragment per 16 slots
+        // serves four 16-row column groups); Q6_K / Q8_0 on the expert-grouped
+        // K-split kernel (gemm_kq.hip), gate/up with the same SwiGLU epilogue
+        if (gate_up_type == TYPE_Q4_K) {
+            const dim3 gu(static_cast<uint32_t>((i + skinny::ROWS - 1) / skinny::ROWS), n_exp);
+            moe_gate_up_q4k<MOE_WAVES><<<gu, dim3(64 * MOE_WAVES), skinny::lds_bytes<MOE_WAVES>(), st>>>(
+                pg, pu, xh, eoff, elist, topk, static_cast<int>(h), static_cast<int>(i), static_cast<int>(rb_gu),
+                static_cast<uint32_t>(i * rb_gu), static_cast<uint32_t>(nx * 2), hb16);
+            if ((rc = check_launch("vb_moe_grouped_ffn")) != OK) return rc;
+        } else if ((rc = moe_kq(gate_up_type, true, wg, wu, n_exp, xh, nx * 2, topk, eoff, elist, i, h, hb16, nullptr,
+                                st)) != OK) {
+            return rc;
+        }
+        if (down_type == TYPE_Q4_K) {
+            const dim3 dn(static_cast<uint32_t>((h + skinny::ROWS - 1) / skinny::ROWS), n_exp);
+            moe_down_q4k<MOE_WAVES><<<dn, dim3(64 * MOE_WAVES), skinny::lds_bytes<MOE_WAVES>(), st>>>(
+                pd, hb16, eoff, elist, static_cast<int>(h), static_cast<int>(i), static_cast<int>(rb_d),
+                static_cast<uint32_t>(h * rb_d), static_cast<uint32_t>(slots * i * 2), obuf);
+        } else if ((rc = moe_kq(down_type, false, wd, nullptr, n_exp, hb16, slots * i * 2, topk, eoff, elist, h, i,
+                                nullptr, obuf, st)) != OK) {
+            return rc;
+        }
     } else {
         const dim3 gu_grid(static_cast<uint32_t>((i + 15) / 16), n_exp), dn_grid(static_cast<uint32_t>((h + 15) / 16), n_exp);
         moe_gate_up_kernel<TYPE_F32><<<gu_grid, dim3(256), 0, st>>>(pg, pu, x, eoff, elist, topk, h, i,
-                                                                    row_bytes(ggml_type, h), hbuf);
+                                                                    row_bytes(TYPE_F32, h), hbuf);
         if ((rc = check_launch("vb_moe_grouped_ffn")) != OK) return rc;
-        moe_down_kernel<TYPE_F32><<<dn_grid, dim3(256), 0, st>>>(pd, hbuf, eoff, elist, h, i, row_bytes(ggml_type, i),
+        moe_down_kernel<TYPE_F32><<<dn_grid, dim3(256), 0, st>>>(pd, hbuf, eoff, elist, h, i, row_bytes(TYPE_F32, i),
                                                                  obuf);
     }
     if ((rc = check_launch("vb_moe_grouped_ffn")) != OK) return rc;
@@ -506,6 +525,15 @@ extern "C" int vb_moe_grouped_ffn(const void* const* wg, const void* const* wu, 
     moe_combine_routed<<<dim3(static_cast<uint32_t>(n_tokens), static_cast<uint32_t>((h + 1023) / 1024)), dim3(256), 0,
                          st>>>(obuf, ridx, rw, topk, h, y, out_idx, out_w);
     return check_launch("vb_moe_grouped_ffn");
+}
+
+extern "C" int vb_moe_grouped_ffn(const void* const* wg, const void* const* wu, const void* const* wd,
+                                  int32_t n_exp, const float* x, int32_t n_tokens, const float* router_logits,
+                                  int32_t topk, float* y, int32_t* out_idx, float* out_w, int64_t h,
+                                  int64_t i, int32_t ggml_type, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+    return vb_moe_grouped_ffn_types(wg, wu, wd, n_exp, x, n_tokens, router_logits, topk, y, out_idx, out_w, h, i,
+                                    ggml_type, ggml_type, workspace, workspace_bytes, stream);
 }
 
 namespace vb {

@@ -306,19 +306,21 @@ def moe_route(logits: torch.Tensor, topk: int):
 
 
 def moe_grouped_ffn(gates, ups, downs, x: torch.Tensor, logits: torch.Tensor, topk: int):
-    """Top-k MoE over experts (lists of QTensors: gate/up i x h, down h x i).
-    Returns (y (T, h) fp32, indices (T, topk) int32, weights (T, topk) fp32)."""
+    """Top-k MoE over experts (lists of QTensors: gate/up i x h, down h x i;
+    gate/up of one ggml type, down of the same or another).  Returns (y (T, h) fp32, indices (T, topk) int32, weights (T, topk) fp32)."""
     import ctypes
     n_exp = len(gates)
     if not (len(ups) == len(downs) == n_exp) or n_exp == 0:
         raise ValueError("moe_grouped_ffn: need the same number of gate/up/down experts")
     g0 = gates[0]
-    h, i, qtype = g0.k, g0.rows, g0.qtype
+    h, i = g0.k, g0.rows
+    gu_type, dn_type = g0.qtype, downs[0].qtype
     for e in range(n_exp):
         if gates[e].shape != (i, h) or ups[e].shape != (i, h) or downs[e].shape != (h, i):
             raise ValueError(f"moe_grouped_ffn: expert {e} has inconsistent shapes")
-        if not (gates[e].qtype == ups[e].qtype == downs[e].qtype == qtype):
-            raise ValueError("moe_grouped_ffn: experts must share one ggml type")
+        if not (gates[e].qtype == ups[e].qtype == gu_type and downs[e].qtype == dn_type):
+            raise ValueError("moe_grouped_ffn: every expert's gate/up must share one ggml type, "
+                             "and every expert's down another (or the same)")
     dev = g0.device
     x = _as_f32_dev(x, dev)
     if x.dim() == 1:
@@ -337,9 +339,9 @@ def moe_grouped_ffn(gates, ups, downs, x: torch.Tensor, logits: torch.Tensor, to
         raise ValueError("moe_grouped_ffn: bad shape")
     ws = _workspace(nbytes, dev)
     vp = ctypes.c_void_p
-    _lib.call("vb_moe_grouped_ffn", ctypes.cast(pg, vp), ctypes.cast(pu, vp), ctypes.cast(pd, vp), n_exp,
-              x.data_ptr(), t, logits.data_ptr(), topk,
-              y.data_ptr(), idx.data_ptr(), w.data_ptr(), h, i, qtype, ws.data_ptr(), ws.numel(), _stream())
+    _lib.call("vb_moe_grouped_ffn_types", ctypes.cast(pg, vp), ctypes.cast(pu, vp), ctypes.cast(pd, vp), n_exp,
+              x.data_ptr(), t, logits.data_ptr(), topk, y.data_ptr(), idx.data_ptr(), w.data_ptr(), h, i,
+              gu_type, dn_type, ws.data_ptr(), ws.numel(), _stream())
     return y, idx, w
 
 
