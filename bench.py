@@ -79,10 +79,13 @@ def parse():
                    help="comma list of extra workloads: " + ",".join(EXTRA_ALL))
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--pmc-pass", nargs="?", const="gemv", choices=["gemv", "lmhead", "down", "gemm8", "gemm512"],
-                   help="eager launches for rocprofv3 --pmc: 32 headline GEMVs (gemv) or 16 Q4_K GEMMs "
-                        "14336x4096 at M=8 / 512 (gemm8, gemm512), then a 256 MiB copy (torch.neg) "
-                        "that calibrates FETCH_SIZE / WRITE_SIZE")
+    p.add_argument("--pmc-pass", nargs="?", const="gemv",
+                   choices=["gemv", "lmhead", "down", "gemm8", "gemm512", "down512", "sparse", "moe"],
+                   help="eager launches for rocprofv3 --pmc: 32 headline GEMVs (gemv), 16 Q4_K GEMMs "
+                        "14336x4096 at M=8 / 512 (gemm8, gemm512) or 4096x14336 at M=512 (down512), 16 "
+                        "neuron-major TurboSparse FFN calls (sparse) or 8 MoE calls (moe), each as the timed "
+                        "run launches it, then a 256 MiB copy (torch.neg) that calibrates FETCH_SIZE / "
+                        "WRITE_SIZE")
     p.add_argument("--counter-table", nargs="+", metavar="CSV",
                    help="per-kernel means of every counter in rocprofv3 counter_collection.csv files, "
                         "as a markdown table, with the MFMA and traffic figures derived from them")
@@ -639,16 +642,59 @@ def pmc_pass(workload="gemv"):
             c = copies[i % ncop]
             _lib.check("vb_gemv", lib.vb_gemv(c.ptr(), x.data_ptr(), y.data_ptr(), n, k, qtype, st))
         what = f"{ndisp} GEMV dispatches ({workload})"
+    elif workload == "sparse":
+        from vibeblade_amd.tensor import QTensor, ACT_RELU2
+        h, i = 4096, 14336
+        gen = torch.Generator(device="cuda").manual_seed(SEED + 4)
+        rng = np.random.default_rng(42)
+        q = lambda shape: QTensor.quantize(torch.randn(shape, generator=gen, device="cuda") * 0.02, qtype)
+        copies = [(q((i, h)), q((i, h)), q((i, h)),
+                   torch.from_numpy(np.flatnonzero(rng.random(i) < 0.10).astype(np.int32)).cuda())
+                  for _ in range(NCOPIES)]
+        x = torch.randn(h, generator=gen, device="cuda")
+        y = torch.empty(h, device="cuda")
+        nb = max(lib.vb_sparse_ffn_workspace(h, i, c[3].numel(), 1) for c in copies)
+        ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
+        for j in range(16):
+            g, u, d, s = copies[j % NCOPIES]
+            _lib.check("vb_sparse_ffn", lib.vb_sparse_ffn(g.ptr(), u.ptr(), d.ptr(), 1, x.data_ptr(), s.data_ptr(),
+                                                          s.numel(), ACT_RELU2, y.data_ptr(), h, i, qtype,
+                                                          ws.data_ptr(), ws.numel(), st))
+        what = "16 neuron-major sparse FFN calls"
+    elif workload == "moe":
+        import ctypes
+        from vibeblade_amd.tensor import QTensor
+        e_n, h, i, t, topk = 8, 4096, 14336, 16, 2
+        gen = torch.Generator(device="cuda").manual_seed(SEED + 5)
+        q = lambda shape: QTensor.quantize(torch.randn(shape, generator=gen, device="cuda") * 0.02, qtype)
+        copies = [q((i, h)) for _ in range(2 * e_n)] + [q((h, i)) for _ in range(e_n)]
+        arr = ctypes.c_void_p * e_n
+        pg, pu, pd = (arr(*[c.ptr() for c in copies[a * e_n:(a + 1) * e_n]]) for a in range(3))
+        x = torch.randn((t, h), generator=gen, device="cuda")
+        logits = torch.randn((t, e_n), generator=gen, device="cuda")
+        ws = torch.empty(lib.vb_moe_workspace(t, topk, h, i), dtype=torch.uint8, device="cuda")
+        y = torch.empty((t, h), device="cuda")
+        vp = ctypes.c_void_p
+        for _ in range(8):
+            _lib.check("vb_moe_grouped_ffn", lib.vb_moe_grouped_ffn(
+                ctypes.cast(pg, vp), ctypes.cast(pu, vp), ctypes.cast(pd, vp), e_n, x.data_ptr(), t,
+                logits.data_ptr(), topk, y.data_ptr(), None, None, h, i, qtype, ws.data_ptr(), ws.numel(), st))
+        what = "8 MoE calls"
     else:
         m = 8 if workload == "gemm8" else 512
+        if workload == "down512":
+            n, k = 4096, 14336
         gen = torch.Generator(device="cuda").manual_seed(SEED + m)
         copies = make_copies(qtype, n, k, NCOPIES, gen)
         xh = gemm_inputs(m, k, gen)
         y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        nb = int(lib.vb_gemm_workspace(m, n, k, qtype, 1, 0))
+        ws = torch.empty(max(nb, 16), dtype=torch.uint8, device="cuda")
         for i in range(16):
             c = copies[i % NCOPIES]
-            _lib.check("vb_gemm", lib.vb_gemm(c.ptr(), xh.data_ptr(), 1, y.data_ptr(), m, n, k, qtype, 0, st))
-        what = f"16 GEMM dispatches at M={m}"
+            _lib.check("vb_gemm_ws", lib.vb_gemm_ws(c.ptr(), xh.data_ptr(), 1, y.data_ptr(), m, n, k, qtype, 0,
+                                                    ws.data_ptr(), nb, st))
+        what = f"16 GEMM dispatches at M={m}, {n}x{k}"
     torch.cuda.synchronize()
     del copies
     torch.cuda.empty_cache()

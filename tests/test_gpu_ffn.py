@@ -114,14 +114,15 @@ def test_sparse_layouts_agree():
     assert O.rel_l2(y0, y1) <= 0.2
 
 
-@pytest.mark.parametrize("h,i,fused_env,one", [(4096, 4096, "0", False), (8192, 2048, None, False),
-                                               (4096, 512, None, True)])
-def test_sparse_neuron_major_paths(knob, h, i, fused_env, one):
-    """Layout 1 on each of its paths: the fused gate/up/down kernel (h <= 4096),
-    the gathered GEMV + down-rows launches (forced with VB_SPARSE_FUSED=0, and
-    for h > 4096), and a single active neuron on the fused path."""
-    if fused_env is not None:
-        knob("VB_SPARSE_FUSED", fused_env)
+@pytest.mark.parametrize("h,i,env,one", [(4096, 4096, ("VB_SPARSE_FUSED", "0"), False), (8192, 2048, None, False),
+                                         (4096, 512, None, True), (768, 2304, None, False)])
+def test_sparse_neuron_major_paths(knob, h, i, env, one):
+    """Layout 1 on each of its paths: the fused gate/up/down kernel (h <= 4096,
+    also at h = 768, 12 units of a 64-lane wave), the gathered GEMV +
+    down-rows launches (forced with VB_SPARSE_FUSED=0, and for h > 4096), and
+    a single active neuron on the fused path."""
+    if env is not None:
+        knob(*env)
     gq, uq, dq, gd, ud, dd = ffn_weights(h, i, Q4K, 17, DOWN_NEURON_MAJOR)
     rng = np.random.default_rng(8)
     s = np.array([137], np.int32) if one else np.flatnonzero(rng.random(i) < 0.1).astype(np.int32)
