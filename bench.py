@@ -724,12 +724,16 @@ def _counter_means(path, counter):
 
 
 def counter_table(paths):
-    """Markdown table of per-kernel mean counter values (per dispatch) over
-    rocprofv3 counter_collection.csv files, plus derived figures:
+    """Markdown table of per-dispatch mean counter values of the library's
+    kernels (namespace vb) over rocprofv3 counter_collection.csv files, one
+    row per counter and one column per kernel, plus derived rows:
     MFMA FLOPs = SQ_INSTS_VALU_MFMA_MOPS_F16 x 512 (the counter counts units
-    of 512 FLOPs), MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8
-    XCDs x 256 CUs x 4 SIMDs), and FETCH_SIZE / WRITE_SIZE scaled by the calibration
-    copy (CALIB_BYTES read and written) when it is in the same file."""
+    of 512 FLOPs); MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8
+    XCDs x 256 CUs x 4 SIMDs); wait / issue shares of the wave lifetime
+    (SQ_WAIT_ANY, SQ_ACTIVE_INST_ANY over SQ_WAVE_CYCLES); lanes per VALU
+    instruction (SQ_THREAD_CYCLES_VALU / SQ_ACTIVE_INST_VALU); and FETCH_SIZE /
+    WRITE_SIZE scaled by the calibration copy (CALIB_BYTES read and written)
+    when it is in the same file."""
     import csv
     rows = {}
     for path in paths:
@@ -740,24 +744,52 @@ def counter_table(paths):
             for name, (v, cnt) in _counter_means(path, c).items():
                 rows.setdefault(name, {})[c] = (v, cnt)
     calib = {c: v for name, d in rows.items() if "neg_kernel" in name for c, (v, _) in d.items()}
-    names = sorted({c for d in rows.values() for c in d})
-    print("| Kernel | dispatches | " + " | ".join(names) + " | derived |")
-    print("|---" * (len(names) + 3) + "|")
-    for kname, d in sorted(rows.items(), key=lambda t: t[0]):
-        short = kname.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0][:80]
-        nd = max(cnt for _, cnt in d.values())
-        cells = [f"{d[c][0]:.4g}" if c in d else "" for c in names]
-        der = []
-        if "SQ_INSTS_VALU_MFMA_MOPS_F16" in d:
-            der.append(f"MFMA f16 {d['SQ_INSTS_VALU_MFMA_MOPS_F16'][0] * 512 / 1e9:.3f} GFLOP")
-        if "SQ_VALU_MFMA_BUSY_CYCLES" in d and "GRBM_GUI_ACTIVE" in d:
-            # GRBM_GUI_ACTIVE comes summed over the 8 XCDs' GRBM instances
-            der.append("MFMA busy {:.1%}".format(
-                d["SQ_VALU_MFMA_BUSY_CYCLES"][0] / (d["GRBM_GUI_ACTIVE"][0] / 8 * 256 * 4)))
-        for c, fac_name in (("FETCH_SIZE", "read"), ("WRITE_SIZE", "write")):
-            if c in d and calib.get(c):
-                der.append(f"{fac_name} {d[c][0] * CALIB_BYTES / calib[c] / 1e6:.2f} MB (copy-scaled)")
-        print(f"| `{short}` | {nd} | " + " | ".join(cells) + " | " + "; ".join(der) + " |")
+
+    def demangle(name):
+        # the library's kernels in an anonymous namespace: _ZN2vb12_GLOBAL__N_1<len><name>...
+        # (some rocprofv3 builds leave names with _Float16 parameters mangled)
+        import re
+        m = re.match(r"_ZN2vb12_GLOBAL__N_1(\d+)", name)
+        if not m:
+            return name
+        n = int(m.group(1))
+        base = name[m.end():m.end() + n]
+        rest = name[m.end() + n:]
+        tmpl = re.match(r"IL[ij](\d+)E", rest)
+        return f"vb::{base}" + (f"<{tmpl.group(1)}>" if tmpl else "")
+    rows = {demangle(k): d for k, d in rows.items()}
+    kern = sorted(k for k in rows if "vb::" in k)
+    short = [k.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0][:70] for k in kern]
+    names = sorted({c for k in kern for c in rows[k]})
+    print("| Counter | " + " | ".join(f"`{s}`" for s in short) + " |")
+    print("|---" * (len(kern) + 1) + "|")
+    print("| dispatches | " + " | ".join(str(max(n for _, n in rows[k].values())) for k in kern) + " |")
+    for c in names:
+        print(f"| {c} | " + " | ".join(f"{rows[k][c][0]:.4g}" if c in rows[k] else "" for k in kern) + " |")
+
+    def derived(label, fn):
+        vals = []
+        for k in kern:
+            try:
+                vals.append(fn(rows[k]))
+            except (KeyError, ZeroDivisionError):
+                vals.append("")
+        if any(vals):
+            print(f"| {label} | " + " | ".join(vals) + " |")
+    v = lambda d, c: d[c][0]
+    derived("MFMA f16 GFLOP", lambda d: f"{v(d, 'SQ_INSTS_VALU_MFMA_MOPS_F16') * 512 / 1e9:.3f}")
+    derived("MFMA busy", lambda d: "{:.1%}".format(
+        v(d, "SQ_VALU_MFMA_BUSY_CYCLES") / (v(d, "GRBM_GUI_ACTIVE") / 8 * 256 * 4)))
+    derived("waiting / wave lifetime", lambda d: "{:.1%}".format(v(d, "SQ_WAIT_ANY") / v(d, "SQ_WAVE_CYCLES")))
+    derived("issuing / wave lifetime", lambda d: "{:.1%}".format(
+        v(d, "SQ_ACTIVE_INST_ANY") / v(d, "SQ_WAVE_CYCLES")))
+    derived("lanes per VALU instruction", lambda d: "{:.1f}".format(
+        v(d, "SQ_THREAD_CYCLES_VALU") / v(d, "SQ_ACTIVE_INST_VALU")))
+    derived("LDS bank conflict / LDS active", lambda d: "{:.1%}".format(
+        v(d, "SQ_LDS_BANK_CONFLICT") / v(d, "SQ_ACTIVE_INST_LDS")))
+    for c, lab in (("FETCH_SIZE", "read MB (copy-scaled)"), ("WRITE_SIZE", "written MB (copy-scaled)")):
+        if calib.get(c):
+            derived(lab, lambda d, c=c: f"{v(d, c) * CALIB_BYTES / calib[c] / 1e6:.2f}")
 
 
 def summarize_pmc(fetch_csv, write_csv):

@@ -250,7 +250,10 @@ def test_xreg_auto_route():
     assert lib.vb_gemm_workspace(512, 14336, 4096, Q4K, 1, 0) == 512 * 4096 * 2
     assert lib.vb_gemm_workspace(300, 14336, 4096, Q4K, 1, 0) == 512 * 4096 * 2  # whole 256-row tiles
     assert lib.vb_gemm_workspace(256, 14336, 4096, Q4K, 1, 0) == 0   # M = 256: another kernel
-    assert lib.vb_gemm_workspace(512, 4096, 14336, Q4K, 1, 0) == 0   # N < 8192
+    # N < 8192 with fewer output tiles than CUs: K splits (3 at 37 x 2 tiles),
+    # the packed X plus one fp32 partial product per split
+    assert lib.vb_gemm_workspace(512, 4096, 14336, Q4K, 1, 0) == 512 * 14336 * 2 + 3 * 512 * 4096 * 4
+    assert lib.vb_gemm_workspace(1024, 4096, 4096, Q4K, 1, 0) == 0   # 148 tiles: no split, another kernel
     assert lib.vb_gemm_workspace(512, 14336, 4096, Q4K, 0, 0) == 0   # fp32 X
     assert lib.vb_gemm_workspace(512, 14336, 4096, Q6K, 1, 0) == 0
     assert lib.vb_gemm_workspace(256, 64, 256, Q4K, 1, 5) == 256 * 256 * 2
@@ -260,6 +263,28 @@ def test_xreg_auto_route():
     b = gemm(qt, xt, variant=GEMM_XREG).cpu().numpy()
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     assert O.rel_l2(a, ref_gemm(qt, xt.float().cpu().numpy())) <= TOL
+
+
+@pytest.mark.parametrize("m,n,k,splits", [(512, 4096, 14336, 3), (300, 2000, 8192, 4), (256, 64, 4096, 2)])
+def test_xreg_ksplit(m, n, k, splits):
+    """The packed-X kernel with K splits (output tiles fewer than the CUs):
+    each split sums its super-blocks into a partial product, a second launch
+    adds them in split order.  The FFN down shape (4096 x 14336, M = 512),
+    ragged M and N with four splits, one tile with two.  Against the oracle,
+    the tiled kernel (to fp32 rounding of the same fp16 products), and the
+    default route (the same bits)."""
+    lib = _lib.load()
+    xf = -(-m // 256) * 256 * k * 2
+    assert lib.vb_gemm_workspace(m, n, k, Q4K, 1, GEMM_XREG) == xf + splits * m * n * 4
+    qt, x = make(m, n, k, m + n + k + 1)
+    xt = torch.from_numpy(x).to("cuda", torch.float16)
+    y = gemm(qt, xt, variant=GEMM_XREG).cpu().numpy()
+    assert O.rel_l2(y, ref_gemm(qt, xt.float().cpu().numpy())) <= TOL
+    assert np.all(np.abs(y).sum(axis=1) > 0)
+    t = gemm(qt, xt, variant=GEMM_TILED).cpu().numpy()
+    assert O.rel_l2(y, t.astype(np.float64)) <= 1e-5
+    if m > 256:
+        assert np.array_equal(gemm(qt, xt).cpu().numpy().view(np.uint32), y.view(np.uint32))
 
 
 def test_xreg_rejects():

@@ -672,8 +672,12 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
     // K = 4096 on MI355X, pack pass included: M = 384 / 512 / 1024 at 62.8 /
     // 62.6 / 117.5 us against 68.5 / 70.7 / 139.9 us on the role-split and
     // tiled kernels; behind at M = 256, 50.8 against 48.5)
-    const bool xr_auto = variant == 0 && type == TYPE_Q4_K && x_dtype == X_F16 && M > 256 && N >= 8192 &&
-                         ws != nullptr && static_cast<int64_t>(ws_bytes) >= gemm_q4k_xr_workspace(M, K) &&
+    // With fewer output tiles than CUs (the down projection 4096 x 14336 at
+    // M = 512) the same kernel splits K (gemm_q4k_xr_ksplit) and a small
+    // launch adds the partial products in a fixed order.
+    const bool xr_auto = variant == 0 && type == TYPE_Q4_K && x_dtype == X_F16 && M > 256 &&
+                         (N >= 8192 || gemm_q4k_xr_ksplit(M, N, K) > 1) && ws != nullptr &&
+                         static_cast<int64_t>(ws_bytes) >= gemm_q4k_xr_workspace(M, N, K) &&
                          reinterpret_cast<uintptr_t>(ws) % 16 == 0;
     if (xr_auto) return gemm_q4k_xr(w, X, Y, M, N, K, ws, st);
     if (type == TYPE_Q4_K && variant == 5) {
@@ -681,7 +685,7 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
             set_error("vb_gemm: variant 5 (X in registers) takes m >= 256, got %lld", static_cast<long long>(M));
             return E_INVAL;
         }
-        const int64_t need = gemm_q4k_xr_workspace(M, K);
+        const int64_t need = gemm_q4k_xr_workspace(M, N, K);
         if (!ws || static_cast<int64_t>(ws_bytes) < need || reinterpret_cast<uintptr_t>(ws) % 16) {
             set_error("vb_gemm: variant 5 needs a 16-byte-aligned workspace of %lld bytes (got %zu)",
                       static_cast<long long>(need), ws_bytes);
@@ -721,7 +725,8 @@ extern "C" int64_t vb_gemm_workspace(int64_t m, int64_t n, int64_t k, int32_t gg
                                      int32_t variant) {
     if (k <= 0 || k % 256 != 0 || ggml_type != vb::TYPE_Q4_K || x_dtype != 1) return 0;
     // the shapes gemm_dispatch sends to the packed-X kernel
-    if ((variant == 5 && m >= 256) || (variant == 0 && m > 256 && n >= 8192)) return vb::gemm_q4k_xr_workspace(m, k);
+    if ((variant == 5 && m >= 256) || (variant == 0 && m > 256 && (n >= 8192 || vb::gemm_q4k_xr_ksplit(m, n, k) > 1)))
+        return vb::gemm_q4k_xr_workspace(m, n, k);
     return 0;
 }
 

@@ -103,6 +103,9 @@ __global__ void __launch_bounds__(256) xr_pack_kernel(const uint8_t* __restrict_
     }
 }
 
+// K split (blockIdx.z = kz of gridDim.z): the workgroup takes super-blocks
+// [kz nsb / KS, (kz + 1) nsb / KS) and writes its sums to Y + kz M N (the
+// caller's partial buffers when KS > 1; xr_ksum_kernel adds them).
 template <int NF>
 __global__ void __launch_bounds__(XR_THREADS) gemm_q4k_xr_kernel(const uint8_t* __restrict__ w, uint32_t wbytes,
                                                                   const uint8_t* __restrict__ Xf,
@@ -132,7 +135,11 @@ __global__ void __launch_bounds__(XR_THREADS) gemm_q4k_xr_kernel(const uint8_t* 
     // written twice with the same values
     const int mt0 = xr_tile_row0(tile_m, M);
     const int n0 = tile_n * 16 * NF;
-    const int nsb = K >> 8, nsteps = 4 * nsb;
+    const int nsteps = 4 * (K >> 8);  // packed X steps of the whole row
+    const int kz = static_cast<int>(blockIdx.z), ks = static_cast<int>(gridDim.z);
+    const int sb0 = (kz * (K >> 8)) / ks;
+    const int nsb = ((kz + 1) * (K >> 8)) / ks - sb0;  // this workgroup's super-blocks sb0 .. sb0 + nsb - 1
+    Y += static_cast<int64_t>(kz) * M * N;
 
     if (wave < XR_CW) {
         // ---------------- consumer ----------------
@@ -141,8 +148,10 @@ __global__ void __launch_bounds__(XR_THREADS) gemm_q4k_xr_kernel(const uint8_t* 
                       static_cast<uint32_t>(nsteps) * XR_STEP_BYTES);
         const uint32_t xv = 16u * static_cast<uint32_t>(lane);
         Frag areg[2][2][4];  // [slot][ks][a]
+        const int s_last = 4 * (sb0 + nsb) - 1;
         auto load_a = [&](int s, int slot, int ks) {
-            s = s < nsteps ? s : nsteps - 1;
+            s = 4 * sb0 + s;  // local step -> step of the row
+            s = s < s_last ? s : s_last;
 #pragma unroll
             for (int a = 0; a < 4; a++) {
                 const uint32_t so = static_cast<uint32_t>(((s * 2 + ks) * 16 + wave * 4 + a) * 1024);
@@ -235,7 +244,7 @@ __global__ void __launch_bounds__(XR_THREADS) gemm_q4k_xr_kernel(const uint8_t* 
         }
         u32x4 rr[RPT];
         auto load_raw = [&](int sb) {
-            sb = sb < nsb ? sb : nsb - 1;
+            sb = sb0 + (sb < nsb ? sb : nsb - 1);  // local -> super-block of the row
 #pragma unroll
             for (int i = 0; i < RPT; i++)
                 rr[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, static_cast<int>(roff[i]),
@@ -302,25 +311,70 @@ __global__ void __launch_bounds__(XR_THREADS) gemm_q4k_xr_kernel(const uint8_t* 
     }
 }
 
+// Y = sum of the KS partial products in the order kz = 0, 1, ... (fixed,
+// deterministic); four outputs per thread.
+__global__ void __launch_bounds__(256) xr_ksum_kernel(const float* __restrict__ P, float* __restrict__ Y,
+                                                      int64_t total, int ks) {
+    const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+    if (i + 4 <= total) {
+        float4 s = *reinterpret_cast<const float4*>(P + i);
+        for (int z = 1; z < ks; z++) {
+            const float4 v = *reinterpret_cast<const float4*>(P + static_cast<int64_t>(z) * total + i);
+            s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+        }
+        *reinterpret_cast<float4*>(Y + i) = s;
+    } else {
+        for (int64_t e = i; e < total; e++) {
+            float s = P[e];
+            for (int z = 1; z < ks; z++) s += P[static_cast<int64_t>(z) * total + e];
+            Y[e] = s;
+        }
+    }
+}
+
+constexpr int XR_NF = 7;
+
 }  // namespace
 
-int64_t gemm_q4k_xr_workspace(int64_t M, int64_t K) {
-    return (M + XR_TM - 1) / XR_TM * XR_TM * K * 2;
+// K splits: as many as fit the CUs with one workgroup each (a shape with
+// fewer output tiles than CUs, such as the FFN down projection 4096 x 14336
+// at M = 512: 37 x 2 tiles, 3 splits), at least 8 super-blocks per split.
+int gemm_q4k_xr_ksplit(int64_t M, int64_t N, int64_t K) {
+    const int64_t tiles = (N + 16 * XR_NF - 1) / (16 * XR_NF) * ((M + XR_TM - 1) / XR_TM);
+    int64_t ks = num_cus() / (tiles > 0 ? tiles : 1);
+    const int64_t kmax = (K / 256) / 8;
+    ks = ks < kmax ? ks : kmax;
+    return static_cast<int>(ks < 1 ? 1 : (ks > 8 ? 8 : ks));
+}
+
+int64_t gemm_q4k_xr_workspace(int64_t M, int64_t N, int64_t K) {
+    const int64_t xf = (M + XR_TM - 1) / XR_TM * XR_TM * K * 2;
+    const int ks = gemm_q4k_xr_ksplit(M, N, K);
+    return xf + (ks > 1 ? static_cast<int64_t>(ks) * M * N * 4 : 0);
 }
 
 // Caller (gemm_dispatch) has validated type (Q4_K), alignment (W, X 16 B),
 // the 32-bit offset bounds (N * row bytes, M * K * 2 < 2^32), M >= 256 and
-// the workspace (gemm_q4k_xr_workspace bytes, 16-byte aligned).
+// the workspace (gemm_q4k_xr_workspace bytes, 16-byte aligned): the packed X,
+// then, with K splits, one fp32 M x N partial product per split.
 int gemm_q4k_xr(const void* w, const void* X, float* Y, int64_t M, int64_t N, int64_t K, void* ws, hipStream_t st) {
-    constexpr int NF = 7;
+    constexpr int NF = XR_NF;
     const int64_t rb = row_bytes(TYPE_Q4_K, K);
     const uint32_t mtiles = static_cast<uint32_t>((M + XR_TM - 1) / XR_TM);
+    const int ks = gemm_q4k_xr_ksplit(M, N, K);
     xr_pack_kernel<<<dim3(static_cast<uint32_t>(K / 256), XR_TM / 16, mtiles), dim3(256), 0, st>>>(
         static_cast<const uint8_t*>(X), static_cast<uint4*>(ws), static_cast<int>(M), static_cast<int>(K));
-    const dim3 grid(static_cast<uint32_t>((N + 16 * NF - 1) / (16 * NF)), mtiles);
+    float* out = Y;
+    if (ks > 1) out = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + mtiles * XR_TM * K * 2);
+    const dim3 grid(static_cast<uint32_t>((N + 16 * NF - 1) / (16 * NF)), mtiles, static_cast<uint32_t>(ks));
     gemm_q4k_xr_kernel<NF><<<grid, dim3(XR_THREADS), 0, st>>>(
-        static_cast<const uint8_t*>(w), static_cast<uint32_t>(N * rb), static_cast<const uint8_t*>(ws), Y,
+        static_cast<const uint8_t*>(w), static_cast<uint32_t>(N * rb), static_cast<const uint8_t*>(ws), out,
         static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), static_cast<uint32_t>(rb));
+    if (ks > 1) {
+        const int64_t total = M * N;
+        xr_ksum_kernel<<<dim3(static_cast<uint32_t>((total / 4 + 255) / 256 + 1)), dim3(256), 0, st>>>(out, Y, total,
+                                                                                                    ks);
+    }
     return check_launch("vb_gemm");
 }
 

@@ -134,8 +134,10 @@ int gemm_q4k_split(const void* w, const void* X, float* Y, int64_t M, int64_t N,
 // Q4_K GEMM with the activation fragments loaded into registers from X
 // packed in fragment order, fp16 X (gemm_xr.hip): the preconditions of
 // gemm_q4k_split plus M >= 256 and a 16-byte-aligned workspace of
-// gemm_q4k_xr_workspace(M, K) bytes (the packed X).
-int64_t gemm_q4k_xr_workspace(int64_t M, int64_t K);
+// gemm_q4k_xr_workspace(M, N, K) bytes (the packed X, and the partial
+// products of the K splits when the output tiles are fewer than the CUs).
+int gemm_q4k_xr_ksplit(int64_t M, int64_t N, int64_t K);
+int64_t gemm_q4k_xr_workspace(int64_t M, int64_t N, int64_t K);
 int gemm_q4k_xr(const void* w, const void* X, float* Y, int64_t M, int64_t N, int64_t K, void* ws, hipStream_t st);
 // Q6_K / Q8_0 GEMM, every M (gemm_kq.hip); pointers, alignment, x_dtype and
 // M, N > 0 already validated.
