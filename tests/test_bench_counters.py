@@ -33,9 +33,23 @@ def test_counter_table_derived_figures(tmp_path, capsys):
     p = tmp_path / "run_counter_collection.csv"
     _write(p, rows)
     bench.counter_table([str(p)])
-    out = capsys.readouterr().out
-    line = next(l for l in out.splitlines() if "gemm_q4k_tiled<1, 8, 2>" in l)
-    assert "| 2 |" in line                                  # dispatches
-    assert f"MFMA f16 {1.1e8 * 512 / 1e9:.3f} GFLOP" in line  # mean of 1.0e8 and 1.2e8, x 512 FLOP
-    assert "MFMA busy 25.0%" in line                        # GRBM summed over 8 XCDs
-    assert f"read {1000.0 * 1024 * 2 / 1e6:.2f} MB" in line  # copy factor 2 applied to KiB
+    out = capsys.readouterr().out.splitlines()
+    # one column per library kernel (the copy is not one), one row per counter
+    assert "gemm_q4k_tiled<1, 8, 2>" in out[0] and "neg_kernel" not in out[0]
+    row = {l.split("|")[1].strip(): l.split("|")[2].strip() for l in out[2:]}
+    assert row["dispatches"] == "2"
+    assert row["MFMA f16 GFLOP"] == f"{1.1e8 * 512 / 1e9:.3f}"  # mean of 1.0e8 and 1.2e8, x 512 FLOP
+    assert row["MFMA busy"] == "25.0%"                        # GRBM summed over 8 XCDs
+    assert row["read MB (copy-scaled)"] == f"{1000.0 * 1024 * 2 / 1e6:.2f}"  # copy factor 2 applied to KiB
+
+
+def test_counter_table_mangled_names(tmp_path, capsys):
+    """Kernel names left mangled by the profiler (_Float16 parameters) still
+    count as the library's, under a readable name."""
+    name = "_ZN2vb12_GLOBAL__N_115moe_gate_up_q4kILi4EEEvNS0_10ExpertPtrsES2_PKDF16_PKiS6_iiiijjPDF16_"
+    p = tmp_path / "run_counter_collection.csv"
+    _write(p, [(1, name, "SQ_WAVES", 7168.0)])
+    bench.counter_table([str(p)])
+    out = capsys.readouterr().out.splitlines()
+    assert "`vb::moe_gate_up_q4k<4>`" in out[0]
+    assert out[3].split("|")[1].strip() == "SQ_WAVES" and out[3].split("|")[2].strip() == "7168"
