@@ -488,10 +488,31 @@ def test_small_m_long_k_runs_ksplit(m):
 
 
 @pytest.mark.parametrize("qtype", [Q6K, Q80])
+@pytest.mark.parametrize("m,n,k,zs", [(400, 1000, 4096, 4), (384, 4096, 14336, 4)])
+def test_tiled_types_zsplit(qtype, m, n, k, zs):
+    """Q6_K / Q8_0, fp16 X, M >= 384, N < 8192: the default splits K between
+    workgroups of 256 x 128 tiles (partial products in the workspace, added in
+    split order): ragged M and N with four splits, and the down shape at
+    M = 384.  Against the oracle and the unsplit tiled kernel (same fp16
+    products, sums grouped differently)."""
+    lib = _lib.load()
+    assert lib.vb_gemm_workspace(m, n, k, qtype, 1, 0) == zs * m * n * 4
+    assert lib.vb_gemm_workspace(m, n, k, qtype, 0, 0) == 0  # fp32 X: no split
+    qt, x = make(m, n, k, m + n + qtype, qtype=qtype)
+    xt = torch.from_numpy(x).to("cuda", torch.float16)
+    y = gemm(qt, xt).cpu().numpy()
+    assert O.rel_l2(y, ref_gemm(qt, xt.float().cpu().numpy())) <= TOL
+    assert np.all(np.abs(y).sum(axis=1) > 0)
+    t = gemm(qt, xt, variant=GEMM_TILED).cpu().numpy()
+    assert O.rel_l2(y, t.astype(np.float64)) <= 1e-5
+
+
+@pytest.mark.parametrize("qtype", [Q6K, Q80])
 def test_tiled_types_down_shape(qtype):
     """4096 x 14336 Q6_K / Q8_0 weights (the down projection) at M = 512 on
-    the default path (the tiled kernel), against the K-split kernel and the
-    oracle; fp16 X with 0.1 % outliers x20."""
+    the default path (the tiled kernel with K split four ways between
+    workgroups), against the K-split kernel and the oracle; fp16 X with 0.1 %
+    outliers x20."""
     n, k, m = 4096, 14336, 512
     gen = torch.Generator(device="cuda").manual_seed(300 + qtype)
     qt = QTensor.quantize(torch.randn((n, k), generator=gen, device="cuda") * 0.02, qtype)

@@ -183,6 +183,9 @@ struct TiledW<TYPE_Q8_0> {
 // its own LDS stage (the tiles below); both run the same number of steps, so
 // the one barrier per step serves both.  At the end group 1 hands its
 // accumulators to group 0 through LDS (fixed order), which stores Y.
+// gridDim.z > 1 splits K between workgroups as well: workgroup z takes steps
+// [z nsteps / Z, (z + 1) nsteps / Z) and stores to Y + z M N (a partial
+// product; gemm_ksum adds them).
 template <int TYPE, int XT, int NF, int WM, int WN, int KS>
 __global__ void __launch_bounds__(64 * WM * WN * KS) gemm_tiled(const uint8_t* __restrict__ w, uint32_t wbytes,
                                                                 const void* __restrict__ X, float* __restrict__ Y,
@@ -217,22 +220,30 @@ __global__ void __launch_bounds__(64 * WM * WN * KS) gemm_tiled(const uint8_t* _
     const int wm = wave / WN, wn = wave - wm * WN;
     const int j = lane & 15, g = lane >> 4;
     // Tile of this workgroup.  Workgroups are dealt to the 8 XCDs round
-    // robin (linear id % 8).  With 2, 4 or 8 M-tiles, each M-tile gets 8 / mt
-    // XCDs of its own, so each XCD's L2 holds one M-tile of X (a bijection
-    // when nt is a multiple of 8 / mt).
+    // robin (linear id % 8).  With Q = (M-tiles) x (K splits) = 2, 4 or 8
+    // blocks of X (one per M-tile and K range), each block gets 8 / Q XCDs
+    // of its own, so each XCD's L2 holds one block (a bijection when nt is a
+    // multiple of 8 / Q).  At 4096 x 14336, M = 512, with four K splits:
+    // eight 1.8 MB blocks, one per XCD, instead of all 14.7 MB on every XCD.
     const int nt = static_cast<int>(gridDim.x), mt = static_cast<int>(gridDim.y);
+    const int zs = static_cast<int>(gridDim.z);
     int tile_n = static_cast<int>(blockIdx.x), tile_m = static_cast<int>(blockIdx.y);
-    if ((mt == 2 || mt == 4 || mt == 8) && nt % (8 / mt) == 0) {
-        const int G = 8 / mt;  // XCDs per M-tile
-        const int lin = tile_n + nt * tile_m, xcd = lin & 7, r = lin >> 3;
-        tile_m = xcd / G;
+    int kz = static_cast<int>(blockIdx.z);
+    const int Q = mt * zs;
+    if ((Q == 2 || Q == 4 || Q == 8) && nt % (8 / Q) == 0) {
+        const int G = 8 / Q;  // XCDs per X block
+        const int lin = tile_n + nt * (tile_m + mt * kz), xcd = lin & 7, r = lin >> 3;
+        const int q = xcd / G;
+        tile_m = q % mt;
+        kz = q / mt;
         tile_n = (xcd % G) * (nt / G) + r;
     }
     const int mt0 = tile_m * TB_M;
     const int n0 = tile_n * 16 * NF;
     const int nsteps = K / 64;
     // this group's steps: [s_base, s_base + nloc); nloc % PD == 0 (host)
-    const int nloc = nsteps / KS, s_base = grp * nloc;
+    const int nloc = nsteps / (KS * zs), s_base = (kz * KS + grp) * nloc;
+    Y += static_cast<int64_t>(kz) * M * N;
 
     // ---- weights: dequant unit u = tid + NT i is LDS lane slot u: fragment
     // u / 64, lane l = u % 64 -> weight row un = 16 (u / 64) + l % 16, qs part
@@ -513,9 +524,9 @@ TileCfg tiled_cfg(int type, int x_dtype, int64_t M, int64_t N, int64_t K) {
 
 template <int TYPE, int XT, int NF, int WM, int WN>
 void launch_tiled_cfg(const uint8_t* w, uint32_t wbytes, const void* X, float* Y, int M, int N, int K, int64_t rb,
-                      int ks, hipStream_t st) {
+                      int ks, int zs, hipStream_t st) {
     const dim3 grid(static_cast<uint32_t>((N + 16 * NF - 1) / (16 * NF)),
-                    static_cast<uint32_t>((M + 64 * WM - 1) / (64 * WM)));
+                    static_cast<uint32_t>((M + 64 * WM - 1) / (64 * WM)), static_cast<uint32_t>(zs));
     if constexpr (ks2_tile(WM, WN, NF)) {
         if (ks == 2) {
             gemm_tiled<TYPE, XT, NF, WM, WN, 2><<<grid, dim3(128 * WM * WN), 0, st>>>(w, wbytes, X, Y, M, N, K, rb);
@@ -527,11 +538,11 @@ void launch_tiled_cfg(const uint8_t* w, uint32_t wbytes, const void* X, float* Y
 
 template <int TYPE, int XT>
 int launch_tiled(const TileCfg& c, const uint8_t* w, uint32_t wbytes, const void* X, float* Y, int M, int N, int K,
-                 int64_t rb, hipStream_t st) {
-#define VB_TILE(WM_, WN_, NF_)                                                        \
-    if (c.wm == WM_ && c.wn == WN_ && c.nf == NF_) {                                 \
-        launch_tiled_cfg<TYPE, XT, NF_, WM_, WN_>(w, wbytes, X, Y, M, N, K, rb, c.ks, st);  \
-        return OK;                                                                    \
+                 int64_t rb, hipStream_t st, int zs = 1) {
+#define VB_TILE(WM_, WN_, NF_)                                                              \
+    if (c.wm == WM_ && c.wn == WN_ && c.nf == NF_) {                                       \
+        launch_tiled_cfg<TYPE, XT, NF_, WM_, WN_>(w, wbytes, X, Y, M, N, K, rb, c.ks, zs, st);  \
+        return OK;                                                                          \
     }
     VB_TILE(4, 2, 8)
     VB_TILE(4, 2, 6)
@@ -551,6 +562,21 @@ int launch_tiled(const TileCfg& c, const uint8_t* w, uint32_t wbytes, const void
 }
 
 }  // namespace
+
+// K split between workgroups for Q6_K / Q8_0 with fp16 X at M >= 384 and
+// N < 8192 (the FFN down projection, 4096 x 14336): the 256 x 128 tile,
+// whose grid alone (32 x 2 tiles at M = 512) leaves most CUs idle, in as
+// many K splits as fill the CUs; each split a whole number of PD-step rounds.
+// Returns 1 when the shape does not take it.
+int tiled_zsplit(int type, int x_dtype, int64_t M, int64_t N, int64_t K) {
+    if ((type != TYPE_Q6_K && type != TYPE_Q8_0) || x_dtype != X_F16 || M < 384 || N >= 8192 || knobs().gemm_tile_wm)
+        return 1;
+    const int64_t tiles = tile_count(TileCfg{4, 2, 8, 1}, M, N);
+    const int64_t nsteps = K / 64;
+    for (int64_t z = num_cus() / (tiles > 0 ? tiles : 1); z >= 2; z--)
+        if (z <= 8 && nsteps % (z * PD) == 0 && nsteps / z >= 4 * PD) return static_cast<int>(z);
+    return 1;
+}
 
 int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, int64_t N, int64_t K,
                   int32_t type, int32_t variant, void* ws, size_t ws_bytes, hipStream_t st) {
@@ -701,6 +727,17 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
     const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
     const uint32_t wby = static_cast<uint32_t>(wbytes);
     int rc;
+    // K split between workgroups (partial products in the workspace)
+    const int zs = variant == 0 ? tiled_zsplit(type, x_dtype, M, N, K) : 1;
+    if (zs > 1 && ws && static_cast<int64_t>(ws_bytes) >= zs * M * N * 4 && reinterpret_cast<uintptr_t>(ws) % 16 == 0) {
+        float* part = static_cast<float*>(ws);
+        const TileCfg big{4, 2, 8, 1};
+        rc = type == TYPE_Q6_K ? launch_tiled<TYPE_Q6_K, X_F16>(big, wb, wby, X, part, m, n, k, rb, st, zs)
+                               : launch_tiled<TYPE_Q8_0, X_F16>(big, wb, wby, X, part, m, n, k, rb, st, zs);
+        if (rc != OK) return rc;
+        if ((rc = check_launch("vb_gemm")) != OK) return rc;
+        return gemm_ksum(part, Y, M * N, zs, st);
+    }
     if (type == TYPE_Q4_K)
         rc = x_dtype == X_F16 ? launch_tiled<TYPE_Q4_K, X_F16>(cfg, wb, wby, X, Y, m, n, k, rb, st)
                               : launch_tiled<TYPE_Q4_K, X_F32>(cfg, wb, wby, X, Y, m, n, k, rb, st);
@@ -723,7 +760,13 @@ extern "C" int vb_gemm(const void* w, const void* x, int32_t x_dtype, float* y, 
 
 extern "C" int64_t vb_gemm_workspace(int64_t m, int64_t n, int64_t k, int32_t ggml_type, int32_t x_dtype,
                                      int32_t variant) {
-    if (k <= 0 || k % 256 != 0 || ggml_type != vb::TYPE_Q4_K || x_dtype != 1) return 0;
+    if (k <= 0 || k % 256 != 0 || m <= 0 || n <= 0 || x_dtype != 1) return 0;
+    if (ggml_type == vb::TYPE_Q6_K || ggml_type == vb::TYPE_Q8_0) {
+        // the tiled kernel's K splits: one fp32 partial product each
+        const int zs = variant == 0 ? vb::tiled_zsplit(ggml_type, x_dtype, m, n, k) : 1;
+        return zs > 1 ? static_cast<int64_t>(zs) * m * n * 4 : 0;
+    }
+    if (ggml_type != vb::TYPE_Q4_K) return 0;
     // the shapes gemm_dispatch sends to the packed-X kernel
     if ((variant == 5 && m >= 256) || (variant == 0 && m > 256 && (n >= 8192 || vb::gemm_q4k_xr_ksplit(m, n, k) > 1)))
         return vb::gemm_q4k_xr_workspace(m, n, k);

@@ -347,6 +347,11 @@ int gemm_q4k_xr_ksplit(int64_t M, int64_t N, int64_t K) {
     return static_cast<int>(ks < 1 ? 1 : (ks > 8 ? 8 : ks));
 }
 
+int gemm_ksum(const float* P, float* Y, int64_t total, int ks, hipStream_t st) {
+    xr_ksum_kernel<<<dim3(static_cast<uint32_t>((total / 4 + 255) / 256 + 1)), dim3(256), 0, st>>>(P, Y, total, ks);
+    return check_launch("vb_gemm");
+}
+
 int64_t gemm_q4k_xr_workspace(int64_t M, int64_t N, int64_t K) {
     const int64_t xf = (M + XR_TM - 1) / XR_TM * XR_TM * K * 2;
     const int ks = gemm_q4k_xr_ksplit(M, N, K);
@@ -371,9 +376,8 @@ int gemm_q4k_xr(const void* w, const void* X, float* Y, int64_t M, int64_t N, in
         static_cast<const uint8_t*>(w), static_cast<uint32_t>(N * rb), static_cast<const uint8_t*>(ws), out,
         static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), static_cast<uint32_t>(rb));
     if (ks > 1) {
-        const int64_t total = M * N;
-        xr_ksum_kernel<<<dim3(static_cast<uint32_t>((total / 4 + 255) / 256 + 1)), dim3(256), 0, st>>>(out, Y, total,
-                                                                                                    ks);
+        if (const int rc = check_launch("vb_gemm"); rc != OK) return rc;
+        return gemm_ksum(out, Y, M * N, ks, st);
     }
     return check_launch("vb_gemm");
 }

@@ -137,6 +137,11 @@ int gemm_q4k_split(const void* w, const void* X, float* Y, int64_t M, int64_t N,
 // gemm_q4k_xr_workspace(M, N, K) bytes (the packed X, and the partial
 // products of the K splits when the output tiles are fewer than the CUs).
 int gemm_q4k_xr_ksplit(int64_t M, int64_t N, int64_t K);
+// Y[0, total) = P[0, total) + P[total, 2 total) + ... (ks partial products,
+// added in that order), fp32 (gemm_xr.hip).
+int gemm_ksum(const float* P, float* Y, int64_t total, int ks, hipStream_t st);
+// K splits of the tiled GEMM between workgroups for this shape (1: none; gemm.hip).
+int tiled_zsplit(int type, int x_dtype, int64_t M, int64_t N, int64_t K);
 int64_t gemm_q4k_xr_workspace(int64_t M, int64_t N, int64_t K);
 int gemm_q4k_xr(const void* w, const void* X, float* Y, int64_t M, int64_t N, int64_t K, void* ws, hipStream_t st);
 // Q6_K / Q8_0 GEMM, every M (gemm_kq.hip); pointers, alignment, x_dtype and
