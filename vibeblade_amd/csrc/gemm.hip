@@ -569,8 +569,13 @@ int launch_tiled(const TileCfg& c, const uint8_t* w, uint32_t wbytes, const void
 // many K splits as fill the CUs; each split a whole number of PD-step rounds.
 // Returns 1 when the shape does not take it.
 int tiled_zsplit(int type, int x_dtype, int64_t M, int64_t N, int64_t K) {
-    if ((type != TYPE_Q6_K && type != TYPE_Q8_0) || x_dtype != X_F16 || M < 384 || N >= 8192 || knobs().gemm_tile_wm)
-        return 1;
+    if ((type != TYPE_Q6_K && type != TYPE_Q8_0) || x_dtype != X_F16 || M < 384 || N >= 8192) return 1;
+    if (knobs().gemm_tile_wm) {
+        // VB_GEMM_TILE with VB_GEMM_ZSPLIT: that tile in that many splits
+        const int z = knobs().gemm_zsplit;
+        const int64_t nsteps = K / 64;
+        return z >= 2 && z <= 8 && nsteps % (z * PD * knobs().gemm_tile_ks) == 0 ? z : 1;
+    }
     const int64_t tiles = tile_count(TileCfg{4, 2, 8, 1}, M, N);
     const int64_t nsteps = K / 64;
     for (int64_t z = num_cus() / (tiles > 0 ? tiles : 1); z >= 2; z--)
@@ -731,7 +736,7 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
     const int zs = variant == 0 ? tiled_zsplit(type, x_dtype, M, N, K) : 1;
     if (zs > 1 && ws && static_cast<int64_t>(ws_bytes) >= zs * M * N * 4 && reinterpret_cast<uintptr_t>(ws) % 16 == 0) {
         float* part = static_cast<float*>(ws);
-        const TileCfg big{4, 2, 8, 1};
+        const TileCfg big = knobs().gemm_tile_wm ? cfg : TileCfg{4, 2, 8, 1};
         rc = type == TYPE_Q6_K ? launch_tiled<TYPE_Q6_K, X_F16>(big, wb, wby, X, part, m, n, k, rb, st, zs)
                                : launch_tiled<TYPE_Q8_0, X_F16>(big, wb, wby, X, part, m, n, k, rb, st, zs);
         if (rc != OK) return rc;

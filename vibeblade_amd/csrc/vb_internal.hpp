@@ -16,6 +16,8 @@ namespace vb {
 //   VB_GEMM_TILE="wm,wn,nf[,ks]"              tiled GEMM tile configuration (ks: K halves per
 //                                             workgroup, 1 or 2)
 //   VB_GEMM_SPLIT_MIN_M=m                     smallest M (up to 768) on the role-split GEMM (0: never)
+//   VB_GEMM_ZSPLIT=z                          with VB_GEMM_TILE: K splits between workgroups (Q6_K / Q8_0,
+//                                             fp16 X, M >= 384, N < 8192)
 //   VB_GEMV_SPLIT="sl,d"                      split-row Q4_K GEMV: slices per row (2, 4, 8), rows in flight (1-4)
 //   VB_SPARSE_FUSED=0, VB_SPARSE_NPW=1|2      sparse FFN kernel choice (NPW: the row-split fused
 //                                             kernel with 1 or 2 neurons per wave)
@@ -31,6 +33,7 @@ struct Knobs {
     int gemm_nf = 0;
     int gemm_tile_wm = 0, gemm_tile_wn = 0, gemm_tile_nf = 0, gemm_tile_ks = 1;
     int gemm_split_min_m = -1;  // smallest M on the role-split kernel (-1: default)
+    int gemm_zsplit = 0;        // with VB_GEMM_TILE: K splits between workgroups (Q6_K / Q8_0)
     int gemv_split_sl = 0, gemv_split_d = 0;  // split-row Q4_K GEMV: slices per row, rows in flight
     bool sparse_fused = true;
     int sparse_npw = 0;
