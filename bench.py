@@ -80,9 +80,10 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--pmc-pass", nargs="?", const="gemv",
-                   choices=["gemv", "lmhead", "down", "gemm8", "gemm512", "down512", "sparse", "moe"],
+                   choices=["gemv", "lmhead", "down", "gemm8", "gemm512", "down512", "down512q6", "sparse", "moe"],
                    help="eager launches for rocprofv3 --pmc: 32 headline GEMVs (gemv), 16 Q4_K GEMMs "
-                        "14336x4096 at M=8 / 512 (gemm8, gemm512) or 4096x14336 at M=512 (down512), 16 "
+                        "14336x4096 at M=8 / 512 (gemm8, gemm512) or 4096x14336 at M=512 (down512; Q6_K: "
+                        "down512q6), 16 "
                         "neuron-major TurboSparse FFN calls (sparse) or 8 MoE calls (moe), each as the timed "
                         "run launches it, then a 256 MiB copy (torch.neg) that calibrates FETCH_SIZE / "
                         "WRITE_SIZE")
@@ -682,8 +683,10 @@ def pmc_pass(workload="gemv"):
         what = "8 MoE calls"
     else:
         m = 8 if workload == "gemm8" else 512
-        if workload == "down512":
+        if workload in ("down512", "down512q6"):
             n, k = 4096, 14336
+        if workload == "down512q6":
+            qtype = ggml.GGML_TYPE_Q6_K
         gen = torch.Generator(device="cuda").manual_seed(SEED + m)
         copies = make_copies(qtype, n, k, NCOPIES, gen)
         xh = gemm_inputs(m, k, gen)
