@@ -145,7 +145,8 @@ int vb_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k,
  * dequantize_row (cpp/src/dequant.cpp:407-425), and cuda::gemm_f32
  * (cpp/include/cuda_kernels.h, cpp/src/cuda_kernels.cu:184-212).
  * Weight types: Q4_K (variants 0-4), Q6_K and Q8_0 (variants 0, 2, 4; Q8_0
- * needs k % 128 == 0).  W and x 16-byte aligned. */
+ * needs k % 128 == 0 at every m, m == 1 included, although vb_gemv itself
+ * takes Q8_0 rows of any whole number of blocks).  W and x 16-byte aligned. */
 int vb_gemm(const void* w, const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n,
             int64_t k, int32_t ggml_type, int32_t variant, void* stream);
 /* vb_gemm with a caller-owned workspace, which lets variant 0 (and variant 5)

@@ -157,3 +157,24 @@ class TestMoEContainers:
         r2, es2, _ = load_moe_weights_from_layer(alt, 2)
         assert es2.num_experts == 2 and r2.shape == (16, 2)
         assert repr(MoEConfig(4, 2, 32, 16, has_shared_expert=True)).endswith("shared_expert=True)")
+
+
+def test_stats_and_map_are_dataclasses():
+    """ExecutorStats and HotColdMap are dataclasses with the reference's
+    fields, order and defaults (vibeblade/moe_executor.py:31-38,
+    vibeblade/moe_profiler.py:8-16): asdict / replace / fields work on them,
+    and attributes can be added as on the reference's."""
+    import dataclasses
+    assert [f.name for f in dataclasses.fields(ExecutorStats)] == [
+        "gpu_hits", "cpu_falls", "gpu_latency_ms", "cpu_latency_ms", "sync_latency_ms"]
+    st = ExecutorStats(gpu_hits=3, cpu_falls=1, gpu_latency_ms=1.23456)
+    assert dataclasses.asdict(st)["gpu_latency_ms"] == 1.23456
+    assert dataclasses.replace(st, cpu_falls=3).hit_rate == 0.5
+    st.extra = 1  # no __slots__
+    assert st.copy() == ExecutorStats(3, 1, 1.23456)
+    assert [(f.name, f.default) for f in dataclasses.fields(HotColdMap)][2:] == [
+        ("num_layers", dataclasses.MISSING), ("num_experts", dataclasses.MISSING),
+        ("profile_tokens", 0), ("profile_dataset", "")]
+    m = HotColdMap({0: [1, 2]}, {0: [3]}, 1, 4)
+    assert dataclasses.is_dataclass(m) and dataclasses.asdict(m)["hot_experts"] == {0: [1, 2]}
+    assert dataclasses.replace(m, profile_tokens=7).profile_tokens == 7

@@ -381,6 +381,20 @@ def test_kq_matches_gemv_rows():
             assert O.rel_l2(y[r], yr) <= TOL, (qtype, r)
 
 
+@pytest.mark.parametrize("m", [1, 2])
+def test_q8_0_k_rule_at_every_m(m):
+    """Q8_0 needs K % 128 == 0 in vb_gemm at every M: the one-row case, which
+    runs on the GEMV (which itself takes K % 32 == 0 through vb_gemv), is
+    refused the same way as M = 2, so a shape valid at M = 1 stays valid at
+    M = 2."""
+    qt, x = make(m, 16, 192, 5, qtype=Q80)
+    with pytest.raises(VBError, match="K % 128"):
+        gemm(qt, torch.from_numpy(x).to("cuda", torch.float16))
+    from vibeblade_amd.tensor import gemv
+    y = gemv(qt, torch.from_numpy(x[0]).cuda())  # the GEMV entry takes it
+    assert O.rel_l2(y.cpu().numpy(), ref_gemm(qt, x[:1].astype(np.float32))[0]) <= TOL
+
+
 def test_kq_rejects():
     qt, x = make(4, 16, 256, 3, qtype=Q80)  # Q8_0 K = 256 is fine
     gemm(qt, torch.from_numpy(x).to("cuda", torch.float16))

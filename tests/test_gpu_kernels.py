@@ -171,6 +171,28 @@ def test_gemv_extreme_activations():
     assert O.rel_l2(y, want) <= GEMV_TOL
 
 
+@pytest.mark.parametrize("qtype,k", [(ggml.GGML_TYPE_Q4_K, 4096), (ggml.GGML_TYPE_Q6_K, 4096),
+                                     (ggml.GGML_TYPE_Q8_0, 4096), (ggml.GGML_TYPE_Q4_K, 14336),
+                                     (ggml.GGML_TYPE_Q6_K, 14336), (ggml.GGML_TYPE_Q8_0, 14336)])
+def test_gemv_outlier_unit_precision(qtype, k):
+    """A 300x outlier sets the scale of its 64-element unit in the 15-bit
+    activation encoding of the short-row (k = 4096) and split-row (k = 14336)
+    kernels.  The whole-vector rel-L2 is dominated by the outlier's own
+    product, so its exact fp64 contribution W[:, 100] x[100] is taken out of
+    both outputs: the remainder (every other element, the 63 in the outlier's
+    unit included) must still meet the bound."""
+    n = 512
+    qt = QTensor.quantize(rand_weights(n, k, 7), qtype)
+    rng = np.random.default_rng(k + qtype)
+    x = rng.standard_normal(k).astype(np.float32)
+    x[100] = 300.0
+    y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy().astype(np.float64)
+    w = O.dequantize(qt.to_numpy_bytes(), k, qtype).astype(np.float64)
+    want = w @ x.astype(np.float64)
+    out = w[:, 100] * 300.0
+    assert O.rel_l2(y - out, want - out) <= GEMV_TOL
+
+
 CONFIG_SHAPES = [
     (ggml.GGML_TYPE_Q8_0, 4096, 4096),     # Q8_0 GEMV 4096x4096
     (ggml.GGML_TYPE_Q4_K, 14336, 4096),    # Q4_K gate/up

@@ -603,6 +603,13 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
         set_error("vb_gemm: W and X must be 16-byte aligned");
         return E_INVAL;
     }
+    // Q8_0: the batched kernels step K by 128; the rule holds at every M, the
+    // one row that runs on the GEMV included, so a shape valid at M = 1 is
+    // valid at M = 2
+    if (type == TYPE_Q8_0 && K % 128 != 0) {
+        set_error("vb_gemm: Q8_0 weights need K %% 128 == 0 (K=%lld)", static_cast<long long>(K));
+        return E_UNSUPPORTED;
+    }
     // one row: the GEMV (the short-row and split-row kernels; rel-L2 near
     // 5e-5, and at 14336 x 4096 on MI355X 7.4 us against 11.8 us for the
     // skinny tile).  fp32 X for every type; fp16 X on the short-row kernels

@@ -16,6 +16,7 @@ from __future__ import annotations
 
 import threading
 import time
+from dataclasses import dataclass
 
 import numpy as np
 import torch
@@ -29,17 +30,18 @@ _COUNTS = ("gpu_hits", "cpu_falls")
 _TIMES_MS = ("gpu_latency_ms", "cpu_latency_ms", "sync_latency_ms")
 
 
+@dataclass
 class ExecutorStats:
     """Routed-expert counters and time spent, for one dispatch or summed over
-    dispatches.  Field names, ``hit_rate`` and the ``to_dict`` keys and
-    rounding are the reference's interface (vibeblade/moe_executor.py:31-54)."""
+    dispatches.  A dataclass with the reference's fields, order and defaults;
+    ``hit_rate`` and the ``to_dict`` keys and rounding are the reference's
+    interface (vibeblade/moe_executor.py:31-54)."""
 
-    __slots__ = _COUNTS + _TIMES_MS
-
-    def __init__(self, gpu_hits: int = 0, cpu_falls: int = 0, gpu_latency_ms: float = 0.0,
-                 cpu_latency_ms: float = 0.0, sync_latency_ms: float = 0.0):
-        self.gpu_hits, self.cpu_falls = gpu_hits, cpu_falls
-        self.gpu_latency_ms, self.cpu_latency_ms, self.sync_latency_ms = gpu_latency_ms, cpu_latency_ms, sync_latency_ms
+    gpu_hits: int = 0
+    cpu_falls: int = 0
+    gpu_latency_ms: float = 0.0
+    cpu_latency_ms: float = 0.0
+    sync_latency_ms: float = 0.0
 
     @property
     def hit_rate(self) -> float:
@@ -49,7 +51,7 @@ class ExecutorStats:
 
     def add(self, other: "ExecutorStats") -> "ExecutorStats":
         """Accumulate another record into this one (counts and times)."""
-        for name in self.__slots__:
+        for name in _COUNTS + _TIMES_MS:
             setattr(self, name, getattr(self, name) + getattr(other, name))
         return self
 
@@ -61,14 +63,6 @@ class ExecutorStats:
         d.update((name, round(getattr(self, name), 3)) for name in _TIMES_MS)
         d["hit_rate"] = round(self.hit_rate, 4)
         return d
-
-    def __eq__(self, other) -> bool:
-        if not isinstance(other, ExecutorStats):
-            return NotImplemented
-        return all(getattr(self, n) == getattr(other, n) for n in self.__slots__)
-
-    def __repr__(self) -> str:
-        return "ExecutorStats(" + ", ".join(f"{n}={getattr(self, n)!r}" for n in self.__slots__) + ")"
 
 
 class HotColdExecutor:

@@ -13,6 +13,7 @@ the two maps written as strings, since JSON keys are strings).
 from __future__ import annotations
 
 import json
+from dataclasses import dataclass
 
 import numpy as np
 
@@ -25,17 +26,19 @@ def _keys_to(layer_map: dict, conv) -> dict:
     return {conv(layer): list(ids) for layer, ids in layer_map.items()}
 
 
+@dataclass
 class HotColdMap:
-    """Per-layer hot and cold expert ids of a MoE model."""
+    """Per-layer hot and cold expert ids of a MoE model.  A dataclass with the
+    reference's fields, order and defaults, so ``dataclasses.asdict``,
+    ``replace``, ``fields`` and ``is_dataclass`` work on it as on the
+    reference's."""
 
-    def __init__(self, hot_experts: dict, cold_experts: dict, num_layers: int, num_experts: int,
-                 profile_tokens: int = 0, profile_dataset: str = ""):
-        self.hot_experts = hot_experts
-        self.cold_experts = cold_experts
-        self.num_layers = num_layers
-        self.num_experts = num_experts
-        self.profile_tokens = profile_tokens
-        self.profile_dataset = profile_dataset
+    hot_experts: dict    # {layer: [expert ids]} kept resident in HBM
+    cold_experts: dict   # {layer: [expert ids]} uploaded on first use
+    num_layers: int
+    num_experts: int
+    profile_tokens: int = 0
+    profile_dataset: str = ""
 
     # ---- queries ----------------------------------------------------------
 
@@ -89,11 +92,3 @@ class HotColdMap:
     def load(cls, path: str) -> "HotColdMap":
         with open(path) as f:
             return cls.from_json_dict(json.load(f))
-
-    def __eq__(self, other) -> bool:
-        if not isinstance(other, HotColdMap):
-            return NotImplemented
-        return all(getattr(self, n) == getattr(other, n) for n in _FIELDS)
-
-    def __repr__(self) -> str:
-        return "HotColdMap(" + ", ".join(f"{n}={getattr(self, n)!r}" for n in _FIELDS) + ")"
