@@ -52,7 +52,7 @@
 //
 // A k-step is 64 elements = chunk c of a super-block (Q4_K sub-blocks 2c,
 // 2c + 1); lane (j, g) of 16-row block a holds X[64 w + 16 a + j, 64 s + 32
-// ks + 8 g .. + 8) (natural k order, as q4k_bfrags_nat2 gives the weights).
+// ks + 8 g .. + 8) (natural k order, as q4k_bfrags_cvt gives the weights).
 #include "mfma_q4k.hpp"
 #include "vb_internal.hpp"
 #include "../../include/vbhip.h"
@@ -265,7 +265,6 @@ __global__ void __launch_bounds__(XR_THREADS) gemm_q4k_xr_kernel(const uint8_t* 
             ic[q] = i / NF;
             ifr[q] = i - NF * ic[q];
         }
-        const NatConsts kc = nat_consts();
         auto dequant_item = [&](int q, int rbuf, int buf) {
             const uint8_t* rw = reinterpret_cast<const uint8_t*>(raw + rbuf * RAW) + (16 * ifr[q] + j) * 144;
             const uint4 h = *reinterpret_cast<const uint4*>(rw);
@@ -273,7 +272,7 @@ __global__ void __launch_bounds__(XR_THREADS) gemm_q4k_xr_kernel(const uint8_t* 
             half2_t ds[2], nm[2];
             q4k_chunk_scales_sel(h, ic[q], ds, nm);
             Frag lo, hi;
-            q4k_bfrags_nat2(qs.x, qs.y, ds, nm, kc, lo, hi);
+            q4k_bfrags_cvt(qs.x, qs.y, ds, nm, lo, hi);
             uint4* dst = bt + buf * SB + ic[q] * SS + ifr[q] * 64 + lane;
             dst[0] = make_uint4(lo.u[0], lo.u[1], lo.u[2], lo.u[3]);
             dst[HS] = make_uint4(hi.u[0], hi.u[1], hi.u[2], hi.u[3]);

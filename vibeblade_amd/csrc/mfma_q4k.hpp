@@ -134,46 +134,30 @@ __device__ __forceinline__ void q4k_bfrags_nat(uint32_t q0, uint32_t q1, const h
     }
 }
 
-// Natural k order with one mask-and-or per nibble pair: after v_perm spreads
-// bytes (b0, b1) into the two halves, the low nibbles or-ed into 0x6400 give
-// the halves 1024 + q (exponent 2^10, ulp 1) and the high nibbles, left in
-// place (b & 0xF0), or-ed into 0x5400 give 64 + q (exponent 2^6, ulp 1/16);
-// both are exact.  Same results as q4k_bfrags_nat.
-// The four constants live in VGPRs (NatConsts): gfx9 VOP3 takes no literal
-// and one scalar operand at most, and without them the compiler splits each
-// v_and_or_b32 into an and plus an or.
-struct NatConsts {
-    uint32_t lo_mask, lo_or, hi_mask, hi_or;
-};
-
-__device__ __forceinline__ NatConsts nat_consts() {
-    NatConsts c;
-    // opaque to the optimizer so the values stay in registers
-    asm volatile("v_mov_b32 %0, 0x000F000F" : "=v"(c.lo_mask));
-    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(c.lo_or));
-    asm volatile("v_mov_b32 %0, 0x00F000F0" : "=v"(c.hi_mask));
-    asm volatile("v_mov_b32 %0, 0x54005400" : "=v"(c.hi_or));
-    return c;
-}
-
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(o));
-    return r;
-}
-
-__device__ __forceinline__ void q4k_bfrags_nat2(uint32_t q0, uint32_t q1, const half2_t* ds, const half2_t* nm,
-                                                const NatConsts& kc, Frag& lo, Frag& hi) {
-    const half2_t k1024 = half2_t{static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
-    const half2_t k64 = half2_t{static_cast<_Float16>(64.0f), static_cast<_Float16>(64.0f)};
-    const uint32_t src[4] = {__builtin_amdgcn_perm(0u, q0, 0x0C010C00u), __builtin_amdgcn_perm(0u, q0, 0x0C030C02u),
-                             __builtin_amdgcn_perm(0u, q1, 0x0C010C00u), __builtin_amdgcn_perm(0u, q1, 0x0C030C02u)};
+// Natural k order through the scaled fp8 -> fp16 conversion: a byte holding
+// a nibble q (0..15) is the OCP e4m3 code of q * 2^-9 exactly (codes 0..7
+// are the subnormals q/8 * 2^-6, codes 8..15 the first binade (1 + (q-8)/8)
+// * 2^-6), and v_cvt_scalef32_pk_f16_fp8 multiplies by the power of two in
+// its f32 scale, so scale 2^9 gives q as fp16 exactly, two per instruction.
+// One mask takes the four low nibbles of a word, a shift and a mask the four
+// high ones.  The fma then rounds q * d * sc - dmin * m once, as in
+// q4k_bfrags_nat: same results.
+__device__ __forceinline__ void q4k_bfrags_cvt(uint32_t q0, uint32_t q1, const half2_t* ds, const half2_t* nm,
+                                               Frag& lo, Frag& hi) {
+    const uint32_t l0 = q0 & 0x0F0F0F0Fu, l1 = q1 & 0x0F0F0F0Fu;
+    const uint32_t h0 = (q0 >> 4) & 0x0F0F0F0Fu, h1 = (q1 >> 4) & 0x0F0F0F0Fu;
+    const half2_t a[4] = {__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(l0, 512.0f, false),
+                          __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(l0, 512.0f, true),
+                          __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(l1, 512.0f, false),
+                          __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(l1, 512.0f, true)};
+    const half2_t b[4] = {__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(h0, 512.0f, false),
+                          __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(h0, 512.0f, true),
+                          __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(h1, 512.0f, false),
+                          __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(h1, 512.0f, true)};
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const half2_t a = bits2h(and_or(src[i], kc.lo_mask, kc.lo_or)) - k1024;
-        const half2_t b = bits2h(and_or(src[i], kc.hi_mask, kc.hi_or)) - k64;
-        lo.u[i] = h2bits(__builtin_elementwise_fma(a, ds[0], nm[0]));
-        hi.u[i] = h2bits(__builtin_elementwise_fma(b, ds[1], nm[1]));
+        lo.u[i] = h2bits(__builtin_elementwise_fma(a[i], ds[0], nm[0]));
+        hi.u[i] = h2bits(__builtin_elementwise_fma(b[i], ds[1], nm[1]));
     }
 }
 

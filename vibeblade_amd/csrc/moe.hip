@@ -265,11 +265,12 @@ __global__ void __launch_bounds__(PREP_THREADS) moe_prep_kernel(
     }
 }
 
-// gate/up: grid (ceil(i / 64), E), 8 waves.  A workgroup streams 64 rows of
-// the expert's gate and up matrices once per group of 16 routed slots (the
-// two matrices alternate in the tile's unit ring and share the activation
-// fragments) and writes silu(g) * u for every (slot, row) into hbuf as fp16
-// -- the down kernel rounds its activations to fp16 anyway.
+// gate/up: grid (ceil(i / 64), E).  A workgroup streams 64 rows of the
+// expert's gate and up matrices once per group of 16 routed slots (the tile
+// takes super-blocks in interleaved pairs, the gate units of a pair then its
+// up units, which share the activation fragments) and writes silu(g) * u for
+// every (slot, row) into hbuf as fp16 -- the down kernel rounds its
+// activations to fp16 anyway.
 // Four-wave workgroups with at most 256 VGPRs, so two run on each CU: one's
 // start-up and reduction overlap the other's weight stream.
 constexpr int MOE_WAVES = 4;
@@ -299,7 +300,7 @@ __global__ void __launch_bounds__(64 * NW, NW <= 4 ? 2 : 1) moe_gate_up_q4k(
         ta.xoff[0] = j < nrow ? (static_cast<uint32_t>(slots[m0 + j] / topk) * static_cast<uint32_t>(h) + 64u * g) * 2u
                            : skinny::X_NONE;
         float4_t s[2];
-        skinny::tile<skinny::X_F16, 2, 2, NW>(ta, reinterpret_cast<uint8_t*>(moe_lds), s);
+        skinny::tile<skinny::X_F16, 2, 2, NW, 1, true>(ta, reinterpret_cast<uint8_t*>(moe_lds), s);
         if (threadIdx.x < 256) {
             const int q = threadIdx.x >> 6, l = threadIdx.x & 63;
             const int r = 16 * q + (l & 15), n = ta.row0 + r;
@@ -344,7 +345,7 @@ __global__ void __launch_bounds__(64 * NW, NW <= 4 ? 2 : 1) moe_down_q4k(
         ta.xoff[0] = j < nrow ? (static_cast<uint32_t>(slots[m0 + j]) * static_cast<uint32_t>(i_dim) + 64u * g) * 2u
                            : skinny::X_NONE;
         float4_t s[1];
-        skinny::tile<skinny::X_F16, 1, 2, NW>(ta, reinterpret_cast<uint8_t*>(moe_lds), s);
+        skinny::tile<skinny::X_F16, 1, 2, NW, 1, true>(ta, reinterpret_cast<uint8_t*>(moe_lds), s);
         if (threadIdx.x < 256) {
             const int q = threadIdx.x >> 6, l = threadIdx.x & 63;
             const int r = 16 * q + (l & 15), n = ta.row0 + r;

@@ -115,7 +115,7 @@ __device__ __forceinline__ void load_xwords(__amdgpu_buffer_rsrc_t xr, uint32_t 
     }
 }
 
-// A fragments in natural k order (q4k_bfrags_nat2): fp16 words are used as
+// A fragments in natural k order (q4k_bfrags_cvt): fp16 words are used as
 // loaded, fp32 ones rounded to fp16.
 template <int XT>
 __device__ __forceinline__ void xwords_to_frags(const XWords<XT>& xw, Frag* a) {
@@ -154,15 +154,35 @@ struct TileArgs {
 // + m].  MT activation tiles (16 rows each) share every dequantized weight
 // fragment.  All threads of the workgroup must call it (it synchronises);
 // `lds` = the launch's dynamic LDS (lds_bytes<NW>()).
-template <int XT, int NMAT, int RING = 2, int NW = WAVES, int MT = 1>
+// PAIRS (fp16 X, one activation tile, a ring of two): super-blocks are taken
+// in pairs t, t + 1 (t even) and the pairs dealt round-robin over the waves
+// (pair p of wave w: t = 2 (NW p + w)); a wave issues the units of one
+// matrix for both super-blocks of its pair back to back (g(t), g(t + 1),
+// then u(t), u(t + 1) with two matrices g, u).  A 144-byte super-block slice
+// of a row always straddles two 128-byte lines; this way the two slices
+// sharing a line are requested together (same wave, or neighbouring waves
+// in the same period), and a period of the workgroup spans 2 NW super-blocks
+// = 9 NW lines of every row, so no line is shared across periods.  Without
+// it a line shared by units issued a period apart is fetched twice (the
+// MoE expert kernels read 1.3-1.6x their weight bytes).  The wave keeps no
+// weight load in flight while it computes; its workgroup and the other
+// workgroup on the CU cover that time.
+template <int XT, int NMAT, int RING = 2, int NW = WAVES, int MT = 1, bool PAIRS = false>
 __device__ __forceinline__ void tile(const TileArgs<NMAT, MT>& ta, uint8_t* lds, float4_t* out) {
     static_assert(MT * NMAT * 4096 <= STAGE, "the final sums must fit in the staging areas");
+    static_assert(!PAIRS || (RING == 2 && XT == X_F16 && MT == 1), "paired units: a ring of two, fp16 X, one token tile");
     const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int nsb = ta.nsb;
     const int sb0 = __builtin_amdgcn_readfirstlane((wave * nsb) / NW);
     const int sb1 = __builtin_amdgcn_readfirstlane(((wave + 1) * nsb) / NW);
-    const int nunits = (sb1 - sb0) * NMAT;  // 0 when nsb < 8 for some waves
+    const int nsbw = sb1 - sb0;             // the wave's super-blocks (0 when nsb < NW for some waves)
+    const int nunits = nsbw * NMAT;
+    // PAIRS: periods (one pair per wave); the wave's idx-th super-block
+    const int nper = (nsb + 2 * NW - 1) / (2 * NW);
+    auto sb_of = [&](int idx) __attribute__((always_inline)) -> int {
+        return 2 * (NW * (idx >> 1) + wave) + (idx & 1);
+    };
     uint8_t* stage = lds + wave * STAGE;
 
     // Pieces of this lane: p = 64 i + lane -> row p / 9, word p % 9 of the
@@ -182,7 +202,6 @@ __device__ __forceinline__ void tile(const TileArgs<NMAT, MT>& ta, uint8_t* lds,
     }
     constexpr uint32_t ES = XT == X_F16 ? 2u : 4u;
     const LaneScaleSel sel = lane_scale_sel(g);
-    const NatConsts kc = nat_consts();
 
     // Weight units run two ahead (ring of two register buffers); the
     // activations (L2-resident) one super-block ahead: gfx9 loads retire in
@@ -214,9 +233,20 @@ __device__ __forceinline__ void tile(const TileArgs<NMAT, MT>& ta, uint8_t* lds,
         }
         ++itw;
     };
+    // PAIRS: unit itw of period p = itw / (2 NMAT) is matrix mat (a constant
+    // of the caller) over the wave's super-block 2 p + slot
+    auto issue_wp = [&](auto slot_c, auto mat_c) __attribute__((always_inline)) {
+        constexpr int slot = decltype(slot_c)::value, mat = decltype(mat_c)::value;
+        int sb = sb_of(2 * (itw / (2 * NMAT)) + slot);
+        sb = sb < nsb - 1 ? sb : nsb - 1;  // padding units reload the last super-block
+#pragma unroll
+        for (int i = 0; i < PPL; i++)
+            pv[slot][i] = buf_ld128(ta.w[mat], poff[i], static_cast<uint32_t>(sb) * 144u);
+        ++itw;
+    };
     auto issue_x = [&](auto buf_c) __attribute__((always_inline)) {
         constexpr int buf = decltype(buf_c)::value % XB;
-        int sb = sb0 + itx;
+        int sb = PAIRS ? sb_of(itx) : sb0 + itx;
         sb = sb < nsb - 1 ? sb : nsb - 1;
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
@@ -234,9 +264,20 @@ __device__ __forceinline__ void tile(const TileArgs<NMAT, MT>& ta, uint8_t* lds,
     int ct = 0;
     auto compute = [&](auto u_c) __attribute__((always_inline)) {
         constexpr int u = decltype(u_c)::value;  // position in the period
-        constexpr int slot = RING == 1 ? 0 : u % 2, m = u % NMAT, xb = (u / NMAT) % 2;
-        if (ct >= nunits) return;  // padding unit (uniform)
-        if constexpr (m == 0) {
+        constexpr int slot = RING == 1 ? 0 : u % 2;
+        constexpr int m = PAIRS ? u / 2 : u % NMAT, xb = PAIRS ? u % 2 : (u / NMAT) % 2;
+        if constexpr (PAIRS) {
+            // padding units (uniform): super-blocks past the end, in the
+            // last period of some waves
+            const bool pad = sb_of(2 * (ct / (2 * NMAT)) + (u & 1)) >= nsb;
+            if (pad) {
+                ++ct;
+                return;
+            }
+        } else if (ct >= nunits) {
+            return;  // padding unit (uniform)
+        }
+        if constexpr (m == 0 && !PAIRS) {
             if constexpr (XT == X_F32) {
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++) xwords_to_frags<XT>(xw[mt][0], a[mt]);
@@ -275,7 +316,7 @@ __device__ __forceinline__ void tile(const TileArgs<NMAT, MT>& ta, uint8_t* lds,
 #pragma unroll
             for (int s = 0; s < 4; s++) {
                 Frag lo, hi;
-                q4k_bfrags_nat2(qd[2 * s], qd[2 * s + 1], ds, nm, kc, lo, hi);
+                q4k_bfrags_cvt(qd[2 * s], qd[2 * s + 1], ds, nm, lo, hi);
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++) {
                     acc[mt][m][q] = mfma16x16x32(afrag(mt, s), lo, acc[mt][m][q]);
@@ -290,7 +331,32 @@ __device__ __forceinline__ void tile(const TileArgs<NMAT, MT>& ta, uint8_t* lds,
     // computes P units and refills the ring two units ahead; the last period
     // issues nothing past the end.
     const int nunits_p = nunits <= P ? P : ((nunits + P - 1) / P) * P;
-    if constexpr (RING == 1) {
+    if constexpr (PAIRS) {
+        // Period: the activations of t, t + 1 and the first matrix's units
+        // of t, t + 1 are in flight; those units are computed, the second
+        // matrix's units issued and computed, then the next period's loads
+        // issued.
+        issue_x(std::integral_constant<int, 0>{});
+        issue_x(std::integral_constant<int, 1>{});
+        issue_wp(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+        issue_wp(std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{});
+        for (int pp = 0; pp < nper; pp++) {
+            compute(std::integral_constant<int, 0>{});
+            compute(std::integral_constant<int, 1>{});
+            if constexpr (NMAT == 2) {
+                issue_wp(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
+                issue_wp(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
+                compute(std::integral_constant<int, 2>{});
+                compute(std::integral_constant<int, 3>{});
+            }
+            if (pp + 1 < nper) {
+                issue_x(std::integral_constant<int, 0>{});
+                issue_x(std::integral_constant<int, 1>{});
+                issue_wp(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+                issue_wp(std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{});
+            }
+        }
+    } else if constexpr (RING == 1) {
         // one unit in flight per wave, refilled as soon as it is staged
         issue_w(std::integral_constant<int, 0>{});
         issue_x(std::integral_constant<int, 0>{});
