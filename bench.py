@@ -45,7 +45,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 TRAFFIC_FILE = os.path.join("profiles", "q4k_gemv_14336x4096_traffic.json")
-GEMV_KERNEL = "gemv_q4k_kernel<"  # the Q4_K short-row GEMV instantiations
+GEMV_KERNELS = ("gemv_q4k_dma_kernel<", "gemv_q4k_kernel<")  # the Q4_K short-row GEMV instantiations
 CALIB_BYTES = 256 << 20            # bytes read and written by the calibration copy
 MFMA_FP16_PEAK_TFS = 2500.0  # dense fp16 MFMA, MI355X
 NCOPIES = 16
@@ -802,7 +802,7 @@ def summarize_pmc(fetch_csv, write_csv):
     out = {}
     for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
         means = _counter_means(path, counter)
-        gemv = [(v, c, name) for name, (v, c) in means.items() if GEMV_KERNEL in name]
+        gemv = [(v, c, name) for name, (v, c) in means.items() if any(k in name for k in GEMV_KERNELS)]
         calib = [(v, c, name) for name, (v, c) in means.items() if "neg_kernel" in name]
         if not gemv or not calib:
             raise SystemExit(f"{path}: no {counter} rows for the GEMV or the calibration copy")
@@ -836,7 +836,9 @@ def run_floor(steps, warmup):
     replay stream):
       * vb_stream_read: the GEMV's grid (256 workgroups of 8 waves, 7 rows
         per wave) and row-contiguous non-temporal loads, nothing computed;
-        ring 3 is the GEMV's schedule, ring 0 issues a wave's 7 rows at once;
+        into registers (ring 3 is the register-ring GEMV's schedule, ring 0
+        issues a wave's 7 rows at once) or into LDS by DMA (DMA ring 2 is
+        the default GEMV's schedule);
       * torch.sum over the copy viewed as int32 (a vendor reduction kernel);
       * torch copy_ of the copy into a second buffer (reads and writes 33 MB);
       * vb_stream_read of one row (one workgroup): the launch cost alone."""
@@ -859,8 +861,9 @@ def run_floor(steps, warmup):
             return f
         return time_launches([mk(c) for c in copies], steps, warmup)
 
-    for ring in (3, 1, 2, 4, 6, 0):
-        what = "all 7 rows of a wave at once" if ring == 0 else f"ring {ring}"
+    for ring in (-2, -1, -3, 3, 1, 2, 4, 6, 0):
+        what = ("all 7 rows of a wave at once" if ring == 0 else
+                f"rows into LDS by DMA, ring {-ring}" if ring < 0 else f"rows into registers, ring {ring}")
         rows.append((f"read-only probe, GEMV shape and loads, {what}", probe(ring, n)))
     views = [c.data.reshape(-1).view(torch.int32) for c in copies]
     out = torch.empty((), dtype=torch.int64, device="cuda")

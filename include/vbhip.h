@@ -167,8 +167,10 @@ int vb_gemm_ws(const void* w, const void* x, int32_t x_dtype, float* y, int64_t 
  * shape and load pattern of the short-row Q4_K GEMV (one 8-wave workgroup
  * per CU slot, n / (CUs x 8) rows per wave, contiguous 16-byte
  * non-temporal pieces per row; `ring` rows loaded ahead of the row being
- * consumed, as the GEMV's ring of 3; 0 = all of a wave's rows at once) and
- * computes nothing from them: the time one launch
+ * consumed into registers, as the register-ring GEMV's ring of 3; 0 = all
+ * of a wave's rows at once; -1..-3 = 1..3 rows ahead landing in LDS by DMA,
+ * as the default GEMV's DMA ring of 2) and computes nothing from them: the
+ * time one launch
  * needs to read what the GEMV reads.  sink: 4 bytes of device memory the
  * kernel may write (it keeps the loads in the program).  No counterpart in
  * the reference: it exists for the bench's floor table. */

@@ -311,13 +311,20 @@ def _q4k_case(rows, k, seed):
 
 @pytest.mark.parametrize("wpg", [8, 16])
 @pytest.mark.parametrize("rpw", [1, 2, 3, 4, 5, 6, 7, 8])
-@pytest.mark.parametrize("ring", ["", "1", "2"])
-def test_gemv_q4k_short_rows_per_wave(knob, wpg, rpw, ring):
+@pytest.mark.parametrize("ring", ["", "1", "2", "3", "4"])
+@pytest.mark.parametrize("dma", ["", "0"])
+def test_gemv_q4k_short_rows_per_wave(knob, wpg, rpw, ring, dma):
     """Every rows-per-wave count with 8- and 16-wave workgroups (forced with
-    VB_GEMV_CFG), at each ring depth; three full workgroups and a ragged one."""
+    VB_GEMV_CFG), at each ring depth, 8-wave workgroups with the rows landing
+    in LDS by DMA (the default) and in the register ring (VB_GEMV_DMA=0);
+    three full workgroups and a ragged one."""
+    if wpg == 16 and dma == "0":
+        pytest.skip("16-wave workgroups always use the register ring")
     knob("VB_GEMV_CFG", f"{wpg},{rpw}")
     if ring:
         knob("VB_GEMV_RING", ring)
+    if dma:
+        knob("VB_GEMV_DMA", dma)
     rows = 3 * wpg * rpw + 5
     qt, x = _q4k_case(rows, 4096, 10 * wpg + rpw)
     y = gemv(qt, torch.from_numpy(x).cuda()).cpu().numpy()
@@ -568,6 +575,38 @@ def test_gemv_q4k_split_matches_general_kernel(knob):
     y_gen = gemv(qt, x).cpu().numpy()
     want = O.gemv(qt.to_numpy_bytes(), x.cpu().numpy(), rows, k, qt.qtype)
     assert O.rel_l2(y_split, want) <= 2e-4 and O.rel_l2(y_gen, want) <= 2e-4
+
+
+@pytest.mark.parametrize("rows,k", [(14336, 4096), (2047, 4096), (129, 2048), (17, 768), (1, 256)])
+def test_gemv_q4k_dma_rows_match_register_ring(knob, rows, k):
+    """Rows landing in LDS by DMA and rows through the register ring feed the
+    same arithmetic: the outputs are bit-identical."""
+    qt, x = _q4k_case(rows, k, 3 * rows + k)
+    xt = torch.from_numpy(x).cuda()
+    y_dma = gemv(qt, xt).cpu().numpy()
+    knob("VB_GEMV_DMA", "0")
+    y_reg = gemv(qt, xt).cpu().numpy()
+    assert np.array_equal(bits(y_dma), bits(y_reg))
+    want = O.gemv(qt.to_numpy_bytes(), x, rows, k, qt.qtype)
+    assert O.rel_l2(y_dma, want) <= GEMV_TOL
+
+
+def test_stream_read_probe_modes():
+    """The floor probe runs in its register and DMA modes and refuses rings
+    it does not have (it computes nothing: only the return codes are checked)."""
+    from vibeblade_amd import _lib
+    lib = _lib.load()
+    rows, k = 14336, 4096
+    rb = ggml.row_bytes(ggml.GGML_TYPE_Q4_K, k)
+    w = torch.zeros(rows * rb, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    for ring in (-3, -2, -1, 0, 1, 3, 8):
+        assert lib.vb_stream_read(w.data_ptr(), rows, rb, ring, sink.data_ptr(), s) == 0, ring
+    torch.cuda.synchronize()
+    assert int(sink.abs().sum()) == 0  # zeros fold to 0, never the sink's trigger value
+    for ring in (-4, 9):
+        assert lib.vb_stream_read(w.data_ptr(), rows, rb, ring, sink.data_ptr(), s) != 0, ring
 
 
 def test_gemv_q4k_short_matches_general_kernel(knob):

@@ -80,7 +80,27 @@ __device__ __forceinline__ int dpp_mov_i(int v) {
 // tasks of a unit sit on adjacent lanes.  Units at or past `units` encode
 // as zeros (their lanes contribute nothing).  US is the unit stride of the
 // encoding (the most units it holds).
-template <int US = UNITS_MAX>
+// LDS stores the compiler does not see (ds_write in asm; "memory" keeps
+// them in order with the surrounding code).  The DMA kernel's encode uses
+// them: a compiler-visible LDS store issued while LDS DMA is in flight gets
+// a full vmcnt(0) wait whenever the compiler cannot tell it apart from the
+// DMA's destination (merged ds_write2 stores lose that information).  The
+// caller makes them visible with lgkmcnt(0) before its barrier.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    typedef const __attribute__((address_space(3))) char* lds_cptr;
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_cptr)p));
+}
+__device__ __forceinline__ void lds_st64(void* p, uint2 v) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 d = {v.x, v.y};
+    asm volatile("ds_write_b64 %0, %1" : : "v"(lds_addr(p)), "v"(d) : "memory");
+}
+__device__ __forceinline__ void lds_st128(void* p, uint4 v) {
+    const u32x4 d = {v.x, v.y, v.z, v.w};
+    asm volatile("ds_write_b128 %0, %1" : : "v"(lds_addr(p)), "v"(d) : "memory");
+}
+
+template <int US = UNITS_MAX, bool ASM_ST = false>
 __device__ __forceinline__ void encode_task(const float* v_in, int task, int units, uint4* xq, bool store = true) {
     const int u = task >> 3, p = task & 7;
     float v[8];
@@ -112,15 +132,19 @@ __device__ __forceinline__ void encode_task(const float* v_in, int task, int uni
     const int isum1 = dpp_mov_i<0x141>(isum);   // part 0 reads run 1's sum from part 7
     if (!store) return;
     uint4* b = xq + u;
-    reinterpret_cast<uint2*>(&b[(p >> 1) * US])[p & 1] = make_uint2(ph[0], ph[1]);
-    reinterpret_cast<uint2*>(&b[(4 + (p >> 1)) * US])[p & 1] = make_uint2(pl[0], pl[1]);
-    if (p == 0) {
-        uint4 m;
-        m.x = __float_as_uint(amax / static_cast<float>(X15_MAX));
-        m.y = static_cast<uint32_t>(isum);
-        m.z = static_cast<uint32_t>(isum1);
-        m.w = static_cast<uint32_t>(128 * isum1);
-        b[8 * US] = m;
+    uint4 m;
+    m.x = __float_as_uint(amax / static_cast<float>(X15_MAX));
+    m.y = static_cast<uint32_t>(isum);
+    m.z = static_cast<uint32_t>(isum1);
+    m.w = static_cast<uint32_t>(128 * isum1);
+    if constexpr (ASM_ST) {
+        lds_st64(&reinterpret_cast<uint2*>(&b[(p >> 1) * US])[p & 1], make_uint2(ph[0], ph[1]));
+        lds_st64(&reinterpret_cast<uint2*>(&b[(4 + (p >> 1)) * US])[p & 1], make_uint2(pl[0], pl[1]));
+        if (p == 0) lds_st128(&b[8 * US], m);
+    } else {
+        reinterpret_cast<uint2*>(&b[(p >> 1) * US])[p & 1] = make_uint2(ph[0], ph[1]);
+        reinterpret_cast<uint2*>(&b[(4 + (p >> 1)) * US])[p & 1] = make_uint2(pl[0], pl[1]);
+        if (p == 0) b[8 * US] = m;
     }
 }
 
@@ -336,6 +360,129 @@ __global__ void __launch_bounds__(64 * WPG) gemv_q4k_kernel(const uint8_t* __res
         cur = nxt;
         __builtin_amdgcn_sched_barrier(0);
     }
+    const float tot = reduce8(acc);
+    const int g = lane >> 3;
+    const int r = row_of_group(g);
+    if ((lane & 7) == 0 && r < RPW && row0 + r < n) y[row0 + r] = tot;
+}
+
+// ---- The same GEMV with the rows landing in LDS by DMA ---------------------
+//
+// Rows are read with buffer_load ... lds: lane L's 16 bytes of a piece go
+// straight to LDS at slot L of the wave's ring buffer, so no row passes
+// through VGPRs and nothing is staged by hand; the wave reads its unit
+// layout (header, qs pieces) back from the slot when the row is due.  The
+// ring is NS slots per wave, each its own __shared__ array: the compiler's
+// wait counting for LDS DMA separates LDS objects, so reading slot s waits
+// only for the DMA of row s (loads retire in order: vmcnt = the loads issued
+// after it) and the x encoding's LDS traffic waits for none.  The encode is
+// published with lgkmcnt(0) and a bare s_barrier: __syncthreads' release
+// fence would wait for every DMA in flight.  Piece c is loaded by all 64
+// lanes (lanes 16..63 repeat lanes 0..15's addresses), so a slot holds
+// 192 16-byte slots, 144 of them the row.  Same arithmetic, same results as
+// gemv_q4k_kernel.
+constexpr int DMA_SLOTS = 192;
+
+template <int RPW, int NS>
+__global__ void __launch_bounds__(512) gemv_q4k_dma_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                                           float* __restrict__ y, int n, int units, uint32_t rb) {
+    static_assert(NS >= 2 && NS <= 5, "ring of 2..5 rows");
+    constexpr int WPG = 8;
+    __shared__ uint4 xq[XQ_UNIT_QUADS * UNITS_MAX];
+    __shared__ u32x4 ring0[WPG][DMA_SLOTS], ring1[WPG][DMA_SLOTS], ring2[WPG][DMA_SLOTS], ring3[WPG][DMA_SLOTS],
+            ring4[WPG][DMA_SLOTS];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int row0 = (static_cast<int>(blockIdx.x) * WPG + wave) * RPW;
+    const int rlast = n - 1;
+    const int rbase = row0 < rlast ? row0 : rlast;
+    const uint8_t* wb = w + static_cast<int64_t>(rbase) * rb;
+    const int64_t span64 = static_cast<int64_t>(n - rbase) * rb;
+    const uint32_t span = span64 < 0xFFFFFFFFll ? static_cast<uint32_t>(span64) : 0xFFFFFFFFu;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(wb, span);
+    const bool valid = lane < units;
+    const int u = valid ? lane : (lane & 3);
+    const int slots = static_cast<int>(rb >> 4);
+    const uint32_t va = 16u * static_cast<uint32_t>(lane < slots ? lane : lane & 7);
+    const uint32_t vb = 16u * static_cast<uint32_t>(64 + lane < slots ? 64 + lane : lane & 7);
+    const uint32_t vc = 16u * static_cast<uint32_t>(128 + (lane & 15) < slots ? 128 + (lane & 15) : lane & 7);
+    const int sh = 9 * (u >> 2), sq = sh + 1 + 2 * (u & 3);
+
+    auto slot_base = [&](auto k_c) __attribute__((always_inline)) -> u32x4* {
+        constexpr int k = decltype(k_c)::value;
+        if constexpr (k == 0) return ring0[wave];
+        else if constexpr (k == 1) return ring1[wave];
+        else if constexpr (k == 2) return ring2[wave];
+        else if constexpr (k == 3) return ring3[wave];
+        else return ring4[wave];
+    };
+    auto issue = [&](auto k_c, int s) __attribute__((always_inline)) {
+        int r = row0 + s;
+        r = r < rlast ? r : rlast;
+        const uint32_t so = static_cast<uint32_t>(r - rbase) * rb;
+        u32x4* b = slot_base(k_c);
+        typedef __attribute__((address_space(3))) void* lds_ptr;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)b, 16, static_cast<int>(va), static_cast<int>(so), 0,
+                                                 CACHE_NT);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(b + 64), 16, static_cast<int>(vb),
+                                                 static_cast<int>(so), 0, CACHE_NT);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(b + 128), 16, static_cast<int>(vc),
+                                                 static_cast<int>(so), 0, CACHE_NT);
+    };
+
+    float xv[8];
+    const int task = static_cast<int>(threadIdx.x);
+    {
+        const int tu = task >> 3;
+        const int off = (tu < units ? tu : units - 1) * 64 + 8 * (task & 7);
+        const float4 a = *reinterpret_cast<const float4*>(x + off);
+        const float4 b = *reinterpret_cast<const float4*>(x + off + 4);
+        xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
+        xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (NS - 1 >= 1) if (0 < RPW) issue(std::integral_constant<int, 0>{}, 0);
+    if constexpr (NS - 1 >= 2) if (1 < RPW) issue(std::integral_constant<int, 1>{}, 1);
+    if constexpr (NS - 1 >= 3) if (2 < RPW) issue(std::integral_constant<int, 2>{}, 2);
+    if constexpr (NS - 1 >= 4) if (3 < RPW) issue(std::integral_constant<int, 3>{}, 3);
+    __builtin_amdgcn_sched_barrier(0);
+    encode_task<UNITS_MAX, true>(xv, task, units, xq, true);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the encode is in LDS
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const XU xu = read_unit(xq, u);
+    const ScaleSel ss = make_sel(u & 3);
+
+    float acc[8];
+#pragma unroll
+    for (int s = 0; s < 8; s++) acc[s] = 0.f;
+    auto step = [&](auto s_c) __attribute__((always_inline)) {
+        constexpr int s = decltype(s_c)::value;
+        if constexpr (s < RPW) {
+            if constexpr (s + NS - 1 < RPW) issue(std::integral_constant<int, (s + NS - 1) % NS>{}, s + NS - 1);
+            // row s is complete once at most the loads issued after it remain
+            constexpr int after = 3 * (s + NS - 1 < RPW ? NS - 1 : RPW - 1 - s);
+            static_assert(after < 16, "vmcnt field");
+            __builtin_amdgcn_s_waitcnt(0x0F70 | after);
+            const u32x4* b = slot_base(std::integral_constant<int, s % NS>{});
+            RowBuf r;
+            r.hdr = b[sh];
+            r.qa = b[sq];
+            r.qb = b[sq + 1];
+            const float part = row_part(r, xu, ss);
+            acc[s] = valid ? part : 0.f;
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    step(std::integral_constant<int, 0>{});
+    step(std::integral_constant<int, 1>{});
+    step(std::integral_constant<int, 2>{});
+    step(std::integral_constant<int, 3>{});
+    step(std::integral_constant<int, 4>{});
+    step(std::integral_constant<int, 5>{});
+    step(std::integral_constant<int, 6>{});
+    step(std::integral_constant<int, 7>{});
     const float tot = reduce8(acc);
     const int g = lane >> 3;
     const int r = row_of_group(g);
@@ -1239,6 +1386,24 @@ void launch_rpw(int rpw, const void* w, const void* x, float* y, int n, int unit
     }
 }
 
+template <int NS>
+void launch_dma_rpw(int rpw, const void* w, const float* x, float* y, int n, int units, uint32_t rb,
+                    hipStream_t st) {
+    const int grid = (n + 8 * rpw - 1) / (8 * rpw);
+    const dim3 g(static_cast<uint32_t>(grid)), b(512);
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
+    switch (rpw) {
+    case 1: gemv_q4k_dma_kernel<1, NS><<<g, b, 0, st>>>(wb, x, y, n, units, rb); break;
+    case 2: gemv_q4k_dma_kernel<2, NS><<<g, b, 0, st>>>(wb, x, y, n, units, rb); break;
+    case 3: gemv_q4k_dma_kernel<3, NS><<<g, b, 0, st>>>(wb, x, y, n, units, rb); break;
+    case 4: gemv_q4k_dma_kernel<4, NS><<<g, b, 0, st>>>(wb, x, y, n, units, rb); break;
+    case 5: gemv_q4k_dma_kernel<5, NS><<<g, b, 0, st>>>(wb, x, y, n, units, rb); break;
+    case 6: gemv_q4k_dma_kernel<6, NS><<<g, b, 0, st>>>(wb, x, y, n, units, rb); break;
+    case 7: gemv_q4k_dma_kernel<7, NS><<<g, b, 0, st>>>(wb, x, y, n, units, rb); break;
+    default: gemv_q4k_dma_kernel<8, NS><<<g, b, 0, st>>>(wb, x, y, n, units, rb); break;
+    }
+}
+
 template <int TYPE, int G, int NS, bool XH>
 void launch_short(const void* w, const void* x, float* y, int n, int units, uint32_t rb, int rpw,
                   hipStream_t st) {
@@ -1324,7 +1489,19 @@ int gemv_q4k_short(const void* w, const void* x, float* y, int64_t n, int64_t k,
             launch_rpw<4, 16, true>(sh.rpw, w, x, y, ni, units, rb, st);
         return check_launch("vb_gemm");
     }
-    const int ring = knobs().gemv_ring;  // NS - 1 rows in flight while computing (default 3)
+    // NS - 1 rows in flight while computing: default 2 with the rows landing
+    // in LDS by DMA, 3 with the register ring (VB_GEMV_DMA=0).  On MI355X at
+    // 14336 x 4096: DMA 6.98 us (ring 2), 7.07-7.09 (ring 3), 7.15 (ring 4);
+    // register ring 7.24 us.
+    const int ring = knobs().gemv_ring;
+    if (sh.wpg == 8 && knobs().gemv_dma) {
+        const float* xf = static_cast<const float*>(x);
+        if (ring == 1) launch_dma_rpw<2>(sh.rpw, w, xf, y, ni, units, rb, st);
+        else if (ring == 3) launch_dma_rpw<4>(sh.rpw, w, xf, y, ni, units, rb, st);
+        else if (ring >= 4) launch_dma_rpw<5>(sh.rpw, w, xf, y, ni, units, rb, st);
+        else launch_dma_rpw<3>(sh.rpw, w, xf, y, ni, units, rb, st);
+        return check_launch("vb_gemv");
+    }
     if (sh.wpg == 8) {
         if (ring == 1) launch_rpw<2, 8>(sh.rpw, w, x, y, ni, units, rb, st);
         else if (ring == 2) launch_rpw<3, 8>(sh.rpw, w, x, y, ni, units, rb, st);

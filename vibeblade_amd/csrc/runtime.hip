@@ -32,6 +32,7 @@ Knobs read_knobs() {
         const int d = std::atoi(e);
         if (d >= 1 && d <= 6) k.gemv_ring = d;  // the general kernel takes 1..4
     }
+    if (const char* e = std::getenv("VB_GEMV_DMA")) k.gemv_dma = std::atoi(e) != 0;
     if (const char* e = std::getenv("VB_GEMV_CFG")) {
         int a = 0, b = 0;
         if (std::sscanf(e, "%d,%d", &a, &b) == 2 && a >= 1 && b >= 1) {
