@@ -146,7 +146,13 @@ int vb_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k,
  * (cpp/include/cuda_kernels.h, cpp/src/cuda_kernels.cu:184-212).
  * Weight types: Q4_K (variants 0-4), Q6_K and Q8_0 (variants 0, 2, 4; Q8_0
  * needs k % 128 == 0 at every m, m == 1 included, although vb_gemv itself
- * takes Q8_0 rows of any whole number of blocks).  W and x 16-byte aligned. */
+ * takes Q8_0 rows of any whole number of blocks); Q4_0, Q4_1, Q5_0, Q5_1,
+ * Q5_K, Q2_K, Q3_K, BF16 and F32 (variants 0, 2; k % 256 == 0 except on the
+ * GEMV) decoded once to fp16 (each value rounded once) into n x k x 2 bytes
+ * of workspace and multiplied on the tiled kernel, and F16 on the tiled
+ * kernel in place; vb_gemm allocates that workspace on the stream for the
+ * call (stream-ordered), vb_gemm_ws takes it from the caller.  W and x
+ * 16-byte aligned. */
 int vb_gemm(const void* w, const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n,
             int64_t k, int32_t ggml_type, int32_t variant, void* stream);
 /* vb_gemm with a caller-owned workspace, which lets variant 0 (and variant 5)
@@ -155,7 +161,8 @@ int vb_gemm(const void* w, const void* x, int32_t x_dtype, float* y, int64_t m, 
  * MFMA waves load their A fragments from it directly and only the
  * dequantized weight tile goes through LDS.  vb_gemm_workspace returns the
  * bytes variant `variant` needs for the shape (0: none, then vb_gemm_ws is
- * vb_gemm); the workspace must be 16-byte aligned.  Same reference path as
+ * vb_gemm; the fp16 decode of the types without a fused decoder, n x k x 2,
+ * at any x_dtype); the workspace must be 16-byte aligned.  Same reference path as
  * vb_gemm (cpp/src/fast_model.cpp:644-669, :905-960); the reference's
  * batched loop has no workspace (its scratch row is decoded per token). */
 int64_t vb_gemm_workspace(int64_t m, int64_t n, int64_t k, int32_t ggml_type, int32_t x_dtype, int32_t variant);

@@ -555,3 +555,66 @@ def test_ksplit_q4k(dtype, m, n, k):
     assert O.rel_l2(y, want) <= TOL
     other = gemm(qt, xt, variant=GEMM_SKINNY if m == 1 else GEMM_AUTO).cpu().numpy()
     assert O.rel_l2(y, other) <= 1e-5
+
+
+# ---- the other GGUF types: decoded once to fp16, then the tiled kernel ------
+
+OTHER_TYPES = [ggml.GGML_TYPE_Q4_0, ggml.GGML_TYPE_Q4_1, ggml.GGML_TYPE_Q5_0, ggml.GGML_TYPE_Q5_1,
+               ggml.GGML_TYPE_Q5_K, ggml.GGML_TYPE_Q2_K, ggml.GGML_TYPE_Q3_K, ggml.GGML_TYPE_BF16,
+               ggml.GGML_TYPE_F16, ggml.GGML_TYPE_F32]
+
+
+def make_other(qtype, n, k, seed):
+    """Weights of `qtype` as raw GGUF bytes: random blocks with moderate
+    scales for the block types, N(0, 0.02) values for the plain ones."""
+    if qtype in (ggml.GGML_TYPE_F32, ggml.GGML_TYPE_F16, ggml.GGML_TYPE_BF16):
+        w = (np.random.default_rng(seed).standard_normal((n, k)) * 0.02).astype(np.float32)
+        if qtype == ggml.GGML_TYPE_F32:
+            raw = w.view(np.uint8)
+        elif qtype == ggml.GGML_TYPE_F16:
+            raw = w.astype(np.float16).view(np.uint8)
+        else:
+            raw = (w.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8)
+        return QTensor.from_bytes(np.ascontiguousarray(raw).reshape(n, -1), qtype, n, k)
+    from qblocks import rand_qblocks
+    return QTensor.from_bytes(rand_qblocks(qtype, n, k, seed), qtype, n, k)
+
+
+@pytest.mark.parametrize("qtype", OTHER_TYPES)
+@pytest.mark.parametrize("m,n,k,dtype", [(8, 300, 512, torch.float16), (65, 200, 768, torch.float32),
+                                         (1, 129, 256, torch.float16), (300, 1000, 1024, torch.float16),
+                                         (2, 64, 4096, torch.float32)])
+def test_gemm_other_types(qtype, m, n, k, dtype):
+    """Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q5_K / Q2_K / Q3_K / BF16 / F32 weights are
+    decoded once to fp16 (one rounding, as the fused decoders round) and run
+    on the tiled kernel; F16 weights in place.  Against the fp64 product of
+    the oracle's decode; the workspace the call asks for; without a
+    workspace (decoded into a stream-ordered allocation) the same bits."""
+    lib = _lib.load()
+    qt = make_other(qtype, n, k, m + n + k + qtype)
+    x = np.random.default_rng(m + k).standard_normal((m, k)).astype(np.float32)
+    xt = torch.from_numpy(x).to("cuda", dtype)
+    xdt = 1 if dtype == torch.float16 else 0
+    want_ws = 0 if qtype == ggml.GGML_TYPE_F16 or (m == 1 and xdt == 0) else n * k * 2
+    assert lib.vb_gemm_workspace(m, n, k, qtype, xdt, 0) == want_ws
+    y = gemm(qt, xt).cpu().numpy()
+    want = ref_gemm(qt, xt.float().cpu().numpy())
+    assert y.shape == (m, n) and np.all(np.isfinite(y))
+    assert O.rel_l2(y, want) <= TOL
+    out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    rc = lib.vb_gemm(qt.ptr(), xt.data_ptr(), xdt, out.data_ptr(), m, n, k, qtype, 0, s)
+    assert rc == 0
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), y.view(np.uint32))
+
+
+def test_gemm_other_types_rejects():
+    """Shapes and variants the fp16-decode path does not take fail with a
+    clear error: K not a multiple of 256 at M >= 2, a variant other than 0 / 2."""
+    qt = make_other(ggml.GGML_TYPE_Q4_0, 64, 288, 5)
+    xt = torch.randn((4, 288), device="cuda", dtype=torch.float16)
+    with pytest.raises(VBError, match="256"):
+        gemm(qt, xt)
+    qt = make_other(ggml.GGML_TYPE_Q5_K, 64, 512, 6)
+    with pytest.raises(VBError, match="tiled kernel only"):
+        gemm(qt, torch.randn((4, 512), device="cuda", dtype=torch.float16), variant=GEMM_SKINNY)

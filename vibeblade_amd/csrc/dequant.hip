@@ -216,6 +216,34 @@ __global__ void __launch_bounds__(256) dequant_plain_kernel(const uint8_t* __res
         out[i] = __half2float(reinterpret_cast<const __half*>(w)[i]);
 }
 
+// The same decode with each value rounded once to fp16 (round to nearest
+// even): the weight operand of the batched kernels for the types that have
+// no fused decoder (gemm.hip).  Four elements a thread; plain types take
+// the fp32 / bf16 value as is before the rounding.
+template <int TYPE>
+__global__ void __launch_bounds__(256) dequant_f16_kernel(const uint8_t* __restrict__ w, _Float16* __restrict__ out,
+                                                          int64_t n_groups, int64_t k, int64_t rb) {
+    const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (g >= n_groups) return;
+    const int64_t gpr = k / 4;
+    const int64_t row = g / gpr;
+    const int64_t e0 = (g - row * gpr) * 4;
+    float4 y;
+    if constexpr (TYPE == TYPE_F32) {
+        y = *reinterpret_cast<const float4*>(w + row * rb + e0 * 4);
+    } else if constexpr (TYPE == TYPE_BF16) {
+        const uint2 v = *reinterpret_cast<const uint2*>(w + row * rb + e0 * 2);
+        y = make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xFFFF0000u), __uint_as_float(v.y << 16),
+                        __uint_as_float(v.y & 0xFFFF0000u));
+    } else {
+        y = decode4<TYPE>(w + row * rb, e0);
+    }
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const h4 h = {static_cast<_Float16>(y.x), static_cast<_Float16>(y.y), static_cast<_Float16>(y.z),
+                  static_cast<_Float16>(y.w)};
+    *reinterpret_cast<h4*>(out + row * k + e0) = h;
+}
+
 // ---- quantizers (one thread per block) ------------------------------------
 
 __device__ __forceinline__ void st_u16(uint8_t* p, uint16_t v) {
@@ -342,6 +370,39 @@ int launch_quantize(const float* src, void* w, int64_t n_blocks, hipStream_t st)
 }
 
 }  // namespace
+
+// n_rows x k of W (any decodable type but F16) as row-major fp16 at out
+// (16-byte aligned, k % 4 == 0); the caller has checked the type and k.
+int dequant_rows_f16(const void* w, _Float16* out, int64_t n_rows, int64_t k, int32_t type, hipStream_t st) {
+    const int64_t rb = row_bytes(type, k);
+    const int64_t n_groups = n_rows * (k / 4);
+    const int64_t grid = (n_groups + 255) / 256;
+    if (rb < 0 || k % 4 != 0 || grid > 0x7fffffff) {
+        set_error("vb_gemm: cannot decode %lld x %lld of type %d to fp16", static_cast<long long>(n_rows),
+                  static_cast<long long>(k), type);
+        return E_INVAL;
+    }
+    if (n_rows == 0) return OK;
+    const dim3 g(static_cast<uint32_t>(grid)), b(256);
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
+    switch (type) {
+    case TYPE_F32: dequant_f16_kernel<TYPE_F32><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
+    case TYPE_BF16: dequant_f16_kernel<TYPE_BF16><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
+    case TYPE_Q4_K: dequant_f16_kernel<TYPE_Q4_K><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
+    case TYPE_Q6_K: dequant_f16_kernel<TYPE_Q6_K><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
+    case TYPE_Q8_0: dequant_f16_kernel<TYPE_Q8_0><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
+    case TYPE_Q5_K: dequant_f16_kernel<TYPE_Q5_K><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
+    case TYPE_Q2_K: dequant_f16_kernel<TYPE_Q2_K><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
+    case TYPE_Q3_K: dequant_f16_kernel<TYPE_Q3_K><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
+    case TYPE_Q4_0: dequant_f16_kernel<TYPE_Q4_0><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
+    case TYPE_Q4_1: dequant_f16_kernel<TYPE_Q4_1><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
+    case TYPE_Q5_0: dequant_f16_kernel<TYPE_Q5_0><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
+    case TYPE_Q5_1: dequant_f16_kernel<TYPE_Q5_1><<<g, b, 0, st>>>(wb, out, n_groups, k, rb); break;
+    default: set_error("vb_gemm: no fp16 decode for type %d", type); return E_UNSUPPORTED;
+    }
+    return check_launch("vb_gemm");
+}
+
 }  // namespace vb
 
 using namespace vb;

@@ -179,6 +179,28 @@ struct TiledW<TYPE_Q8_0> {
     }
 };
 
+// fp16 weights, row-major (a GGUF F16 tensor, or any other type decoded to
+// fp16 first): lane (row, ug) of a step's fragments is elements 8 ug .. +7
+// and 32 + 8 ug .. +7 of the step's 64, 16 bytes each, used as loaded.
+template <>
+struct TiledW<TYPE_F16> {
+    static constexpr bool kPairOrder = false;
+    struct Raw {
+        u32x4 lo, hi;
+    };
+    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t w, uint32_t rowoff, int step, uint32_t g8,
+                                                 Raw& r) {
+        const uint32_t base = rowoff + static_cast<uint32_t>(step) * 128u + 2u * g8;
+        r.lo = buf_ld128(w, base, 0);
+        r.hi = buf_ld128(w, base + 64u, 0);
+    }
+    __device__ static __forceinline__ void decode(const Raw& r, uint32_t, int, uint32_t, const KqConsts&, Frag& lo,
+                                                  Frag& hi) {
+        lo.u[0] = r.lo.x; lo.u[1] = r.lo.y; lo.u[2] = r.lo.z; lo.u[3] = r.lo.w;
+        hi.u[0] = r.hi.x; hi.u[1] = r.hi.y; hi.u[2] = r.hi.z; hi.u[3] = r.hi.w;
+    }
+};
+
 // KS = 2 splits K in halves between two groups of WM x WN waves, each with
 // its own LDS stage (the tiles below); both run the same number of steps, so
 // the one barrier per step serves both.  At the end group 1 hands its
@@ -583,10 +605,75 @@ int tiled_zsplit(int type, int x_dtype, int64_t M, int64_t N, int64_t K) {
     return 1;
 }
 
+// The types without a fused decoder: Q4_0, Q4_1, Q5_0, Q5_1, Q5_K, Q2_K, Q3_K,
+// BF16 and F32 weights are decoded once to fp16 (each value rounded once, as
+// the fused decoders round) into the workspace, then multiplied on the tiled
+// kernel with fp16 weights; F16 weights are used in place.  The workspace,
+// n x k x 2 bytes (none for F16), comes from the caller (vb_gemm_ws) or is
+// allocated on the stream for the call (hipMallocAsync / hipFreeAsync).
+bool gemm_other_type(int32_t type) {
+    return type == TYPE_F32 || type == TYPE_F16 || type == TYPE_BF16 || type == TYPE_Q4_0 || type == TYPE_Q4_1 ||
+           type == TYPE_Q5_0 || type == TYPE_Q5_1 || type == TYPE_Q5_K || type == TYPE_Q2_K || type == TYPE_Q3_K;
+}
+
+int64_t gemm_other_workspace(int32_t type, int64_t N, int64_t K) { return type == TYPE_F16 ? 0 : N * K * 2; }
+
+int gemm_other(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, int64_t N, int64_t K, int32_t type,
+               int32_t variant, void* ws, size_t ws_bytes, hipStream_t st) {
+    if (variant != 0 && variant != 2) {
+        set_error("vb_gemm: type %d runs the tiled kernel only (variant 0 or 2, got %d)", type, variant);
+        return E_UNSUPPORTED;
+    }
+    if (K % 256 != 0) {
+        set_error("vb_gemm: type %d needs K %% 256 == 0 for M >= 2 or fp16 X (K=%lld)", type,
+                  static_cast<long long>(K));
+        return E_UNSUPPORTED;
+    }
+    const int64_t xbytes = M * K * (x_dtype == X_F16 ? 2 : 4);
+    const int64_t wbytes = N * K * 2;
+    if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX || wbytes >= (int64_t(1) << 32) ||
+        xbytes >= (int64_t(1) << 32)) {
+        set_error("vb_gemm: shape too large (M=%lld N=%lld K=%lld)", static_cast<long long>(M),
+                  static_cast<long long>(N), static_cast<long long>(K));
+        return E_INVAL;
+    }
+    const uint8_t* wf = static_cast<const uint8_t*>(w);
+    void* own = nullptr;
+    int rc = OK;
+    if (type != TYPE_F16) {
+        void* buf = ws;
+        if (!buf || static_cast<int64_t>(ws_bytes) < wbytes || reinterpret_cast<uintptr_t>(buf) % 16) {
+            if (hipMallocAsync(&own, static_cast<size_t>(wbytes), st) != hipSuccess) {
+                (void)hipGetLastError();
+                set_error("vb_gemm: could not allocate %lld bytes for the fp16 weights", static_cast<long long>(wbytes));
+                return E_NOMEM;
+            }
+            buf = own;
+        }
+        rc = dequant_rows_f16(w, static_cast<_Float16*>(buf), N, K, type, st);
+        wf = static_cast<const uint8_t*>(buf);
+    }
+    if (rc == OK) {
+        const TileCfg cfg = tiled_cfg(TYPE_F16, x_dtype, M, N, K);
+        const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
+        rc = x_dtype == X_F16 ? launch_tiled<TYPE_F16, X_F16>(cfg, wf, static_cast<uint32_t>(wbytes), X, Y, m, n, k,
+                                                              K * 2, st)
+                              : launch_tiled<TYPE_F16, X_F32>(cfg, wf, static_cast<uint32_t>(wbytes), X, Y, m, n, k,
+                                                              K * 2, st);
+        if (rc == OK) rc = check_launch("vb_gemm");
+    }
+    if (own && hipFreeAsync(own, st) != hipSuccess && rc == OK) {
+        (void)hipGetLastError();
+        set_error("vb_gemm: could not free the fp16 weights");
+        rc = E_HIP;
+    }
+    return rc;
+}
+
 int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, int64_t N, int64_t K,
                   int32_t type, int32_t variant, void* ws, size_t ws_bytes, hipStream_t st) {
-    if (type != TYPE_Q4_K && type != TYPE_Q6_K && type != TYPE_Q8_0) {
-        set_error("vb_gemm: weight type %d has no MFMA path (Q4_K, Q6_K, Q8_0)", type);
+    if (type != TYPE_Q4_K && type != TYPE_Q6_K && type != TYPE_Q8_0 && !gemm_other_type(type)) {
+        set_error("vb_gemm: weight type %d has no batched path", type);
         return E_UNSUPPORTED;
     }
     const int64_t rb = row_bytes(type, K);
@@ -632,6 +719,7 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
         if (type != TYPE_Q4_K && !general && K > 4096 && gemv_split_rpw(type, N, K) > 0)
             return gemv_split(type, w, X, Y, nullptr, N, K, st, true);
     }
+    if (gemm_other_type(type)) return gemm_other(w, X, x_dtype, Y, M, N, K, type, variant, ws, ws_bytes, st);
     bool tiled = false;
     if (type != TYPE_Q4_K) {
         // Q6_K / Q8_0: the K-split kernel (gemm_kq.hip) up to M = 64, where
@@ -772,7 +860,11 @@ extern "C" int vb_gemm(const void* w, const void* x, int32_t x_dtype, float* y, 
 
 extern "C" int64_t vb_gemm_workspace(int64_t m, int64_t n, int64_t k, int32_t ggml_type, int32_t x_dtype,
                                      int32_t variant) {
-    if (k <= 0 || k % 256 != 0 || m <= 0 || n <= 0 || x_dtype != 1) return 0;
+    if (k <= 0 || k % 256 != 0 || m <= 0 || n <= 0) return 0;
+    // the other types: their fp16 decode (none where the call runs the GEMV)
+    if (vb::gemm_other_type(ggml_type))
+        return m == 1 && x_dtype == 0 && variant == 0 ? 0 : vb::gemm_other_workspace(ggml_type, n, k);
+    if (x_dtype != 1) return 0;
     if (ggml_type == vb::TYPE_Q6_K || ggml_type == vb::TYPE_Q8_0) {
         // the tiled kernel's K splits: one fp32 partial product each
         const int zs = variant == 0 ? vb::tiled_zsplit(ggml_type, x_dtype, m, n, k) : 1;

@@ -148,6 +148,13 @@ int gemm_ksum(const float* P, float* Y, int64_t total, int ks, hipStream_t st);
 // K splits of the tiled GEMM between workgroups for this shape (1: none; gemm.hip).
 int tiled_zsplit(int type, int x_dtype, int64_t M, int64_t N, int64_t K);
 int64_t gemm_q4k_xr_workspace(int64_t M, int64_t N, int64_t K);
+// n_rows x k of W (a decodable type other than F16) as row-major fp16 at out,
+// each value rounded once (dequant.hip; k % 4 == 0, out 16-byte aligned).
+int dequant_rows_f16(const void* w, _Float16* out, int64_t n_rows, int64_t k, int32_t type, hipStream_t st);
+// Weight types the batched GEMM runs through their fp16 decode (gemm.hip),
+// and the workspace that decode needs (n x k x 2 bytes; 0 for F16).
+bool gemm_other_type(int32_t type);
+int64_t gemm_other_workspace(int32_t type, int64_t N, int64_t K);
 int gemm_q4k_xr(const void* w, const void* X, float* Y, int64_t M, int64_t N, int64_t K, void* ws, hipStream_t st);
 // Q6_K / Q8_0 GEMM, every M (gemm_kq.hip); pointers, alignment, x_dtype and
 // M, N > 0 already validated.
