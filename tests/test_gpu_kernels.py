@@ -577,10 +577,12 @@ def test_gemv_q4k_split_matches_general_kernel(knob):
     assert O.rel_l2(y_split, want) <= 2e-4 and O.rel_l2(y_gen, want) <= 2e-4
 
 
-@pytest.mark.parametrize("rows,k", [(14336, 4096), (2047, 4096), (129, 2048), (17, 768), (1, 256)])
+@pytest.mark.parametrize("rows,k", [(14336, 4096), (2047, 4096), (129, 2048), (17, 768), (1, 256),
+                                    (4096, 14336), (129, 8192), (5, 16384)])
 def test_gemv_q4k_dma_rows_match_register_ring(knob, rows, k):
-    """Rows landing in LDS by DMA and rows through the register ring feed the
-    same arithmetic: the outputs are bit-identical."""
+    """Rows (k <= 4096) or row slices (the split-row kernel, k > 4096) landing
+    in LDS by DMA and the same through the register ring feed the same
+    arithmetic: the outputs are bit-identical."""
     qt, x = _q4k_case(rows, k, 3 * rows + k)
     xt = torch.from_numpy(x).cuda()
     y_dma = gemv(qt, xt).cpu().numpy()

@@ -1178,6 +1178,128 @@ __global__ void __launch_bounds__(1024) gemv_q4k_split_kernel(const uint8_t* __r
     }
 }
 
+// The split-row kernel with the slices landing in LDS by DMA (fp32 x), as
+// gemv_q4k_dma_kernel does for short rows: one __shared__ array per ring
+// slot, the encode written with asm stores and published with lgkmcnt(0) and
+// a bare s_barrier, explicit vmcnt waits for each row.  Same arithmetic and
+// results as gemv_q4k_split_kernel.
+template <int RPW, int NS, int SL>
+__global__ void __launch_bounds__(1024) gemv_q4k_split_dma_kernel(const uint8_t* __restrict__ w,
+                                                                  const float* __restrict__ x, float* y,
+                                                                  const float* resid, int n, int units, int upw,
+                                                                  uint32_t rb) {
+    static_assert(NS >= 2 && NS <= 3, "ring of 2..3 slices");
+    constexpr int WPG = 16;
+    constexpr int NG = WPG / SL;
+    __shared__ uint4 xq[XQ_UNIT_QUADS * SPLIT_US];
+    __shared__ u32x4 ring0[WPG][128], ring1[WPG][128], ring2[WPG][128];
+    __shared__ float red[NG][SL][8];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int grp = wave / SL, slc = wave - grp * SL;
+    const int row0 = (static_cast<int>(blockIdx.x) * NG + grp) * RPW;
+    const int rlast = n - 1;
+    const int rbase = row0 < rlast ? row0 : rlast;
+    const int u0 = slc * upw;
+    const int su = units - u0 < upw ? units - u0 : upw;
+    const uint8_t* wb = w + static_cast<int64_t>(rbase) * rb + 36u * static_cast<uint32_t>(u0);
+    const int64_t span64 = static_cast<int64_t>(n - rbase) * rb - 36 * static_cast<int64_t>(u0);
+    const uint32_t span = span64 < 0xFFFFFFFFll ? static_cast<uint32_t>(span64) : 0xFFFFFFFFu;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(wb, span);
+    const bool valid = lane < su;
+    const int u = valid ? lane : (lane & 3);
+    const int sslots = 9 * su / 4;
+    const uint32_t va = 16u * static_cast<uint32_t>(lane < sslots ? lane : lane & 7);
+    const uint32_t vb = 16u * static_cast<uint32_t>(64 + lane < sslots ? 64 + lane : lane & 7);
+    const int sh = 9 * (u >> 2), sq = sh + 1 + 2 * (u & 3);
+
+    auto slot_base = [&](auto k_c) __attribute__((always_inline)) -> u32x4* {
+        constexpr int k = decltype(k_c)::value;
+        if constexpr (k == 0) return ring0[wave];
+        else if constexpr (k == 1) return ring1[wave];
+        else return ring2[wave];
+    };
+    auto issue = [&](auto k_c, int s) __attribute__((always_inline)) {
+        int r = row0 + s;
+        r = r < rlast ? r : rlast;
+        const uint32_t so = static_cast<uint32_t>(r - rbase) * rb;
+        u32x4* b = slot_base(k_c);
+        typedef __attribute__((address_space(3))) void* lds_ptr;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)b, 16, static_cast<int>(va), static_cast<int>(so), 0,
+                                                 CACHE_NT);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(b + 64), 16, static_cast<int>(vb),
+                                                 static_cast<int>(so), 0, CACHE_NT);
+    };
+
+    float xv[2][8];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const int task = static_cast<int>(threadIdx.x) + 1024 * t;
+        const int tu = task >> 3;
+        const int off = (tu < units ? tu : units - 1) * 64 + 8 * (task & 7);
+        const float4 a = *reinterpret_cast<const float4*>(x + off);
+        const float4 b = *reinterpret_cast<const float4*>(x + off + 4);
+        xv[t][0] = a.x; xv[t][1] = a.y; xv[t][2] = a.z; xv[t][3] = a.w;
+        xv[t][4] = b.x; xv[t][5] = b.y; xv[t][6] = b.z; xv[t][7] = b.w;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (NS - 1 >= 1) issue(std::integral_constant<int, 0>{}, 0);
+    if constexpr (NS - 1 >= 2) if (1 < RPW) issue(std::integral_constant<int, 1>{}, 1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+        encode_task<SPLIT_US, true>(xv[t], static_cast<int>(threadIdx.x) + 1024 * t, units, xq);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the encode is in LDS
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const XU xu = read_unit<SPLIT_US>(xq, u0 + u);
+    const ScaleSel ss = make_sel(u & 3);
+
+    float acc[8];
+#pragma unroll
+    for (int s = 0; s < 8; s++) acc[s] = 0.f;
+    auto step = [&](auto s_c) __attribute__((always_inline)) {
+        constexpr int s = decltype(s_c)::value;
+        if constexpr (s < RPW) {
+            if constexpr (s + NS - 1 < RPW) issue(std::integral_constant<int, (s + NS - 1) % NS>{}, s + NS - 1);
+            constexpr int after = 2 * (s + NS - 1 < RPW ? NS - 1 : RPW - 1 - s);
+            __builtin_amdgcn_s_waitcnt(0x0F70 | after);
+            const u32x4* b = slot_base(std::integral_constant<int, s % NS>{});
+            RowBuf rw;
+            rw.hdr = b[sh];
+            rw.qa = b[sq];
+            rw.qb = b[sq + 1];
+            const float part = row_part(rw, xu, ss);
+            acc[s] = valid ? part : 0.f;
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    step(std::integral_constant<int, 0>{});
+    step(std::integral_constant<int, 1>{});
+    step(std::integral_constant<int, 2>{});
+    step(std::integral_constant<int, 3>{});
+    step(std::integral_constant<int, 4>{});
+    step(std::integral_constant<int, 5>{});
+    step(std::integral_constant<int, 6>{});
+    step(std::integral_constant<int, 7>{});
+    const float tot = reduce8(acc);
+    const int g8 = lane >> 3;
+    const int rr = row_of_group(g8);
+    if ((lane & 7) == 0 && rr < RPW) red[grp][slc][rr] = tot;
+    __syncthreads();
+    if (threadIdx.x < NG * RPW) {
+        const int gq = static_cast<int>(threadIdx.x) / RPW, r = static_cast<int>(threadIdx.x) - gq * RPW;
+        const int row = (static_cast<int>(blockIdx.x) * NG + gq) * RPW + r;
+        if (row < n) {
+            float v = 0.f;
+#pragma unroll
+            for (int j = 0; j < SL; j++) v += red[gq][j][r];
+            y[row] = resid ? v + resid[row] : v;
+        }
+    }
+}
+
 // Split rows for Q6_K / Q8_0 (4096 < k <= 16384): the Q4_K split-row kernel's
 // work split with the short-row Q6_K / Q8_0 units (ShortRow).  A slice of
 // upw units starts on a 4-byte boundary (Q6_K: an even super-block), is read
@@ -1337,6 +1459,25 @@ void launch_split(const void* w, const void* x, float* y, const float* resid, in
     const int grid = (n + NG * RPW - 1) / (NG * RPW);
     gemv_q4k_split_kernel<RPW, NS, SL, XH><<<dim3(static_cast<uint32_t>(grid)), dim3(1024), 0, st>>>(
         static_cast<const uint8_t*>(w), x, y, resid, n, units, upw, rb);
+}
+
+template <int D, int SL>
+void launch_split_dma_rpw(int rpw, const void* w, const float* x, float* y, const float* resid, int n, int units,
+                          int upw, uint32_t rb, hipStream_t st) {
+    constexpr int NG = 16 / SL;
+    const int grid = (n + NG * rpw - 1) / (NG * rpw);
+    const dim3 g(static_cast<uint32_t>(grid)), b(1024);
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
+    switch (rpw) {
+    case 1: gemv_q4k_split_dma_kernel<1, 2, SL><<<g, b, 0, st>>>(wb, x, y, resid, n, units, upw, rb); break;
+    case 2: gemv_q4k_split_dma_kernel<2, (D < 2 ? D : 2) + 1, SL><<<g, b, 0, st>>>(wb, x, y, resid, n, units, upw, rb); break;
+    case 3: gemv_q4k_split_dma_kernel<3, D + 1, SL><<<g, b, 0, st>>>(wb, x, y, resid, n, units, upw, rb); break;
+    case 4: gemv_q4k_split_dma_kernel<4, D + 1, SL><<<g, b, 0, st>>>(wb, x, y, resid, n, units, upw, rb); break;
+    case 5: gemv_q4k_split_dma_kernel<5, D + 1, SL><<<g, b, 0, st>>>(wb, x, y, resid, n, units, upw, rb); break;
+    case 6: gemv_q4k_split_dma_kernel<6, D + 1, SL><<<g, b, 0, st>>>(wb, x, y, resid, n, units, upw, rb); break;
+    case 7: gemv_q4k_split_dma_kernel<7, D + 1, SL><<<g, b, 0, st>>>(wb, x, y, resid, n, units, upw, rb); break;
+    default: gemv_q4k_split_dma_kernel<8, D + 1, SL><<<g, b, 0, st>>>(wb, x, y, resid, n, units, upw, rb); break;
+    }
 }
 
 template <int D, int SL, bool XH = false>
@@ -1607,6 +1748,20 @@ int gemv_q4k_split(const void* w, const void* x, float* y, const float* resid, i
         return check_launch("vb_gemm");
     }
     const int d = knobs().gemv_split_d;
+    if (knobs().gemv_dma && d <= 2) {
+        // the slices land in LDS by DMA (rows in flight: 2, or 1 with VB_GEMV_SPLIT="sl,1")
+        const float* xf = static_cast<const float*>(x);
+        if (sh.sl == 2)
+            d == 1 ? launch_split_dma_rpw<1, 2>(sh.rpw, w, xf, y, resid, ni, units, sh.upw, rb, st)
+                   : launch_split_dma_rpw<2, 2>(sh.rpw, w, xf, y, resid, ni, units, sh.upw, rb, st);
+        else if (sh.sl == 4)
+            d == 1 ? launch_split_dma_rpw<1, 4>(sh.rpw, w, xf, y, resid, ni, units, sh.upw, rb, st)
+                   : launch_split_dma_rpw<2, 4>(sh.rpw, w, xf, y, resid, ni, units, sh.upw, rb, st);
+        else
+            d == 1 ? launch_split_dma_rpw<1, 8>(sh.rpw, w, xf, y, resid, ni, units, sh.upw, rb, st)
+                   : launch_split_dma_rpw<2, 8>(sh.rpw, w, xf, y, resid, ni, units, sh.upw, rb, st);
+        return check_launch("vb_gemv");
+    }
     if (sh.sl == 2)
         launch_split_d<2>(d, sh.rpw, w, x, y, resid, ni, units, sh.upw, rb, st);
     else if (sh.sl == 4)

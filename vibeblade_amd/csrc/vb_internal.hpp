@@ -18,7 +18,8 @@ namespace vb {
 //   VB_GEMM_SPLIT_MIN_M=m                     smallest M (up to 768) on the role-split GEMM (0: never)
 //   VB_GEMM_ZSPLIT=z                          with VB_GEMM_TILE: K splits between workgroups (Q6_K / Q8_0,
 //                                             fp16 X, M >= 384, N < 8192)
-//   VB_GEMV_DMA=0                             short-row Q4_K GEMV (fp32 x): register ring instead of LDS DMA
+//   VB_GEMV_DMA=0                             short- and split-row Q4_K GEMV (fp32 x): register ring
+//                                             instead of LDS DMA
 //   VB_GEMV_SPLIT="sl,d"                      split-row Q4_K GEMV: slices per row (2, 4, 8), rows in flight (1-4)
 //   VB_SPARSE_FUSED=0, VB_SPARSE_NPW=1|2      sparse FFN kernel choice (NPW: the row-split fused
 //                                             kernel with 1 or 2 neurons per wave)
