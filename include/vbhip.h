@@ -146,11 +146,11 @@ int vb_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k,
  * (cpp/include/cuda_kernels.h, cpp/src/cuda_kernels.cu:184-212).
  * Weight types: Q4_K (variants 0-4), Q6_K and Q8_0 (variants 0, 2, 4; Q8_0
  * needs k % 128 == 0 at every m, m == 1 included, although vb_gemv itself
- * takes Q8_0 rows of any whole number of blocks); Q4_0, Q4_1, Q5_0, Q5_1,
- * Q5_K, Q2_K, Q3_K, BF16 and F32 (variants 0, 2; k % 256 == 0 except on the
- * GEMV) decoded once to fp16 (each value rounded once) into n x k x 2 bytes
- * of workspace and multiplied on the tiled kernel, and F16 on the tiled
- * kernel in place; vb_gemm allocates that workspace on the stream for the
+ * takes Q8_0 rows of any whole number of blocks); Q5_K (variants 0, 2) on the
+ * tiled kernel with its own decoder; Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K,
+ * BF16 and F32 (variants 0, 2; k % 256 == 0 except on the GEMV) decoded once
+ * to fp16 (each value rounded once) into n x k x 2 bytes of workspace and
+ * multiplied on the tiled kernel, and F16 on the tiled kernel in place; vb_gemm allocates that workspace on the stream for the
  * call (stream-ordered), vb_gemm_ws takes it from the caller.  W and x
  * 16-byte aligned. */
 int vb_gemm(const void* w, const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n,

@@ -585,17 +585,19 @@ def make_other(qtype, n, k, seed):
                                          (1, 129, 256, torch.float16), (300, 1000, 1024, torch.float16),
                                          (2, 64, 4096, torch.float32)])
 def test_gemm_other_types(qtype, m, n, k, dtype):
-    """Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q5_K / Q2_K / Q3_K / BF16 / F32 weights are
+    """Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q2_K / Q3_K / BF16 / F32 weights are
     decoded once to fp16 (one rounding, as the fused decoders round) and run
-    on the tiled kernel; F16 weights in place.  Against the fp64 product of
-    the oracle's decode; the workspace the call asks for; without a
-    workspace (decoded into a stream-ordered allocation) the same bits."""
+    on the tiled kernel; F16 weights in place; Q5_K on the tiled kernel with
+    its fused decoder.  Against the fp64 product of the oracle's decode; the
+    workspace the call asks for; without a workspace (decoded into a
+    stream-ordered allocation) the same bits."""
     lib = _lib.load()
     qt = make_other(qtype, n, k, m + n + k + qtype)
     x = np.random.default_rng(m + k).standard_normal((m, k)).astype(np.float32)
     xt = torch.from_numpy(x).to("cuda", dtype)
     xdt = 1 if dtype == torch.float16 else 0
-    want_ws = 0 if qtype == ggml.GGML_TYPE_F16 or (m == 1 and xdt == 0) else n * k * 2
+    in_place = qtype in (ggml.GGML_TYPE_F16, ggml.GGML_TYPE_Q5_K)
+    want_ws = 0 if in_place or (m == 1 and xdt == 0) else n * k * 2
     assert lib.vb_gemm_workspace(m, n, k, qtype, xdt, 0) == want_ws
     y = gemm(qt, xt).cpu().numpy()
     want = ref_gemm(qt, xt.float().cpu().numpy())
@@ -618,3 +620,20 @@ def test_gemm_other_types_rejects():
     qt = make_other(ggml.GGML_TYPE_Q5_K, 64, 512, 6)
     with pytest.raises(VBError, match="tiled kernel only"):
         gemm(qt, torch.randn((4, 512), device="cuda", dtype=torch.float16), variant=GEMM_SKINNY)
+
+
+@pytest.mark.parametrize("m,n,k,dtype", [(8, 300, 512, torch.float16), (300, 1000, 1024, torch.float16),
+                                         (65, 200, 768, torch.float32)])
+def test_gemm_q5k_fused_matches_fp16_decode(m, n, k, dtype):
+    """The fused Q5_K decoder (d sc and dmin m rounded to fp16, then one fma
+    per weight) against the same tiled kernel fed the oracle's decode rounded
+    to fp16 as F16 weights: the two differ only by those roundings."""
+    qt = make_other(ggml.GGML_TYPE_Q5_K, n, k, m + n + 1)
+    x = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
+    xt = torch.from_numpy(x).to("cuda", dtype)
+    y = gemm(qt, xt).cpu().numpy()
+    wf16 = torch.from_numpy(O.dequantize(qt.to_numpy_bytes(), k, qt.qtype).astype(np.float16)).cuda()
+    qh = QTensor.from_bytes(wf16.view(torch.uint8).reshape(-1), ggml.GGML_TYPE_F16, n, k)
+    y16 = gemm(qh, xt).cpu().numpy()
+    assert O.rel_l2(y, y16.astype(np.float64)) <= 2e-3
+    assert O.rel_l2(y, ref_gemm(qt, xt.float().cpu().numpy())) <= TOL

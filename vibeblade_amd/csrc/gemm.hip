@@ -179,6 +179,53 @@ struct TiledW<TYPE_Q8_0> {
     }
 };
 
+// Q5_K in the GGUF layout (super-block of 256, 176 bytes: fp16 d @0, fp16
+// dmin @2, scales[12] @4 in the Q4_K 6-bit packing, qh[32] @16, qs[128] @48).
+// Element 64 c + l (l < 64) of a super-block has sub-block 2 c + l / 32 and
+// code q5 = ((qs[32 c + l % 32] >> 4 (l / 32)) & 15) | ((qh[l % 32] >> (2 c + l
+// / 32)) & 1) << 4, weight d sc q5 - dmin m (the vb_dequant_rows formula).
+// Step 4 sb + c: a lane needs the header, qs bytes 32 c + 8 ug .. + 8 (low
+// nibbles: k-half 0, high: k-half 1) and qh bytes 8 ug .. + 8 (bits 2 c,
+// 2 c + 1).  Each code goes into the low bits of 0x6400 (1024 + q5, exact),
+// then (h - 1024) d sc - dmin m with one rounding.
+template <>
+struct TiledW<TYPE_Q5_K> {
+    static constexpr bool kPairOrder = false;
+    struct Raw {
+        u32x4 hd;
+        uint32_t q0, q1, h0, h1;
+    };
+    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t w, uint32_t rowoff, int step, uint32_t g8,
+                                                 Raw& r) {
+        const uint32_t base = rowoff + static_cast<uint32_t>(step >> 2) * 176u;
+        const uint32_t c = static_cast<uint32_t>(step) & 3u;
+        r.hd = buf_ld128(w, base, 0);
+        r.q0 = ld32(w, base + 48u + 32u * c + g8);
+        r.q1 = ld32(w, base + 52u + 32u * c + g8);
+        r.h0 = ld32(w, base + 16u + g8);
+        r.h1 = ld32(w, base + 20u + g8);
+    }
+    __device__ static __forceinline__ void decode(const Raw& r, uint32_t, int step, uint32_t, const KqConsts& kc,
+                                                  Frag& lo, Frag& hi) {
+        const int c = step & 3;
+        half2_t ds[2], nm[2];
+        q4k_chunk_scales(make_uint4(r.hd.x, r.hd.y, r.hd.z, r.hd.w), c, ds, nm);
+        const uint32_t s0 = 2u * static_cast<uint32_t>(c), s1 = s0 + 1u;
+        const half2_t k1024 = half2_t{static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            // bytes (2 i, 2 i + 1) of the 8 into the two halves
+            const uint32_t sel = (i & 1) ? 0x0C030C02u : 0x0C010C00u;
+            const uint32_t q = __builtin_amdgcn_perm(0u, i < 2 ? r.q0 : r.q1, sel);
+            const uint32_t h = __builtin_amdgcn_perm(0u, i < 2 ? r.h0 : r.h1, sel);
+            const uint32_t a = (q & kc.m0f) | (((h >> s0) & 0x00010001u) << 4) | kc.h64;
+            const uint32_t b = ((q >> 4) & kc.m0f) | (((h >> s1) & 0x00010001u) << 4) | kc.h64;
+            lo.u[i] = h2bits(__builtin_elementwise_fma(bits2h(a) - k1024, ds[0], nm[0]));
+            hi.u[i] = h2bits(__builtin_elementwise_fma(bits2h(b) - k1024, ds[1], nm[1]));
+        }
+    }
+};
+
 // fp16 weights, row-major (a GGUF F16 tensor, or any other type decoded to
 // fp16 first): lane (row, ug) of a step's fragments is elements 8 ug .. +7
 // and 32 + 8 ug .. +7 of the step's 64, 16 bytes each, used as loaded.
@@ -605,15 +652,15 @@ int tiled_zsplit(int type, int x_dtype, int64_t M, int64_t N, int64_t K) {
     return 1;
 }
 
-// The types without a fused decoder: Q4_0, Q4_1, Q5_0, Q5_1, Q5_K, Q2_K, Q3_K,
-// BF16 and F32 weights are decoded once to fp16 (each value rounded once, as
+// The types without a fused decoder: Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, BF16
+// and F32 weights are decoded once to fp16 (each value rounded once, as
 // the fused decoders round) into the workspace, then multiplied on the tiled
 // kernel with fp16 weights; F16 weights are used in place.  The workspace,
 // n x k x 2 bytes (none for F16), comes from the caller (vb_gemm_ws) or is
 // allocated on the stream for the call (hipMallocAsync / hipFreeAsync).
 bool gemm_other_type(int32_t type) {
     return type == TYPE_F32 || type == TYPE_F16 || type == TYPE_BF16 || type == TYPE_Q4_0 || type == TYPE_Q4_1 ||
-           type == TYPE_Q5_0 || type == TYPE_Q5_1 || type == TYPE_Q5_K || type == TYPE_Q2_K || type == TYPE_Q3_K;
+           type == TYPE_Q5_0 || type == TYPE_Q5_1 || type == TYPE_Q2_K || type == TYPE_Q3_K;
 }
 
 int64_t gemm_other_workspace(int32_t type, int64_t N, int64_t K) { return type == TYPE_F16 ? 0 : N * K * 2; }
@@ -672,7 +719,7 @@ int gemm_other(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t 
 
 int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, int64_t N, int64_t K,
                   int32_t type, int32_t variant, void* ws, size_t ws_bytes, hipStream_t st) {
-    if (type != TYPE_Q4_K && type != TYPE_Q6_K && type != TYPE_Q8_0 && !gemm_other_type(type)) {
+    if (type != TYPE_Q4_K && type != TYPE_Q6_K && type != TYPE_Q8_0 && type != TYPE_Q5_K && !gemm_other_type(type)) {
         set_error("vb_gemm: weight type %d has no batched path", type);
         return E_UNSUPPORTED;
     }
@@ -721,7 +768,14 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
     }
     if (gemm_other_type(type)) return gemm_other(w, X, x_dtype, Y, M, N, K, type, variant, ws, ws_bytes, st);
     bool tiled = false;
-    if (type != TYPE_Q4_K) {
+    if (type == TYPE_Q5_K) {
+        // Q5_K: the tiled kernel with its fused decoder, at every M
+        if (variant != 0 && variant != 2) {
+            set_error("vb_gemm: Q5_K runs the tiled kernel only (variant 0 or 2, got %d)", variant);
+            return E_UNSUPPORTED;
+        }
+        tiled = true;
+    } else if (type != TYPE_Q4_K) {
         // Q6_K / Q8_0: the K-split kernel (gemm_kq.hip) up to M = 64, where
         // it decodes each weight once; above, the tiled kernel, which decodes
         // each weight once per 64-256 rows of M (the K-split kernel once per
@@ -844,6 +898,9 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
     else if (type == TYPE_Q6_K)
         rc = x_dtype == X_F16 ? launch_tiled<TYPE_Q6_K, X_F16>(cfg, wb, wby, X, Y, m, n, k, rb, st)
                               : launch_tiled<TYPE_Q6_K, X_F32>(cfg, wb, wby, X, Y, m, n, k, rb, st);
+    else if (type == TYPE_Q5_K)
+        rc = x_dtype == X_F16 ? launch_tiled<TYPE_Q5_K, X_F16>(cfg, wb, wby, X, Y, m, n, k, rb, st)
+                              : launch_tiled<TYPE_Q5_K, X_F32>(cfg, wb, wby, X, Y, m, n, k, rb, st);
     else
         rc = x_dtype == X_F16 ? launch_tiled<TYPE_Q8_0, X_F16>(cfg, wb, wby, X, Y, m, n, k, rb, st)
                               : launch_tiled<TYPE_Q8_0, X_F32>(cfg, wb, wby, X, Y, m, n, k, rb, st);
