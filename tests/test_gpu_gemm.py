@@ -255,7 +255,8 @@ def test_xreg_auto_route():
     assert lib.vb_gemm_workspace(512, 4096, 14336, Q4K, 1, 0) == 512 * 14336 * 2 + 3 * 512 * 4096 * 4
     assert lib.vb_gemm_workspace(1024, 4096, 4096, Q4K, 1, 0) == 0   # 148 tiles: no split, another kernel
     assert lib.vb_gemm_workspace(512, 14336, 4096, Q4K, 0, 0) == 0   # fp32 X
-    assert lib.vb_gemm_workspace(512, 14336, 4096, Q6K, 1, 0) == 0
+    assert lib.vb_gemm_workspace(512, 14336, 4096, Q6K, 1, 0) == 512 * 4096 * 2  # Q6_K / Q8_0 too
+    assert lib.vb_gemm_workspace(512, 14336, 4096, Q80, 1, 0) == 512 * 4096 * 2
     assert lib.vb_gemm_workspace(256, 64, 256, Q4K, 1, 5) == 256 * 256 * 2
     qt, x = make(384, 8192, 1024, 5)
     xt = torch.from_numpy(x).to("cuda", torch.float16)
@@ -306,6 +307,55 @@ def test_xreg_rejects():
                         1024, None)
     assert rc == -1
     assert b"workspace" in lib.vb_last_error()
+
+
+@pytest.mark.parametrize("qtype", [Q6K, Q80])
+@pytest.mark.parametrize("m,n,k", [(256, 224, 256), (300, 4096, 1024), (600, 1136, 512), (777, 128, 2048),
+                                   (256, 16, 768), (257, 5, 2304), (512, 14336, 4096)])
+def test_xreg_types(qtype, m, n, k):
+    """Q6_K and Q8_0 on the packed-X kernel (one raw buffer, two barriers per
+    super-block): one or several 256-row M-tiles with a moved-back last tile,
+    ragged N, K of 1 to 16 super-blocks; Q6_K rows of k = 2304 (1890 bytes)
+    and 5 rows put super-blocks at every even byte offset within their
+    16-byte window.  Against the oracle, and against the tiled kernel, which
+    decodes the same fp16 weights."""
+    qt, x = make(m, n, k, m * 5 + n + k + qtype, qtype=qtype)
+    xt = torch.from_numpy(x).to("cuda", torch.float16)
+    y = gemm(qt, xt, variant=GEMM_XREG).cpu().numpy()
+    want = ref_gemm(qt, xt.float().cpu().numpy())
+    assert y.shape == (m, n)
+    assert O.rel_l2(y, want) <= TOL, (qtype, m, n, k)
+    assert np.all(np.abs(y).sum(axis=1) > 0)
+    t = gemm(qt, xt, variant=GEMM_TILED).cpu().numpy()
+    assert O.rel_l2(y, t.astype(np.float64)) <= 1e-5
+
+
+@pytest.mark.parametrize("qtype", [Q6K, Q80])
+@pytest.mark.parametrize("m,n,k,splits", [(512, 4096, 14336, 3), (300, 2000, 8192, 4), (384, 1000, 4096, 2)])
+def test_xreg_types_ksplit(knob, qtype, m, n, k, splits):
+    """Q6_K / Q8_0 on the packed-X kernel with K splits: the default route at
+    M > 256 with a workspace (the same bits as variant 5), against the
+    oracle and the tiled kernel with its own K splits (VB_GEMM_XR_KQ=0)."""
+    lib = _lib.load()
+    xf = -(-m // 256) * 256 * k * 2
+    assert lib.vb_gemm_workspace(m, n, k, qtype, 1, 0) == xf + splits * m * n * 4
+    qt, x = make(m, n, k, m + n + k + qtype, qtype=qtype)
+    xt = torch.from_numpy(x).to("cuda", torch.float16)
+    y = gemm(qt, xt).cpu().numpy()
+    assert O.rel_l2(y, ref_gemm(qt, xt.float().cpu().numpy())) <= TOL
+    assert np.all(np.abs(y).sum(axis=1) > 0)
+    assert np.array_equal(gemm(qt, xt, variant=GEMM_XREG).cpu().numpy().view(np.uint32), y.view(np.uint32))
+    knob("VB_GEMM_XR_KQ", "0")
+    t = gemm(qt, xt).cpu().numpy()
+    assert O.rel_l2(y, t.astype(np.float64)) <= 1e-5
+
+
+def test_xreg_types_rejects():
+    """Variant 5 with Q8_0 needs K % 256 == 0 (the other Q8_0 kernels take
+    K % 128 == 0)."""
+    qt, x = make(256, 64, 384, 6, qtype=Q80)
+    with pytest.raises(VBError):
+        gemm(qt, torch.from_numpy(x).to("cuda", torch.float16), variant=GEMM_XREG)
 
 
 # ---- Q6_K and Q8_0 weights (gemm_kq.hip) ----------------------------------
@@ -503,12 +553,14 @@ def test_small_m_long_k_runs_ksplit(m):
 
 @pytest.mark.parametrize("qtype", [Q6K, Q80])
 @pytest.mark.parametrize("m,n,k,zs", [(400, 1000, 4096, 4), (384, 4096, 14336, 4)])
-def test_tiled_types_zsplit(qtype, m, n, k, zs):
-    """Q6_K / Q8_0, fp16 X, M >= 384, N < 8192: the default splits K between
+def test_tiled_types_zsplit(knob, qtype, m, n, k, zs):
+    """Q6_K / Q8_0, fp16 X, M >= 384, N < 8192, with the packed-X kernel
+    switched off (VB_GEMM_XR_KQ=0): the tiled kernel splits K between
     workgroups of 256 x 128 tiles (partial products in the workspace, added in
     split order): ragged M and N with four splits, and the down shape at
     M = 384.  Against the oracle and the unsplit tiled kernel (same fp16
     products, sums grouped differently)."""
+    knob("VB_GEMM_XR_KQ", "0")
     lib = _lib.load()
     assert lib.vb_gemm_workspace(m, n, k, qtype, 1, 0) == zs * m * n * 4
     assert lib.vb_gemm_workspace(m, n, k, qtype, 0, 0) == 0  # fp32 X: no split
@@ -524,7 +576,7 @@ def test_tiled_types_zsplit(qtype, m, n, k, zs):
 @pytest.mark.parametrize("qtype", [Q6K, Q80])
 def test_tiled_types_down_shape(qtype):
     """4096 x 14336 Q6_K / Q8_0 weights (the down projection) at M = 512 on
-    the default path (the tiled kernel with K split four ways between
+    the default path (the packed-X kernel with K split three ways between
     workgroups), against the K-split kernel and the oracle; fp16 X with 0.1 %
     outliers x20."""
     n, k, m = 4096, 14336, 512

@@ -96,7 +96,6 @@ struct TiledW<TYPE_Q6_K> {
     __device__ static __forceinline__ void decode(const Raw& r, uint32_t rowoff, int step, uint32_t g8,
                                                   const KqConsts& kc, Frag& lo, Frag& hi) {
         const uint32_t sh = (rowoff + static_cast<uint32_t>(step >> 2) * 210u) & 3u;
-        const uint32_t sx = 4u * (static_cast<uint32_t>(step) & 1u);  // nibble p
         uint32_t l0[2], l1[2], qh[2];
         realign(r.l0, sh, l0[0], l0[1]);
         realign(r.l1, sh, l1[0], l1[1]);
@@ -111,19 +110,7 @@ struct TiledW<TYPE_Q6_K> {
         const uint32_t sb = 8u * (g8 >> 4);  // byte of scale ug / 2 within the four
         const _Float16 v0 = static_cast<_Float16>(d * static_cast<float>(static_cast<int8_t>(sc >> sb)));
         const _Float16 v1 = static_cast<_Float16>(d * static_cast<float>(static_cast<int8_t>(sc >> (sb + 16u))));
-        const half2_t ds0 = half2_t{v0, v0}, ds1 = half2_t{v1, v1};
-        const half2_t k1056 = half2_t{static_cast<_Float16>(1056.0f), static_cast<_Float16>(1056.0f)};
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            // elements 2 i, 2 i + 1: halves (ql | qh << 8); 1024 + q in each half (exact)
-            const uint32_t sel = (i & 1) ? 0x07030602u : 0x05010400u;
-            const uint32_t x = __builtin_amdgcn_perm(qh[i >> 1], l0[i >> 1], sel);
-            const uint32_t y = __builtin_amdgcn_perm(qh[i >> 1], l1[i >> 1], sel);
-            const uint32_t q0 = ((x >> sx) & kc.m0f) | (((x >> (sx + 4u)) & kc.m30) | kc.h64);
-            const uint32_t q1 = ((y >> sx) & kc.m0f) | (((y >> (sx + 6u)) & kc.m30) | kc.h64);
-            lo.u[i] = h2bits((bits2h(q0) - k1056) * ds0);
-            hi.u[i] = h2bits((bits2h(q1) - k1056) * ds1);
-        }
+        q6k_frags(l0, l1, qh, static_cast<uint32_t>(step) & 1u, half2_t{v0, v0}, half2_t{v1, v1}, kc, lo, hi);
     }
 };
 
@@ -780,12 +767,12 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
         // it decodes each weight once; above, the tiled kernel, which decodes
         // each weight once per 64-256 rows of M (the K-split kernel once per
         // 64).  The tiled kernel takes K % 256 == 0.
-        if (variant != 0 && variant != 2 && variant != 4) {
-            set_error("vb_gemm: variant %d is Q4_K-only (use 0, 2 or 4 for Q6_K / Q8_0)", variant);
+        if (variant != 0 && variant != 2 && variant != 4 && variant != 5) {
+            set_error("vb_gemm: variant %d is Q4_K-only (use 0, 2, 4 or 5 for Q6_K / Q8_0)", variant);
             return E_UNSUPPORTED;
         }
-        if (variant == 2 && K % 256 != 0) {
-            set_error("vb_gemm: the tiled kernel takes K %% 256 == 0 for Q6_K / Q8_0 (K=%lld)",
+        if ((variant == 2 || variant == 5) && K % 256 != 0) {
+            set_error("vb_gemm: the tiled and packed-X kernels take K %% 256 == 0 for Q6_K / Q8_0 (K=%lld)",
                       static_cast<long long>(K));
             return E_UNSUPPORTED;
         }
@@ -796,7 +783,7 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
         // tiled from M = 65 (93-95 us against 95-109)
         const int kq_max = x_dtype == X_F16 ? (type == TYPE_Q6_K ? 256 : 0) : 128;
         const bool kq_narrow = N < 8192 && M <= kq_max;
-        tiled = variant == 2 || (variant == 0 && M >= kKqTiledMinM && K % 256 == 0 && !kq_narrow);
+        tiled = variant == 2 || variant == 5 || (variant == 0 && M >= kKqTiledMinM && K % 256 == 0 && !kq_narrow);
         if (!tiled) return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
     } else if (variant == 4) {
         return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
@@ -853,25 +840,30 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
     // 62.6 / 117.5 us against 68.5 / 70.7 / 139.9 us on the role-split and
     // tiled kernels; behind at M = 256, 50.8 against 48.5)
     // With fewer output tiles than CUs (the down projection 4096 x 14336 at
-    // M = 512) the same kernel splits K (gemm_q4k_xr_ksplit) and a small
-    // launch adds the partial products in a fixed order.
-    const bool xr_auto = variant == 0 && type == TYPE_Q4_K && x_dtype == X_F16 && M > 256 &&
-                         (N >= 8192 || gemm_q4k_xr_ksplit(M, N, K) > 1) && ws != nullptr &&
-                         static_cast<int64_t>(ws_bytes) >= gemm_q4k_xr_workspace(M, N, K) &&
+    // M = 512) the same kernel splits K (gemm_xr_ksplit) and a small
+    // launch adds the partial products in a fixed order.  Q6_K and Q8_0 take
+    // it at the same shapes (MI355X, M = 512: 14336 x 4096 Q6_K / Q8_0 70.0 /
+    // 67.9 us against 84.6 / 81.7 on the tiled kernel; 4096 x 14336 84.1 /
+    // 80.1 against 85.9 / 83.2 with its K splits; M = 1024 at 14336 x 4096:
+    // 131.3 / 124.9 against 165.0 / 156.7).
+    const bool xr_auto = variant == 0 && gemm_xr_type(type) && (type == TYPE_Q4_K || knobs().gemm_xr_kq) &&
+                         x_dtype == X_F16 && M > 256 && K % 256 == 0 &&
+                         (N >= 8192 || gemm_xr_ksplit(M, N, K) > 1) && ws != nullptr &&
+                         static_cast<int64_t>(ws_bytes) >= gemm_xr_workspace(M, N, K) &&
                          reinterpret_cast<uintptr_t>(ws) % 16 == 0;
-    if (xr_auto) return gemm_q4k_xr(w, X, Y, M, N, K, ws, st);
-    if (type == TYPE_Q4_K && variant == 5) {
+    if (xr_auto) return gemm_xr(w, X, Y, M, N, K, type, ws, st);
+    if (variant == 5) {
         if (M < 256) {
             set_error("vb_gemm: variant 5 (X in registers) takes m >= 256, got %lld", static_cast<long long>(M));
             return E_INVAL;
         }
-        const int64_t need = gemm_q4k_xr_workspace(M, N, K);
+        const int64_t need = gemm_xr_workspace(M, N, K);
         if (!ws || static_cast<int64_t>(ws_bytes) < need || reinterpret_cast<uintptr_t>(ws) % 16) {
             set_error("vb_gemm: variant 5 needs a 16-byte-aligned workspace of %lld bytes (got %zu)",
                       static_cast<long long>(need), ws_bytes);
             return E_INVAL;
         }
-        return gemm_q4k_xr(w, X, Y, M, N, K, ws, st);
+        return gemm_xr(w, X, Y, M, N, K, type, ws, st);
     }
     if (type == TYPE_Q4_K && (variant == 3 || (variant == 0 && x_dtype == X_F16 && split_range))) {
         return gemm_q4k_split(w, X, Y, M, N, K, st);
@@ -922,15 +914,17 @@ extern "C" int64_t vb_gemm_workspace(int64_t m, int64_t n, int64_t k, int32_t gg
     if (vb::gemm_other_type(ggml_type))
         return m == 1 && x_dtype == 0 && variant == 0 ? 0 : vb::gemm_other_workspace(ggml_type, n, k);
     if (x_dtype != 1) return 0;
+    if (!vb::gemm_xr_type(ggml_type)) return 0;
+    // the shapes gemm_dispatch sends to the packed-X kernel
+    const bool xr_on = ggml_type == vb::TYPE_Q4_K || vb::knobs().gemm_xr_kq;
+    if ((variant == 5 && m >= 256) ||
+        (variant == 0 && xr_on && m > 256 && (n >= 8192 || vb::gemm_xr_ksplit(m, n, k) > 1)))
+        return vb::gemm_xr_workspace(m, n, k);
     if (ggml_type == vb::TYPE_Q6_K || ggml_type == vb::TYPE_Q8_0) {
         // the tiled kernel's K splits: one fp32 partial product each
         const int zs = variant == 0 ? vb::tiled_zsplit(ggml_type, x_dtype, m, n, k) : 1;
         return zs > 1 ? static_cast<int64_t>(zs) * m * n * 4 : 0;
     }
-    if (ggml_type != vb::TYPE_Q4_K) return 0;
-    // the shapes gemm_dispatch sends to the packed-X kernel
-    if ((variant == 5 && m >= 256) || (variant == 0 && m > 256 && (n >= 8192 || vb::gemm_q4k_xr_ksplit(m, n, k) > 1)))
-        return vb::gemm_q4k_xr_workspace(m, n, k);
     return 0;
 }
 

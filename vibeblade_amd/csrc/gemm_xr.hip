@@ -103,21 +103,108 @@ __global__ void __launch_bounds__(256) xr_pack_kernel(const uint8_t* __restrict_
     }
 }
 
+// ---- the weight types of the producers.  A super-block (256 elements of a
+// row) is staged as a window of kPieces 16-byte pieces, kStride pieces
+// apart in LDS (Q6_K padded by one: rows 224 bytes apart put the 16 rows of
+// a decode read on 4 banks, 240 bytes on 8).  The window starts on the
+// super-block for Q4_K (144 = 9 x 16 bytes) and Q8_0 (eight 34-byte blocks,
+// 272 = 17 x 16), whose rows are multiples of 16 bytes long; a Q6_K
+// super-block (210 bytes) starts on any even byte, so its window starts at
+// the 16-byte boundary below and spans the 14 pieces that cover it.
+// kOneRaw: one raw buffer instead of two (Q6_K / Q8_0: the B ring and two
+// raw buffers of 112 rows would pass the 160 KB of LDS), which costs a
+// second barrier per super-block.
+template <int TYPE> struct XrRaw;
+template <> struct XrRaw<TYPE_Q4_K> {
+    static constexpr int kPieces = 9, kStride = 9;
+    static constexpr uint32_t kBytes = 144;
+    static constexpr bool kOneRaw = false;
+};
+template <> struct XrRaw<TYPE_Q6_K> {
+    static constexpr int kPieces = 14, kStride = 15;
+    static constexpr uint32_t kBytes = 210;
+    static constexpr bool kOneRaw = true;
+};
+template <> struct XrRaw<TYPE_Q8_0> {
+    static constexpr int kPieces = 17, kStride = 17;
+    static constexpr uint32_t kBytes = 272;
+    static constexpr bool kOneRaw = true;
+};
+
+// Decode of one producer item from a staged window: chunk c (elements 64 c
+// .. 64 c + 63 of the super-block) of one row, lane group g; lo = elements
+// 8 g .. + 8 of the chunk, hi = 32 + 8 g .. + 8 (natural k order, the order
+// of the packed X).  rw: the window's first dword at or below the data, s =
+// the data's byte offset within it (0 or 2).  Each weight is rounded to fp16
+// once, with the arithmetic of the tiled kernel's decoders (gemm.hip), so
+// both kernels multiply the same fp16 weights.
+//
+// Q6_K (ql[128] @0, qh[64] @128, int8 scales[16] @192, fp16 d @208): chunk
+// c is half h = c / 2, nibble p = c % 2; lo takes ql[64 h + 8 g ..], qh bits
+// 4 p, 4 p + 1 and scale 8 h + 4 p + g / 2; hi ql[64 h + 32 + 8 g ..], qh
+// bits 4 p + 2, 4 p + 3 and that scale + 2.
+__device__ __forceinline__ void xr_q6k_item(const uint32_t* rw, uint32_t s, int c, int g, const KqConsts& kc,
+                                            Frag& lo, Frag& hi) {
+    const int h = c >> 1, p = c & 1;
+    const uint32_t sb8 = 8u * s;
+    auto r8 = [&](int dw, uint32_t& x, uint32_t& y) {
+        const uint32_t a = rw[dw], b = rw[dw + 1], e = rw[dw + 2];
+        x = __builtin_amdgcn_alignbyte(b, a, s);
+        y = __builtin_amdgcn_alignbyte(e, b, s);
+    };
+    uint32_t l0[2], l1[2], qh[2];
+    r8(16 * h + 2 * g, l0[0], l0[1]);
+    r8(16 * h + 8 + 2 * g, l1[0], l1[1]);
+    r8(32 + 8 * h + 2 * g, qh[0], qh[1]);
+    const uint32_t sc = __builtin_amdgcn_alignbyte(rw[48 + 2 * h + p + 1], rw[48 + 2 * h + p], s);
+    const float d = f16lo(rw[52] >> sb8);
+    const uint32_t sb = 8u * static_cast<uint32_t>(g >> 1);
+    const _Float16 v0 = static_cast<_Float16>(d * static_cast<float>(static_cast<int8_t>(sc >> sb)));
+    const _Float16 v1 = static_cast<_Float16>(d * static_cast<float>(static_cast<int8_t>(sc >> (sb + 16u))));
+    q6k_frags(l0, l1, qh, static_cast<uint32_t>(p), half2_t{v0, v0}, half2_t{v1, v1}, kc, lo, hi);
+}
+
+// Q8_0 (blocks of 32: fp16 d @0, int8 qs[32] @2; the window is aligned):
+// chunk c is blocks 2 c (lo: codes 8 g .. + 8) and 2 c + 1 (hi).
+__device__ __forceinline__ void xr_q8_item(const uint32_t* rw, int c, int g, const KqConsts& kc, Frag& lo,
+                                           Frag& hi) {
+    const int b0 = 17 * c;  // block 2 c at byte 68 c, block 2 c + 1 at 68 c + 34
+    const uint32_t a0 = rw[b0 + 2 * g], a1 = rw[b0 + 2 * g + 1], a2 = rw[b0 + 2 * g + 2];
+    const uint32_t qs[4] = {__builtin_amdgcn_alignbyte(a1, a0, 2u), __builtin_amdgcn_alignbyte(a2, a1, 2u),
+                            rw[b0 + 9 + 2 * g], rw[b0 + 10 + 2 * g]};
+    const uint32_t d0 = rw[b0] & 0xFFFFu, d1 = rw[b0 + 8] >> 16;
+    const half2_t dd[2] = {bits2h(d0 | (d0 << 16)), bits2h(d1 | (d1 << 16))};
+    const half2_t k1152 = half2_t{static_cast<_Float16>(1152.0f), static_cast<_Float16>(1152.0f)};
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+        Frag& f = ks ? hi : lo;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            // bytes (b0, b1) into the two halves; (b ^ 0x80) | 0x6400 is the
+            // half 1024 + q + 128 (exact)
+            const uint32_t src = __builtin_amdgcn_perm(0u, qs[2 * ks + (i >> 1)], (i & 1) ? 0x0C030C02u : 0x0C010C00u);
+            f.u[i] = h2bits((bits2h(src ^ kc.x80) - k1152) * dd[ks]);
+        }
+    }
+}
+
 // K split (blockIdx.z = kz of gridDim.z): the workgroup takes super-blocks
 // [kz nsb / KS, (kz + 1) nsb / KS) and writes its sums to Y + kz M N (the
 // caller's partial buffers when KS > 1; xr_ksum_kernel adds them).
-template <int NF>
-__global__ void __launch_bounds__(XR_THREADS) gemm_q4k_xr_kernel(const uint8_t* __restrict__ w, uint32_t wbytes,
-                                                                  const uint8_t* __restrict__ Xf,
-                                                                  float* __restrict__ Y, int M, int N, int K,
-                                                                  uint32_t rb) {
+template <int TYPE, int NF>
+__global__ void __launch_bounds__(XR_THREADS) gemm_xr_kernel(const uint8_t* __restrict__ w, uint32_t wbytes,
+                                                             const uint8_t* __restrict__ Xf, float* __restrict__ Y,
+                                                             int M, int N, int K, uint32_t rb) {
+    using R = XrRaw<TYPE>;
+    constexpr bool ONE = R::kOneRaw;
     constexpr int HS = NF * 64;  // uint4 per (step, ks) half of the B ring
     constexpr int SS = 2 * HS;   // per step
     constexpr int SB = 4 * SS;   // per super-block
-    constexpr int RAW = 9 * 16 * NF;          // uint4 of one raw super-block (16 NF rows x 144 B)
-    constexpr int RPT = (RAW + 255) / 256;    // raw pieces per producer thread
+    constexpr int RAW = R::kPieces * 16 * NF;     // pieces of one raw super-block (16 NF rows)
+    constexpr int RAWS = R::kStride * 16 * NF;    // uint4 of one raw buffer in LDS
+    constexpr int RPT = (RAW + 255) / 256;        // raw pieces per producer thread
     __shared__ uint4 bt[2 * SB];
-    __shared__ uint4 raw[2 * RAW];
+    __shared__ uint4 raw[(ONE ? 1 : 2) * RAWS];
 
     const int lane = static_cast<int>(threadIdx.x) & 63, j = lane & 15, g = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -186,7 +273,7 @@ __global__ void __launch_bounds__(XR_THREADS) gemm_q4k_xr_kernel(const uint8_t* 
         load_a(0, 0, 1);
         load_a(1, 1, 0);
         load_a(1, 1, 1);
-        __syncthreads();  // raw super-blocks 0 and 1 staged
+        __syncthreads();  // raw super-block 0 (and 1) staged
         __syncthreads();  // ring half 0 (super-block 0) written
         Frag b0[NF], b1[NF];
         read_b(0, 0, 0, b0);
@@ -202,7 +289,9 @@ __global__ void __launch_bounds__(XR_THREADS) gemm_q4k_xr_kernel(const uint8_t* 
                 mfmas(areg[slot][0], b0);
                 __builtin_amdgcn_sched_barrier(0);
                 load_a(s + 2, slot, 0);
-                if (t == 3) __syncthreads();
+                // one raw buffer: the producers' mid-super-block barrier
+                // (raw bytes of super-block sb + 1 staged)
+                if (t == 3 || (ONE && t == 0)) __syncthreads();
                 read_b(t == 3 ? nxt : cur, (t + 1) & 3, 0, b0);
                 __builtin_amdgcn_sched_barrier(0);
                 mfmas(areg[slot][1], b1);
@@ -230,31 +319,43 @@ __global__ void __launch_bounds__(XR_THREADS) gemm_q4k_xr_kernel(const uint8_t* 
         const int pw = wave - XR_CW;
         const int pt = static_cast<int>(threadIdx.x) - 64 * XR_CW;
         const __amdgpu_buffer_rsrc_t wrs = make_rsrc(w, wbytes);
-        // raw piece p = pt + 256 i of a super-block: 16-byte piece p % 9 of
-        // tile row p / 9 (rows past N repeat row N - 1, never stored; pieces
-        // past the tile repeat the last one and are not written)
-        uint32_t roff[RPT];
+        // raw piece p = pt + 256 i of a super-block: 16-byte piece p % kPieces
+        // of tile row p / kPieces (rows past N repeat row N - 1, never
+        // stored; pieces past the tile repeat the last one and are not
+        // written)
+        uint32_t rowb[RPT], pc16[RPT];
+        int lidx[RPT];
 #pragma unroll
         for (int i = 0; i < RPT; i++) {
             int p = pt + 256 * i;
             p = p < RAW ? p : RAW - 1;
-            int n = n0 + p / 9;
+            const int row = p / R::kPieces, piece = p - R::kPieces * row;
+            int n = n0 + row;
             n = n < N ? n : N - 1;
-            roff[i] = static_cast<uint32_t>(n) * rb + 16u * static_cast<uint32_t>(p % 9);
+            rowb[i] = static_cast<uint32_t>(n) * rb;
+            pc16[i] = 16u * static_cast<uint32_t>(piece);
+            lidx[i] = row * R::kStride + piece;
         }
         u32x4 rr[RPT];
         auto load_raw = [&](int sb) {
             sb = sb0 + (sb < nsb ? sb : nsb - 1);  // local -> super-block of the row
 #pragma unroll
-            for (int i = 0; i < RPT; i++)
-                rr[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, static_cast<int>(roff[i]),
-                                                              static_cast<int>(static_cast<uint32_t>(sb) * 144u), 0);
+            for (int i = 0; i < RPT; i++) {
+                if constexpr (TYPE == TYPE_Q6_K) {
+                    const uint32_t off = ((rowb[i] + static_cast<uint32_t>(sb) * R::kBytes) & ~15u) + pc16[i];
+                    rr[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, static_cast<int>(off), 0, 0);
+                } else {
+                    rr[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, static_cast<int>(rowb[i] + pc16[i]),
+                                                                  static_cast<int>(static_cast<uint32_t>(sb) * R::kBytes),
+                                                                  0);
+                }
+            }
         };
         auto store_raw = [&](int buf) {
 #pragma unroll
             for (int i = 0; i < RPT; i++) {
                 const int p = pt + 256 * i;
-                if (i + 1 < RPT || p < RAW) raw[buf * RAW + p] = make_uint4(rr[i].x, rr[i].y, rr[i].z, rr[i].w);
+                if (i + 1 < RPT || p < RAW) raw[buf * RAWS + lidx[i]] = make_uint4(rr[i].x, rr[i].y, rr[i].z, rr[i].w);
             }
         };
         // the wave's dequant items q = 0 .. NF - 1: chunk ic[q], fragment ifr[q]
@@ -265,47 +366,87 @@ __global__ void __launch_bounds__(XR_THREADS) gemm_q4k_xr_kernel(const uint8_t* 
             ic[q] = i / NF;
             ifr[q] = i - NF * ic[q];
         }
-        auto dequant_item = [&](int q, int rbuf, int buf) {
-            const uint8_t* rw = reinterpret_cast<const uint8_t*>(raw + rbuf * RAW) + (16 * ifr[q] + j) * 144;
-            const uint4 h = *reinterpret_cast<const uint4*>(rw);
-            const uint2 qs = *reinterpret_cast<const uint2*>(rw + 16 + 32 * ic[q] + 8 * g);
-            half2_t ds[2], nm[2];
-            q4k_chunk_scales_sel(h, ic[q], ds, nm);
+        const KqConsts kc = kq_consts();
+        // super-block sb (local) of item q from raw buffer rbuf into ring half buf
+        auto dequant_item = [&](int q, int sb, int rbuf, int buf) {
+            const uint8_t* rw = reinterpret_cast<const uint8_t*>(raw + rbuf * RAWS) + (16 * ifr[q] + j) * 16 * R::kStride;
             Frag lo, hi;
-            q4k_bfrags_cvt(qs.x, qs.y, ds, nm, lo, hi);
+            if constexpr (TYPE == TYPE_Q4_K) {
+                (void)sb;
+                const uint4 h = *reinterpret_cast<const uint4*>(rw);
+                const uint2 qs = *reinterpret_cast<const uint2*>(rw + 16 + 32 * ic[q] + 8 * g);
+                half2_t ds[2], nm[2];
+                q4k_chunk_scales_sel(h, ic[q], ds, nm);
+                q4k_bfrags_cvt(qs.x, qs.y, ds, nm, lo, hi);
+            } else if constexpr (TYPE == TYPE_Q6_K) {
+                // the window starts (row start + 210 sb) % 16 bytes before the data
+                int n = n0 + 16 * ifr[q] + j;
+                n = n < N ? n : N - 1;
+                const uint32_t sh =
+                    (static_cast<uint32_t>(n) * rb + static_cast<uint32_t>(sb0 + (sb < nsb ? sb : nsb - 1)) * 210u) & 15u;
+                xr_q6k_item(reinterpret_cast<const uint32_t*>(rw + (sh & ~3u)), sh & 3u, ic[q], g, kc, lo, hi);
+            } else {
+                (void)sb;
+                xr_q8_item(reinterpret_cast<const uint32_t*>(rw), ic[q], g, kc, lo, hi);
+            }
             uint4* dst = bt + buf * SB + ic[q] * SS + ifr[q] * 64 + lane;
             dst[0] = make_uint4(lo.u[0], lo.u[1], lo.u[2], lo.u[3]);
             dst[HS] = make_uint4(hi.u[0], hi.u[1], hi.u[2], hi.u[3]);
         };
 
-        load_raw(0);
-        store_raw(0);
-        load_raw(1);
-        store_raw(1);
-        __syncthreads();  // raw super-blocks 0 and 1 staged
+        if constexpr (ONE) {
+            load_raw(0);
+            store_raw(0);
+            load_raw(1);
+            __syncthreads();  // raw super-block 0 staged
 #pragma unroll
-        for (int q = 0; q < NF; q++) dequant_item(q, 0, 0);
-        load_raw(2);
-        __syncthreads();  // ring half 0 written
-        for (int sb = 0; sb < nsb; sb++) {
-            // dequantize super-block sb + 1 (raw half (sb + 1) % 2) into ring
-            // half (sb + 1) % 2, two items per step; then stage the raw bytes
-            // of super-block sb + 2 (loaded during sb - 1) into raw half sb % 2,
-            // free since super-block sb was dequantized during sb - 1, and
-            // load those of sb + 3.  Past the last super-block: clamped
-            // loads, halves nobody reads.
-            const int nxt = (sb & 1) ^ 1;
+            for (int q = 0; q < NF; q++) dequant_item(q, 0, 0, 0);
+            __syncthreads();  // ring half 0 written, raw buffer free
+            for (int sb = 0; sb < nsb; sb++) {
+                // stage super-block sb + 1 (loaded during sb - 1) and load sb +
+                // 2; the consumers' barrier at step 0 of sb publishes it; then
+                // dequantize it into ring half (sb + 1) % 2, which the
+                // consumers last read during sb - 1, before their barrier at
+                // step 3.  Past the last super-block: clamped loads, a half
+                // nobody reads.
+                const int nxt = (sb & 1) ^ 1;
+                store_raw(0);
+                load_raw(sb + 2);
+                __syncthreads();
 #pragma unroll
-            for (int t = 0; t < 4; t++) {
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int k2 = 0; k2 < 2; k2++)
-                    if (2 * t + k2 < NF) dequant_item(2 * t + k2, nxt, nxt);
+                for (int q = 0; q < NF; q++) dequant_item(q, sb + 1, 0, nxt);
+                __syncthreads();
             }
-            __builtin_amdgcn_sched_barrier(0);
-            store_raw(sb & 1);
-            load_raw(sb + 3);
-            __syncthreads();
+        } else {
+            load_raw(0);
+            store_raw(0);
+            load_raw(1);
+            store_raw(1);
+            __syncthreads();  // raw super-blocks 0 and 1 staged
+#pragma unroll
+            for (int q = 0; q < NF; q++) dequant_item(q, 0, 0, 0);
+            load_raw(2);
+            __syncthreads();  // ring half 0 written
+            for (int sb = 0; sb < nsb; sb++) {
+                // dequantize super-block sb + 1 (raw half (sb + 1) % 2) into ring
+                // half (sb + 1) % 2, two items per step; then stage the raw bytes
+                // of super-block sb + 2 (loaded during sb - 1) into raw half sb % 2,
+                // free since super-block sb was dequantized during sb - 1, and
+                // load those of sb + 3.  Past the last super-block: clamped
+                // loads, halves nobody reads.
+                const int nxt = (sb & 1) ^ 1;
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int k2 = 0; k2 < 2; k2++)
+                        if (2 * t + k2 < NF) dequant_item(2 * t + k2, sb + 1, nxt, nxt);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                store_raw(sb & 1);
+                load_raw(sb + 3);
+                __syncthreads();
+            }
         }
     }
 }
@@ -338,7 +479,7 @@ constexpr int XR_NF = 7;
 // K splits: as many as fit the CUs with one workgroup each (a shape with
 // fewer output tiles than CUs, such as the FFN down projection 4096 x 14336
 // at M = 512: 37 x 2 tiles, 3 splits), at least 8 super-blocks per split.
-int gemm_q4k_xr_ksplit(int64_t M, int64_t N, int64_t K) {
+int gemm_xr_ksplit(int64_t M, int64_t N, int64_t K) {
     const int64_t tiles = (N + 16 * XR_NF - 1) / (16 * XR_NF) * ((M + XR_TM - 1) / XR_TM);
     int64_t ks = num_cus() / (tiles > 0 ? tiles : 1);
     const int64_t kmax = (K / 256) / 8;
@@ -351,29 +492,42 @@ int gemm_ksum(const float* P, float* Y, int64_t total, int ks, hipStream_t st) {
     return check_launch("vb_gemm");
 }
 
-int64_t gemm_q4k_xr_workspace(int64_t M, int64_t N, int64_t K) {
+int64_t gemm_xr_workspace(int64_t M, int64_t N, int64_t K) {
     const int64_t xf = (M + XR_TM - 1) / XR_TM * XR_TM * K * 2;
-    const int ks = gemm_q4k_xr_ksplit(M, N, K);
+    const int ks = gemm_xr_ksplit(M, N, K);
     return xf + (ks > 1 ? static_cast<int64_t>(ks) * M * N * 4 : 0);
 }
 
-// Caller (gemm_dispatch) has validated type (Q4_K), alignment (W, X 16 B),
-// the 32-bit offset bounds (N * row bytes, M * K * 2 < 2^32), M >= 256 and
-// the workspace (gemm_q4k_xr_workspace bytes, 16-byte aligned): the packed X,
-// then, with K splits, one fp32 M x N partial product per split.
-int gemm_q4k_xr(const void* w, const void* X, float* Y, int64_t M, int64_t N, int64_t K, void* ws, hipStream_t st) {
+bool gemm_xr_type(int32_t type) { return type == TYPE_Q4_K || type == TYPE_Q6_K || type == TYPE_Q8_0; }
+
+// Caller (gemm_dispatch) has validated the type (gemm_xr_type), alignment
+// (W, X 16 B), the 32-bit offset bounds (N * row bytes rounded up to whole
+// dwords, M * K * 2 < 2^32), K % 256 == 0, M >= 256 and the workspace
+// (gemm_xr_workspace bytes, 16-byte aligned): the packed X, then, with K
+// splits, one fp32 M x N partial product per split.
+int gemm_xr(const void* w, const void* X, float* Y, int64_t M, int64_t N, int64_t K, int32_t type, void* ws,
+            hipStream_t st) {
     constexpr int NF = XR_NF;
-    const int64_t rb = row_bytes(TYPE_Q4_K, K);
+    const int64_t rb = row_bytes(type, K);
+    // whole dwords: a Q6_K window's last dword may hold the tensor's last two bytes
+    const uint32_t wbytes = static_cast<uint32_t>((N * rb + 3) & ~int64_t(3));
     const uint32_t mtiles = static_cast<uint32_t>((M + XR_TM - 1) / XR_TM);
-    const int ks = gemm_q4k_xr_ksplit(M, N, K);
+    const int ks = gemm_xr_ksplit(M, N, K);
     xr_pack_kernel<<<dim3(static_cast<uint32_t>(K / 256), XR_TM / 16, mtiles), dim3(256), 0, st>>>(
         static_cast<const uint8_t*>(X), static_cast<uint4*>(ws), static_cast<int>(M), static_cast<int>(K));
     float* out = Y;
     if (ks > 1) out = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + mtiles * XR_TM * K * 2);
     const dim3 grid(static_cast<uint32_t>((N + 16 * NF - 1) / (16 * NF)), mtiles, static_cast<uint32_t>(ks));
-    gemm_q4k_xr_kernel<NF><<<grid, dim3(XR_THREADS), 0, st>>>(
-        static_cast<const uint8_t*>(w), static_cast<uint32_t>(N * rb), static_cast<const uint8_t*>(ws), out,
-        static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), static_cast<uint32_t>(rb));
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
+    const uint8_t* xf = static_cast<const uint8_t*>(ws);
+    const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
+    const uint32_t r = static_cast<uint32_t>(rb);
+    if (type == TYPE_Q4_K)
+        gemm_xr_kernel<TYPE_Q4_K, NF><<<grid, dim3(XR_THREADS), 0, st>>>(wb, wbytes, xf, out, m, n, k, r);
+    else if (type == TYPE_Q6_K)
+        gemm_xr_kernel<TYPE_Q6_K, NF><<<grid, dim3(XR_THREADS), 0, st>>>(wb, wbytes, xf, out, m, n, k, r);
+    else
+        gemm_xr_kernel<TYPE_Q8_0, NF><<<grid, dim3(XR_THREADS), 0, st>>>(wb, wbytes, xf, out, m, n, k, r);
     if (ks > 1) {
         if (const int rc = check_launch("vb_gemm"); rc != OK) return rc;
         return gemm_ksum(out, Y, M * N, ks, st);

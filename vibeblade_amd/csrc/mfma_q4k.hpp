@@ -208,4 +208,30 @@ __device__ __forceinline__ KqConsts kq_consts() {
     return c;
 }
 
+// Q6_K codes to B-fragment dwords, 8 elements of each of two runs: l0 / l1
+// the ql bytes of the runs (nibble p of each), qh their common qh bytes
+// (bits 4 p, 4 p + 1 for the first run, 4 p + 2, 4 p + 3 for the second).
+// Four codes per dword operation: rotating a qh dword right by 28 + 4 p (30
+// + 4 p) moves each byte's two bits to bits 4, 5 of the same byte, the
+// nibbles fill bits 0-3, and v_perm with the 0x64 bytes of kc.h64 spreads
+// bytes (0, 1) and (2, 3) into fp16 halves 1024 + q (exact); then (h - 1056)
+// x scale rounds each weight once.
+__device__ __forceinline__ void q6k_frags(const uint32_t* l0, const uint32_t* l1, const uint32_t* qh, uint32_t p,
+                                          half2_t ds0, half2_t ds1, const KqConsts& kc, Frag& lo, Frag& hi) {
+    const half2_t k1056 = half2_t{static_cast<_Float16>(1056.0f), static_cast<_Float16>(1056.0f)};
+    const uint32_t sx = 4u * p;
+    const uint32_t rl = (28u + sx) & 31u, rh = (30u + sx) & 31u;
+#pragma unroll
+    for (int d = 0; d < 2; d++) {
+        const uint32_t a =
+            (__builtin_amdgcn_alignbit(qh[d], qh[d], rl) & 0x30303030u) | ((l0[d] >> sx) & 0x0F0F0F0Fu);
+        const uint32_t b =
+            (__builtin_amdgcn_alignbit(qh[d], qh[d], rh) & 0x30303030u) | ((l1[d] >> sx) & 0x0F0F0F0Fu);
+        lo.u[2 * d] = h2bits((bits2h(__builtin_amdgcn_perm(kc.h64, a, 0x07010500u)) - k1056) * ds0);
+        lo.u[2 * d + 1] = h2bits((bits2h(__builtin_amdgcn_perm(kc.h64, a, 0x07030502u)) - k1056) * ds0);
+        hi.u[2 * d] = h2bits((bits2h(__builtin_amdgcn_perm(kc.h64, b, 0x07010500u)) - k1056) * ds1);
+        hi.u[2 * d + 1] = h2bits((bits2h(__builtin_amdgcn_perm(kc.h64, b, 0x07030502u)) - k1056) * ds1);
+    }
+}
+
 }  // namespace vb

@@ -83,6 +83,7 @@ Knobs read_knobs() {
         const int v = std::atoi(e);
         if (v >= 1 && v <= 8) k.gemm_zsplit = v;
     }
+    if (const char* e = std::getenv("VB_GEMM_XR_KQ")) k.gemm_xr_kq = std::atoi(e) != 0;
     if (const char* e = std::getenv("VB_SPARSE_FUSED")) k.sparse_fused = e[0] != '0';
     if (const char* e = std::getenv("VB_SPARSE_NPW")) k.sparse_npw = e[0] == '2' ? 2 : (e[0] == '1' ? 1 : 0);
     return k;

@@ -37,6 +37,7 @@ struct Knobs {
     int gemm_tile_wm = 0, gemm_tile_wn = 0, gemm_tile_nf = 0, gemm_tile_ks = 1;
     int gemm_split_min_m = -1;  // smallest M on the role-split kernel (-1: default)
     int gemm_zsplit = 0;        // with VB_GEMM_TILE: K splits between workgroups (Q6_K / Q8_0)
+    bool gemm_xr_kq = true;     // Q6_K / Q8_0 on the packed-X kernel where Q4_K takes it (VB_GEMM_XR_KQ=0: tiled)
     int gemv_split_sl = 0, gemv_split_d = 0;  // split-row Q4_K GEMV: slices per row, rows in flight
     bool sparse_fused = true;
     int sparse_npw = 0;
@@ -137,18 +138,20 @@ int gemm_q4k_skinny(const void* w, const void* X, int32_t x_dtype, float* Y, int
 // Role-split Q4_K GEMM, fp16 X (gemm_split.hip); type, alignment and the
 // 32-bit offset bounds already validated.
 int gemm_q4k_split(const void* w, const void* X, float* Y, int64_t M, int64_t N, int64_t K, hipStream_t st);
-// Q4_K GEMM with the activation fragments loaded into registers from X
-// packed in fragment order, fp16 X (gemm_xr.hip): the preconditions of
-// gemm_q4k_split plus M >= 256 and a 16-byte-aligned workspace of
-// gemm_q4k_xr_workspace(M, N, K) bytes (the packed X, and the partial
-// products of the K splits when the output tiles are fewer than the CUs).
-int gemm_q4k_xr_ksplit(int64_t M, int64_t N, int64_t K);
+// Q4_K / Q6_K / Q8_0 GEMM with the activation fragments loaded into
+// registers from X packed in fragment order, fp16 X (gemm_xr.hip): a type
+// gemm_xr_type takes, W and X 16-byte aligned, the 32-bit offset bounds,
+// K % 256 == 0, M >= 256 and a 16-byte-aligned workspace of
+// gemm_xr_workspace(M, N, K) bytes (the packed X, and the partial products
+// of the K splits when the output tiles are fewer than the CUs).
+bool gemm_xr_type(int32_t type);
+int gemm_xr_ksplit(int64_t M, int64_t N, int64_t K);
 // Y[0, total) = P[0, total) + P[total, 2 total) + ... (ks partial products,
 // added in that order), fp32 (gemm_xr.hip).
 int gemm_ksum(const float* P, float* Y, int64_t total, int ks, hipStream_t st);
 // K splits of the tiled GEMM between workgroups for this shape (1: none; gemm.hip).
 int tiled_zsplit(int type, int x_dtype, int64_t M, int64_t N, int64_t K);
-int64_t gemm_q4k_xr_workspace(int64_t M, int64_t N, int64_t K);
+int64_t gemm_xr_workspace(int64_t M, int64_t N, int64_t K);
 // n_rows x k of W (a decodable type other than F16) as row-major fp16 at out,
 // each value rounded once (dequant.hip; k % 4 == 0, out 16-byte aligned).
 int dequant_rows_f16(const void* w, _Float16* out, int64_t n_rows, int64_t k, int32_t type, hipStream_t st);
@@ -156,7 +159,8 @@ int dequant_rows_f16(const void* w, _Float16* out, int64_t n_rows, int64_t k, in
 // and the workspace that decode needs (n x k x 2 bytes; 0 for F16).
 bool gemm_other_type(int32_t type);
 int64_t gemm_other_workspace(int32_t type, int64_t N, int64_t K);
-int gemm_q4k_xr(const void* w, const void* X, float* Y, int64_t M, int64_t N, int64_t K, void* ws, hipStream_t st);
+int gemm_xr(const void* w, const void* X, float* Y, int64_t M, int64_t N, int64_t K, int32_t type, void* ws,
+            hipStream_t st);
 // Q6_K / Q8_0 GEMM, every M (gemm_kq.hip); pointers, alignment, x_dtype and
 // M, N > 0 already validated.
 int gemm_kq(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, int64_t N, int64_t K, int32_t type,
