@@ -69,8 +69,8 @@ int64_t vb_row_bytes(int32_t ggml_type, int64_t k);
 /* Select the device and check that it is a gfx950; also reads the launch
  * tuning overrides (VB_GEMV_RING, VB_GEMV_CFG, VB_GEMV_Q4K_PATH,
  * VB_GEMV_Q6K_PATH, VB_GEMV_Q8_PATH, VB_GEMV_SPLIT, VB_GEMV_MFMA_CFG,
- * VB_GEMM_NF, VB_GEMM_TILE, VB_GEMM_SPLIT_MIN_M, VB_SPARSE_FUSED,
- * VB_SPARSE_NPW) from the environment, once per process, and the device's
+ * VB_GEMM_NF, VB_GEMM_TILE, VB_GEMM_SPLIT_MIN_M, VB_GEMM_XR_KQ,
+ * VB_SPARSE_FUSED, VB_SPARSE_NPW) from the environment, once per process, and the device's
  * compute-unit count. */
 int vb_init(int device);
 /* Re-read the tuning overrides from the environment (for tuning sweeps and
@@ -144,7 +144,7 @@ int vb_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k,
  * (cpp/src/fast_model.cpp:644-669, :905-960) over rows decoded by
  * dequantize_row (cpp/src/dequant.cpp:407-425), and cuda::gemm_f32
  * (cpp/include/cuda_kernels.h, cpp/src/cuda_kernels.cu:184-212).
- * Weight types: Q4_K (variants 0-4), Q6_K and Q8_0 (variants 0, 2, 4; Q8_0
+ * Weight types: Q4_K (variants 0-5), Q6_K and Q8_0 (variants 0, 2, 4, 5; Q8_0
  * needs k % 128 == 0 at every m, m == 1 included, although vb_gemv itself
  * takes Q8_0 rows of any whole number of blocks); Q5_K (variants 0, 2) on the
  * tiled kernel with its own decoder; Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K,
@@ -156,10 +156,13 @@ int vb_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k,
 int vb_gemm(const void* w, const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n,
             int64_t k, int32_t ggml_type, int32_t variant, void* stream);
 /* vb_gemm with a caller-owned workspace, which lets variant 0 (and variant 5)
- * use the GEMM that needs one: 5 = X in registers (Q4_K, fp16 X, m >= 256):
- * a pack pass writes X into the workspace in MFMA fragment order, then the
- * MFMA waves load their A fragments from it directly and only the
- * dequantized weight tile goes through LDS.  vb_gemm_workspace returns the
+ * use the GEMM that needs one: 5 = X in registers (Q4_K, Q6_K, Q8_0; fp16 X,
+ * m >= 256, k % 256 == 0): a pack pass writes X into the workspace in MFMA
+ * fragment order, then the MFMA waves load their A fragments from it
+ * directly and only the dequantized weight tile goes through LDS.  Variant
+ * 0 takes it for m > 256 where n >= 8192 or the output tiles are fewer than
+ * the CUs (then K is split between workgroups; VB_GEMM_XR_KQ=0 keeps Q6_K /
+ * Q8_0 on the tiled kernel, with its own K splits).  vb_gemm_workspace returns the
  * bytes variant `variant` needs for the shape (0: none, then vb_gemm_ws is
  * vb_gemm; the fp16 decode of the types without a fused decoder, n x k x 2,
  * at any x_dtype); the workspace must be 16-byte aligned.  Same reference path as

@@ -141,19 +141,22 @@ struct Kq<TYPE_Q6_K> {
         }
         const half2_t k1056 = half2_t{static_cast<_Float16>(1056.0f), static_cast<_Float16>(1056.0f)};
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            // elements 2 i, 2 i + 1: halves (ql | qh << 8) of each
-            const uint32_t sel = (i & 1) ? 0x07030602u : 0x05010400u;
-            const uint32_t x = __builtin_amdgcn_perm(qh[i >> 1], l0[i >> 1], sel);
-            const uint32_t y = __builtin_amdgcn_perm(qh[i >> 1], l1[i >> 1], sel);
-            // 1024 + q in each half (exact), q = 6-bit value
+        for (int dw = 0; dw < 2; dw++) {
+            // four 6-bit codes per dword: run t takes nibble t / 2 of l0 (t
+            // even) or l1 (t odd) and qh bits 2 t, 2 t + 1, moved to bits 4, 5
+            // of the same byte
             uint32_t q[4];
-            q[0] = (x & kc.m0f) | (((x >> 4) & kc.m30) | kc.h64);
-            q[2] = ((x >> 4) & kc.m0f) | (((x >> 8) & kc.m30) | kc.h64);
-            q[1] = (y & kc.m0f) | (((y >> 6) & kc.m30) | kc.h64);
-            q[3] = ((y >> 4) & kc.m0f) | (((y >> 10) & kc.m30) | kc.h64);
+            q[0] = ((qh[dw] << 4) & 0x30303030u) | (l0[dw] & 0x0F0F0F0Fu);
+            q[1] = ((qh[dw] << 2) & 0x30303030u) | (l1[dw] & 0x0F0F0F0Fu);
+            q[2] = (qh[dw] & 0x30303030u) | ((l0[dw] >> 4) & 0x0F0F0F0Fu);
+            q[3] = ((qh[dw] >> 2) & 0x30303030u) | ((l1[dw] >> 4) & 0x0F0F0F0Fu);
 #pragma unroll
-            for (int t = 0; t < 4; t++) f[t].u[i] = h2bits((bits2h(q[t]) - k1056) * dsc[t]);
+            for (int t = 0; t < 4; t++) {
+                // bytes (0, 1) and (2, 3) into fp16 halves 1024 + q (exact)
+                f[t].u[2 * dw] = h2bits((bits2h(__builtin_amdgcn_perm(kc.h64, q[t], 0x07010500u)) - k1056) * dsc[t]);
+                f[t].u[2 * dw + 1] =
+                    h2bits((bits2h(__builtin_amdgcn_perm(kc.h64, q[t], 0x07030502u)) - k1056) * dsc[t]);
+            }
         }
     }
 };
