@@ -95,6 +95,11 @@ def parse():
                         "128-launch graph replays): the GEMV beside a read-only probe with its launch shape and "
                         "loads (vb_stream_read, several rings), torch's reduction and copy over the same bytes, "
                         "and a one-workgroup launch; one JSON line each on stderr")
+    p.add_argument("--mfma-ceiling", action="store_true",
+                   help="what the chip's fp16 MFMA reaches on the GEMM shapes with the vendor library: "
+                        "torch.matmul (hipBLASLt) on fp16 weights (no decode) at 14336x4096, M = 512 / 1024 / "
+                        "2048 / 4096, and 4096x14336 at M = 512, with random and with all-zero X, beside the "
+                        "Q4_K GEMM at the same shapes; one JSON line each on stderr")
     p.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                    help="turn the counter_collection.csv files of two --pmc-pass runs (FETCH_SIZE, "
                         "WRITE_SIZE) into " + TRAFFIC_FILE)
@@ -829,6 +834,47 @@ def load_traffic():
         return None
 
 
+def run_mfma_ceiling(steps, warmup):
+    """fp16 GEMM on the vendor library (torch.matmul -> hipBLASLt) with fp16
+    weights already in HBM (nothing to decode; 3.5x the Q4_K bytes), rotating
+    over > 512 MB of weight copies like the other lines, at the Q4_K GEMM
+    shapes: the MFMA rate this chip sustains on them with random fp16 data
+    (and with all-zero X, which draws less power), beside time_gemm's Q4_K
+    numbers for the same shapes."""
+    import torch
+    shapes = ((512, 14336, 4096), (1024, 14336, 4096), (2048, 14336, 4096), (4096, 14336, 4096),
+              (512, 4096, 14336))
+    gen = torch.Generator(device="cuda").manual_seed(SEED + 7)
+    for m, n, k in shapes:
+        ncop = copies_for(n * k * 2, 2)
+        ws = [torch.randn((n, k), generator=gen, device="cuda", dtype=torch.float16) * 0.02 for _ in range(ncop)]
+        x = torch.randn((m, k), generator=gen, device="cuda", dtype=torch.float16)
+        outs = [torch.empty((m, n), device="cuda", dtype=torch.float16) for _ in range(ncop)]
+        line = {"kernel": "torch.matmul fp16 (hipBLASLt)", "m": m, "n": n, "k": k, "weight_copies": ncop}
+        for label, xx in (("random", x), ("zero", torch.zeros_like(x))):
+            for i in range(warmup * ncop):
+                torch.matmul(xx, ws[i % ncop].t(), out=outs[i % ncop])
+            torch.cuda.synchronize()
+            it = steps * ncop
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(it):
+                torch.matmul(xx, ws[i % ncop].t(), out=outs[i % ncop])
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / it
+            line[f"us_{label}_x"] = round(us, 2)
+            line[f"frac_{label}_x"] = round(2 * m * n * k / (us * 1e-6) / 2.5e15, 4)
+        del ws, outs
+        torch.cuda.empty_cache()
+        tm, err = time_gemm(m, n, k, steps, warmup)
+        line["q4k_us"] = tm.us()
+        line["q4k_frac"] = round(2 * m * n * k / (tm.ms * 1e-3) / 2.5e15, 4)
+        line["q4k_rel_l2"] = float(f"{err:.3g}")
+        torch.cuda.empty_cache()
+        print(json.dumps(line), file=sys.stderr, flush=True)
+
+
 def run_floor(steps, warmup):
     """The headline GEMV (14336 x 4096 Q4_K) and what one launch over the same
     33 MB costs without the GEMV's arithmetic, all under the bench protocol
@@ -1008,6 +1054,13 @@ def main():
         from vibeblade_amd import _lib
         _lib.init(0)
         run_floor(args.steps, args.warmup)
+        return
+    if args.mfma_ceiling:
+        import torch
+        from vibeblade_amd import _lib
+        torch.zeros(1, device="cuda")
+        _lib.init(0)
+        run_mfma_ceiling(args.steps, args.warmup)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
