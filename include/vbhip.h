@@ -134,7 +134,8 @@ int vb_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k,
  * 4 at 17 <= m <= 32 for fp32 X and n < 12288, and at n < 8192 for
  * 33 <= m <= 64 and (k >= 8192) 2 <= m <= 16; 3 at 257 <= m <= 768 for fp16
  * X and n >= 8192.  Q6_K / Q8_0: 4 up to m = 64 (at n < 8192: Q6_K up to
- * m = 256 with fp16 X, both up to 128 with fp32 X), 2 above.  Variants 1 and 3 are Q4_K-only.  With variant 0 and
+ * m = 256 with fp16 X, both up to 128 with fp32 X), 2 above.  Q5_K: 4 up to
+ * m = 32 (64 at n < 8192), 2 above.  Variants 1 and 3 are Q4_K-only.  With variant 0 and
  * m == 1 the GEMV runs instead: vb_gemv's kernels for fp32 X (bit-identical
  * to vb_gemv), and for fp16 X the short-row kernels reading the halves
  * directly (Q4_K k <= 4096; Q6_K k = 2048 / 4096; Q8_0 k % 256 == 0 up to
@@ -146,8 +147,8 @@ int vb_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k,
  * (cpp/include/cuda_kernels.h, cpp/src/cuda_kernels.cu:184-212).
  * Weight types: Q4_K (variants 0-5), Q6_K and Q8_0 (variants 0, 2, 4, 5; Q8_0
  * needs k % 128 == 0 at every m, m == 1 included, although vb_gemv itself
- * takes Q8_0 rows of any whole number of blocks); Q5_K (variants 0, 2) on the
- * tiled kernel with its own decoder; Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K,
+ * takes Q8_0 rows of any whole number of blocks); Q5_K (variants 0, 2, 4, 5)
+ * with its own decoder in each kernel; Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K,
  * BF16 and F32 (variants 0, 2; k % 256 == 0 except on the GEMV) decoded once
  * to fp16 (each value rounded once) into n x k x 2 bytes of workspace and
  * multiplied on the tiled kernel, and F16 on the tiled kernel in place; vb_gemm allocates that workspace on the stream for the
@@ -156,7 +157,7 @@ int vb_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k,
 int vb_gemm(const void* w, const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n,
             int64_t k, int32_t ggml_type, int32_t variant, void* stream);
 /* vb_gemm with a caller-owned workspace, which lets variant 0 (and variant 5)
- * use the GEMM that needs one: 5 = X in registers (Q4_K, Q6_K, Q8_0; fp16 X,
+ * use the GEMM that needs one: 5 = X in registers (Q4_K, Q5_K, Q6_K, Q8_0; fp16 X,
  * m >= 256, k % 256 == 0): a pack pass writes X into the workspace in MFMA
  * fragment order, then the MFMA waves load their A fragments from it
  * directly and only the dequantized weight tile goes through LDS.  Variant

@@ -670,7 +670,7 @@ def test_gemm_other_types_rejects():
     with pytest.raises(VBError, match="256"):
         gemm(qt, xt)
     qt = make_other(ggml.GGML_TYPE_Q5_K, 64, 512, 6)
-    with pytest.raises(VBError, match="tiled kernel only"):
+    with pytest.raises(VBError, match="Q5_K runs the tiled"):
         gemm(qt, torch.randn((4, 512), device="cuda", dtype=torch.float16), variant=GEMM_SKINNY)
 
 
@@ -689,3 +689,45 @@ def test_gemm_q5k_fused_matches_fp16_decode(m, n, k, dtype):
     y16 = gemm(qh, xt).cpu().numpy()
     assert O.rel_l2(y, y16.astype(np.float64)) <= 2e-3
     assert O.rel_l2(y, ref_gemm(qt, xt.float().cpu().numpy())) <= TOL
+@pytest.mark.parametrize("m,n,k,dtype", [(2, 300, 512, torch.float16), (8, 1000, 4096, torch.float32),
+                                         (17, 64, 768, torch.float16), (64, 257, 2048, torch.float16),
+                                         (300, 130, 1024, torch.float32)])
+def test_q5k_ksplit_kernel(m, n, k, dtype):
+    """Q5_K on the K-split kernel (variant 4, and variant 0 up to M = 64 at
+    N < 8192, 32 above; half a super-block per step, the fifth bits from qh):
+    against the oracle, and against the tiled kernel, which multiplies the
+    same fp16 weights."""
+    qt = make_other(ggml.GGML_TYPE_Q5_K, n, k, m * 3 + n + k)
+    x = np.random.default_rng(m + 5).standard_normal((m, k)).astype(np.float32)
+    xt = torch.from_numpy(x).to("cuda", dtype)
+    y = gemm(qt, xt, variant=GEMM_KSPLIT).cpu().numpy()
+    if m <= (64 if n < 8192 else 32):  # the default route at small M
+        assert np.array_equal(gemm(qt, xt).cpu().numpy().view(np.uint32), y.view(np.uint32))
+    assert y.shape == (m, n) and np.all(np.abs(y).sum(axis=1) > 0)
+    assert O.rel_l2(y, ref_gemm(qt, xt.float().cpu().numpy())) <= TOL
+    t = gemm(qt, xt, variant=GEMM_TILED).cpu().numpy()
+    assert O.rel_l2(y, t.astype(np.float64)) <= 1e-5
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 224, 256), (300, 4096, 1024), (777, 128, 2048), (512, 14336, 4096),
+                                   (512, 4096, 14336)])
+def test_q5k_xreg(m, n, k):
+    """Q5_K on the packed-X kernel (11-piece raw windows, two raw buffers):
+    variant 5 against the oracle and the tiled kernel (same fp16 weights);
+    the default route with a workspace takes it at M > 256 where Q4_K does
+    (bit-identical to variant 5), K split at the down shape."""
+    lib = _lib.load()
+    qt = make_other(ggml.GGML_TYPE_Q5_K, n, k, m + n + k + 13)
+    x = np.random.default_rng(m + 6).standard_normal((m, k)).astype(np.float32)
+    xt = torch.from_numpy(x).to("cuda", torch.float16)
+    y = gemm(qt, xt, variant=GEMM_XREG).cpu().numpy()
+    assert y.shape == (m, n) and np.all(np.abs(y).sum(axis=1) > 0)
+    assert O.rel_l2(y, ref_gemm(qt, xt.float().cpu().numpy())) <= TOL
+    t = gemm(qt, xt, variant=GEMM_TILED).cpu().numpy()
+    assert O.rel_l2(y, t.astype(np.float64)) <= 1e-5
+    auto = lib.vb_gemm_workspace(m, n, k, ggml.GGML_TYPE_Q5_K, 1, 0)
+    if m > 256 and (n >= 8192 or k >= 8192):
+        assert auto == lib.vb_gemm_workspace(m, n, k, ggml.GGML_TYPE_Q5_K, 1, GEMM_XREG) > 0
+        assert np.array_equal(gemm(qt, xt).cpu().numpy().view(np.uint32), y.view(np.uint32))
+
+

@@ -173,8 +173,8 @@ struct TiledW<TYPE_Q8_0> {
 // / 32)) & 1) << 4, weight d sc q5 - dmin m (the vb_dequant_rows formula).
 // Step 4 sb + c: a lane needs the header, qs bytes 32 c + 8 ug .. + 8 (low
 // nibbles: k-half 0, high: k-half 1) and qh bytes 8 ug .. + 8 (bits 2 c,
-// 2 c + 1).  Each code goes into the low bits of 0x6400 (1024 + q5, exact),
-// then (h - 1024) d sc - dmin m with one rounding.
+// 2 c + 1), decoded by q5k_frags (1024 + q5 in fp16 halves, exact, then
+// (h - 1024) d sc - dmin m with one rounding).
 template <>
 struct TiledW<TYPE_Q5_K> {
     static constexpr bool kPairOrder = false;
@@ -197,19 +197,7 @@ struct TiledW<TYPE_Q5_K> {
         const int c = step & 3;
         half2_t ds[2], nm[2];
         q4k_chunk_scales(make_uint4(r.hd.x, r.hd.y, r.hd.z, r.hd.w), c, ds, nm);
-        const uint32_t s0 = 2u * static_cast<uint32_t>(c), s1 = s0 + 1u;
-        const half2_t k1024 = half2_t{static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            // bytes (2 i, 2 i + 1) of the 8 into the two halves
-            const uint32_t sel = (i & 1) ? 0x0C030C02u : 0x0C010C00u;
-            const uint32_t q = __builtin_amdgcn_perm(0u, i < 2 ? r.q0 : r.q1, sel);
-            const uint32_t h = __builtin_amdgcn_perm(0u, i < 2 ? r.h0 : r.h1, sel);
-            const uint32_t a = (q & kc.m0f) | (((h >> s0) & 0x00010001u) << 4) | kc.h64;
-            const uint32_t b = ((q >> 4) & kc.m0f) | (((h >> s1) & 0x00010001u) << 4) | kc.h64;
-            lo.u[i] = h2bits(__builtin_elementwise_fma(bits2h(a) - k1024, ds[0], nm[0]));
-            hi.u[i] = h2bits(__builtin_elementwise_fma(bits2h(b) - k1024, ds[1], nm[1]));
-        }
+        q5k_frags(r.q0, r.q1, r.h0, r.h1, static_cast<uint32_t>(c), ds, nm, kc, lo, hi);
     }
 };
 
@@ -756,11 +744,20 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
     if (gemm_other_type(type)) return gemm_other(w, X, x_dtype, Y, M, N, K, type, variant, ws, ws_bytes, st);
     bool tiled = false;
     if (type == TYPE_Q5_K) {
-        // Q5_K: the tiled kernel with its fused decoder, at every M
-        if (variant != 0 && variant != 2) {
-            set_error("vb_gemm: Q5_K runs the tiled kernel only (variant 0 or 2, got %d)", variant);
+        // Q5_K: the K-split kernel at small M (every x dtype, M = 1
+        // included), the tiled kernel with its fused decoder above, and the
+        // packed-X kernel where Q4_K takes it.  MI355X, fp16 X: 14336 x 4096
+        // at M = 2 / 8 / 32 / 64: 26.4 / 28.6 / 29.7 / 37.7 us K-split against
+        // 36.2-36.9 tiled; 4096 x 14336 at M = 2 / 8 / 64 / 128: 21.7 / 25.5 /
+        // 67.3 / 109.1 against 94.2 / 94.3 / 97.6 / 96.0 tiled; M = 512 on the
+        // packed-X kernel 65.7 / 77.5 us against 78.1 / 119.4 tiled.
+        if (variant != 0 && variant != 2 && variant != 4 && variant != 5) {
+            set_error("vb_gemm: Q5_K runs the tiled, K-split and packed-X kernels (variant 0, 2, 4 or 5, got %d)",
+                      variant);
             return E_UNSUPPORTED;
         }
+        if (variant == 4 || (variant == 0 && M <= (N < 8192 ? 64 : 32)))
+            return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
         tiled = true;
     } else if (type != TYPE_Q4_K) {
         // Q6_K / Q8_0: the K-split kernel (gemm_kq.hip) up to M = 64, where
@@ -846,7 +843,8 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
     // 67.9 us against 84.6 / 81.7 on the tiled kernel; 4096 x 14336 84.1 /
     // 80.1 against 85.9 / 83.2 with its K splits; M = 1024 at 14336 x 4096:
     // 131.3 / 124.9 against 165.0 / 156.7).
-    const bool xr_auto = variant == 0 && gemm_xr_type(type) && (type == TYPE_Q4_K || knobs().gemm_xr_kq) &&
+    const bool xr_auto = variant == 0 && gemm_xr_type(type) &&
+                         (type == TYPE_Q4_K || type == TYPE_Q5_K || knobs().gemm_xr_kq) &&
                          x_dtype == X_F16 && M > 256 && K % 256 == 0 &&
                          (N >= 8192 || gemm_xr_ksplit(M, N, K) > 1) && ws != nullptr &&
                          static_cast<int64_t>(ws_bytes) >= gemm_xr_workspace(M, N, K) &&
@@ -916,7 +914,7 @@ extern "C" int64_t vb_gemm_workspace(int64_t m, int64_t n, int64_t k, int32_t gg
     if (x_dtype != 1) return 0;
     if (!vb::gemm_xr_type(ggml_type)) return 0;
     // the shapes gemm_dispatch sends to the packed-X kernel
-    const bool xr_on = ggml_type == vb::TYPE_Q4_K || vb::knobs().gemm_xr_kq;
+    const bool xr_on = ggml_type == vb::TYPE_Q4_K || ggml_type == vb::TYPE_Q5_K || vb::knobs().gemm_xr_kq;
     if ((variant == 5 && m >= 256) ||
         (variant == 0 && xr_on && m > 256 && (n >= 8192 || vb::gemm_xr_ksplit(m, n, k) > 1)))
         return vb::gemm_xr_workspace(m, n, k);

@@ -1,4 +1,5 @@
-// Batched dequant-fused GEMM for Q6_K and Q8_0 weights on MFMA:
+// Batched dequant-fused GEMM for Q6_K, Q8_0 and Q5_K weights (and Q4_K at
+// some small-M shapes) on MFMA:
 //   Y[M, N] = X[M, K] . W[N, K]^T   (W in GGUF layout, X fp16 or fp32
 //   row-major, Y fp32 row-major).
 //
@@ -79,6 +80,47 @@ struct Kq<TYPE_Q4_K> {
             half2_t ds[2], nm[2];
             q4k_chunk_scales(hd, 2 * (step & 1) + c, ds, nm);
             q4k_bfrags_nat(r.q[c].x, r.q[c].y, ds, nm, f[2 * c], f[2 * c + 1]);
+        }
+    }
+};
+
+// Q5_K (super-block of 256, 176 bytes: the Q4_K header d, dmin, scales[12]
+// @0, qh[32] @16, qs[128] @48; rows 16-byte aligned): a step is half a
+// super-block, chunks c = 2 h and 2 h + 1, as for Q4_K; lane group g also
+// takes qh bytes [8 g, +8), whose bits 2 c, 2 c + 1 are the fifth bits of the
+// chunk's two sub-blocks (q5k_frags).
+template <>
+struct Kq<TYPE_Q5_K> {
+    static constexpr bool kBlockLane = false;
+    struct Raw {
+        u32x4 hd;
+        uint2 q[2];
+        uint2 h;
+    };
+    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t w, uint32_t rowoff, int step, int g,
+                                                 Raw& r) {
+        const uint32_t base = rowoff + static_cast<uint32_t>(step >> 1) * 176u;
+        const uint32_t g8 = 8u * static_cast<uint32_t>(g);
+        const uint32_t qo = base + 48u + 64u * static_cast<uint32_t>(step & 1) + g8;
+        r.hd = buf_ld128(w, base, 0);
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(w, static_cast<int>(qo + 32u * c), 0, 0);
+            r.q[c] = make_uint2(v[0], v[1]);
+        }
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(w, static_cast<int>(base + 16u + g8), 0, 0);
+        r.h = make_uint2(v[0], v[1]);
+    }
+    __device__ static __forceinline__ void decode(const Raw& r, uint32_t, int step, int, const KqConsts& kc,
+                                                  Frag* f) {
+        const uint4 hd = make_uint4(r.hd.x, r.hd.y, r.hd.z, r.hd.w);
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const int cc = 2 * (step & 1) + c;
+            half2_t ds[2], nm[2];
+            q4k_chunk_scales(hd, cc, ds, nm);
+            q5k_frags(r.q[c].x, r.q[c].y, r.h.x, r.h.y, static_cast<uint32_t>(cc), ds, nm, kc, f[2 * c],
+                      f[2 * c + 1]);
         }
     }
 };
@@ -532,6 +574,11 @@ int gemm_kq(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, 
             launch_kq_m<TYPE_Q4_K, KQ_X_F16>(wb, wby, xb, xby, Y, m, n, k, rbu, st);
         else
             launch_kq_m<TYPE_Q4_K, KQ_X_F32>(wb, wby, xb, xby, Y, m, n, k, rbu, st);
+    } else if (type == TYPE_Q5_K) {
+        if (x_dtype == KQ_X_F16)
+            launch_kq_m<TYPE_Q5_K, KQ_X_F16>(wb, wby, xb, xby, Y, m, n, k, rbu, st);
+        else
+            launch_kq_m<TYPE_Q5_K, KQ_X_F32>(wb, wby, xb, xby, Y, m, n, k, rbu, st);
     } else if (type == TYPE_Q6_K) {
         if (x_dtype == KQ_X_F16)
             launch_kq_m<TYPE_Q6_K, KQ_X_F16>(wb, wby, xb, xby, Y, m, n, k, rbu, st);

@@ -107,8 +107,9 @@ __global__ void __launch_bounds__(256) xr_pack_kernel(const uint8_t* __restrict_
 // row) is staged as a window of kPieces 16-byte pieces, kStride pieces
 // apart in LDS (Q6_K padded by one: rows 224 bytes apart put the 16 rows of
 // a decode read on 4 banks, 240 bytes on 8).  The window starts on the
-// super-block for Q4_K (144 = 9 x 16 bytes) and Q8_0 (eight 34-byte blocks,
-// 272 = 17 x 16), whose rows are multiples of 16 bytes long; a Q6_K
+// super-block for Q4_K (144 = 9 x 16 bytes), Q5_K (176 = 11 x 16) and Q8_0
+// (eight 34-byte blocks, 272 = 17 x 16), whose rows are multiples of 16
+// bytes long; a Q6_K
 // super-block (210 bytes) starts on any even byte, so its window starts at
 // the 16-byte boundary below and spans the 14 pieces that cover it.
 // kOneRaw: one raw buffer instead of two (Q6_K / Q8_0: the B ring and two
@@ -118,6 +119,11 @@ template <int TYPE> struct XrRaw;
 template <> struct XrRaw<TYPE_Q4_K> {
     static constexpr int kPieces = 9, kStride = 9;
     static constexpr uint32_t kBytes = 144;
+    static constexpr bool kOneRaw = false;
+};
+template <> struct XrRaw<TYPE_Q5_K> {
+    static constexpr int kPieces = 11, kStride = 11;
+    static constexpr uint32_t kBytes = 176;
     static constexpr bool kOneRaw = false;
 };
 template <> struct XrRaw<TYPE_Q6_K> {
@@ -378,6 +384,15 @@ __global__ void __launch_bounds__(XR_THREADS) gemm_xr_kernel(const uint8_t* __re
                 half2_t ds[2], nm[2];
                 q4k_chunk_scales_sel(h, ic[q], ds, nm);
                 q4k_bfrags_cvt(qs.x, qs.y, ds, nm, lo, hi);
+            } else if constexpr (TYPE == TYPE_Q5_K) {
+                // d, dmin, scales[12] @0 (the Q4_K header), qh[32] @16, qs[128] @48
+                (void)sb;
+                const uint4 h = *reinterpret_cast<const uint4*>(rw);
+                const uint2 qs = *reinterpret_cast<const uint2*>(rw + 48 + 32 * ic[q] + 8 * g);
+                const uint2 qh = *reinterpret_cast<const uint2*>(rw + 16 + 8 * g);
+                half2_t ds[2], nm[2];
+                q4k_chunk_scales_sel(h, ic[q], ds, nm);
+                q5k_frags(qs.x, qs.y, qh.x, qh.y, static_cast<uint32_t>(ic[q]), ds, nm, kc, lo, hi);
             } else if constexpr (TYPE == TYPE_Q6_K) {
                 // the window starts (row start + 210 sb) % 16 bytes before the data
                 int n = n0 + 16 * ifr[q] + j;
@@ -498,7 +513,9 @@ int64_t gemm_xr_workspace(int64_t M, int64_t N, int64_t K) {
     return xf + (ks > 1 ? static_cast<int64_t>(ks) * M * N * 4 : 0);
 }
 
-bool gemm_xr_type(int32_t type) { return type == TYPE_Q4_K || type == TYPE_Q6_K || type == TYPE_Q8_0; }
+bool gemm_xr_type(int32_t type) {
+    return type == TYPE_Q4_K || type == TYPE_Q5_K || type == TYPE_Q6_K || type == TYPE_Q8_0;
+}
 
 // Caller (gemm_dispatch) has validated the type (gemm_xr_type), alignment
 // (W, X 16 B), the 32-bit offset bounds (N * row bytes rounded up to whole
@@ -524,6 +541,8 @@ int gemm_xr(const void* w, const void* X, float* Y, int64_t M, int64_t N, int64_
     const uint32_t r = static_cast<uint32_t>(rb);
     if (type == TYPE_Q4_K)
         gemm_xr_kernel<TYPE_Q4_K, NF><<<grid, dim3(XR_THREADS), 0, st>>>(wb, wbytes, xf, out, m, n, k, r);
+    else if (type == TYPE_Q5_K)
+        gemm_xr_kernel<TYPE_Q5_K, NF><<<grid, dim3(XR_THREADS), 0, st>>>(wb, wbytes, xf, out, m, n, k, r);
     else if (type == TYPE_Q6_K)
         gemm_xr_kernel<TYPE_Q6_K, NF><<<grid, dim3(XR_THREADS), 0, st>>>(wb, wbytes, xf, out, m, n, k, r);
     else

@@ -208,6 +208,36 @@ __device__ __forceinline__ KqConsts kq_consts() {
     return c;
 }
 
+// Q5_K codes to B-fragment dwords: chunk c of a super-block (elements 64 c ..
+// 64 c + 63), 8 elements of each of its sub-blocks 2 c (lo) and 2 c + 1 (hi).
+// q0, q1: the 8 qs bytes (low nibbles: sub-block 2 c, high: 2 c + 1); h0, h1:
+// the qh bytes of the same element positions (bit 2 c, bit 2 c + 1).  Four
+// codes per dword operation: a rotation moves each byte's qh bit to bit 4 of
+// the same byte, the nibbles fill bits 0-3, v_perm with the 0x64 bytes of
+// kc.h64 spreads bytes (0, 1) and (2, 3) into fp16 halves 1024 + q5 (exact);
+// then (h - 1024) d sc - dmin m with one rounding.
+__device__ __forceinline__ void q5k_frags(uint32_t q0, uint32_t q1, uint32_t h0, uint32_t h1, uint32_t c,
+                                          const half2_t* ds, const half2_t* nm, const KqConsts& kc, Frag& lo,
+                                          Frag& hi) {
+    const half2_t k1024 = half2_t{static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+    const uint32_t rl = (28u + 2u * c) & 31u, rh = (29u + 2u * c) & 31u;
+    const uint32_t qd[2] = {q0, q1}, hd[2] = {h0, h1};
+#pragma unroll
+    for (int d = 0; d < 2; d++) {
+        const uint32_t a = (__builtin_amdgcn_alignbit(hd[d], hd[d], rl) & 0x10101010u) | (qd[d] & 0x0F0F0F0Fu);
+        const uint32_t b =
+            (__builtin_amdgcn_alignbit(hd[d], hd[d], rh) & 0x10101010u) | ((qd[d] >> 4) & 0x0F0F0F0Fu);
+        lo.u[2 * d] = h2bits(__builtin_elementwise_fma(bits2h(__builtin_amdgcn_perm(kc.h64, a, 0x07010500u)) - k1024,
+                                                       ds[0], nm[0]));
+        lo.u[2 * d + 1] = h2bits(__builtin_elementwise_fma(
+            bits2h(__builtin_amdgcn_perm(kc.h64, a, 0x07030502u)) - k1024, ds[0], nm[0]));
+        hi.u[2 * d] = h2bits(__builtin_elementwise_fma(bits2h(__builtin_amdgcn_perm(kc.h64, b, 0x07010500u)) - k1024,
+                                                       ds[1], nm[1]));
+        hi.u[2 * d + 1] = h2bits(__builtin_elementwise_fma(
+            bits2h(__builtin_amdgcn_perm(kc.h64, b, 0x07030502u)) - k1024, ds[1], nm[1]));
+    }
+}
+
 // Q6_K codes to B-fragment dwords, 8 elements of each of two runs: l0 / l1
 // the ql bytes of the runs (nibble p of each), qh their common qh bytes
 // (bits 4 p, 4 p + 1 for the first run, 4 p + 2, 4 p + 3 for the second).
