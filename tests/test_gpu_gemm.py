@@ -616,6 +616,9 @@ OTHER_TYPES = [ggml.GGML_TYPE_Q4_0, ggml.GGML_TYPE_Q4_1, ggml.GGML_TYPE_Q5_0, gg
                ggml.GGML_TYPE_F16, ggml.GGML_TYPE_F32]
 
 
+B32_TYPES = [ggml.GGML_TYPE_Q4_0, ggml.GGML_TYPE_Q4_1, ggml.GGML_TYPE_Q5_0, ggml.GGML_TYPE_Q5_1]
+
+
 def make_other(qtype, n, k, seed):
     """Weights of `qtype` as raw GGUF bytes: random blocks with moderate
     scales for the block types, N(0, 0.02) values for the plain ones."""
@@ -648,7 +651,7 @@ def test_gemm_other_types(qtype, m, n, k, dtype):
     x = np.random.default_rng(m + k).standard_normal((m, k)).astype(np.float32)
     xt = torch.from_numpy(x).to("cuda", dtype)
     xdt = 1 if dtype == torch.float16 else 0
-    in_place = qtype in (ggml.GGML_TYPE_F16, ggml.GGML_TYPE_Q5_K)
+    in_place = qtype in (ggml.GGML_TYPE_F16, ggml.GGML_TYPE_Q5_K) or (qtype in B32_TYPES and m <= 128)
     want_ws = 0 if in_place or (m == 1 and xdt == 0) else n * k * 2
     assert lib.vb_gemm_workspace(m, n, k, qtype, xdt, 0) == want_ws
     y = gemm(qt, xt).cpu().numpy()
@@ -663,12 +666,20 @@ def test_gemm_other_types(qtype, m, n, k, dtype):
 
 
 def test_gemm_other_types_rejects():
-    """Shapes and variants the fp16-decode path does not take fail with a
-    clear error: K not a multiple of 256 at M >= 2, a variant other than 0 / 2."""
+    """Shapes and variants the kernels do not take fail with a clear error:
+    a 32-element type with K not a multiple of 128 at small M (the K-split
+    kernel) or of 256 above (the fp16 decode pass), a variant other than 0 /
+    2 on the decode pass."""
     qt = make_other(ggml.GGML_TYPE_Q4_0, 64, 288, 5)
     xt = torch.randn((4, 288), device="cuda", dtype=torch.float16)
+    with pytest.raises(VBError, match="128"):
+        gemm(qt, xt)
+    xt = torch.randn((200, 288), device="cuda", dtype=torch.float16)
     with pytest.raises(VBError, match="256"):
         gemm(qt, xt)
+    qt = make_other(ggml.GGML_TYPE_Q4_1, 64, 384, 7)
+    with pytest.raises(ValueError):  # variant 5: k % 256
+        gemm(qt, torch.randn((256, 384), device="cuda", dtype=torch.float16), variant=GEMM_XREG)
     qt = make_other(ggml.GGML_TYPE_Q5_K, 64, 512, 6)
     with pytest.raises(VBError, match="Q5_K runs the tiled"):
         gemm(qt, torch.randn((4, 512), device="cuda", dtype=torch.float16), variant=GEMM_SKINNY)
@@ -689,6 +700,52 @@ def test_gemm_q5k_fused_matches_fp16_decode(m, n, k, dtype):
     y16 = gemm(qh, xt).cpu().numpy()
     assert O.rel_l2(y, y16.astype(np.float64)) <= 2e-3
     assert O.rel_l2(y, ref_gemm(qt, xt.float().cpu().numpy())) <= TOL
+@pytest.mark.parametrize("qtype", B32_TYPES)
+@pytest.mark.parametrize("m,n,k,dtype", [(1, 300, 512, torch.float16), (2, 130, 384, torch.float32),
+                                         (8, 1000, 4096, torch.float16), (17, 64, 1280, torch.float16),
+                                         (64, 257, 2048, torch.float32), (40, 9000, 256, torch.float16)])
+def test_b32_ksplit_kernel(qtype, m, n, k, dtype):
+    """Q4_0 / Q4_1 / Q5_0 / Q5_1 on the K-split kernel (one 18-24-byte block
+    per lane group, odd 18- and 22-byte blocks 2 bytes into a dword; K = 384
+    and 1280 leave steps over the 8 waves unevenly): variant 4 against the
+    oracle, the default route up to M = 128 (no workspace; the same bits), and
+    the fp16 decode pass on the tiled kernel (the same fp16 weights)."""
+    lib = _lib.load()
+    qt = make_other(qtype, n, k, m * 7 + n + k + qtype)
+    x = np.random.default_rng(m + 9).standard_normal((m, k)).astype(np.float32)
+    xt = torch.from_numpy(x).to("cuda", dtype)
+    y = gemm(qt, xt, variant=GEMM_KSPLIT).cpu().numpy()
+    assert y.shape == (m, n) and np.all(np.abs(y).sum(axis=1) > 0)
+    assert O.rel_l2(y, ref_gemm(qt, xt.float().cpu().numpy())) <= TOL
+    if m <= 128 and not (m == 1 and dtype == torch.float32):
+        assert lib.vb_gemm_workspace(m, n, k, qtype, 1 if dtype == torch.float16 else 0, 0) == 0
+        assert np.array_equal(gemm(qt, xt).cpu().numpy().view(np.uint32), y.view(np.uint32))
+    if k % 256 == 0:
+        t = gemm(qt, xt, variant=GEMM_TILED).cpu().numpy()
+        assert O.rel_l2(y, t.astype(np.float64)) <= 1e-5
+
+
+@pytest.mark.parametrize("qtype", B32_TYPES)
+@pytest.mark.parametrize("m,n,k", [(256, 224, 256), (300, 8192, 1024), (777, 128, 2048), (512, 4096, 14336)])
+def test_b32_xreg(qtype, m, n, k):
+    """The 32-element types on the packed-X kernel (9-12-piece windows of
+    eight blocks): variant 5 against the oracle and the tiled kernel on the
+    fp16 decode; the default route takes it at M > 256 where Q4_K does (the
+    same bits), with K splits at the down shape."""
+    lib = _lib.load()
+    qt = make_other(qtype, n, k, m + n + k + 3 * qtype)
+    x = np.random.default_rng(m + 10).standard_normal((m, k)).astype(np.float32)
+    xt = torch.from_numpy(x).to("cuda", torch.float16)
+    y = gemm(qt, xt, variant=GEMM_XREG).cpu().numpy()
+    assert y.shape == (m, n) and np.all(np.abs(y).sum(axis=1) > 0)
+    assert O.rel_l2(y, ref_gemm(qt, xt.float().cpu().numpy())) <= TOL
+    t = gemm(qt, xt, variant=GEMM_TILED).cpu().numpy()
+    assert O.rel_l2(y, t.astype(np.float64)) <= 1e-5
+    if m > 256 and (n >= 8192 or k >= 8192):
+        assert lib.vb_gemm_workspace(m, n, k, qtype, 1, 0) == lib.vb_gemm_workspace(m, n, k, qtype, 1, GEMM_XREG) > 0
+        assert np.array_equal(gemm(qt, xt).cpu().numpy().view(np.uint32), y.view(np.uint32))
+
+
 @pytest.mark.parametrize("m,n,k,dtype", [(2, 300, 512, torch.float16), (8, 1000, 4096, torch.float32),
                                          (17, 64, 768, torch.float16), (64, 257, 2048, torch.float16),
                                          (300, 130, 1024, torch.float32)])

@@ -633,6 +633,19 @@ int tiled_zsplit(int type, int x_dtype, int64_t M, int64_t N, int64_t K) {
 // kernel with fp16 weights; F16 weights are used in place.  The workspace,
 // n x k x 2 bytes (none for F16), comes from the caller (vb_gemm_ws) or is
 // allocated on the stream for the call (hipMallocAsync / hipFreeAsync).
+bool gemm_b32_type(int32_t type) {
+    return type == TYPE_Q4_0 || type == TYPE_Q4_1 || type == TYPE_Q5_0 || type == TYPE_Q5_1;
+}
+
+// Largest M the 32-element types take the K-split kernel at by default.
+// MI355X, fp16 X, Q4_0 / Q5_1: 14336 x 4096 at M = 1 / 8 / 64 / 128: 16.6 /
+// 19.7 / 31.9 / 55.9 and 17.3 / 19.9 / 34.4 / 59.3 us, against 76-79 us
+// through the fp16 decode pass and the tiled kernel; 4096 x 14336 at M = 8 /
+// 128: 18.7 / 90.5 and 18.8 / 94.5 against 112-115.  The packed-X kernel at
+// M = 512: 61.3 / 66.9 us (14336 x 4096) and 72.2 / 78.0 (4096 x 14336)
+// against 114.8-145.2.
+int64_t gemm_b32_kq_max_m(int64_t) { return 128; }
+
 bool gemm_other_type(int32_t type) {
     return type == TYPE_F32 || type == TYPE_F16 || type == TYPE_BF16 || type == TYPE_Q4_0 || type == TYPE_Q4_1 ||
            type == TYPE_Q5_0 || type == TYPE_Q5_1 || type == TYPE_Q2_K || type == TYPE_Q3_K;
@@ -740,6 +753,29 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
         // and 4096 < k <= 16384 on their split-row kernel
         if (type != TYPE_Q4_K && !general && K > 4096 && gemv_split_rpw(type, N, K) > 0)
             return gemv_split(type, w, X, Y, nullptr, N, K, st, true);
+    }
+    if (gemm_b32_type(type)) {
+        // Q4_0 / Q4_1 / Q5_0 / Q5_1: their decoder in the K-split kernel at
+        // small M (variant 4) and in the packed-X kernel for M > 256 with a
+        // workspace (variant 5); between, the fp16 decode pass and the tiled
+        // kernel (variants 0, 2)
+        if (variant == 4 || (variant == 0 && M <= gemm_b32_kq_max_m(N)))
+            return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
+        const int64_t xr_need = gemm_xr_workspace(M, N, K);
+        const bool xr_ok = x_dtype == X_F16 && M >= 256 && K % 256 == 0 && M <= INT32_MAX && N <= INT32_MAX &&
+                           K <= INT32_MAX && ((N * rb + 3) & ~int64_t(3)) < (int64_t(1) << 32) &&
+                           M * K * 2 < (int64_t(1) << 32) && ws != nullptr &&
+                           static_cast<int64_t>(ws_bytes) >= xr_need && reinterpret_cast<uintptr_t>(ws) % 16 == 0;
+        if (variant == 5) {
+            if (!xr_ok) {
+                set_error("vb_gemm: variant 5 takes fp16 X, m >= 256, k %% 256 == 0 and a 16-byte-aligned workspace "
+                          "of %lld bytes", static_cast<long long>(xr_need));
+                return E_INVAL;
+            }
+            return gemm_xr(w, X, Y, M, N, K, type, ws, st);
+        }
+        if (variant == 0 && xr_ok && M > 256 && (N >= 8192 || gemm_xr_ksplit(M, N, K) > 1))
+            return gemm_xr(w, X, Y, M, N, K, type, ws, st);
     }
     if (gemm_other_type(type)) return gemm_other(w, X, x_dtype, Y, M, N, K, type, variant, ws, ws_bytes, st);
     bool tiled = false;
@@ -908,6 +944,14 @@ extern "C" int vb_gemm(const void* w, const void* x, int32_t x_dtype, float* y, 
 extern "C" int64_t vb_gemm_workspace(int64_t m, int64_t n, int64_t k, int32_t ggml_type, int32_t x_dtype,
                                      int32_t variant) {
     if (k <= 0 || k % 256 != 0 || m <= 0 || n <= 0) return 0;
+    // the 32-element types: none on the K-split kernel, the packed X (and
+    // partial products) on the packed-X kernel
+    if (vb::gemm_b32_type(ggml_type)) {
+        if ((variant == 0 && m <= vb::gemm_b32_kq_max_m(n)) || variant == 4) return 0;
+        if ((variant == 5 && m >= 256 && x_dtype == 1) ||
+            (variant == 0 && x_dtype == 1 && m > 256 && (n >= 8192 || vb::gemm_xr_ksplit(m, n, k) > 1)))
+            return vb::gemm_xr_workspace(m, n, k);
+    }
     // the other types: their fp16 decode (none where the call runs the GEMV)
     if (vb::gemm_other_type(ggml_type))
         return m == 1 && x_dtype == 0 && variant == 0 ? 0 : vb::gemm_other_workspace(ggml_type, n, k);

@@ -31,6 +31,8 @@
 // address rounded down to 4 and realigned with v_alignbyte; the weight
 // resource spans the tensor rounded up to whole dwords (the last dword
 // holds tensor bytes, so it is mapped memory).
+#include <type_traits>
+
 #include "mfma_q4k.hpp"
 #include "vb_internal.hpp"
 #include "../../include/vbhip.h"
@@ -249,6 +251,57 @@ struct Kq<TYPE_Q8_0> {
         }
     }
 };
+
+// Q4_0 / Q4_1 / Q5_0 / Q5_1 (B32 in mfma_q4k.hpp): as Q8_0, a step is four
+// blocks, lane group g takes block 4 s + g whole and k-step ks its codes
+// [8 ks, +8) (kBlockLane).  The block (18-24 bytes) is read as the six
+// dwords from its start rounded down to 4 (rows are multiples of 8 bytes at
+// K % 128 == 0, so 18- and 22-byte blocks start 2 (g % 2) bytes into a
+// dword) and realigned.
+template <int TYPE>
+struct KqB32 {
+    static constexpr bool kBlockLane = true;
+    using B = B32<TYPE>;
+    struct Raw {
+        u32x3 q[2];
+    };
+    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t w, uint32_t rowoff, int step, int g,
+                                                 Raw& r) {
+        const uint32_t a = (rowoff + (4u * static_cast<uint32_t>(step) + static_cast<uint32_t>(g)) * B::kBytes) & ~3u;
+        r.q[0] = ld96(w, a);
+        r.q[1] = ld96(w, a + 12u);
+    }
+    __device__ static __forceinline__ void decode(const Raw& r, uint32_t rowoff, int, int g, const KqConsts& kc,
+                                                  Frag* f) {
+        const uint32_t w[6] = {r.q[0].x, r.q[0].y, r.q[0].z, r.q[1].x, r.q[1].y, r.q[1].z};
+        const uint32_t sh = (rowoff + static_cast<uint32_t>(g) * B::kBytes) & 3u;  // 0 or 2
+        // block bytes [4 i, 4 i + 4); of b[5] only bytes 20, 21 are used
+        // (the end of a 22-byte block, or a 24-byte block read aligned)
+        uint32_t b[6];
+#pragma unroll
+        for (int i = 0; i < 5; i++) b[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], sh);
+        b[5] = __builtin_amdgcn_alignbyte(w[5], w[5], sh);
+        half2_t d, nb;
+        b32_scales<TYPE>(b[0], d, nb);
+        // dword k of a field at block byte o (o even): bytes [o + 4 k, +4)
+        auto field = [&](uint32_t o, int k) -> uint32_t {
+            const int i = static_cast<int>(o >> 2) + k;
+            return (o & 3u) == 0 ? b[i] : __builtin_amdgcn_alignbyte(b[i + 1], b[i], 2u);
+        };
+        uint32_t qs[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) qs[k] = field(B::kQs, k);
+        const uint32_t qh = B::kHigh ? field(B::kQh, 0) : 0u;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++)
+            b32_frag<TYPE>(qs[2 * (ks & 1)], qs[2 * (ks & 1) + 1], static_cast<uint32_t>(ks >> 1),
+                           (qh >> (8 * ks)) & 0xFFu, d, nb, kc, f[ks]);
+    }
+};
+template <> struct Kq<TYPE_Q4_0> : KqB32<TYPE_Q4_0> {};
+template <> struct Kq<TYPE_Q4_1> : KqB32<TYPE_Q4_1> {};
+template <> struct Kq<TYPE_Q5_0> : KqB32<TYPE_Q5_0> {};
+template <> struct Kq<TYPE_Q5_1> : KqB32<TYPE_Q5_1> {};
 
 // X fragments of one step: A[ks][a] for activation rows 16 a + j.
 template <int XT, int MA>
@@ -552,7 +605,7 @@ void launch_kq_m(const uint8_t* w, uint32_t wbytes, const uint8_t* X, uint32_t x
 int gemm_kq(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, int64_t N, int64_t K, int32_t type,
             hipStream_t st) {
     if (K % KQ_STEP != 0) {
-        set_error("vb_gemm: Q8_0 weights need K %% 128 == 0 (K=%lld)", static_cast<long long>(K));
+        set_error("vb_gemm: the K-split kernel needs K %% 128 == 0 (K=%lld)", static_cast<long long>(K));
         return E_UNSUPPORTED;
     }
     const int64_t rb = row_bytes(type, K);
@@ -579,6 +632,18 @@ int gemm_kq(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, 
             launch_kq_m<TYPE_Q5_K, KQ_X_F16>(wb, wby, xb, xby, Y, m, n, k, rbu, st);
         else
             launch_kq_m<TYPE_Q5_K, KQ_X_F32>(wb, wby, xb, xby, Y, m, n, k, rbu, st);
+    } else if (type == TYPE_Q4_0 || type == TYPE_Q4_1 || type == TYPE_Q5_0 || type == TYPE_Q5_1) {
+        auto go = [&](auto t_c) {
+            constexpr int T = decltype(t_c)::value;
+            if (x_dtype == KQ_X_F16)
+                launch_kq_m<T, KQ_X_F16>(wb, wby, xb, xby, Y, m, n, k, rbu, st);
+            else
+                launch_kq_m<T, KQ_X_F32>(wb, wby, xb, xby, Y, m, n, k, rbu, st);
+        };
+        if (type == TYPE_Q4_0) go(std::integral_constant<int, TYPE_Q4_0>{});
+        else if (type == TYPE_Q4_1) go(std::integral_constant<int, TYPE_Q4_1>{});
+        else if (type == TYPE_Q5_0) go(std::integral_constant<int, TYPE_Q5_0>{});
+        else go(std::integral_constant<int, TYPE_Q5_1>{});
     } else if (type == TYPE_Q6_K) {
         if (x_dtype == KQ_X_F16)
             launch_kq_m<TYPE_Q6_K, KQ_X_F16>(wb, wby, xb, xby, Y, m, n, k, rbu, st);

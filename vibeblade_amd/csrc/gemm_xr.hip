@@ -126,6 +126,16 @@ template <> struct XrRaw<TYPE_Q5_K> {
     static constexpr uint32_t kBytes = 176;
     static constexpr bool kOneRaw = false;
 };
+// Q4_0 / Q4_1 / Q5_0 / Q5_1: eight 32-element blocks of 18-24 bytes
+template <int TYPE> struct XrRawB32 {
+    static constexpr int kPieces = static_cast<int>(B32<TYPE>::kBytes) / 2, kStride = kPieces;
+    static constexpr uint32_t kBytes = 8 * B32<TYPE>::kBytes;
+    static constexpr bool kOneRaw = false;
+};
+template <> struct XrRaw<TYPE_Q4_0> : XrRawB32<TYPE_Q4_0> {};
+template <> struct XrRaw<TYPE_Q4_1> : XrRawB32<TYPE_Q4_1> {};
+template <> struct XrRaw<TYPE_Q5_0> : XrRawB32<TYPE_Q5_0> {};
+template <> struct XrRaw<TYPE_Q5_1> : XrRawB32<TYPE_Q5_1> {};
 template <> struct XrRaw<TYPE_Q6_K> {
     static constexpr int kPieces = 14, kStride = 15;
     static constexpr uint32_t kBytes = 210;
@@ -194,6 +204,33 @@ __device__ __forceinline__ void xr_q8_item(const uint32_t* rw, int c, int g, con
     }
 }
 
+// 32-element block types (B32): chunk c is blocks 2 c (lo) and 2 c + 1 (hi),
+// codes [8 g, +8) of each (b32_frag); 18- and 22-byte blocks start on even
+// bytes, so each field is read as dwords realigned by its offset.
+template <int TYPE>
+__device__ __forceinline__ void xr_b32_item(const uint8_t* rw, int c, int g, const KqConsts& kc, Frag& lo,
+                                            Frag& hi) {
+    using B = B32<TYPE>;
+    const uint32_t* r32 = reinterpret_cast<const uint32_t*>(rw);
+    auto rd4 = [&](uint32_t o) -> uint32_t {  // bytes [o, o + 4), o even
+        if constexpr (B::kBytes % 4 == 0 && B::kQs % 4 == 0 && B::kQh % 4 == 0) {
+            return r32[o >> 2];
+        } else {
+            const uint32_t i = o >> 2;
+            return (o & 3u) ? __builtin_amdgcn_alignbyte(r32[i + 1], r32[i], o & 3u) : r32[i];
+        }
+    };
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const uint32_t bo = (2u * static_cast<uint32_t>(c) + h) * B::kBytes;
+        half2_t d, nb;
+        b32_scales<TYPE>(rd4(bo), d, nb);
+        const uint32_t qo = bo + B::kQs + 8u * static_cast<uint32_t>(g & 1);
+        const uint32_t qhb = B::kHigh ? (rd4(bo + B::kQh) >> (8 * g)) & 0xFFu : 0u;
+        b32_frag<TYPE>(rd4(qo), rd4(qo + 4u), static_cast<uint32_t>(g >> 1), qhb, d, nb, kc, h ? hi : lo);
+    }
+}
+
 // K split (blockIdx.z = kz of gridDim.z): the workgroup takes super-blocks
 // [kz nsb / KS, (kz + 1) nsb / KS) and writes its sums to Y + kz M N (the
 // caller's partial buffers when KS > 1; xr_ksum_kernel adds them).
@@ -210,7 +247,9 @@ __global__ void __launch_bounds__(XR_THREADS) gemm_xr_kernel(const uint8_t* __re
     constexpr int RAWS = R::kStride * 16 * NF;    // uint4 of one raw buffer in LDS
     constexpr int RPT = (RAW + 255) / 256;        // raw pieces per producer thread
     __shared__ uint4 bt[2 * SB];
-    __shared__ uint4 raw[(ONE ? 1 : 2) * RAWS];
+    // one spare piece: a realigned 32-element-block read may touch the dword
+    // past a window's last used byte
+    __shared__ uint4 raw[(ONE ? 1 : 2) * RAWS + 1];
 
     const int lane = static_cast<int>(threadIdx.x) & 63, j = lane & 15, g = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -400,9 +439,12 @@ __global__ void __launch_bounds__(XR_THREADS) gemm_xr_kernel(const uint8_t* __re
                 const uint32_t sh =
                     (static_cast<uint32_t>(n) * rb + static_cast<uint32_t>(sb0 + (sb < nsb ? sb : nsb - 1)) * 210u) & 15u;
                 xr_q6k_item(reinterpret_cast<const uint32_t*>(rw + (sh & ~3u)), sh & 3u, ic[q], g, kc, lo, hi);
-            } else {
+            } else if constexpr (TYPE == TYPE_Q8_0) {
                 (void)sb;
                 xr_q8_item(reinterpret_cast<const uint32_t*>(rw), ic[q], g, kc, lo, hi);
+            } else {
+                (void)sb;
+                xr_b32_item<TYPE>(rw, ic[q], g, kc, lo, hi);
             }
             uint4* dst = bt + buf * SB + ic[q] * SS + ifr[q] * 64 + lane;
             dst[0] = make_uint4(lo.u[0], lo.u[1], lo.u[2], lo.u[3]);
@@ -514,7 +556,8 @@ int64_t gemm_xr_workspace(int64_t M, int64_t N, int64_t K) {
 }
 
 bool gemm_xr_type(int32_t type) {
-    return type == TYPE_Q4_K || type == TYPE_Q5_K || type == TYPE_Q6_K || type == TYPE_Q8_0;
+    return type == TYPE_Q4_K || type == TYPE_Q5_K || type == TYPE_Q6_K || type == TYPE_Q8_0 || type == TYPE_Q4_0 ||
+           type == TYPE_Q4_1 || type == TYPE_Q5_0 || type == TYPE_Q5_1;
 }
 
 // Caller (gemm_dispatch) has validated the type (gemm_xr_type), alignment
@@ -545,6 +588,14 @@ int gemm_xr(const void* w, const void* X, float* Y, int64_t M, int64_t N, int64_
         gemm_xr_kernel<TYPE_Q5_K, NF><<<grid, dim3(XR_THREADS), 0, st>>>(wb, wbytes, xf, out, m, n, k, r);
     else if (type == TYPE_Q6_K)
         gemm_xr_kernel<TYPE_Q6_K, NF><<<grid, dim3(XR_THREADS), 0, st>>>(wb, wbytes, xf, out, m, n, k, r);
+    else if (type == TYPE_Q4_0)
+        gemm_xr_kernel<TYPE_Q4_0, NF><<<grid, dim3(XR_THREADS), 0, st>>>(wb, wbytes, xf, out, m, n, k, r);
+    else if (type == TYPE_Q4_1)
+        gemm_xr_kernel<TYPE_Q4_1, NF><<<grid, dim3(XR_THREADS), 0, st>>>(wb, wbytes, xf, out, m, n, k, r);
+    else if (type == TYPE_Q5_0)
+        gemm_xr_kernel<TYPE_Q5_0, NF><<<grid, dim3(XR_THREADS), 0, st>>>(wb, wbytes, xf, out, m, n, k, r);
+    else if (type == TYPE_Q5_1)
+        gemm_xr_kernel<TYPE_Q5_1, NF><<<grid, dim3(XR_THREADS), 0, st>>>(wb, wbytes, xf, out, m, n, k, r);
     else
         gemm_xr_kernel<TYPE_Q8_0, NF><<<grid, dim3(XR_THREADS), 0, st>>>(wb, wbytes, xf, out, m, n, k, r);
     if (ks > 1) {

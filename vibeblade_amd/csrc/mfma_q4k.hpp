@@ -238,6 +238,86 @@ __device__ __forceinline__ void q5k_frags(uint32_t q0, uint32_t q1, uint32_t h0,
     }
 }
 
+// ---- 32-element block types (GGUF Q4_0, Q4_1, Q5_0, Q5_1): fp16 d @0, fp16
+// m @2 (Q4_1, Q5_1), then qh (Q5_0 @2, Q5_1 @4: bit e is the fifth bit of
+// element e), then qs[16] (element e < 16: low nibble of qs[e], element
+// 16 + e: high nibble).  w = d (q - kBias) or d q + m.
+template <int TYPE> struct B32;
+template <> struct B32<TYPE_Q4_0> {
+    static constexpr uint32_t kBytes = 18, kQs = 2, kQh = 0;
+    static constexpr bool kMin = false, kHigh = false;
+    static constexpr int kBias = 8;
+};
+template <> struct B32<TYPE_Q4_1> {
+    static constexpr uint32_t kBytes = 20, kQs = 4, kQh = 0;
+    static constexpr bool kMin = true, kHigh = false;
+    static constexpr int kBias = 0;
+};
+template <> struct B32<TYPE_Q5_0> {
+    static constexpr uint32_t kBytes = 22, kQs = 6, kQh = 2;
+    static constexpr bool kMin = false, kHigh = true;
+    static constexpr int kBias = 16;
+};
+template <> struct B32<TYPE_Q5_1> {
+    static constexpr uint32_t kBytes = 24, kQs = 8, kQh = 4;
+    static constexpr bool kMin = true, kHigh = true;
+    static constexpr int kBias = 0;
+};
+
+// Codes [8 e, 8 e + 8) of one block as a B fragment (dword i: elements 2 i,
+// 2 i + 1): q0, q1 the qs bytes [8 (e % 2), +8), nibble nib = e / 2; qhb =
+// byte e of qh; d = {d, d}; nb = {m, m} (Q4_1, Q5_1) or {-kBias d, ..}
+// (Q4_0: exact, a power-of-two multiple of d).  4-bit codes become fp16
+// through the scaled fp8 conversion (a byte n < 16 is the e4m3 code of n
+// 2^-9), 5-bit codes through v_perm into halves 1024 + q (the qh bits spread
+// to bit 4 of each byte by a multiply: no two shifted copies overlap); each
+// weight is rounded to fp16 once.
+template <int TYPE>
+__device__ __forceinline__ void b32_frag(uint32_t q0, uint32_t q1, uint32_t nib, uint32_t qhb, half2_t d,
+                                         half2_t nb, const KqConsts& kc, Frag& f) {
+    using B = B32<TYPE>;
+    const uint32_t v[2] = {(q0 >> (4u * nib)) & 0x0F0F0F0Fu, (q1 >> (4u * nib)) & 0x0F0F0F0Fu};
+#pragma unroll
+    for (int dd = 0; dd < 2; dd++) {
+        if constexpr (!B::kHigh) {
+            const half2_t n01 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(v[dd], 512.0f, false);
+            const half2_t n23 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(v[dd], 512.0f, true);
+            f.u[2 * dd] = h2bits(__builtin_elementwise_fma(n01, d, nb));
+            f.u[2 * dd + 1] = h2bits(__builtin_elementwise_fma(n23, d, nb));
+        } else {
+            const uint32_t hb = (((qhb >> (4u * dd)) & 0xFu) * 0x00204081u) & 0x01010101u;
+            const uint32_t a = v[dd] | (hb << 4);
+            const half2_t h01 = bits2h(__builtin_amdgcn_perm(kc.h64, a, 0x07010500u));
+            const half2_t h23 = bits2h(__builtin_amdgcn_perm(kc.h64, a, 0x07030502u));
+            if constexpr (B::kMin) {
+                const half2_t k1024 = half2_t{static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+                f.u[2 * dd] = h2bits(__builtin_elementwise_fma(h01 - k1024, d, nb));
+                f.u[2 * dd + 1] = h2bits(__builtin_elementwise_fma(h23 - k1024, d, nb));
+            } else {
+                const _Float16 kb = static_cast<_Float16>(1024.0f + B::kBias);
+                const half2_t kbb = half2_t{kb, kb};
+                f.u[2 * dd] = h2bits((h01 - kbb) * d);
+                f.u[2 * dd + 1] = h2bits((h23 - kbb) * d);
+            }
+        }
+    }
+}
+
+// d and nb of b32_frag from the block's first dword (bytes 0-3 of the block)
+template <int TYPE>
+__device__ __forceinline__ void b32_scales(uint32_t w0, half2_t& d, half2_t& nb) {
+    using B = B32<TYPE>;
+    const uint32_t d16 = w0 & 0xFFFFu;
+    d = bits2h(d16 | (d16 << 16));
+    if constexpr (B::kMin) {
+        const uint32_t m16 = w0 >> 16;
+        nb = bits2h(m16 | (m16 << 16));
+    } else {
+        const _Float16 kb = static_cast<_Float16>(-static_cast<float>(B::kBias));
+        nb = d * half2_t{kb, kb};
+    }
+}
+
 // Q6_K codes to B-fragment dwords, 8 elements of each of two runs: l0 / l1
 // the ql bytes of the runs (nibble p of each), qh their common qh bytes
 // (bits 4 p, 4 p + 1 for the first run, 4 p + 2, 4 p + 3 for the second).

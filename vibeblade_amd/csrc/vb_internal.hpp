@@ -158,6 +158,11 @@ int dequant_rows_f16(const void* w, _Float16* out, int64_t n_rows, int64_t k, in
 // Weight types the batched GEMM runs through their fp16 decode (gemm.hip),
 // and the workspace that decode needs (n x k x 2 bytes; 0 for F16).
 bool gemm_other_type(int32_t type);
+// Q4_0 / Q4_1 / Q5_0 / Q5_1, which the K-split and packed-X kernels decode
+// themselves, and the largest M at which they take the K-split kernel by
+// default (gemm.hip)
+bool gemm_b32_type(int32_t type);
+int64_t gemm_b32_kq_max_m(int64_t N);
 int64_t gemm_other_workspace(int32_t type, int64_t N, int64_t K);
 int gemm_xr(const void* w, const void* X, float* Y, int64_t M, int64_t N, int64_t K, int32_t type, void* ws,
             hipStream_t st);
