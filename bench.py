@@ -111,10 +111,33 @@ def copies_for(bytes_per_copy: int, minimum: int = NCOPIES) -> int:
     return max(minimum, MIN_ROTATION_BYTES // max(1, bytes_per_copy) + 1)
 
 
+def random_blocks(qtype, n, k, rng):
+    """(n, row_bytes) uint8 of random blocks whose fp16 scale fields (d, and
+    dmin / m where the type has one) have exponent 2^-7 .. 2^-4 and a random
+    sign and mantissa: for the types vb_quantize_rows does not write."""
+    from vibeblade_amd import ggml
+    offsets = {ggml.GGML_TYPE_Q4_0: (0,), ggml.GGML_TYPE_Q4_1: (0, 2), ggml.GGML_TYPE_Q5_0: (0,),
+               ggml.GGML_TYPE_Q5_1: (0, 2), ggml.GGML_TYPE_Q5_K: (0, 2)}[qtype]
+    raw = rng.integers(0, 256, (n, ggml.row_bytes(qtype, k)), dtype=np.uint8)
+    blk = raw.reshape(-1, ggml.BLOCK[qtype][1])
+    for o in offsets:
+        blk[:, o + 1] = (blk[:, o + 1] & 0x83) | (0x20 + (blk[:, o] & 0x0C))
+    return raw
+
+
 def make_copies(qtype, n, k, ncopies, gen):
+    """Weight copies: N(0, 0.02) quantized on the device for Q4_K / Q6_K /
+    Q8_0, random blocks (random_blocks) for the other block types."""
     import torch
+    from vibeblade_amd import ggml
     from vibeblade_amd.tensor import QTensor
     copies = []
+    if qtype not in (ggml.GGML_TYPE_Q4_K, ggml.GGML_TYPE_Q6_K, ggml.GGML_TYPE_Q8_0):
+        rng = np.random.default_rng(SEED + qtype)
+        for _ in range(ncopies):
+            copies.append(QTensor.from_bytes(random_blocks(qtype, n, k, rng), qtype, n, k))
+        torch.cuda.synchronize()
+        return copies
     for _ in range(ncopies):
         w = torch.randn((n, k), generator=gen, device="cuda") * 0.02
         copies.append(QTensor.quantize(w, qtype))
@@ -1015,9 +1038,23 @@ def run_extra(which, args):
               "GB/s": gbs, "frac_hbm": fr, "rel_l2": e3, "dtype": DTYPE_GEMM if m > 1 else DTYPE_GEMV})
         torch.cuda.empty_cache()
     if "gemm" in which:
+        # the other weight types at the gate/up shape: Q6_K / Q8_0 (quantized
+        # on the device), Q5_K / Q4_0 (random blocks)
+        for qtype, name in ((ggml.GGML_TYPE_Q6_K, "Q6_K"), (ggml.GGML_TYPE_Q8_0, "Q8_0"),
+                            (ggml.GGML_TYPE_Q5_K, "Q5_K"), (ggml.GGML_TYPE_Q4_0, "Q4_0")):
+            n, k = 14336, 4096
+            wb = n * ggml.row_bytes(qtype, k)
+            for m in (8, 512):
+                tm, e3 = time_gemm(m, n, k, 20, 2, qtype=qtype)
+                tfs = 2.0 * m * n * k / (tm.ms * 1e-3) / 1e12
+                gbs, fr = frac(wb + 2 * m * k + 4 * m * n, tm)
+                emit({"workload": f"3: {name} GEMM M={m} N={n} K={k} fp16 X", "us_per_call": tm.us(),
+                      "launches": tm.launches, "TFLOP/s": round(tfs, 2),
+                      "frac_mfma_fp16": round(tfs / MFMA_FP16_PEAK_TFS, 4), "GB/s": gbs, "frac_hbm": fr,
+                      "rel_l2": e3, "dtype": DTYPE_GEMM})
+                torch.cuda.empty_cache()
         # the down projection: Q6_K in a Q4_K_M file, Q4_K in a Q4_K_S file,
         # Q8_0 in a Q8_0 file
-        from vibeblade_amd import ggml
         for qtype, name in ((ggml.GGML_TYPE_Q6_K, "Q6_K"), (ggml.GGML_TYPE_Q4_K, "Q4_K"),
                             (ggml.GGML_TYPE_Q8_0, "Q8_0")):
             n, k = 4096, 14336

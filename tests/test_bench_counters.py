@@ -53,3 +53,21 @@ def test_counter_table_mangled_names(tmp_path, capsys):
     out = capsys.readouterr().out.splitlines()
     assert "`vb::moe_gate_up_q4k<4>`" in out[0]
     assert out[3].split("|")[1].strip() == "SQ_WAVES" and out[3].split("|")[2].strip() == "7168"
+
+
+def test_random_blocks_decode_to_finite_moderate_weights():
+    """The random weight blocks of the GEMM lines for Q5_K and the 32-element
+    types decode (oracle) to finite weights of moderate size: the fp16 scale
+    fields get exponents 2^-7 .. 2^-4 whatever the random bytes were."""
+    import numpy as np
+    import oracle as O
+    from vibeblade_amd import ggml
+    rng = np.random.default_rng(3)
+    for qtype in (ggml.GGML_TYPE_Q4_0, ggml.GGML_TYPE_Q4_1, ggml.GGML_TYPE_Q5_0, ggml.GGML_TYPE_Q5_1,
+                  ggml.GGML_TYPE_Q5_K):
+        raw = bench.random_blocks(qtype, 7, 512, rng)
+        assert raw.shape == (7, ggml.row_bytes(qtype, 512)) and raw.dtype == np.uint8
+        w = O.dequantize(raw, 512, qtype)
+        assert np.all(np.isfinite(w))
+        # |d| < 2^-3 times at most 31 (Q5_0 / Q5_1 codes; Q5_K times a 6-bit sub-block scale, 63)
+        assert 0 < np.abs(w).max() < (300 if qtype == ggml.GGML_TYPE_Q5_K else 8) and np.abs(w).mean() > 1e-4
