@@ -148,13 +148,15 @@ int vb_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k,
  * Weight types: Q4_K (variants 0-5), Q6_K and Q8_0 (variants 0, 2, 4, 5; Q8_0
  * needs k % 128 == 0 at every m, m == 1 included, although vb_gemv itself
  * takes Q8_0 rows of any whole number of blocks); Q5_K (variants 0, 2, 4, 5)
- * with its own decoder in each kernel; Q4_0, Q4_1, Q5_0, Q5_1 with their
- * decoder in the K-split kernel (variant 4, k % 128 == 0; variant 0 up to
- * m = 128) and the packed-X kernel (variant 5; variant 0 above m = 256 where
- * Q4_K takes it), else (variants 0, 2) like Q2_K, Q3_K, BF16 and F32
- * (k % 256 == 0 except on the GEMV): decoded once to fp16 (each value
- * rounded once) into n x k x 2 bytes of workspace and multiplied on the
- * tiled kernel; F16 on the tiled kernel in place.  vb_gemm allocates that
+ * with its own decoder in each kernel; Q4_0, Q4_1, Q5_0, Q5_1 (variants 0,
+ * 2, 4, 5) with their decoder in the K-split kernel (variant 4, k % 128 ==
+ * 0; variant 0 up to m = 256 at n < 8192, 128 above), the tiled kernel
+ * (variant 2; variant 0 between those ranges for Q4_0 / Q4_1) and the
+ * packed-X kernel (variant 5; variant 0 above m = 256 where Q4_K takes it);
+ * Q5_0 / Q5_1 between the ranges with variant 0, and Q2_K, Q3_K, BF16 and
+ * F32 at every m (k % 256 == 0 except on the GEMV): decoded once to fp16
+ * (each value rounded once) into n x k x 2 bytes of workspace and
+ * multiplied on the tiled kernel; F16 on the tiled kernel in place.  vb_gemm allocates that
  * workspace on the stream for the call (stream-ordered), vb_gemm_ws takes
  * it from the caller.  W and x 16-byte aligned. */
 int vb_gemm(const void* w, const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n,

@@ -640,18 +640,21 @@ def make_other(qtype, n, k, seed):
                                          (1, 129, 256, torch.float16), (300, 1000, 1024, torch.float16),
                                          (2, 64, 4096, torch.float32)])
 def test_gemm_other_types(qtype, m, n, k, dtype):
-    """Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q2_K / Q3_K / BF16 / F32 weights are
-    decoded once to fp16 (one rounding, as the fused decoders round) and run
-    on the tiled kernel; F16 weights in place; Q5_K on the tiled kernel with
-    its fused decoder.  Against the fp64 product of the oracle's decode; the
-    workspace the call asks for; without a workspace (decoded into a
-    stream-ordered allocation) the same bits."""
+    """Q2_K / Q3_K / BF16 / F32 weights are decoded once to fp16 (one
+    rounding, as the fused decoders round) and run on the tiled kernel; F16
+    weights in place; Q5_K and the 32-element types with their own decoders
+    (no workspace at these shapes).  Against the fp64 product of the
+    oracle's decode; the workspace the call asks for; without a workspace
+    (decoded into a stream-ordered allocation) the same bits."""
     lib = _lib.load()
     qt = make_other(qtype, n, k, m + n + k + qtype)
     x = np.random.default_rng(m + k).standard_normal((m, k)).astype(np.float32)
     xt = torch.from_numpy(x).to("cuda", dtype)
     xdt = 1 if dtype == torch.float16 else 0
-    in_place = qtype in (ggml.GGML_TYPE_F16, ggml.GGML_TYPE_Q5_K) or (qtype in B32_TYPES and m <= 128)
+    # the 32-element types decode themselves, except Q5_0 / Q5_1 between the
+    # K-split kernel's range (M <= 256 at N < 8192, 128 above) and the packed-X one
+    five_bit_pass = qtype in (ggml.GGML_TYPE_Q5_0, ggml.GGML_TYPE_Q5_1) and m > (256 if n < 8192 else 128)
+    in_place = qtype in (ggml.GGML_TYPE_F16, ggml.GGML_TYPE_Q5_K) or (qtype in B32_TYPES and not five_bit_pass)
     want_ws = 0 if in_place or (m == 1 and xdt == 0) else n * k * 2
     assert lib.vb_gemm_workspace(m, n, k, qtype, xdt, 0) == want_ws
     y = gemm(qt, xt).cpu().numpy()
@@ -667,14 +670,14 @@ def test_gemm_other_types(qtype, m, n, k, dtype):
 
 def test_gemm_other_types_rejects():
     """Shapes and variants the kernels do not take fail with a clear error:
-    a 32-element type with K not a multiple of 128 at small M (the K-split
-    kernel) or of 256 above (the fp16 decode pass), a variant other than 0 /
-    2 on the decode pass."""
+    a 32-element type with K not a multiple of 128 on the K-split kernel or
+    of 256 above its range (the tiled kernel), a variant other than 0 / 2 on
+    the decode pass."""
     qt = make_other(ggml.GGML_TYPE_Q4_0, 64, 288, 5)
     xt = torch.randn((4, 288), device="cuda", dtype=torch.float16)
     with pytest.raises(VBError, match="128"):
         gemm(qt, xt)
-    xt = torch.randn((200, 288), device="cuda", dtype=torch.float16)
+    xt = torch.randn((300, 288), device="cuda", dtype=torch.float16)
     with pytest.raises(VBError, match="256"):
         gemm(qt, xt)
     qt = make_other(ggml.GGML_TYPE_Q4_1, 64, 384, 7)
@@ -723,6 +726,31 @@ def test_b32_ksplit_kernel(qtype, m, n, k, dtype):
     if k % 256 == 0:
         t = gemm(qt, xt, variant=GEMM_TILED).cpu().numpy()
         assert O.rel_l2(y, t.astype(np.float64)) <= 1e-5
+
+
+@pytest.mark.parametrize("qtype", B32_TYPES)
+@pytest.mark.parametrize("m,n,k,dtype", [(200, 300, 512, torch.float16), (129, 1000, 2048, torch.float32),
+                                         (256, 8192, 256, torch.float16), (40, 90, 768, torch.float16)])
+def test_b32_tiled_kernel(qtype, m, n, k, dtype):
+    """The 32-element types on the tiled kernel with their own decoder
+    (variant 2 at any M; the default for Q4_0 / Q4_1 at N >= 8192 and 128 < M
+    <= 256): against the oracle, and against the same kernel fed the oracle's
+    decode rounded to fp16 as F16 weights (the same fp16 weights, so the same
+    sums to fp32 rounding)."""
+    lib = _lib.load()
+    qt = make_other(qtype, n, k, m * 5 + n + k + qtype)
+    x = np.random.default_rng(m + 11).standard_normal((m, k)).astype(np.float32)
+    xt = torch.from_numpy(x).to("cuda", dtype)
+    y = gemm(qt, xt, variant=GEMM_TILED).cpu().numpy()
+    assert y.shape == (m, n) and np.all(np.abs(y).sum(axis=1) > 0)
+    assert O.rel_l2(y, ref_gemm(qt, xt.float().cpu().numpy())) <= TOL
+    wf16 = torch.from_numpy(O.dequantize(qt.to_numpy_bytes(), k, qtype).astype(np.float16)).cuda()
+    qh = QTensor.from_bytes(wf16.view(torch.uint8).reshape(-1), ggml.GGML_TYPE_F16, n, k)
+    y16 = gemm(qh, xt, variant=GEMM_TILED).cpu().numpy()
+    assert O.rel_l2(y, y16.astype(np.float64)) <= 1e-5
+    if 128 < m <= 256 and n >= 8192 and qtype in (ggml.GGML_TYPE_Q4_0, ggml.GGML_TYPE_Q4_1):
+        assert lib.vb_gemm_workspace(m, n, k, qtype, 1 if dtype == torch.float16 else 0, 0) == 0
+        assert np.array_equal(gemm(qt, xt).cpu().numpy().view(np.uint32), y.view(np.uint32))
 
 
 @pytest.mark.parametrize("qtype", B32_TYPES)

@@ -201,6 +201,42 @@ struct TiledW<TYPE_Q5_K> {
     }
 };
 
+// Q4_0 / Q4_1 / Q5_0 / Q5_1 (B32 in mfma_q4k.hpp): step s is blocks 2 s
+// (k-half 0) and 2 s + 1 (k-half 1); unit ug takes codes [8 ug, +8) of each.
+// Rows are multiples of 16 bytes (K % 256 == 0), so block 2 s starts on a
+// dword and block 2 s + 1 kBytes later (2 bytes into a dword for the 18- and
+// 22-byte blocks); each block is read as the six dwords from its start
+// rounded down to 4 (the four units of a row read the same bytes).
+template <int TYPE>
+struct TiledB32 {
+    static constexpr bool kPairOrder = false;
+    using B = B32<TYPE>;
+    struct Raw {
+        u32x3 a[2], b[2];
+    };
+    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t w, uint32_t rowoff, int step, uint32_t,
+                                                 Raw& r) {
+        const uint32_t o0 = rowoff + 2u * static_cast<uint32_t>(step) * B::kBytes;
+        const uint32_t o1 = (o0 + B::kBytes) & ~3u;
+        r.a[0] = ld96(w, o0);
+        r.a[1] = ld96(w, o0 + 12u);
+        r.b[0] = ld96(w, o1);
+        r.b[1] = ld96(w, o1 + 12u);
+    }
+    __device__ static __forceinline__ void decode(const Raw& r, uint32_t, int, uint32_t g8, const KqConsts& kc,
+                                                  Frag& lo, Frag& hi) {
+        const uint32_t wa[6] = {r.a[0].x, r.a[0].y, r.a[0].z, r.a[1].x, r.a[1].y, r.a[1].z};
+        const uint32_t wb[6] = {r.b[0].x, r.b[0].y, r.b[0].z, r.b[1].x, r.b[1].y, r.b[1].z};
+        const int e = static_cast<int>(g8 >> 3);
+        b32_block_frag<TYPE>(wa, 0u, e, kc, lo);
+        b32_block_frag<TYPE>(wb, B::kBytes & 3u, e, kc, hi);
+    }
+};
+template <> struct TiledW<TYPE_Q4_0> : TiledB32<TYPE_Q4_0> {};
+template <> struct TiledW<TYPE_Q4_1> : TiledB32<TYPE_Q4_1> {};
+template <> struct TiledW<TYPE_Q5_0> : TiledB32<TYPE_Q5_0> {};
+template <> struct TiledW<TYPE_Q5_1> : TiledB32<TYPE_Q5_1> {};
+
 // fp16 weights, row-major (a GGUF F16 tensor, or any other type decoded to
 // fp16 first): lane (row, ug) of a step's fragments is elements 8 ug .. +7
 // and 32 + 8 ug .. +7 of the step's 64, 16 bytes each, used as loaded.
@@ -627,15 +663,19 @@ int tiled_zsplit(int type, int x_dtype, int64_t M, int64_t N, int64_t K) {
     return 1;
 }
 
-// The types without a fused decoder: Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, BF16
-// and F32 weights are decoded once to fp16 (each value rounded once, as
-// the fused decoders round) into the workspace, then multiplied on the tiled
-// kernel with fp16 weights; F16 weights are used in place.  The workspace,
+// The 32-element block types (Q4_0, Q4_1, Q5_0, Q5_1) have their decoder in
+// the K-split, tiled and packed-X kernels.  The types without a fused
+// decoder: Q2_K, Q3_K, BF16 and F32 weights are decoded once to fp16 (each
+// value rounded once, as the fused decoders round) into the workspace, then
+// multiplied on the tiled kernel with fp16 weights; F16 weights are used in
+// place.  The workspace,
 // n x k x 2 bytes (none for F16), comes from the caller (vb_gemm_ws) or is
 // allocated on the stream for the call (hipMallocAsync / hipFreeAsync).
 bool gemm_b32_type(int32_t type) {
     return type == TYPE_Q4_0 || type == TYPE_Q4_1 || type == TYPE_Q5_0 || type == TYPE_Q5_1;
 }
+
+bool gemm_b32_high(int32_t type) { return type == TYPE_Q5_0 || type == TYPE_Q5_1; }
 
 // Largest M the 32-element types take the K-split kernel at by default.
 // MI355X, fp16 X, Q4_0 / Q5_1: 14336 x 4096 at M = 1 / 8 / 64 / 128: 16.6 /
@@ -644,11 +684,14 @@ bool gemm_b32_type(int32_t type) {
 // 128: 18.7 / 90.5 and 18.8 / 94.5 against 112-115.  The packed-X kernel at
 // M = 512: 61.3 / 66.9 us (14336 x 4096) and 72.2 / 78.0 (4096 x 14336)
 // against 114.8-145.2.
-int64_t gemm_b32_kq_max_m(int64_t) { return 128; }
+// At N < 8192 the K-split kernel stays ahead up to M = 256 (Q4_0 / Q5_1,
+// 4096 x 14336, M = 192 / 256: 87.6 / 87.1 and 90.9 / 89.9 us, against
+// 114.5-115.1 and 241.7-242.7 on the tiled kernel with TiledB32, about 114
+// through the decode pass).
+int64_t gemm_b32_kq_max_m(int64_t N) { return N < 8192 ? 256 : 128; }
 
 bool gemm_other_type(int32_t type) {
-    return type == TYPE_F32 || type == TYPE_F16 || type == TYPE_BF16 || type == TYPE_Q4_0 || type == TYPE_Q4_1 ||
-           type == TYPE_Q5_0 || type == TYPE_Q5_1 || type == TYPE_Q2_K || type == TYPE_Q3_K;
+    return type == TYPE_F32 || type == TYPE_F16 || type == TYPE_BF16 || type == TYPE_Q2_K || type == TYPE_Q3_K;
 }
 
 int64_t gemm_other_workspace(int32_t type, int64_t N, int64_t K) { return type == TYPE_F16 ? 0 : N * K * 2; }
@@ -707,7 +750,8 @@ int gemm_other(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t 
 
 int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, int64_t N, int64_t K,
                   int32_t type, int32_t variant, void* ws, size_t ws_bytes, hipStream_t st) {
-    if (type != TYPE_Q4_K && type != TYPE_Q6_K && type != TYPE_Q8_0 && type != TYPE_Q5_K && !gemm_other_type(type)) {
+    if (type != TYPE_Q4_K && type != TYPE_Q6_K && type != TYPE_Q8_0 && type != TYPE_Q5_K && !gemm_b32_type(type) &&
+        !gemm_other_type(type)) {
         set_error("vb_gemm: weight type %d has no batched path", type);
         return E_UNSUPPORTED;
     }
@@ -777,8 +821,27 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
         if (variant == 0 && xr_ok && M > 256 && (N >= 8192 || gemm_xr_ksplit(M, N, K) > 1))
             return gemm_xr(w, X, Y, M, N, K, type, ws, st);
     }
-    if (gemm_other_type(type)) return gemm_other(w, X, x_dtype, Y, M, N, K, type, variant, ws, ws_bytes, st);
     bool tiled = false;
+    if (gemm_b32_type(type)) {
+        // the tiled kernel with its own decoder (TiledB32); by default for
+        // the 4-bit types only: the 5-bit ones run the fp16 decode pass
+        // there (14336 x 4096, M = 192 / 256: Q4_0 72.0 / 73.1 us tiled,
+        // about 80 through the decode pass; Q5_1 106.7 / 105.5 tiled)
+        if (variant == 0 && gemm_b32_high(type))
+            return gemm_other(w, X, x_dtype, Y, M, N, K, type, variant, ws, ws_bytes, st);
+        if (variant != 0 && variant != 2) {
+            set_error("vb_gemm: type %d runs the K-split, tiled and packed-X kernels (variant 0, 2, 4 or 5, got %d)",
+                      type, variant);
+            return E_UNSUPPORTED;
+        }
+        if (K % 256 != 0) {
+            set_error("vb_gemm: the tiled kernel takes K %% 256 == 0 (K=%lld)", static_cast<long long>(K));
+            return E_UNSUPPORTED;
+        }
+        tiled = true;
+    } else if (gemm_other_type(type)) {
+        return gemm_other(w, X, x_dtype, Y, M, N, K, type, variant, ws, ws_bytes, st);
+    }
     if (type == TYPE_Q5_K) {
         // Q5_K: the K-split kernel at small M (every x dtype, M = 1
         // included), the tiled kernel with its fused decoder above, and the
@@ -795,7 +858,7 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
         if (variant == 4 || (variant == 0 && M <= (N < 8192 ? 64 : 32)))
             return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
         tiled = true;
-    } else if (type != TYPE_Q4_K) {
+    } else if (type == TYPE_Q6_K || type == TYPE_Q8_0) {
         // Q6_K / Q8_0: the K-split kernel (gemm_kq.hip) up to M = 64, where
         // it decodes each weight once; above, the tiled kernel, which decodes
         // each weight once per 64-256 rows of M (the K-split kernel once per
@@ -927,6 +990,18 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
     else if (type == TYPE_Q5_K)
         rc = x_dtype == X_F16 ? launch_tiled<TYPE_Q5_K, X_F16>(cfg, wb, wby, X, Y, m, n, k, rb, st)
                               : launch_tiled<TYPE_Q5_K, X_F32>(cfg, wb, wby, X, Y, m, n, k, rb, st);
+    else if (type == TYPE_Q4_0)
+        rc = x_dtype == X_F16 ? launch_tiled<TYPE_Q4_0, X_F16>(cfg, wb, wby, X, Y, m, n, k, rb, st)
+                              : launch_tiled<TYPE_Q4_0, X_F32>(cfg, wb, wby, X, Y, m, n, k, rb, st);
+    else if (type == TYPE_Q4_1)
+        rc = x_dtype == X_F16 ? launch_tiled<TYPE_Q4_1, X_F16>(cfg, wb, wby, X, Y, m, n, k, rb, st)
+                              : launch_tiled<TYPE_Q4_1, X_F32>(cfg, wb, wby, X, Y, m, n, k, rb, st);
+    else if (type == TYPE_Q5_0)
+        rc = x_dtype == X_F16 ? launch_tiled<TYPE_Q5_0, X_F16>(cfg, wb, wby, X, Y, m, n, k, rb, st)
+                              : launch_tiled<TYPE_Q5_0, X_F32>(cfg, wb, wby, X, Y, m, n, k, rb, st);
+    else if (type == TYPE_Q5_1)
+        rc = x_dtype == X_F16 ? launch_tiled<TYPE_Q5_1, X_F16>(cfg, wb, wby, X, Y, m, n, k, rb, st)
+                              : launch_tiled<TYPE_Q5_1, X_F32>(cfg, wb, wby, X, Y, m, n, k, rb, st);
     else
         rc = x_dtype == X_F16 ? launch_tiled<TYPE_Q8_0, X_F16>(cfg, wb, wby, X, Y, m, n, k, rb, st)
                               : launch_tiled<TYPE_Q8_0, X_F32>(cfg, wb, wby, X, Y, m, n, k, rb, st);
@@ -951,6 +1026,9 @@ extern "C" int64_t vb_gemm_workspace(int64_t m, int64_t n, int64_t k, int32_t gg
         if ((variant == 5 && m >= 256 && x_dtype == 1) ||
             (variant == 0 && x_dtype == 1 && m > 256 && (n >= 8192 || vb::gemm_xr_ksplit(m, n, k) > 1)))
             return vb::gemm_xr_workspace(m, n, k);
+        // the tiled kernel (variant 2; variant 0 for Q4_0 / Q4_1), or the
+        // fp16 decode pass (variant 0, Q5_0 / Q5_1)
+        return variant == 0 && vb::gemm_b32_high(ggml_type) ? n * k * 2 : 0;
     }
     // the other types: their fp16 decode (none where the call runs the GEMV)
     if (vb::gemm_other_type(ggml_type))

@@ -275,27 +275,8 @@ struct KqB32 {
                                                   Frag* f) {
         const uint32_t w[6] = {r.q[0].x, r.q[0].y, r.q[0].z, r.q[1].x, r.q[1].y, r.q[1].z};
         const uint32_t sh = (rowoff + static_cast<uint32_t>(g) * B::kBytes) & 3u;  // 0 or 2
-        // block bytes [4 i, 4 i + 4); of b[5] only bytes 20, 21 are used
-        // (the end of a 22-byte block, or a 24-byte block read aligned)
-        uint32_t b[6];
 #pragma unroll
-        for (int i = 0; i < 5; i++) b[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], sh);
-        b[5] = __builtin_amdgcn_alignbyte(w[5], w[5], sh);
-        half2_t d, nb;
-        b32_scales<TYPE>(b[0], d, nb);
-        // dword k of a field at block byte o (o even): bytes [o + 4 k, +4)
-        auto field = [&](uint32_t o, int k) -> uint32_t {
-            const int i = static_cast<int>(o >> 2) + k;
-            return (o & 3u) == 0 ? b[i] : __builtin_amdgcn_alignbyte(b[i + 1], b[i], 2u);
-        };
-        uint32_t qs[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++) qs[k] = field(B::kQs, k);
-        const uint32_t qh = B::kHigh ? field(B::kQh, 0) : 0u;
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++)
-            b32_frag<TYPE>(qs[2 * (ks & 1)], qs[2 * (ks & 1) + 1], static_cast<uint32_t>(ks >> 1),
-                           (qh >> (8 * ks)) & 0xFFu, d, nb, kc, f[ks]);
+        for (int ks = 0; ks < 4; ks++) b32_block_frag<TYPE>(w, sh, ks, kc, f[ks]);
     }
 };
 template <> struct Kq<TYPE_Q4_0> : KqB32<TYPE_Q4_0> {};

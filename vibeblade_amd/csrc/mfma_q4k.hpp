@@ -318,6 +318,30 @@ __device__ __forceinline__ void b32_scales(uint32_t w0, half2_t& d, half2_t& nb)
     }
 }
 
+// Codes [8 e, 8 e + 8) of a 32-element block from the six dwords that start
+// at the block's address rounded down to 4 (sh = that address % 4, 0 or 2).
+template <int TYPE>
+__device__ __forceinline__ void b32_block_frag(const uint32_t* w, uint32_t sh, int e, const KqConsts& kc, Frag& f) {
+    using B = B32<TYPE>;
+    // block bytes [4 i, 4 i + 4); of b[5] only bytes 20, 21 are used (the
+    // end of a 22-byte block, or a 24-byte block read aligned)
+    uint32_t b[6];
+#pragma unroll
+    for (int i = 0; i < 5; i++) b[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], sh);
+    b[5] = __builtin_amdgcn_alignbyte(w[5], w[5], sh);
+    half2_t d, nb;
+    b32_scales<TYPE>(b[0], d, nb);
+    // dword k of a field at block byte o (o even): bytes [o + 4 k, +4)
+    auto field = [&](uint32_t o, int k) -> uint32_t {
+        const int i = static_cast<int>(o >> 2) + k;
+        return (o & 3u) == 0 ? b[i] : __builtin_amdgcn_alignbyte(b[i + 1], b[i], 2u);
+    };
+    const uint32_t qo = B::kQs + 8u * static_cast<uint32_t>(e & 1);
+    const uint32_t qh = B::kHigh ? field(B::kQh, 0) : 0u;
+    b32_frag<TYPE>(field(qo, 0), field(qo, 1), static_cast<uint32_t>(e >> 1), (qh >> (8 * e)) & 0xFFu, d, nb, kc,
+                   f);
+}
+
 // Q6_K codes to B-fragment dwords, 8 elements of each of two runs: l0 / l1
 // the ql bytes of the runs (nibble p of each), qh their common qh bytes
 // (bits 4 p, 4 p + 1 for the first run, 4 p + 2, 4 p + 3 for the second).

@@ -162,6 +162,7 @@ bool gemm_other_type(int32_t type);
 // themselves, and the largest M at which they take the K-split kernel by
 // default (gemm.hip)
 bool gemm_b32_type(int32_t type);
+bool gemm_b32_high(int32_t type);  // Q5_0 / Q5_1
 int64_t gemm_b32_kq_max_m(int64_t N);
 int64_t gemm_other_workspace(int32_t type, int64_t N, int64_t K);
 int gemm_xr(const void* w, const void* X, float* Y, int64_t M, int64_t N, int64_t K, int32_t type, void* ws,
