@@ -298,7 +298,8 @@ int vb_topk_indices(const float* v, int64_t n, int32_t k, int32_t* out_idx, void
  * (vibeblade/moe_executor.py:331-344, vibeblade/moe.py:457-482,
  * cpp/src/fast_model.cpp:552-572).  wg / wu / wd: host arrays of n_exp
  * device pointers; Wg_e, Wu_e: i rows x h, Wd_e: h rows x i (GGUF layout,
- * Q4_K, Q6_K or Q8_0).  x: n_tokens x h fp32; router_logits: n_tokens x n_exp fp32;
+ * Q4_K, Q6_K, Q8_0, Q5_K, Q4_0, Q4_1, Q5_0 or Q5_1).  x: n_tokens x h fp32;
+ * router_logits: n_tokens x n_exp fp32;
  * y: n_tokens x h fp32; out_idx / out_w (optional, may be NULL):
  * n_tokens x topk routing result.  Experts may also be F32 (same shapes).
  * Replaces HotColdExecutor.dispatch's
@@ -312,7 +313,8 @@ int vb_moe_grouped_ffn(const void* const* wg, const void* const* wu, const void*
                        int32_t topk, float* y, int32_t* out_idx, float* out_w, int64_t h, int64_t i,
                        int32_t ggml_type, void* workspace, size_t workspace_bytes, void* stream);
 /* vb_moe_grouped_ffn with the gate/up type and the down type given apart:
- * each Q4_K, Q6_K or Q8_0 (or both F32), as a GGUF MoE layer stores
+ * each Q4_K, Q6_K, Q8_0, Q5_K, Q4_0, Q4_1, Q5_0 or Q5_1 (or both F32), as a
+ * GGUF MoE layer stores
  * ffn_gate_exps / ffn_up_exps and ffn_down_exps with their own types (the
  * engine's expert FFN, cpp/src/fast_model.cpp:552-572, takes each matrix with
  * its own type).  Same layout, limits and workspace as vb_moe_grouped_ffn,

@@ -313,6 +313,34 @@ def test_moe_mixed_types(gu, dn):
         assert torch.equal(y2, y)
 
 
+@pytest.mark.parametrize("gu,dn", [(ggml.GGML_TYPE_Q5_K, Q6K), (ggml.GGML_TYPE_Q4_0, ggml.GGML_TYPE_Q4_0),
+                                   (ggml.GGML_TYPE_Q4_1, ggml.GGML_TYPE_Q5_K), (ggml.GGML_TYPE_Q5_0, Q80),
+                                   (Q4K, ggml.GGML_TYPE_Q5_1)])
+def test_moe_more_types(gu, dn):
+    """Experts of Q5_K and the 32-element types (random blocks: a Q5_K_M
+    MoE file keeps Q5_K gate/up and Q6_K down; legacy files Q4_0 .. Q5_1) on
+    the expert-grouped K-split kernel, against the oracle: a spread routing
+    and one with an idle expert."""
+    from qblocks import rand_qblocks
+    e_n, h, i, t, topk = 4, 512, 768, 13, 2
+
+    def mk(qt, rows, k, seed):
+        return QTensor.from_bytes(rand_qblocks(qt, rows, k, seed), qt, rows, k)
+    gates = [mk(gu, i, h, 100 + e) for e in range(e_n)]
+    ups = [mk(gu, i, h, 200 + e) for e in range(e_n)]
+    downs = [mk(dn, h, i, 300 + e) for e in range(e_n)]
+    rng = np.random.default_rng(gu * 11 + dn)
+    x = (rng.standard_normal((t, h)) * 0.05).astype(np.float32)
+    for lg in (rng.standard_normal((t, e_n)).astype(np.float32),
+               np.where(np.arange(e_n) == 2, 3.0, -1.0).astype(np.float32)[None, :].repeat(t, 0)):
+        y, idx, _ = moe_grouped_ffn(gates, ups, downs, x, lg, topk)
+        want, widx, _ = moe_oracle(gates, ups, downs, x, lg, topk)
+        assert np.array_equal(idx.cpu().numpy(), widx)
+        yn = y.cpu().numpy()
+        assert np.all(np.isfinite(yn))
+        assert O.rel_l2(yn, want) <= 5e-3, (gu, dn)
+
+
 def test_moe_type_mix_rejected():
     from vibeblade_amd._lib import VBError
     gates, ups, downs = moe_weights(2, 256, 256, 3, Q4K, ggml.GGML_TYPE_F32)

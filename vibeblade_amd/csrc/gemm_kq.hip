@@ -639,7 +639,8 @@ int gemm_kq(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, 
     return check_launch("vb_gemm");
 }
 
-// Expert-grouped Q6_K / Q8_0 / Q4_K products for the MoE FFN; the caller
+// Expert-grouped products for the MoE FFN (Q6_K, Q8_0, Q5_K, Q4_0, Q4_1,
+// Q5_0, Q5_1; Q4_K where the caller sends it here); the caller
 // (moe.hip) has validated the shapes (K % 128 == 0, 32-bit offsets) and the
 // per-expert pointers.  gate_up: hout = fp16 silu(W0 x) * (W1 x) over
 // rows slot / topk of X (N = i, K = h); else fout = W0 x over rows slot of
@@ -664,14 +665,21 @@ int moe_kq(int32_t type, bool gate_up, const void* const* w0, const void* const*
         kernel<<<grid, dim3(64 * KQ_WAVES), lds, st>>>(a, b, wbytes, xb, xby, gate_up ? topk : 1, eoff, elist, n, k,
                                                        rbu, hout, fout);
     };
-    if (gate_up) {
-        if (type == TYPE_Q6_K) go(moe_kq_kernel<TYPE_Q6_K, 2, 2, 2>, 2, 2);
-        else if (type == TYPE_Q8_0) go(moe_kq_kernel<TYPE_Q8_0, 2, 2, 2>, 2, 2);
-        else go(moe_kq_kernel<TYPE_Q4_K, 2, 2, 2>, 2, 2);
-    } else {
-        if (type == TYPE_Q6_K) go(moe_kq_kernel<TYPE_Q6_K, 1, 1, 3>, 1, 1);
-        else if (type == TYPE_Q8_0) go(moe_kq_kernel<TYPE_Q8_0, 1, 1, 3>, 1, 1);
-        else go(moe_kq_kernel<TYPE_Q4_K, 1, 1, 3>, 1, 1);
+    // gate/up: two matrices, 32-slot tiles; down: one matrix, ring of three
+    auto run = [&](auto t_c) {
+        constexpr int T = decltype(t_c)::value;
+        if (gate_up) go(moe_kq_kernel<T, 2, 2, 2>, 2, 2);
+        else go(moe_kq_kernel<T, 1, 1, 3>, 1, 1);
+    };
+    switch (type) {
+        case TYPE_Q6_K: run(std::integral_constant<int, TYPE_Q6_K>{}); break;
+        case TYPE_Q8_0: run(std::integral_constant<int, TYPE_Q8_0>{}); break;
+        case TYPE_Q5_K: run(std::integral_constant<int, TYPE_Q5_K>{}); break;
+        case TYPE_Q4_0: run(std::integral_constant<int, TYPE_Q4_0>{}); break;
+        case TYPE_Q4_1: run(std::integral_constant<int, TYPE_Q4_1>{}); break;
+        case TYPE_Q5_0: run(std::integral_constant<int, TYPE_Q5_0>{}); break;
+        case TYPE_Q5_1: run(std::integral_constant<int, TYPE_Q5_1>{}); break;
+        default: run(std::integral_constant<int, TYPE_Q4_K>{}); break;
     }
     return check_launch("vb_moe_grouped_ffn");
 }

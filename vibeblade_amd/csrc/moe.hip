@@ -420,7 +420,10 @@ extern "C" int64_t vb_moe_workspace(int32_t n_tokens, int32_t topk, int64_t h, i
 }
 
 namespace {
-bool moe_quant_type(int32_t t) { return t == TYPE_Q4_K || t == TYPE_Q6_K || t == TYPE_Q8_0; }
+bool moe_quant_type(int32_t t) {
+    return t == TYPE_Q4_K || t == TYPE_Q6_K || t == TYPE_Q8_0 || t == TYPE_Q5_K || t == TYPE_Q4_0 || t == TYPE_Q4_1 ||
+           t == TYPE_Q5_0 || t == TYPE_Q5_1;
+}
 }  // namespace
 
 extern "C" int vb_moe_grouped_ffn_types(const void* const* wg, const void* const* wu, const void* const* wd,
@@ -438,8 +441,9 @@ extern "C" int vb_moe_grouped_ffn_types(const void* const* wg, const void* const
     }
     const bool f32 = gate_up_type == TYPE_F32 && down_type == TYPE_F32;
     if (!(f32 || (moe_quant_type(gate_up_type) && moe_quant_type(down_type))) || h % 256 != 0 || i % 256 != 0) {
-        set_error("vb_moe_grouped_ffn: experts of Q4_K / Q6_K / Q8_0 (gate/up and down each; or F32 throughout) "
-                  "with h, i multiples of 256 are supported (got gate/up %d, down %d)", gate_up_type, down_type);
+        set_error("vb_moe_grouped_ffn: experts of Q4_K / Q6_K / Q8_0 / Q5_K / Q4_0 / Q4_1 / Q5_0 / Q5_1 (gate/up "
+                  "and down each; or F32 throughout) with h, i multiples of 256 are supported (got gate/up %d, down "
+                  "%d)", gate_up_type, down_type);
         return E_UNSUPPORTED;
     }
     if (n_tokens == 0) return OK;
@@ -492,8 +496,9 @@ extern "C" int vb_moe_grouped_ffn_types(const void* const* wg, const void* const
         }
         _Float16* hb16 = reinterpret_cast<_Float16*>(hbuf);
         // Q4_K on the skinny tiles (one activation fragment per 16 slots
-        // serves four 16-row column groups); Q6_K / Q8_0 on the expert-grouped
-        // K-split kernel (gemm_kq.hip), gate/up with the same SwiGLU epilogue
+        // serves four 16-row column groups); the other types on the
+        // expert-grouped K-split kernel (gemm_kq.hip), gate/up with the same
+        // SwiGLU epilogue
         if (gate_up_type == TYPE_Q4_K) {
             const dim3 gu(static_cast<uint32_t>((i + skinny::ROWS - 1) / skinny::ROWS), n_exp);
             moe_gate_up_q4k<MOE_WAVES><<<gu, dim3(64 * MOE_WAVES), skinny::lds_bytes<MOE_WAVES>(), st>>>(
