@@ -128,9 +128,11 @@ int vb_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k,
  * Y[m, n] = sum_k X[m, k] * W[n, k]; X row-major (m x k) in fp32
  * (x_dtype = 0) or fp16 (x_dtype = 1), Y fp32 row-major (m x n).  Products
  * run on v_mfma_f32_16x16x32_f16 with W dequantized to fp16 in registers and
- * fp32 accumulation.  variant: 0 = choose, 1 = skinny (m <= 32), 2 = tiled
+ * fp32 accumulation.  variant: 0 = choose, 1 = skinny (m <= 32; m <= 64 with
+ * fp16 X), 2 = tiled
  * (every type; Q6_K / Q8_0 need k % 256 == 0), 3 = role-split (fp16 X only),
- * 4 = K-split (every type).  Variant 0 for Q4_K: 1 at m <= 32, 2 above, with
+ * 4 = K-split (every type).  Variant 0 for Q4_K: 1 at m <= 32 (m <= 64 for
+ * fp16 X and n >= 8192), 2 above, with
  * 4 at 17 <= m <= 32 for fp32 X and n < 12288, and at n < 8192 for
  * 33 <= m <= 64 and (k >= 8192) 2 <= m <= 16; 3 at 257 <= m <= 768 for fp16
  * X and n >= 8192.  Q6_K / Q8_0: 4 up to m = 64 (at n < 8192: Q6_K up to

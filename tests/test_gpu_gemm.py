@@ -119,6 +119,24 @@ def test_skinny_two_tiles(dtype, m, n, k):
     assert np.all(np.abs(y).sum(axis=1) > 0)  # every token row written
 
 
+@pytest.mark.parametrize("m,n,k", [(33, 16, 256), (48, 300, 1024), (64, 4100, 4096), (40, 14336, 4096),
+                                   (57, 33, 14336)])
+def test_skinny_four_tiles(m, n, k):
+    """33 <= M <= 64, fp16 X: four activation tiles share every dequantized
+    weight fragment (4-wave workgroups, the final sums in LDS past the
+    staging areas); ragged row counts and tokens past M; the default route
+    at N >= 8192 gives the same bits."""
+    qt, x = make(m, n, k, m * 13 + n)
+    xt = torch.from_numpy(x).to("cuda", torch.float16)
+    y = gemm(qt, xt, variant=GEMM_SKINNY).cpu().numpy()
+    want = ref_gemm(qt, xt.float().cpu().numpy())
+    assert y.shape == (m, n)
+    assert O.rel_l2(y, want) <= TOL
+    assert np.all(np.abs(y).sum(axis=1) > 0)
+    if n >= 8192:
+        assert np.array_equal(gemm(qt, xt).cpu().numpy().view(np.uint32), y.view(np.uint32))
+
+
 def test_tiled_matches_skinny_on_overlap():
     qt, x = make(16, 96, 1024, 5)
     xt = torch.from_numpy(x).to("cuda", torch.float16)
@@ -132,7 +150,9 @@ def test_gemm_rejects_bad_shapes():
     with pytest.raises(ValueError):
         gemm(qt, torch.zeros((4, 255), device="cuda"))
     with pytest.raises(ValueError):
-        gemm(qt, torch.zeros((33, 256), device="cuda"), variant=GEMM_SKINNY)
+        gemm(qt, torch.zeros((33, 256), device="cuda"), variant=GEMM_SKINNY)  # fp32 X: M <= 32
+    with pytest.raises(ValueError):
+        gemm(qt, torch.zeros((65, 256), device="cuda", dtype=torch.float16), variant=GEMM_SKINNY)
 
 
 @pytest.mark.parametrize("m", [8, 512])

@@ -900,10 +900,14 @@ int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64
         return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
     if (!tiled && variant == 0 && M >= 2 && M <= 16 && N < 8192 && K >= 8192)
         return gemm_kq(w, X, x_dtype, Y, M, N, K, type, st);
-    const bool skinny = !tiled && (variant == 1 || (variant == 0 && M <= 32));
+    // 33 <= M <= 64, fp16 X, N >= 8192: four activation tiles per wave
+    // (14336 x 4096, M = 33 / 48 / 64: 18.6 / 21.5 / 25.8 us against 24.5 /
+    // 25.1 / 25.9 tiled; at N < 8192 the K-split kernel above stays ahead)
+    const bool skinny = !tiled && (variant == 1 || (variant == 0 && (M <= 32 || (M <= 64 && x_dtype == X_F16))));
     if (skinny) {
-        if (M > 32) {
-            set_error("vb_gemm: variant 1 (skinny) takes M <= 32, got %lld", static_cast<long long>(M));
+        if (M > (x_dtype == X_F16 ? 64 : 32)) {
+            set_error("vb_gemm: variant 1 (skinny) takes M <= 32 (64 with fp16 X), got %lld",
+                      static_cast<long long>(M));
             return E_INVAL;
         }
         return gemm_q4k_skinny(w, X, x_dtype, Y, M, N, K, st);

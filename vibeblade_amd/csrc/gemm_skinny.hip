@@ -58,7 +58,8 @@ __global__ void __launch_bounds__(64 * NW) gemm_q4k_skinny_kernel(
 
 }  // namespace
 
-// Caller (gemm_dispatch) has validated type, M <= 32, alignment (W, X 16 B).
+// Caller (gemm_dispatch) has validated type, M <= 32 (M <= 64 with fp16 X),
+// alignment (W, X 16 B).
 int gemm_q4k_skinny(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, int64_t N, int64_t K,
                     hipStream_t st) {
     const int64_t nsb = K / 256, rb = nsb * 144;
@@ -78,7 +79,12 @@ int gemm_q4k_skinny(const void* w, const void* X, int32_t x_dtype, float* Y, int
     const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
     const int rbi = static_cast<int>(rb), rowsi = static_cast<int>(rows), nsbi = static_cast<int>(nsb);
     const uint32_t wbytes = static_cast<uint32_t>(N * rb), xby = static_cast<uint32_t>(xbytes);
-    if (M > 16) {
+    if (M > 32) {
+        // four activation tiles (fp16 X): 4-wave workgroups, one per CU
+        constexpr int NW4 = 4;
+        gemm_q4k_skinny_kernel<skinny::X_F16, 4, NW4><<<grid, dim3(64 * NW4), skinny::lds_bytes_mt<NW4, 4, 1>(), st>>>(
+            wb, xb, Y, m, n, k, rbi, rowsi, nsbi, wbytes, xby);
+    } else if (M > 16) {
         // two activation tiles: 4-wave workgroups (the register file of a
         // SIMD to one wave), one per CU
         constexpr int NW2 = 4;

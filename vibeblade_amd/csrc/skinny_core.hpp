@@ -45,6 +45,12 @@ constexpr int STAGE = ROWS * 144 + 16;     // per-wave LDS bytes (+ one discard 
 // sums (NMAT x NW x 4 KiB, NMAT <= 2) reuse.
 template <int NW = WAVES>
 constexpr int lds_bytes() { return NW * STAGE; }
+// With MT activation tiles of NMAT matrices the final sums take MT NMAT 4 KB
+// per wave, which passes the staging areas from MT NMAT = 3 on.
+template <int NW, int MT, int NMAT>
+constexpr int lds_bytes_mt() {
+    return NW * STAGE > MT * NMAT * NW * 4096 ? NW * STAGE : MT * NMAT * NW * 4096;
+}
 constexpr int LDS_BYTES = lds_bytes<WAVES>();
 constexpr int X_F32 = 0;
 constexpr int X_F16 = 1;
@@ -169,7 +175,8 @@ struct TileArgs {
 // workgroup on the CU cover that time.
 template <int XT, int NMAT, int RING = 2, int NW = WAVES, int MT = 1, bool PAIRS = false>
 __device__ __forceinline__ void tile(const TileArgs<NMAT, MT>& ta, uint8_t* lds, float4_t* out) {
-    static_assert(MT * NMAT * 4096 <= STAGE, "the final sums must fit in the staging areas");
+    // the launch gives the workgroup lds_bytes_mt<NW, MT, NMAT>() bytes: the
+    // staging areas, or the final sums where those need more
     static_assert(!PAIRS || (RING == 2 && XT == X_F16 && MT == 1), "paired units: a ring of two, fp16 X, one token tile");
     const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
