@@ -81,6 +81,11 @@ int gemm_q4k_skinny(const void* w, const void* X, int32_t x_dtype, float* Y, int
     const uint32_t wbytes = static_cast<uint32_t>(N * rb), xby = static_cast<uint32_t>(xbytes);
     if (M > 32) {
         // four activation tiles (fp16 X): 4-wave workgroups, one per CU
+        if (x_dtype != skinny::X_F16 || M > 64) {
+            set_error("vb_gemm: the skinny kernel takes M <= 32 (M <= 64 with fp16 X), got %lld",
+                      static_cast<long long>(M));
+            return E_INVAL;
+        }
         constexpr int NW4 = 4;
         gemm_q4k_skinny_kernel<skinny::X_F16, 4, NW4><<<grid, dim3(64 * NW4), skinny::lds_bytes_mt<NW4, 4, 1>(), st>>>(
             wb, xb, Y, m, n, k, rbi, rowsi, nsbi, wbytes, xby);
