@@ -341,6 +341,29 @@ def test_moe_more_types(gu, dn):
         assert O.rel_l2(yn, want) <= 5e-3, (gu, dn)
 
 
+@pytest.mark.parametrize("dn", [Q4K, Q6K])
+@pytest.mark.parametrize("topk", [1, 2, 3])
+def test_moe_combine_paths(dn, topk):
+    """Top-k <= 2: the down kernels add each slot's weighted output into y
+    (zeroed by the prep launch), so no combine launch runs; top-k = 3 keeps
+    the fixed-order combine.  Both against the oracle, with the routing
+    result returned either way; the atomic path repeats bit for bit (at most
+    two additions into zero per output)."""
+    e_n, h, i, t = 6, 512, 768, 11
+    gates, ups, downs = moe_weights(e_n, h, i, 40 + topk + dn, Q4K, dn)
+    rng = np.random.default_rng(topk * 5 + dn)
+    x = rng.standard_normal((t, h)).astype(np.float32)
+    logits = rng.standard_normal((t, e_n)).astype(np.float32)
+    y, idx, w = moe_grouped_ffn(gates, ups, downs, x, logits, topk)
+    want, widx, ww = moe_oracle(gates, ups, downs, x, logits, topk)
+    assert np.array_equal(idx.cpu().numpy(), widx)
+    assert np.allclose(w.cpu().numpy(), ww, rtol=1e-5, atol=1e-6)
+    assert O.rel_l2(y.cpu().numpy(), want) <= 5e-3
+    for _ in range(3):
+        y2, _, _ = moe_grouped_ffn(gates, ups, downs, x, logits, topk)
+        assert torch.equal(y2, y)
+
+
 def test_moe_type_mix_rejected():
     from vibeblade_amd._lib import VBError
     gates, ups, downs = moe_weights(2, 256, 256, 3, Q4K, ggml.GGML_TYPE_F32)

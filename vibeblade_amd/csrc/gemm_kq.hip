@@ -415,14 +415,18 @@ __global__ void __launch_bounds__(64 * KQ_WAVES) gemm_kq_kernel(const uint8_t* _
 // gemm_kq_kernel.  Activation rows are gathered: slot q reads row q / xdiv of
 // X (fp16; xdiv = topk for the tokens' rows, 1 for the hidden rows of the
 // slots).  NMAT = 2: gate and up weights over the same rows, written as fp16
-// silu(g) * u into hout[slot][n]; NMAT = 1: fp32 into fout[slot][n].
+// silu(g) * u into hout[slot][n]; NMAT = 1: fp32 into fout[slot][n], or
+// with yacc (top-k <= 2) rw[slot] times it added atomically to
+// yacc[slot / topk][n], which the caller has zeroed.
 template <int TYPE, int NMAT, int NCG, int RD>
 __global__ void __launch_bounds__(64 * KQ_WAVES) moe_kq_kernel(KqExperts w0, KqExperts w1, uint32_t wbytes,
                                                                const uint8_t* __restrict__ X, uint32_t xbytes,
                                                                int xdiv, const int32_t* __restrict__ eoff,
                                                                const int32_t* __restrict__ elist, int N, int K,
                                                                uint32_t rb, _Float16* __restrict__ hout,
-                                                               float* __restrict__ fout) {
+                                                               float* __restrict__ fout,
+                                                               const float* __restrict__ rw, int topk,
+                                                               float* __restrict__ yacc) {
     using T = Kq<TYPE>;
     extern __shared__ float4_t kq_red[];  // [wave][NMAT * NCG][lane]
     const int e = static_cast<int>(blockIdx.y);
@@ -518,10 +522,16 @@ __global__ void __launch_bounds__(64 * KQ_WAVES) moe_kq_kernel(KqExperts w0, KqE
                 const int t = 4 * (l >> 4) + r;
                 if (t >= nrow) continue;
                 const int64_t o = static_cast<int64_t>(slots[m0 + t]) * N + col;
-                if constexpr (NMAT == 2)
+                if constexpr (NMAT == 2) {
                     hout[o] = static_cast<_Float16>(s0[r] / (1.0f + __expf(-s0[r])) * s1[r]);
-                else
+                } else if (yacc) {
+                    // the token's weighted sum over its (at most two) slots:
+                    // two additions into zero, in either order the same bits
+                    const int q = slots[m0 + t];
+                    unsafeAtomicAdd(yacc + static_cast<int64_t>(q / topk) * N + col, rw[q] * s0[r]);
+                } else {
                     fout[o] = s0[r];
+                }
             }
         }
         __syncthreads();  // kq_red is rewritten by the next 16 slots
@@ -647,7 +657,7 @@ int gemm_kq(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, 
 // X (N = h, K = i).
 int moe_kq(int32_t type, bool gate_up, const void* const* w0, const void* const* w1, int n_exp, const void* X,
            int64_t xbytes, int topk, const int32_t* eoff, const int32_t* elist, int64_t N, int64_t K,
-           _Float16* hout, float* fout, hipStream_t st) {
+           _Float16* hout, float* fout, const float* rw, float* yacc, hipStream_t st) {
     if (n_exp > MOE_KQ_MAX_EXPERTS || K % KQ_STEP != 0) return E_UNSUPPORTED;
     KqExperts a{}, b{};
     for (int e = 0; e < n_exp; e++) {
@@ -663,7 +673,7 @@ int moe_kq(int32_t type, bool gate_up, const void* const* w0, const void* const*
         const dim3 grid(static_cast<uint32_t>((N + 16 * ncg - 1) / (16 * ncg)), static_cast<uint32_t>(n_exp));
         const size_t lds = static_cast<size_t>(KQ_WAVES) * nmat * ncg * 64 * sizeof(float4_t);
         kernel<<<grid, dim3(64 * KQ_WAVES), lds, st>>>(a, b, wbytes, xb, xby, gate_up ? topk : 1, eoff, elist, n, k,
-                                                       rbu, hout, fout);
+                                                       rbu, hout, fout, rw, topk, yacc);
     };
     // gate/up: two matrices, 32-slot tiles; down: one matrix, ring of three
     auto run = [&](auto t_c) {

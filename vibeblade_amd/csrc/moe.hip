@@ -222,7 +222,8 @@ constexpr int PREP_THREADS = 1024;
 __global__ void __launch_bounds__(PREP_THREADS) moe_prep_kernel(
         const float* __restrict__ x, const float* __restrict__ logits, int t_n, int e_n, int topk, int64_t nx,
         _Float16* __restrict__ xh, int32_t* __restrict__ ridx, float* __restrict__ rw, int32_t* __restrict__ eoff,
-        int32_t* __restrict__ elist) {
+        int32_t* __restrict__ elist, float* __restrict__ yzero, int32_t* __restrict__ out_idx,
+        float* __restrict__ out_w) {
     if (blockIdx.x > 0) {
         const int64_t i8 = (static_cast<int64_t>(blockIdx.x - 1) * PREP_THREADS + threadIdx.x) * 8;
         if (i8 < nx) {  // nx = t_n * h, a multiple of 256
@@ -231,6 +232,10 @@ __global__ void __launch_bounds__(PREP_THREADS) moe_prep_kernel(
             uint32_t o[4];
             f32x8_to_frag_nat(a, b, o);
             *reinterpret_cast<uint4*>(xh + i8) = make_uint4(o[0], o[1], o[2], o[3]);
+            if (yzero) {  // y has x's shape; the down kernels add into it
+                *reinterpret_cast<float4*>(yzero + i8) = make_float4(0.f, 0.f, 0.f, 0.f);
+                *reinterpret_cast<float4*>(yzero + i8 + 4) = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
         }
         return;
     }
@@ -242,6 +247,12 @@ __global__ void __launch_bounds__(PREP_THREADS) moe_prep_kernel(
         route_token_wave(logits + static_cast<int64_t>(t) * e_n, e_n, topk, ridx + t * topk, rw + t * topk,
                          sexp + t * topk);
     __syncthreads();
+    if (yzero) {  // no combine launch follows: the routing result is written here
+        for (int q = static_cast<int>(threadIdx.x); q < nslots; q += PREP_THREADS) {
+            if (out_idx) out_idx[q] = ridx[q];
+            if (out_w) out_w[q] = rw[q];
+        }
+    }
     // counts per expert, then exclusive offsets (slots with no expert -- NaN
     // logits -- are in no list)
     if (threadIdx.x < e_n) {
@@ -325,7 +336,7 @@ template <int NW>
 __global__ void __launch_bounds__(64 * NW, NW <= 4 ? 2 : 1) moe_down_q4k(
         ExpertPtrs wd, const _Float16* __restrict__ hbuf, const int32_t* __restrict__ eoff,
         const int32_t* __restrict__ elist, int h, int i_dim, int rb, uint32_t wbytes, uint32_t hbytes,
-        float* __restrict__ obuf) {
+        float* __restrict__ obuf, const float* __restrict__ rw, int topk, float* __restrict__ yacc) {
     extern __shared__ skinny::u32x4 moe_lds[];
     const int e = blockIdx.y;
     const int base = eoff[e], cnt = eoff[e + 1] - base;
@@ -353,7 +364,12 @@ __global__ void __launch_bounds__(64 * NW, NW <= 4 ? 2 : 1) moe_down_q4k(
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
                     const int t = 4 * (l >> 4) + v;
-                    if (t < nrow) obuf[static_cast<int64_t>(slots[m0 + t]) * h + n] = s[0][v];
+                    if (t >= nrow) continue;
+                    const int q = slots[m0 + t];
+                    if (yacc)  // at most two additions into zero: the same bits in either order
+                        unsafeAtomicAdd(yacc + static_cast<int64_t>(q / topk) * h + n, rw[q] * s[0][v]);
+                    else
+                        obuf[static_cast<int64_t>(q) * h + n] = s[0][v];
                 }
             }
         }
@@ -483,8 +499,12 @@ extern "C" int vb_moe_grouped_ffn_types(const void* const* wg, const void* const
     int32_t* elist = reinterpret_cast<int32_t*>(wsb + ws.elist);
     // 1. routing, per-expert slot lists, fp16 activations
     const dim3 prep(static_cast<uint32_t>(1 + (nx / 8 + PREP_THREADS - 1) / PREP_THREADS));
+    // top-k <= 2 on the quantized experts: the down kernels add each slot's
+    // weighted output into y (zeroed here), so no combine launch follows
+    const bool fused_combine = !f32 && topk <= 2;
+    float* yacc = fused_combine ? y : nullptr;
     moe_prep_kernel<<<prep, dim3(PREP_THREADS), 0, st>>>(x, router_logits, n_tokens, n_exp, topk, nx, xh, ridx, rw,
-                                                         eoff, elist);
+                                                         eoff, elist, yacc, out_idx, out_w);
     int rc = check_launch("vb_moe_grouped_ffn");
     if (rc != OK) return rc;
     // 2, 3. experts
@@ -506,16 +526,16 @@ extern "C" int vb_moe_grouped_ffn_types(const void* const* wg, const void* const
                 static_cast<uint32_t>(i * rb_gu), static_cast<uint32_t>(nx * 2), hb16);
             if ((rc = check_launch("vb_moe_grouped_ffn")) != OK) return rc;
         } else if ((rc = moe_kq(gate_up_type, true, wg, wu, n_exp, xh, nx * 2, topk, eoff, elist, i, h, hb16, nullptr,
-                                st)) != OK) {
+                                nullptr, nullptr, st)) != OK) {
             return rc;
         }
         if (down_type == TYPE_Q4_K) {
             const dim3 dn(static_cast<uint32_t>((h + skinny::ROWS - 1) / skinny::ROWS), n_exp);
             moe_down_q4k<MOE_WAVES><<<dn, dim3(64 * MOE_WAVES), skinny::lds_bytes<MOE_WAVES>(), st>>>(
                 pd, hb16, eoff, elist, static_cast<int>(h), static_cast<int>(i), static_cast<int>(rb_d),
-                static_cast<uint32_t>(h * rb_d), static_cast<uint32_t>(slots * i * 2), obuf);
+                static_cast<uint32_t>(h * rb_d), static_cast<uint32_t>(slots * i * 2), obuf, rw, topk, yacc);
         } else if ((rc = moe_kq(down_type, false, wd, nullptr, n_exp, hb16, slots * i * 2, topk, eoff, elist, h, i,
-                                nullptr, obuf, st)) != OK) {
+                                nullptr, obuf, rw, yacc, st)) != OK) {
             return rc;
         }
     } else {
@@ -527,7 +547,8 @@ extern "C" int vb_moe_grouped_ffn_types(const void* const* wg, const void* const
                                                                  obuf);
     }
     if ((rc = check_launch("vb_moe_grouped_ffn")) != OK) return rc;
-    // 4. weighted combine
+    // 4. weighted combine (F32 experts, top-k > 2)
+    if (fused_combine) return OK;
     moe_combine_routed<<<dim3(static_cast<uint32_t>(n_tokens), static_cast<uint32_t>((h + 1023) / 1024)), dim3(256), 0,
                          st>>>(obuf, ridx, rw, topk, h, y, out_idx, out_w);
     return check_launch("vb_moe_grouped_ffn");
