@@ -253,6 +253,28 @@ __global__ void __launch_bounds__(PREP_THREADS) moe_prep_kernel(
             if (out_w) out_w[q] = rw[q];
         }
     }
+    if (nslots <= 64) {
+        // one wave: expert e's slots are the lanes whose expert is e; a
+        // ballot per expert gives its count, the running total its offset,
+        // and the lanes below a slot with the same expert its position
+        // (slot order, as the loops below)
+        if (threadIdx.x < 64) {
+            const int q = static_cast<int>(threadIdx.x);
+            const int eq = q < nslots ? sexp[q] : -1;
+            const uint64_t below = (uint64_t(1) << q) - 1u;
+            int total = 0, my_off = 0, my_pos = -1;
+            for (int e = 0; e < e_n; e++) {
+                const uint64_t m = __ballot(eq == e);
+                if (q == e) my_off = total;
+                if (eq == e) my_pos = total + __popcll(m & below);
+                total += __popcll(m);
+            }
+            if (q < e_n) eoff[q] = my_off;
+            if (q == 0) eoff[e_n] = total;
+            if (my_pos >= 0) elist[my_pos] = q;
+        }
+        return;
+    }
     // counts per expert, then exclusive offsets (slots with no expert -- NaN
     // logits -- are in no list)
     if (threadIdx.x < e_n) {
