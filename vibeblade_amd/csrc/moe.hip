@@ -38,9 +38,61 @@ struct ExpertPtrs {
     const uint8_t* p[MOE_MAX_EXPERTS];
 };
 
+// Butterfly exchanges over a wave without LDS: quad xor 1 and 2, half-row
+// and row mirrors (DPP), then the 16- and 32-lane halves swapped
+// (v_permlane16 / v_permlane32_swap).  Each step pairs lanes symmetrically,
+// so a commutative combine leaves every lane with the same bits.
+template <typename C>
+__device__ __forceinline__ float wave_allreduce_f(float v, C comb) {
+    v = comb(v, dpp_f<0xB1>(v));
+    v = comb(v, dpp_f<0x4E>(v));
+    v = comb(v, dpp_f<0x141>(v));
+    v = comb(v, dpp_f<0x140>(v));
+    const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = comb(__uint_as_float(s16[0]), __uint_as_float(s16[1]));
+    const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return comb(__uint_as_float(s32[0]), __uint_as_float(s32[1]));
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+// (p, id) of the lane that ranks first by (p desc, id asc), a total order,
+// on every lane
+__device__ __forceinline__ void wave_argmax(float& bp, int& bi) {
+    auto take = [&](float op, int oi) {
+        if (op > bp || (op == bp && oi < bi)) {
+            bp = op;
+            bi = oi;
+        }
+    };
+    take(dpp_f<0xB1>(bp), dpp_i<0xB1>(bi));
+    take(dpp_f<0x4E>(bp), dpp_i<0x4E>(bi));
+    take(dpp_f<0x141>(bp), dpp_i<0x141>(bi));
+    take(dpp_f<0x140>(bp), dpp_i<0x140>(bi));
+    {
+        const auto sp = __builtin_amdgcn_permlane16_swap(__float_as_uint(bp), __float_as_uint(bp), false, false);
+        const auto si = __builtin_amdgcn_permlane16_swap(static_cast<uint32_t>(bi), static_cast<uint32_t>(bi), false,
+                                                         false);
+        bp = __uint_as_float(sp[0]);
+        bi = static_cast<int>(si[0]);
+        take(__uint_as_float(sp[1]), static_cast<int>(si[1]));
+    }
+    {
+        const auto sp = __builtin_amdgcn_permlane32_swap(__float_as_uint(bp), __float_as_uint(bp), false, false);
+        const auto si = __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(bi), static_cast<uint32_t>(bi), false,
+                                                         false);
+        bp = __uint_as_float(sp[0]);
+        bi = static_cast<int>(si[0]);
+        take(__uint_as_float(sp[1]), static_cast<int>(si[1]));
+    }
+}
+
 // Route one token with one wave, lane e = expert e (e_n <= 64): top-k of
 // softmax(clamp(logits, -50, 50)), renormalised; ties go to the lower expert
-// id.  Max and sum are xor butterflies (every lane ends with the same bits:
+// id.  Max and sum are butterflies (every lane ends with the same bits:
 // each step adds the same two values, a + b == b + a); the top k come out
 // one per round of a butterfly argmax over (p desc, id asc), a total order,
 // so every lane agrees on the winner.  Lanes k < topk write slot k.
@@ -52,27 +104,16 @@ __device__ __forceinline__ void route_token_wave(const float* __restrict__ logit
     const bool live = lane < e_n;
     float z = logits[live ? lane : e_n - 1];  // clamped index: the load stays outside any branch
     z = live ? fminf(fmaxf(z, -50.f), 50.f) : -INFINITY;
-    float mx = z;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    const float mx = wave_allreduce_f(z, [](float a, float b) { return fmaxf(a, b); });
     const float ex = live ? __expf(z - mx) : 0.f;
-    float den = ex;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) den += __shfl_xor(den, off);
+    const float den = wave_allreduce_f(ex, [](float a, float b) { return a + b; });
     float p = live ? ex / den : -1.f;  // absent experts rank below every live one
     float s = 0.f, myw = 0.f;
     int myi = -1;
     for (int k = 0; k < topk; k++) {
         float bp = p;
         int bi = lane;
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            const float op = __shfl_xor(bp, off);
-            const int oi = __shfl_xor(bi, off);
-            const bool take = op > bp || (op == bp && oi < bi);
-            bp = take ? op : bp;
-            bi = take ? oi : bi;
-        }
+        wave_argmax(bp, bi);
         s += bp;
         if (lane == k) {
             myw = bp;
