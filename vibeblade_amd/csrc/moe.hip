@@ -99,7 +99,8 @@ __device__ __forceinline__ void wave_argmax(float& bp, int& bi) {
 // The weight sum runs in rank order.
 __device__ __forceinline__ void route_token_wave(const float* __restrict__ logits, int e_n, int topk,
                                                  int32_t* __restrict__ out_idx, float* __restrict__ out_w,
-                                                 int* __restrict__ sexp) {
+                                                 int* __restrict__ sexp, int32_t* __restrict__ copy_idx = nullptr,
+                                                 float* __restrict__ copy_w = nullptr) {
     const int lane = threadIdx.x & 63;
     const bool live = lane < e_n;
     float z = logits[live ? lane : e_n - 1];  // clamped index: the load stays outside any branch
@@ -123,9 +124,12 @@ __device__ __forceinline__ void route_token_wave(const float* __restrict__ logit
     }
     s = s < 1e-12f ? 1.f : s;
     if (lane < topk) {
+        const float wn = myw / s;
         out_idx[lane] = myi;
-        out_w[lane] = myw / s;
+        out_w[lane] = wn;
         if (sexp) sexp[lane] = myi;
+        if (copy_idx) copy_idx[lane] = myi;  // the caller's routing outputs, from registers
+        if (copy_w) copy_w[lane] = wn;
     }
 }
 
@@ -284,16 +288,14 @@ __global__ void __launch_bounds__(PREP_THREADS) moe_prep_kernel(
     __shared__ int scnt[MOE_MAX_EXPERTS + 1];
     const int nslots = t_n * topk;
     // one wave per token
+    // with yzero no combine launch follows, and the routing result goes to
+    // out_idx / out_w here
+    int32_t* const cidx = yzero ? out_idx : nullptr;
+    float* const cw = yzero ? out_w : nullptr;
     for (int t = static_cast<int>(threadIdx.x >> 6); t < t_n; t += PREP_THREADS / 64)
         route_token_wave(logits + static_cast<int64_t>(t) * e_n, e_n, topk, ridx + t * topk, rw + t * topk,
-                         sexp + t * topk);
+                         sexp + t * topk, cidx ? cidx + t * topk : nullptr, cw ? cw + t * topk : nullptr);
     __syncthreads();
-    if (yzero) {  // no combine launch follows: the routing result is written here
-        for (int q = static_cast<int>(threadIdx.x); q < nslots; q += PREP_THREADS) {
-            if (out_idx) out_idx[q] = ridx[q];
-            if (out_w) out_w[q] = rw[q];
-        }
-    }
     if (nslots <= 64) {
         // one wave: expert e's slots are the lanes whose expert is e; a
         // ballot per expert gives its count, the running total its offset,
