@@ -173,6 +173,10 @@ def time_launches(launch_fns, steps, warmup, min_launches=200):
     max(steps, ceil(min_launches / launches per step)) timed steps, each
     bracketed by HIP events on the replay stream.  Returns a Timing."""
     import torch
+    # the inputs were made on torch's current stream, and the closures run on
+    # a new one: wait for every pending kernel first, so no buffer (nor a
+    # block the caching allocator handed out again) is still being written
+    torch.cuda.synchronize()
     stream = torch.cuda.Stream()
     passes = -(-GRAPH_MIN_LAUNCHES // len(launch_fns))
     nl = passes * len(launch_fns)

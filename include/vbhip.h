@@ -8,6 +8,13 @@
  * the default stream).  Launches are asynchronous on `stream`.  There is no
  * global scratch state: functions that need temporaries take a caller-owned
  * workspace, so calls on different streams or threads are independent.
+ * Every buffer of a call (inputs, outputs, workspace) must be ready in the
+ * order of `stream` when the call is enqueued: memory that work on another
+ * stream still writes (a block a caching allocator handed out again while a
+ * kernel on its old stream is pending, say) needs an event wait or a
+ * synchronisation first.  The MoE routing lists in the workspace are used as
+ * indices, so such a race there ends in out-of-bounds accesses, not just in
+ * wrong values.
  *
  * Weights are GGUF tensors in the on-disk layout: n rows of k elements, each
  * row a sequence of blocks along k (rows = outputs).  Supported ggml types
