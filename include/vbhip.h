@@ -12,9 +12,9 @@
  * order of `stream` when the call is enqueued: memory that work on another
  * stream still writes (a block a caching allocator handed out again while a
  * kernel on its old stream is pending, say) needs an event wait or a
- * synchronisation first.  The MoE routing lists in the workspace are used as
- * indices, so such a race there ends in out-of-bounds accesses, not just in
- * wrong values.
+ * synchronisation first.  (The MoE expert kernels clamp the routing lists
+ * they read from the workspace, so a race there gives wrong values, not
+ * accesses outside the buffers.)
  *
  * Weights are GGUF tensors in the on-disk layout: n rows of k elements, each
  * row a sequence of blocks along k (rows = outputs).  Supported ggml types

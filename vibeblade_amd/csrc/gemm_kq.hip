@@ -422,7 +422,8 @@ template <int TYPE, int NMAT, int NCG, int RD>
 __global__ void __launch_bounds__(64 * KQ_WAVES) moe_kq_kernel(KqExperts w0, KqExperts w1, uint32_t wbytes,
                                                                const uint8_t* __restrict__ X, uint32_t xbytes,
                                                                int xdiv, const int32_t* __restrict__ eoff,
-                                                               const int32_t* __restrict__ elist, int N, int K,
+                                                               const int32_t* __restrict__ elist, int nslots,
+                                                               int N, int K,
                                                                uint32_t rb, _Float16* __restrict__ hout,
                                                                float* __restrict__ fout,
                                                                const float* __restrict__ rw, int topk,
@@ -430,9 +431,9 @@ __global__ void __launch_bounds__(64 * KQ_WAVES) moe_kq_kernel(KqExperts w0, KqE
     using T = Kq<TYPE>;
     extern __shared__ float4_t kq_red[];  // [wave][NMAT * NCG][lane]
     const int e = static_cast<int>(blockIdx.y);
-    const int base = eoff[e], cnt = eoff[e + 1] - base;
+    const SlotRange slots = expert_slots(eoff, elist, e, nslots);
+    const int cnt = slots.count;
     if (cnt <= 0) return;
-    const int32_t* slots = elist + base;
     const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int n0 = static_cast<int>(blockIdx.x) * 16 * NCG;
@@ -656,7 +657,7 @@ int gemm_kq(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, 
 // rows slot / topk of X (N = i, K = h); else fout = W0 x over rows slot of
 // X (N = h, K = i).
 int moe_kq(int32_t type, bool gate_up, const void* const* w0, const void* const* w1, int n_exp, const void* X,
-           int64_t xbytes, int topk, const int32_t* eoff, const int32_t* elist, int64_t N, int64_t K,
+           int64_t xbytes, int topk, const int32_t* eoff, const int32_t* elist, int nslots, int64_t N, int64_t K,
            _Float16* hout, float* fout, const float* rw, float* yacc, hipStream_t st) {
     if (n_exp > MOE_KQ_MAX_EXPERTS || K % KQ_STEP != 0) return E_UNSUPPORTED;
     KqExperts a{}, b{};
@@ -672,7 +673,8 @@ int moe_kq(int32_t type, bool gate_up, const void* const* w0, const void* const*
     auto go = [&](auto kernel, int ncg, int nmat) {
         const dim3 grid(static_cast<uint32_t>((N + 16 * ncg - 1) / (16 * ncg)), static_cast<uint32_t>(n_exp));
         const size_t lds = static_cast<size_t>(KQ_WAVES) * nmat * ncg * 64 * sizeof(float4_t);
-        kernel<<<grid, dim3(64 * KQ_WAVES), lds, st>>>(a, b, wbytes, xb, xby, gate_up ? topk : 1, eoff, elist, n, k,
+        kernel<<<grid, dim3(64 * KQ_WAVES), lds, st>>>(a, b, wbytes, xb, xby, gate_up ? topk : 1, eoff, elist, nslots,
+                                                       n, k,
                                                        rbu, hout, fout, rw, topk, yacc);
     };
     // gate/up: two matrices, 32-slot tiles; down: one matrix, ring of three

@@ -181,14 +181,15 @@ __device__ void tile_mfma(const uint8_t* const* wrow, const float* const* arow, 
 template <int WT>
 __global__ void __launch_bounds__(256) moe_gate_up_kernel(ExpertPtrs wg, ExpertPtrs wu, const float* __restrict__ x,
                                                           const int32_t* __restrict__ eoff,
-                                                          const int32_t* __restrict__ elist, int topk, int64_t h,
-                                                          int64_t i_dim, int64_t rb, float* __restrict__ hbuf) {
+                                                          const int32_t* __restrict__ elist, int nslots, int topk,
+                                                          int64_t h, int64_t i_dim, int64_t rb,
+                                                          float* __restrict__ hbuf) {
     __shared__ float4_t red[2][4][64];
     const int e = blockIdx.y;
     const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
-    const int cnt = eoff[e + 1] - eoff[e];
+    const SlotRange slots = expert_slots(eoff, elist, e, nslots);
+    const int cnt = slots.count;
     if (cnt <= 0) return;
-    const int32_t* slots = elist + eoff[e];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = lane & 15, g = lane >> 4;
     int64_t n = n0 + j;
@@ -223,14 +224,14 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(ExpertPtrs wg, ExpertP
 template <int WT>
 __global__ void __launch_bounds__(256) moe_down_kernel(ExpertPtrs wd, const float* __restrict__ hbuf,
                                                        const int32_t* __restrict__ eoff,
-                                                       const int32_t* __restrict__ elist, int64_t h, int64_t i_dim,
-                                                       int64_t rb, float* __restrict__ obuf) {
+                                                       const int32_t* __restrict__ elist, int nslots, int64_t h,
+                                                       int64_t i_dim, int64_t rb, float* __restrict__ obuf) {
     __shared__ float4_t red[1][4][64];
     const int e = blockIdx.y;
     const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
-    const int cnt = eoff[e + 1] - eoff[e];
+    const SlotRange slots = expert_slots(eoff, elist, e, nslots);
+    const int cnt = slots.count;
     if (cnt <= 0) return;
-    const int32_t* slots = elist + eoff[e];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = lane & 15, g = lane >> 4;
     int64_t n = n0 + j;
@@ -354,13 +355,13 @@ constexpr int MOE_WAVES = 4;
 template <int NW>
 __global__ void __launch_bounds__(64 * NW, NW <= 4 ? 2 : 1) moe_gate_up_q4k(
         ExpertPtrs wg, ExpertPtrs wu, const _Float16* __restrict__ xh, const int32_t* __restrict__ eoff,
-        const int32_t* __restrict__ elist, int topk, int h, int i_dim, int rb, uint32_t wbytes, uint32_t xbytes,
-        _Float16* __restrict__ hbuf) {
+        const int32_t* __restrict__ elist, int nslots, int topk, int h, int i_dim, int rb, uint32_t wbytes,
+        uint32_t xbytes, _Float16* __restrict__ hbuf) {
     extern __shared__ skinny::u32x4 moe_lds[];
     const int e = blockIdx.y;
-    const int base = eoff[e], cnt = eoff[e + 1] - base;
+    const SlotRange slots = expert_slots(eoff, elist, e, nslots);
+    const int cnt = slots.count;
     if (cnt <= 0) return;
-    const int32_t* slots = elist + base;
     const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
     skinny::TileArgs<2> ta;
     ta.w[0] = skinny::make_rsrc(wg.p[e], wbytes);
@@ -400,13 +401,13 @@ __global__ void __launch_bounds__(64 * NW, NW <= 4 ? 2 : 1) moe_gate_up_q4k(
 template <int NW>
 __global__ void __launch_bounds__(64 * NW, NW <= 4 ? 2 : 1) moe_down_q4k(
         ExpertPtrs wd, const _Float16* __restrict__ hbuf, const int32_t* __restrict__ eoff,
-        const int32_t* __restrict__ elist, int h, int i_dim, int rb, uint32_t wbytes, uint32_t hbytes,
+        const int32_t* __restrict__ elist, int nslots, int h, int i_dim, int rb, uint32_t wbytes, uint32_t hbytes,
         float* __restrict__ obuf, const float* __restrict__ rw, int topk, float* __restrict__ yacc) {
     extern __shared__ skinny::u32x4 moe_lds[];
     const int e = blockIdx.y;
-    const int base = eoff[e], cnt = eoff[e + 1] - base;
+    const SlotRange slots = expert_slots(eoff, elist, e, nslots);
+    const int cnt = slots.count;
     if (cnt <= 0) return;
-    const int32_t* slots = elist + base;
     const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
     skinny::TileArgs<1> ta;
     ta.w[0] = skinny::make_rsrc(wd.p[e], wbytes);
@@ -587,28 +588,32 @@ extern "C" int vb_moe_grouped_ffn_types(const void* const* wg, const void* const
         if (gate_up_type == TYPE_Q4_K) {
             const dim3 gu(static_cast<uint32_t>((i + skinny::ROWS - 1) / skinny::ROWS), n_exp);
             moe_gate_up_q4k<MOE_WAVES><<<gu, dim3(64 * MOE_WAVES), skinny::lds_bytes<MOE_WAVES>(), st>>>(
-                pg, pu, xh, eoff, elist, topk, static_cast<int>(h), static_cast<int>(i), static_cast<int>(rb_gu),
+                pg, pu, xh, eoff, elist, static_cast<int>(slots), topk, static_cast<int>(h), static_cast<int>(i),
+                static_cast<int>(rb_gu),
                 static_cast<uint32_t>(i * rb_gu), static_cast<uint32_t>(nx * 2), hb16);
             if ((rc = check_launch("vb_moe_grouped_ffn")) != OK) return rc;
-        } else if ((rc = moe_kq(gate_up_type, true, wg, wu, n_exp, xh, nx * 2, topk, eoff, elist, i, h, hb16, nullptr,
-                                nullptr, nullptr, st)) != OK) {
+        } else if ((rc = moe_kq(gate_up_type, true, wg, wu, n_exp, xh, nx * 2, topk, eoff, elist,
+                                static_cast<int>(slots), i, h, hb16, nullptr, nullptr, nullptr, st)) != OK) {
             return rc;
         }
         if (down_type == TYPE_Q4_K) {
             const dim3 dn(static_cast<uint32_t>((h + skinny::ROWS - 1) / skinny::ROWS), n_exp);
             moe_down_q4k<MOE_WAVES><<<dn, dim3(64 * MOE_WAVES), skinny::lds_bytes<MOE_WAVES>(), st>>>(
-                pd, hb16, eoff, elist, static_cast<int>(h), static_cast<int>(i), static_cast<int>(rb_d),
+                pd, hb16, eoff, elist, static_cast<int>(slots), static_cast<int>(h), static_cast<int>(i),
+                static_cast<int>(rb_d),
                 static_cast<uint32_t>(h * rb_d), static_cast<uint32_t>(slots * i * 2), obuf, rw, topk, yacc);
-        } else if ((rc = moe_kq(down_type, false, wd, nullptr, n_exp, hb16, slots * i * 2, topk, eoff, elist, h, i,
-                                nullptr, obuf, rw, yacc, st)) != OK) {
+        } else if ((rc = moe_kq(down_type, false, wd, nullptr, n_exp, hb16, slots * i * 2, topk, eoff, elist,
+                                static_cast<int>(slots), h, i, nullptr, obuf, rw, yacc, st)) != OK) {
             return rc;
         }
     } else {
         const dim3 gu_grid(static_cast<uint32_t>((i + 15) / 16), n_exp), dn_grid(static_cast<uint32_t>((h + 15) / 16), n_exp);
-        moe_gate_up_kernel<TYPE_F32><<<gu_grid, dim3(256), 0, st>>>(pg, pu, x, eoff, elist, topk, h, i,
+        moe_gate_up_kernel<TYPE_F32><<<gu_grid, dim3(256), 0, st>>>(pg, pu, x, eoff, elist, static_cast<int>(slots),
+                                                                    topk, h, i,
                                                                     row_bytes(TYPE_F32, h), hbuf);
         if ((rc = check_launch("vb_moe_grouped_ffn")) != OK) return rc;
-        moe_down_kernel<TYPE_F32><<<dn_grid, dim3(256), 0, st>>>(pd, hbuf, eoff, elist, h, i, row_bytes(TYPE_F32, i),
+        moe_down_kernel<TYPE_F32><<<dn_grid, dim3(256), 0, st>>>(pd, hbuf, eoff, elist, static_cast<int>(slots), h,
+                                                                 i, row_bytes(TYPE_F32, i),
                                                                  obuf);
     }
     if ((rc = check_launch("vb_moe_grouped_ffn")) != OK) return rc;

@@ -197,4 +197,28 @@ __device__ __forceinline__ float act_pair(float g, float u, int kind) {
     return fmaxf(g, 0.f) * fmaxf(u, 0.f);
 }
 
+// One expert's routed slots from the MoE routing lists: elist[eoff[e] ..
+// eoff[e + 1]) with every slot in [0, nslots).  The prep kernel writes the
+// lists; the clamps (range inside elist[0, nslots), slot values inside
+// [0, nslots)) keep the expert kernels' plain loads and stores inside their
+// buffers even if that memory was overwritten by a race with another stream.
+struct SlotRange {
+    const int32_t* list;
+    int count;
+    int nslots;
+    __device__ __forceinline__ int operator[](int r) const {
+        const int q = list[r];
+        return static_cast<unsigned>(q) < static_cast<unsigned>(nslots) ? q : 0;
+    }
+};
+
+__device__ __forceinline__ SlotRange expert_slots(const int32_t* __restrict__ eoff,
+                                                  const int32_t* __restrict__ elist, int e, int nslots) {
+    int64_t b = eoff[e];
+    int64_t c = static_cast<int64_t>(eoff[e + 1]) - b;
+    b = b < 0 ? 0 : (b > nslots ? nslots : b);
+    c = c > nslots - b ? nslots - b : c;
+    return SlotRange{elist + b, c < 0 ? 0 : static_cast<int>(c), nslots};
+}
+
 }  // namespace vb

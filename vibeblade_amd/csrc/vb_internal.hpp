@@ -178,10 +178,11 @@ int gemm_kq(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, 
 // writes fp16 silu(W0 x) * (W1 x) into hout[slot][n] from rows slot / topk of
 // the fp16 X; otherwise fout[slot][n] = W0 x from rows slot of X, or, with
 // yacc (top-k <= 2), rw[slot] W0 x added atomically into the zeroed
-// yacc[slot / topk][n].  eoff / elist: per-expert slot lists.
+// yacc[slot / topk][n].  eoff / elist: per-expert slot lists over nslots
+// slots.
 constexpr int MOE_KQ_MAX_EXPERTS = 64;
 int moe_kq(int32_t type, bool gate_up, const void* const* w0, const void* const* w1, int n_exp, const void* X,
-           int64_t xbytes, int topk, const int32_t* eoff, const int32_t* elist, int64_t N, int64_t K,
+           int64_t xbytes, int topk, const int32_t* eoff, const int32_t* elist, int nslots, int64_t N, int64_t K,
            _Float16* hout, float* fout, const float* rw, float* yacc, hipStream_t st);
 int gemm_dispatch(const void* w, const void* X, int32_t x_dtype, float* Y, int64_t M, int64_t N, int64_t K,
                   int32_t type, int32_t variant, void* ws, size_t ws_bytes, hipStream_t st);
