@@ -5,9 +5,11 @@
  * stated otherwise; vb_last_error() returns the thread-local text of the last
  * failure.  No C++ exception crosses this boundary.  All pointers passed to
  * the op functions are device pointers; `stream` is a hipStream_t (NULL =
- * the default stream).  Launches are asynchronous on `stream`.  There is no
- * global scratch state: functions that need temporaries take a caller-owned
- * workspace, so calls on different streams or threads are independent.
+ * the default stream).  Launches are asynchronous on `stream`.  Apart from
+ * vb_sparse_ffn_noalloc (a static device array, described at its
+ * declaration) there is no global scratch state: functions that need
+ * temporaries take a caller-owned workspace, so calls on different streams
+ * or threads are independent.
  * Every buffer of a call (inputs, outputs, workspace) must be ready in the
  * order of `stream` when the call is enqueued: memory that work on another
  * stream still writes (a block a caching allocator handed out again while a
